@@ -1,0 +1,203 @@
+"""ctypes view of the C oracle (liboracle.so) and of the compiled reference
+kernels (_ref/libref.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by the smoke check and by the
+cpu_baseline leg of bench.py, never by the product library.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_u32 = C.c_uint32
+
+
+def _load(name: str) -> C.CDLL:
+    path = HERE / name
+    if not path.exists():
+        raise FileNotFoundError(f"{path} is not built (run `make -C {HERE}`)")
+    return C.CDLL(str(path))
+
+
+class Oracle:
+    """Scalar C restatement (liboracle.so)."""
+
+    def __init__(self, libname: str = "liboracle.so"):
+        L = self.lib = _load(libname)
+        L.oc_fp16_to_fp32.argtypes = [C.c_uint16]
+        L.oc_fp16_to_fp32.restype = C.c_float
+        L.oc_fp32_to_fp16.argtypes = [C.c_float]
+        L.oc_fp32_to_fp16.restype = C.c_uint16
+        L.oc_splitmix64_at.argtypes = [C.c_uint64, C.c_uint64]
+        L.oc_splitmix64_at.restype = C.c_uint64
+        L.oc_quantize_per_token_symmetric.argtypes = [_f32p, _i8p, _f32p, _u32, _u32]
+        L.oc_fused_dequant_dot_int8.argtypes = [_f32p, _i8p, _f32p, _f32p, _u32, _u32]
+        L.oc_dot_q8_0_f64.argtypes = [_u8p, _u32, _f32p]
+        L.oc_dot_q8_0_f64.restype = C.c_double
+        L.oc_dot_q4_K_f64.argtypes = [_u8p, _u32, _f32p]
+        L.oc_dot_q4_K_f64.restype = C.c_double
+        for fn in (L.oc_matvec_q8_0, L.oc_matvec_q4_K):
+            fn.argtypes = [_u8p, _f32p, _f32p, _u32, _u32]
+        L.oc_q4k_pos.argtypes = [_u32, _u32]
+        L.oc_q4k_pos.restype = _u32
+        L.oc_quantize_act_q8_0.argtypes = [_f32p, _i8p, _f32p, _u32]
+        L.oc_quantize_act_q4_K.argtypes = [_f32p, _i8p, _f32p, _i32p, _u32]
+        L.oc_dequant_act_q8_0.argtypes = [_i8p, _f32p, _f32p, _u32]
+        L.oc_dequant_act_q4_K.argtypes = [_i8p, _f32p, _f32p, _u32]
+        L.oc_block_dots_q8_0.argtypes = [_u8p, _i8p, _i32p, _u32, _u32]
+        L.oc_block_dots_q4_K.argtypes = [_u8p, _i8p, _i32p, _u32, _u32]
+        L.oc_kv_append.argtypes = [_f32p, _f32p, _i8p, _i8p, _f32p, _f32p, _u32, _u32, _u32]
+        L.oc_attn_decode_int8.argtypes = [_f32p, _i8p, _i8p, _f32p, _f32p, _f32p, _u32, _u32, _u32, _u32]
+        L.oc_deltanet_step.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _u32, _u32, _u32, _u32]
+        L.oc_rmsnorm.argtypes = [_f32p, _f32p, _f32p, _u32]
+        L.oc_head_rmsnorm.argtypes = [_f32p, _f32p, _u32, _u32]
+        L.oc_rope_inv_freq.argtypes = [_f32p, _u32, C.c_float]
+        L.oc_rope.argtypes = [_f32p, _u32, _u32, _u32, _f32p]
+        L.oc_silu.argtypes = [C.c_float]
+        L.oc_silu.restype = C.c_float
+        L.oc_softplus.argtypes = [C.c_float]
+        L.oc_softplus.restype = C.c_float
+        L.oc_l2norm_heads.argtypes = [_f32p, _u32, _u32]
+        L.oc_conv_step.argtypes = [_f32p, _f32p, _f32p, _f32p, _u32, _u32]
+        L.oc_argmax.argtypes = [_f32p, _u32]
+        L.oc_argmax.restype = _u32
+
+    # -- wrappers returning numpy arrays
+    def quantize(self, x: np.ndarray, width: int):
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+        rows = x.size // width
+        q = np.zeros(rows * width, np.int8)
+        s = np.zeros(rows, np.float32)
+        self.lib.oc_quantize_per_token_symmetric(x, q, s, rows, width)
+        return q.reshape(rows, width), s
+
+    def matvec_q8_0(self, W: np.ndarray, x: np.ndarray, y0: np.ndarray | None = None):
+        M = W.shape[0]
+        K = x.size
+        y = np.zeros(M, np.float32) if y0 is None else np.array(y0, np.float32)
+        self.lib.oc_matvec_q8_0(np.ascontiguousarray(W).reshape(-1), np.ascontiguousarray(x, np.float32), y, M, K)
+        return y
+
+    def matvec_q4_K(self, W: np.ndarray, x: np.ndarray, y0: np.ndarray | None = None):
+        M = W.shape[0]
+        K = x.size
+        y = np.zeros(M, np.float32) if y0 is None else np.array(y0, np.float32)
+        self.lib.oc_matvec_q4_K(np.ascontiguousarray(W).reshape(-1), np.ascontiguousarray(x, np.float32), y, M, K)
+        return y
+
+    def quantize_act_q8_0(self, x: np.ndarray):
+        K = x.size
+        xq = np.zeros(K, np.int8)
+        xd = np.zeros(K // 32, np.float32)
+        self.lib.oc_quantize_act_q8_0(np.ascontiguousarray(x, np.float32), xq, xd, K)
+        return xq, xd
+
+    def quantize_act_q4_K(self, x: np.ndarray):
+        K = x.size
+        xq = np.zeros(K, np.int8)
+        xd = np.zeros(K // 32, np.float32)
+        xs = np.zeros(K // 32, np.int32)
+        self.lib.oc_quantize_act_q4_K(np.ascontiguousarray(x, np.float32), xq, xd, xs, K)
+        return xq, xd, xs
+
+    def dequant_act_q8_0(self, xq, xd):
+        out = np.zeros(xq.size, np.float32)
+        self.lib.oc_dequant_act_q8_0(np.ascontiguousarray(xq), np.ascontiguousarray(xd), out, xq.size)
+        return out
+
+    def dequant_act_q4_K(self, xq, xd):
+        out = np.zeros(xq.size, np.float32)
+        self.lib.oc_dequant_act_q4_K(np.ascontiguousarray(xq), np.ascontiguousarray(xd), out, xq.size)
+        return out
+
+    def block_dots_q8_0(self, W, xq):
+        M = W.shape[0]
+        K = xq.size
+        out = np.zeros(M * (K // 32), np.int32)
+        self.lib.oc_block_dots_q8_0(np.ascontiguousarray(W).reshape(-1), np.ascontiguousarray(xq), out, M, K)
+        return out.reshape(M, K // 32)
+
+    def block_dots_q4_K(self, W, xq):
+        M = W.shape[0]
+        K = xq.size
+        out = np.zeros(M * (K // 32), np.int32)
+        self.lib.oc_block_dots_q4_K(np.ascontiguousarray(W).reshape(-1), np.ascontiguousarray(xq), out, M, K)
+        return out.reshape(M, K // 32)
+
+    def kv_append(self, k, v, keys, vals, ks, vs, pos, n_kv, head_dim):
+        self.lib.oc_kv_append(np.ascontiguousarray(k, np.float32), np.ascontiguousarray(v, np.float32),
+                              keys, vals, ks, vs, pos, n_kv, head_dim)
+
+    def attn_decode(self, q, keys, vals, ks, vs, n_heads, n_kv, head_dim, ctx):
+        out = np.zeros(n_heads * head_dim, np.float32)
+        self.lib.oc_attn_decode_int8(np.ascontiguousarray(q, np.float32).reshape(-1),
+                                     np.ascontiguousarray(keys).reshape(-1), np.ascontiguousarray(vals).reshape(-1),
+                                     np.ascontiguousarray(ks, np.float32).reshape(-1),
+                                     np.ascontiguousarray(vs, np.float32).reshape(-1), out, n_heads, n_kv, head_dim,
+                                     ctx)
+        return out.reshape(n_heads, head_dim)
+
+    def deltanet_step(self, state, q, k, v, decay, beta, n_v, n_k, d_k, d_v):
+        """Advances ``state`` ([n_v, d_k, d_v] float32, reference layout) in place."""
+        out = np.zeros(n_v * d_v, np.float32)
+        self.lib.oc_deltanet_step(state.reshape(-1), np.ascontiguousarray(q, np.float32).reshape(-1),
+                                  np.ascontiguousarray(k, np.float32).reshape(-1),
+                                  np.ascontiguousarray(v, np.float32).reshape(-1),
+                                  np.ascontiguousarray(decay, np.float32), np.ascontiguousarray(beta, np.float32),
+                                  out, n_v, n_k, d_k, d_v)
+        return out.reshape(n_v, d_v)
+
+
+class Reference:
+    """The reference's own kernels, compiled from its sources into _ref/libref.so
+    (oracle/Makefile `ref`).  C++ linkage, so symbols are looked up mangled."""
+
+    SYMS = {
+        "quantize_per_token_symmetric": "_Z28quantize_per_token_symmetricPKfPaPfjj",
+        "fused_dequant_dot_int8": "_Z22fused_dequant_dot_int8PKfPKaS0_Pfjj",
+        "fused_dequant_dot_q8_0": "_Z22fused_dequant_dot_q8_0PK10block_q8_0jPKf",
+        "fused_dequant_dot_q4_K": "_Z22fused_dequant_dot_q4_KPK10block_q4_KjPKf",
+        "matvec_q8_0": "_Z11matvec_q8_0PKvPKfPfjj",
+        "matvec_q4_K": "_Z11matvec_q4_KPKvPKfPfjj",
+    }
+
+    def __init__(self):
+        L = self.lib = _load("_ref/libref.so")
+        f = self.fn = {k: getattr(L, v) for k, v in self.SYMS.items()}
+        f["quantize_per_token_symmetric"].argtypes = [_f32p, _i8p, _f32p, _u32, _u32]
+        f["fused_dequant_dot_int8"].argtypes = [_f32p, _i8p, _f32p, _f32p, _u32, _u32]
+        f["fused_dequant_dot_q8_0"].argtypes = [_u8p, _u32, _f32p]
+        f["fused_dequant_dot_q8_0"].restype = C.c_float
+        f["fused_dequant_dot_q4_K"].argtypes = [_u8p, _u32, _f32p]
+        f["fused_dequant_dot_q4_K"].restype = C.c_float
+        f["matvec_q8_0"].argtypes = [_u8p, _f32p, _f32p, _u32, _u32]
+        f["matvec_q4_K"].argtypes = [_u8p, _f32p, _f32p, _u32, _u32]
+
+    @staticmethod
+    def available() -> bool:
+        return (HERE / "_ref" / "libref.so").exists()
+
+
+class Baseline:
+    """AVX2 + OpenMP CPU baseline (liboracle_avx2.so)."""
+
+    def __init__(self):
+        L = self.lib = _load("liboracle_avx2.so")
+        L.ob_matvec_q8_0_avx2.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, _u32, _u32]
+        L.ob_matvec_q4_K_avx2.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, _u32, _u32]
+        L.ob_set_threads.argtypes = [C.c_int]
+        L.ob_max_threads.restype = C.c_int
+        L.oc_attn_decode_int8.argtypes = [C.c_void_p] * 6 + [_u32] * 4
+        L.oc_deltanet_step.argtypes = [C.c_void_p] * 7 + [_u32] * 4
+
+    def threads(self, n: int):
+        self.lib.ob_set_threads(int(n))
