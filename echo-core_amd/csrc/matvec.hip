@@ -1,0 +1,441 @@
+// matvec.hip — decode matvec / skinny GEMM over block-quantized weights.
+//
+// y[m][n] (+)= sum over 32-element blocks of d_w * d_x * isum for M <= 16 token
+// rows (src/kernels/matvec.cpp:62-142 computes the same sums for one row of
+// fp32 activations).  The integer block dot isum is one
+// v_mfma_i32_16x16x32_i8: A = 16 token rows x 32 int8 activations, B = 32 int8
+// weights x 16 weight rows, so a wave turns 16 rows x 32 elements of weights
+// into 16x16 exact int32 dots per instruction.  The kernel is a weight stream:
+// each wave reads a contiguous run of 2 KB chunks of the tiled layout (two
+// 16-byte loads per lane per chunk), the 16-token activation operand comes
+// from L1/L2, and the fp32 epilogue applies the per-block scales.  The K range
+// of one 16-row tile is split across the waves of a workgroup and reduced
+// through LDS in a fixed order (deterministic results).
+//
+// MFMA lane layout (16x16x32 i8): A[i][k] and B[k][j] live in lane
+// (i or j) + 16*(k/8), byte k%8; D[i][j] lives in lane j + 16*(i/4), element i%4.
+#include "common.hpp"
+#include "layout.hpp"
+
+namespace ec {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) {
+    return (long)(((uint64_t)hi << 32) | (uint64_t)lo);
+}
+
+__device__ __forceinline__ v4i mfma_i8(long a, long b) {
+    const v4i z = {0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
+}
+
+// Cross-wave reduction of acc[4] and the store of y / accumulate.
+template <int R>
+__device__ __forceinline__ void reduce_store(float (&acc)[4], float* red, float* __restrict__ y, uint32_t t,
+                                             uint32_t M, uint32_t N, uint32_t ldy, int accumulate) {
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if (nw > 1) {
+        for (int r = 0; r < R; ++r) red[(w * 64 + lane) * 4 + r] = acc[r];
+        __syncthreads();
+        if (w != 0) return;
+        for (int r = 0; r < R; ++r) {
+            float s = red[lane * 4 + r];
+            for (uint32_t v = 1; v < nw; ++v) s += red[(v * 64 + lane) * 4 + r];
+            acc[r] = s;
+        }
+    }
+    const uint32_t row = lane & 15, g = lane >> 4, n = 16 * t + row;
+    if (n >= N) return;
+    for (int r = 0; r < R; ++r) {
+        uint32_t m = 4 * g + r;
+        if (m < M) {
+            float* dst = y + (size_t)m * ldy + n;
+            *dst = accumulate ? *dst + acc[r] : acc[r];
+        }
+    }
+}
+
+// --------------------------------------------------------------------- Q8_0
+template <int MT, bool DOTS>
+__global__ __launch_bounds__(1024) void k_mv_q8_0(const uint8_t* __restrict__ W, const uint8_t* __restrict__ act,
+                                                  float* __restrict__ y, int32_t* __restrict__ dots, uint32_t M,
+                                                  uint32_t N, uint32_t K, uint32_t nG, uint32_t gpw, uint32_t xd_off,
+                                                  uint32_t ldy, int accumulate) {
+    extern __shared__ float red[];
+    constexpr int R = MT < 4 ? MT : 4;
+    const uint32_t t = blockIdx.x;
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t row = lane & 15, g = lane >> 4;
+    const uint32_t G0 = w * gpw;
+    const uint32_t G1 = min(nG, G0 + gpw);
+    const uint8_t* wt = W + (size_t)t * nG * kQ8TChunk;
+    const float* __restrict__ xd = (const float*)(act + xd_off);
+    const bool aval = row < M;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t G = G0; G < G1; ++G) {
+        const uint8_t* ch = wt + (size_t)G * kQ8TChunk;
+        const uint4 b01 = *(const uint4*)(ch + lane * 32);
+        const uint4 b23 = *(const uint4*)(ch + lane * 32 + 16);
+        const uint2 dw = *(const uint2*)(ch + 2048 + row * 8);
+        uint4 a01 = {0u, 0u, 0u, 0u}, a23 = {0u, 0u, 0u, 0u};
+        if (aval) {
+            const uint8_t* ap = act + (((size_t)G * 4 + g) * M + row) * 32;
+            a01 = *(const uint4*)ap;
+            a23 = *(const uint4*)(ap + 16);
+        }
+        const long A[4] = {pack2(a01.x, a01.y), pack2(a01.z, a01.w), pack2(a23.x, a23.y), pack2(a23.z, a23.w)};
+        const long B[4] = {pack2(b01.x, b01.y), pack2(b01.z, b01.w), pack2(b23.x, b23.y), pack2(b23.z, b23.w)};
+        const float dwf[4] = {h2f(dw.x & 0xFFFF), h2f(dw.x >> 16), h2f(dw.y & 0xFFFF), h2f(dw.y >> 16)};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const v4i c = mfma_i8(A[j], B[j]);
+            const uint32_t b = 4 * G + j;
+            if constexpr (DOTS) {
+                const uint32_t n = 16 * t + row, nb = K / 32;
+                if (n < N && b < nb)
+                    for (int r = 0; r < 4; ++r)
+                        if (4 * g + r < M) dots[((size_t)(4 * g + r) * N + n) * nb + b] = c[r];
+            } else if constexpr (MT == 1) {
+                const float dx = xd[b * 16];
+                acc[0] = fmaf((float)c[0], dwf[j] * dx, acc[0]);
+            } else {
+                const float4 dx = *(const float4*)(xd + b * 16 + 4 * g);
+                const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[r] = fmaf((float)c[r], dwf[j] * dxv[r], acc[r]);
+            }
+        }
+    }
+    if constexpr (!DOTS) reduce_store<R>(acc, red, y, t, M, N, ldy, accumulate);
+}
+
+// --------------------------------------------------------------------- Q4_K
+__device__ __forceinline__ void q4k_scale_min(const uint32_t (&q)[3], int s, uint32_t& sc, uint32_t& m) {
+    // q holds scales[0..11] little-endian: byte i = (q[i/4] >> 8*(i%4)) & 0xFF
+    auto byte = [&](int i) -> uint32_t { return (q[i >> 2] >> (8 * (i & 3))) & 0xFFu; };
+    if (s < 4) {
+        sc = byte(s) & 63u;
+        m = byte(s + 4) & 63u;
+    } else {
+        sc = (byte(s + 4) & 0x0Fu) | ((byte(s - 4) >> 6) << 4);
+        m = (byte(s + 4) >> 4) | ((byte(s) >> 6) << 4);
+    }
+}
+
+template <int MT, bool DOTS>
+__global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W, const uint8_t* __restrict__ act,
+                                                  float* __restrict__ y, int32_t* __restrict__ dots, uint32_t M,
+                                                  uint32_t N, uint32_t K, uint32_t nB, uint32_t gpw, uint32_t xd_off,
+                                                  uint32_t dxs_off, uint32_t ldy, int accumulate) {
+    extern __shared__ float red[];
+    constexpr int R = MT < 4 ? MT : 4;
+    const uint32_t t = blockIdx.x;
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t row = lane & 15, g = lane >> 4;
+    const uint32_t B0 = w * gpw;
+    const uint32_t B1 = min(nB, B0 + gpw);
+    const uint8_t* wt = W + (size_t)t * nB * kQ4TChunk;
+    const float* __restrict__ xd = (const float*)(act + xd_off);
+    const float* __restrict__ dxs = (const float*)(act + dxs_off);
+    const bool aval = row < M;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t b = B0; b < B1; ++b) {
+        const uint8_t* ch = wt + (size_t)b * kQ4TChunk;
+        const uint4 q0 = *(const uint4*)(ch + lane * 32);
+        const uint4 q1 = *(const uint4*)(ch + lane * 32 + 16);
+        const uint4 hdr = *(const uint4*)(ch + 2048 + row * 16);
+        uint4 a[4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+        if (aval) {
+            const uint8_t* ap = act + (((size_t)b * 4 + g) * M + row) * 64;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[i] = *(const uint4*)(ap + 16 * i);
+        }
+        const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        const uint32_t aw[16] = {a[0].x, a[0].y, a[0].z, a[0].w, a[1].x, a[1].y, a[1].z, a[1].w,
+                                 a[2].x, a[2].y, a[2].z, a[2].w, a[3].x, a[3].y, a[3].z, a[3].w};
+        const float d = h2f(hdr.x & 0xFFFF), dmin = h2f(hdr.x >> 16);
+        const uint32_t scb[3] = {hdr.y, hdr.z, hdr.w};
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const uint32_t lo = qw[s] & 0x0F0F0F0Fu, hi = (qw[s] >> 4) & 0x0F0F0F0Fu;
+            const v4i c = mfma_i8(pack2(aw[2 * s], aw[2 * s + 1]), pack2(lo, hi));
+            const uint32_t sbi = 8 * b + s;
+            if constexpr (DOTS) {
+                const uint32_t n = 16 * t + row, nsb = K / 32;
+                if (n < N && sbi < nsb)
+                    for (int r = 0; r < 4; ++r)
+                        if (4 * g + r < M) dots[((size_t)(4 * g + r) * N + n) * nsb + sbi] = c[r];
+            } else {
+                uint32_t sc, mn;
+                q4k_scale_min(scb, s, sc, mn);
+                const float dsc = d * (float)sc, dmn = dmin * (float)mn;
+                if constexpr (MT == 1) {
+                    const float dx = xd[sbi * 16], dxm = dxs[sbi * 16];
+                    acc[0] = fmaf((float)c[0], dsc * dx, acc[0]);
+                    acc[0] = fmaf(-dmn, dxm, acc[0]);
+                } else {
+                    const float4 dx = *(const float4*)(xd + sbi * 16 + 4 * g);
+                    const float4 dm = *(const float4*)(dxs + sbi * 16 + 4 * g);
+                    const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
+                    const float dmv[4] = {dm.x, dm.y, dm.z, dm.w};
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        acc[r] = fmaf((float)c[r], dsc * dxv[r], acc[r]);
+                        acc[r] = fmaf(-dmn, dmv[r], acc[r]);
+                    }
+                }
+            }
+        }
+    }
+    if constexpr (!DOTS) reduce_store<R>(acc, red, y, t, M, N, ldy, accumulate);
+}
+
+// ------------------------------------------------ reference-semantics fp32 path
+// One wave per output row, fp32 activations, GGUF bytes read in place.
+// Q8_0 follows src/kernels/matvec.cpp:62-87 per block; Q4_K :92-142; Q2_K
+// :146-183; F16 :18-45.  The row sum is a wave reduction (order differs from
+// the reference's sequential loop by rounding only).
+__device__ __forceinline__ uint16_t ld16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+__global__ __launch_bounds__(64) void k_matvec_gguf_f32(int fmt, const uint8_t* __restrict__ Wb,
+                                                        const float* __restrict__ x, float* __restrict__ y,
+                                                        uint32_t M, uint32_t K) {
+    const uint32_t m = blockIdx.x, lane = threadIdx.x;
+    if (m >= M) return;
+    float sum = 0.0f;
+    if (fmt == EC_Q8_0) {
+        const uint32_t nb = K / 32;
+        const uint8_t* row = Wb + (size_t)m * nb * 34;
+        for (uint32_t b = lane; b < nb; b += 64) {
+            const uint8_t* bp = row + (size_t)b * 34;
+            const float d = h2f(ld16(bp));
+            float bs = 0.0f;
+            for (int j = 0; j < 32; ++j) bs = fmaf((float)(int8_t)bp[2 + j], x[32 * b + j], bs);
+            sum = fmaf(d, bs, sum);
+        }
+    } else if (fmt == EC_Q4_K) {
+        const uint32_t nb = K / 256;
+        const uint8_t* row = Wb + (size_t)m * nb * 144;
+        for (uint32_t b = lane; b < nb * 4; b += 64) {  // one 64-weight group per lane step
+            const uint32_t sbk = b / 4, blk = b % 4;
+            const uint8_t* bp = row + (size_t)sbk * 144;
+            const float d = h2f(ld16(bp)), dmin = h2f(ld16(bp + 2));
+            const uint32_t scw[3] = {(uint32_t)bp[4] | (uint32_t)bp[5] << 8 | (uint32_t)bp[6] << 16 | (uint32_t)bp[7] << 24,
+                                     (uint32_t)bp[8] | (uint32_t)bp[9] << 8 | (uint32_t)bp[10] << 16 | (uint32_t)bp[11] << 24,
+                                     (uint32_t)bp[12] | (uint32_t)bp[13] << 8 | (uint32_t)bp[14] << 16 | (uint32_t)bp[15] << 24};
+            uint32_t sc0, mn0, sc1, mn1;
+            q4k_scale_min(scw, 2 * blk, sc0, mn0);
+            q4k_scale_min(scw, 2 * blk + 1, sc1, mn1);
+            const float rs0 = d * (float)sc0, rm0 = dmin * (float)mn0, rs1 = d * (float)sc1, rm1 = dmin * (float)mn1;
+            const uint8_t* qs = bp + 16 + 32 * blk;
+            const float* xb = x + 256 * sbk + 64 * blk;
+            for (int j = 0; j < 16; ++j) {
+                sum = fmaf(rs0 * (float)(qs[j] & 0x0F) - rm0, xb[j], sum);
+                sum = fmaf(rs1 * (float)(qs[16 + j] & 0x0F) - rm1, xb[16 + j], sum);
+                sum = fmaf(rs0 * (float)(qs[j] >> 4) - rm0, xb[32 + j], sum);
+                sum = fmaf(rs1 * (float)(qs[16 + j] >> 4) - rm1, xb[48 + j], sum);
+            }
+        }
+    } else if (fmt == EC_Q2_K) {
+        const uint32_t nb = K / 256;
+        const uint8_t* row = Wb + (size_t)m * nb * 84;
+        for (uint32_t b = lane; b < nb * 32; b += 64) {  // one 8-weight sub-block per lane step
+            const uint32_t sbk = b / 32, sb = b % 32;
+            const uint8_t* bp = row + (size_t)sbk * 84;
+            const float d_all = h2f(ld16(bp)), m_all = h2f(ld16(bp + 2));
+            const uint8_t* sc = bp + 4;
+            const uint8_t* qs = bp + 20;
+            const uint32_t s = sb / 2;
+            const uint8_t sv = (sb % 2 == 0) ? sc[s] : sc[s + 8];
+            const float scale = d_all * (float)(sv & 0x0F), minv = m_all * (float)(sv >> 4);
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t j = 8 * sb + i;
+                const int q = (qs[j / 4] >> ((j % 4) * 2)) & 3;
+                sum = fmaf(scale * (float)q - minv, x[256 * sbk + j], sum);
+            }
+        }
+    } else {  // F16 rows
+        const uint16_t* row = (const uint16_t*)Wb + (size_t)m * K;
+        for (uint32_t k = lane; k < K; k += 64) sum = fmaf(h2f(row[k]), x[k], sum);
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) y[m] += sum;
+}
+
+// scores[p] = sum_k K[p][k] * scale[p] * q[k]  (src/kernels/quant.cpp:100-144)
+__global__ void k_dequant_dot_int8(const float* __restrict__ q, const int8_t* __restrict__ keys,
+                                   const float* __restrict__ scales, float* __restrict__ scores, uint32_t dim,
+                                   uint32_t seq) {
+    const uint32_t p = blockIdx.x, lane = threadIdx.x;
+    if (p >= seq) return;
+    const int8_t* kp = keys + (size_t)p * dim;
+    const float s = scales[p];
+    float acc = 0.0f;
+    for (uint32_t k = lane; k < dim; k += 64) acc = fmaf((float)kp[k] * s, q[k], acc);
+    acc = wave_sum(acc);
+    if (lane == 0) scores[p] = acc;
+}
+
+// GGUF blocks -> fp16, one thread per block (src/kernels/quant.cpp:308-396).
+__global__ void k_dequant_fp16(int fmt, const uint8_t* __restrict__ src, uint16_t* __restrict__ dst, size_t nblk) {
+    const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblk) return;
+    if (fmt == EC_Q8_0) {
+        const uint8_t* bp = src + b * 34;
+        const float d = h2f(ld16(bp));
+        for (int j = 0; j < 32; ++j) dst[b * 32 + j] = __half_as_ushort(__float2half_rn(d * (float)(int8_t)bp[2 + j]));
+    } else if (fmt == EC_Q4_K) {
+        const uint8_t* bp = src + b * 144;
+        const float d = h2f(ld16(bp)), dmin = h2f(ld16(bp + 2));
+        uint32_t scw[3];
+        for (int i = 0; i < 3; ++i)
+            scw[i] = (uint32_t)bp[4 + 4 * i] | (uint32_t)bp[5 + 4 * i] << 8 | (uint32_t)bp[6 + 4 * i] << 16 |
+                     (uint32_t)bp[7 + 4 * i] << 24;
+        for (int blk = 0; blk < 4; ++blk) {
+            uint32_t sc0, mn0, sc1, mn1;
+            q4k_scale_min(scw, 2 * blk, sc0, mn0);
+            q4k_scale_min(scw, 2 * blk + 1, sc1, mn1);
+            const float rs0 = d * (float)sc0, rm0 = dmin * (float)mn0, rs1 = d * (float)sc1, rm1 = dmin * (float)mn1;
+            const uint8_t* qs = bp + 16 + 32 * blk;
+            uint16_t* o = dst + b * 256 + 64 * blk;
+            for (int j = 0; j < 16; ++j) {
+                o[j] = __half_as_ushort(__float2half_rn(rs0 * (float)(qs[j] & 0x0F) - rm0));
+                o[16 + j] = __half_as_ushort(__float2half_rn(rs1 * (float)(qs[16 + j] & 0x0F) - rm1));
+                o[32 + j] = __half_as_ushort(__float2half_rn(rs0 * (float)(qs[j] >> 4) - rm0));
+                o[48 + j] = __half_as_ushort(__float2half_rn(rs1 * (float)(qs[16 + j] >> 4) - rm1));
+            }
+        }
+    } else {  // Q2_K
+        const uint8_t* bp = src + b * 84;
+        const float d_all = h2f(ld16(bp)), m_all = h2f(ld16(bp + 2));
+        for (int j = 0; j < 256; ++j) {
+            const int sb = j / 8, s = sb / 2;
+            const uint8_t sv = (sb % 2 == 0) ? bp[4 + s] : bp[4 + s + 8];
+            const int q = (bp[20 + j / 4] >> ((j % 4) * 2)) & 3;
+            dst[b * 256 + j] =
+                __half_as_ushort(__float2half_rn(d_all * (float)(sv & 0x0F) * (float)q - m_all * (float)(sv >> 4)));
+        }
+    }
+}
+
+// Waves per workgroup for one 16-row tile: aim for ~4096 waves in flight and
+// at least one chunk per wave.
+static void split_k(uint32_t n_tiles, uint32_t n_chunks, uint32_t& nw, uint32_t& per_wave) {
+    uint32_t target = (4096 + n_tiles - 1) / n_tiles;
+    target = target < 1 ? 1 : (target > 16 ? 16 : target);
+    per_wave = (n_chunks + target - 1) / target;
+    nw = (n_chunks + per_wave - 1) / per_wave;
+}
+
+template <int MT, bool DOTS>
+static void launch_q8(const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N, uint32_t K,
+                      uint32_t ldy, int accumulate, hipStream_t st) {
+    const ActLayout L = act_layout(EC_Q8_0, M, K);
+    const uint32_t nT = round_up(N, 16) / 16, nG = L.Kp / 128;
+    uint32_t nw, gpw;
+    split_k(nT, nG, nw, gpw);
+    const size_t lds = nw > 1 ? (size_t)nw * 64 * 4 * sizeof(float) : 0;
+    hipLaunchKernelGGL((k_mv_q8_0<MT, DOTS>), dim3(nT), dim3(64 * nw), lds, st, (const uint8_t*)W,
+                       (const uint8_t*)act, y, dots, M, N, K, nG, gpw, (uint32_t)L.xd_off, ldy, accumulate);
+}
+
+template <int MT, bool DOTS>
+static void launch_q4(const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N, uint32_t K,
+                      uint32_t ldy, int accumulate, hipStream_t st) {
+    const ActLayout L = act_layout(EC_Q4_K, M, K);
+    const uint32_t nT = round_up(N, 16) / 16, nB = L.Kp / 256;
+    uint32_t nw, gpw;
+    split_k(nT, nB, nw, gpw);
+    const size_t lds = nw > 1 ? (size_t)nw * 64 * 4 * sizeof(float) : 0;
+    hipLaunchKernelGGL((k_mv_q4_K<MT, DOTS>), dim3(nT), dim3(64 * nw), lds, st, (const uint8_t*)W,
+                       (const uint8_t*)act, y, dots, M, N, K, nB, gpw, (uint32_t)L.xd_off, (uint32_t)L.dxs_off, ldy,
+                       accumulate);
+}
+
+template <bool DOTS>
+static int dispatch(int fmt, const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N,
+                    uint32_t K, uint32_t ldy, int accumulate, hipStream_t st) {
+    if (fmt == EC_Q8_0) {
+        if (M == 1) launch_q8<1, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
+        else if (M <= 4) launch_q8<4, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
+        else if (M <= 8) launch_q8<8, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
+        else launch_q8<16, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
+    } else {
+        if (M == 1) launch_q4<1, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
+        else if (M <= 4) launch_q4<4, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
+        else if (M <= 8) launch_q4<8, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
+        else launch_q4<16, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
+    }
+    return EC_OK;
+}
+
+}  // namespace ec
+
+using namespace ec;
+
+static int check_mv(int fmt, const void* W, const void* act, const void* out, uint32_t M, uint32_t N, uint32_t K,
+                    const char* who) {
+    if (fmt != EC_Q8_0 && fmt != EC_Q4_K) return ec_set_error(EC_ERR_UNSUPPORTED, "matvec: format must be Q8_0 or Q4_K");
+    if (!W || !act || !out || M == 0 || M > 16 || N == 0 || K == 0 || K % (fmt == EC_Q8_0 ? 32u : 256u)) {
+        char buf[160];
+        snprintf(buf, sizeof buf, "%s: bad arguments (M=%u N=%u K=%u; need 1<=M<=16, K%%%u==0)", who, M, N, K,
+                 fmt == EC_Q8_0 ? 32u : 256u);
+        return ec_set_error(EC_ERR_ARG, buf);
+    }
+    return EC_OK;
+}
+
+extern "C" int ec_matvec(int fmt, const void* tiled, const void* act, float* y, uint32_t M, uint32_t N, uint32_t K,
+                         uint32_t ldy, int accumulate, void* stream) {
+    int rc = check_mv(fmt, tiled, act, y, M, N, K, "ec_matvec");
+    if (rc) return rc;
+    if (ldy < N) return ec_set_error(EC_ERR_ARG, "ec_matvec: ldy < N");
+    dispatch<false>(fmt, tiled, act, y, nullptr, M, N, K, ldy, accumulate, (hipStream_t)stream);
+    EC_CHECK_LAUNCH();
+    return EC_OK;
+}
+
+extern "C" int ec_block_dots(int fmt, const void* tiled, const void* act, int32_t* out, uint32_t M, uint32_t N,
+                             uint32_t K, void* stream) {
+    int rc = check_mv(fmt, tiled, act, out, M, N, K, "ec_block_dots");
+    if (rc) return rc;
+    dispatch<true>(fmt, tiled, act, nullptr, out, M, N, K, N, 0, (hipStream_t)stream);
+    EC_CHECK_LAUNCH();
+    return EC_OK;
+}
+
+extern "C" int ec_matvec_gguf_f32(int fmt, const void* gguf, const float* x, float* y, uint32_t M, uint32_t K,
+                                  void* stream) {
+    if (M == 0) return EC_OK;
+    if (!gguf || !x || !y) return ec_set_error(EC_ERR_ARG, "ec_matvec_gguf_f32: null pointer");
+    if (fmt != EC_Q8_0 && fmt != EC_Q4_K && fmt != EC_Q2_K && fmt != EC_F16)
+        return ec_set_error(EC_ERR_UNSUPPORTED, "ec_matvec_gguf_f32: unsupported format");
+    hipLaunchKernelGGL(k_matvec_gguf_f32, dim3(M), dim3(64), 0, (hipStream_t)stream, fmt, (const uint8_t*)gguf, x, y,
+                       M, K);
+    EC_CHECK_LAUNCH();
+    return EC_OK;
+}
+
+extern "C" int ec_dequant_dot_int8(const float* q, const int8_t* keys, const float* scales, float* scores,
+                                   uint32_t dim, uint32_t seq_len, void* stream) {
+    if (seq_len == 0) return EC_OK;
+    if (!q || !keys || !scales || !scores) return ec_set_error(EC_ERR_ARG, "ec_dequant_dot_int8: null pointer");
+    hipLaunchKernelGGL(k_dequant_dot_int8, dim3(seq_len), dim3(64), 0, (hipStream_t)stream, q, keys, scales, scores,
+                       dim, seq_len);
+    EC_CHECK_LAUNCH();
+    return EC_OK;
+}
+
+extern "C" int ec_dequantize_to_fp16(int fmt, const void* src, uint16_t* dst, size_t n_weights, void* stream) {
+    size_t per = fmt == EC_Q8_0 ? 32 : 256;
+    if (fmt != EC_Q8_0 && fmt != EC_Q4_K && fmt != EC_Q2_K)
+        return ec_set_error(EC_ERR_UNSUPPORTED, "ec_dequantize_to_fp16: unsupported format");
+    size_t nblk = n_weights / per;
+    if (nblk == 0) return EC_OK;
+    if (!src || !dst) return ec_set_error(EC_ERR_ARG, "ec_dequantize_to_fp16: null pointer");
+    hipLaunchKernelGGL(k_dequant_fp16, dim3((nblk + 127) / 128), dim3(128), 0, (hipStream_t)stream, fmt,
+                       (const uint8_t*)src, dst, nblk);
+    EC_CHECK_LAUNCH();
+    return EC_OK;
+}

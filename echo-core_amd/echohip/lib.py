@@ -1,0 +1,156 @@
+"""ctypes binding of libechohip.so's C ABI (include/echo_hip.h).
+
+Arguments that are device buffers accept torch tensors (their data_ptr is
+passed) or raw integer addresses.  Every call checks the returned ec_status and
+raises EchoHipError with the library's message.  There is no fallback: if the
+library is missing the import fails loudly.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parents[1]
+LIBPATH = PKG / "libechohip.so"
+
+Q8_0 = 6
+Q4_K = 10
+Q2_K = 8
+F16 = 1
+
+_vp = C.c_void_p
+_u32 = C.c_uint32
+_u64 = C.c_uint64
+_sz = C.c_size_t
+
+_SIGS = {
+    "ec_device_init": [C.c_int],
+    "ec_quantize_rows": [_vp, _vp, _vp, _u32, _u32, _vp],
+    "ec_repack": [C.c_int, _vp, _vp, _u32, _u32, _vp],
+    "ec_quantize_act": [C.c_int, _vp, _vp, _u32, _u32, _vp],
+    "ec_act_unpack": [C.c_int, _vp, _vp, _vp, _u32, _u32, _vp],
+    "ec_matvec": [C.c_int, _vp, _vp, _vp, _u32, _u32, _u32, _u32, C.c_int, _vp],
+    "ec_block_dots": [C.c_int, _vp, _vp, _vp, _u32, _u32, _u32, _vp],
+    "ec_matvec_gguf_f32": [C.c_int, _vp, _vp, _vp, _u32, _u32, _vp],
+    "ec_dequant_dot_int8": [_vp, _vp, _vp, _vp, _u32, _u32, _vp],
+    "ec_dequantize_to_fp16": [C.c_int, _vp, _vp, _sz, _vp],
+    "ec_kv_append": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u64, _u32, _u32, _vp],
+    "ec_attn_decode": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u64, _u32, _u32, _u32, _u32, _vp, _vp],
+    "ec_deltanet": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp],
+    "ec_fill_random": [C.c_int, _vp, _u64, _u64, C.c_float, _u32, _vp],
+}
+_SIZE_FNS = {
+    "ec_tiled_bytes": [C.c_int, _u32, _u32],
+    "ec_act_bytes": [C.c_int, _u32, _u32],
+    "ec_attn_ws_bytes": [_u32, _u32, _u32, _u32],
+}
+
+
+class EchoHipError(RuntimeError):
+    pass
+
+
+def _ptr(x):
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    return x.data_ptr()
+
+
+class Lib:
+    def __init__(self, path: Path = LIBPATH):
+        if not path.exists():
+            raise FileNotFoundError(f"{path} is not built: run __graft_entry__.build() (make -C echo-core_amd)")
+        self.path = path
+        L = self.L = C.CDLL(str(path))
+        for name, args in _SIGS.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = C.c_int
+        for name, args in _SIZE_FNS.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = _sz
+        L.ec_last_error.restype = C.c_char_p
+
+    def _call(self, name, *args):
+        rc = getattr(self.L, name)(*args)
+        if rc != 0:
+            raise EchoHipError(f"{name} failed ({rc}): {self.L.ec_last_error().decode()}")
+
+    @staticmethod
+    def _stream(stream):
+        if stream is None:
+            import torch
+            return torch.cuda.current_stream().cuda_stream
+        return stream
+
+    # ---- sizes
+    def tiled_bytes(self, fmt, N, K):
+        return self.L.ec_tiled_bytes(fmt, N, K)
+
+    def act_bytes(self, fmt, M, K):
+        return self.L.ec_act_bytes(fmt, M, K)
+
+    def attn_ws_bytes(self, n_seq, n_heads, head_dim, max_ctx):
+        return self.L.ec_attn_ws_bytes(n_seq, n_heads, head_dim, max_ctx)
+
+    # ---- entry points
+    def device_init(self, dev=0):
+        self._call("ec_device_init", dev)
+
+    def quantize_rows(self, x, q, scales, rows, width, stream=None):
+        self._call("ec_quantize_rows", _ptr(x), _ptr(q), _ptr(scales), rows, width, self._stream(stream))
+
+    def repack(self, fmt, gguf, tiled, N, K, stream=None):
+        self._call("ec_repack", fmt, _ptr(gguf), _ptr(tiled), N, K, self._stream(stream))
+
+    def quantize_act(self, fmt, x, act, M, K, stream=None):
+        self._call("ec_quantize_act", fmt, _ptr(x), _ptr(act), M, K, self._stream(stream))
+
+    def act_unpack(self, fmt, act, xq, xd, M, K, stream=None):
+        self._call("ec_act_unpack", fmt, _ptr(act), _ptr(xq), _ptr(xd), M, K, self._stream(stream))
+
+    def matvec(self, fmt, tiled, act, y, M, N, K, ldy=None, accumulate=False, stream=None):
+        self._call("ec_matvec", fmt, _ptr(tiled), _ptr(act), _ptr(y), M, N, K, N if ldy is None else ldy,
+                   int(bool(accumulate)), self._stream(stream))
+
+    def block_dots(self, fmt, tiled, act, out, M, N, K, stream=None):
+        self._call("ec_block_dots", fmt, _ptr(tiled), _ptr(act), _ptr(out), M, N, K, self._stream(stream))
+
+    def matvec_gguf_f32(self, fmt, gguf, x, y, M, K, stream=None):
+        self._call("ec_matvec_gguf_f32", fmt, _ptr(gguf), _ptr(x), _ptr(y), M, K, self._stream(stream))
+
+    def dequant_dot_int8(self, q, keys, scales, scores, dim, seq, stream=None):
+        self._call("ec_dequant_dot_int8", _ptr(q), _ptr(keys), _ptr(scales), _ptr(scores), dim, seq,
+                   self._stream(stream))
+
+    def dequantize_to_fp16(self, fmt, src, dst, n, stream=None):
+        self._call("ec_dequantize_to_fp16", fmt, _ptr(src), _ptr(dst), n, self._stream(stream))
+
+    def kv_append(self, k, v, keys, vals, ks, vs, pos, n_seq, seq_stride, n_kv, head_dim, stream=None):
+        self._call("ec_kv_append", _ptr(k), _ptr(v), _ptr(keys), _ptr(vals), _ptr(ks), _ptr(vs), _ptr(pos), n_seq,
+                   seq_stride, n_kv, head_dim, self._stream(stream))
+
+    def attn_decode(self, q, keys, vals, ks, vs, out, ctx, n_seq, seq_stride, n_heads, n_kv, head_dim, max_ctx, ws,
+                    stream=None):
+        self._call("ec_attn_decode", _ptr(q), _ptr(keys), _ptr(vals), _ptr(ks), _ptr(vs), _ptr(out), _ptr(ctx),
+                   n_seq, seq_stride, n_heads, n_kv, head_dim, max_ctx, _ptr(ws), self._stream(stream))
+
+    def deltanet(self, state, q, k, v, decay, beta, out, T, n_seq, n_v, n_k, d_k, d_v, stream=None):
+        self._call("ec_deltanet", _ptr(state), _ptr(q), _ptr(k), _ptr(v), _ptr(decay), _ptr(beta), _ptr(out), T,
+                   n_seq, n_v, n_k, d_k, d_v, self._stream(stream))
+
+    def fill_random(self, kind, dst, n, seed, scale=1.0, K=0, stream=None):
+        self._call("ec_fill_random", kind, _ptr(dst), n, seed, scale, K, self._stream(stream))
+
+
+_LIB = None
+
+
+def load() -> Lib:
+    global _LIB
+    if _LIB is None:
+        _LIB = Lib()
+    return _LIB

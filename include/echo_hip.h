@@ -1,0 +1,135 @@
+/*
+ * echo_hip.h — the C ABI of libechohip.so, echo-core's decode hot path on
+ * AMD Instinct MI355X (gfx950).
+ *
+ * Every entry point takes DEVICE pointers (hipMalloc'd or managed), sizes and
+ * a hipStream_t passed as void* (NULL = the null stream), is stream-ordered and
+ * returns an ec_status (0 = success).  Nothing here allocates except where a
+ * function says so.  ec_last_error() returns a thread-local message for the
+ * last failure.  The reference-signature wrappers (include/kernels/quant.h,
+ * include/kernels/matvec.h, include/kv_cache.h, include/inference.h) are
+ * built on these.
+ *
+ * Reference correspondence (paths relative to the echo-core source tree):
+ *   ec_quantize_rows       src/kernels/quant.cpp:18-98  quantize_per_token_symmetric
+ *   ec_matvec_q8_0         src/kernels/matvec.cpp:62-87 matvec_q8_0 (y += W x), M tokens at once
+ *   ec_matvec_q4_K         src/kernels/matvec.cpp:92-142 matvec_q4_K
+ *   ec_kv_append           src/kv_cache.cpp:89-113 KVCache::append
+ *   ec_attn_decode         src/inference.cpp:330-405, echo-core-zig/src/inference/engine.zig:563-616
+ *   ec_deltanet            echo-core-zig/src/kernels/qwen_linear.zig:207-250
+ */
+#ifndef ECHO_HIP_H
+#define ECHO_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum ec_status {
+    EC_OK = 0,
+    EC_ERR_ARG = 1,      /* bad size, alignment or null pointer */
+    EC_ERR_HIP = 2,      /* a HIP runtime call failed */
+    EC_ERR_UNSUPPORTED = 3,
+};
+
+/* Weight formats, numbered as the reference's GGMLType (include/gguf_reader.h:13-41). */
+enum ec_wfmt { EC_F32 = 0, EC_F16 = 1, EC_Q8_0 = 6, EC_Q2_K = 8, EC_Q4_K = 10 };
+
+const char* ec_last_error(void);
+int ec_device_init(int device);
+
+/* ------------------------------------------------------------------ quantizer
+ * Reference per-row quantizer on device (bit-exact): scale = amax/127 (1 if the
+ * row is all zero); elements of whole 8-chunks q = sat8(rne(x*(1/scale))), tail
+ * elements q = clamp(round_half_away(x/scale), +-127). */
+int ec_quantize_rows(const float* x, int8_t* q, float* scales, uint32_t rows, uint32_t width, void* stream);
+
+/* ------------------------------------------------------- decode weight layout
+ * Weights are uploaded in GGUF byte order and repacked once into a "tiled"
+ * layout whose loads are 16-byte aligned and match the int8 MFMA operand
+ * layout.  Rows are grouped in tiles of 16 (N padded to 16); K is padded to
+ * 128 (Q8_0) or 256 (Q4_K) with zero blocks.  The repacked buffer holds the
+ * same bytes per block as GGUF (34 B per Q8_0 block, 144 B per Q4_K block).
+ * gguf: N rows of K/32*34 (Q8_0) or K/256*144 (Q4_K) bytes. */
+size_t ec_tiled_bytes(int fmt, uint32_t N, uint32_t K);
+int ec_repack(int fmt, const void* gguf, void* tiled, uint32_t N, uint32_t K, void* stream);
+
+/* --------------------------------------------------- activation quantization
+ * M (1..16) fp32 activation rows x[M][K] are quantized per 32-element block
+ * with the reference quantizer and stored in the lane order the matvec reads.
+ * Q8_0 blocks are 32 consecutive elements; Q4_K blocks are the 32 positions of
+ * one Q4_K sub-block (so every int8 block meets one 6-bit scale/min pair).
+ * K must be a multiple of 32; the buffer is padded like the weights. */
+size_t ec_act_bytes(int fmt, uint32_t M, uint32_t K);
+int ec_quantize_act(int fmt, const float* x, void* act, uint32_t M, uint32_t K, void* stream);
+/* Read back the quantized activation in natural order: xq[M][K] int8 (block
+ * grouping as above, i.e. Q4_K values in sub-block order) and xd[M][K/32]. */
+int ec_act_unpack(int fmt, const void* act, int8_t* xq, float* xd, uint32_t M, uint32_t K, void* stream);
+
+/* ------------------------------------------------------- decode matvec / GEMV
+ * y[m][n] (+)= sum_b d_w[n,b] * d_x[m,b] * isum[m,n,b] for M (1..16) token rows,
+ * isum = exact int32 dot of one 32-element block (Q8_0), and for Q4_K
+ * y += sum_sb d_x * (d*sc * isum - dmin*m * xsum).  accumulate != 0 adds into y
+ * (the reference's y += W x), else y is overwritten.  y is [M][ldy] fp32. */
+int ec_matvec(int fmt, const void* tiled, const void* act, float* y, uint32_t M, uint32_t N, uint32_t K,
+              uint32_t ldy, int accumulate, void* stream);
+/* The int32 block dots themselves: out[m][n][K/32] (parity contract). */
+int ec_block_dots(int fmt, const void* tiled, const void* act, int32_t* out, uint32_t M, uint32_t N, uint32_t K,
+                  void* stream);
+
+/* ------------------------------------------- reference-semantics fp32 matvec
+ * y[m] += W[m,:] . x over GGUF bytes with fp32 activations (no activation
+ * quantization), for the drop-in wrappers of include/kernels/matvec.h. */
+int ec_matvec_gguf_f32(int fmt, const void* gguf, const float* x, float* y, uint32_t M, uint32_t K, void* stream);
+/* scores[p] = sum_k K[p,k]*scale[p]*q[k] (src/kernels/quant.cpp:100-144). */
+int ec_dequant_dot_int8(const float* q, const int8_t* keys, const float* scales, float* scores, uint32_t dim,
+                        uint32_t seq_len, void* stream);
+/* GGUF blocks -> fp16 (src/kernels/quant.cpp:308-396). */
+int ec_dequantize_to_fp16(int fmt, const void* src, uint16_t* dst, size_t n_weights, void* stream);
+
+/* ----------------------------------------------------------------- KV cache
+ * Cache layout per layer (the reference's, include/kv_cache.h:7-19):
+ * keys/vals int8 [max_seq][n_kv][head_dim], kscales/vscales fp32 [max_seq][n_kv].
+ * ec_kv_append quantizes one token per sequence: k, v [n_seq][n_kv*head_dim];
+ * sequence s writes position pos[s] of its own cache (cache base + s*seq_stride
+ * elements for int8 arrays, s*seq_stride/head_dim for scales).  pos[s] < 0
+ * skips the sequence.  One scale per (token, kv_head) row of head_dim. */
+int ec_kv_append(const float* k, const float* v, int8_t* keys, int8_t* vals, float* kscales, float* vscales,
+                 const int32_t* pos, uint32_t n_seq, uint64_t seq_stride, uint32_t n_kv, uint32_t head_dim,
+                 void* stream);
+
+/* ------------------------------------------------------- INT8 attention decode
+ * out[s][h][:] = softmax_p(q[s][h].K[p, h%n_kv] * ks / sqrt(head_dim)) . V[p, h%n_kv] * vs
+ * over p < ctx[s] (ctx[s] <= 0: output zeros).  q, out: [n_seq][n_heads*head_dim].
+ * Split-K over the context: ws must hold ec_attn_ws_bytes(...) bytes. */
+size_t ec_attn_ws_bytes(uint32_t n_seq, uint32_t n_heads, uint32_t head_dim, uint32_t max_ctx);
+int ec_attn_decode(const float* q, const int8_t* keys, const int8_t* vals, const float* kscales,
+                   const float* vscales, float* out, const int32_t* ctx, uint32_t n_seq, uint64_t seq_stride,
+                   uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t max_ctx, void* ws, void* stream);
+
+/* --------------------------------------------------------------- delta-net
+ * Gated delta rule for T tokens of n_seq sequences (qwen_linear.zig:207-250):
+ *   S <- decay*S; kv = S^T k; delta = (v - kv)*beta; S += k (x) delta; o = S^T q/sqrt(d_k)
+ * state: [n_seq][n_v][d_v][d_k] fp32, i.e. each head's S stored TRANSPOSED
+ * relative to the reference (S[v][k], one contiguous d_k column per value
+ * channel).  q, k: [T][n_seq][n_k][d_k] (L2-normalised by the caller),
+ * v, out: [T][n_seq][n_v][d_v]; decay, beta: [T][n_seq][n_v] (beta after the
+ * sigmoid).  v-head h reads q/k head h/(n_v/n_k).  d_k must be 128 and d_v a
+ * multiple of 16.  The state stays on chip across the T tokens. */
+int ec_deltanet(float* state, const float* q, const float* k, const float* v, const float* decay, const float* beta,
+                float* out, uint32_t T, uint32_t n_seq, uint32_t n_v, uint32_t n_k, uint32_t d_k, uint32_t d_v,
+                void* stream);
+
+/* ----------------------------------------------------------------- random
+ * Fill device memory from the portable splitmix64 stream: element i gets
+ * bits of splitmix64(seed, i) (echohip/synth.py).  kind 0: uint8 bytes (low
+ * byte); 1: Q8_0 GGUF weights (qs ~ U{-127..127}, d = fp16(|N(0,1)|*scale));
+ * 2: fp32 N(0,1)*scale. */
+int ec_fill_random(int kind, void* dst, uint64_t n, uint64_t seed, float scale, uint32_t K, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,289 @@
+"""GPU parity: libechohip.so kernels vs the oracle on identical seeded inputs.
+
+Integer work (quantizer, block dots, KV int8) must be bit-exact; fp32 outputs
+must be within 1e-3 relative L2 of the oracle (the reference's kernels on the
+same quantized activations).
+"""
+import numpy as np
+import pytest
+
+from conftest import rel_l2
+from echohip import synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def empty(n, dtype):
+    import torch
+    return torch.zeros(n, dtype=dtype, device="cuda")
+
+
+# ------------------------------------------------------------------ quantizer
+@pytest.mark.parametrize("width", [4, 8, 12, 16, 32, 37, 256, 1024])
+def test_quantize_rows_bit_exact(hip, oc, golden, width):
+    import torch
+    x = golden[f"quant_w{width}_x"]
+    rows = x.size // width
+    q = empty(x.size, torch.int8)
+    s = empty(rows, torch.float32)
+    hip.quantize_rows(dev(x), q, s, rows, width)
+    assert np.array_equal(host(q), golden[f"quant_w{width}_q"])
+    assert np.array_equal(host(s).view(np.uint32), golden[f"quant_w{width}_s"].view(np.uint32))
+
+
+def test_quantize_rows_ties_zero(hip, golden):
+    import torch
+    x = golden["quant_ties_x"]
+    q = empty(x.size, torch.int8)
+    s = empty(1, torch.float32)
+    hip.quantize_rows(dev(x), q, s, 1, x.size)
+    assert np.array_equal(host(q), golden["quant_ties_q"])
+    z = np.zeros(32, np.float32)
+    q = empty(32, torch.int8)
+    hip.quantize_rows(dev(z), q, s, 1, 32)
+    assert host(s)[0] == 1.0 and not host(q).any()
+
+
+# --------------------------------------------------------- decode matvec core
+def _prep(hip, fmt, W, X):
+    """Upload GGUF weights, repack, quantize M activation rows."""
+    import torch
+    N = W.shape[0]
+    M, K = X.shape
+    Wd = dev(W)
+    tiled = empty(hip.tiled_bytes(fmt, N, K), torch.uint8)
+    hip.repack(fmt, Wd, tiled, N, K)
+    act = empty(hip.act_bytes(fmt, M, K), torch.uint8)
+    hip.quantize_act(fmt, dev(X.astype(np.float32)), act, M, K)
+    return tiled, act
+
+
+def _unpack(hip, fmt, act, M, K):
+    import torch
+    xq = empty(M * K, torch.int8)
+    xd = empty(M * K // 32, torch.float32)
+    hip.act_unpack(fmt, act, xq, xd, M, K)
+    return host(xq).reshape(M, K), host(xd).reshape(M, K // 32)
+
+
+CASES = [(1, 48, 512), (3, 40, 384), (8, 64, 2560), (16, 16, 256), (5, 33, 1024)]
+
+
+@pytest.mark.parametrize("M,N,K", CASES)
+def test_q8_0_act_and_block_dots_bit_exact(hip, oc, M, N, K):
+    import torch
+    W = synth.q8_0_blocks(1000 + K, N, K)
+    X = synth.activations(2000 + M, M * K).reshape(M, K)
+    tiled, act = _prep(hip, 6, W, X)
+    xq, xd = _unpack(hip, 6, act, M, K)
+    dots = empty(M * N * (K // 32), torch.int32)
+    hip.block_dots(6, tiled, act, dots, M, N, K)
+    dots = host(dots).reshape(M, N, K // 32)
+    for m in range(M):
+        rq, rd = oc.quantize_act_q8_0(X[m])
+        assert np.array_equal(xq[m], rq)
+        assert np.array_equal(xd[m].view(np.uint32), rd.view(np.uint32))
+        assert np.array_equal(dots[m], oc.block_dots_q8_0(W, rq))
+
+
+@pytest.mark.parametrize("M,N,K", CASES)
+def test_q8_0_matvec(hip, oc, M, N, K):
+    import torch
+    W = synth.q8_0_blocks(3000 + K, N, K)
+    X = synth.activations(4000 + M, M * K).reshape(M, K)
+    tiled, act = _prep(hip, 6, W, X)
+    y0 = synth.activations(5, M * N).reshape(M, N)
+    y = dev(y0)
+    hip.matvec(6, tiled, act, y, M, N, K, accumulate=True)
+    y = host(y)
+    for m in range(M):
+        rq, rd = oc.quantize_act_q8_0(X[m])
+        ref = oc.matvec_q8_0(W, oc.dequant_act_q8_0(rq, rd), y0[m])
+        assert rel_l2(y[m], ref) < TOL
+        assert rel_l2(y[m] - y0[m], ref - y0[m]) < 1e-5
+    # overwrite mode
+    y2 = dev(np.full((M, N), 7.0, np.float32))
+    hip.matvec(6, tiled, act, y2, M, N, K, accumulate=False)
+    assert np.allclose(host(y2), y - y0, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 48, 512), (3, 40, 768), (8, 64, 2560), (16, 16, 256)])
+def test_q4_K_act_and_block_dots_bit_exact(hip, oc, M, N, K):
+    import torch
+    W = synth.q4_K_blocks(5000 + K, N, K)
+    X = synth.activations(6000 + M, M * K).reshape(M, K)
+    tiled, act = _prep(hip, 10, W, X)
+    xq, xd = _unpack(hip, 10, act, M, K)
+    dots = empty(M * N * (K // 32), torch.int32)
+    hip.block_dots(10, tiled, act, dots, M, N, K)
+    dots = host(dots).reshape(M, N, K // 32)
+    for m in range(M):
+        rq, rd, _ = oc.quantize_act_q4_K(X[m])
+        assert np.array_equal(xq[m], rq)
+        assert np.array_equal(xd[m].view(np.uint32), rd.view(np.uint32))
+        assert np.array_equal(dots[m], oc.block_dots_q4_K(W, rq))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 48, 512), (3, 40, 768), (8, 64, 2560), (16, 16, 256)])
+def test_q4_K_matvec(hip, oc, M, N, K):
+    W = synth.q4_K_blocks(7000 + K, N, K)
+    X = synth.activations(8000 + M, M * K).reshape(M, K)
+    tiled, act = _prep(hip, 10, W, X)
+    y0 = synth.activations(9, M * N).reshape(M, N)
+    y = dev(y0)
+    hip.matvec(10, tiled, act, y, M, N, K, accumulate=True)
+    y = host(y)
+    for m in range(M):
+        rq, rd, _ = oc.quantize_act_q4_K(X[m])
+        ref = oc.matvec_q4_K(W, oc.dequant_act_q4_K(rq, rd), y0[m])
+        assert rel_l2(y[m] - y0[m], ref - y0[m]) < TOL
+
+
+# ------------------------------------------------- full benchmark shapes (M=1)
+@pytest.mark.parametrize("fmt,N,K", [(6, 9216, 2560), (10, 9216, 2560), (10, 2560, 9216)])
+def test_full_shape_matvec(hip, oc, fmt, N, K):
+    """The measured shapes: every int32 block dot bit-exact, y within 1e-3."""
+    import torch
+    W = synth.q8_0_blocks(0, N, K) if fmt == 6 else synth.q4_K_blocks(0, N, K)
+    x = synth.activations(1, K)
+    tiled, act = _prep(hip, fmt, W, x[None])
+    dots = empty(N * (K // 32), torch.int32)
+    hip.block_dots(fmt, tiled, act, dots, 1, N, K)
+    y = empty(N, torch.float32)
+    hip.matvec(fmt, tiled, act, y, 1, N, K)
+    dots, y = host(dots).reshape(N, K // 32), host(y)
+    if fmt == 6:
+        rq, rd = oc.quantize_act_q8_0(x)
+        assert np.array_equal(dots, oc.block_dots_q8_0(W, rq))
+        ref = oc.matvec_q8_0(W, oc.dequant_act_q8_0(rq, rd))
+    else:
+        rq, rd, _ = oc.quantize_act_q4_K(x)
+        assert np.array_equal(dots, oc.block_dots_q4_K(W, rq))
+        ref = oc.matvec_q4_K(W, oc.dequant_act_q4_K(rq, rd))
+    assert rel_l2(y, ref) < TOL
+
+
+# ------------------------------------------------ reference-semantics fp32 path
+def test_gguf_f32_matvec_golden(hip, golden):
+    x, y0 = golden["mv_x"], golden["mv_y0"]
+    for fmt, key in ((6, "q8"), (10, "q4")):
+        W = golden[f"{key}_W"]
+        y = dev(y0)
+        hip.matvec_gguf_f32(fmt, dev(W), dev(x), y, W.shape[0], x.size)
+        assert rel_l2(host(y), golden[f"{key}_matvec"]) < 1e-5
+
+
+def test_dequant_dot_int8_golden(hip, golden):
+    import torch
+    out = empty(64, torch.float32)
+    hip.dequant_dot_int8(dev(golden["int8dot_q"]), dev(golden["int8dot_k"]), dev(golden["int8dot_s"]), out, 256, 64)
+    ref = golden["int8dot_out"]
+    assert np.max(np.abs(host(out) - ref)) < 1e-4 * max(1.0, float(np.max(np.abs(ref))))
+
+
+def test_dequantize_to_fp16(hip, golden):
+    import torch
+    W = golden["q8_W"]
+    out = empty(W.shape[0] * 512, torch.float16)
+    hip.dequantize_to_fp16(6, dev(W), out, W.shape[0] * 512)
+    blk = W.reshape(-1, 34)
+    ref = (blk[:, 0:2].copy().view(np.float16).astype(np.float32) * blk[:, 2:].view(np.int8)).astype(np.float16)
+    assert np.array_equal(host(out).view(np.uint16), ref.reshape(-1).view(np.uint16))
+
+
+# ------------------------------------------------------------ KV + attention
+def _kv_case(oc, n_seq, ctxs, max_ctx, n_kv, hd, seed):
+    keys = np.zeros((n_seq, max_ctx * n_kv * hd), np.int8)
+    vals = np.zeros_like(keys)
+    ks = np.zeros((n_seq, max_ctx * n_kv), np.float32)
+    vs = np.zeros_like(ks)
+    kf, vf = [], []
+    for s in range(n_seq):
+        k = synth.activations(seed + 2 * s, ctxs[s] * n_kv * hd).reshape(ctxs[s], n_kv * hd)
+        v = synth.activations(seed + 2 * s + 1, ctxs[s] * n_kv * hd).reshape(ctxs[s], n_kv * hd)
+        for p in range(ctxs[s]):
+            oc.kv_append(k[p], v[p], keys[s], vals[s], ks[s], vs[s], p, n_kv, hd)
+        kf.append(k)
+        vf.append(v)
+    return keys, vals, ks, vs, kf, vf
+
+
+def test_kv_append_bit_exact(hip, oc):
+    import torch
+    n_seq, max_ctx, n_kv, hd = 3, 8, 4, 256
+    keys_r, vals_r, ks_r, vs_r, kf, vf = _kv_case(oc, n_seq, [5, 8, 2], max_ctx, n_kv, hd, 11)
+    keys = empty(n_seq * max_ctx * n_kv * hd, torch.int8)
+    vals = empty(n_seq * max_ctx * n_kv * hd, torch.int8)
+    ks = empty(n_seq * max_ctx * n_kv, torch.float32)
+    vs = empty(n_seq * max_ctx * n_kv, torch.float32)
+    for p in range(max_ctx):
+        pos = np.array([p if p < c else -1 for c in (5, 8, 2)], np.int32)
+        k = np.stack([kf[s][min(p, len(kf[s]) - 1)] for s in range(n_seq)])
+        v = np.stack([vf[s][min(p, len(vf[s]) - 1)] for s in range(n_seq)])
+        hip.kv_append(dev(k), dev(v), keys, vals, ks, vs, dev(pos), n_seq, max_ctx * n_kv * hd, n_kv, hd)
+    assert np.array_equal(host(keys).reshape(n_seq, -1), keys_r)
+    assert np.array_equal(host(vals).reshape(n_seq, -1), vals_r)
+    assert np.array_equal(host(ks).reshape(n_seq, -1).view(np.uint32), ks_r.view(np.uint32))
+    assert np.array_equal(host(vs).reshape(n_seq, -1).view(np.uint32), vs_r.view(np.uint32))
+
+
+@pytest.mark.parametrize("ctxs,max_ctx", [([1], 1), ([7], 7), ([512], 512), ([4096], 4096),
+                                          ([300, 1, 0, 777], 800)])
+def test_attention_decode(hip, oc, ctxs, max_ctx):
+    import torch
+    n_heads, n_kv, hd = 16, 4, 256
+    n_seq = len(ctxs)
+    keys, vals, ks, vs, _, _ = _kv_case(oc, n_seq, ctxs, max_ctx, n_kv, hd, 50)
+    q = synth.activations(77, n_seq * n_heads * hd).reshape(n_seq, n_heads * hd)
+    out = empty(n_seq * n_heads * hd, torch.float32)
+    ws = empty(hip.attn_ws_bytes(n_seq, n_heads, hd, max_ctx), torch.uint8)
+    hip.attn_decode(dev(q), dev(keys), dev(vals), dev(ks), dev(vs), out, dev(np.array(ctxs, np.int32)), n_seq,
+                    max_ctx * n_kv * hd, n_heads, n_kv, hd, max_ctx, ws)
+    out = host(out).reshape(n_seq, n_heads, hd)
+    for s in range(n_seq):
+        if ctxs[s] == 0:
+            assert not out[s].any()
+            continue
+        ref = oc.attn_decode(q[s], keys[s], vals[s], ks[s], vs[s], n_heads, n_kv, hd, ctxs[s])
+        assert rel_l2(out[s], ref) < TOL
+
+
+# ------------------------------------------------------------------- delta-net
+@pytest.mark.parametrize("T,n_seq,n_v,n_k", [(1, 1, 32, 32), (16, 2, 32, 16), (64, 1, 4, 4)])
+def test_deltanet(hip, oc, T, n_seq, n_v, n_k):
+    d = 128
+    rng = np.random.default_rng(T + n_v)
+    S0 = (rng.standard_normal((n_seq, n_v, d, d)) * 0.02).astype(np.float32)  # reference layout [k][v]
+    q = rng.standard_normal((T, n_seq, n_k, d)).astype(np.float32)
+    k = rng.standard_normal((T, n_seq, n_k, d)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    v = rng.standard_normal((T, n_seq, n_v, d)).astype(np.float32)
+    dec = synth.sigmoid(rng.normal(2, 0.5, (T, n_seq, n_v))).astype(np.float32)
+    bet = synth.sigmoid(rng.normal(0, 1, (T, n_seq, n_v))).astype(np.float32)
+    state = dev(np.ascontiguousarray(S0.transpose(0, 1, 3, 2)))  # device layout [v][k]
+    import torch
+    out = empty(T * n_seq * n_v * d, torch.float32)
+    hip.deltanet(state, dev(q), dev(k), dev(v), dev(dec), dev(bet), out, T, n_seq, n_v, n_k, d, d)
+    out = host(out).reshape(T, n_seq, n_v, d)
+    S = host(state).reshape(n_seq, n_v, d, d).transpose(0, 1, 3, 2)
+    Sr = S0.copy()
+    ref_o = np.zeros_like(out)
+    for t in range(T):
+        for s in range(n_seq):
+            ref_o[t, s] = oc.deltanet_step(Sr[s], q[t, s], k[t, s], v[t, s], dec[t, s], bet[t, s], n_v, n_k, d, d)
+    assert rel_l2(out, ref_o) < TOL
+    assert rel_l2(S, Sr) < TOL
