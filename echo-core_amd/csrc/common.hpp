@@ -4,6 +4,8 @@
 #include <hip/hip_fp16.h>
 #include <cstdint>
 #include <cstddef>
+#include <cstdlib>
+#include <cstdio>
 
 #include "echo_hip.h"
 

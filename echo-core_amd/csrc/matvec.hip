@@ -7,7 +7,8 @@
 // weights x 16 weight rows, so a wave turns 16 rows x 32 elements of weights
 // into 16x16 exact int32 dots per instruction.  The kernel is a weight stream:
 // each wave reads a contiguous run of 2 KB chunks of the tiled layout (two
-// 16-byte loads per lane per chunk), the 16-token activation operand comes
+// 16-byte loads per lane per chunk, each instruction one contiguous 1 KB),
+// the 16-token activation operand comes
 // from L1/L2, and the fp32 epilogue applies the per-block scales.  The K range
 // of one 16-row tile is split across the waves of a workgroup and reduced
 // through LDS in a fixed order (deterministic results).
@@ -56,54 +57,141 @@ __device__ __forceinline__ void reduce_store(float (&acc)[4], float* red, float*
     }
 }
 
+// ------------------------------------------------------------ wave program
+// Every wave owns GPW consecutive chunks (2 KB Q8_0 groups or 2.3 KB Q4_K
+// super-blocks) of one 16-row tile and runs straight-line code:
+//   1. load the activation scales of its blocks (vector loads, issued first),
+//   2. load all GPW weight chunks and activation operands (no branches: an
+//      index past the wave's range is clamped, the chunk is loaded again and
+//      not computed; an empty token slot reads token 0 and is zeroed at use),
+//   3. stage the scales in the wave's own LDS slice (waits only for step 1),
+//   4. MFMA + fp32 epilogue chunk by chunk as the loads land.
+// With no data-dependent branch around a load, the compiler's waitcnts count
+// exactly and GPW*2 KB per wave stay in flight.
+template <int MT>
+constexpr int slots() { return MT == 1 ? 1 : (MT <= 4 ? 4 : (MT <= 8 ? 8 : 16)); }
+
+// Scales of blocks [b0, b0+NB) for token slots [0, S): LDS slice xs[NB][S],
+// source layout token-major [16][nblk].  Values for tokens >= M are zero.
+template <int NB, int S>
+struct ScaleStage {
+    static constexpr int N = NB * S;
+    static constexpr int PER_LANE = (N + 63) / 64;
+    float v[PER_LANE];
+    __device__ __forceinline__ void load(const float* __restrict__ src, uint32_t nblk, uint32_t b0, uint32_t M,
+                                         uint32_t lane) {
+#pragma unroll
+        for (int i = 0; i < PER_LANE; ++i) {
+            const uint32_t e = lane + 64 * i;
+            const uint32_t b = b0 + e / S, t = e % S;
+            const bool ok = e < (uint32_t)N && b < nblk && t < M;
+            const float x = src[(size_t)(ok ? t : 0) * nblk + (ok ? b : 0)];
+            v[i] = ok ? x : 0.0f;
+        }
+    }
+    __device__ __forceinline__ void store(float* xs, uint32_t lane) const {
+#pragma unroll
+        for (int i = 0; i < PER_LANE; ++i) {
+            const uint32_t e = lane + 64 * i;
+            if (e < (uint32_t)N) xs[e] = v[i];
+        }
+    }
+};
+
+// A wave's activation operand bytes for its chunks form one contiguous range
+// (the act layout is chunk-major); it is loaded with full 1 KB-per-instruction
+// loads, clamped to the buffer, and staged in LDS next to the scales.
+template <int MAXB>
+struct ByteStage {
+    static constexpr int PER_LANE = (MAXB + 1023) / 1024;
+    uint4 v[PER_LANE];
+    __device__ __forceinline__ void load(const uint8_t* __restrict__ src, size_t begin, size_t nbytes, size_t limit,
+                                         uint32_t lane) {
+#pragma unroll
+        for (int i = 0; i < PER_LANE; ++i) {
+            const size_t off = begin + 1024 * i + 16 * lane;
+            const bool ok = 1024 * i + 16 * lane < nbytes && off + 16 <= limit;
+            const uint4 x = *(const uint4*)(src + (ok ? off : 0));
+            v[i] = ok ? x : make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    __device__ __forceinline__ void store(uint8_t* dst, size_t nbytes, uint32_t lane) const {
+#pragma unroll
+        for (int i = 0; i < PER_LANE; ++i)
+            if (1024 * i + 16 * lane < nbytes) *(uint4*)(dst + 1024 * i + 16 * lane) = v[i];
+    }
+};
+
 // --------------------------------------------------------------------- Q8_0
-template <int MT, bool DOTS>
+template <int MT, bool DOTS, int GPW>
 __global__ __launch_bounds__(1024) void k_mv_q8_0(const uint8_t* __restrict__ W, const uint8_t* __restrict__ act,
                                                   float* __restrict__ y, int32_t* __restrict__ dots, uint32_t M,
-                                                  uint32_t N, uint32_t K, uint32_t nG, uint32_t gpw, uint32_t xd_off,
-                                                  uint32_t ldy, int accumulate) {
-    extern __shared__ float red[];
+                                                  uint32_t N, uint32_t K, uint32_t nG, uint32_t xd_off, uint32_t ldy,
+                                                  int accumulate) {
+    extern __shared__ float lds[];
     constexpr int R = MT < 4 ? MT : 4;
-    const uint32_t t = blockIdx.x;
-    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const uint32_t row = lane & 15, g = lane >> 4;
-    const uint32_t G0 = w * gpw;
-    const uint32_t G1 = min(nG, G0 + gpw);
+    constexpr int S = slots<MT>();
+    constexpr int NB = 4 * GPW;
+    const uint32_t t = blockIdx.x, lane = threadIdx.x & 63, row = lane & 15, g = lane >> 4;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nw = blockDim.x >> 6;
+    constexpr int ACT_MAX = GPW * 128 * S;  // act bytes per wave pass (M <= S tokens)
+    float* red = lds;
+    float* xs = lds + nw * 256 + w * (NB * S + ACT_MAX / 4);
+    uint8_t* as = (uint8_t*)(xs + NB * S);
     const uint8_t* wt = W + (size_t)t * nG * kQ8TChunk;
-    const float* __restrict__ xd = (const float*)(act + xd_off);
     const bool aval = row < M;
+    const size_t act_bytes = (size_t)nG * 128 * M;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (uint32_t G = G0; G < G1; ++G) {
-        const uint8_t* ch = wt + (size_t)G * kQ8TChunk;
-        const uint4 b01 = *(const uint4*)(ch + lane * 32);
-        const uint4 b23 = *(const uint4*)(ch + lane * 32 + 16);
-        const uint2 dw = *(const uint2*)(ch + 2048 + row * 8);
-        uint4 a01 = {0u, 0u, 0u, 0u}, a23 = {0u, 0u, 0u, 0u};
-        if (aval) {
-            const uint8_t* ap = act + (((size_t)G * 4 + g) * M + row) * 32;
-            a01 = *(const uint4*)ap;
-            a23 = *(const uint4*)(ap + 16);
+
+    for (uint32_t G0 = w * GPW; G0 < nG; G0 += nw * GPW) {
+        ScaleStage<NB, S> sc;
+        ByteStage<ACT_MAX> ast;
+        if constexpr (!DOTS) sc.load((const float*)(act + xd_off), nG * 4, 4 * G0, M, lane);
+        ast.load(act, (size_t)G0 * 128 * M, (size_t)GPW * 128 * M, act_bytes, lane);
+        uint4 b01[GPW], b23[GPW];
+        uint2 dw[GPW];
+#pragma unroll
+        for (int u = 0; u < GPW; ++u) {
+            const uint32_t G = min(G0 + u, nG - 1);
+            const uint8_t* ch = wt + (size_t)G * kQ8TChunk;
+            b01[u] = *(const uint4*)(ch + lane * 16);
+            b23[u] = *(const uint4*)(ch + 1024 + lane * 16);
+            dw[u] = *(const uint2*)(ch + 2048 + row * 8);
         }
-        const long A[4] = {pack2(a01.x, a01.y), pack2(a01.z, a01.w), pack2(a23.x, a23.y), pack2(a23.z, a23.w)};
-        const long B[4] = {pack2(b01.x, b01.y), pack2(b01.z, b01.w), pack2(b23.x, b23.y), pack2(b23.z, b23.w)};
-        const float dwf[4] = {h2f(dw.x & 0xFFFF), h2f(dw.x >> 16), h2f(dw.y & 0xFFFF), h2f(dw.y >> 16)};
+        if constexpr (!DOTS) sc.store(xs, lane);
+        ast.store(as, (size_t)GPW * 128 * M, lane);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const v4i c = mfma_i8(A[j], B[j]);
-            const uint32_t b = 4 * G + j;
-            if constexpr (DOTS) {
-                const uint32_t n = 16 * t + row, nb = K / 32;
-                if (n < N && b < nb)
-                    for (int r = 0; r < 4; ++r)
-                        if (4 * g + r < M) dots[((size_t)(4 * g + r) * N + n) * nb + b] = c[r];
-            } else if constexpr (MT == 1) {
-                const float dx = xd[b * 16];
-                acc[0] = fmaf((float)c[0], dwf[j] * dx, acc[0]);
-            } else {
-                const float4 dx = *(const float4*)(xd + b * 16 + 4 * g);
-                const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
+        for (int u = 0; u < GPW; ++u) {
+            const uint32_t G = G0 + u;
+            if (G >= nG) break;
+            const uint8_t* ap = as + (((size_t)u * 4 + g) * M + (aval ? row : 0)) * 32;
+            const uint4 a01 = *(const uint4*)ap;
+            const uint4 a23 = *(const uint4*)(ap + 16);
+            const long A[4] = {aval ? pack2(a01.x, a01.y) : 0l, aval ? pack2(a01.z, a01.w) : 0l,
+                               aval ? pack2(a23.x, a23.y) : 0l, aval ? pack2(a23.z, a23.w) : 0l};
+            const long B[4] = {pack2(b01[u].x, b01[u].y), pack2(b01[u].z, b01[u].w), pack2(b23[u].x, b23[u].y),
+                               pack2(b23[u].z, b23[u].w)};
+            const float dwf[4] = {h2f(dw[u].x & 0xFFFF), h2f(dw[u].x >> 16), h2f(dw[u].y & 0xFFFF),
+                                  h2f(dw[u].y >> 16)};
 #pragma unroll
-                for (int r = 0; r < R; ++r) acc[r] = fmaf((float)c[r], dwf[j] * dxv[r], acc[r]);
+            for (int j = 0; j < 4; ++j) {
+                const v4i cc = mfma_i8(A[j], B[j]);
+                const uint32_t b = 4 * G + j;
+                if constexpr (DOTS) {
+                    const uint32_t n = 16 * t + row, nb = K / 32;
+                    if (n < N && b < nb)
+                        for (int r = 0; r < 4; ++r)
+                            if (4 * g + r < M) dots[((size_t)(4 * g + r) * N + n) * nb + b] = cc[r];
+                } else if constexpr (MT == 1) {
+                    acc[0] = fmaf((float)cc[0], dwf[j] * xs[4 * u + j], acc[0]);
+                } else {
+                    const float4 dx =
+                        (4 * g < S) ? *(const float4*)(xs + (4 * u + j) * S + 4 * g) : make_float4(0.f, 0.f, 0.f, 0.f);
+                    const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+                    for (int r = 0; r < R; ++r) acc[r] = fmaf((float)cc[r], dwf[j] * dxv[r], acc[r]);
+                }
             }
         }
     }
@@ -123,66 +211,92 @@ __device__ __forceinline__ void q4k_scale_min(const uint32_t (&q)[3], int s, uin
     }
 }
 
-template <int MT, bool DOTS>
+template <int MT, bool DOTS, int GPW>
 __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W, const uint8_t* __restrict__ act,
                                                   float* __restrict__ y, int32_t* __restrict__ dots, uint32_t M,
-                                                  uint32_t N, uint32_t K, uint32_t nB, uint32_t gpw, uint32_t xd_off,
+                                                  uint32_t N, uint32_t K, uint32_t nB, uint32_t xd_off,
                                                   uint32_t dxs_off, uint32_t ldy, int accumulate) {
-    extern __shared__ float red[];
+    extern __shared__ float lds[];
     constexpr int R = MT < 4 ? MT : 4;
-    const uint32_t t = blockIdx.x;
-    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const uint32_t row = lane & 15, g = lane >> 4;
-    const uint32_t B0 = w * gpw;
-    const uint32_t B1 = min(nB, B0 + gpw);
+    constexpr int S = slots<MT>();
+    constexpr int NB = 8 * GPW;
+    const uint32_t t = blockIdx.x, lane = threadIdx.x & 63, row = lane & 15, g = lane >> 4;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nw = blockDim.x >> 6;
+    constexpr int ACT_MAX = GPW * 256 * S;
+    float* red = lds;
+    float* xs = lds + nw * 256 + w * (2 * NB * S + ACT_MAX / 4);
+    float* xms = xs + NB * S;
+    uint8_t* as = (uint8_t*)(xms + NB * S);
     const uint8_t* wt = W + (size_t)t * nB * kQ4TChunk;
-    const float* __restrict__ xd = (const float*)(act + xd_off);
-    const float* __restrict__ dxs = (const float*)(act + dxs_off);
     const bool aval = row < M;
+    const size_t act_bytes = (size_t)nB * 256 * M;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (uint32_t b = B0; b < B1; ++b) {
-        const uint8_t* ch = wt + (size_t)b * kQ4TChunk;
-        const uint4 q0 = *(const uint4*)(ch + lane * 32);
-        const uint4 q1 = *(const uint4*)(ch + lane * 32 + 16);
-        const uint4 hdr = *(const uint4*)(ch + 2048 + row * 16);
-        uint4 a[4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
-        if (aval) {
-            const uint8_t* ap = act + (((size_t)b * 4 + g) * M + row) * 64;
+
+    for (uint32_t B0 = w * GPW; B0 < nB; B0 += nw * GPW) {
+        ScaleStage<NB, S> sd, sm;
+        ByteStage<ACT_MAX> ast;
+        if constexpr (!DOTS) {
+            sd.load((const float*)(act + xd_off), nB * 8, 8 * B0, M, lane);
+            sm.load((const float*)(act + dxs_off), nB * 8, 8 * B0, M, lane);
+        }
+        ast.load(act, (size_t)B0 * 256 * M, (size_t)GPW * 256 * M, act_bytes, lane);
+        uint4 q0[GPW], q1[GPW], hdr[GPW];
+#pragma unroll
+        for (int u = 0; u < GPW; ++u) {
+            const uint32_t b = min(B0 + u, nB - 1);
+            const uint8_t* ch = wt + (size_t)b * kQ4TChunk;
+            q0[u] = *(const uint4*)(ch + lane * 16);
+            q1[u] = *(const uint4*)(ch + 1024 + lane * 16);
+            hdr[u] = *(const uint4*)(ch + 2048 + row * 16);
+        }
+        if constexpr (!DOTS) {
+            sd.store(xs, lane);
+            sm.store(xms, lane);
+        }
+        ast.store(as, (size_t)GPW * 256 * M, lane);
+#pragma unroll
+        for (int u = 0; u < GPW; ++u) {
+            const uint32_t b = B0 + u;
+            if (b >= nB) break;
+            uint4 a[4];
+            const uint8_t* ap = as + (((size_t)u * 4 + g) * M + (aval ? row : 0)) * 64;
 #pragma unroll
             for (int i = 0; i < 4; ++i) a[i] = *(const uint4*)(ap + 16 * i);
-        }
-        const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-        const uint32_t aw[16] = {a[0].x, a[0].y, a[0].z, a[0].w, a[1].x, a[1].y, a[1].z, a[1].w,
-                                 a[2].x, a[2].y, a[2].z, a[2].w, a[3].x, a[3].y, a[3].z, a[3].w};
-        const float d = h2f(hdr.x & 0xFFFF), dmin = h2f(hdr.x >> 16);
-        const uint32_t scb[3] = {hdr.y, hdr.z, hdr.w};
+            const uint32_t qw[8] = {q0[u].x, q0[u].y, q0[u].z, q0[u].w, q1[u].x, q1[u].y, q1[u].z, q1[u].w};
+            const uint32_t aw[16] = {a[0].x, a[0].y, a[0].z, a[0].w, a[1].x, a[1].y, a[1].z, a[1].w,
+                                     a[2].x, a[2].y, a[2].z, a[2].w, a[3].x, a[3].y, a[3].z, a[3].w};
+            const float d = h2f(hdr[u].x & 0xFFFF), dmin = h2f(hdr[u].x >> 16);
+            const uint32_t scb[3] = {hdr[u].y, hdr[u].z, hdr[u].w};
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const uint32_t lo = qw[s] & 0x0F0F0F0Fu, hi = (qw[s] >> 4) & 0x0F0F0F0Fu;
-            const v4i c = mfma_i8(pack2(aw[2 * s], aw[2 * s + 1]), pack2(lo, hi));
-            const uint32_t sbi = 8 * b + s;
-            if constexpr (DOTS) {
-                const uint32_t n = 16 * t + row, nsb = K / 32;
-                if (n < N && sbi < nsb)
-                    for (int r = 0; r < 4; ++r)
-                        if (4 * g + r < M) dots[((size_t)(4 * g + r) * N + n) * nsb + sbi] = c[r];
-            } else {
-                uint32_t sc, mn;
-                q4k_scale_min(scb, s, sc, mn);
-                const float dsc = d * (float)sc, dmn = dmin * (float)mn;
-                if constexpr (MT == 1) {
-                    const float dx = xd[sbi * 16], dxm = dxs[sbi * 16];
-                    acc[0] = fmaf((float)c[0], dsc * dx, acc[0]);
-                    acc[0] = fmaf(-dmn, dxm, acc[0]);
+            for (int s = 0; s < 8; ++s) {
+                const uint32_t lo = qw[s] & 0x0F0F0F0Fu, hi = (qw[s] >> 4) & 0x0F0F0F0Fu;
+                const v4i cc = mfma_i8(aval ? pack2(aw[2 * s], aw[2 * s + 1]) : 0l, pack2(lo, hi));
+                const uint32_t sbi = 8 * b + s;
+                if constexpr (DOTS) {
+                    const uint32_t n = 16 * t + row, nsb = K / 32;
+                    if (n < N && sbi < nsb)
+                        for (int r = 0; r < 4; ++r)
+                            if (4 * g + r < M) dots[((size_t)(4 * g + r) * N + n) * nsb + sbi] = cc[r];
                 } else {
-                    const float4 dx = *(const float4*)(xd + sbi * 16 + 4 * g);
-                    const float4 dm = *(const float4*)(dxs + sbi * 16 + 4 * g);
-                    const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
-                    const float dmv[4] = {dm.x, dm.y, dm.z, dm.w};
+                    uint32_t scv, mnv;
+                    q4k_scale_min(scb, s, scv, mnv);
+                    const float dsc = d * (float)scv, dmn = dmin * (float)mnv;
+                    const int e = 8 * u + s;
+                    if constexpr (MT == 1) {
+                        acc[0] = fmaf((float)cc[0], dsc * xs[e], acc[0]);
+                        acc[0] = fmaf(-dmn, xms[e], acc[0]);
+                    } else {
+                        const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+                        const float4 dx = (4 * g < S) ? *(const float4*)(xs + e * S + 4 * g) : z4;
+                        const float4 dm = (4 * g < S) ? *(const float4*)(xms + e * S + 4 * g) : z4;
+                        const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
+                        const float dmv[4] = {dm.x, dm.y, dm.z, dm.w};
 #pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        acc[r] = fmaf((float)c[r], dsc * dxv[r], acc[r]);
-                        acc[r] = fmaf(-dmn, dmv[r], acc[r]);
+                        for (int r = 0; r < R; ++r) {
+                            acc[r] = fmaf((float)cc[r], dsc * dxv[r], acc[r]);
+                            acc[r] = fmaf(-dmn, dmv[r], acc[r]);
+                        }
                     }
                 }
             }
@@ -319,38 +433,77 @@ __global__ void k_dequant_fp16(int fmt, const uint8_t* __restrict__ src, uint16_
     }
 }
 
-// Waves per workgroup for one 16-row tile: aim for ~4096 waves in flight and
-// at least one chunk per wave.
-static void split_k(uint32_t n_tiles, uint32_t n_chunks, uint32_t& nw, uint32_t& per_wave) {
-    uint32_t target = (4096 + n_tiles - 1) / n_tiles;
-    target = target < 1 ? 1 : (target > 16 ? 16 : target);
-    per_wave = (n_chunks + target - 1) / target;
-    nw = (n_chunks + per_wave - 1) / per_wave;
+// Chunks per wave (GPW, compile-time) and waves per 16-row tile (nw <= 16):
+// aim for EC_MV_TARGET_WAVES waves in total (default 4096) with every tile's K
+// range covered by one pass where possible.
+static uint32_t target_waves() {
+    static uint32_t v = [] {
+        const char* e = getenv("EC_MV_TARGET_WAVES");
+        return e ? (uint32_t)atoi(e) : 4096u;
+    }();
+    return v;
+}
+
+static void plan(uint32_t n_tiles, uint32_t n_chunks, int max_gpw, int& gpw, uint32_t& nw) {
+    const uint32_t want = (target_waves() + n_tiles - 1) / n_tiles;  // waves per tile wanted
+    gpw = (int)((n_chunks + want - 1) / (want ? want : 1));
+    if (gpw < 1) gpw = 1;
+    if (gpw > max_gpw) gpw = max_gpw;
+    nw = (n_chunks + gpw - 1) / gpw;
+    if (nw > 16) nw = 16;  // larger K: several passes per wave
+}
+
+template <int MT, bool DOTS, int GPW>
+static void launch_q8_g(const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N, uint32_t K,
+                        uint32_t ldy, int accumulate, uint32_t nw, hipStream_t st) {
+    const ActLayout L = act_layout(EC_Q8_0, M, K);
+    const uint32_t nT = round_up(N, 16) / 16, nG = L.Kp / 128;
+    const size_t lds = ((size_t)nw * 256 + (size_t)nw * (4 * GPW * slots<MT>() + GPW * 128 * slots<MT>() / 4)) *
+                       sizeof(float);
+    hipLaunchKernelGGL((k_mv_q8_0<MT, DOTS, GPW>), dim3(nT), dim3(64 * nw), lds, st, (const uint8_t*)W,
+                       (const uint8_t*)act, y, dots, M, N, K, nG, (uint32_t)L.xd_off, ldy, accumulate);
 }
 
 template <int MT, bool DOTS>
 static void launch_q8(const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N, uint32_t K,
                       uint32_t ldy, int accumulate, hipStream_t st) {
-    const ActLayout L = act_layout(EC_Q8_0, M, K);
-    const uint32_t nT = round_up(N, 16) / 16, nG = L.Kp / 128;
-    uint32_t nw, gpw;
-    split_k(nT, nG, nw, gpw);
-    const size_t lds = nw > 1 ? (size_t)nw * 64 * 4 * sizeof(float) : 0;
-    hipLaunchKernelGGL((k_mv_q8_0<MT, DOTS>), dim3(nT), dim3(64 * nw), lds, st, (const uint8_t*)W,
-                       (const uint8_t*)act, y, dots, M, N, K, nG, gpw, (uint32_t)L.xd_off, ldy, accumulate);
+    const uint32_t nT = round_up(N, 16) / 16, nG = round_up(K, 128) / 128;
+    int gpw;
+    uint32_t nw;
+    plan(nT, nG, 5, gpw, nw);  // GPW <= 5 keeps every variant under 128 VGPRs (1024 threads)
+    switch (gpw) {
+        case 1: launch_q8_g<MT, DOTS, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
+        case 2: launch_q8_g<MT, DOTS, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
+        case 3: launch_q8_g<MT, DOTS, 3>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
+        case 4: launch_q8_g<MT, DOTS, 4>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
+        default: launch_q8_g<MT, DOTS, 5>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
+    }
+}
+
+template <int MT, bool DOTS, int GPW>
+static void launch_q4_g(const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N, uint32_t K,
+                        uint32_t ldy, int accumulate, uint32_t nw, hipStream_t st) {
+    const ActLayout L = act_layout(EC_Q4_K, M, K);
+    const uint32_t nT = round_up(N, 16) / 16, nB = L.Kp / 256;
+    const size_t lds =
+        ((size_t)nw * 256 + (size_t)nw * (2 * 8 * GPW * slots<MT>() + GPW * 256 * slots<MT>() / 4)) * sizeof(float);
+    hipLaunchKernelGGL((k_mv_q4_K<MT, DOTS, GPW>), dim3(nT), dim3(64 * nw), lds, st, (const uint8_t*)W,
+                       (const uint8_t*)act, y, dots, M, N, K, nB, (uint32_t)L.xd_off, (uint32_t)L.dxs_off, ldy,
+                       accumulate);
 }
 
 template <int MT, bool DOTS>
 static void launch_q4(const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N, uint32_t K,
                       uint32_t ldy, int accumulate, hipStream_t st) {
-    const ActLayout L = act_layout(EC_Q4_K, M, K);
-    const uint32_t nT = round_up(N, 16) / 16, nB = L.Kp / 256;
-    uint32_t nw, gpw;
-    split_k(nT, nB, nw, gpw);
-    const size_t lds = nw > 1 ? (size_t)nw * 64 * 4 * sizeof(float) : 0;
-    hipLaunchKernelGGL((k_mv_q4_K<MT, DOTS>), dim3(nT), dim3(64 * nw), lds, st, (const uint8_t*)W,
-                       (const uint8_t*)act, y, dots, M, N, K, nB, gpw, (uint32_t)L.xd_off, (uint32_t)L.dxs_off, ldy,
-                       accumulate);
+    const uint32_t nT = round_up(N, 16) / 16, nB = round_up(K, 256) / 256;
+    int gpw;
+    uint32_t nw;
+    plan(nT, nB, MT == 1 ? 3 : 1, gpw, nw);
+    switch (gpw) {
+        case 1: launch_q4_g<MT, DOTS, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
+        case 2: launch_q4_g<MT, DOTS, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
+        default: launch_q4_g<MT, DOTS, 3>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
+    }
 }
 
 template <bool DOTS>
@@ -370,9 +523,28 @@ static int dispatch(int fmt, const void* W, const void* act, float* y, int32_t* 
     return EC_OK;
 }
 
+// Plain streaming read (HBM bandwidth calibration): each thread sums 16-byte
+// loads with a grid stride (nothing is written unless a checksum hits a magic value).
+__global__ __launch_bounds__(256) void k_stream_read(const uint4* __restrict__ src, size_t n16, uint32_t* out) {
+    uint32_t acc = 0;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x) {
+        const uint4 v = src[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == 0x9E3779B9u) out[blockIdx.x] = acc;  // keeps the loads live; practically never taken
+}
+
 }  // namespace ec
 
 using namespace ec;
+
+extern "C" int ec_stream_read(const void* src, size_t bytes, uint32_t* out, uint32_t blocks, void* stream) {
+    if (!src || !out || bytes % 16 || blocks == 0) return ec_set_error(EC_ERR_ARG, "ec_stream_read: bad argument");
+    hipLaunchKernelGGL(k_stream_read, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const uint4*)src, bytes / 16,
+                       out);
+    EC_CHECK_LAUNCH();
+    return EC_OK;
+}
 
 static int check_mv(int fmt, const void* W, const void* act, const void* out, uint32_t M, uint32_t N, uint32_t K,
                     const char* who) {

@@ -4,16 +4,19 @@
 //
 // Q8_0 tiled weights ("Q8T"): rows in tiles of 16, K in groups of 4 blocks
 // (128 elements).  Chunk (tile t, group G) = 2176 bytes at (t*nG+G)*2176:
-//   [0,2048)   lane l (0..63) owns bytes [32l, 32l+32): for j=0..3 the 8 int8
-//              weights W[16t + l%16][128G + 32j + 8(l/16) .. +8]
+//   [0,1024)    lane l (0..63) owns bytes [16l, 16l+16): for j=0..1 the 8 int8
+//               weights W[16t + l%16][128G + 32j + 8(l/16) .. +8]
+//   [1024,2048) the same for j=2..3 at 1024 + 16l
 //   [2048,2176) row r (0..15) owns 8 bytes: fp16 d of blocks 4G..4G+3
 // Lane l's 8 bytes per block are exactly its B operand of
 // v_mfma_i32_16x16x32_i8 (B[k][j]: lane j + 16*(k/8), byte k%8), so a wave
-// streams 2 KB of weights with two 16-byte loads per lane and no shuffles.
+// streams 2 KB of weights with two 16-byte loads per lane, each load
+// instruction covering one contiguous 1 KB, and no shuffles.
 //
 // Q4_K tiled weights ("Q4T"): chunk (tile t, super-block b) = 2304 bytes:
-//   [0,2048)   lane l owns 32 bytes: for sub-block s=0..7 the 4 packed bytes
-//              qs[16s + 4g .. +4] (g = l/16) of row 16t + l%16
+//   [0,1024)   lane l owns bytes [16l, 16l+16): for sub-block s=0..3 the 4
+//              packed bytes qs[16s + 4g .. +4] (g = l/16) of row 16t + l%16
+//   [1024,2048) the same for s=4..7 at 1024 + 16l
 //   [2048,2304) row r owns its 16-byte header (d, dmin, scales[12])
 // With k' = 8g + j, j<4 -> low nibble of byte 4g+j, j>=4 -> high nibble of
 // byte 4g+j-4, the MFMA k index of sub-block s maps to element
@@ -22,8 +25,8 @@
 // Activations ("act") for M <= 16 token rows, per format:
 //   xq   Q8_0: [nG][4][M][32 B]: j=0..3 x 8 int8 of x[i][128G+32j+8g..+8]
 //        Q4_K: [nB][4][M][64 B]: s=0..7 x (xsub[4g..+4], xsub[16+4g..+4])
-//   xd   fp32 [Kp/32][16]   scale of each 32-block per token (0 for padding)
-//   dxs  fp32 [Kp/32][16]   Q4_K only: xd * sum(block int8), the min term
+//   xd   fp32 [16][Kp/32]   scale of each 32-block per token slot (0 for padding)
+//   dxs  fp32 [16][Kp/32]   Q4_K only: xd * sum(block int8), the min term
 #include "common.hpp"
 #include "layout.hpp"
 
@@ -65,7 +68,7 @@ __global__ void k_repack_q8_0(const uint8_t* __restrict__ src, uint8_t* __restri
     uint32_t nG = Kp / 128, t = row / 16, r = row % 16, G = b / 4, j = b % 4;
     uint8_t* ch = dst + ((size_t)t * nG + G) * 2176;
     for (int g = 0; g < 4; ++g) {
-        uint8_t* p = ch + (size_t)(r + 16 * g) * 32 + 8 * j;
+        uint8_t* p = ch + (j / 2) * 1024 + (size_t)(r + 16 * g) * 16 + 8 * (j % 2);
         for (int e = 0; e < 8; ++e) p[e] = blk[2 + 8 * g + e];
     }
     ch[2048 + r * 8 + 2 * j] = blk[0];
@@ -85,7 +88,7 @@ __global__ void k_repack_q4_K(const uint8_t* __restrict__ src, uint8_t* __restri
     for (int g = 0; g < 4; ++g)
         for (int sb = 0; sb < 8; ++sb)
             for (int e = 0; e < 4; ++e)
-                ch[(size_t)(r + 16 * g) * 32 + 4 * sb + e] = s ? s[16 + 16 * sb + 4 * g + e] : 0;
+                ch[(sb / 4) * 1024 + (size_t)(r + 16 * g) * 16 + 4 * (sb % 4) + e] = s ? s[16 + 16 * sb + 4 * g + e] : 0;
 }
 
 // ------------------------------------------------------- activation packing
@@ -98,7 +101,7 @@ __global__ void k_quantize_act_q8_0(const float* __restrict__ x, uint8_t* __rest
     uint32_t i = idx % 16, sb = idx / 16;
     float* xd = (float*)(act + xd_off);
     if (i >= M) {
-        xd[sb * 16 + i] = 0.0f;
+        xd[(size_t)i * nbp + sb] = 0.0f;
         return;
     }
     float v[32];
@@ -117,7 +120,7 @@ __global__ void k_quantize_act_q8_0(const float* __restrict__ x, uint8_t* __rest
         uint8_t* p = act + (((size_t)G * 4 + g) * M + i) * 32 + 8 * j;
         for (int e = 0; e < 8; ++e) p[e] = (uint8_t)qv[8 * g + e];
     }
-    xd[sb * 16 + i] = scale;
+    xd[(size_t)i * nbp + sb] = scale;
 }
 
 __global__ void k_quantize_act_q4_K(const float* __restrict__ x, uint8_t* __restrict__ act, uint32_t M, uint32_t K,
@@ -129,8 +132,8 @@ __global__ void k_quantize_act_q4_K(const float* __restrict__ x, uint8_t* __rest
     float* xd = (float*)(act + xd_off);
     float* dxs = (float*)(act + dxs_off);
     if (i >= M) {
-        xd[sbi * 16 + i] = 0.0f;
-        dxs[sbi * 16 + i] = 0.0f;
+        xd[(size_t)i * nsb + sbi] = 0.0f;
+        dxs[(size_t)i * nsb + sbi] = 0.0f;
         return;
     }
     uint32_t b = sbi / 8, s = sbi % 8, gq = s / 2, p = s % 2;
@@ -158,12 +161,12 @@ __global__ void k_quantize_act_q4_K(const float* __restrict__ x, uint8_t* __rest
             dp[4 + e] = (uint8_t)qv[16 + 4 * g + e];
         }
     }
-    xd[sbi * 16 + i] = scale;
-    dxs[sbi * 16 + i] = __fmul_rn(scale, (float)sum);
+    xd[(size_t)i * nsb + sbi] = scale;
+    dxs[(size_t)i * nsb + sbi] = __fmul_rn(scale, (float)sum);
 }
 
 __global__ void k_act_unpack(int fmt, const uint8_t* __restrict__ act, int8_t* __restrict__ xq,
-                             float* __restrict__ xdo, uint32_t M, uint32_t K, size_t xd_off) {
+                             float* __restrict__ xdo, uint32_t M, uint32_t K, uint32_t Kp, size_t xd_off) {
     uint32_t nb = K / 32;
     uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= M * nb) return;
@@ -182,7 +185,7 @@ __global__ void k_act_unpack(int fmt, const uint8_t* __restrict__ act, int8_t* _
                 out[16 + 4 * g + e] = (int8_t)act[(((size_t)b * 4 + g) * M + i) * 64 + 8 * s + 4 + e];
             }
     }
-    xdo[(size_t)i * nb + sb] = xd[sb * 16 + i];
+    xdo[(size_t)i * nb + sb] = xd[(size_t)i * (Kp / 32) + sb];
 }
 
 // ------------------------------------------------------------------ random
@@ -318,7 +321,7 @@ extern "C" int ec_act_unpack(int fmt, const void* act, int8_t* xq, float* xd, ui
     ActLayout L = act_layout(fmt, M, K);
     uint32_t n = M * (K / 32);
     hipLaunchKernelGGL(k_act_unpack, dim3((n + 127) / 128), dim3(128), 0, (hipStream_t)stream, fmt,
-                       (const uint8_t*)act, xq, xd, M, K, L.xd_off);
+                       (const uint8_t*)act, xq, xd, M, K, L.Kp, L.xd_off);
     EC_CHECK_LAUNCH();
     return EC_OK;
 }

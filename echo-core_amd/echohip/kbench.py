@@ -1,0 +1,180 @@
+"""Kernel-level measurements of the decode hot path on one GPU.
+
+Each HBM-bound case cycles through >= 512 MB of distinct buffers (the 256 MB
+Infinity Cache would otherwise hold the working set) and times every launch
+with its own pair of HIP events on the launch stream; the reported duration is
+the mean over launches.  Algorithmic bytes / FLOPs per launch follow the
+workload definitions (weights + activations + outputs actually required).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+from . import lib as L
+from . import synth
+
+HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3
+ROTATE_BYTES = 512 << 20
+
+
+def _events_mean_us(launch, n_copies, iters, replays=5):
+    """Mean GPU time per launch: `iters` launches over the rotation are captured
+    in one HIP graph (so host submission never gaps the GPU), the graph is
+    replayed between two HIP events on the launch stream, and the elapsed time is
+    divided by the launch count.  Returns (mean, best-replay mean) in us."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(n_copies):  # warm every copy once, outside the capture
+            launch(i, side.cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        st = torch.cuda.current_stream().cuda_stream
+        for i in range(iters):
+            launch(i % n_copies, st)
+    g.replay()
+    torch.cuda.synchronize()
+    t = []
+    for _ in range(replays):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        t.append(a.elapsed_time(b) * 1e3 / iters)
+    del g
+    return float(np.mean(t)), float(np.min(t))
+
+
+def matvec_case(hip, fmt, N, K, M=1, iters=200, seed=0):
+    """Decode matvec y = W x over a rotation of weight copies."""
+    st = torch.cuda.current_stream().cuda_stream
+    if fmt == L.Q8_0:
+        wbytes = N * K // 32 * 34
+        Wd = torch.empty(wbytes, dtype=torch.uint8, device="cuda")
+        hip.fill_random(1, Wd, N * K // 32, seed, 0.02, stream=st)  # same bytes as synth.q8_0_blocks
+    else:
+        wbytes = N * K // 256 * 144
+        Wd = torch.from_numpy(synth.q4_K_blocks(seed, N, K)).cuda()
+    tb = hip.tiled_bytes(fmt, N, K)
+    n_copies = max(2, math.ceil(ROTATE_BYTES / tb) + 1)
+    tiled = torch.empty((n_copies, tb), dtype=torch.uint8, device="cuda")
+    hip.repack(fmt, Wd, tiled[0], N, K, stream=st)
+    for i in range(1, n_copies):
+        tiled[i].copy_(tiled[0])
+    del Wd
+    x = torch.from_numpy(synth.activations(seed + 1, M * K)).cuda()
+    act = torch.empty(hip.act_bytes(fmt, M, K), dtype=torch.uint8, device="cuda")
+    hip.quantize_act(fmt, x, act, M, K, stream=st)
+    y = torch.empty(M * N, dtype=torch.float32, device="cuda")
+
+    def launch(i, stream):
+        hip.matvec(fmt, tiled[i], act, y, M, N, K, stream=stream)
+
+    mean_us, med_us = _events_mean_us(launch, n_copies, iters)
+    x_bytes = M * (K + K // 32 * 4 * (2 if fmt == L.Q4_K else 1))
+    alg = wbytes + x_bytes + M * N * 4
+    gbs = alg / (mean_us * 1e-6) / 1e9
+    del tiled
+    torch.cuda.empty_cache()
+    return {"kernel": "k_mv_q8_0" if fmt == L.Q8_0 else "k_mv_q4_K", "M": M, "N": N, "K": K,
+            "bytes": alg, "us": round(mean_us, 3), "us_best": round(med_us, 3), "GBs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": n_copies}
+
+
+def stream_read_case(hip, nbytes, iters=100, blocks=4096):
+    """Plain streaming read over a >= 512 MB rotation: the achievable-HBM reference."""
+    n_copies = max(2, math.ceil(ROTATE_BYTES / nbytes) + 1)
+    buf = torch.empty((n_copies, nbytes), dtype=torch.uint8, device="cuda")
+    buf.fill_(1)
+    out = torch.zeros(blocks, dtype=torch.int32, device="cuda")
+
+    def launch(i, stream):
+        hip.stream_read(buf[i], nbytes, out, blocks, stream=stream)
+
+    mean_us, best_us = _events_mean_us(launch, n_copies, iters)
+    gbs = nbytes / (mean_us * 1e-6) / 1e9
+    del buf
+    torch.cuda.empty_cache()
+    return {"kernel": "k_stream_read", "bytes": nbytes, "us": round(mean_us, 3), "GBs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": n_copies}
+
+
+def attention_case(hip, ctx, n_heads=16, n_kv=4, hd=256, iters=100, seed=0):
+    st = torch.cuda.current_stream().cuda_stream
+    kv = ctx * n_kv * hd
+    per = 2 * kv + 2 * ctx * n_kv * 4
+    n_copies = max(2, math.ceil(ROTATE_BYTES / per) + 1)
+    keys = torch.randint(-127, 128, (n_copies, kv), dtype=torch.int8, device="cuda")
+    vals = torch.randint(-127, 128, (n_copies, kv), dtype=torch.int8, device="cuda")
+    ks = torch.rand((n_copies, ctx * n_kv), device="cuda") * 0.02 + 0.01
+    vs = torch.rand((n_copies, ctx * n_kv), device="cuda") * 0.02 + 0.01
+    q = torch.from_numpy(synth.activations(seed, n_heads * hd)).cuda()
+    out = torch.empty(n_heads * hd, dtype=torch.float32, device="cuda")
+    cl = torch.tensor([ctx], dtype=torch.int32, device="cuda")
+    ws = torch.empty(hip.attn_ws_bytes(1, n_heads, hd, ctx), dtype=torch.uint8, device="cuda")
+
+    def launch(i, stream):
+        hip.attn_decode(q, keys[i], vals[i], ks[i], vs[i], out, cl, 1, kv, n_heads, n_kv, hd, ctx, ws, stream=stream)
+
+    mean_us, med_us = _events_mean_us(launch, n_copies, iters)
+    alg = per + 2 * n_heads * hd * 4
+    gbs = alg / (mean_us * 1e-6) / 1e9
+    return {"kernel": "k_attn_partial+combine", "ctx": ctx, "bytes": alg, "us": round(mean_us, 3),
+            "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": n_copies}
+
+
+def deltanet_case(hip, T=1024, n_v=32, d=128, iters=5, seed=0):
+    st = torch.cuda.current_stream().cuda_stream
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    state0 = torch.randn((n_v, d, d), generator=g, device="cuda") * 0.02
+    q = torch.nn.functional.normalize(torch.randn((T, n_v, d), generator=g, device="cuda"), dim=-1)
+    k = torch.nn.functional.normalize(torch.randn((T, n_v, d), generator=g, device="cuda"), dim=-1)
+    v = torch.randn((T, n_v, d), generator=g, device="cuda")
+    dec = torch.sigmoid(torch.randn((T, n_v), generator=g, device="cuda") * 0.5 + 2)
+    bet = torch.sigmoid(torch.randn((T, n_v), generator=g, device="cuda"))
+    out = torch.empty((T, n_v, d), device="cuda")
+    state = state0.clone()
+
+    # time only the recurrence: events around the delta-net launch
+    evs = []
+    for i in range(iters + 1):
+        state.copy_(state0)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        hip.deltanet(state, q, k, v, dec, bet, out, T, 1, n_v, n_v, d, d, stream=st)
+        b.record()
+        evs.append((a, b))
+    torch.cuda.synchronize()
+    us = float(np.mean([a.elapsed_time(b) for a, b in evs[1:]]) * 1e3)
+    flops = 7 * n_v * d * d * T
+    tf = flops / (us * 1e-6) / 1e12
+    return {"kernel": "k_deltanet", "T": T, "flops": flops, "us": round(us, 2), "us_per_token": round(us / T, 4),
+            "TFLOPs": round(tf, 2), "frac": round(tf / FP32_PEAK_TFLOPS, 4)}
+
+
+def run_all(hip, quick=False):
+    res = {}
+    res["q8_0_9216x2560_m1"] = matvec_case(hip, L.Q8_0, 9216, 2560)
+    res["q4_K_9216x2560_m1"] = matvec_case(hip, L.Q4_K, 9216, 2560)
+    res["q4_K_2560x9216_m1"] = matvec_case(hip, L.Q4_K, 2560, 9216)
+    res["q8_0_9216x2560_m8"] = matvec_case(hip, L.Q8_0, 9216, 2560, M=8)
+    res["q8_0_151936x2560_m8"] = matvec_case(hip, L.Q8_0, 151936, 2560, M=8, iters=20)
+    for ctx in (512, 4096, 32768):
+        res[f"attn_ctx{ctx}"] = attention_case(hip, ctx)
+    res["deltanet_1024"] = deltanet_case(hip)
+    return res
+
+
+if __name__ == "__main__":
+    import json
+    hip = L.load()
+    r = run_all(hip)
+    for k, v in r.items():
+        print(k, json.dumps(v), flush=True)

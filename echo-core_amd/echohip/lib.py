@@ -38,6 +38,7 @@ _SIGS = {
     "ec_attn_decode": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u64, _u32, _u32, _u32, _u32, _vp, _vp],
     "ec_deltanet": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp],
     "ec_fill_random": [C.c_int, _vp, _u64, _u64, C.c_float, _u32, _vp],
+    "ec_stream_read": [_vp, _sz, _vp, _u32, _vp],
 }
 _SIZE_FNS = {
     "ec_tiled_bytes": [C.c_int, _u32, _u32],
@@ -141,6 +142,9 @@ class Lib:
     def deltanet(self, state, q, k, v, decay, beta, out, T, n_seq, n_v, n_k, d_k, d_v, stream=None):
         self._call("ec_deltanet", _ptr(state), _ptr(q), _ptr(k), _ptr(v), _ptr(decay), _ptr(beta), _ptr(out), T,
                    n_seq, n_v, n_k, d_k, d_v, self._stream(stream))
+
+    def stream_read(self, src, nbytes, out, blocks, stream=None):
+        self._call("ec_stream_read", _ptr(src), nbytes, _ptr(out), blocks, self._stream(stream))
 
     def fill_random(self, kind, dst, n, seed, scale=1.0, K=0, stream=None):
         self._call("ec_fill_random", kind, _ptr(dst), n, seed, scale, K, self._stream(stream))

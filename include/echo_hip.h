@@ -122,6 +122,10 @@ int ec_deltanet(float* state, const float* q, const float* k, const float* v, co
                 float* out, uint32_t T, uint32_t n_seq, uint32_t n_v, uint32_t n_k, uint32_t d_k, uint32_t d_v,
                 void* stream);
 
+/* Plain streaming read of `bytes` (multiple of 16) with `blocks` workgroups of
+ * 256 threads: the HBM-bandwidth calibration used by the benchmarks. */
+int ec_stream_read(const void* src, size_t bytes, uint32_t* out, uint32_t blocks, void* stream);
+
 /* ----------------------------------------------------------------- random
  * Fill device memory from the portable splitmix64 stream: element i gets
  * bits of splitmix64(seed, i) (echohip/synth.py).  kind 0: uint8 bytes (low
