@@ -43,9 +43,10 @@ __global__ __launch_bounds__(256) void k_deltanet(float* __restrict__ state, con
                                                   const float* __restrict__ k, const float* __restrict__ v,
                                                   const float* __restrict__ decay, const float* __restrict__ beta,
                                                   float* __restrict__ out, uint32_t T, uint32_t n_seq, uint32_t n_v,
-                                                  uint32_t n_k, uint32_t d_v) {
+                                                  uint32_t n_k, uint32_t d_v, const int32_t* __restrict__ seq_pos) {
     const uint32_t groups = d_v / 16;
     const uint32_t h = blockIdx.x / groups, s = blockIdx.y;
+    if (seq_pos && seq_pos[s] < 0) return;
     const uint32_t col = 16 * (blockIdx.x % groups) + threadIdx.x / 16, ks = threadIdx.x % 16;
     const uint32_t qh = h / (n_v / n_k);
     const float scale = 1.0f / sqrtf(128.0f);
@@ -87,13 +88,13 @@ using namespace ec;
 
 extern "C" int ec_deltanet(float* state, const float* q, const float* k, const float* v, const float* decay,
                            const float* beta, float* out, uint32_t T, uint32_t n_seq, uint32_t n_v, uint32_t n_k,
-                           uint32_t d_k, uint32_t d_v, void* stream) {
+                           uint32_t d_k, uint32_t d_v, const int32_t* seq_pos, void* stream) {
     if (T == 0 || n_seq == 0) return EC_OK;
     if (!state || !q || !k || !v || !decay || !beta || !out || n_k == 0 || n_v % n_k || d_k != 128 || d_v == 0 ||
         d_v % 16)
         return ec_set_error(EC_ERR_ARG, "ec_deltanet: need d_k == 128, d_v % 16 == 0, n_v % n_k == 0");
     hipLaunchKernelGGL(k_deltanet, dim3(n_v * (d_v / 16), n_seq), dim3(256), 0, (hipStream_t)stream, state, q, k, v,
-                       decay, beta, out, T, n_seq, n_v, n_k, d_v);
+                       decay, beta, out, T, n_seq, n_v, n_k, d_v, seq_pos);
     EC_CHECK_LAUNCH();
     return EC_OK;
 }

@@ -1,0 +1,377 @@
+// glue.hip — the small per-token ops of the hybrid decode step, fused so that
+// each produces exactly what the next matvec or recurrence consumes.
+//
+// Semantics follow the reference engine (echo-core-zig):
+//   embedding row decode           inference/engine.zig:30-54 (Q8_0 branch)
+//   RMSNorm                        engine.zig:783-792 (x * 1/sqrt(mean(x^2)+1e-6) * w)
+//   conv shift + conv + SiLU       kernels/qwen_linear.zig:182-201 (tap-major weights)
+//   L2 norm of q, k heads          qwen_linear.zig:87-101, :203-204
+//   decay / beta gates             qwen_linear.zig:215-219, softplus :71-74
+//   gated RMSNorm                  qwen_linear.zig:252-257
+//   head RMSNorm, RoPE, KV append  engine.zig:507-518, :466-504, :556-561
+//   SwiGLU                         engine.zig:748-781, core/math.zig:35-37
+//   greedy argmax (first maximum)  engine.zig:860-867
+// Every op that feeds a matvec quantizes its output per 32-element block with
+// the reference quantizer directly into the matvec's activation layout
+// (quant.hip header), token-major scales xd[slot][block].
+//
+// A sequence s is active when pos[s] >= 0; inactive sequences never touch
+// their recurrent state, conv state or KV cache.
+#include "common.hpp"
+#include "layout.hpp"
+
+namespace ec {
+
+// Block-wide sum over 256 threads (4 waves); every thread gets the total.
+__device__ __forceinline__ float block_sum256(float v, float* sh) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) sh[w] = v;
+    __syncthreads();
+    return sh[0] + sh[1] + sh[2] + sh[3];
+}
+
+__device__ __forceinline__ float block_max256(float v, float* sh) {
+    v = wave_max(v);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) sh[w] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+// Quantize 32 values (one block) and store them into the Q8_0 activation
+// layout for token slot i of an M-row activation buffer; scale to xd[i][sb].
+__device__ __forceinline__ void store_block_q8(const float (&v)[32], uint8_t* act, uint32_t M, uint32_t i,
+                                               uint32_t sb, uint32_t nbp, float* xd) {
+    float amax = 0.0f;
+    for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(v[e]));
+    const float scale = q_scale(amax);
+    const float inv = __fdiv_rn(1.0f, scale);
+    const uint32_t G = sb / 4, j = sb % 4;
+    for (int g = 0; g < 4; ++g) {
+        uint32_t lo = 0, hi = 0;
+        for (int e = 0; e < 4; ++e) lo |= (uint32_t)(uint8_t)q_body(v[8 * g + e], inv) << (8 * e);
+        for (int e = 0; e < 4; ++e) hi |= (uint32_t)(uint8_t)q_body(v[8 * g + 4 + e], inv) << (8 * e);
+        *(uint2*)(act + (((size_t)G * 4 + g) * M + i) * 32 + 8 * j) = make_uint2(lo, hi);
+    }
+    xd[(size_t)i * nbp + sb] = scale;
+}
+
+// ------------------------------------------------------------------ embedding
+__global__ __launch_bounds__(256) void k_embed_q8_0(const uint8_t* __restrict__ emb, const int32_t* __restrict__ tok,
+                                                    float* __restrict__ x, uint32_t H, uint32_t vocab) {
+    const uint32_t s = blockIdx.x;
+    int32_t t = tok[s];
+    t = t < 0 ? 0 : (t >= (int32_t)vocab ? (int32_t)vocab - 1 : t);
+    const uint32_t nb = H / 32;
+    const uint8_t* row = emb + (size_t)t * nb * 34;
+    for (uint32_t i = threadIdx.x; i < H; i += 256) {
+        const uint8_t* bp = row + (i / 32) * 34;
+        const float d = h2f((uint16_t)(bp[0] | (bp[1] << 8)));
+        x[(size_t)s * H + i] = d * (float)(int8_t)bp[2 + (i % 32)];
+    }
+}
+
+// ---------------------------------------------------------- RMSNorm + quantize
+// grid (M): row i of x [M][H] -> act (Q8_0 layout, K = H).
+__global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__ x, const float* __restrict__ w,
+                                                       uint8_t* __restrict__ act, uint32_t M, uint32_t H,
+                                                       uint32_t xd_off) {
+    __shared__ float sh[4];
+    const uint32_t i = blockIdx.x;
+    const float* xr = x + (size_t)i * H;
+    float ss = 0.0f;
+    for (uint32_t k = threadIdx.x; k < H; k += 256) ss = fmaf(xr[k], xr[k], ss);
+    ss = block_sum256(ss, sh);
+    const float inv = 1.0f / sqrtf(ss / (float)H + 1e-6f);
+    const uint32_t nbp = round_up(H, 128) / 32;
+    float* xd = (float*)(act + xd_off);
+    for (uint32_t sb = threadIdx.x; sb < nbp; sb += 256) {
+        float v[32];
+        for (int e = 0; e < 32; ++e) {
+            const uint32_t k = 32 * sb + e;
+            v[e] = k < H ? xr[k] * inv * w[k] : 0.0f;
+        }
+        store_block_q8(v, act, M, i, sb, nbp, xd);
+    }
+}
+
+// ------------------------------------------------------- SwiGLU + quantize
+// gu [M][2F] (gate rows then up rows) -> act (K = F).  One thread per block.
+__global__ __launch_bounds__(256) void k_swiglu_quant(const float* __restrict__ gu, uint8_t* __restrict__ act,
+                                                      uint32_t M, uint32_t F, uint32_t xd_off) {
+    const uint32_t nbp = round_up(F, 128) / 32;
+    const uint32_t idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= M * nbp) return;
+    const uint32_t i = idx / nbp, sb = idx % nbp;
+    const float* g = gu + (size_t)i * 2 * F;
+    float v[32];
+    for (int e = 0; e < 32; ++e) {
+        const uint32_t k = 32 * sb + e;
+        v[e] = k < F ? silu(g[k]) * g[F + k] : 0.0f;
+    }
+    store_block_q8(v, act, M, i, sb, nbp, (float*)(act + xd_off));
+}
+
+// ------------------------------------------------ delta-net conv + norms + gates
+// grid (n_k, n_seq), block 256.  proj [n_seq][Nin]: conv channels
+// [0, conv_dim) = q (key_dim) | k (key_dim) | v (value_dim), then z (value_dim),
+// alpha (n_v), beta (n_v).  conv_state [n_seq][kern][conv_dim] (slot 0 newest).
+// Outputs: q, k [n_seq][n_k][128] (L2-normalised), v [n_seq][n_v][128],
+// decay, beta [n_seq][n_v].  Requires head dims of 128 and n_v = rep * n_k
+// with rep <= 2.
+__global__ __launch_bounds__(256) void k_conv_gates(const float* __restrict__ proj, uint32_t Nin,
+                                                    float* __restrict__ conv_state, const float* __restrict__ conv_w,
+                                                    const float* __restrict__ a_log, const float* __restrict__ dt_bias,
+                                                    float* __restrict__ q_out, float* __restrict__ k_out,
+                                                    float* __restrict__ v_out, float* __restrict__ dec,
+                                                    float* __restrict__ beta, const int32_t* __restrict__ pos,
+                                                    uint32_t n_k, uint32_t n_v, uint32_t kern) {
+    __shared__ float sh[4];
+    __shared__ float sq[2];
+    const uint32_t qh = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
+    if (pos[s] < 0) return;
+    const uint32_t key_dim = n_k * 128, value_dim = n_v * 128, conv_dim = 2 * key_dim + value_dim;
+    const uint32_t rep = n_v / n_k;
+    const float* pr = proj + (size_t)s * Nin;
+    float* st = conv_state + (size_t)s * kern * conv_dim;
+    auto conv = [&](uint32_t c) -> float {
+        for (uint32_t k = kern - 1; k > 0; --k) st[(size_t)k * conv_dim + c] = st[(size_t)(k - 1) * conv_dim + c];
+        st[c] = pr[c];
+        float acc = 0.0f;
+        for (uint32_t k = 0; k < kern; ++k) acc += st[(size_t)k * conv_dim + c] * conv_w[(size_t)(kern - 1 - k) * conv_dim + c];
+        return silu(acc);
+    };
+    // q (t < 128) or k (t >= 128) channel of this k-head
+    const uint32_t half = t / 128, i = t % 128;
+    const uint32_t cqk = half * key_dim + qh * 128 + i;
+    const float a = conv(cqk);
+    // v channels of the v-heads of this k-head
+    for (uint32_t r = half; r < rep; r += 2) {
+        const uint32_t h = qh * rep + r;
+        v_out[((size_t)s * n_v + h) * 128 + i] = conv(2 * key_dim + h * 128 + i);
+    }
+    // L2 norms of q and k over their 128 channels (two waves each)
+    float ss = wave_sum(a * a);
+    const uint32_t w = t >> 6;
+    if ((t & 63) == 0) sh[w] = ss;
+    __syncthreads();
+    if (t == 0) sq[0] = sh[0] + sh[1];
+    if (t == 128) sq[1] = sh[2] + sh[3];
+    __syncthreads();
+    const float inv = 1.0f / sqrtf(sq[half] + 1e-6f);
+    (half == 0 ? q_out : k_out)[((size_t)s * n_k + qh) * 128 + i] = a * inv;
+    if (t < rep) {
+        const uint32_t h = qh * rep + t;
+        const float al = pr[conv_dim + value_dim + h];
+        const float br = pr[conv_dim + value_dim + n_v + h];
+        const float sp_in = al + dt_bias[h];
+        const float sp = sp_in > 20.0f ? sp_in : log1pf(expf(sp_in));
+        const float g = -expf(a_log[h]) * sp;
+        dec[(size_t)s * n_v + h] = expf(g);
+        beta[(size_t)s * n_v + h] = 1.0f / (1.0f + expf(-br));
+    }
+}
+
+// ------------------------------------------------ gated RMSNorm + quantize
+// grid (n_v, M), block 128: core [M][n_v][128], z at proj[s][z_off + h*128 + i]
+// -> act (K = n_v*128).  The head's 128 outputs are 4 whole 32-blocks.
+__global__ __launch_bounds__(128) void k_gated_norm_quant(const float* __restrict__ core,
+                                                          const float* __restrict__ proj, uint32_t Nin,
+                                                          uint32_t z_off, const float* __restrict__ norm_w,
+                                                          uint8_t* __restrict__ act, uint32_t M, uint32_t n_v,
+                                                          uint32_t xd_off) {
+    __shared__ float sh[2];
+    const uint32_t h = blockIdx.x, s = blockIdx.y, i = threadIdx.x;
+    const float o = core[((size_t)s * n_v + h) * 128 + i];
+    float ss = wave_sum(o * o);
+    if ((i & 63) == 0) sh[i >> 6] = ss;
+    __syncthreads();
+    const float rms = sqrtf((sh[0] + sh[1]) / 128.0f + 1e-6f);
+    const float inv = 1.0f / rms;
+    const float val = o * inv * norm_w[i] * silu(proj[(size_t)s * Nin + z_off + h * 128 + i]);
+    // quantize the 32-lane group (one block)
+    float amax = fabsf(val);
+    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+    const float scale = q_scale(amax);
+    const float qinv = __fdiv_rn(1.0f, scale);
+    const int8_t qv = q_body(val, qinv);
+    const uint32_t nbp = round_up(n_v * 128, 128) / 32;
+    const uint32_t sb = h * 4 + i / 32, e = i % 32;
+    const uint32_t G = sb / 4, j = sb % 4, g = e / 8;
+    act[(((size_t)G * 4 + g) * M + s) * 32 + 8 * j + e % 8] = (uint8_t)qv;
+    if (e == 0) ((float*)(act + xd_off))[(size_t)s * nbp + sb] = scale;
+}
+
+// -------------------------------------------- head norm + RoPE + KV append
+// grid (n_heads + 2*n_kv, n_seq), block = head_dim (256).  proj [n_seq][Nin]
+// holds q | k | v.  Head kinds: q heads -> q_out (normed, rotated); k heads ->
+// normed, rotated, quantized into the cache at pos; v heads -> quantized.
+__global__ __launch_bounds__(256) void k_qk_rope_append(const float* __restrict__ proj, uint32_t Nin,
+                                                        const float* __restrict__ q_norm,
+                                                        const float* __restrict__ k_norm, int use_qn, int use_kn,
+                                                        const float* __restrict__ inv_freq, const int32_t* pos,
+                                                        float* __restrict__ q_out, int8_t* __restrict__ keys,
+                                                        int8_t* __restrict__ vals, float* __restrict__ kscales,
+                                                        float* __restrict__ vscales, int32_t* __restrict__ ctx,
+                                                        uint64_t seq_stride, uint32_t max_ctx, uint32_t n_heads,
+                                                        uint32_t n_kv) {
+    __shared__ float sh[4];
+    const uint32_t HD = 256;
+    const uint32_t head = blockIdx.x, s = blockIdx.y, d = threadIdx.x;
+    const int32_t p = pos[s];
+    if (head == 0 && d == 0) ctx[s] = (p >= 0 && (uint32_t)p < max_ctx) ? p + 1 : 0;
+    if (p < 0 || (uint32_t)p >= max_ctx) return;
+    const float* pr = proj + (size_t)s * Nin;
+    const bool is_q = head < n_heads, is_k = !is_q && head < n_heads + n_kv;
+    const uint32_t off = is_q ? head * HD : (is_k ? n_heads * HD + (head - n_heads) * HD
+                                                  : n_heads * HD + n_kv * HD + (head - n_heads - n_kv) * HD);
+    float val = pr[off + d];
+    if ((is_q && use_qn) || (is_k && use_kn)) {
+        const float ss = block_sum256(val * val, sh);
+        const float inv = 1.0f / sqrtf(ss / (float)HD + 1e-6f);
+        val = val * inv * (is_q ? q_norm : k_norm)[d];
+    }
+    if (is_q || is_k) {
+        const float other = __shfl_xor(val, 1);
+        const float ang = (float)p * inv_freq[d / 2];
+        float sn, cs;
+        sincosf(ang, &sn, &cs);
+        val = (d & 1) ? other * sn + val * cs : val * cs - other * sn;
+    }
+    if (is_q) {
+        q_out[(size_t)s * n_heads * HD + head * HD + d] = val;
+        return;
+    }
+    const uint32_t kvh = is_k ? head - n_heads : head - n_heads - n_kv;
+    const float amax = block_max256(fabsf(val), sh);
+    const float scale = q_scale(amax);
+    const float inv = __fdiv_rn(1.0f, scale);
+    int8_t* dst = (is_k ? keys : vals) + s * seq_stride + ((size_t)p * n_kv + kvh) * HD;
+    dst[d] = q_body(val, inv);
+    if (d == 0) (is_k ? kscales : vscales)[s * (seq_stride / HD) + (size_t)p * n_kv + kvh] = scale;
+}
+
+// ----------------------------------------------------------------- argmax
+// grid (n_seq), block 1024: first index of the maximum (engine.zig:860-867).
+// Active sequences write the token to gen and next and advance pos.
+__global__ __launch_bounds__(1024) void k_argmax_advance(const float* __restrict__ logits, uint32_t vocab,
+                                                         int32_t* __restrict__ gen, int32_t* __restrict__ next,
+                                                         int32_t* __restrict__ pos) {
+    __shared__ float sv[16];
+    __shared__ int32_t si[16];
+    const uint32_t s = blockIdx.x, t = threadIdx.x;
+    const float* l = logits + (size_t)s * vocab;
+    float best = -INFINITY;
+    int32_t bi = 0x7FFFFFFF;
+    for (uint32_t k = t; k < vocab; k += 1024) {
+        const float v = l[k];
+        if (v > best) {
+            best = v;
+            bi = (int32_t)k;
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o);
+        const int32_t oi = __shfl_xor(bi, o);
+        if (ov > best || (ov == best && oi < bi)) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    if ((t & 63) == 0) {
+        sv[t >> 6] = best;
+        si[t >> 6] = bi;
+    }
+    __syncthreads();
+    if (t == 0) {
+        for (int w = 1; w < 16; ++w)
+            if (sv[w] > best || (sv[w] == best && si[w] < bi)) {
+                best = sv[w];
+                bi = si[w];
+            }
+        if (bi == 0x7FFFFFFF) bi = 0;  // all NaN: token 0, as the reference's scan
+        if (pos[s] >= 0) {
+            gen[s] = bi;
+            next[s] = bi;
+            pos[s] += 1;
+        }
+    }
+}
+
+}  // namespace ec
+
+using namespace ec;
+
+#define EC_GLUE_LAUNCH(...)                        \
+    do {                                           \
+        hipLaunchKernelGGL(__VA_ARGS__);           \
+        EC_CHECK_LAUNCH();                         \
+        return EC_OK;                              \
+    } while (0)
+
+extern "C" int ec_glue_embed(const void* emb, const int32_t* tok, float* x, uint32_t n_seq, uint32_t H,
+                             uint32_t vocab, void* stream) {
+    if (!emb || !tok || !x || H % 32) return ec_set_error(EC_ERR_ARG, "ec_glue_embed: bad argument");
+    EC_GLUE_LAUNCH(k_embed_q8_0, dim3(n_seq), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)emb, tok, x, H,
+                   vocab);
+}
+
+extern "C" int ec_glue_rmsnorm_quant(const float* x, const float* w, void* act, uint32_t M, uint32_t H,
+                                     void* stream) {
+    if (!x || !w || !act || M == 0 || M > 16 || H % 32) return ec_set_error(EC_ERR_ARG, "ec_glue_rmsnorm_quant");
+    const ActLayout L = act_layout(EC_Q8_0, M, H);
+    EC_GLUE_LAUNCH(k_rmsnorm_quant, dim3(M), dim3(256), 0, (hipStream_t)stream, x, w, (uint8_t*)act, M, H,
+                   (uint32_t)L.xd_off);
+}
+
+extern "C" int ec_glue_swiglu_quant(const float* gu, void* act, uint32_t M, uint32_t F, void* stream) {
+    if (!gu || !act || M == 0 || M > 16 || F % 32) return ec_set_error(EC_ERR_ARG, "ec_glue_swiglu_quant");
+    const ActLayout L = act_layout(EC_Q8_0, M, F);
+    const uint32_t n = M * (L.Kp / 32);
+    EC_GLUE_LAUNCH(k_swiglu_quant, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, gu, (uint8_t*)act, M,
+                   F, (uint32_t)L.xd_off);
+}
+
+extern "C" int ec_glue_conv_gates(const float* proj, uint32_t Nin, float* conv_state, const float* conv_w,
+                                  const float* a_log, const float* dt_bias, float* q, float* k, float* v, float* dec,
+                                  float* beta, const int32_t* pos, uint32_t n_seq, uint32_t n_k, uint32_t n_v,
+                                  uint32_t kern, void* stream) {
+    if (!proj || !conv_state || !conv_w || !a_log || !dt_bias || !q || !k || !v || !dec || !beta || !pos ||
+        n_k == 0 || n_v % n_k || n_v / n_k > 2 || kern == 0 || Nin < 3 * n_k * 128 + n_v * 128 + 2 * n_v)
+        return ec_set_error(EC_ERR_ARG, "ec_glue_conv_gates: bad argument");
+    EC_GLUE_LAUNCH(k_conv_gates, dim3(n_k, n_seq), dim3(256), 0, (hipStream_t)stream, proj, Nin, conv_state, conv_w,
+                   a_log, dt_bias, q, k, v, dec, beta, pos, n_k, n_v, kern);
+}
+
+extern "C" int ec_glue_gated_norm_quant(const float* core, const float* proj, uint32_t Nin, uint32_t z_off,
+                                        const float* norm_w, void* act, uint32_t M, uint32_t n_v, void* stream) {
+    if (!core || !proj || !norm_w || !act || M == 0 || M > 16) return ec_set_error(EC_ERR_ARG, "ec_glue_gated_norm");
+    const ActLayout L = act_layout(EC_Q8_0, M, n_v * 128);
+    EC_GLUE_LAUNCH(k_gated_norm_quant, dim3(n_v, M), dim3(128), 0, (hipStream_t)stream, core, proj, Nin, z_off,
+                   norm_w, (uint8_t*)act, M, n_v, (uint32_t)L.xd_off);
+}
+
+extern "C" int ec_glue_qk_rope_append(const float* proj, uint32_t Nin, const float* q_norm, const float* k_norm,
+                                      int use_qn, int use_kn, const float* inv_freq, const int32_t* pos, float* q_out,
+                                      int8_t* keys, int8_t* vals, float* kscales, float* vscales, int32_t* ctx,
+                                      uint32_t n_seq, uint64_t seq_stride, uint32_t max_ctx, uint32_t n_heads,
+                                      uint32_t n_kv, uint32_t head_dim, void* stream) {
+    if (head_dim != 256) return ec_set_error(EC_ERR_UNSUPPORTED, "ec_glue_qk_rope_append: head_dim must be 256");
+    if (!proj || !inv_freq || !pos || !q_out || !keys || !vals || !kscales || !vscales || !ctx ||
+        seq_stride < (uint64_t)max_ctx * n_kv * head_dim)
+        return ec_set_error(EC_ERR_ARG, "ec_glue_qk_rope_append: bad argument");
+    EC_GLUE_LAUNCH(k_qk_rope_append, dim3(n_heads + 2 * n_kv, n_seq), dim3(256), 0, (hipStream_t)stream, proj, Nin,
+                   q_norm, k_norm, use_qn, use_kn, inv_freq, pos, q_out, keys, vals, kscales, vscales, ctx,
+                   seq_stride, max_ctx, n_heads, n_kv);
+}
+
+extern "C" int ec_glue_argmax_advance(const float* logits, uint32_t vocab, int32_t* gen, int32_t* next, int32_t* pos,
+                                      uint32_t n_seq, void* stream) {
+    if (!logits || !gen || !next || !pos) return ec_set_error(EC_ERR_ARG, "ec_glue_argmax_advance: bad argument");
+    EC_GLUE_LAUNCH(k_argmax_advance, dim3(n_seq), dim3(1024), 0, (hipStream_t)stream, logits, vocab, gen, next, pos);
+}

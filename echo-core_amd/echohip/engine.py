@@ -1,0 +1,155 @@
+"""ctypes binding of the device-resident hybrid decoder (include/echo_engine.h)."""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, fields
+
+import numpy as np
+
+from .lib import EchoHipError, load
+
+T_EMBED, T_FINAL_NORM, T_LM_HEAD = 0, 1, 2
+T_ATTN_NORM, T_FFN_NORM, T_W_IN, T_W_OUT, T_W_GATE, T_W_UP, T_W_DOWN = 10, 11, 12, 13, 14, 15, 16
+T_CONV_W, T_A_LOG, T_DT_BIAS, T_SSM_NORM, T_Q_NORM, T_K_NORM = 17, 18, 19, 20, 21, 22
+
+
+@dataclass
+class EngineConfig:
+    vocab: int = 151936
+    hidden: int = 2560
+    ffn: int = 9216
+    n_layers: int = 32
+    n_heads: int = 16
+    n_kv: int = 4
+    head_dim: int = 256
+    ssm_inner: int = 4096
+    ssm_heads: int = 32
+    conv_kernel: int = 4
+    attn_interval: int = 4
+    max_batch: int = 8
+    max_ctx: int = 4608
+    rope_base: float = 10000.0
+
+    def is_attn(self, layer: int) -> bool:
+        return self.attn_interval != 0 and (layer + 1) % self.attn_interval == 0
+
+    @property
+    def key_dim(self):
+        return self.ssm_inner // 2
+
+    @property
+    def conv_dim(self):
+        return 2 * self.key_dim + self.ssm_inner
+
+    @property
+    def nin_delta(self):
+        return self.conv_dim + self.ssm_inner + 2 * self.ssm_heads
+
+    @property
+    def nin_attn(self):
+        return (self.n_heads + 2 * self.n_kv) * self.head_dim
+
+
+class _Cfg(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("vocab", "hidden", "ffn", "n_layers", "n_heads", "n_kv", "head_dim",
+                                          "ssm_inner", "ssm_heads", "conv_kernel", "attn_interval", "max_batch",
+                                          "max_ctx")] + [("rope_base", C.c_float)]
+
+
+class Engine:
+    def __init__(self, cfg: EngineConfig):
+        self.cfg = cfg
+        self.hip = load()
+        L = self.L = self.hip.L
+        vp, u32, i32 = C.c_void_p, C.c_uint32, C.c_int
+        L.ec_engine_create.argtypes = [C.POINTER(_Cfg), C.POINTER(vp)]
+        L.ec_engine_destroy.argtypes = [vp]
+        L.ec_engine_destroy.restype = None
+        L.ec_engine_set_tensor.argtypes = [vp, i32, i32, vp, C.c_size_t]
+        L.ec_engine_init_random.argtypes = [vp, C.c_uint64, C.c_float]
+        L.ec_engine_get_tensor.argtypes = [vp, i32, i32, vp, C.c_size_t]
+        L.ec_engine_reset.argtypes = [vp]
+        L.ec_engine_set_inputs.argtypes = [vp, vp, vp, u32]
+        L.ec_engine_step.argtypes = [vp, i32]
+        L.ec_engine_sync.argtypes = [vp]
+        L.ec_engine_get_tokens.argtypes = [vp, vp, vp]
+        L.ec_engine_get_logits.argtypes = [vp, vp, u32]
+        L.ec_engine_stream.argtypes = [vp]
+        L.ec_engine_stream.restype = vp
+        L.ec_engine_weight_bytes.argtypes = [vp]
+        L.ec_engine_weight_bytes.restype = C.c_size_t
+        L.ec_engine_profile_step.argtypes = [vp, u32, vp, vp, vp, C.POINTER(u32)]
+        c = _Cfg(**{f.name: getattr(cfg, f.name) for f in fields(cfg)})
+        h = vp()
+        self._check(L.ec_engine_create(C.byref(c), C.byref(h)), "ec_engine_create")
+        self.h = h
+
+    def _check(self, rc, name):
+        if rc != 0:
+            raise EchoHipError(f"{name} failed ({rc}): {self.L.ec_last_error().decode()}")
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.L.ec_engine_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    # ---- weights
+    def set_tensor(self, layer: int, tensor: int, arr: np.ndarray):
+        a = np.ascontiguousarray(arr)
+        self._check(self.L.ec_engine_set_tensor(self.h, layer, tensor, a.ctypes.data, a.nbytes), "set_tensor")
+
+    def get_tensor(self, layer: int, tensor: int, nbytes: int, dtype=np.uint8) -> np.ndarray:
+        out = np.empty(nbytes, np.uint8)
+        self._check(self.L.ec_engine_get_tensor(self.h, layer, tensor, out.ctypes.data, nbytes), "get_tensor")
+        return out.view(dtype)
+
+    def init_random(self, seed: int = 0, w_scale: float = 0.02 / 73.0):
+        self._check(self.L.ec_engine_init_random(self.h, seed, w_scale), "init_random")
+
+    # ---- running
+    def reset(self):
+        self._check(self.L.ec_engine_reset(self.h), "reset")
+
+    def set_inputs(self, tok, pos):
+        t = np.ascontiguousarray(tok, np.int32)
+        p = np.ascontiguousarray(pos, np.int32)
+        assert t.size == p.size
+        self._check(self.L.ec_engine_set_inputs(self.h, t.ctypes.data, p.ctypes.data, t.size), "set_inputs")
+
+    def step(self, graph: bool = True):
+        self._check(self.L.ec_engine_step(self.h, int(graph)), "step")
+
+    def sync(self):
+        self._check(self.L.ec_engine_sync(self.h), "sync")
+
+    def tokens(self):
+        B = self.cfg.max_batch
+        gen = np.zeros(B, np.int32)
+        pos = np.zeros(B, np.int32)
+        self._check(self.L.ec_engine_get_tokens(self.h, gen.ctypes.data, pos.ctypes.data), "get_tokens")
+        return gen, pos
+
+    def logits(self, seq: int):
+        out = np.zeros(self.cfg.vocab, np.float32)
+        self._check(self.L.ec_engine_get_logits(self.h, out.ctypes.data, seq), "get_logits")
+        return out
+
+    @property
+    def stream(self) -> int:
+        return self.L.ec_engine_stream(self.h)
+
+    def weight_bytes(self) -> int:
+        return self.L.ec_engine_weight_bytes(self.h)
+
+    def profile_step(self, cap: int = 4096):
+        kind = np.zeros(cap, np.int32)
+        by = np.zeros(cap, np.float64)
+        us = np.zeros(cap, np.float64)
+        n = C.c_uint32()
+        self._check(self.L.ec_engine_profile_step(self.h, cap, kind.ctypes.data, by.ctypes.data, us.ctypes.data,
+                                                  C.byref(n)), "profile_step")
+        m = min(n.value, cap)
+        return by[:m], us[:m]

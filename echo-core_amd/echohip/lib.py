@@ -36,7 +36,7 @@ _SIGS = {
     "ec_dequantize_to_fp16": [C.c_int, _vp, _vp, _sz, _vp],
     "ec_kv_append": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u64, _u32, _u32, _vp],
     "ec_attn_decode": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u64, _u32, _u32, _u32, _u32, _vp, _vp],
-    "ec_deltanet": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp],
+    "ec_deltanet": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp, _vp],
     "ec_fill_random": [C.c_int, _vp, _u64, _u64, C.c_float, _u32, _vp],
     "ec_stream_read": [_vp, _sz, _vp, _u32, _vp],
 }
@@ -61,6 +61,10 @@ def _ptr(x):
 
 class Lib:
     def __init__(self, path: Path = LIBPATH):
+        # torch ships its own HIP runtime (same soname, different DT_NEEDED
+        # name).  Loading torch first makes libechohip bind to that runtime, so
+        # one process never holds two HIP runtimes.
+        import torch  # noqa: F401
         if not path.exists():
             raise FileNotFoundError(f"{path} is not built: run __graft_entry__.build() (make -C echo-core_amd)")
         self.path = path
@@ -139,9 +143,9 @@ class Lib:
         self._call("ec_attn_decode", _ptr(q), _ptr(keys), _ptr(vals), _ptr(ks), _ptr(vs), _ptr(out), _ptr(ctx),
                    n_seq, seq_stride, n_heads, n_kv, head_dim, max_ctx, _ptr(ws), self._stream(stream))
 
-    def deltanet(self, state, q, k, v, decay, beta, out, T, n_seq, n_v, n_k, d_k, d_v, stream=None):
+    def deltanet(self, state, q, k, v, decay, beta, out, T, n_seq, n_v, n_k, d_k, d_v, seq_pos=None, stream=None):
         self._call("ec_deltanet", _ptr(state), _ptr(q), _ptr(k), _ptr(v), _ptr(decay), _ptr(beta), _ptr(out), T,
-                   n_seq, n_v, n_k, d_k, d_v, self._stream(stream))
+                   n_seq, n_v, n_k, d_k, d_v, _ptr(seq_pos), self._stream(stream))
 
     def stream_read(self, src, nbytes, out, blocks, stream=None):
         self._call("ec_stream_read", _ptr(src), nbytes, _ptr(out), blocks, self._stream(stream))

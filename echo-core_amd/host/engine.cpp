@@ -1,0 +1,609 @@
+// engine.cpp — device-resident hybrid decoder behind the C ABI of echo_engine.h.
+//
+// Host control only: every operation is a call into libechohip's C ABI
+// (echo_hip.h), launched on the engine's stream; a decode step is captured
+// once into a HIP graph and replayed.  Layer structure and op order follow
+// echo-core-zig/src/inference/engine.zig:397-463 (layerForward), the attention
+// block :520-621 and qwen_linear.forward (kernels/qwen_linear.zig:103-271).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "echo_engine.h"
+#include "echo_hip.h"
+
+namespace {
+
+#define EC_HIP(call)                                                             \
+    do {                                                                         \
+        hipError_t _e = (call);                                                  \
+        if (_e != hipSuccess) return ec_set_hip_error_host(_e, #call);           \
+    } while (0)
+#define EC_TRY(call)                  \
+    do {                                \
+        int _rc = (call);               \
+        if (_rc != EC_OK) return _rc;   \
+    } while (0)
+
+extern "C" int ec_set_error(int code, const char* msg);
+extern "C" int ec_set_hip_error(hipError_t e, const char* where);
+int ec_set_hip_error_host(hipError_t e, const char* where) { return ec_set_hip_error(e, where); }
+
+// splitmix64 / Box-Muller, identical to echohip/synth.py.
+uint64_t sm64(uint64_t seed, uint64_t i) {
+    uint64_t z = seed + (i + 1) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+double u01(uint64_t z) { return (double)(z >> 40) * (1.0 / 16777216.0); }
+double normal_at(uint64_t seed, uint64_t i) {
+    double a = 1.0 - u01(sm64(seed, 2 * i)), b = u01(sm64(seed, 2 * i + 1));
+    return std::sqrt(-2.0 * std::log(a)) * std::cos(6.283185307179586 * b);
+}
+
+struct Mat {
+    void* tiled = nullptr;
+    uint32_t N = 0, K = 0;
+};
+
+struct Layer {
+    bool attn = false;
+    Mat w_in, w_out, w_gu, w_down;
+    float* attn_norm = nullptr;
+    float* ffn_norm = nullptr;
+    float* conv_w = nullptr;
+    float* a_log = nullptr;
+    float* dt_bias = nullptr;
+    float* ssm_norm = nullptr;
+    float* conv_state = nullptr;
+    float* ssm_state = nullptr;
+    float* q_norm = nullptr;
+    float* k_norm = nullptr;
+    int use_qn = 0, use_kn = 0;
+    int8_t* keys = nullptr;
+    int8_t* vals = nullptr;
+    float* ks = nullptr;
+    float* vs = nullptr;
+};
+
+}  // namespace
+
+struct ec_engine {
+    ec_engine_cfg c{};
+    hipStream_t st = nullptr;
+    std::vector<Layer> L;
+    void* embed = nullptr;
+    float* final_norm = nullptr;
+    Mat lm_head;
+    uint32_t B = 0, H = 0, F = 0, q_dim = 0, kv_dim = 0, value_dim = 0, key_dim = 0, conv_dim = 0, n_v = 0, n_k = 0;
+    uint32_t nin_delta = 0, nin_attn = 0, nin_max = 0;
+    uint64_t seq_stride = 0;
+    float *x = nullptr, *proj = nullptr, *gu = nullptr, *core = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
+    float *dec = nullptr, *beta = nullptr, *qbuf = nullptr, *attn_out = nullptr, *logits = nullptr;
+    float* inv_freq = nullptr;
+    void *act_h = nullptr, *act_v = nullptr, *act_f = nullptr, *act_q = nullptr, *attn_ws = nullptr;
+    int32_t *tok = nullptr, *pos = nullptr, *gen = nullptr, *ctx = nullptr;
+    int32_t* h_io = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    std::vector<void*> allocs;
+    size_t weight_bytes = 0;
+    // profiling hooks (eager step only)
+    std::vector<hipEvent_t>* prof_ev = nullptr;
+    std::vector<double>* prof_bytes = nullptr;
+};
+
+namespace {
+
+int dalloc(ec_engine* e, void** p, size_t bytes) {
+    EC_HIP(hipMalloc(p, bytes ? bytes : 16));
+    EC_HIP(hipMemsetAsync(*p, 0, bytes ? bytes : 16, e->st));
+    e->allocs.push_back(*p);
+    return EC_OK;
+}
+template <class T>
+int dalloc(ec_engine* e, T** p, size_t count) {
+    return dalloc(e, (void**)p, count * sizeof(T));
+}
+
+int alloc_mat(ec_engine* e, Mat& m, uint32_t N, uint32_t K) {
+    m.N = N;
+    m.K = K;
+    return dalloc(e, &m.tiled, ec_tiled_bytes(EC_Q8_0, N, K));
+}
+
+bool is_attn(const ec_engine_cfg& c, uint32_t l) { return c.attn_interval && ((l + 1) % c.attn_interval) == 0; }
+
+size_t gguf_bytes(uint32_t N, uint32_t K) { return (size_t)N * (K / 32) * 34; }
+
+// Upload GGUF bytes (host) of rows [row0, row0+N) of matrix m's logical rows
+// and repack them into the tiled layout at that tile offset (row0 % 16 == 0).
+int upload_rows(ec_engine* e, Mat& m, uint32_t row0, const void* host, uint32_t N) {
+    if (row0 % 16 || row0 + N > m.N) return ec_set_error(EC_ERR_ARG, "engine: bad row range");
+    void* tmp = nullptr;
+    EC_HIP(hipMalloc(&tmp, gguf_bytes(N, m.K)));
+    EC_HIP(hipMemcpyAsync(tmp, host, gguf_bytes(N, m.K), hipMemcpyHostToDevice, e->st));
+    uint8_t* dst = (uint8_t*)m.tiled + ec_tiled_bytes(EC_Q8_0, row0, m.K);
+    int rc = ec_repack(EC_Q8_0, tmp, dst, N, m.K, e->st);
+    EC_HIP(hipStreamSynchronize(e->st));
+    EC_HIP(hipFree(tmp));
+    return rc;
+}
+
+int random_rows(ec_engine* e, Mat& m, uint32_t row0, uint32_t N, uint64_t seed, float scale, void* tmp) {
+    EC_TRY(ec_fill_random(1, tmp, (uint64_t)N * (m.K / 32), seed, scale, m.K, e->st));
+    uint8_t* dst = (uint8_t*)m.tiled + ec_tiled_bytes(EC_Q8_0, row0, m.K);
+    return ec_repack(EC_Q8_0, tmp, dst, N, m.K, e->st);
+}
+
+int upload_vec(ec_engine* e, float* dst, const std::vector<float>& v) {
+    EC_HIP(hipMemcpy(dst, v.data(), v.size() * sizeof(float), hipMemcpyHostToDevice));
+    return EC_OK;
+}
+
+std::vector<float> gen_vec(uint64_t seed, size_t n, double mean, double std) {
+    std::vector<float> v(n);
+    for (size_t i = 0; i < n; ++i) v[i] = (float)(mean + std * normal_at(seed, i));
+    return v;
+}
+
+// One matvec launch, optionally bracketed by profiling events.
+int mv(ec_engine* e, const Mat& m, const void* act, float* y, uint32_t ldy, int acc) {
+    if (e->prof_ev) {
+        hipEvent_t a, b;
+        EC_HIP(hipEventCreate(&a));
+        EC_HIP(hipEventCreate(&b));
+        EC_HIP(hipEventRecord(a, e->st));
+        EC_TRY(ec_matvec(EC_Q8_0, m.tiled, act, y, e->B, m.N, m.K, ldy, acc, e->st));
+        EC_HIP(hipEventRecord(b, e->st));
+        e->prof_ev->push_back(a);
+        e->prof_ev->push_back(b);
+        const double bytes = (double)gguf_bytes(m.N, m.K) + (double)e->B * (m.K + m.K / 32 * 4) +
+                             (double)e->B * m.N * 4 * (acc ? 2 : 1);
+        e->prof_bytes->push_back(bytes);
+        return EC_OK;
+    }
+    return ec_matvec(EC_Q8_0, m.tiled, act, y, e->B, m.N, m.K, ldy, acc, e->st);
+}
+
+// The decode step (stream-ordered; captured once into a graph).
+int record_step(ec_engine* e) {
+    const ec_engine_cfg& c = e->c;
+    const uint32_t B = e->B, H = e->H, F = e->F;
+    hipStream_t st = e->st;
+    EC_TRY(ec_glue_embed(e->embed, e->tok, e->x, B, H, c.vocab, st));
+    for (uint32_t l = 0; l < c.n_layers; ++l) {
+        Layer& y = e->L[l];
+        EC_TRY(ec_glue_rmsnorm_quant(e->x, y.attn_norm, e->act_h, B, H, st));
+        if (!y.attn) {
+            const uint32_t Nin = e->nin_delta;
+            EC_TRY(mv(e, y.w_in, e->act_h, e->proj, Nin, 0));
+            EC_TRY(ec_glue_conv_gates(e->proj, Nin, y.conv_state, y.conv_w, y.a_log, y.dt_bias, e->q, e->k, e->v,
+                                      e->dec, e->beta, e->pos, B, e->n_k, e->n_v, c.conv_kernel, st));
+            EC_TRY(ec_deltanet(y.ssm_state, e->q, e->k, e->v, e->dec, e->beta, e->core, 1, B, e->n_v, e->n_k, 128,
+                               128, e->pos, st));
+            EC_TRY(ec_glue_gated_norm_quant(e->core, e->proj, Nin, e->conv_dim, y.ssm_norm, e->act_v, B, e->n_v,
+                                            st));
+            EC_TRY(mv(e, y.w_out, e->act_v, e->x, H, 1));
+        } else {
+            const uint32_t Nin = e->nin_attn;
+            EC_TRY(mv(e, y.w_in, e->act_h, e->proj, Nin, 0));
+            EC_TRY(ec_glue_qk_rope_append(e->proj, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn, e->inv_freq, e->pos,
+                                          e->qbuf, y.keys, y.vals, y.ks, y.vs, e->ctx, B, e->seq_stride, c.max_ctx,
+                                          c.n_heads, c.n_kv, c.head_dim, st));
+            EC_TRY(ec_attn_decode(e->qbuf, y.keys, y.vals, y.ks, y.vs, e->attn_out, e->ctx, B, e->seq_stride,
+                                  c.n_heads, c.n_kv, c.head_dim, c.max_ctx, e->attn_ws, st));
+            EC_TRY(ec_quantize_act(EC_Q8_0, e->attn_out, e->act_q, B, e->q_dim, st));
+            EC_TRY(mv(e, y.w_out, e->act_q, e->x, H, 1));
+        }
+        EC_TRY(ec_glue_rmsnorm_quant(e->x, y.ffn_norm, e->act_h, B, H, st));
+        EC_TRY(mv(e, y.w_gu, e->act_h, e->gu, 2 * F, 0));
+        EC_TRY(ec_glue_swiglu_quant(e->gu, e->act_f, B, F, st));
+        EC_TRY(mv(e, y.w_down, e->act_f, e->x, H, 1));
+    }
+    EC_TRY(ec_glue_rmsnorm_quant(e->x, e->final_norm, e->act_h, B, H, st));
+    EC_TRY(mv(e, e->lm_head, e->act_h, e->logits, c.vocab, 0));
+    EC_TRY(ec_glue_argmax_advance(e->logits, c.vocab, e->gen, e->tok, e->pos, B, st));
+    return EC_OK;
+}
+
+int destroy_graph(ec_engine* e) {
+    if (e->exec) (void)hipGraphExecDestroy(e->exec);
+    if (e->graph) (void)hipGraphDestroy(e->graph);
+    e->exec = nullptr;
+    e->graph = nullptr;
+    return EC_OK;
+}
+
+}  // namespace
+
+extern "C" int ec_engine_create(const ec_engine_cfg* cfg, ec_engine** out) {
+    if (!cfg || !out) return ec_set_error(EC_ERR_ARG, "ec_engine_create: null argument");
+    const ec_engine_cfg& c = *cfg;
+    if (c.hidden % 128 || c.ffn % 128 || c.head_dim != 256 || c.n_kv == 0 || c.n_heads % c.n_kv ||
+        c.ssm_heads == 0 || c.ssm_inner != c.ssm_heads * 128 || (c.ssm_heads / 2) % 1 || c.ssm_inner % 256 ||
+        c.max_batch == 0 || c.max_batch > 16 || c.max_ctx == 0 || c.conv_kernel == 0 || c.vocab == 0)
+        return ec_set_error(EC_ERR_ARG,
+                            "ec_engine_create: need hidden, ffn % 128 == 0, head_dim 256, ssm_inner = 128*ssm_heads, "
+                            "1 <= max_batch <= 16");
+    ec_engine* e = new ec_engine();
+    e->c = c;
+    e->B = c.max_batch;
+    e->H = c.hidden;
+    e->F = c.ffn;
+    e->q_dim = c.n_heads * c.head_dim;
+    e->kv_dim = c.n_kv * c.head_dim;
+    e->value_dim = c.ssm_inner;
+    e->key_dim = c.ssm_inner / 2;  // qwen_linear.zig:117-119
+    e->n_v = c.ssm_heads;
+    e->n_k = e->key_dim / 128;
+    e->conv_dim = 2 * e->key_dim + e->value_dim;
+    e->nin_delta = e->conv_dim + e->value_dim + 2 * e->n_v;
+    e->nin_attn = e->q_dim + 2 * e->kv_dim;
+    e->nin_max = std::max(e->nin_delta, e->nin_attn);
+    e->seq_stride = (uint64_t)c.max_ctx * e->kv_dim;
+    int rc = EC_OK;
+    auto fail = [&](int r) {
+        ec_engine_destroy(e);
+        return r;
+    };
+    if (hipStreamCreateWithFlags(&e->st, hipStreamNonBlocking) != hipSuccess)
+        return fail(ec_set_error(EC_ERR_HIP, "ec_engine_create: stream"));
+    const uint32_t B = e->B, H = e->H;
+    e->L.resize(c.n_layers);
+    size_t wb = 0;
+    for (uint32_t l = 0; l < c.n_layers && rc == EC_OK; ++l) {
+        Layer& y = e->L[l];
+        y.attn = is_attn(c, l);
+        const uint32_t Nin = y.attn ? e->nin_attn : e->nin_delta;
+        const uint32_t Kout = y.attn ? e->q_dim : e->value_dim;
+        if ((rc = alloc_mat(e, y.w_in, Nin, H)) || (rc = alloc_mat(e, y.w_out, H, Kout)) ||
+            (rc = alloc_mat(e, y.w_gu, 2 * e->F, H)) || (rc = alloc_mat(e, y.w_down, H, e->F)) ||
+            (rc = dalloc(e, &y.attn_norm, H)) || (rc = dalloc(e, &y.ffn_norm, H)))
+            break;
+        wb += ec_tiled_bytes(EC_Q8_0, Nin, H) + ec_tiled_bytes(EC_Q8_0, H, Kout) +
+              ec_tiled_bytes(EC_Q8_0, 2 * e->F, H) + ec_tiled_bytes(EC_Q8_0, H, e->F) + 2 * H * 4;
+        if (!y.attn) {
+            if ((rc = dalloc(e, &y.conv_w, (size_t)c.conv_kernel * e->conv_dim)) ||
+                (rc = dalloc(e, &y.a_log, e->n_v)) || (rc = dalloc(e, &y.dt_bias, e->n_v)) ||
+                (rc = dalloc(e, &y.ssm_norm, 128)) ||
+                (rc = dalloc(e, &y.conv_state, (size_t)B * c.conv_kernel * e->conv_dim)) ||
+                (rc = dalloc(e, &y.ssm_state, (size_t)B * e->n_v * 128 * 128)))
+                break;
+            wb += ((size_t)c.conv_kernel * e->conv_dim + 2 * e->n_v + 128) * 4;
+        } else {
+            if ((rc = dalloc(e, &y.q_norm, c.head_dim)) || (rc = dalloc(e, &y.k_norm, c.head_dim)) ||
+                (rc = dalloc(e, &y.keys, (size_t)B * e->seq_stride)) ||
+                (rc = dalloc(e, &y.vals, (size_t)B * e->seq_stride)) ||
+                (rc = dalloc(e, &y.ks, (size_t)B * c.max_ctx * c.n_kv)) ||
+                (rc = dalloc(e, &y.vs, (size_t)B * c.max_ctx * c.n_kv)))
+                break;
+            wb += 2 * c.head_dim * 4;
+        }
+    }
+    if (rc) return fail(rc);
+    wb += ec_tiled_bytes(EC_Q8_0, c.vocab, H) + H * 4;
+    e->weight_bytes = wb;
+    const size_t maxK = std::max(std::max(H, e->F), std::max(e->value_dim, e->q_dim));
+    (void)maxK;
+    if ((rc = dalloc(e, &e->embed, gguf_bytes(c.vocab, H))) || (rc = dalloc(e, &e->final_norm, H)) ||
+        (rc = alloc_mat(e, e->lm_head, c.vocab, H)) || (rc = dalloc(e, &e->x, (size_t)B * H)) ||
+        (rc = dalloc(e, &e->proj, (size_t)B * e->nin_max)) || (rc = dalloc(e, &e->gu, (size_t)B * 2 * e->F)) ||
+        (rc = dalloc(e, &e->core, (size_t)B * e->value_dim)) || (rc = dalloc(e, &e->q, (size_t)B * e->key_dim)) ||
+        (rc = dalloc(e, &e->k, (size_t)B * e->key_dim)) || (rc = dalloc(e, &e->v, (size_t)B * e->value_dim)) ||
+        (rc = dalloc(e, &e->dec, (size_t)B * e->n_v)) || (rc = dalloc(e, &e->beta, (size_t)B * e->n_v)) ||
+        (rc = dalloc(e, &e->qbuf, (size_t)B * e->q_dim)) || (rc = dalloc(e, &e->attn_out, (size_t)B * e->q_dim)) ||
+        (rc = dalloc(e, &e->logits, (size_t)B * c.vocab)) || (rc = dalloc(e, &e->inv_freq, c.head_dim / 2)) ||
+        (rc = dalloc(e, &e->act_h, ec_act_bytes(EC_Q8_0, B, H))) ||
+        (rc = dalloc(e, &e->act_v, ec_act_bytes(EC_Q8_0, B, e->value_dim))) ||
+        (rc = dalloc(e, &e->act_f, ec_act_bytes(EC_Q8_0, B, e->F))) ||
+        (rc = dalloc(e, &e->act_q, ec_act_bytes(EC_Q8_0, B, e->q_dim))) ||
+        (rc = dalloc(e, &e->attn_ws, ec_attn_ws_bytes(B, c.n_heads, c.head_dim, c.max_ctx))) ||
+        (rc = dalloc(e, &e->tok, B)) || (rc = dalloc(e, &e->pos, B)) || (rc = dalloc(e, &e->gen, B)) ||
+        (rc = dalloc(e, &e->ctx, B)))
+        return fail(rc);
+    if (hipHostMalloc((void**)&e->h_io, 4 * 16 * sizeof(int32_t)) != hipSuccess)
+        return fail(ec_set_error(EC_ERR_HIP, "ec_engine_create: pinned buffer"));
+    // RoPE inverse frequencies, 1/pow(base, i/head_dim) in fp32 (engine.zig:476)
+    std::vector<float> inv(c.head_dim / 2);
+    for (uint32_t i = 0; i < c.head_dim; i += 2)
+        inv[i / 2] = 1.0f / powf(c.rope_base, (float)i / (float)c.head_dim);
+    if ((rc = upload_vec(e, e->inv_freq, inv))) return fail(rc);
+    std::vector<int32_t> neg(B, -1);
+    if (hipMemcpy(e->pos, neg.data(), B * 4, hipMemcpyHostToDevice) != hipSuccess)
+        return fail(ec_set_error(EC_ERR_HIP, "ec_engine_create: pos"));
+    if (hipStreamSynchronize(e->st) != hipSuccess) return fail(ec_set_error(EC_ERR_HIP, "ec_engine_create: sync"));
+    *out = e;
+    return EC_OK;
+}
+
+extern "C" void ec_engine_destroy(ec_engine* e) {
+    if (!e) return;
+    if (e->st) (void)hipStreamSynchronize(e->st);
+    destroy_graph(e);
+    for (void* p : e->allocs) (void)hipFree(p);
+    if (e->h_io) (void)hipHostFree(e->h_io);
+    if (e->st) (void)hipStreamDestroy(e->st);
+    delete e;
+}
+
+extern "C" int ec_engine_set_tensor(ec_engine* e, int layer, int tensor, const void* host, size_t bytes) {
+    if (!e || !host) return ec_set_error(EC_ERR_ARG, "ec_engine_set_tensor: null argument");
+    const ec_engine_cfg& c = e->c;
+    auto need = [&](size_t n) -> int {
+        if (bytes != n) {
+            char buf[160];
+            snprintf(buf, sizeof buf, "ec_engine_set_tensor(%d, %d): %zu bytes given, %zu expected", layer, tensor,
+                     bytes, n);
+            return ec_set_error(EC_ERR_ARG, buf);
+        }
+        return EC_OK;
+    };
+    auto vec = [&](float* dst, size_t n) -> int {
+        EC_TRY(need(n * 4));
+        EC_HIP(hipMemcpy(dst, host, bytes, hipMemcpyHostToDevice));
+        return EC_OK;
+    };
+    if (tensor == EC_T_EMBED) {
+        EC_TRY(need(gguf_bytes(c.vocab, e->H)));
+        EC_HIP(hipMemcpy(e->embed, host, bytes, hipMemcpyHostToDevice));
+        return EC_OK;
+    }
+    if (tensor == EC_T_FINAL_NORM) return vec(e->final_norm, e->H);
+    if (tensor == EC_T_LM_HEAD) {
+        EC_TRY(need(gguf_bytes(c.vocab, e->H)));
+        return upload_rows(e, e->lm_head, 0, host, c.vocab);
+    }
+    if (layer < 0 || (uint32_t)layer >= c.n_layers) return ec_set_error(EC_ERR_ARG, "ec_engine_set_tensor: layer");
+    Layer& y = e->L[layer];
+    destroy_graph(e);  // weights are captured by address only, but keep the rule simple
+    switch (tensor) {
+        case EC_T_ATTN_NORM: return vec(y.attn_norm, e->H);
+        case EC_T_FFN_NORM: return vec(y.ffn_norm, e->H);
+        case EC_T_W_IN: EC_TRY(need(gguf_bytes(y.w_in.N, e->H))); return upload_rows(e, y.w_in, 0, host, y.w_in.N);
+        case EC_T_W_OUT: EC_TRY(need(gguf_bytes(e->H, y.w_out.K))); return upload_rows(e, y.w_out, 0, host, e->H);
+        case EC_T_W_GATE: EC_TRY(need(gguf_bytes(e->F, e->H))); return upload_rows(e, y.w_gu, 0, host, e->F);
+        case EC_T_W_UP: EC_TRY(need(gguf_bytes(e->F, e->H))); return upload_rows(e, y.w_gu, e->F, host, e->F);
+        case EC_T_W_DOWN: EC_TRY(need(gguf_bytes(e->H, e->F))); return upload_rows(e, y.w_down, 0, host, e->H);
+        default: break;
+    }
+    if (!y.attn) {
+        switch (tensor) {
+            case EC_T_CONV_W: return vec(y.conv_w, (size_t)c.conv_kernel * e->conv_dim);
+            case EC_T_A_LOG: return vec(y.a_log, e->n_v);
+            case EC_T_DT_BIAS: return vec(y.dt_bias, e->n_v);
+            case EC_T_SSM_NORM: return vec(y.ssm_norm, 128);
+            default: break;
+        }
+    } else if (tensor == EC_T_Q_NORM || tensor == EC_T_K_NORM) {
+        EC_TRY(need((size_t)c.head_dim * 4));
+        const float* f = (const float*)host;
+        int nz = 0;
+        for (uint32_t i = 0; i < c.head_dim; ++i) nz |= f[i] != 0.0f;
+        (tensor == EC_T_Q_NORM ? y.use_qn : y.use_kn) = nz;
+        return vec(tensor == EC_T_Q_NORM ? y.q_norm : y.k_norm, c.head_dim);
+    }
+    return ec_set_error(EC_ERR_ARG, "ec_engine_set_tensor: tensor id not valid for this layer");
+}
+
+namespace {
+int download_rows(ec_engine* e, const Mat& m, uint32_t row0, void* host, uint32_t N) {
+    void* tmp = nullptr;
+    EC_HIP(hipMalloc(&tmp, gguf_bytes(N, m.K)));
+    const uint8_t* src = (const uint8_t*)m.tiled + ec_tiled_bytes(EC_Q8_0, row0, m.K);
+    int rc = ec_unpack_tiled(EC_Q8_0, src, tmp, N, m.K, e->st);
+    if (!rc && hipMemcpyAsync(host, tmp, gguf_bytes(N, m.K), hipMemcpyDeviceToHost, e->st) != hipSuccess)
+        rc = ec_set_error(EC_ERR_HIP, "download_rows: copy");
+    (void)hipStreamSynchronize(e->st);
+    (void)hipFree(tmp);
+    return rc;
+}
+}  // namespace
+
+extern "C" int ec_engine_get_tensor(ec_engine* e, int layer, int tensor, void* host, size_t bytes) {
+    if (!e || !host) return ec_set_error(EC_ERR_ARG, "ec_engine_get_tensor: null argument");
+    const ec_engine_cfg& c = e->c;
+    auto need = [&](size_t n) -> int {
+        return bytes == n ? EC_OK : ec_set_error(EC_ERR_ARG, "ec_engine_get_tensor: wrong byte count");
+    };
+    auto vec = [&](const float* src, size_t n) -> int {
+        EC_TRY(need(n * 4));
+        EC_HIP(hipMemcpy(host, src, bytes, hipMemcpyDeviceToHost));
+        return EC_OK;
+    };
+    if (tensor == EC_T_EMBED) {
+        EC_TRY(need(gguf_bytes(c.vocab, e->H)));
+        EC_HIP(hipMemcpy(host, e->embed, bytes, hipMemcpyDeviceToHost));
+        return EC_OK;
+    }
+    if (tensor == EC_T_FINAL_NORM) return vec(e->final_norm, e->H);
+    if (tensor == EC_T_LM_HEAD) {
+        EC_TRY(need(gguf_bytes(c.vocab, e->H)));
+        return download_rows(e, e->lm_head, 0, host, c.vocab);
+    }
+    if (layer < 0 || (uint32_t)layer >= c.n_layers) return ec_set_error(EC_ERR_ARG, "ec_engine_get_tensor: layer");
+    const Layer& y = e->L[layer];
+    switch (tensor) {
+        case EC_T_ATTN_NORM: return vec(y.attn_norm, e->H);
+        case EC_T_FFN_NORM: return vec(y.ffn_norm, e->H);
+        case EC_T_W_IN: EC_TRY(need(gguf_bytes(y.w_in.N, e->H))); return download_rows(e, y.w_in, 0, host, y.w_in.N);
+        case EC_T_W_OUT: EC_TRY(need(gguf_bytes(e->H, y.w_out.K))); return download_rows(e, y.w_out, 0, host, e->H);
+        case EC_T_W_GATE: EC_TRY(need(gguf_bytes(e->F, e->H))); return download_rows(e, y.w_gu, 0, host, e->F);
+        case EC_T_W_UP: EC_TRY(need(gguf_bytes(e->F, e->H))); return download_rows(e, y.w_gu, e->F, host, e->F);
+        case EC_T_W_DOWN: EC_TRY(need(gguf_bytes(e->H, e->F))); return download_rows(e, y.w_down, 0, host, e->H);
+        default: break;
+    }
+    if (!y.attn) {
+        switch (tensor) {
+            case EC_T_CONV_W: return vec(y.conv_w, (size_t)c.conv_kernel * e->conv_dim);
+            case EC_T_A_LOG: return vec(y.a_log, e->n_v);
+            case EC_T_DT_BIAS: return vec(y.dt_bias, e->n_v);
+            case EC_T_SSM_NORM: return vec(y.ssm_norm, 128);
+            default: break;
+        }
+    } else if (tensor == EC_T_Q_NORM) {
+        return vec(y.q_norm, c.head_dim);
+    } else if (tensor == EC_T_K_NORM) {
+        return vec(y.k_norm, c.head_dim);
+    }
+    return ec_set_error(EC_ERR_ARG, "ec_engine_get_tensor: tensor id not valid for this layer");
+}
+
+extern "C" int ec_engine_init_random(ec_engine* e, uint64_t seed, float w_scale) {
+    if (!e) return ec_set_error(EC_ERR_ARG, "ec_engine_init_random: null engine");
+    const ec_engine_cfg& c = e->c;
+    destroy_graph(e);
+    size_t tmp_bytes = gguf_bytes(c.vocab, e->H);
+    for (const Layer& y : e->L)
+        tmp_bytes = std::max(tmp_bytes, std::max(gguf_bytes(y.w_in.N, e->H), gguf_bytes(e->F, e->H)));
+    void* tmp = nullptr;
+    EC_HIP(hipMalloc(&tmp, tmp_bytes));
+    uint64_t stream_id = 0;
+    auto next_seed = [&]() { return sm64(seed, stream_id++); };
+    int rc = EC_OK;
+    // embedding (GGUF rows, looked up in place) and the output head
+    rc = ec_fill_random(1, e->embed, (uint64_t)c.vocab * (e->H / 32), next_seed(), w_scale, e->H, e->st);
+    if (!rc) rc = random_rows(e, e->lm_head, 0, c.vocab, next_seed(), w_scale, tmp);
+    if (!rc) rc = upload_vec(e, e->final_norm, gen_vec(next_seed(), e->H, 1.0, 0.1));
+    for (uint32_t l = 0; l < c.n_layers && !rc; ++l) {
+        Layer& y = e->L[l];
+        rc = random_rows(e, y.w_in, 0, y.w_in.N, next_seed(), w_scale, tmp);
+        if (!rc) rc = random_rows(e, y.w_out, 0, e->H, next_seed(), w_scale, tmp);
+        if (!rc) rc = random_rows(e, y.w_gu, 0, e->F, next_seed(), w_scale, tmp);
+        if (!rc) rc = random_rows(e, y.w_gu, e->F, e->F, next_seed(), w_scale, tmp);
+        if (!rc) rc = random_rows(e, y.w_down, 0, e->H, next_seed(), w_scale, tmp);
+        if (!rc) rc = upload_vec(e, y.attn_norm, gen_vec(next_seed(), e->H, 1.0, 0.1));
+        if (!rc) rc = upload_vec(e, y.ffn_norm, gen_vec(next_seed(), e->H, 1.0, 0.1));
+        if (rc) break;
+        if (!y.attn) {
+            rc = upload_vec(e, y.conv_w, gen_vec(next_seed(), (size_t)c.conv_kernel * e->conv_dim, 0.0, 0.5));
+            std::vector<float> al(e->n_v);
+            const uint64_t sa = next_seed();
+            for (uint32_t h = 0; h < e->n_v; ++h) al[h] = (float)std::log(1.0 + 15.0 * u01(sm64(sa, h)));
+            if (!rc) rc = upload_vec(e, y.a_log, al);
+            if (!rc) rc = upload_vec(e, y.dt_bias, gen_vec(next_seed(), e->n_v, 0.0, 0.1));
+            if (!rc) rc = upload_vec(e, y.ssm_norm, gen_vec(next_seed(), 128, 1.0, 0.1));
+        } else {
+            rc = upload_vec(e, y.q_norm, gen_vec(next_seed(), c.head_dim, 1.0, 0.1));
+            if (!rc) rc = upload_vec(e, y.k_norm, gen_vec(next_seed(), c.head_dim, 1.0, 0.1));
+            y.use_qn = y.use_kn = 1;
+        }
+        if (!rc && hipStreamSynchronize(e->st) != hipSuccess) rc = ec_set_error(EC_ERR_HIP, "init_random: sync");
+    }
+    (void)hipStreamSynchronize(e->st);
+    (void)hipFree(tmp);
+    return rc;
+}
+
+extern "C" int ec_engine_reset(ec_engine* e) {
+    if (!e) return ec_set_error(EC_ERR_ARG, "ec_engine_reset: null engine");
+    const ec_engine_cfg& c = e->c;
+    for (Layer& y : e->L) {
+        if (!y.attn) {
+            EC_HIP(hipMemsetAsync(y.conv_state, 0, (size_t)e->B * c.conv_kernel * e->conv_dim * 4, e->st));
+            EC_HIP(hipMemsetAsync(y.ssm_state, 0, (size_t)e->B * e->n_v * 128 * 128 * 4, e->st));
+        } else {
+            EC_HIP(hipMemsetAsync(y.keys, 0, (size_t)e->B * e->seq_stride, e->st));
+            EC_HIP(hipMemsetAsync(y.vals, 0, (size_t)e->B * e->seq_stride, e->st));
+            EC_HIP(hipMemsetAsync(y.ks, 0, (size_t)e->B * c.max_ctx * c.n_kv * 4, e->st));
+            EC_HIP(hipMemsetAsync(y.vs, 0, (size_t)e->B * c.max_ctx * c.n_kv * 4, e->st));
+        }
+    }
+    std::vector<int32_t> neg(e->B, -1);
+    EC_HIP(hipMemcpyAsync(e->pos, neg.data(), e->B * 4, hipMemcpyHostToDevice, e->st));
+    EC_HIP(hipStreamSynchronize(e->st));
+    return EC_OK;
+}
+
+extern "C" int ec_engine_set_inputs(ec_engine* e, const int32_t* tok, const int32_t* pos, uint32_t n) {
+    if (!e || !tok || !pos || n > e->B) return ec_set_error(EC_ERR_ARG, "ec_engine_set_inputs: bad argument");
+    for (uint32_t i = 0; i < e->B; ++i) {
+        const bool in = i < n;
+        int32_t t = in ? tok[i] : 0;
+        if (t < 0 || (uint32_t)t >= e->c.vocab) return ec_set_error(EC_ERR_ARG, "ec_engine_set_inputs: token id");
+        int32_t p = in ? pos[i] : -1;
+        if (p >= 0 && (uint32_t)p >= e->c.max_ctx) return ec_set_error(EC_ERR_ARG, "ec_engine_set_inputs: KV cache full");
+        e->h_io[i] = t;
+        e->h_io[16 + i] = p;
+    }
+    EC_HIP(hipMemcpyAsync(e->tok, e->h_io, e->B * 4, hipMemcpyHostToDevice, e->st));
+    EC_HIP(hipMemcpyAsync(e->pos, e->h_io + 16, e->B * 4, hipMemcpyHostToDevice, e->st));
+    return EC_OK;
+}
+
+extern "C" int ec_engine_step(ec_engine* e, int use_graph) {
+    if (!e) return ec_set_error(EC_ERR_ARG, "ec_engine_step: null engine");
+    if (!use_graph) return record_step(e);
+    if (!e->exec) {
+        EC_HIP(hipStreamBeginCapture(e->st, hipStreamCaptureModeThreadLocal));
+        int rc = record_step(e);
+        hipGraph_t g = nullptr;
+        hipError_t ce = hipStreamEndCapture(e->st, &g);
+        if (rc) {
+            if (g) (void)hipGraphDestroy(g);
+            return rc;
+        }
+        if (ce != hipSuccess) return ec_set_hip_error_host(ce, "ec_engine_step: end capture");
+        e->graph = g;
+        EC_HIP(hipGraphInstantiate(&e->exec, e->graph, nullptr, nullptr, 0));
+    }
+    EC_HIP(hipGraphLaunch(e->exec, e->st));
+    return EC_OK;
+}
+
+extern "C" int ec_engine_sync(ec_engine* e) {
+    if (!e) return ec_set_error(EC_ERR_ARG, "ec_engine_sync: null engine");
+    EC_HIP(hipStreamSynchronize(e->st));
+    return EC_OK;
+}
+
+extern "C" int ec_engine_get_tokens(ec_engine* e, int32_t* gen, int32_t* pos) {
+    if (!e) return ec_set_error(EC_ERR_ARG, "ec_engine_get_tokens: null engine");
+    EC_HIP(hipStreamSynchronize(e->st));
+    if (gen) EC_HIP(hipMemcpy(gen, e->gen, e->B * 4, hipMemcpyDeviceToHost));
+    if (pos) EC_HIP(hipMemcpy(pos, e->pos, e->B * 4, hipMemcpyDeviceToHost));
+    return EC_OK;
+}
+
+extern "C" int ec_engine_get_logits(ec_engine* e, float* host, uint32_t seq) {
+    if (!e || !host || seq >= e->B) return ec_set_error(EC_ERR_ARG, "ec_engine_get_logits: bad argument");
+    EC_HIP(hipStreamSynchronize(e->st));
+    EC_HIP(hipMemcpy(host, e->logits + (size_t)seq * e->c.vocab, (size_t)e->c.vocab * 4, hipMemcpyDeviceToHost));
+    return EC_OK;
+}
+
+extern "C" void* ec_engine_stream(ec_engine* e) { return e ? (void*)e->st : nullptr; }
+
+extern "C" size_t ec_engine_weight_bytes(const ec_engine* e) { return e ? e->weight_bytes : 0; }
+
+extern "C" int ec_engine_profile_step(ec_engine* e, uint32_t cap, int32_t* kind, double* bytes, double* us,
+                                      uint32_t* n) {
+    if (!e || !n) return ec_set_error(EC_ERR_ARG, "ec_engine_profile_step: bad argument");
+    std::vector<hipEvent_t> ev;
+    std::vector<double> by;
+    e->prof_ev = &ev;
+    e->prof_bytes = &by;
+    int rc = record_step(e);
+    e->prof_ev = nullptr;
+    e->prof_bytes = nullptr;
+    if (hipStreamSynchronize(e->st) != hipSuccess && !rc) rc = ec_set_error(EC_ERR_HIP, "profile: sync");
+    uint32_t m = 0;
+    for (size_t i = 0; i + 1 < ev.size(); i += 2) {
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+        if (m < cap) {
+            if (kind) kind[m] = 0;
+            if (bytes) bytes[m] = by[i / 2];
+            if (us) us[m] = ms * 1e3;
+        }
+        ++m;
+    }
+    for (hipEvent_t x : ev) (void)hipEventDestroy(x);
+    *n = m;
+    return rc;
+}

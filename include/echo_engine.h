@@ -1,0 +1,106 @@
+/*
+ * echo_engine.h — C ABI of the device-resident hybrid decoder (libechohip.so).
+ *
+ * The model is the reference's hybrid Qwen3.5 stack
+ * (echo-core-zig/src/inference/engine.zig:360-463): n_layers blocks, block i
+ * is full attention iff (i+1) % attn_interval == 0
+ * (echo-core-zig/src/ports/inference.zig:135-140), otherwise a gated-delta-net
+ * ("qwen_linear") block (echo-core-zig/src/kernels/qwen_linear.zig:103-271);
+ * each block is followed by a SwiGLU FFN; RMSNorm before every sub-block,
+ * greedy argmax at the end.  All matrices are GGUF Q8_0.
+ *
+ * The engine decodes a batch of up to max_batch sequences per step, each at
+ * its own position (ragged).  Inputs of a step are, per sequence, a token and
+ * a position (position < 0: sequence inactive this step; its state, KV cache
+ * and position are untouched).  After a step the greedy next token of every
+ * active sequence is in the engine's `gen` array and its position has
+ * advanced by one; the next step consumes `gen` as input unless new inputs
+ * are set.  A step runs as one captured HIP graph on the engine's stream.
+ *
+ * Differences from the reference, all deliberate:
+ *  - activations entering a matvec are quantized per 32-element block with the
+ *    reference quantizer (src/kernels/quant.cpp:18-98) and multiplied with
+ *    int8 MFMA (exact int32 block dots, fp32 scale epilogue);
+ *  - the INT8 KV cache has one scale per (token, kv head) row, the layout its
+ *    readers index (src/inference.cpp:347,387) (the reference writers store
+ *    one scale per token);
+ *  - an attention block attends over its own layer's cache length (the
+ *    reference reads layer 0's, echo-core-zig/src/kv_cache/cache.zig:131-134,
+ *    which a hybrid stack whose layer 0 is a delta-net block never appends to).
+ */
+#ifndef ECHO_ENGINE_H
+#define ECHO_ENGINE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ec_engine ec_engine;
+
+typedef struct {
+    uint32_t vocab, hidden, ffn, n_layers;
+    uint32_t n_heads, n_kv, head_dim;  /* attention blocks (head_dim 256) */
+    uint32_t ssm_inner, ssm_heads;     /* delta-net value_dim and value heads (head dims 128) */
+    uint32_t conv_kernel;              /* causal depthwise conv taps */
+    uint32_t attn_interval;
+    uint32_t max_batch, max_ctx;
+    float rope_base;
+} ec_engine_cfg;
+
+/* Tensor ids for ec_engine_set_tensor.  Matrices are GGUF Q8_0 bytes, rows x
+ * (K/32*34); vectors are fp32.  Per-layer tensors: */
+enum ec_tensor {
+    EC_T_EMBED = 0,      /* [vocab x hidden] Q8_0 (global) */
+    EC_T_FINAL_NORM = 1, /* [hidden] (global) */
+    EC_T_LM_HEAD = 2,    /* [vocab x hidden] Q8_0 (global) */
+    EC_T_ATTN_NORM = 10, /* [hidden] */
+    EC_T_FFN_NORM = 11,  /* [hidden] */
+    EC_T_W_IN = 12,      /* delta: rows qkv(conv_dim) | z(ssm_inner) | alpha(ssm_heads) | beta(ssm_heads);
+                            attention: rows q(n_heads*hd) | k(n_kv*hd) | v(n_kv*hd); K = hidden */
+    EC_T_W_OUT = 13,     /* delta: [hidden x ssm_inner]; attention: [hidden x n_heads*hd] */
+    EC_T_W_GATE = 14,    /* [ffn x hidden] */
+    EC_T_W_UP = 15,      /* [ffn x hidden] */
+    EC_T_W_DOWN = 16,    /* [hidden x ffn] */
+    EC_T_CONV_W = 17,    /* delta: [conv_kernel][conv_dim], tap-major (qwen_linear.zig:197) */
+    EC_T_A_LOG = 18,     /* delta: [ssm_heads] */
+    EC_T_DT_BIAS = 19,   /* delta: [ssm_heads] */
+    EC_T_SSM_NORM = 20,  /* delta: [128] */
+    EC_T_Q_NORM = 21,    /* attention: [head_dim]; all zero = not applied (engine.zig:548-553) */
+    EC_T_K_NORM = 22,    /* attention: [head_dim] */
+};
+
+int ec_engine_create(const ec_engine_cfg* cfg, ec_engine** out);
+void ec_engine_destroy(ec_engine* e);
+/* Copy one tensor from host memory (layer ignored for global tensors). */
+int ec_engine_set_tensor(ec_engine* e, int layer, int tensor, const void* host, size_t bytes);
+/* Copy one tensor back to host memory in the set_tensor format (matrices as
+ * GGUF Q8_0 bytes; EC_T_W_GATE / EC_T_W_UP each return their half). */
+int ec_engine_get_tensor(ec_engine* e, int layer, int tensor, void* host, size_t bytes);
+/* Fill every tensor with seeded synthetic values generated on the device:
+ * matrices Q8_0 with qs ~ U{-127..127} and d = fp16(|N(0,1)| * w_scale);
+ * norms 1 + 0.1*N(0,1); conv taps 0.5*N(0,1); A_log = ln U[1,16]; dt_bias 0.1*N(0,1). */
+int ec_engine_init_random(ec_engine* e, uint64_t seed, float w_scale);
+/* Zero recurrent state, conv state and KV caches; all positions inactive. */
+int ec_engine_reset(ec_engine* e);
+/* Set this step's inputs for n <= max_batch sequences (host arrays). */
+int ec_engine_set_inputs(ec_engine* e, const int32_t* tok, const int32_t* pos, uint32_t n);
+/* Run one decode step (graph-captured after the first call when use_graph). */
+int ec_engine_step(ec_engine* e, int use_graph);
+int ec_engine_sync(ec_engine* e);
+/* Device -> host copies (synchronous). */
+int ec_engine_get_tokens(ec_engine* e, int32_t* gen, int32_t* pos);
+int ec_engine_get_logits(ec_engine* e, float* host, uint32_t seq);
+void* ec_engine_stream(ec_engine* e);
+/* HBM bytes of weights one decode step reads (tiled Q8_0 matrices + vectors). */
+size_t ec_engine_weight_bytes(const ec_engine* e);
+/* Per-step launch list with its matvecs timed by HIP events: fills up to
+ * `cap` entries of (kind, bytes, microseconds); kind 0 = Q8_0 matvec.
+ * Runs one eager step (state advances as a normal step). */
+int ec_engine_profile_step(ec_engine* e, uint32_t cap, int32_t* kind, double* bytes, double* us, uint32_t* n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

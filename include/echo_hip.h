@@ -55,6 +55,8 @@ int ec_quantize_rows(const float* x, int8_t* q, float* scales, uint32_t rows, ui
  * gguf: N rows of K/32*34 (Q8_0) or K/256*144 (Q4_K) bytes. */
 size_t ec_tiled_bytes(int fmt, uint32_t N, uint32_t K);
 int ec_repack(int fmt, const void* gguf, void* tiled, uint32_t N, uint32_t K, void* stream);
+/* Inverse of ec_repack (Q8_0): tiled -> GGUF rows. */
+int ec_unpack_tiled(int fmt, const void* tiled, void* gguf, uint32_t N, uint32_t K, void* stream);
 
 /* --------------------------------------------------- activation quantization
  * M (1..16) fp32 activation rows x[M][K] are quantized per 32-element block
@@ -120,7 +122,29 @@ int ec_attn_decode(const float* q, const int8_t* keys, const int8_t* vals, const
  * multiple of 16.  The state stays on chip across the T tokens. */
 int ec_deltanet(float* state, const float* q, const float* k, const float* v, const float* decay, const float* beta,
                 float* out, uint32_t T, uint32_t n_seq, uint32_t n_v, uint32_t n_k, uint32_t d_k, uint32_t d_v,
-                void* stream);
+                const int32_t* seq_pos, void* stream);
+/* seq_pos (may be NULL): sequence s is skipped entirely (state untouched, no
+ * output written) when seq_pos[s] < 0. */
+
+/* ------------------------------------------------------------ decode-step glue
+ * Fused per-token ops of the hybrid decoder (semantics in glue.hip); every
+ * "_quant" op writes the Q8_0 activation layout consumed by ec_matvec. */
+int ec_glue_embed(const void* emb, const int32_t* tok, float* x, uint32_t n_seq, uint32_t H, uint32_t vocab,
+                  void* stream);
+int ec_glue_rmsnorm_quant(const float* x, const float* w, void* act, uint32_t M, uint32_t H, void* stream);
+int ec_glue_swiglu_quant(const float* gu, void* act, uint32_t M, uint32_t F, void* stream);
+int ec_glue_conv_gates(const float* proj, uint32_t Nin, float* conv_state, const float* conv_w, const float* a_log,
+                       const float* dt_bias, float* q, float* k, float* v, float* dec, float* beta,
+                       const int32_t* pos, uint32_t n_seq, uint32_t n_k, uint32_t n_v, uint32_t kern, void* stream);
+int ec_glue_gated_norm_quant(const float* core, const float* proj, uint32_t Nin, uint32_t z_off, const float* norm_w,
+                             void* act, uint32_t M, uint32_t n_v, void* stream);
+int ec_glue_qk_rope_append(const float* proj, uint32_t Nin, const float* q_norm, const float* k_norm, int use_qn,
+                           int use_kn, const float* inv_freq, const int32_t* pos, float* q_out, int8_t* keys,
+                           int8_t* vals, float* kscales, float* vscales, int32_t* ctx, uint32_t n_seq,
+                           uint64_t seq_stride, uint32_t max_ctx, uint32_t n_heads, uint32_t n_kv, uint32_t head_dim,
+                           void* stream);
+int ec_glue_argmax_advance(const float* logits, uint32_t vocab, int32_t* gen, int32_t* next, int32_t* pos,
+                           uint32_t n_seq, void* stream);
 
 /* Plain streaming read of `bytes` (multiple of 16) with `blocks` workgroups of
  * 256 threads: the HBM-bandwidth calibration used by the benchmarks. */

@@ -201,3 +201,104 @@ class Baseline:
 
     def threads(self, n: int):
         self.lib.ob_set_threads(int(n))
+
+
+# ---------------------------------------------------------------- decoder
+class _OcCfg(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("hidden", "ffn", "n_layers", "vocab", "n_heads", "n_kv", "head_dim",
+                                          "ssm_inner", "ssm_heads", "conv_kernel", "attn_interval", "max_ctx")] + \
+               [("rope_base", C.c_float)]
+
+
+_PP = C.POINTER(C.c_void_p)
+
+
+class _OcW(C.Structure):
+    _fields_ = [(n, _PP) for n in ("w_qkv", "w_z", "w_ab", "w_out", "w_gate", "w_up", "w_down", "attn_norm",
+                                   "ffn_norm", "conv_w", "a_log", "dt_bias", "ssm_norm", "q_norm", "k_norm")] + \
+               [("embed", C.c_void_p), ("final_norm", C.c_void_p), ("lm_head", C.c_void_p)]
+
+
+class _OcSeq(C.Structure):
+    _fields_ = [(n, _PP) for n in ("conv_state", "ssm_state", "keys", "vals", "kscales", "vscales")] + \
+               [("pos", C.c_uint32)]
+
+
+class Decoder:
+    """n_seq independent sequences decoded token by token by oc_decoder_token
+    (oracle.c).  `cfg` is an echohip.engine.EngineConfig-like object and `m`
+    the weight dict of tests/decoder_util.make_model (GGUF Q8_0 matrices,
+    fp32 vectors, the fused w_in rows of the engine)."""
+
+    def __init__(self, oc, cfg: EngineConfig, m, n_seq, quant_act=True):
+        self.oc, self.cfg, self.quant_act = oc, cfg, int(quant_act)
+        L = cfg.n_layers
+        self.keep = []
+        c = self.c = _OcCfg(hidden=cfg.hidden, ffn=cfg.ffn, n_layers=L, vocab=cfg.vocab, n_heads=cfg.n_heads,
+                            n_kv=cfg.n_kv, head_dim=cfg.head_dim, ssm_inner=cfg.ssm_inner, ssm_heads=cfg.ssm_heads,
+                            conv_kernel=cfg.conv_kernel, attn_interval=cfg.attn_interval, max_ctx=cfg.max_ctx,
+                            rope_base=cfg.rope_base)
+
+        def arr(ptrs):
+            a = (C.c_void_p * L)(*ptrs)
+            self.keep.append(a)
+            return C.cast(a, _PP)
+
+        def p(x):
+            if x is None:
+                return None
+            x = np.ascontiguousarray(x)
+            self.keep.append(x)
+            return x.ctypes.data
+
+        H = cfg.hidden
+        rowb = H // 32 * 34
+        lay = m["layers"]
+        w = {k: [] for k, _ in _OcW._fields_[:15]}
+        for y in lay:
+            w["w_qkv"].append(p(y["w_in"]))
+            base = y["w_in"].reshape(-1)
+            if y["attn"]:
+                w["w_z"].append(None)
+                w["w_ab"].append(None)
+            else:
+                w["w_z"].append(p(base[cfg.conv_dim * rowb:]))
+                w["w_ab"].append(p(base[(cfg.conv_dim + cfg.ssm_inner) * rowb:]))
+            for k in ("w_out", "w_gate", "w_up", "w_down", "attn_norm", "ffn_norm", "conv_w", "a_log", "dt_bias",
+                      "ssm_norm", "q_norm", "k_norm"):
+                w[k].append(p(y.get(k)))
+        self.w = _OcW(**{k: arr(v) for k, v in w.items()}, embed=p(m["embed"]), final_norm=p(m["final_norm"]),
+                      lm_head=p(m["lm_head"]))
+        self.seqs = []
+        kvd = cfg.n_kv * cfg.head_dim
+        for _ in range(n_seq):
+            st = {"conv": [], "ssm": [], "k": [], "v": [], "ks": [], "vs": []}
+            for l in range(L):
+                if cfg.is_attn(l):
+                    st["conv"].append(None)
+                    st["ssm"].append(None)
+                    st["k"].append(np.zeros(cfg.max_ctx * kvd, np.int8))
+                    st["v"].append(np.zeros(cfg.max_ctx * kvd, np.int8))
+                    st["ks"].append(np.zeros(cfg.max_ctx * cfg.n_kv, np.float32))
+                    st["vs"].append(np.zeros(cfg.max_ctx * cfg.n_kv, np.float32))
+                else:
+                    st["conv"].append(np.zeros(cfg.conv_kernel * cfg.conv_dim, np.float32))
+                    st["ssm"].append(np.zeros(cfg.ssm_heads * 128 * 128, np.float32))
+                    for k in ("k", "v", "ks", "vs"):
+                        st[k].append(None)
+            self.keep.append(st)
+            s = _OcSeq(conv_state=arr([p(x) for x in st["conv"]]), ssm_state=arr([p(x) for x in st["ssm"]]),
+                       keys=arr([p(x) for x in st["k"]]), vals=arr([p(x) for x in st["v"]]),
+                       kscales=arr([p(x) for x in st["ks"]]), vscales=arr([p(x) for x in st["vs"]]), pos=0)
+            self.seqs.append(s)
+        oc.lib.oc_decoder_token.argtypes = [C.POINTER(_OcCfg), C.POINTER(_OcW), C.POINTER(_OcSeq), C.c_uint32,
+                                            C.c_void_p, C.c_int]
+
+    def token(self, seq: int, tok: int):
+        logits = np.zeros(self.cfg.vocab, np.float32)
+        self.oc.lib.oc_decoder_token(C.byref(self.c), C.byref(self.w), C.byref(self.seqs[seq]), tok,
+                                     logits.ctypes.data, self.quant_act)
+        return logits
+
+    def pos(self, seq: int) -> int:
+        return self.seqs[seq].pos
