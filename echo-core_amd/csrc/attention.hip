@@ -13,8 +13,15 @@
 // max / sum / output per head (online softmax) and writes one partial per
 // chunk; a second kernel merges the partials.
 #include "common.hpp"
+#include "layout.hpp"
 
 namespace ec {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) {
+    return (long)(((uint64_t)hi << 32) | (uint64_t)lo);
+}
 
 constexpr uint32_t kAttnChunk = 256;  // context positions per workgroup
 
@@ -178,6 +185,260 @@ __global__ __launch_bounds__(64) void k_attn_combine(const float* __restrict__ w
     for (int d = 0; d < DPL; ++d) dst[d] = acc[d] * inv;
 }
 
+// ===================================================================== MFMA path
+// head_dim 256.  QK^T runs on v_mfma_i32_16x16x32_i8.  q of each head is split
+// into three int8 vectors, q ~ s0*Q0 + s1*Q1 + s2*Q2 with s0 = max|q|/127,
+// s1 = s0/254, s2 = s1/254 (each piece quantizes the previous residual, so
+// |q - approx| <= max|q|/16387064, below fp32 rounding of the dot products);
+// the pieces occupy A rows g, G+g and 2G+g.  K stays int8 (B operand), every
+// dot product is an exact int32 and
+//   score = ks * (s0*dot0 + s1*dot1 + s2*dot2) / sqrt(256).
+// One wave owns a 64-position chunk of one kv head for all G query heads of
+// its GQA group, keeps the chunk's max / sum / output per head and writes one
+// partial; softmax(.)V runs on the VALU from probabilities (times the V row
+// scale) broadcast through LDS, with the chunk's V rows staged in LDS.
+//
+// Packed q layout: layout.hpp (store_q_pieces).
+constexpr uint32_t kChunk64 = 64;
+constexpr uint32_t kRec64 = 260;  // partial record [m, l, -, -, o[256]] (16-byte aligned output)
+
+// grid (n_heads, n_seq), block 256 (thread = dim): pack q [n_seq][n_heads][256].
+__global__ __launch_bounds__(256) void k_pack_q(const float* __restrict__ q, uint8_t* __restrict__ qa,
+                                                float* __restrict__ qsc, uint32_t n_heads, uint32_t n_kv) {
+    __shared__ float mx[4];
+    const uint32_t head = blockIdx.x, s = blockIdx.y, d = threadIdx.x;
+    const float val = q[((size_t)s * n_heads + head) * 256 + d];
+    const float a = wave_max(fabsf(val));
+    if ((d & 63) == 0) mx[d >> 6] = a;
+    __syncthreads();
+    const float amax = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+    store_q_pieces(val, amax, d, s, head, n_heads, n_kv, qa, qsc);
+}
+
+template <int G>
+__global__ __launch_bounds__(64) void k_attn_mfma(const uint8_t* __restrict__ qa, const float* __restrict__ qsc,
+                                                  const int8_t* __restrict__ keys, const int8_t* __restrict__ vals,
+                                                  const float* __restrict__ kscales, const float* __restrict__ vscales,
+                                                  const int32_t* __restrict__ ctx, uint64_t seq_stride, uint32_t n_kv,
+                                                  uint32_t n_chunks_max, uint32_t max_ctx, float* __restrict__ ws) {
+    static_assert(G == 1 || G == 2 || G == 4, "3G A rows must fit the 16 MFMA rows");
+    constexpr uint32_t HD = 256;
+    __shared__ float part_s[kQPieces * G][64];  // per-piece scores (times the K row scale)
+    __shared__ float p_s[64][4];
+    __shared__ u32x4 v_s[64 * 16];  // the chunk's V rows, [position][256 bytes]
+    const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z, lane = threadIdx.x;
+    const int32_t L = min(ctx[s], (int32_t)max_ctx);
+    const uint32_t c0 = chunk * kChunk64;
+    if (L <= 0 || c0 >= (uint32_t)L) return;
+    const uint32_t ntok = min((uint32_t)L - c0, kChunk64);
+    const uint32_t n_heads = n_kv * G;
+    const size_t row = (size_t)n_kv * HD;
+    const int8_t* kb = keys + s * seq_stride + (size_t)kvh * HD;
+    const int8_t* vb = vals + s * seq_stride + (size_t)kvh * HD;
+    const float* ksb = kscales + s * (seq_stride / HD) + kvh;
+    const float* vsb = vscales + s * (seq_stride / HD) + kvh;
+    const uint32_t r16 = lane & 15, gq = lane >> 4;
+
+    // ---- loads, in the order they are consumed (waitcnt retires them in order):
+    // A operand (packed q) and scales, K for 4 x 16 positions, then V.
+    constexpr uint32_t NR = kQPieces * G;  // A rows in use
+    const bool arow = r16 < NR;
+    const uint8_t* qp = qa + ((((size_t)s * n_kv + kvh) * NR + (arow ? r16 : 0)) * 4 + gq) * 64;
+    u32x4 aq[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) aq[i] = *(const u32x4*)(qp + 16 * i);
+    const float* scq = qsc + ((size_t)s * n_kv + kvh) * NR;
+    float rs[4];  // scale of the A row of each C element this lane holds
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint32_t r = 4 * gq + c;
+        rs[c] = scq[r < NR ? r : 0];
+    }
+    float ksv[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        const uint32_t t = 16 * st + r16;
+        ksv[st] = ksb[(size_t)(c0 + (t < ntok ? t : 0)) * n_kv];
+    }
+    const float vsv = vsb[(size_t)(c0 + (lane < ntok ? lane : 0)) * n_kv];
+    u32x4 kw[4][4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        const uint32_t t = 16 * st + r16;
+        const int8_t* kr = kb + (size_t)(c0 + (t < ntok ? t : 0)) * row + 16 * gq;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kw[st][i] = *(const u32x4*)(kr + 64 * i);
+    }
+    // V: instruction j brings positions 4j .. 4j+3 (256 bytes each, lane = 16 bytes)
+    u32x4 vv[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const uint32_t t = 4 * j + (lane >> 4);
+        vv[j] = *(const u32x4*)(vb + (size_t)(c0 + (t < ntok ? t : 0)) * row + 16 * (lane & 15));
+    }
+
+    // ---- scores: 8 accumulating MFMAs per 16 positions; C row r = 4*gq + c
+    long A[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        A[2 * i] = arow ? pack2(aq[i].x, aq[i].y) : 0l;
+        A[2 * i + 1] = arow ? pack2(aq[i].z, aq[i].w) : 0l;
+    }
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        v4i C = {0, 0, 0, 0};
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const u32x4 w = kw[st][m / 2];
+            const long B = (m & 1) ? pack2(w.z, w.w) : pack2(w.x, w.y);
+            C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[m], B, C, 0, 0, 0);
+        }
+        const uint32_t t = 16 * st + r16;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (4 * gq + c < NR) part_s[4 * gq + c][t] = (float)C[c] * rs[c] * ksv[st];
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v_s[64 * j + lane] = vv[j];
+    __syncthreads();
+
+    // ---- softmax over the chunk (lane = position)
+    constexpr float scale = 1.0f / 16.0f;  // 1/sqrt(256)
+    float m[G], l[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float raw = (part_s[g][lane] + part_s[G + g][lane]) + part_s[2 * G + g][lane];
+        const float sc = lane < ntok ? raw * scale : -INFINITY;
+        m[g] = wave_max(sc);
+        const float e = lane < ntok ? __expf(sc - m[g]) : 0.0f;
+        l[g] = wave_sum(e);
+        p_s[lane][g] = e * vsv;
+    }
+    __syncthreads();
+
+    // ---- softmax . V (lane = 4 dims)
+    float o[G][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+        for (int e = 0; e < 4; ++e) o[g][e] = 0.0f;
+    // positions past the chunk end carry p = 0 (their clamped V rows add nothing)
+    const uint32_t* vrow = (const uint32_t*)v_s;
+#pragma unroll 8
+    for (uint32_t t = 0; t < 64; ++t) {
+        const uint32_t w = vrow[64 * t + lane];
+        const float v0 = (float)(int8_t)(w & 0xFF), v1 = (float)(int8_t)((w >> 8) & 0xFF);
+        const float v2 = (float)(int8_t)((w >> 16) & 0xFF), v3 = (float)(int8_t)(w >> 24);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float pg = p_s[t][g];
+            o[g][0] = fmaf(pg, v0, o[g][0]);
+            o[g][1] = fmaf(pg, v1, o[g][1]);
+            o[g][2] = fmaf(pg, v2, o[g][2]);
+            o[g][3] = fmaf(pg, v3, o[g][3]);
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float* rec = ws + (((size_t)s * n_chunks_max + chunk) * n_heads + kvh + n_kv * g) * kRec64;
+        if (lane == 0) *(float4*)rec = make_float4(m[g], l[g], 0.0f, 0.0f);
+        *(float4*)(rec + 4 + 4 * lane) = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
+    }
+}
+
+// grid (n_heads, n_seq), block 512 (8 waves): merge chunk partials.  The chunk
+// weights exp(m_c - M) go through LDS; wave w then sums chunks w, w+8, ...
+// with lane = 4 dims (1 KB per wave load), and the eight wave sums are added
+// in LDS.
+constexpr uint32_t kMergeWaves = 8;
+
+// Lanes 32k .. 32k+31 of a wave hold the 32 values of one Q8_0 block (k % 32 ==
+// lane % 32): quantize it with the reference quantizer's body rule and store
+// it in the Q8_0 activation layout (row i of M, K % 128 == 0).
+__device__ __forceinline__ void store_act_q8(float v, uint8_t* __restrict__ act, uint32_t M, uint32_t K, uint32_t i,
+                                             uint32_t k) {
+    float amax = fabsf(v);
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    const float scale = q_scale(amax);
+    const float inv = __fdiv_rn(1.0f, scale);
+    const uint32_t sb = k / 32, e = k % 32, G = sb / 4, j = sb % 4, g = e / 8;
+    act[(((size_t)G * 4 + g) * M + i) * 32 + 8 * j + (e % 8)] = (uint8_t)q_body(v, inv);
+    if (e == 0) {
+        const ActLayout L = act_layout(EC_Q8_0, M, K);
+        ((float*)(act + L.xd_off))[(size_t)i * (L.Kp / 32) + sb] = scale;
+    }
+}
+// With act != nullptr the merged rows are also quantized into the Q8_0
+// activation layout (M = n_seq rows, K = n_heads*256; quantize_act's format).
+__global__ __launch_bounds__(512) void k_attn_merge(const float* __restrict__ ws, const int32_t* __restrict__ ctx,
+                                                    float* __restrict__ out, uint8_t* __restrict__ act,
+                                                    uint32_t n_seq, uint32_t n_heads, uint32_t n_chunks_max,
+                                                    uint32_t max_ctx, uint32_t chunk) {
+    extern __shared__ float w_s[];
+    __shared__ float red[kMergeWaves];
+    __shared__ float4 acc_s[kMergeWaves][64];
+    const uint32_t HD = 256;
+    const uint32_t h = blockIdx.x, s = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int32_t L = min(ctx[s], (int32_t)max_ctx);
+    float* dst = out + ((size_t)s * n_heads + h) * HD;
+    if (L <= 0) {
+        if (tid < HD) {
+            dst[tid] = 0.0f;
+            if (act) store_act_q8(0.0f, act, n_seq, n_heads * HD, s, h * HD + tid);
+        }
+        return;
+    }
+    const uint32_t nc = ((uint32_t)L + chunk - 1) / chunk;
+    const float* base = ws + ((size_t)s * n_chunks_max * n_heads + h) * kRec64;
+    const size_t cs = (size_t)n_heads * kRec64;
+    float M = -INFINITY;
+    for (uint32_t c = tid; c < nc; c += 512) M = fmaxf(M, base[c * cs]);
+    M = wave_max(M);
+    if (lane == 0) red[wv] = M;
+    __syncthreads();
+    M = red[0];
+#pragma unroll
+    for (int i = 1; i < (int)kMergeWaves; ++i) M = fmaxf(M, red[i]);
+    __syncthreads();
+    float den = 0.0f;
+    for (uint32_t c = tid; c < nc; c += 512) {
+        const float w = __expf(base[c * cs] - M);
+        w_s[c] = w;
+        den = fmaf(w, base[c * cs + 1], den);
+    }
+    den = wave_sum(den);
+    if (lane == 0) red[wv] = den;
+    __syncthreads();
+    float4 a0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), a1 = a0;
+    uint32_t c = wv;
+    for (; c + kMergeWaves < nc; c += 2 * kMergeWaves) {
+        const float4 o0 = *(const float4*)(base + c * cs + 4 + 4 * lane);
+        const float4 o1 = *(const float4*)(base + (c + kMergeWaves) * cs + 4 + 4 * lane);
+        const float w0 = w_s[c], w1 = w_s[c + kMergeWaves];
+        a0.x = fmaf(w0, o0.x, a0.x), a0.y = fmaf(w0, o0.y, a0.y), a0.z = fmaf(w0, o0.z, a0.z), a0.w = fmaf(w0, o0.w, a0.w);
+        a1.x = fmaf(w1, o1.x, a1.x), a1.y = fmaf(w1, o1.y, a1.y), a1.z = fmaf(w1, o1.z, a1.z), a1.w = fmaf(w1, o1.w, a1.w);
+    }
+    if (c < nc) {
+        const float4 o0 = *(const float4*)(base + c * cs + 4 + 4 * lane);
+        const float w0 = w_s[c];
+        a0.x = fmaf(w0, o0.x, a0.x), a0.y = fmaf(w0, o0.y, a0.y), a0.z = fmaf(w0, o0.z, a0.z), a0.w = fmaf(w0, o0.w, a0.w);
+    }
+    acc_s[wv][lane] = make_float4(a0.x + a1.x, a0.y + a1.y, a0.z + a1.z, a0.w + a1.w);
+    __syncthreads();
+    if (tid < HD) {
+        float dn = red[0], o = 0.0f;
+#pragma unroll
+        for (int i = 1; i < (int)kMergeWaves; ++i) dn += red[i];
+        const float* col = (const float*)acc_s + tid;  // dim tid of every wave's sum
+#pragma unroll
+        for (int i = 0; i < (int)kMergeWaves; ++i) o += col[i * 256];
+        o = o / dn;
+        dst[tid] = o;
+        if (act) store_act_q8(o, act, n_seq, n_heads * HD, s, h * HD + tid);
+    }
+}
+
+// ----------------------------------------------------------- VALU fallback
 template <int HD, int G>
 static void launch_attn(const float* q, const int8_t* keys, const int8_t* vals, const float* ks, const float* vs,
                         float* out, const int32_t* ctx, uint32_t n_seq, uint64_t seq_stride, uint32_t n_kv,
@@ -186,6 +447,33 @@ static void launch_attn(const float* q, const int8_t* keys, const int8_t* vals, 
                        seq_stride, n_kv, ncm, max_ctx, ws);
     hipLaunchKernelGGL((k_attn_combine<HD>), dim3(n_kv * G, n_seq), dim3(64), 0, st, ws, ctx, out, n_kv * G, ncm,
                        max_ctx);
+}
+
+
+template <int G>
+static void launch_mfma(const uint8_t* qa, const float* qsc, const int8_t* keys, const int8_t* vals, const float* ks,
+                        const float* vs, float* out, uint8_t* act, const int32_t* ctx, uint32_t n_seq,
+                        uint64_t seq_stride, uint32_t n_kv, uint32_t max_ctx, float* ws, hipStream_t st) {
+    const uint32_t ncm = (max_ctx + kChunk64 - 1) / kChunk64;
+    hipLaunchKernelGGL((k_attn_mfma<G>), dim3(ncm, n_kv, n_seq), dim3(64), 0, st, qa, qsc, keys, vals, ks, vs, ctx,
+                       seq_stride, n_kv, ncm, max_ctx, ws);
+    hipLaunchKernelGGL(k_attn_merge, dim3(n_kv * G, n_seq), dim3(512), ncm * sizeof(float), st, ws, ctx, out, act,
+                       n_seq, n_kv * G, ncm, max_ctx, kChunk64);
+}
+
+static int mfma_dispatch(uint32_t G, const uint8_t* qa, const float* qsc, const int8_t* keys, const int8_t* vals,
+                         const float* ks, const float* vs, float* out, uint8_t* act, const int32_t* ctx,
+                         uint32_t n_seq, uint64_t seq_stride, uint32_t n_kv, uint32_t max_ctx, float* ws,
+                         hipStream_t st) {
+#define EC_MF(G_) launch_mfma<G_>(qa, qsc, keys, vals, ks, vs, out, act, ctx, n_seq, seq_stride, n_kv, max_ctx, ws, st)
+    switch (G) {
+        case 1: EC_MF(1); break;
+        case 2: EC_MF(2); break;
+        case 4: EC_MF(4); break;
+        default: return ec_set_error(EC_ERR_UNSUPPORTED, "packed attention: n_heads/n_kv must be 1, 2 or 4");
+    }
+#undef EC_MF
+    return EC_OK;
 }
 
 }  // namespace ec
@@ -206,8 +494,10 @@ extern "C" int ec_kv_append(const float* k, const float* v, int8_t* keys, int8_t
 }
 
 extern "C" size_t ec_attn_ws_bytes(uint32_t n_seq, uint32_t n_heads, uint32_t head_dim, uint32_t max_ctx) {
-    const size_t ncm = (max_ctx + kAttnChunk - 1) / kAttnChunk;
-    return (size_t)n_seq * (ncm ? ncm : 1) * n_heads * (head_dim + 2) * sizeof(float);
+    // partial records for the smallest chunk (64 positions), then packed q and its scales
+    const size_t ncm = (max_ctx + kChunk64 - 1) / kChunk64;
+    const size_t part = (size_t)n_seq * (ncm ? ncm : 1) * n_heads * (head_dim + 4) * sizeof(float);
+    return ((part + 255) & ~(size_t)255) + qa_bytes(n_seq, n_heads) + (size_t)n_seq * n_heads * kQPieces * sizeof(float);
 }
 
 extern "C" int ec_attn_decode(const float* q, const int8_t* keys, const int8_t* vals, const float* kscales,
@@ -222,6 +512,17 @@ extern "C" int ec_attn_decode(const float* q, const int8_t* keys, const int8_t* 
     const uint32_t ncm = (max_ctx + kAttnChunk - 1) / kAttnChunk;
     hipStream_t st = (hipStream_t)stream;
     float* w = (float*)ws;
+    if (head_dim == 256 && (G == 1 || G == 2 || G == 4)) {
+        const size_t part = (size_t)n_seq * ((max_ctx + kChunk64 - 1) / kChunk64) * n_heads * kRec64 * 4;
+        uint8_t* qa = (uint8_t*)ws + ((part + 255) & ~(size_t)255);
+        float* qsc = (float*)(qa + qa_bytes(n_seq, n_heads));
+        hipLaunchKernelGGL(k_pack_q, dim3(n_heads, n_seq), dim3(256), 0, st, q, qa, qsc, n_heads, n_kv);
+        int rc = mfma_dispatch(G, qa, qsc, keys, vals, kscales, vscales, out, nullptr, ctx, n_seq, seq_stride, n_kv,
+                               max_ctx, w, st);
+        if (rc) return rc;
+        EC_CHECK_LAUNCH();
+        return EC_OK;
+    }
 #define EC_ATTN(HD_, G_) \
     launch_attn<HD_, G_>(q, keys, vals, kscales, vscales, out, ctx, n_seq, seq_stride, n_kv, ncm, max_ctx, w, st)
     if (head_dim == 256 && G == 4) EC_ATTN(256, 4);
@@ -242,3 +543,20 @@ extern "C" int ec_attn_decode(const float* q, const int8_t* keys, const int8_t* 
     EC_CHECK_LAUNCH();
     return EC_OK;
 }
+
+extern "C" int ec_attn_decode_packed(const void* qa, const float* qsc, const int8_t* keys, const int8_t* vals,
+                                     const float* kscales, const float* vscales, float* out, void* act_q8,
+                                     const int32_t* ctx, uint32_t n_seq, uint64_t seq_stride, uint32_t n_heads,
+                                     uint32_t n_kv, uint32_t max_ctx, void* ws, void* stream) {
+    if (n_seq == 0) return EC_OK;
+    if (!qa || !qsc || !keys || !vals || !kscales || !vscales || !out || !ctx || !ws || n_kv == 0 ||
+        n_heads % n_kv || max_ctx == 0 || seq_stride < (uint64_t)max_ctx * n_kv * 256 || (act_q8 && n_seq > 16))
+        return ec_set_error(EC_ERR_ARG, "ec_attn_decode_packed: bad argument");
+    int rc = mfma_dispatch(n_heads / n_kv, (const uint8_t*)qa, qsc, keys, vals, kscales, vscales, out,
+                           (uint8_t*)act_q8, ctx, n_seq, seq_stride, n_kv, max_ctx, (float*)ws, (hipStream_t)stream);
+    if (rc) return rc;
+    EC_CHECK_LAUNCH();
+    return EC_OK;
+}
+
+extern "C" size_t ec_attn_qa_bytes(uint32_t n_seq, uint32_t n_heads) { return qa_bytes(n_seq, n_heads); }

@@ -215,7 +215,8 @@ __global__ __launch_bounds__(256) void k_qk_rope_append(const float* __restrict_
                                                         const float* __restrict__ q_norm,
                                                         const float* __restrict__ k_norm, int use_qn, int use_kn,
                                                         const float* __restrict__ inv_freq, const int32_t* pos,
-                                                        float* __restrict__ q_out, int8_t* __restrict__ keys,
+                                                        float* __restrict__ q_out, uint8_t* __restrict__ qa,
+                                                        float* __restrict__ qsc, int8_t* __restrict__ keys,
                                                         int8_t* __restrict__ vals, float* __restrict__ kscales,
                                                         float* __restrict__ vscales, int32_t* __restrict__ ctx,
                                                         uint64_t seq_stride, uint32_t max_ctx, uint32_t n_heads,
@@ -244,7 +245,11 @@ __global__ __launch_bounds__(256) void k_qk_rope_append(const float* __restrict_
         val = (d & 1) ? other * sn + val * cs : val * cs - other * sn;
     }
     if (is_q) {
-        q_out[(size_t)s * n_heads * HD + head * HD + d] = val;
+        if (qa) {
+            store_q_pieces(val, block_max256(fabsf(val), sh), d, s, head, n_heads, n_kv, qa, qsc);
+        } else {
+            q_out[(size_t)s * n_heads * HD + head * HD + d] = val;
+        }
         return;
     }
     const uint32_t kvh = is_k ? head - n_heads : head - n_heads - n_kv;
@@ -358,16 +363,17 @@ extern "C" int ec_glue_gated_norm_quant(const float* core, const float* proj, ui
 
 extern "C" int ec_glue_qk_rope_append(const float* proj, uint32_t Nin, const float* q_norm, const float* k_norm,
                                       int use_qn, int use_kn, const float* inv_freq, const int32_t* pos, float* q_out,
-                                      int8_t* keys, int8_t* vals, float* kscales, float* vscales, int32_t* ctx,
-                                      uint32_t n_seq, uint64_t seq_stride, uint32_t max_ctx, uint32_t n_heads,
-                                      uint32_t n_kv, uint32_t head_dim, void* stream) {
+                                      void* q_packed, float* q_scales, int8_t* keys, int8_t* vals, float* kscales,
+                                      float* vscales, int32_t* ctx, uint32_t n_seq, uint64_t seq_stride,
+                                      uint32_t max_ctx, uint32_t n_heads, uint32_t n_kv, uint32_t head_dim,
+                                      void* stream) {
     if (head_dim != 256) return ec_set_error(EC_ERR_UNSUPPORTED, "ec_glue_qk_rope_append: head_dim must be 256");
-    if (!proj || !inv_freq || !pos || !q_out || !keys || !vals || !kscales || !vscales || !ctx ||
-        seq_stride < (uint64_t)max_ctx * n_kv * head_dim)
+    if (!proj || !inv_freq || !pos || (!q_out && !(q_packed && q_scales)) || !keys || !vals || !kscales ||
+        !vscales || !ctx || n_kv == 0 || n_heads % n_kv || seq_stride < (uint64_t)max_ctx * n_kv * head_dim)
         return ec_set_error(EC_ERR_ARG, "ec_glue_qk_rope_append: bad argument");
     EC_GLUE_LAUNCH(k_qk_rope_append, dim3(n_heads + 2 * n_kv, n_seq), dim3(256), 0, (hipStream_t)stream, proj, Nin,
-                   q_norm, k_norm, use_qn, use_kn, inv_freq, pos, q_out, keys, vals, kscales, vscales, ctx,
-                   seq_stride, max_ctx, n_heads, n_kv);
+                   q_norm, k_norm, use_qn, use_kn, inv_freq, pos, q_out, (uint8_t*)q_packed, q_scales, keys, vals,
+                   kscales, vscales, ctx, seq_stride, max_ctx, n_heads, n_kv);
 }
 
 extern "C" int ec_glue_argmax_advance(const float* logits, uint32_t vocab, int32_t* gen, int32_t* next, int32_t* pos,

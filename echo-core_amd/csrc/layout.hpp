@@ -29,4 +29,43 @@ __host__ __device__ inline ActLayout act_layout(int fmt, uint32_t M, uint32_t K)
     return a;
 }
 
+// ---- packed q for decode attention (head_dim 256, int8 MFMA A operand)
+// q of each head is split into kQPieces int8 vectors, q ~ sum_p s_p * Q_p with
+// s_0 = max|q|/127 and s_{p+1} = s_p/254.  Per (sequence, kv head) the A bytes
+// are [kQPieces*G rows][4 k-groups][64]: row p*G + g holds piece p of head
+// kvh + n_kv*g; within a (row, k-group g') record, byte 8m + e is dim
+// 16g' + 64(m/2) + 8(m%2) + e (m < 8, e < 8).  Scales [kQPieces*G] fp32 follow
+// the same row order.
+constexpr uint32_t kQPieces = 3;
+
+__host__ __device__ inline size_t qa_bytes(uint32_t n_seq, uint32_t n_heads) {
+    return (size_t)n_seq * n_heads * kQPieces * 4 * 64;
+}
+
+// k-group of dim d in bits 16.., byte position inside its 64-byte record in bits 0..15
+__host__ __device__ inline uint32_t qa_offset(uint32_t d) {
+    const uint32_t i = d / 64, gq = (d % 64) / 16, h = (d % 16) / 8, e = d % 8;
+    return (gq << 16) | ((2 * i + h) * 8 + e);
+}
+
+#ifdef __HIPCC__
+// Thread d of a 256-thread group stores dim d of (sequence s, head) given the head's max|q|.
+__device__ inline void store_q_pieces(float val, float amax, uint32_t d, uint32_t s, uint32_t head, uint32_t n_heads,
+                                      uint32_t n_kv, uint8_t* __restrict__ qa, float* __restrict__ qsc) {
+    const uint32_t G = n_heads / n_kv, kvh = head % n_kv, g = head / n_kv;
+    const uint32_t off = qa_offset(d), gq = off >> 16, at = off & 0xFFFF;
+    uint8_t* base = qa + ((size_t)s * n_kv + kvh) * (kQPieces * G) * 4 * 64;
+    float* sc = qsc + ((size_t)s * n_kv + kvh) * kQPieces * G;
+    float r = val, step = amax > 0.0f ? amax / 127.0f : 1.0f;
+#pragma unroll
+    for (uint32_t pc = 0; pc < kQPieces; ++pc) {
+        const float qi = fminf(fmaxf(rintf(r / step), -127.0f), 127.0f);
+        base[((size_t)(pc * G + g) * 4 + gq) * 64 + at] = (uint8_t)(int8_t)qi;
+        if (d == 0) sc[pc * G + g] = step;
+        r = fmaf(-qi, step, r);
+        step = step / 254.0f;
+    }
+}
+#endif
+
 }  // namespace ec

@@ -106,28 +106,34 @@ def stream_read_case(hip, nbytes, iters=100, blocks=4096):
             "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": n_copies}
 
 
-def attention_case(hip, ctx, n_heads=16, n_kv=4, hd=256, iters=100, seed=0):
-    st = torch.cuda.current_stream().cuda_stream
-    kv = ctx * n_kv * hd
-    per = 2 * kv + 2 * ctx * n_kv * 4
+def attention_case(hip, ctxs, n_heads=16, n_kv=4, hd=256, iters=100, seed=0):
+    """Decode attention over n_seq = len(ctxs) sequences, each with its own context length
+    (a ragged batch); the cache is sized to the longest one."""
+    ctxs = [int(c) for c in np.atleast_1d(ctxs)]
+    n_seq, max_ctx = len(ctxs), max(ctxs)
+    kv = max_ctx * n_kv * hd
+    per = n_seq * (2 * kv + 2 * max_ctx * n_kv * 4)
     n_copies = max(2, math.ceil(ROTATE_BYTES / per) + 1)
-    keys = torch.randint(-127, 128, (n_copies, kv), dtype=torch.int8, device="cuda")
-    vals = torch.randint(-127, 128, (n_copies, kv), dtype=torch.int8, device="cuda")
-    ks = torch.rand((n_copies, ctx * n_kv), device="cuda") * 0.02 + 0.01
-    vs = torch.rand((n_copies, ctx * n_kv), device="cuda") * 0.02 + 0.01
-    q = torch.from_numpy(synth.activations(seed, n_heads * hd)).cuda()
-    out = torch.empty(n_heads * hd, dtype=torch.float32, device="cuda")
-    cl = torch.tensor([ctx], dtype=torch.int32, device="cuda")
-    ws = torch.empty(hip.attn_ws_bytes(1, n_heads, hd, ctx), dtype=torch.uint8, device="cuda")
+    keys = torch.randint(-127, 128, (n_copies, n_seq * kv), dtype=torch.int8, device="cuda")
+    vals = torch.randint(-127, 128, (n_copies, n_seq * kv), dtype=torch.int8, device="cuda")
+    ks = torch.rand((n_copies, n_seq * max_ctx * n_kv), device="cuda") * 0.02 + 0.01
+    vs = torch.rand((n_copies, n_seq * max_ctx * n_kv), device="cuda") * 0.02 + 0.01
+    q = torch.from_numpy(synth.activations(seed, n_seq * n_heads * hd)).cuda()
+    out = torch.empty(n_seq * n_heads * hd, dtype=torch.float32, device="cuda")
+    cl = torch.tensor(ctxs, dtype=torch.int32, device="cuda")
+    ws = torch.empty(hip.attn_ws_bytes(n_seq, n_heads, hd, max_ctx), dtype=torch.uint8, device="cuda")
 
     def launch(i, stream):
-        hip.attn_decode(q, keys[i], vals[i], ks[i], vs[i], out, cl, 1, kv, n_heads, n_kv, hd, ctx, ws, stream=stream)
+        hip.attn_decode(q, keys[i], vals[i], ks[i], vs[i], out, cl, n_seq, kv, n_heads, n_kv, hd, max_ctx, ws,
+                        stream=stream)
 
     mean_us, med_us = _events_mean_us(launch, n_copies, iters)
-    alg = per + 2 * n_heads * hd * 4
+    # bytes the path must read: K and V rows plus their scales for every live position, q, out
+    alg = sum(ctxs) * n_kv * (2 * hd + 8) + 2 * n_seq * n_heads * hd * 4
     gbs = alg / (mean_us * 1e-6) / 1e9
-    return {"kernel": "k_attn_partial+combine", "ctx": ctx, "bytes": alg, "us": round(mean_us, 3),
-            "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": n_copies}
+    return {"kernel": "k_pack_q+k_attn_mfma+k_attn_merge", "ctxs": ctxs if n_seq <= 8 else f"{n_seq} seqs",
+            "bytes": alg, "us": round(mean_us, 3), "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "copies": n_copies}
 
 
 def deltanet_case(hip, T=1024, n_v=32, d=128, iters=5, seed=0):
@@ -167,7 +173,10 @@ def run_all(hip, quick=False):
     res["q8_0_9216x2560_m8"] = matvec_case(hip, L.Q8_0, 9216, 2560, M=8)
     res["q8_0_151936x2560_m8"] = matvec_case(hip, L.Q8_0, 151936, 2560, M=8, iters=20)
     for ctx in (512, 4096, 32768):
-        res[f"attn_ctx{ctx}"] = attention_case(hip, ctx)
+        res[f"attn_ctx{ctx}"] = attention_case(hip, [ctx])
+    # a decode batch like the hybrid decoder's: 8 ragged prompts of U[128, 4096] plus 128 generated tokens
+    ctxs = (synth.randint(synth.stream_seed(5, 0), 8, 128, 4096) + 128).tolist()
+    res["attn_batch8"] = attention_case(hip, ctxs)
     res["deltanet_1024"] = deltanet_case(hip)
     return res
 

@@ -36,6 +36,7 @@ _SIGS = {
     "ec_dequantize_to_fp16": [C.c_int, _vp, _vp, _sz, _vp],
     "ec_kv_append": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u64, _u32, _u32, _vp],
     "ec_attn_decode": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u64, _u32, _u32, _u32, _u32, _vp, _vp],
+    "ec_attn_decode_packed": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u64, _u32, _u32, _u32, _vp, _vp],
     "ec_deltanet": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp, _vp],
     "ec_fill_random": [C.c_int, _vp, _u64, _u64, C.c_float, _u32, _vp],
     "ec_stream_read": [_vp, _sz, _vp, _u32, _vp],
@@ -44,6 +45,7 @@ _SIZE_FNS = {
     "ec_tiled_bytes": [C.c_int, _u32, _u32],
     "ec_act_bytes": [C.c_int, _u32, _u32],
     "ec_attn_ws_bytes": [_u32, _u32, _u32, _u32],
+    "ec_attn_qa_bytes": [_u32, _u32],
 }
 
 
@@ -142,6 +144,15 @@ class Lib:
                     stream=None):
         self._call("ec_attn_decode", _ptr(q), _ptr(keys), _ptr(vals), _ptr(ks), _ptr(vs), _ptr(out), _ptr(ctx),
                    n_seq, seq_stride, n_heads, n_kv, head_dim, max_ctx, _ptr(ws), self._stream(stream))
+
+    def attn_decode_packed(self, q_packed, q_scales, keys, vals, ks, vs, out, act_q8, ctx, n_seq, seq_stride, n_heads,
+                           n_kv, max_ctx, ws, stream=None):
+        self._call("ec_attn_decode_packed", _ptr(q_packed), _ptr(q_scales), _ptr(keys), _ptr(vals), _ptr(ks),
+                   _ptr(vs), _ptr(out), _ptr(act_q8), _ptr(ctx), n_seq, seq_stride, n_heads, n_kv, max_ctx, _ptr(ws),
+                   self._stream(stream))
+
+    def attn_qa_bytes(self, n_seq, n_heads):
+        return self.L.ec_attn_qa_bytes(n_seq, n_heads)
 
     def deltanet(self, state, q, k, v, decay, beta, out, T, n_seq, n_v, n_k, d_k, d_v, seq_pos=None, stream=None):
         self._call("ec_deltanet", _ptr(state), _ptr(q), _ptr(k), _ptr(v), _ptr(decay), _ptr(beta), _ptr(out), T,

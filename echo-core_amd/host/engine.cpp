@@ -87,6 +87,9 @@ struct ec_engine {
     float *dec = nullptr, *beta = nullptr, *qbuf = nullptr, *attn_out = nullptr, *logits = nullptr;
     float* inv_freq = nullptr;
     void *act_h = nullptr, *act_v = nullptr, *act_f = nullptr, *act_q = nullptr, *attn_ws = nullptr;
+    void* q_packed = nullptr;
+    float* q_scales = nullptr;
+    bool packed_attn = false;  // int8-MFMA attention with q packed by the rope kernel
     int32_t *tok = nullptr, *pos = nullptr, *gen = nullptr, *ctx = nullptr;
     int32_t* h_io = nullptr;
     hipGraph_t graph = nullptr;
@@ -193,12 +196,24 @@ int record_step(ec_engine* e) {
         } else {
             const uint32_t Nin = e->nin_attn;
             EC_TRY(mv(e, y.w_in, e->act_h, e->proj, Nin, 0));
-            EC_TRY(ec_glue_qk_rope_append(e->proj, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn, e->inv_freq, e->pos,
-                                          e->qbuf, y.keys, y.vals, y.ks, y.vs, e->ctx, B, e->seq_stride, c.max_ctx,
-                                          c.n_heads, c.n_kv, c.head_dim, st));
-            EC_TRY(ec_attn_decode(e->qbuf, y.keys, y.vals, y.ks, y.vs, e->attn_out, e->ctx, B, e->seq_stride,
-                                  c.n_heads, c.n_kv, c.head_dim, c.max_ctx, e->attn_ws, st));
-            EC_TRY(ec_quantize_act(EC_Q8_0, e->attn_out, e->act_q, B, e->q_dim, st));
+            if (e->packed_attn) {
+                // rope + KV append write q as int8 pieces; attention writes the
+                // Q8_0 activation of its output for the output projection
+                EC_TRY(ec_glue_qk_rope_append(e->proj, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn, e->inv_freq,
+                                              e->pos, nullptr, e->q_packed, e->q_scales, y.keys, y.vals, y.ks, y.vs,
+                                              e->ctx, B, e->seq_stride, c.max_ctx, c.n_heads, c.n_kv, c.head_dim,
+                                              st));
+                EC_TRY(ec_attn_decode_packed(e->q_packed, e->q_scales, y.keys, y.vals, y.ks, y.vs, e->attn_out,
+                                             e->act_q, e->ctx, B, e->seq_stride, c.n_heads, c.n_kv, c.max_ctx,
+                                             e->attn_ws, st));
+            } else {
+                EC_TRY(ec_glue_qk_rope_append(e->proj, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn, e->inv_freq,
+                                              e->pos, e->qbuf, nullptr, nullptr, y.keys, y.vals, y.ks, y.vs, e->ctx,
+                                              B, e->seq_stride, c.max_ctx, c.n_heads, c.n_kv, c.head_dim, st));
+                EC_TRY(ec_attn_decode(e->qbuf, y.keys, y.vals, y.ks, y.vs, e->attn_out, e->ctx, B, e->seq_stride,
+                                      c.n_heads, c.n_kv, c.head_dim, c.max_ctx, e->attn_ws, st));
+                EC_TRY(ec_quantize_act(EC_Q8_0, e->attn_out, e->act_q, B, e->q_dim, st));
+            }
             EC_TRY(mv(e, y.w_out, e->act_q, e->x, H, 1));
         }
         EC_TRY(ec_glue_rmsnorm_quant(e->x, y.ffn_norm, e->act_h, B, H, st));
@@ -306,6 +321,11 @@ extern "C" int ec_engine_create(const ec_engine_cfg* cfg, ec_engine** out) {
         (rc = dalloc(e, &e->attn_ws, ec_attn_ws_bytes(B, c.n_heads, c.head_dim, c.max_ctx))) ||
         (rc = dalloc(e, &e->tok, B)) || (rc = dalloc(e, &e->pos, B)) || (rc = dalloc(e, &e->gen, B)) ||
         (rc = dalloc(e, &e->ctx, B)))
+        return fail(rc);
+    const uint32_t G = c.n_heads / c.n_kv;
+    e->packed_attn = c.head_dim == 256 && (G == 1 || G == 2 || G == 4);
+    if (e->packed_attn && ((rc = dalloc(e, &e->q_packed, ec_attn_qa_bytes(B, c.n_heads))) ||
+                           (rc = dalloc(e, &e->q_scales, (size_t)B * c.n_heads * 3))))
         return fail(rc);
     if (hipHostMalloc((void**)&e->h_io, 4 * 16 * sizeof(int32_t)) != hipSuccess)
         return fail(ec_set_error(EC_ERR_HIP, "ec_engine_create: pinned buffer"));

@@ -105,11 +105,26 @@ int ec_kv_append(const float* k, const float* v, int8_t* keys, int8_t* vals, flo
 /* ------------------------------------------------------- INT8 attention decode
  * out[s][h][:] = softmax_p(q[s][h].K[p, h%n_kv] * ks / sqrt(head_dim)) . V[p, h%n_kv] * vs
  * over p < ctx[s] (ctx[s] <= 0: output zeros).  q, out: [n_seq][n_heads*head_dim].
- * Split-K over the context: ws must hold ec_attn_ws_bytes(...) bytes. */
+ * Split-K over the context: ws must hold ec_attn_ws_bytes(...) bytes.
+ * head_dim 256 with n_heads/n_kv in {1,2,4} runs QK^T on int8 MFMA with q
+ * split into three int8 pieces (|q - sum| <= max|q| * 6.1e-8); other shapes
+ * (head_dim 64/128, 8 heads per kv head) run an fp32 VALU kernel. */
 size_t ec_attn_ws_bytes(uint32_t n_seq, uint32_t n_heads, uint32_t head_dim, uint32_t max_ctx);
 int ec_attn_decode(const float* q, const int8_t* keys, const int8_t* vals, const float* kscales,
                    const float* vscales, float* out, const int32_t* ctx, uint32_t n_seq, uint64_t seq_stride,
                    uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t max_ctx, void* ws, void* stream);
+
+/* Same computation from q already packed into the three-piece int8 layout
+ * (ec_glue_qk_rope_append writes it; ec_attn_qa_bytes(n_seq, n_heads) bytes
+ * plus n_seq*n_heads*3 fp32 scales), head_dim 256, n_heads/n_kv in {1,2,4}.
+ * act_q8 != NULL additionally writes out[] quantized into the Q8_0 activation
+ * layout of ec_quantize_act (n_seq <= 16, K = n_heads*256), ready for the
+ * output projection. */
+size_t ec_attn_qa_bytes(uint32_t n_seq, uint32_t n_heads);
+int ec_attn_decode_packed(const void* q_packed, const float* q_scales, const int8_t* keys, const int8_t* vals,
+                          const float* kscales, const float* vscales, float* out, void* act_q8, const int32_t* ctx,
+                          uint32_t n_seq, uint64_t seq_stride, uint32_t n_heads, uint32_t n_kv, uint32_t max_ctx,
+                          void* ws, void* stream);
 
 /* --------------------------------------------------------------- delta-net
  * Gated delta rule for T tokens of n_seq sequences (qwen_linear.zig:207-250):
@@ -139,10 +154,10 @@ int ec_glue_conv_gates(const float* proj, uint32_t Nin, float* conv_state, const
 int ec_glue_gated_norm_quant(const float* core, const float* proj, uint32_t Nin, uint32_t z_off, const float* norm_w,
                              void* act, uint32_t M, uint32_t n_v, void* stream);
 int ec_glue_qk_rope_append(const float* proj, uint32_t Nin, const float* q_norm, const float* k_norm, int use_qn,
-                           int use_kn, const float* inv_freq, const int32_t* pos, float* q_out, int8_t* keys,
-                           int8_t* vals, float* kscales, float* vscales, int32_t* ctx, uint32_t n_seq,
-                           uint64_t seq_stride, uint32_t max_ctx, uint32_t n_heads, uint32_t n_kv, uint32_t head_dim,
-                           void* stream);
+                           int use_kn, const float* inv_freq, const int32_t* pos, float* q_out, void* q_packed,
+                           float* q_scales, int8_t* keys, int8_t* vals, float* kscales, float* vscales, int32_t* ctx,
+                           uint32_t n_seq, uint64_t seq_stride, uint32_t max_ctx, uint32_t n_heads, uint32_t n_kv,
+                           uint32_t head_dim, void* stream);
 int ec_glue_argmax_advance(const float* logits, uint32_t vocab, int32_t* gen, int32_t* next, int32_t* pos,
                            uint32_t n_seq, void* stream);
 

@@ -9,6 +9,7 @@ import pytest
 
 from conftest import rel_l2
 from echohip import synth
+from echohip.lib import Q8_0
 
 pytestmark = pytest.mark.gpu
 
@@ -240,11 +241,13 @@ def test_kv_append_bit_exact(hip, oc):
     assert np.array_equal(host(vs).reshape(n_seq, -1).view(np.uint32), vs_r.view(np.uint32))
 
 
-@pytest.mark.parametrize("ctxs,max_ctx", [([1], 1), ([7], 7), ([512], 512), ([4096], 4096),
-                                          ([300, 1, 0, 777], 800)])
-def test_attention_decode(hip, oc, ctxs, max_ctx):
+@pytest.mark.parametrize("ctxs,max_ctx,n_heads,n_kv,hd", [
+    ([1], 1, 16, 4, 256), ([7], 7, 16, 4, 256), ([512], 512, 16, 4, 256), ([4096], 4096, 16, 4, 256),
+    ([300, 1, 0, 777], 800, 16, 4, 256), ([65, 130], 200, 4, 4, 256), ([129, 64], 192, 8, 4, 256),
+    ([333], 400, 32, 4, 256), ([200, 0], 256, 8, 2, 128)])
+def test_attention_decode(hip, oc, ctxs, max_ctx, n_heads, n_kv, hd):
+    """16/4 heads and 4/4, 8/4 run the int8-MFMA kernel; 32/4 and head_dim 128 the VALU kernel."""
     import torch
-    n_heads, n_kv, hd = 16, 4, 256
     n_seq = len(ctxs)
     keys, vals, ks, vs, _, _ = _kv_case(oc, n_seq, ctxs, max_ctx, n_kv, hd, 50)
     q = synth.activations(77, n_seq * n_heads * hd).reshape(n_seq, n_heads * hd)
@@ -258,7 +261,61 @@ def test_attention_decode(hip, oc, ctxs, max_ctx):
             assert not out[s].any()
             continue
         ref = oc.attn_decode(q[s], keys[s], vals[s], ks[s], vs[s], n_heads, n_kv, hd, ctxs[s])
-        assert rel_l2(out[s], ref) < TOL
+        err = rel_l2(out[s], ref)
+        print(f"seq {s} ctx {ctxs[s]}: rel_l2 {err:.2e}")
+        assert err < TOL
+
+
+def _pack_q_pieces(q, n_heads, n_kv):
+    """q [n_seq][n_heads*256] -> the three-piece int8 A-operand layout of
+    ec_attn_decode_packed: per (seq, kv head) [3G rows][4 k-groups][64 bytes],
+    row p*G+g = piece p of head kvh + n_kv*g; byte 8m+e of k-group g' is dim
+    16g' + 64(m//2) + 8(m%2) + e.  Scales s0 = max|q|/127, s_{p+1} = s_p/254."""
+    n_seq, G = q.shape[0], n_heads // n_kv
+    qa = np.zeros((n_seq, n_kv, 3 * G, 4, 64), np.int8)
+    qs = np.zeros((n_seq, n_kv, 3 * G), np.float32)
+    d = np.arange(256)
+    gq, at = (d % 64) // 16, (2 * (d // 64) + (d % 16) // 8) * 8 + d % 8
+    for s in range(n_seq):
+        for head in range(n_heads):
+            kvh, g = head % n_kv, head // n_kv
+            r = q[s, head * 256:(head + 1) * 256].astype(np.float64)
+            step = np.abs(r).max() / 127.0 or 1.0
+            for pc in range(3):
+                qi = np.clip(np.rint(r / step), -127, 127)
+                qa[s, kvh, pc * G + g, gq, at] = qi
+                qs[s, kvh, pc * G + g] = step
+                r = r - qi * step
+                step /= 254.0
+    return qa.reshape(-1), qs.reshape(-1)
+
+
+@pytest.mark.parametrize("ctxs,n_heads,n_kv", [([300, 1, 0, 777], 16, 4), ([65, 200, 64], 8, 4)])
+def test_attention_decode_packed_fused_act(hip, oc, ctxs, n_heads, n_kv):
+    """Pre-packed q, and the merged output quantized straight into the Q8_0
+    activation layout: the activation must equal ec_quantize_act of the output."""
+    import torch
+    hd, max_ctx, n_seq = 256, 800, len(ctxs)
+    keys, vals, ks, vs, _, _ = _kv_case(oc, n_seq, ctxs, max_ctx, n_kv, hd, 51)
+    q = synth.activations(78, n_seq * n_heads * hd).reshape(n_seq, n_heads * hd)
+    qa, qs = _pack_q_pieces(q, n_heads, n_kv)
+    assert qa.size == hip.attn_qa_bytes(n_seq, n_heads)
+    out = empty(n_seq * n_heads * hd, torch.float32)
+    K = n_heads * hd
+    act = empty(hip.act_bytes(Q8_0, n_seq, K), torch.uint8)
+    ws = empty(hip.attn_ws_bytes(n_seq, n_heads, hd, max_ctx), torch.uint8)
+    hip.attn_decode_packed(dev(qa), dev(qs), dev(keys), dev(vals), dev(ks), dev(vs), out, act,
+                           dev(np.array(ctxs, np.int32)), n_seq, max_ctx * n_kv * hd, n_heads, n_kv, max_ctx, ws)
+    act2 = empty(hip.act_bytes(Q8_0, n_seq, K), torch.uint8)
+    hip.quantize_act(Q8_0, out, act2, n_seq, K)
+    assert np.array_equal(host(act), host(act2))
+    out = host(out).reshape(n_seq, n_heads, hd)
+    for s in range(n_seq):
+        if ctxs[s] == 0:
+            assert not out[s].any()
+            continue
+        ref = oc.attn_decode(q[s], keys[s], vals[s], ks[s], vs[s], n_heads, n_kv, hd, ctxs[s])
+        assert rel_l2(out[s], ref) < 1e-5
 
 
 # ------------------------------------------------------------------- delta-net
