@@ -351,28 +351,12 @@ __global__ __launch_bounds__(64) void k_attn_mfma(const uint8_t* __restrict__ qa
 // in LDS.
 constexpr uint32_t kMergeWaves = 8;
 
-// Lanes 32k .. 32k+31 of a wave hold the 32 values of one Q8_0 block (k % 32 ==
-// lane % 32): quantize it with the reference quantizer's body rule and store
-// it in the Q8_0 activation layout (row i of M, K % 128 == 0).
-__device__ __forceinline__ void store_act_q8(float v, uint8_t* __restrict__ act, uint32_t M, uint32_t K, uint32_t i,
-                                             uint32_t k) {
-    float amax = fabsf(v);
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-    const float scale = q_scale(amax);
-    const float inv = __fdiv_rn(1.0f, scale);
-    const uint32_t sb = k / 32, e = k % 32, G = sb / 4, j = sb % 4, g = e / 8;
-    act[(((size_t)G * 4 + g) * M + i) * 32 + 8 * j + (e % 8)] = (uint8_t)q_body(v, inv);
-    if (e == 0) {
-        const ActLayout L = act_layout(EC_Q8_0, M, K);
-        ((float*)(act + L.xd_off))[(size_t)i * (L.Kp / 32) + sb] = scale;
-    }
-}
 // With act != nullptr the merged rows are also quantized into the Q8_0
 // activation layout (M = n_seq rows, K = n_heads*256; quantize_act's format).
 __global__ __launch_bounds__(512) void k_attn_merge(const float* __restrict__ ws, const int32_t* __restrict__ ctx,
                                                     float* __restrict__ out, uint8_t* __restrict__ act,
-                                                    uint32_t n_seq, uint32_t n_heads, uint32_t n_chunks_max,
+                                                    uint32_t act_xd_off, uint32_t n_seq, uint32_t n_heads,
+                                                    uint32_t n_chunks_max,
                                                     uint32_t max_ctx, uint32_t chunk) {
     extern __shared__ float w_s[];
     __shared__ float red[kMergeWaves];
@@ -384,7 +368,7 @@ __global__ __launch_bounds__(512) void k_attn_merge(const float* __restrict__ ws
     if (L <= 0) {
         if (tid < HD) {
             dst[tid] = 0.0f;
-            if (act) store_act_q8(0.0f, act, n_seq, n_heads * HD, s, h * HD + tid);
+            if (act) store_act_q8_lane(0.0f, act, (float*)(act + act_xd_off), n_seq, n_heads * HD / 32, s, h * HD + tid);
         }
         return;
     }
@@ -434,7 +418,7 @@ __global__ __launch_bounds__(512) void k_attn_merge(const float* __restrict__ ws
         for (int i = 0; i < (int)kMergeWaves; ++i) o += col[i * 256];
         o = o / dn;
         dst[tid] = o;
-        if (act) store_act_q8(o, act, n_seq, n_heads * HD, s, h * HD + tid);
+        if (act) store_act_q8_lane(o, act, (float*)(act + act_xd_off), n_seq, n_heads * HD / 32, s, h * HD + tid);
     }
 }
 
@@ -457,8 +441,9 @@ static void launch_mfma(const uint8_t* qa, const float* qsc, const int8_t* keys,
     const uint32_t ncm = (max_ctx + kChunk64 - 1) / kChunk64;
     hipLaunchKernelGGL((k_attn_mfma<G>), dim3(ncm, n_kv, n_seq), dim3(64), 0, st, qa, qsc, keys, vals, ks, vs, ctx,
                        seq_stride, n_kv, ncm, max_ctx, ws);
+    const uint32_t xd_off = (uint32_t)act_layout(EC_Q8_0, n_seq, n_kv * G * 256).xd_off;
     hipLaunchKernelGGL(k_attn_merge, dim3(n_kv * G, n_seq), dim3(512), ncm * sizeof(float), st, ws, ctx, out, act,
-                       n_seq, n_kv * G, ncm, max_ctx, kChunk64);
+                       xd_off, n_seq, n_kv * G, ncm, max_ctx, kChunk64);
 }
 
 static int mfma_dispatch(uint32_t G, const uint8_t* qa, const float* qsc, const int8_t* keys, const int8_t* vals,

@@ -54,6 +54,39 @@ __device__ __forceinline__ int8_t q_tail(float x, float scale) {
     return (int8_t)v;
 }
 
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+// Causal depthwise conv of channel c at position p over a ring state
+// [kern][conv_dim] (slot q % kern = input of position q, zeros before 0):
+//   sum_k x_{p-k} * w[(kern-1-k)*conv_dim + c], x_p = xin, newest tap first.
+__device__ __forceinline__ float conv_ring(const float* __restrict__ st, const float* __restrict__ w, float xin,
+                                           uint32_t p, uint32_t kern, uint32_t conv_dim, uint32_t c) {
+    float acc = xin * w[(size_t)(kern - 1) * conv_dim + c];
+    for (uint32_t k = 1; k < kern; ++k)
+        acc += st[(size_t)((p + kern - k) % kern) * conv_dim + c] * w[(size_t)(kern - 1 - k) * conv_dim + c];
+    return acc;
+}
+
+// Lanes 32m .. 32m+31 of a wave hold the 32 values of one Q8_0 block of
+// activation row i (block sb = k/32, lane % 32 == k % 32): quantize it with the
+// reference quantizer's body rule and store it in the Q8_0 activation layout
+// (quant.hip: element e of block sb = 4G + j at byte ((G*4 + e/8)*M + i)*32 +
+// 8j + e%8, scale at xd[i][sb], nbp = blocks per row).  Four lanes pack their
+// bytes into one dword store.
+__device__ __forceinline__ void store_act_q8_lane(float v, uint8_t* __restrict__ act, float* __restrict__ xd,
+                                                  uint32_t M, uint32_t nbp, uint32_t i, uint32_t k) {
+    float amax = fabsf(v);
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    const float scale = q_scale(amax);
+    const float inv = __fdiv_rn(1.0f, scale);
+    const uint32_t b = (uint8_t)q_body(v, inv);
+    const uint32_t w = b | (__shfl_down(b, 1) << 8) | (__shfl_down(b, 2) << 16) | (__shfl_down(b, 3) << 24);
+    const uint32_t sb = k / 32, e = k % 32, G = sb / 4, j = sb % 4;
+    if ((e & 3) == 0) *(uint32_t*)(act + (((size_t)G * 4 + e / 8) * M + i) * 32 + 8 * j + (e % 8)) = w;
+    if (e == 0) xd[(size_t)i * nbp + sb] = scale;
+}
+
 }  // namespace ec
 
 // Launch-error plumbing for the C ABI: every entry point returns an ec_status.

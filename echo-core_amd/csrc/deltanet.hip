@@ -14,6 +14,7 @@
 // leaves the VGPRs; q/k/v/decay/beta for the next token are loaded while the
 // current one is computed.
 #include "common.hpp"
+#include "layout.hpp"
 
 namespace ec {
 
@@ -82,6 +83,123 @@ __global__ __launch_bounds__(256) void k_deltanet(float* __restrict__ state, con
     *(float4*)(sp + 4) = make_float4(S[4], S[5], S[6], S[7]);
 }
 
+// ------------------------------------------------------------ fused decode step
+// One decode token of a delta-net block for value head h of sequence s, from
+// the input projection to the output projection's activation:
+//   conv + SiLU of the q/k channels of k-head h/rep and the v channels of h
+//   (ring conv state, as k_conv_gates), L2 norm of q and k, decay / beta gates,
+//   the delta-rule update of the head's 128x128 state, gated RMSNorm of the
+//   128 outputs and Q8_0 quantization into act (K = n_v*128).
+// grid (n_v, n_seq), block 1024: thread t owns column t/8 of the transposed
+// state S[v][k] and k-entries 16*(t%8) .. +15 (the state is loaded first, so
+// its latency overlaps the conv work).  The q/k conv state of a k-head shared
+// by rep value heads is written by the block with h % rep == 0; the others
+// only read slots that step leaves untouched.
+__global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ proj, uint32_t Nin,
+                                                     float* __restrict__ conv_state,
+                                                     const float* __restrict__ conv_w,
+                                                     const float* __restrict__ a_log,
+                                                     const float* __restrict__ dt_bias,
+                                                     const float* __restrict__ norm_w, float* __restrict__ state,
+                                                     uint8_t* __restrict__ act, uint32_t xd_off, uint32_t M,
+                                                     const int32_t* __restrict__ pos, uint32_t n_k, uint32_t n_v,
+                                                     uint32_t kern) {
+    __shared__ float q_s[128], k_s[128], v_s[128], o_s[128];
+    __shared__ float red[4], red2[2], gate_s[2];
+    const uint32_t h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
+    const int32_t p = pos[s];
+    if (p < 0) return;
+    const uint32_t key_dim = n_k * 128, value_dim = n_v * 128, conv_dim = 2 * key_dim + value_dim;
+    const uint32_t rep = n_v / n_k, qh = h / rep;
+    const float* pr = proj + (size_t)s * Nin;
+
+    // state column (loaded first)
+    const uint32_t col = t >> 3, ks = t & 7;
+    float* sp = state + (((size_t)s * n_v + h) * 128 + col) * 128 + 16 * ks;
+    float S[16];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const float4 v4 = *(const float4*)(sp + 4 * u);
+        S[4 * u] = v4.x, S[4 * u + 1] = v4.y, S[4 * u + 2] = v4.z, S[4 * u + 3] = v4.w;
+    }
+
+    // conv: threads 0..127 q channels, 128..255 k channels, 256..383 v channels; 384 gates
+    float* cst = conv_state + (size_t)s * kern * conv_dim;
+    if (t < 384) {
+        const uint32_t part = t >> 7, i = t & 127;
+        const uint32_t c = part == 2 ? 2 * key_dim + h * 128 + i : part * key_dim + qh * 128 + i;
+        const float xin = pr[c];
+        const float a = silu(conv_ring(cst, conv_w, xin, (uint32_t)p, kern, conv_dim, c));
+        if (part == 2 || h % rep == 0) cst[(size_t)((uint32_t)p % kern) * conv_dim + c] = xin;
+        if (part == 2) {
+            v_s[i] = a;
+        } else {
+            const float ss = wave_sum(a * a);  // part is uniform per wave
+            if ((t & 63) == 0) red[t >> 6] = ss;
+            (part == 0 ? q_s : k_s)[i] = a;  // normalized after the barrier
+        }
+    } else if (t == 384) {
+        const float al = pr[conv_dim + value_dim + h];
+        const float br = pr[conv_dim + value_dim + n_v + h];
+        const float sp_in = al + dt_bias[h];
+        const float spl = sp_in > 20.0f ? sp_in : log1pf(expf(sp_in));
+        const float g = -expf(a_log[h]) * spl;
+        gate_s[0] = expf(g);
+        gate_s[1] = 1.0f / (1.0f + expf(-br));
+    }
+    __syncthreads();
+    const float inv_q = 1.0f / sqrtf((red[0] + red[1]) + 1e-6f);
+    const float inv_k = 1.0f / sqrtf((red[2] + red[3]) + 1e-6f);
+    const float dec = gate_s[0], bt = gate_s[1];
+
+    // delta rule on this column: S <- dec*S; kv = S.k; delta = (v - kv)*beta; S += k*delta; o = S.q/sqrt(128)
+    const float scale = 1.0f / sqrtf(128.0f);
+    float kk[16], qq[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        kk[i] = k_s[16 * ks + i] * inv_k;
+        qq[i] = q_s[16 * ks + i] * inv_q;
+    }
+    float kvp = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        S[i] *= dec;
+        kvp = fmaf(S[i], kk[i], kvp);
+    }
+    kvp += __shfl_xor(kvp, 1);
+    kvp += __shfl_xor(kvp, 2);
+    kvp += __shfl_xor(kvp, 4);
+    const float delta = (v_s[col] - kvp) * bt;
+    float op = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        S[i] = fmaf(kk[i], delta, S[i]);
+        op = fmaf(S[i], qq[i] * scale, op);
+    }
+    op += __shfl_xor(op, 1);
+    op += __shfl_xor(op, 2);
+    op += __shfl_xor(op, 4);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) *(float4*)(sp + 4 * u) = make_float4(S[4 * u], S[4 * u + 1], S[4 * u + 2], S[4 * u + 3]);
+    if (ks == 0) o_s[col] = op;
+    __syncthreads();
+
+    // gated RMSNorm over the head's 128 outputs (waves 0 and 1), quantized for the output projection
+    float o = 0.0f;
+    if (t < 128) {
+        o = o_s[t];
+        const float ss = wave_sum(o * o);
+        if ((t & 63) == 0) red2[t >> 6] = ss;
+    }
+    __syncthreads();
+    if (t < 128) {
+        const float rms = sqrtf((red2[0] + red2[1]) / 128.0f + 1e-6f);
+        const float inv = 1.0f / rms;
+        const float val = o * inv * norm_w[t] * silu(pr[conv_dim + h * 128 + t]);
+        store_act_q8_lane(val, act, (float*)(act + xd_off), M, value_dim / 32, s, h * 128 + t);
+    }
+}
+
 }  // namespace ec
 
 using namespace ec;
@@ -95,6 +213,22 @@ extern "C" int ec_deltanet(float* state, const float* q, const float* k, const f
         return ec_set_error(EC_ERR_ARG, "ec_deltanet: need d_k == 128, d_v % 16 == 0, n_v % n_k == 0");
     hipLaunchKernelGGL(k_deltanet, dim3(n_v * (d_v / 16), n_seq), dim3(256), 0, (hipStream_t)stream, state, q, k, v,
                        decay, beta, out, T, n_seq, n_v, n_k, d_v, seq_pos);
+    EC_CHECK_LAUNCH();
+    return EC_OK;
+}
+
+extern "C" int ec_delta_step(const float* proj, uint32_t Nin, float* conv_state, const float* conv_w,
+                             const float* a_log, const float* dt_bias, const float* norm_w, float* state, void* act,
+                             const int32_t* pos, uint32_t n_seq, uint32_t n_k, uint32_t n_v, uint32_t kern,
+                             void* stream) {
+    if (n_seq == 0) return EC_OK;
+    if (!proj || !conv_state || !conv_w || !a_log || !dt_bias || !norm_w || !state || !act || !pos || n_k == 0 ||
+        n_v == 0 || n_v % n_k || kern == 0 || n_seq > 16 || Nin < 2 * n_k * 128 + 2 * n_v * 128 + 2 * n_v)
+        return ec_set_error(EC_ERR_ARG, "ec_delta_step: bad argument");
+    const ActLayout L = act_layout(EC_Q8_0, n_seq, n_v * 128);
+    hipLaunchKernelGGL(k_delta_step, dim3(n_v, n_seq), dim3(1024), 0, (hipStream_t)stream, proj, Nin, conv_state,
+                       conv_w, a_log, dt_bias, norm_w, state, (uint8_t*)act, (uint32_t)L.xd_off, n_seq, pos, n_k,
+                       n_v, kern);
     EC_CHECK_LAUNCH();
     return EC_OK;
 }

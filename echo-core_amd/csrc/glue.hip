@@ -41,7 +41,6 @@ __device__ __forceinline__ float block_max256(float v, float* sh) {
     return fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
 }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
 
 // Quantize 32 values (one block) and store them into the Q8_0 activation
 // layout for token slot i of an M-row activation buffer; scale to xd[i][sb].
@@ -77,104 +76,98 @@ __global__ __launch_bounds__(256) void k_embed_q8_0(const uint8_t* __restrict__ 
 }
 
 // ---------------------------------------------------------- RMSNorm + quantize
-// grid (M): row i of x [M][H] -> act (Q8_0 layout, K = H).
+// grid (ceil(Kp/256), M), block 256: every block reads the whole row i of x
+// [M][H] for the sum of squares (float4 loads, all issued before the
+// reduction) and quantizes its own 256 elements into act (Q8_0 layout,
+// K = H); thread = element, so each 32-lane half-wave quantizes one block.
 __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__ x, const float* __restrict__ w,
                                                        uint8_t* __restrict__ act, uint32_t M, uint32_t H,
                                                        uint32_t xd_off) {
     __shared__ float sh[4];
-    const uint32_t i = blockIdx.x;
+    const uint32_t i = blockIdx.y, t = threadIdx.x, k = blockIdx.x * 256 + t;
     const float* xr = x + (size_t)i * H;
+    const float4* x4 = (const float4*)xr;
+    const uint32_t Kp = round_up(H, 128);
+    const float xk = k < H ? xr[k] : 0.0f;
+    const float wk = k < H ? w[k] : 0.0f;
     float ss = 0.0f;
-    for (uint32_t k = threadIdx.x; k < H; k += 256) ss = fmaf(xr[k], xr[k], ss);
+    uint32_t c = t;
+    for (; c + 3 * 256 < H / 4; c += 4 * 256) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = x4[c + 256 * u];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) ss = fmaf(v[u].x, v[u].x, fmaf(v[u].y, v[u].y, fmaf(v[u].z, v[u].z, fmaf(v[u].w, v[u].w, ss))));
+    }
+    for (; c < H / 4; c += 256) {
+        const float4 v = x4[c];
+        ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
+    }
     ss = block_sum256(ss, sh);
     const float inv = 1.0f / sqrtf(ss / (float)H + 1e-6f);
-    const uint32_t nbp = round_up(H, 128) / 32;
-    float* xd = (float*)(act + xd_off);
-    for (uint32_t sb = threadIdx.x; sb < nbp; sb += 256) {
-        float v[32];
-        for (int e = 0; e < 32; ++e) {
-            const uint32_t k = 32 * sb + e;
-            v[e] = k < H ? xr[k] * inv * w[k] : 0.0f;
-        }
-        store_block_q8(v, act, M, i, sb, nbp, xd);
-    }
+    if (k >= Kp) return;  // whole 32-lane blocks leave together
+    store_act_q8_lane(xk * inv * wk, act, (float*)(act + xd_off), M, Kp / 32, i, k);
 }
 
 // ------------------------------------------------------- SwiGLU + quantize
-// gu [M][2F] (gate rows then up rows) -> act (K = F).  One thread per block.
+// gu [M][2F] (gate rows then up rows) -> act (K = F).  grid (ceil(Kp/256), M),
+// thread = element.
 __global__ __launch_bounds__(256) void k_swiglu_quant(const float* __restrict__ gu, uint8_t* __restrict__ act,
                                                       uint32_t M, uint32_t F, uint32_t xd_off) {
-    const uint32_t nbp = round_up(F, 128) / 32;
-    const uint32_t idx = blockIdx.x * 256 + threadIdx.x;
-    if (idx >= M * nbp) return;
-    const uint32_t i = idx / nbp, sb = idx % nbp;
+    const uint32_t Kp = round_up(F, 128);
+    const uint32_t i = blockIdx.y, k = blockIdx.x * 256 + threadIdx.x;
+    if (k >= Kp) return;  // whole 32-lane blocks leave together (Kp % 32 == 0)
     const float* g = gu + (size_t)i * 2 * F;
-    float v[32];
-    for (int e = 0; e < 32; ++e) {
-        const uint32_t k = 32 * sb + e;
-        v[e] = k < F ? silu(g[k]) * g[F + k] : 0.0f;
-    }
-    store_block_q8(v, act, M, i, sb, nbp, (float*)(act + xd_off));
+    const float v = k < F ? silu(g[k]) * g[F + k] : 0.0f;
+    store_act_q8_lane(v, act, (float*)(act + xd_off), M, Kp / 32, i, k);
 }
 
 // ------------------------------------------------ delta-net conv + norms + gates
-// grid (n_k, n_seq), block 256.  proj [n_seq][Nin]: conv channels
-// [0, conv_dim) = q (key_dim) | k (key_dim) | v (value_dim), then z (value_dim),
-// alpha (n_v), beta (n_v).  conv_state [n_seq][kern][conv_dim] (slot 0 newest).
-// Outputs: q, k [n_seq][n_k][128] (L2-normalised), v [n_seq][n_v][128],
-// decay, beta [n_seq][n_v].  Requires head dims of 128 and n_v = rep * n_k
-// with rep <= 2.
-__global__ __launch_bounds__(256) void k_conv_gates(const float* __restrict__ proj, uint32_t Nin,
+// grid (conv_dim/128, n_seq), block 128: one 128-channel head of the q, k or v
+// region per block, thread = channel.  Conv state [n_seq][kern][conv_dim] is a
+// ring over positions: slot p % kern holds the input of position p, so a step
+// writes one slot and reads the kern-1 older ones (zero after reset).  q and k
+// heads are L2-normalized; v heads also compute their decay / beta gates.
+__global__ __launch_bounds__(128) void k_conv_gates(const float* __restrict__ proj, uint32_t Nin,
                                                     float* __restrict__ conv_state, const float* __restrict__ conv_w,
                                                     const float* __restrict__ a_log, const float* __restrict__ dt_bias,
                                                     float* __restrict__ q_out, float* __restrict__ k_out,
                                                     float* __restrict__ v_out, float* __restrict__ dec,
                                                     float* __restrict__ beta, const int32_t* __restrict__ pos,
                                                     uint32_t n_k, uint32_t n_v, uint32_t kern) {
-    __shared__ float sh[4];
-    __shared__ float sq[2];
-    const uint32_t qh = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
-    if (pos[s] < 0) return;
+    __shared__ float sh[2];
+    const uint32_t hb = blockIdx.x, s = blockIdx.y, i = threadIdx.x;
+    const int32_t p = pos[s];
+    if (p < 0) return;
     const uint32_t key_dim = n_k * 128, value_dim = n_v * 128, conv_dim = 2 * key_dim + value_dim;
-    const uint32_t rep = n_v / n_k;
     const float* pr = proj + (size_t)s * Nin;
     float* st = conv_state + (size_t)s * kern * conv_dim;
-    auto conv = [&](uint32_t c) -> float {
-        for (uint32_t k = kern - 1; k > 0; --k) st[(size_t)k * conv_dim + c] = st[(size_t)(k - 1) * conv_dim + c];
-        st[c] = pr[c];
-        float acc = 0.0f;
-        for (uint32_t k = 0; k < kern; ++k) acc += st[(size_t)k * conv_dim + c] * conv_w[(size_t)(kern - 1 - k) * conv_dim + c];
-        return silu(acc);
-    };
-    // q (t < 128) or k (t >= 128) channel of this k-head
-    const uint32_t half = t / 128, i = t % 128;
-    const uint32_t cqk = half * key_dim + qh * 128 + i;
-    const float a = conv(cqk);
-    // v channels of the v-heads of this k-head
-    for (uint32_t r = half; r < rep; r += 2) {
-        const uint32_t h = qh * rep + r;
-        v_out[((size_t)s * n_v + h) * 128 + i] = conv(2 * key_dim + h * 128 + i);
+    const uint32_t c = hb * 128 + i;
+    const float xin = pr[c];
+    const float a = silu(conv_ring(st, conv_w, xin, (uint32_t)p, kern, conv_dim, c));
+    st[(size_t)((uint32_t)p % kern) * conv_dim + c] = xin;
+    if (c >= 2 * key_dim) {  // v head
+        const uint32_t h = hb - 2 * n_k;
+        v_out[((size_t)s * n_v + h) * 128 + i] = a;
+        if (i == 0) {
+            const float al = pr[conv_dim + value_dim + h];
+            const float br = pr[conv_dim + value_dim + n_v + h];
+            const float sp_in = al + dt_bias[h];
+            const float sp = sp_in > 20.0f ? sp_in : log1pf(expf(sp_in));
+            const float g = -expf(a_log[h]) * sp;
+            dec[(size_t)s * n_v + h] = expf(g);
+            beta[(size_t)s * n_v + h] = 1.0f / (1.0f + expf(-br));
+        }
+        return;
     }
-    // L2 norms of q and k over their 128 channels (two waves each)
-    float ss = wave_sum(a * a);
-    const uint32_t w = t >> 6;
-    if ((t & 63) == 0) sh[w] = ss;
+    // q or k head: L2 norm over its 128 channels (two waves)
+    const float ss = wave_sum(a * a);
+    if ((i & 63) == 0) sh[i >> 6] = ss;
     __syncthreads();
-    if (t == 0) sq[0] = sh[0] + sh[1];
-    if (t == 128) sq[1] = sh[2] + sh[3];
-    __syncthreads();
-    const float inv = 1.0f / sqrtf(sq[half] + 1e-6f);
-    (half == 0 ? q_out : k_out)[((size_t)s * n_k + qh) * 128 + i] = a * inv;
-    if (t < rep) {
-        const uint32_t h = qh * rep + t;
-        const float al = pr[conv_dim + value_dim + h];
-        const float br = pr[conv_dim + value_dim + n_v + h];
-        const float sp_in = al + dt_bias[h];
-        const float sp = sp_in > 20.0f ? sp_in : log1pf(expf(sp_in));
-        const float g = -expf(a_log[h]) * sp;
-        dec[(size_t)s * n_v + h] = expf(g);
-        beta[(size_t)s * n_v + h] = 1.0f / (1.0f + expf(-br));
-    }
+    const float inv = 1.0f / sqrtf((sh[0] + sh[1]) + 1e-6f);
+    const bool is_q = c < key_dim;
+    const uint32_t h = is_q ? hb : hb - n_k;
+    (is_q ? q_out : k_out)[((size_t)s * n_k + h) * 128 + i] = a * inv;
 }
 
 // ------------------------------------------------ gated RMSNorm + quantize
@@ -194,17 +187,7 @@ __global__ __launch_bounds__(128) void k_gated_norm_quant(const float* __restric
     const float rms = sqrtf((sh[0] + sh[1]) / 128.0f + 1e-6f);
     const float inv = 1.0f / rms;
     const float val = o * inv * norm_w[i] * silu(proj[(size_t)s * Nin + z_off + h * 128 + i]);
-    // quantize the 32-lane group (one block)
-    float amax = fabsf(val);
-    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
-    const float scale = q_scale(amax);
-    const float qinv = __fdiv_rn(1.0f, scale);
-    const int8_t qv = q_body(val, qinv);
-    const uint32_t nbp = round_up(n_v * 128, 128) / 32;
-    const uint32_t sb = h * 4 + i / 32, e = i % 32;
-    const uint32_t G = sb / 4, j = sb % 4, g = e / 8;
-    act[(((size_t)G * 4 + g) * M + s) * 32 + 8 * j + e % 8] = (uint8_t)qv;
-    if (e == 0) ((float*)(act + xd_off))[(size_t)s * nbp + sb] = scale;
+    store_act_q8_lane(val, act, (float*)(act + xd_off), M, n_v * 4, s, h * 128 + i);
 }
 
 // -------------------------------------------- head norm + RoPE + KV append
@@ -273,12 +256,35 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float* __restrict
     const float* l = logits + (size_t)s * vocab;
     float best = -INFINITY;
     int32_t bi = 0x7FFFFFFF;
-    for (uint32_t k = t; k < vocab; k += 1024) {
-        const float v = l[k];
+    // strictly greater keeps the first index among equal values within a thread
+    // (its indices only grow); the reductions below break ties by index
+    auto take = [&](float v, uint32_t k) {
         if (v > best) {
             best = v;
             bi = (int32_t)k;
         }
+    };
+    if ((((uintptr_t)l) & 15) == 0) {
+        const uint32_t n4 = vocab / 4;
+        const float4* l4 = (const float4*)l;
+        uint32_t k = t;
+        for (; k + 3 * 1024 < n4; k += 4 * 1024) {
+            float4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = l4[k + u * 1024];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t b = 4 * (k + u * 1024);
+                take(v[u].x, b), take(v[u].y, b + 1), take(v[u].z, b + 2), take(v[u].w, b + 3);
+            }
+        }
+        for (; k < n4; k += 1024) {
+            const float4 v = l4[k];
+            take(v.x, 4 * k), take(v.y, 4 * k + 1), take(v.z, 4 * k + 2), take(v.w, 4 * k + 3);
+        }
+        for (uint32_t r = 4 * n4 + t; r < vocab; r += 1024) take(l[r], r);
+    } else {
+        for (uint32_t k = t; k < vocab; k += 1024) take(l[k], k);
     }
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(best, o);
@@ -328,18 +334,18 @@ extern "C" int ec_glue_embed(const void* emb, const int32_t* tok, float* x, uint
 
 extern "C" int ec_glue_rmsnorm_quant(const float* x, const float* w, void* act, uint32_t M, uint32_t H,
                                      void* stream) {
-    if (!x || !w || !act || M == 0 || M > 16 || H % 32) return ec_set_error(EC_ERR_ARG, "ec_glue_rmsnorm_quant");
+    if (!x || !w || !act || M == 0 || M > 16 || H % 32 || ((uintptr_t)x & 15))
+        return ec_set_error(EC_ERR_ARG, "ec_glue_rmsnorm_quant: bad argument");
     const ActLayout L = act_layout(EC_Q8_0, M, H);
-    EC_GLUE_LAUNCH(k_rmsnorm_quant, dim3(M), dim3(256), 0, (hipStream_t)stream, x, w, (uint8_t*)act, M, H,
-                   (uint32_t)L.xd_off);
+    EC_GLUE_LAUNCH(k_rmsnorm_quant, dim3((L.Kp + 255) / 256, M), dim3(256), 0, (hipStream_t)stream, x, w,
+                   (uint8_t*)act, M, H, (uint32_t)L.xd_off);
 }
 
 extern "C" int ec_glue_swiglu_quant(const float* gu, void* act, uint32_t M, uint32_t F, void* stream) {
     if (!gu || !act || M == 0 || M > 16 || F % 32) return ec_set_error(EC_ERR_ARG, "ec_glue_swiglu_quant");
     const ActLayout L = act_layout(EC_Q8_0, M, F);
-    const uint32_t n = M * (L.Kp / 32);
-    EC_GLUE_LAUNCH(k_swiglu_quant, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, gu, (uint8_t*)act, M,
-                   F, (uint32_t)L.xd_off);
+    EC_GLUE_LAUNCH(k_swiglu_quant, dim3((L.Kp + 255) / 256, M), dim3(256), 0, (hipStream_t)stream, gu,
+                   (uint8_t*)act, M, F, (uint32_t)L.xd_off);
 }
 
 extern "C" int ec_glue_conv_gates(const float* proj, uint32_t Nin, float* conv_state, const float* conv_w,
@@ -347,10 +353,10 @@ extern "C" int ec_glue_conv_gates(const float* proj, uint32_t Nin, float* conv_s
                                   float* beta, const int32_t* pos, uint32_t n_seq, uint32_t n_k, uint32_t n_v,
                                   uint32_t kern, void* stream) {
     if (!proj || !conv_state || !conv_w || !a_log || !dt_bias || !q || !k || !v || !dec || !beta || !pos ||
-        n_k == 0 || n_v % n_k || n_v / n_k > 2 || kern == 0 || Nin < 3 * n_k * 128 + n_v * 128 + 2 * n_v)
+        n_k == 0 || n_v == 0 || kern == 0 || Nin < 2 * n_k * 128 + 2 * n_v * 128 + 2 * n_v)
         return ec_set_error(EC_ERR_ARG, "ec_glue_conv_gates: bad argument");
-    EC_GLUE_LAUNCH(k_conv_gates, dim3(n_k, n_seq), dim3(256), 0, (hipStream_t)stream, proj, Nin, conv_state, conv_w,
-                   a_log, dt_bias, q, k, v, dec, beta, pos, n_k, n_v, kern);
+    EC_GLUE_LAUNCH(k_conv_gates, dim3(2 * n_k + n_v, n_seq), dim3(128), 0, (hipStream_t)stream, proj, Nin,
+                   conv_state, conv_w, a_log, dt_bias, q, k, v, dec, beta, pos, n_k, n_v, kern);
 }
 
 extern "C" int ec_glue_gated_norm_quant(const float* core, const float* proj, uint32_t Nin, uint32_t z_off,

@@ -11,6 +11,7 @@ from .lib import EchoHipError, load
 T_EMBED, T_FINAL_NORM, T_LM_HEAD = 0, 1, 2
 T_ATTN_NORM, T_FFN_NORM, T_W_IN, T_W_OUT, T_W_GATE, T_W_UP, T_W_DOWN = 10, 11, 12, 13, 14, 15, 16
 T_CONV_W, T_A_LOG, T_DT_BIAS, T_SSM_NORM, T_Q_NORM, T_K_NORM = 17, 18, 19, 20, 21, 22
+S_CONV, S_SSM, S_KEYS, S_VALS, S_KSCALES, S_VSCALES = 0, 1, 2, 3, 4, 5
 
 
 @dataclass
@@ -68,6 +69,7 @@ class Engine:
         L.ec_engine_set_tensor.argtypes = [vp, i32, i32, vp, C.c_size_t]
         L.ec_engine_init_random.argtypes = [vp, C.c_uint64, C.c_float]
         L.ec_engine_get_tensor.argtypes = [vp, i32, i32, vp, C.c_size_t]
+        L.ec_engine_get_state.argtypes = [vp, i32, i32, u32, vp, C.c_size_t]
         L.ec_engine_reset.argtypes = [vp]
         L.ec_engine_set_inputs.argtypes = [vp, vp, vp, u32]
         L.ec_engine_step.argtypes = [vp, i32]
@@ -105,6 +107,17 @@ class Engine:
         out = np.empty(nbytes, np.uint8)
         self._check(self.L.ec_engine_get_tensor(self.h, layer, tensor, out.ctypes.data, nbytes), "get_tensor")
         return out.view(dtype)
+
+    def get_state(self, layer: int, which: int, seq: int) -> np.ndarray:
+        """One sequence's state (echo_engine.h ec_engine_get_state) as a flat array."""
+        c = self.cfg
+        conv_dim = c.conv_dim
+        n, dt = {S_CONV: (c.conv_kernel * conv_dim, np.float32), S_SSM: (c.ssm_heads * 128 * 128, np.float32),
+                 S_KEYS: (c.max_ctx * c.n_kv * c.head_dim, np.int8), S_VALS: (c.max_ctx * c.n_kv * c.head_dim, np.int8),
+                 S_KSCALES: (c.max_ctx * c.n_kv, np.float32), S_VSCALES: (c.max_ctx * c.n_kv, np.float32)}[which]
+        out = np.empty(n, dt)
+        self._check(self.L.ec_engine_get_state(self.h, layer, which, seq, out.ctypes.data, out.nbytes), "get_state")
+        return out
 
     def init_random(self, seed: int = 0, w_scale: float = 0.02 / 73.0):
         self._check(self.L.ec_engine_init_random(self.h, seed, w_scale), "init_random")

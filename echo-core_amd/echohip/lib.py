@@ -39,6 +39,12 @@ _SIGS = {
     "ec_attn_decode_packed": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u64, _u32, _u32, _u32, _vp, _vp],
     "ec_deltanet": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp, _vp],
     "ec_fill_random": [C.c_int, _vp, _u64, _u64, C.c_float, _u32, _vp],
+    "ec_delta_step": [_vp, _u32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp],
+    "ec_glue_conv_gates": [_vp, _u32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
+                           _vp],
+    "ec_glue_gated_norm_quant": [_vp, _vp, _u32, _u32, _vp, _vp, _u32, _u32, _vp],
+    "ec_glue_rmsnorm_quant": [_vp, _vp, _vp, _u32, _u32, _vp],
+    "ec_glue_swiglu_quant": [_vp, _vp, _u32, _u32, _vp],
     "ec_stream_read": [_vp, _sz, _vp, _u32, _vp],
 }
 _SIZE_FNS = {
@@ -153,6 +159,27 @@ class Lib:
 
     def attn_qa_bytes(self, n_seq, n_heads):
         return self.L.ec_attn_qa_bytes(n_seq, n_heads)
+
+    def delta_step(self, proj, Nin, conv_state, conv_w, a_log, dt_bias, norm_w, state, act, pos, n_seq, n_k, n_v,
+                   kern, stream=None):
+        self._call("ec_delta_step", _ptr(proj), Nin, _ptr(conv_state), _ptr(conv_w), _ptr(a_log), _ptr(dt_bias),
+                   _ptr(norm_w), _ptr(state), _ptr(act), _ptr(pos), n_seq, n_k, n_v, kern, self._stream(stream))
+
+    def conv_gates(self, proj, Nin, conv_state, conv_w, a_log, dt_bias, q, k, v, dec, beta, pos, n_seq, n_k, n_v,
+                   kern, stream=None):
+        self._call("ec_glue_conv_gates", _ptr(proj), Nin, _ptr(conv_state), _ptr(conv_w), _ptr(a_log),
+                   _ptr(dt_bias), _ptr(q), _ptr(k), _ptr(v), _ptr(dec), _ptr(beta), _ptr(pos), n_seq, n_k, n_v, kern,
+                   self._stream(stream))
+
+    def gated_norm_quant(self, core, proj, Nin, z_off, norm_w, act, M, n_v, stream=None):
+        self._call("ec_glue_gated_norm_quant", _ptr(core), _ptr(proj), Nin, z_off, _ptr(norm_w), _ptr(act), M, n_v,
+                   self._stream(stream))
+
+    def rmsnorm_quant(self, x, w, act, M, H, stream=None):
+        self._call("ec_glue_rmsnorm_quant", _ptr(x), _ptr(w), _ptr(act), M, H, self._stream(stream))
+
+    def swiglu_quant(self, gu, act, M, F, stream=None):
+        self._call("ec_glue_swiglu_quant", _ptr(gu), _ptr(act), M, F, self._stream(stream))
 
     def deltanet(self, state, q, k, v, decay, beta, out, T, n_seq, n_v, n_k, d_k, d_v, seq_pos=None, stream=None):
         self._call("ec_deltanet", _ptr(state), _ptr(q), _ptr(k), _ptr(v), _ptr(decay), _ptr(beta), _ptr(out), T,

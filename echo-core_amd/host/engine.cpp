@@ -186,12 +186,9 @@ int record_step(ec_engine* e) {
         if (!y.attn) {
             const uint32_t Nin = e->nin_delta;
             EC_TRY(mv(e, y.w_in, e->act_h, e->proj, Nin, 0));
-            EC_TRY(ec_glue_conv_gates(e->proj, Nin, y.conv_state, y.conv_w, y.a_log, y.dt_bias, e->q, e->k, e->v,
-                                      e->dec, e->beta, e->pos, B, e->n_k, e->n_v, c.conv_kernel, st));
-            EC_TRY(ec_deltanet(y.ssm_state, e->q, e->k, e->v, e->dec, e->beta, e->core, 1, B, e->n_v, e->n_k, 128,
-                               128, e->pos, st));
-            EC_TRY(ec_glue_gated_norm_quant(e->core, e->proj, Nin, e->conv_dim, y.ssm_norm, e->act_v, B, e->n_v,
-                                            st));
+            // conv + gates + delta rule + gated norm + quantize in one launch
+            EC_TRY(ec_delta_step(e->proj, Nin, y.conv_state, y.conv_w, y.a_log, y.dt_bias, y.ssm_norm, y.ssm_state,
+                                 e->act_v, e->pos, B, e->n_k, e->n_v, c.conv_kernel, st));
             EC_TRY(mv(e, y.w_out, e->act_v, e->x, H, 1));
         } else {
             const uint32_t Nin = e->nin_attn;
@@ -472,6 +469,35 @@ extern "C" int ec_engine_get_tensor(ec_engine* e, int layer, int tensor, void* h
         return vec(y.k_norm, c.head_dim);
     }
     return ec_set_error(EC_ERR_ARG, "ec_engine_get_tensor: tensor id not valid for this layer");
+}
+
+extern "C" int ec_engine_get_state(ec_engine* e, int layer, int which, uint32_t seq, void* host, size_t bytes) {
+    if (!e || !host) return ec_set_error(EC_ERR_ARG, "ec_engine_get_state: null argument");
+    const ec_engine_cfg& c = e->c;
+    if (layer < 0 || (uint32_t)layer >= c.n_layers || seq >= e->B)
+        return ec_set_error(EC_ERR_ARG, "ec_engine_get_state: layer or sequence out of range");
+    const Layer& y = e->L[layer];
+    const void* src = nullptr;
+    size_t n = 0;
+    if (!y.attn && which == EC_S_CONV) {
+        n = (size_t)c.conv_kernel * e->conv_dim * 4;
+        src = y.conv_state + (size_t)seq * c.conv_kernel * e->conv_dim;
+    } else if (!y.attn && which == EC_S_SSM) {
+        n = (size_t)e->n_v * 128 * 128 * 4;
+        src = y.ssm_state + (size_t)seq * e->n_v * 128 * 128;
+    } else if (y.attn && (which == EC_S_KEYS || which == EC_S_VALS)) {
+        n = e->seq_stride;
+        src = (which == EC_S_KEYS ? y.keys : y.vals) + (size_t)seq * e->seq_stride;
+    } else if (y.attn && (which == EC_S_KSCALES || which == EC_S_VSCALES)) {
+        n = (size_t)c.max_ctx * c.n_kv * 4;
+        src = (which == EC_S_KSCALES ? y.ks : y.vs) + (size_t)seq * c.max_ctx * c.n_kv;
+    } else {
+        return ec_set_error(EC_ERR_ARG, "ec_engine_get_state: state id not valid for this layer");
+    }
+    if (bytes != n) return ec_set_error(EC_ERR_ARG, "ec_engine_get_state: wrong byte count");
+    EC_HIP(hipStreamSynchronize(e->st));
+    EC_HIP(hipMemcpy(host, src, n, hipMemcpyDeviceToHost));
+    return EC_OK;
 }
 
 extern "C" int ec_engine_init_random(ec_engine* e, uint64_t seed, float w_scale) {

@@ -78,6 +78,24 @@ int ec_engine_set_tensor(ec_engine* e, int layer, int tensor, const void* host, 
 /* Copy one tensor back to host memory in the set_tensor format (matrices as
  * GGUF Q8_0 bytes; EC_T_W_GATE / EC_T_W_UP each return their half). */
 int ec_engine_get_tensor(ec_engine* e, int layer, int tensor, void* host, size_t bytes);
+
+/* Recurrent and cached state of one sequence after the last completed step
+ * (synchronizes the engine stream), copied to host memory:
+ *   EC_S_CONV     delta-net: fp32 [conv_kernel][conv_dim], a ring over
+ *                 positions (slot p % conv_kernel = conv input of position p)
+ *   EC_S_SSM      delta-net: fp32 [ssm_heads][128 v][128 k] (S transposed)
+ *   EC_S_KEYS/VALS        attention: int8 [max_ctx][n_kv][head_dim]
+ *   EC_S_KSCALES/VSCALES  attention: fp32 [max_ctx][n_kv]
+ * bytes must equal the state's size. */
+enum {
+    EC_S_CONV = 0,
+    EC_S_SSM = 1,
+    EC_S_KEYS = 2,
+    EC_S_VALS = 3,
+    EC_S_KSCALES = 4,
+    EC_S_VSCALES = 5,
+};
+int ec_engine_get_state(ec_engine* e, int layer, int which, uint32_t seq, void* host, size_t bytes);
 /* Fill every tensor with seeded synthetic values generated on the device:
  * matrices Q8_0 with qs ~ U{-127..127} and d = fp16(|N(0,1)| * w_scale);
  * norms 1 + 0.1*N(0,1); conv taps 0.5*N(0,1); A_log = ln U[1,16]; dt_bias 0.1*N(0,1). */

@@ -138,6 +138,17 @@ int ec_attn_decode_packed(const void* q_packed, const float* q_scales, const int
 int ec_deltanet(float* state, const float* q, const float* k, const float* v, const float* decay, const float* beta,
                 float* out, uint32_t T, uint32_t n_seq, uint32_t n_v, uint32_t n_k, uint32_t d_k, uint32_t d_v,
                 const int32_t* seq_pos, void* stream);
+
+/* One decode token of a delta-net block (qwen_linear.zig:182-257), fused:
+ * conv + SiLU over the ring conv state (see ec_glue_conv_gates), q/k L2 norms,
+ * decay/beta gates, the delta rule on state (layout of ec_deltanet, d_k = d_v
+ * = 128), gated RMSNorm with norm_w[128] and z = proj[conv_dim + h*128 + i],
+ * quantized into act (Q8_0 activation layout, M = n_seq <= 16, K = n_v*128).
+ * proj rows [n_seq][Nin] hold q|k|v (conv_dim) | z (n_v*128) | alpha | beta.
+ * Sequences with pos[s] < 0 are skipped (state, conv state and act untouched). */
+int ec_delta_step(const float* proj, uint32_t Nin, float* conv_state, const float* conv_w, const float* a_log,
+                  const float* dt_bias, const float* norm_w, float* state, void* act, const int32_t* pos,
+                  uint32_t n_seq, uint32_t n_k, uint32_t n_v, uint32_t kern, void* stream);
 /* seq_pos (may be NULL): sequence s is skipped entirely (state untouched, no
  * output written) when seq_pos[s] < 0. */
 
@@ -148,6 +159,8 @@ int ec_glue_embed(const void* emb, const int32_t* tok, float* x, uint32_t n_seq,
                   void* stream);
 int ec_glue_rmsnorm_quant(const float* x, const float* w, void* act, uint32_t M, uint32_t H, void* stream);
 int ec_glue_swiglu_quant(const float* gu, void* act, uint32_t M, uint32_t F, void* stream);
+/* conv_state [n_seq][kern][conv_dim] is a ring over positions: slot p % kern
+ * holds the conv input of position p (all zero before position 0). */
 int ec_glue_conv_gates(const float* proj, uint32_t Nin, float* conv_state, const float* conv_w, const float* a_log,
                        const float* dt_bias, float* q, float* k, float* v, float* dec, float* beta,
                        const int32_t* pos, uint32_t n_seq, uint32_t n_k, uint32_t n_v, uint32_t kern, void* stream);

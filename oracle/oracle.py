@@ -269,7 +269,7 @@ class Decoder:
                 w[k].append(p(y.get(k)))
         self.w = _OcW(**{k: arr(v) for k, v in w.items()}, embed=p(m["embed"]), final_norm=p(m["final_norm"]),
                       lm_head=p(m["lm_head"]))
-        self.seqs = []
+        self.seqs, self.states = [], []
         kvd = cfg.n_kv * cfg.head_dim
         for _ in range(n_seq):
             st = {"conv": [], "ssm": [], "k": [], "v": [], "ks": [], "vs": []}
@@ -287,6 +287,7 @@ class Decoder:
                     for k in ("k", "v", "ks", "vs"):
                         st[k].append(None)
             self.keep.append(st)
+            self.states.append(st)
             s = _OcSeq(conv_state=arr([p(x) for x in st["conv"]]), ssm_state=arr([p(x) for x in st["ssm"]]),
                        keys=arr([p(x) for x in st["k"]]), vals=arr([p(x) for x in st["v"]]),
                        kscales=arr([p(x) for x in st["ks"]]), vscales=arr([p(x) for x in st["vs"]]), pos=0)
@@ -302,3 +303,14 @@ class Decoder:
 
     def pos(self, seq: int) -> int:
         return self.seqs[seq].pos
+
+    def load_state(self, seq: int, pos: int, get):
+        """Overwrite sequence `seq`'s state with another decoder's, at position
+        `pos` (tokens processed).  get(layer, kind) returns that decoder's state
+        in the oracle's layout: kind "conv" fp32 [kernel][C] newest first, "ssm"
+        fp32 [heads][k][v], "k"/"v" int8 [max_ctx][n_kv][head_dim], "ks"/"vs" fp32."""
+        st = self.states[seq]
+        for l in range(self.cfg.n_layers):
+            for kind in (("k", "v", "ks", "vs") if self.cfg.is_attn(l) else ("conv", "ssm")):
+                np.copyto(st[kind][l], get(l, kind).reshape(st[kind][l].shape))
+        self.seqs[seq].pos = pos

@@ -5,15 +5,23 @@ three sequences entering at different steps (ragged batch), prompt tokens
 first, then each sequence's own greedy tokens.  The oracle quantizes matvec
 inputs exactly as the GPU path does (quant_act=1), so the two agree to fp32
 rounding (~1e-7 relative L2 of the logits) except where an activation lands on
-an int8 rounding boundary: the GPU's reduction order (RMSNorm, matvec sums)
-differs from the oracle's sequential sums by ~1e-6 relative, which can move one
-element across a .5 boundary and change it by one quantum.  At hidden 256 one
-such flip at the final norm shifts the logits by ~5e-3 relative L2 and leaves
-the carried state untouched (the next step agrees to ~1e-7 again).  The checks:
-  - most steps agree to 1e-5 (the exact-path case);
-  - every step is within 2e-2 (a few single-quantum flips at most);
-  - a step that differs is followed by agreeing steps (no state divergence);
+an int8 rounding boundary: the GPU's reduction orders (RMSNorm, matvec and
+delta-rule sums) differ from the reference's sequential sums by ~1e-6
+relative, which can move one element across a .5 boundary and change it by
+one quantum.  At hidden 256 one such flip moves that step's logits by
+4e-3 .. 2.5e-2 relative L2 (more when it happens in an early block: it then
+passes through the later blocks' quantizers), and when it lands in a cached
+quantity (a KV row, the recurrent state) it persists in later steps.
+
+test_decoder_stepwise_matches_oracle removes the carry-over: before every
+step the oracle is loaded with the GPU's state (KV caches, conv and
+delta-rule states), so each step's logits reflect that step alone:
+  - most steps agree to 1e-5 (the exact-path case: a systematic error in any
+    op would show in every step);
+  - every step is within 5e-2 (single-quantum flips at most);
   - greedy tokens agree wherever the oracle's top-2 margin is clear.
+test_decoder_free_run_tracks_oracle runs both decoders independently and
+checks that the carried differences stay at the flip level (no divergence).
 """
 import numpy as np
 import pytest
@@ -24,7 +32,26 @@ from decoder_util import OracleDecoder, make_model, small_config, upload
 pytestmark = pytest.mark.gpu
 
 
-def _run(oc, graph):
+def _gpu_state(eng, cfg, seq, pos):
+    """The engine's state of `seq` in the oracle's layouts (conv: newest first, ssm: [h][k][v])."""
+    from echohip.engine import S_CONV, S_KEYS, S_KSCALES, S_SSM, S_VALS, S_VSCALES
+
+    def get(l, kind):
+        if kind == "conv":
+            ring = eng.get_state(l, S_CONV, seq).reshape(cfg.conv_kernel, cfg.conv_dim)
+            out = np.zeros_like(ring)
+            for t in range(cfg.conv_kernel):
+                if pos - 1 - t >= 0:
+                    out[t] = ring[(pos - 1 - t) % cfg.conv_kernel]
+            return out
+        if kind == "ssm":
+            return eng.get_state(l, S_SSM, seq).reshape(cfg.ssm_heads, 128, 128).transpose(0, 2, 1)
+        which = {"k": S_KEYS, "v": S_VALS, "ks": S_KSCALES, "vs": S_VSCALES}[kind]
+        return eng.get_state(l, which, seq)
+    return get
+
+
+def _run(oc, graph, sync=False):
     from echohip.engine import Engine
     cfg = small_config(max_batch=3, max_ctx=64)
     m = make_model(cfg, seed=7)
@@ -45,6 +72,10 @@ def _run(oc, graph):
                 continue
             tok[s] = prompt[s][i] if i < len(prompt[s]) else nxt[s]
             pos[s] = i
+        if sync:
+            for s in range(3):
+                if pos[s] >= 0:
+                    ref.load_state(s, int(pos[s]), _gpu_state(eng, cfg, s, int(pos[s])))
         eng.set_inputs(tok, pos)
         eng.step(graph=graph)
         gen, gpos = eng.tokens()
@@ -63,16 +94,7 @@ def _run(oc, graph):
     return got, want, toks
 
 
-def test_decoder_matches_oracle(oc):
-    got, want, toks = _run(oc, graph=False)
-    errs = np.array([rel_l2(g, w) for g, w in zip(got, want)])
-    print("per-step logits rel_l2:", " ".join(f"{e:.1e}" for e in errs))
-    exact = errs < 1e-5
-    assert exact.mean() >= 0.75, errs
-    assert errs.max() < 2e-2, errs
-    # no divergence: the last quarter of the run is dominated by exact steps again
-    tail = exact[-len(exact) // 4:]
-    assert tail.mean() >= 0.5, errs
+def _check_tokens(toks):
     checked = 0
     for g_tok, lr in toks:
         top2 = np.sort(lr)[-2:]
@@ -80,6 +102,24 @@ def test_decoder_matches_oracle(oc):
             assert g_tok == int(np.argmax(lr))
             checked += 1
     assert checked > len(toks) // 2
+
+
+def test_decoder_stepwise_matches_oracle(oc):
+    got, want, toks = _run(oc, graph=False, sync=True)
+    errs = np.array([rel_l2(g, w) for g, w in zip(got, want)])
+    print("per-step logits rel_l2:", " ".join(f"{e:.1e}" for e in errs))
+    assert (errs < 1e-5).mean() >= 0.75, errs
+    assert errs.max() < 5e-2, errs
+    _check_tokens(toks)
+
+
+def test_decoder_free_run_tracks_oracle(oc):
+    got, want, toks = _run(oc, graph=False)
+    errs = np.array([rel_l2(g, w) for g, w in zip(got, want)])
+    print("per-step logits rel_l2:", " ".join(f"{e:.1e}" for e in errs))
+    assert (errs < 1e-5).mean() >= 0.5, errs
+    assert errs.max() < 5e-2, errs
+    _check_tokens(toks)
 
 
 def test_decoder_graph_replay_matches_eager(oc):

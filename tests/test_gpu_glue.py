@@ -1,0 +1,105 @@
+"""GPU parity of the decode-step glue ops (glue.hip, deltanet.hip k_delta_step).
+
+The glue ops produce Q8_0 activations, so they are compared after
+quantization: scales within 1e-5 relative of the oracle's, and int8 values
+equal except where a value sits on a rounding boundary, which moves it by
+exactly one quantum.  The reference sums a norm's squares sequentially in
+fp32 (engine.zig:787), whose rounding error grows like sqrt(n) ulp (~1e-6
+relative at n = 2560); the GPU's tree reduction is closer to the exact sum,
+so the two differ by that much.
+"""
+import numpy as np
+import pytest
+
+from conftest import rel_l2
+from echohip import synth
+from echohip.lib import Q8_0
+from test_gpu_kernels import dev, empty, host
+
+pytestmark = pytest.mark.gpu
+
+
+def _unpack(hip, act, M, K):
+    import torch
+    xq = empty(M * K, torch.int8)
+    xd = empty(M * K // 32, torch.float32)
+    hip.act_unpack(Q8_0, act, xq, xd, M, K)
+    return host(xq).reshape(M, K), host(xd).reshape(M, K // 32)
+
+
+def _check_q8(xq, xd, xq_r, xd_r):
+    assert np.max(np.abs(xd - xd_r) / np.maximum(np.abs(xd_r), 1e-30)) < 1e-5
+    diff = np.abs(xq.astype(np.int32) - xq_r.astype(np.int32))
+    assert diff.max() <= 1
+    assert (diff != 0).mean() < 1e-3, (diff != 0).sum()
+
+
+@pytest.mark.parametrize("M,H", [(8, 2560), (3, 256), (1, 384), (16, 128)])
+def test_rmsnorm_quant(hip, oc, M, H):
+    import torch
+    x = (3.0 * synth.normal(synth.stream_seed(1, H), M * H)).astype(np.float32).reshape(M, H)
+    w = (1.0 + 0.1 * synth.normal(synth.stream_seed(2, H), H)).astype(np.float32)
+    act = empty(hip.act_bytes(Q8_0, M, H), torch.uint8)
+    hip.rmsnorm_quant(dev(x), dev(w), act, M, H)
+    xq, xd = _unpack(hip, act, M, H)
+    for i in range(M):
+        y = np.zeros(H, np.float32)
+        oc.lib.oc_rmsnorm(x[i], w, y, H)
+        xq_r, xd_r = oc.quantize_act_q8_0(y)
+        _check_q8(xq[i], xd[i], xq_r, xd_r)
+
+
+@pytest.mark.parametrize("M,F", [(8, 9216), (2, 512), (5, 384)])
+def test_swiglu_quant(hip, oc, M, F):
+    import torch
+    gu = (2.0 * synth.normal(synth.stream_seed(3, F), M * 2 * F)).astype(np.float32).reshape(M, 2 * F)
+    act = empty(hip.act_bytes(Q8_0, M, F), torch.uint8)
+    hip.swiglu_quant(dev(gu), act, M, F)
+    xq, xd = _unpack(hip, act, M, F)
+    silu = np.vectorize(oc.lib.oc_silu, otypes=[np.float32])
+    for i in range(M):
+        y = (silu(gu[i, :F]) * gu[i, F:]).astype(np.float32)
+        xq_r, xd_r = oc.quantize_act_q8_0(y)
+        _check_q8(xq[i], xd[i], xq_r, xd_r)
+
+
+def test_delta_step_matches_unfused_ops(hip, oc):
+    """ec_delta_step == ec_glue_conv_gates -> ec_deltanet -> ec_glue_gated_norm_quant
+    over a ragged 4-step schedule (one sequence joins late, one idles)."""
+    import torch
+    n_seq, n_k, n_v, kern = 3, 2, 4, 4
+    key_dim, value_dim = 128 * n_k, 128 * n_v
+    conv_dim = 2 * key_dim + value_dim
+    Nin = conv_dim + value_dim + 2 * n_v
+    rng = np.random.default_rng(5)
+    conv_w = dev((0.5 * rng.standard_normal(kern * conv_dim)).astype(np.float32))
+    a_log = dev(np.log(1 + 15 * rng.random(n_v)).astype(np.float32))
+    dt_bias = dev((0.1 * rng.standard_normal(n_v)).astype(np.float32))
+    norm_w = dev((1 + 0.1 * rng.standard_normal(128)).astype(np.float32))
+    S0 = (0.02 * rng.standard_normal(n_seq * n_v * 128 * 128)).astype(np.float32)
+    stA, stB = dev(S0), dev(S0)
+    cA = empty(n_seq * kern * conv_dim, torch.float32)
+    cB = empty(n_seq * kern * conv_dim, torch.float32)
+    q = empty(n_seq * key_dim, torch.float32)
+    k = empty(n_seq * key_dim, torch.float32)
+    v = empty(n_seq * value_dim, torch.float32)
+    dec = empty(n_seq * n_v, torch.float32)
+    bet = empty(n_seq * n_v, torch.float32)
+    core = empty(n_seq * value_dim, torch.float32)
+    actA = empty(hip.act_bytes(Q8_0, n_seq, value_dim), torch.uint8)
+    actB = empty(hip.act_bytes(Q8_0, n_seq, value_dim), torch.uint8)
+    sched = [[0, -1, 0], [1, -1, 1], [2, 0, -1], [3, 1, 2]]
+    for step, p in enumerate(sched):
+        proj = dev(rng.standard_normal(n_seq * Nin).astype(np.float32))
+        pos = dev(np.array(p, np.int32))
+        hip.conv_gates(proj, Nin, cA, conv_w, a_log, dt_bias, q, k, v, dec, bet, pos, n_seq, n_k, n_v, kern)
+        hip.deltanet(stA, q, k, v, dec, bet, core, 1, n_seq, n_v, n_k, 128, 128, seq_pos=pos)
+        hip.gated_norm_quant(core, proj, Nin, conv_dim, norm_w, actA, n_seq, n_v)
+        hip.delta_step(proj, Nin, cB, conv_w, a_log, dt_bias, norm_w, stB, actB, pos, n_seq, n_k, n_v, kern)
+        assert np.array_equal(host(cA), host(cB)), step
+        assert rel_l2(host(stB), host(stA)) < 1e-6, step
+        xqA, xdA = _unpack(hip, actA, n_seq, value_dim)
+        xqB, xdB = _unpack(hip, actB, n_seq, value_dim)
+        for s in range(n_seq):
+            if p[s] >= 0:
+                _check_q8(xqB[s], xdB[s], xqA[s], xdA[s])
