@@ -255,6 +255,8 @@ static thread_local char g_err[512] = "";
 
 extern "C" const char* ec_last_error(void) { return g_err; }
 
+extern "C" void ec_clear_error(void) { g_err[0] = 0; }
+
 extern "C" int ec_set_error(int code, const char* msg) {
     snprintf(g_err, sizeof(g_err), "%s", msg);
     return code;
@@ -268,6 +270,14 @@ extern "C" int ec_set_hip_error(hipError_t e, const char* where) {
 extern "C" int ec_device_init(int device) {
     hipError_t e = hipSetDevice(device);
     if (e != hipSuccess) return ec_set_hip_error(e, "ec_device_init");
+    return EC_OK;
+}
+
+extern "C" int ec_copy(void* dst, const void* src, size_t bytes) {
+    if (bytes == 0) return EC_OK;
+    if (!dst || !src) return ec_set_error(EC_ERR_ARG, "ec_copy: null pointer");
+    hipError_t e = hipMemcpy(dst, src, bytes, hipMemcpyDefault);
+    if (e != hipSuccess) return ec_set_hip_error(e, "ec_copy");
     return EC_OK;
 }
 

@@ -25,6 +25,7 @@ _sz = C.c_size_t
 
 _SIGS = {
     "ec_device_init": [C.c_int],
+    "ec_copy": [_vp, _vp, _sz],
     "ec_quantize_rows": [_vp, _vp, _vp, _u32, _u32, _vp],
     "ec_repack": [C.c_int, _vp, _vp, _u32, _u32, _vp],
     "ec_quantize_act": [C.c_int, _vp, _vp, _u32, _u32, _vp],
@@ -53,6 +54,15 @@ _SIZE_FNS = {
     "ec_attn_ws_bytes": [_u32, _u32, _u32, _u32],
     "ec_attn_qa_bytes": [_u32, _u32],
 }
+
+
+def _hptr(x):
+    """Address of a numpy array, torch tensor or raw integer address."""
+    if x is None or isinstance(x, int):
+        return x
+    if hasattr(x, "ctypes"):
+        return x.ctypes.data
+    return x.data_ptr()
 
 
 class EchoHipError(RuntimeError):
@@ -180,6 +190,10 @@ class Lib:
 
     def swiglu_quant(self, gu, act, M, F, stream=None):
         self._call("ec_glue_swiglu_quant", _ptr(gu), _ptr(act), M, F, self._stream(stream))
+
+    def copy(self, dst, src, nbytes):
+        """Synchronous copy between host (numpy) and device buffers / raw addresses."""
+        self._call("ec_copy", _hptr(dst), _hptr(src), nbytes)
 
     def deltanet(self, state, q, k, v, decay, beta, out, T, n_seq, n_v, n_k, d_k, d_v, seq_pos=None, stream=None):
         self._call("ec_deltanet", _ptr(state), _ptr(q), _ptr(k), _ptr(v), _ptr(decay), _ptr(beta), _ptr(out), T,

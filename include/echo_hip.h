@@ -38,7 +38,13 @@ enum ec_status {
 enum ec_wfmt { EC_F32 = 0, EC_F16 = 1, EC_Q8_0 = 6, EC_Q2_K = 8, EC_Q4_K = 10 };
 
 const char* ec_last_error(void);
+/* Empties this thread's last-error message (the reference-signature wrappers
+ * return void, so a caller clears it before a call and reads it after). */
+void ec_clear_error(void);
 int ec_device_init(int device);
+/* Synchronous copy between any two host / device buffers (direction from the
+ * pointers), for callers without their own HIP runtime binding. */
+int ec_copy(void* dst, const void* src, size_t bytes);
 
 /* ------------------------------------------------------------------ quantizer
  * Reference per-row quantizer on device (bit-exact): scale = amax/127 (1 if the
