@@ -10,8 +10,11 @@ same decode graph, as the reference's own prefill loops tokens), then W
 warm-up and K timed greedy decode steps run as HIP-graph replays.
 
 value = 8 * K / (time of the K steps): decode tokens per second.
-roofline: the Q8_0 matvec (the dominant kernel) — algorithmic bytes of every
-matvec launch of one decode step / their HIP-event durations, vs 8 TB/s.
+roofline: the Q8_0 matvec (the dominant kernel) — algorithmic bytes of the
+129 matvec launches of one decode step / their GPU time (the step's matvecs
+replayed alone in a HIP graph between HIP events), vs 8 TB/s; traffic = HBM
+bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE
+(profiles/matvec_q8_0_traffic.txt).
 cpu_baseline: the oracle's AVX2 restatement of the reference decoder
 (fp32 activations, OpenMP over matvec rows) on this host's cores, on a short
 sample of single-sequence decode tokens with the same weights.
@@ -107,6 +110,12 @@ def main() -> int:
     ap.add_argument("--cpu-tokens", type=int, default=8, help="all-core CPU baseline sample (tokens)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch every step's kernels directly instead of replaying the captured HIP graph "
+                         "(rocprofv3 counter collection does not follow graph launches)")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="after the run, one device-to-device copy of this many MiB (a kernel of known "
+                         "traffic, for calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         sys.exit("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)")
@@ -140,7 +149,7 @@ def main() -> int:
         tok = np.array([prompts[s][t] if t < lens[s] else 0 for s in range(B)], np.int32)
         pos = np.array([t if t < lens[s] else -1 for s in range(B)], np.int32)
         eng.set_inputs(tok, pos)
-        eng.step(graph=True)
+        eng.step(graph=not args.no_graph)
         if t % 512 == 0:
             eng.sync()
             log(f"prefill step {t}/{T}")
@@ -154,14 +163,14 @@ def main() -> int:
     eng.set_inputs(gen, pos)
     ext = torch.cuda.ExternalStream(eng.stream)
     for _ in range(W):
-        eng.step(graph=True)
+        eng.step(graph=not args.no_graph)
     eng.sync()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     w0 = time.perf_counter()
     e0.record(ext)
     for _ in range(K):
-        eng.step(graph=True)
+        eng.step(graph=not args.no_graph)
     e1.record(ext)
     eng.sync()
     torch.cuda.synchronize()
@@ -173,12 +182,19 @@ def main() -> int:
     assert np.array_equal(pos2, pos + W + K)
     log(f"decode: {K} steps in {ms:.1f} ms (wall {wall * 1e3:.1f} ms) -> {value:.1f} tok/s; last tokens {gen2.tolist()}")
 
-    # ---- roofline of the dominant kernel (Q8_0 matvec), live HIP events
-    by, us = eng.profile_step()
-    mv_gbs = float(by.sum() / (us.sum() * 1e-6) / 1e9)
+    # ---- roofline of the dominant kernel (Q8_0 matvec): the step's matvecs
+    # alone, captured in a graph and replayed between HIP events on the engine stream
+    n_mv, mv_bytes, mv_us = eng.profile_matvecs(reps=20)
+    mv_gbs = mv_bytes / (mv_us * 1e-6) / 1e9
+    traffic = None
+    tf = ROOT / "profiles" / "matvec_q8_0_traffic.txt"
+    if tf.exists():  # HBM bytes of one step's matvecs measured with rocprofv3 PMC counters (see that file)
+        for ln in tf.read_text().splitlines():
+            if ln.startswith("hbm_bytes_per_step_matvecs:"):
+                traffic = round(int(ln.split(":")[1]) / n_mv)
     ctx_sum = int((pos2).sum())
     step_bytes = step_traffic_bytes(cfg, eng.weight_bytes(), ctx_sum, B)
-    log(f"matvec: {len(by)} launches/step, {by.sum() / 1e9:.3f} GB in {us.sum():.1f} us -> {mv_gbs:.0f} GB/s; "
+    log(f"matvec: {n_mv} launches/step, {mv_bytes / 1e9:.3f} GB in {mv_us:.1f} us -> {mv_gbs:.0f} GB/s; "
         f"step: {step_bytes / 1e9:.3f} GB in {ms_per_step:.3f} ms -> {step_bytes / ms_per_step / 1e6:.0f} GB/s")
 
     kernels = None
@@ -217,13 +233,23 @@ def main() -> int:
                    "step_hbm_bytes": int(step_bytes),
                    "step_hbm_frac": round(step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(mv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(mv_gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_mv_q8_0 (M=8)",
-                     "bytes_per_step": int(by.sum()), "launches_per_step": int(len(by))},
+                     "frac": round(mv_gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "k_mv_q8_0 (M=8)",
+                     "bytes_per_launch": int(round(mv_bytes / n_mv)), "avg_launch_us": round(mv_us / n_mv, 3),
+                     "bytes_per_step": int(mv_bytes), "launches_per_step": n_mv},
         "cpu_baseline": cpu,
         "kernels": kernels,
     }
     print(json.dumps(line), flush=True)
     eng.close()
+    if args.copy_calibration_mb:
+        n = args.copy_calibration_mb << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: {n} bytes read + {n} bytes written")
     return 0
 
 

@@ -447,6 +447,10 @@ static uint32_t target_waves() {
 static void plan(uint32_t n_tiles, uint32_t n_chunks, int max_gpw, int& gpw, uint32_t& nw) {
     const uint32_t want = (target_waves() + n_tiles - 1) / n_tiles;  // waves per tile wanted
     gpw = (int)((n_chunks + want - 1) / (want ? want : 1));
+    // one pass per wave where 16 waves can cover the tile's K: a second pass
+    // would issue its loads only after the first pass's compute
+    const int one_pass = (int)((n_chunks + 15) / 16);
+    if (gpw < one_pass) gpw = one_pass;
     if (gpw < 1) gpw = 1;
     if (gpw > max_gpw) gpw = max_gpw;
     nw = (n_chunks + gpw - 1) / gpw;

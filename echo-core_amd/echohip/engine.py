@@ -80,7 +80,8 @@ class Engine:
         L.ec_engine_stream.restype = vp
         L.ec_engine_weight_bytes.argtypes = [vp]
         L.ec_engine_weight_bytes.restype = C.c_size_t
-        L.ec_engine_profile_step.argtypes = [vp, u32, vp, vp, vp, C.POINTER(u32)]
+        L.ec_engine_profile_matvecs.argtypes = [vp, u32, C.POINTER(u32), C.POINTER(C.c_double),
+                                                C.POINTER(C.c_double)]
         c = _Cfg(**{f.name: getattr(cfg, f.name) for f in fields(cfg)})
         h = vp()
         self._check(L.ec_engine_create(C.byref(c), C.byref(h)), "ec_engine_create")
@@ -157,12 +158,10 @@ class Engine:
     def weight_bytes(self) -> int:
         return self.L.ec_engine_weight_bytes(self.h)
 
-    def profile_step(self, cap: int = 4096):
-        kind = np.zeros(cap, np.int32)
-        by = np.zeros(cap, np.float64)
-        us = np.zeros(cap, np.float64)
-        n = C.c_uint32()
-        self._check(self.L.ec_engine_profile_step(self.h, cap, kind.ctypes.data, by.ctypes.data, us.ctypes.data,
-                                                  C.byref(n)), "profile_step")
-        m = min(n.value, cap)
-        return by[:m], us[:m]
+    def profile_matvecs(self, reps: int = 20):
+        """(launches per step, algorithmic bytes per step, GPU us per step) of the
+        step's matvecs replayed alone in a HIP graph (ec_engine_profile_matvecs)."""
+        n, by, us = C.c_uint32(), C.c_double(), C.c_double()
+        self._check(self.L.ec_engine_profile_matvecs(self.h, reps, C.byref(n), C.byref(by), C.byref(us)),
+                    "profile_matvecs")
+        return n.value, by.value, us.value

@@ -181,9 +181,85 @@ def run_all(hip, quick=False):
     return res
 
 
+# ---------------------------------------------------------------- PMC traffic
+# Matvec shapes of one decode step of the 4B-class hybrid decoder (M = 8 token
+# rows): (name, N output rows, K, launches per step).
+DECODE_STEP_MATVECS = [("delta_in", 12352, 2560, 24), ("delta_out", 2560, 4096, 24), ("attn_in", 6144, 2560, 8),
+                       ("attn_out", 2560, 4096, 8), ("ffn_gate_up", 18432, 2560, 32), ("ffn_down", 2560, 9216, 32),
+                       ("lm_head", 151936, 2560, 1)]
+PMC_LAUNCHES = 3
+CALIB_BYTES = 256 << 20
+
+
+def pmc_workload(hip, M=8):
+    """Launch sequence for rocprofv3 counter collection: every decode-step
+    matvec shape PMC_LAUNCHES times (eager, each launch on a different weight
+    copy of a >= 512 MB rotation), then the calibration kernels of known
+    traffic: k_stream_read of CALIB_BYTES twice (reads) and a CALIB_BYTES
+    fill twice (writes)."""
+    st = torch.cuda.current_stream().cuda_stream
+    for name, N, K, _ in DECODE_STEP_MATVECS:
+        tb = hip.tiled_bytes(L.Q8_0, N, K)
+        n_copies = max(PMC_LAUNCHES, math.ceil(ROTATE_BYTES / tb) + 1)
+        Wd = torch.empty(N * K // 32 * 34, dtype=torch.uint8, device="cuda")
+        hip.fill_random(1, Wd, N * K // 32, 0, 0.02, stream=st)
+        tiled = torch.empty((n_copies, tb), dtype=torch.uint8, device="cuda")
+        hip.repack(L.Q8_0, Wd, tiled[0], N, K, stream=st)
+        for i in range(1, n_copies):
+            tiled[i].copy_(tiled[0])
+        del Wd
+        x = torch.from_numpy(synth.activations(1, M * K)).cuda()
+        act = torch.empty(hip.act_bytes(L.Q8_0, M, K), dtype=torch.uint8, device="cuda")
+        hip.quantize_act(L.Q8_0, x, act, M, K, stream=st)
+        y = torch.empty(M * N, dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        for i in range(PMC_LAUNCHES):
+            hip.matvec(L.Q8_0, tiled[(i * 7919) % n_copies], act, y, M, N, K, stream=st)
+            torch.cuda.synchronize()
+        del tiled
+        torch.cuda.empty_cache()
+    bufs = [torch.full((CALIB_BYTES,), 1, dtype=torch.uint8, device="cuda") for _ in range(3)]
+    out = torch.zeros(4096, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    for i in range(2):
+        hip.stream_read(bufs[i], CALIB_BYTES, out, 4096, stream=st)
+        torch.cuda.synchronize()
+    for i in range(2):
+        bufs[2 - i].fill_(2)
+        torch.cuda.synchronize()
+
+
+def pmc_summary(csv_path, counter):
+    """Per-dispatch counter values of a pmc_workload run (rocprofv3
+    counter_collection.csv), assigned to the launches in order: mean KiB per
+    launch of every matvec shape and of the two calibration kernels."""
+    import csv
+    rows = [r for r in csv.DictReader(open(csv_path)) if r.get("Counter_Name") == counter]
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    mv = [float(r["Counter_Value"]) for r in rows if "k_mv_q8_0" in r["Kernel_Name"]]
+    rd = [float(r["Counter_Value"]) for r in rows if "k_stream_read" in r["Kernel_Name"]]
+    fl = [float(r["Counter_Value"]) for r in rows if "FillFunctor<unsigned char>" in r["Kernel_Name"]][-2:]
+    assert len(mv) == PMC_LAUNCHES * len(DECODE_STEP_MATVECS), len(mv)
+    res = {"counter": counter, "shapes": {}}
+    for j, (name, N, K, per_step) in enumerate(DECODE_STEP_MATVECS):
+        v = mv[j * PMC_LAUNCHES:(j + 1) * PMC_LAUNCHES]
+        res["shapes"][name] = {"N": N, "K": K, "per_step": per_step, "KiB": [round(x, 1) for x in v]}
+    res["calib_read_KiB"] = [round(x, 1) for x in rd]
+    res["calib_fill_KiB"] = [round(x, 1) for x in fl]
+    res["calib_bytes"] = CALIB_BYTES
+    return res
+
+
 if __name__ == "__main__":
     import json
-    hip = L.load()
-    r = run_all(hip)
-    for k, v in r.items():
-        print(k, json.dumps(v), flush=True)
+    import sys
+    if len(sys.argv) > 1 and sys.argv[1] == "--pmc-workload":
+        pmc_workload(L.load())
+        print("pmc workload done", flush=True)
+    elif len(sys.argv) > 3 and sys.argv[1] == "--pmc-summary":
+        print(json.dumps(pmc_summary(sys.argv[2], sys.argv[3])))
+    else:
+        hip = L.load()
+        r = run_all(hip)
+        for k, v in r.items():
+            print(k, json.dumps(v), flush=True)

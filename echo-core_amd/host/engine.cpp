@@ -97,8 +97,9 @@ struct ec_engine {
     std::vector<void*> allocs;
     size_t weight_bytes = 0;
     // profiling hooks (eager step only)
-    std::vector<hipEvent_t>* prof_ev = nullptr;
-    std::vector<double>* prof_bytes = nullptr;
+    // matvec-only recording (profiling): skip every other launch, collect bytes
+    bool mv_only = false;
+    std::vector<double>* mv_bytes = nullptr;
 };
 
 namespace {
@@ -155,22 +156,12 @@ std::vector<float> gen_vec(uint64_t seed, size_t n, double mean, double std) {
     return v;
 }
 
-// One matvec launch, optionally bracketed by profiling events.
+// One matvec launch; in profiling mode also its algorithmic bytes (weights,
+// activation bytes + scales, outputs written, and read too when accumulating).
 int mv(ec_engine* e, const Mat& m, const void* act, float* y, uint32_t ldy, int acc) {
-    if (e->prof_ev) {
-        hipEvent_t a, b;
-        EC_HIP(hipEventCreate(&a));
-        EC_HIP(hipEventCreate(&b));
-        EC_HIP(hipEventRecord(a, e->st));
-        EC_TRY(ec_matvec(EC_Q8_0, m.tiled, act, y, e->B, m.N, m.K, ldy, acc, e->st));
-        EC_HIP(hipEventRecord(b, e->st));
-        e->prof_ev->push_back(a);
-        e->prof_ev->push_back(b);
-        const double bytes = (double)gguf_bytes(m.N, m.K) + (double)e->B * (m.K + m.K / 32 * 4) +
-                             (double)e->B * m.N * 4 * (acc ? 2 : 1);
-        e->prof_bytes->push_back(bytes);
-        return EC_OK;
-    }
+    if (e->mv_bytes)
+        e->mv_bytes->push_back((double)gguf_bytes(m.N, m.K) + (double)e->B * (m.K + m.K / 32 * 4) +
+                               (double)e->B * m.N * 4 * (acc ? 2 : 1));
     return ec_matvec(EC_Q8_0, m.tiled, act, y, e->B, m.N, m.K, ldy, acc, e->st);
 }
 
@@ -179,15 +170,19 @@ int record_step(ec_engine* e) {
     const ec_engine_cfg& c = e->c;
     const uint32_t B = e->B, H = e->H, F = e->F;
     hipStream_t st = e->st;
-    EC_TRY(ec_glue_embed(e->embed, e->tok, e->x, B, H, c.vocab, st));
+#define EC_GLUE(call)                  \
+    do {                               \
+        if (!e->mv_only) EC_TRY(call); \
+    } while (0)
+    EC_GLUE(ec_glue_embed(e->embed, e->tok, e->x, B, H, c.vocab, st));
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         Layer& y = e->L[l];
-        EC_TRY(ec_glue_rmsnorm_quant(e->x, y.attn_norm, e->act_h, B, H, st));
+        EC_GLUE(ec_glue_rmsnorm_quant(e->x, y.attn_norm, e->act_h, B, H, st));
         if (!y.attn) {
             const uint32_t Nin = e->nin_delta;
             EC_TRY(mv(e, y.w_in, e->act_h, e->proj, Nin, 0));
             // conv + gates + delta rule + gated norm + quantize in one launch
-            EC_TRY(ec_delta_step(e->proj, Nin, y.conv_state, y.conv_w, y.a_log, y.dt_bias, y.ssm_norm, y.ssm_state,
+            EC_GLUE(ec_delta_step(e->proj, Nin, y.conv_state, y.conv_w, y.a_log, y.dt_bias, y.ssm_norm, y.ssm_state,
                                  e->act_v, e->pos, B, e->n_k, e->n_v, c.conv_kernel, st));
             EC_TRY(mv(e, y.w_out, e->act_v, e->x, H, 1));
         } else {
@@ -196,32 +191,33 @@ int record_step(ec_engine* e) {
             if (e->packed_attn) {
                 // rope + KV append write q as int8 pieces; attention writes the
                 // Q8_0 activation of its output for the output projection
-                EC_TRY(ec_glue_qk_rope_append(e->proj, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn, e->inv_freq,
+                EC_GLUE(ec_glue_qk_rope_append(e->proj, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn, e->inv_freq,
                                               e->pos, nullptr, e->q_packed, e->q_scales, y.keys, y.vals, y.ks, y.vs,
                                               e->ctx, B, e->seq_stride, c.max_ctx, c.n_heads, c.n_kv, c.head_dim,
                                               st));
-                EC_TRY(ec_attn_decode_packed(e->q_packed, e->q_scales, y.keys, y.vals, y.ks, y.vs, e->attn_out,
+                EC_GLUE(ec_attn_decode_packed(e->q_packed, e->q_scales, y.keys, y.vals, y.ks, y.vs, e->attn_out,
                                              e->act_q, e->ctx, B, e->seq_stride, c.n_heads, c.n_kv, c.max_ctx,
                                              e->attn_ws, st));
             } else {
-                EC_TRY(ec_glue_qk_rope_append(e->proj, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn, e->inv_freq,
+                EC_GLUE(ec_glue_qk_rope_append(e->proj, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn, e->inv_freq,
                                               e->pos, e->qbuf, nullptr, nullptr, y.keys, y.vals, y.ks, y.vs, e->ctx,
                                               B, e->seq_stride, c.max_ctx, c.n_heads, c.n_kv, c.head_dim, st));
-                EC_TRY(ec_attn_decode(e->qbuf, y.keys, y.vals, y.ks, y.vs, e->attn_out, e->ctx, B, e->seq_stride,
+                EC_GLUE(ec_attn_decode(e->qbuf, y.keys, y.vals, y.ks, y.vs, e->attn_out, e->ctx, B, e->seq_stride,
                                       c.n_heads, c.n_kv, c.head_dim, c.max_ctx, e->attn_ws, st));
-                EC_TRY(ec_quantize_act(EC_Q8_0, e->attn_out, e->act_q, B, e->q_dim, st));
+                EC_GLUE(ec_quantize_act(EC_Q8_0, e->attn_out, e->act_q, B, e->q_dim, st));
             }
             EC_TRY(mv(e, y.w_out, e->act_q, e->x, H, 1));
         }
-        EC_TRY(ec_glue_rmsnorm_quant(e->x, y.ffn_norm, e->act_h, B, H, st));
+        EC_GLUE(ec_glue_rmsnorm_quant(e->x, y.ffn_norm, e->act_h, B, H, st));
         EC_TRY(mv(e, y.w_gu, e->act_h, e->gu, 2 * F, 0));
-        EC_TRY(ec_glue_swiglu_quant(e->gu, e->act_f, B, F, st));
+        EC_GLUE(ec_glue_swiglu_quant(e->gu, e->act_f, B, F, st));
         EC_TRY(mv(e, y.w_down, e->act_f, e->x, H, 1));
     }
-    EC_TRY(ec_glue_rmsnorm_quant(e->x, e->final_norm, e->act_h, B, H, st));
+    EC_GLUE(ec_glue_rmsnorm_quant(e->x, e->final_norm, e->act_h, B, H, st));
     EC_TRY(mv(e, e->lm_head, e->act_h, e->logits, c.vocab, 0));
-    EC_TRY(ec_glue_argmax_advance(e->logits, c.vocab, e->gen, e->tok, e->pos, B, st));
+    EC_GLUE(ec_glue_argmax_advance(e->logits, c.vocab, e->gen, e->tok, e->pos, B, st));
     return EC_OK;
+#undef EC_GLUE
 }
 
 int destroy_graph(ec_engine* e) {
@@ -627,29 +623,45 @@ extern "C" void* ec_engine_stream(ec_engine* e) { return e ? (void*)e->st : null
 
 extern "C" size_t ec_engine_weight_bytes(const ec_engine* e) { return e ? e->weight_bytes : 0; }
 
-extern "C" int ec_engine_profile_step(ec_engine* e, uint32_t cap, int32_t* kind, double* bytes, double* us,
-                                      uint32_t* n) {
-    if (!e || !n) return ec_set_error(EC_ERR_ARG, "ec_engine_profile_step: bad argument");
-    std::vector<hipEvent_t> ev;
+extern "C" int ec_engine_profile_matvecs(ec_engine* e, uint32_t reps, uint32_t* launches, double* bytes_per_step,
+                                         double* us_per_step) {
+    if (!e || !launches || !bytes_per_step || !us_per_step || reps == 0)
+        return ec_set_error(EC_ERR_ARG, "ec_engine_profile_matvecs: bad argument");
     std::vector<double> by;
-    e->prof_ev = &ev;
-    e->prof_bytes = &by;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t x = nullptr;
+    hipEvent_t a = nullptr, b = nullptr;
+    EC_HIP(hipStreamSynchronize(e->st));
+    EC_HIP(hipStreamBeginCapture(e->st, hipStreamCaptureModeThreadLocal));
+    e->mv_only = true;
+    e->mv_bytes = &by;
     int rc = record_step(e);
-    e->prof_ev = nullptr;
-    e->prof_bytes = nullptr;
-    if (hipStreamSynchronize(e->st) != hipSuccess && !rc) rc = ec_set_error(EC_ERR_HIP, "profile: sync");
-    uint32_t m = 0;
-    for (size_t i = 0; i + 1 < ev.size(); i += 2) {
+    e->mv_only = false;
+    e->mv_bytes = nullptr;
+    const hipError_t ce = hipStreamEndCapture(e->st, &g);
+    if (!rc && ce != hipSuccess) rc = ec_set_hip_error_host(ce, "ec_engine_profile_matvecs: capture");
+    auto run = [&]() -> int {
+        EC_HIP(hipGraphInstantiate(&x, g, nullptr, nullptr, 0));
+        EC_HIP(hipGraphLaunch(x, e->st));  // warm-up replay
+        EC_HIP(hipEventCreate(&a));
+        EC_HIP(hipEventCreate(&b));
+        EC_HIP(hipEventRecord(a, e->st));
+        for (uint32_t r = 0; r < reps; ++r) EC_HIP(hipGraphLaunch(x, e->st));
+        EC_HIP(hipEventRecord(b, e->st));
+        EC_HIP(hipEventSynchronize(b));
         float ms = 0.0f;
-        (void)hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
-        if (m < cap) {
-            if (kind) kind[m] = 0;
-            if (bytes) bytes[m] = by[i / 2];
-            if (us) us[m] = ms * 1e3;
-        }
-        ++m;
-    }
-    for (hipEvent_t x : ev) (void)hipEventDestroy(x);
-    *n = m;
+        EC_HIP(hipEventElapsedTime(&ms, a, b));
+        *us_per_step = ms * 1e3 / reps;
+        return EC_OK;
+    };
+    if (!rc) rc = run();
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    if (x) (void)hipGraphExecDestroy(x);
+    if (g) (void)hipGraphDestroy(g);
+    *launches = (uint32_t)by.size();
+    double t = 0.0;
+    for (double v : by) t += v;
+    *bytes_per_step = t;
     return rc;
 }

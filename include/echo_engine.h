@@ -113,10 +113,16 @@ int ec_engine_get_logits(ec_engine* e, float* host, uint32_t seq);
 void* ec_engine_stream(ec_engine* e);
 /* HBM bytes of weights one decode step reads (tiled Q8_0 matrices + vectors). */
 size_t ec_engine_weight_bytes(const ec_engine* e);
-/* Per-step launch list with its matvecs timed by HIP events: fills up to
- * `cap` entries of (kind, bytes, microseconds); kind 0 = Q8_0 matvec.
- * Runs one eager step (state advances as a normal step). */
-int ec_engine_profile_step(ec_engine* e, uint32_t cap, int32_t* kind, double* bytes, double* us, uint32_t* n);
+/* Decode-step matvec timing: the step's Q8_0 matvec launches alone (same
+ * shapes, buffers and order as in the step) are captured into a separate HIP
+ * graph, replayed `reps` times between two HIP events on the engine stream.
+ * Reports the launches per step, their algorithmic bytes per step and GPU
+ * microseconds per step.  Matvecs read weights and activations and write
+ * scratch outputs only: the recurrent state, KV cache and positions are not
+ * touched, so decoding can continue afterwards (the next step recomputes the
+ * scratch). */
+int ec_engine_profile_matvecs(ec_engine* e, uint32_t reps, uint32_t* launches, double* bytes_per_step,
+                              double* us_per_step);
 
 #ifdef __cplusplus
 }
