@@ -168,6 +168,12 @@ class Reference:
         "fused_dequant_dot_q4_K": "_Z22fused_dequant_dot_q4_KPK10block_q4_KjPKf",
         "matvec_q8_0": "_Z11matvec_q8_0PKvPKfPfjj",
         "matvec_q4_K": "_Z11matvec_q4_KPKvPKfPfjj",
+        "matvec_q2_K": "_Z11matvec_q2_KPKvPKfPfjj",
+        "dequantize_q8_0_to_fp16": "_Z23dequantize_q8_0_to_fp16PKvPtm",
+        "dequantize_q4_K_to_fp16": "_Z23dequantize_q4_K_to_fp16PKvPtm",
+        "dequantize_q2_K_to_fp16": "_Z23dequantize_q2_K_to_fp16PKvPtm",
+        "matvec_fp16_fp32<1024,512>": "_Z16matvec_fp16_fp32ILj1024ELj512EEvPKtPKfPfjj",
+        "matvec_fp16_fp32<2048,1024>": "_Z16matvec_fp16_fp32ILj2048ELj1024EEvPKtPKfPfjj",
     }
 
     def __init__(self):
@@ -181,6 +187,11 @@ class Reference:
         f["fused_dequant_dot_q4_K"].restype = C.c_float
         f["matvec_q8_0"].argtypes = [_u8p, _f32p, _f32p, _u32, _u32]
         f["matvec_q4_K"].argtypes = [_u8p, _f32p, _f32p, _u32, _u32]
+        f["matvec_q2_K"].argtypes = [_u8p, _f32p, _f32p, _u32, _u32]
+        for k in ("q8_0", "q4_K", "q2_K"):
+            f[f"dequantize_{k}_to_fp16"].argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
+        for k in ("matvec_fp16_fp32<1024,512>", "matvec_fp16_fp32<2048,1024>"):
+            f[k].argtypes = [C.c_void_p, _f32p, _f32p, _u32, _u32]
 
     @staticmethod
     def available() -> bool:

@@ -24,6 +24,7 @@ from echohip import synth  # noqa: E402
 from oracle import Reference  # noqa: E402
 
 OUT = Path(__file__).resolve().parent / "kernels_golden.npz"
+LEGACY_OUT = Path(__file__).resolve().parent / "legacy_golden.npz"
 
 
 def main() -> None:
@@ -98,6 +99,46 @@ def main() -> None:
 
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes, {len(g)} arrays)")
+    legacy(f)
+
+
+def legacy(f) -> None:
+    """Q2_K matvec, the three fp16 dequantizers and the fp16 matvec templates."""
+    g: dict[str, np.ndarray] = {}
+    # Q2_K blocks as the reference reads them (src/kernels/matvec.cpp:158-162):
+    # fp16 d, fp16 dmin, 16 scale bytes, 64 bytes of 2-bit weights; 84 B / 256 weights
+    M, K = 48, 512
+    nb = K // 256
+    raw = (synth.splitmix64(synth.stream_seed(21, 0), M * nb * 84) & np.uint64(0xFF)).astype(np.uint8)
+    blocks = raw.reshape(M, nb, 84)
+    d = (np.abs(synth.normal(synth.stream_seed(21, 1), M * nb * 2)) * 0.01).astype(np.float16)
+    blocks[:, :, 0:4] = d.view(np.uint8).reshape(M, nb, 4)
+    W2 = np.ascontiguousarray(blocks.reshape(M, nb * 84))
+    x = synth.activations(22, K)
+    y0 = synth.activations(23, M)
+    y = y0.copy()
+    f["matvec_q2_K"](W2.reshape(-1), x, y, M, K)
+    g.update(q2_W=W2, q2_x=x, q2_y0=y0, q2_matvec=y)
+    gold = np.load(OUT)
+    for key, W, n in (("q8", gold["q8_W"], gold["q8_W"].shape[0] * 512),
+                      ("q4", gold["q4_W"], gold["q4_W"].shape[0] * 512), ("q2", W2, M * K)):
+        out = np.zeros(n, np.uint16)
+        src = np.ascontiguousarray(W)
+        name = {"q8": "q8_0", "q4": "q4_K", "q2": "q2_K"}[key]
+        f[f"dequantize_{name}_to_fp16"](src.ctypes.data, out.ctypes.data, n)
+        g[f"deq_{key}"] = out
+    # fp16 matvec templates (y += W x, W row-major fp16 [M][K])
+    Mf, Kf = 160, 1000
+    Wf = (synth.normal(synth.stream_seed(24, 0), Mf * Kf) * 0.05).astype(np.float16)
+    xf = synth.activations(25, Kf)
+    yf0 = synth.activations(26, Mf)
+    g.update(f16_W=Wf.view(np.uint16), f16_x=xf, f16_y0=yf0)
+    for tk, tm in ((1024, 512), (2048, 1024)):
+        y = yf0.copy()
+        f[f"matvec_fp16_fp32<{tk},{tm}>"](Wf.view(np.uint16).ctypes.data, xf, y, Mf, Kf)
+        g[f"f16_matvec_{tk}_{tm}"] = y
+    np.savez_compressed(LEGACY_OUT, **g)
+    print(f"wrote {LEGACY_OUT} ({LEGACY_OUT.stat().st_size} bytes, {len(g)} arrays)")
 
 
 if __name__ == "__main__":

@@ -3,9 +3,9 @@ include/kv_cache.h), called by its mangled names the way a program built
 against the reference's headers links to it, with host (numpy) buffers --
 staged through the device by the library -- and with device tensors.
 
-Expected values are the reference's own outputs (tests/golden/, built from the
-reference's sources) or, for the fp16 and Q2_K paths that no fixture covers,
-closed forms stated per test.  Tolerances: int8 and fp16 outputs bit-exact;
+Expected values are the reference's own outputs (tests/golden/*.npz, written
+by tests/golden/gen_golden.py from the reference's compiled kernels) or closed
+forms stated per test.  Tolerances: int8 and fp16 outputs bit-exact;
 fp32 sums within 1e-5 relative (the GPU's summation order differs from the
 reference's by fp32 rounding).
 """
@@ -16,6 +16,12 @@ from conftest import rel_l2
 from test_gpu_kernels import dev, empty, host
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def lgold():
+    from pathlib import Path
+    return np.load(Path(__file__).resolve().parent / "golden" / "legacy_golden.npz")
 
 
 @pytest.fixture(scope="module")
@@ -217,3 +223,28 @@ def test_kv_cache_fp32_mode(lg):
     lg.hip.copy(got, y.keys_fp32, got.nbytes)
     assert np.array_equal(got, np.concatenate([k, v]))
     kv.close()
+
+
+def test_q2_K_matvec_golden(lg, lgold):
+    W, x, y0 = lgold["q2_W"], lgold["q2_x"], lgold["q2_y0"]
+    y = y0.copy()
+    lg.matvec("q2_K", W, x, y, W.shape[0], x.size)
+    assert rel_l2(y, lgold["q2_matvec"]) < 1e-5
+
+
+@pytest.mark.parametrize("key,fmt", [("q8", "q8_0"), ("q4", "q4_K"), ("q2", "q2_K")])
+def test_dequantize_to_fp16_golden(lg, golden, lgold, key, fmt):
+    W = lgold["q2_W"] if key == "q2" else golden[f"{key}_W"]
+    ref = lgold[f"deq_{key}"]
+    out = np.zeros(ref.size, np.uint16)
+    lg.dequantize_to_fp16(fmt, W, out, out.size)
+    assert np.array_equal(out, ref)
+
+
+@pytest.mark.parametrize("tk,tm", [(1024, 512), (2048, 1024)])
+def test_matvec_fp16_golden(lg, lgold, tk, tm):
+    W, x, y0 = lgold["f16_W"], lgold["f16_x"], lgold["f16_y0"]
+    M, K = y0.size, x.size
+    y = y0.copy()
+    lg.matvec_fp16_fp32((tk, tm), np.ascontiguousarray(W), x, y, M, K)
+    assert rel_l2(y, lgold[f"f16_matvec_{tk}_{tm}"]) < 1e-6
