@@ -1,0 +1,404 @@
+// gemm.hip — prefill GEMM over block-quantized weights on int8 MFMA (gfx950).
+//
+// Y[m][n] (+)= sum over K of X[m][k] * W[n][k] for M tokens (prefill chunks,
+// e.g. 512), with X quantized per 32-element block by the reference quantizer
+// (src/kernels/quant.cpp:18-98) and W in the tiled decode layout (quant.hip).
+// Every 32-block product is one exact int32 (v_mfma_i32_16x16x32_i8: A = 16
+// tokens x 32 int8, B = 32 int8 x 16 weight rows); the fp32 epilogue applies
+// the block scales:
+//   Q8_0: Y += d_x[m,b] * d_w[n,b] * isum_b
+//   Q4_K: Y += d_x[m,s] * (d*sc_s * isum_s - dmin*m_s * xsum_s)   (per sub-block s)
+// which is the reference's matvec arithmetic (matvec.cpp:62-142) on the
+// quantized activations, in a different summation order.
+//
+// Activation layout ("XT"), tokens in tiles of 16:
+//   Q8_0: chunk (token tile T, group G of 4 blocks) = 2048 B at (T*nG+G)*2048,
+//         lane l's 16 B at 16l (blocks 0,1) and 1024+16l (blocks 2,3), 8 B per
+//         block = x[16T + l%16][128G + 32j + 8(l/16) .. +8] (the MFMA A operand);
+//   Q4_K: chunk (T, super-block b) = 4096 B, lane l's 8 B per sub-block s at
+//         (s/2)*1024 + 16l + 8(s%2): the sub-block's elements 4g..4g+3 and
+//         16+4g..16+4g+3 (g = l/16) in the reference's Q4_K position order
+//         (so they meet the weight nibbles of the same positions);
+//   xd  fp32 [Mp][Kp/32] block scales; Q4_K adds dxs = xd * sum(block int8).
+//
+// Tiling: a 256-thread workgroup computes 64 tokens x (32*RTW) rows; each wave
+// 32 tokens (2 token tiles) x 16*RTW rows.  Per K chunk a wave loads its A and
+// B operands straight from global memory (16-byte loads, the next chunk's
+// loads issued before the current chunk's MFMAs), the workgroup stages the
+// chunk's activation scales in LDS.  The epilogue (int32 -> fp32, scale,
+// accumulate: 3 VALU ops per output element per block for Q8_0, 4 for Q4_K)
+// costs more issue slots than the MFMA itself: the kernel is VALU-bound at
+// roughly a third of the int8 MFMA peak by construction of 32-element scales.
+#include <type_traits>
+
+#include "common.hpp"
+#include "layout.hpp"
+
+namespace ec {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ long gpack2(uint32_t lo, uint32_t hi) {
+    return (long)(((uint64_t)hi << 32) | (uint64_t)lo);
+}
+
+struct XtLayout {
+    uint32_t Mp, Kp, nch;  // padded tokens, padded K, chunks per token tile
+    size_t xq_bytes, xd_off, dxs_off, total;
+};
+
+__host__ __device__ inline XtLayout xt_layout(int fmt, uint32_t M, uint32_t K) {
+    XtLayout L;
+    L.Mp = round_up(M, 16);
+    const bool q4 = fmt == EC_Q4_K;
+    L.Kp = round_up(K, q4 ? 256u : 128u);
+    L.nch = L.Kp / (q4 ? 256u : 128u);
+    L.xq_bytes = (size_t)(L.Mp / 16) * L.nch * (q4 ? 4096u : 2048u);
+    L.xd_off = (L.xq_bytes + 255) & ~(size_t)255;
+    const size_t xd = (size_t)L.Mp * (L.Kp / 32) * sizeof(float);
+    L.dxs_off = L.xd_off + ((xd + 255) & ~(size_t)255);
+    L.total = L.dxs_off + (q4 ? xd : 0);
+    return L;
+}
+
+// ----------------------------------------------------------- activation prep
+// grid (Kp/32 blocks, Mp tokens), block 32: one lane per element of a block.
+// Q8_0: block b holds x[m][32b .. 32b+32); Q4_K: sub-block s of super-block
+// b/8 holds the 32 positions pos(s, i) (reference order, oc_q4k_pos).
+template <bool Q4>
+__global__ __launch_bounds__(32) void k_gemm_quantize_x(const float* __restrict__ x, uint8_t* __restrict__ xt,
+                                                        uint32_t M, uint32_t K, uint32_t ldx, uint32_t nch,
+                                                        uint32_t nbp, size_t xd_off, size_t dxs_off) {
+    const uint32_t b = blockIdx.x, m = blockIdx.y, i = threadIdx.x;
+    uint32_t k;
+    if constexpr (Q4) {
+        const uint32_t s = b % 8;  // sub-block of super-block b/8
+        const uint32_t p = (i < 16) ? 64 * (s / 2) + 16 * (s % 2) + i : 64 * (s / 2) + 32 + 16 * (s % 2) + (i - 16);
+        k = 256 * (b / 8) + p;
+    } else {
+        k = 32 * b + i;
+    }
+    const bool real = m < M && k < K;
+    const float v = real ? x[(size_t)m * ldx + k] : 0.0f;
+    float amax = fabsf(v);
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
+    const float scale = q_scale(amax);
+    const float inv = __fdiv_rn(1.0f, scale);
+    const int8_t q = q_body(v, inv);  // a 32-element row: all elements are in whole 8-chunks
+    const uint32_t T = m / 16, r = m % 16;
+    uint8_t* dst;
+    if constexpr (Q4) {
+        // element e = i of the sub-block: lane group g and byte within the lane's 8 bytes
+        const uint32_t s = b % 8, e = i;
+        const uint32_t g = (e % 16) / 4, byte = (e < 16) ? e % 4 : 4 + e % 4;
+        const uint32_t l = r + 16 * g;
+        dst = xt + ((size_t)T * nch + b / 8) * 4096 + (s / 2) * 1024 + 16 * l + 8 * (s % 2) + byte;
+    } else {
+        const uint32_t G = b / 4, j = b % 4, g = i / 8;
+        const uint32_t l = r + 16 * g;
+        dst = xt + ((size_t)T * nch + G) * 2048 + (j / 2) * 1024 + 16 * l + 8 * (j % 2) + i % 8;
+    }
+    *dst = (uint8_t)q;
+    int sum = q;
+    if constexpr (Q4) {
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) sum += __shfl_xor(sum, o, 32);
+    }
+    if (i == 0) {
+        float* xd = (float*)(xt + xd_off);
+        xd[(size_t)m * nbp + b] = m < M ? scale : 0.0f;
+        if constexpr (Q4) ((float*)(xt + dxs_off))[(size_t)m * nbp + b] = scale * (float)sum;
+    }
+}
+
+// ------------------------------------------------------------------ Q8_0
+template <int RTW>
+__global__ __launch_bounds__(256) void k_gemm_q8_0(const uint8_t* __restrict__ W, const uint8_t* __restrict__ xt,
+                                                   float* __restrict__ y, uint32_t M, uint32_t N, uint32_t n_tt,
+                                                   uint32_t n_rt, uint32_t nG, uint32_t nbp, size_t xd_off,
+                                                   uint32_t ldy, int accumulate) {
+    constexpr int TTW = 2;
+    __shared__ float dx_s[2][4][64];  // [buffer][block j of the chunk][token of the workgroup tile]
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4;
+    const uint32_t wt = w & 1, wr = w >> 1;
+    const uint32_t tt0 = blockIdx.y * 4 + wt * TTW;
+    const uint32_t rt0 = blockIdx.x * (2 * RTW) + wr * RTW;
+    const float* xd = (const float*)(xt + xd_off);
+    const uint32_t tok = blockIdx.y * 64 + (threadIdx.x & 63), jj = threadIdx.x >> 6;  // scale staging
+
+    float acc[TTW][RTW][4];
+#pragma unroll
+    for (int t = 0; t < TTW; ++t)
+#pragma unroll
+        for (int r = 0; r < RTW; ++r)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[t][r][e] = 0.0f;
+
+    u32x4 a[2][TTW][2], b[2][RTW][2];
+    uint2 dw[2][RTW];
+    float dxv[2];
+    auto load = [&](int buf, uint32_t G) {
+#pragma unroll
+        for (int t = 0; t < TTW; ++t) {
+            const uint32_t T = min(tt0 + t, n_tt - 1);
+            const uint8_t* p = xt + ((size_t)T * nG + G) * 2048 + 16 * lane;
+            a[buf][t][0] = *(const u32x4*)p;
+            a[buf][t][1] = *(const u32x4*)(p + 1024);
+        }
+#pragma unroll
+        for (int r = 0; r < RTW; ++r) {
+            const uint32_t R = min(rt0 + r, n_rt - 1);
+            const uint8_t* p = W + ((size_t)R * nG + G) * kQ8TChunk;
+            b[buf][r][0] = *(const u32x4*)(p + 16 * lane);
+            b[buf][r][1] = *(const u32x4*)(p + 1024 + 16 * lane);
+            dw[buf][r] = *(const uint2*)(p + 2048 + 8 * (lane & 15));
+        }
+        dxv[buf] = tok < n_tt * 16 ? xd[(size_t)tok * nbp + 4 * G + jj] : 0.0f;
+    };
+
+    // register buffers are indexed by compile-time constants: the chunk loop is
+    // unrolled by two (even chunks in buffer 0, odd chunks in buffer 1)
+    auto step = [&](auto bufc, uint32_t G) {
+        constexpr int cur = decltype(bufc)::value;
+        dx_s[cur][jj][threadIdx.x & 63] = dxv[cur];
+        __syncthreads();
+        if (G + 1 < nG) load(cur ^ 1, G + 1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            long A[TTW], B[RTW];
+            float dwf[RTW];
+#pragma unroll
+            for (int t = 0; t < TTW; ++t) {
+                const u32x4 v = a[cur][t][j >> 1];
+                A[t] = (j & 1) ? gpack2(v.z, v.w) : gpack2(v.x, v.y);
+            }
+#pragma unroll
+            for (int r = 0; r < RTW; ++r) {
+                const u32x4 v = b[cur][r][j >> 1];
+                B[r] = (j & 1) ? gpack2(v.z, v.w) : gpack2(v.x, v.y);
+                const uint32_t h = (j < 2) ? dw[cur][r].x : dw[cur][r].y;
+                dwf[r] = h2f((j & 1) ? (h >> 16) : (h & 0xFFFF));
+            }
+#pragma unroll
+            for (int t = 0; t < TTW; ++t) {
+                const float4 d4 = *(const float4*)&dx_s[cur][j][(wt * TTW + t) * 16 + 4 * g];
+                const float dxe[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                for (int r = 0; r < RTW; ++r) {
+                    const v4i z = {0, 0, 0, 0};
+                    const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[t], B[r], z, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[t][r][e] = fmaf((float)c[e], dxe[e] * dwf[r], acc[t][r][e]);
+                }
+            }
+        }
+    };
+    load(0, 0);
+    for (uint32_t G = 0; G < nG; G += 2) {
+        step(std::integral_constant<int, 0>{}, G);
+        if (G + 1 < nG) step(std::integral_constant<int, 1>{}, G + 1);
+    }
+    // D[i][j]: token row 4g+e of the token tile, weight row lane%16 of the row tile
+#pragma unroll
+    for (int t = 0; t < TTW; ++t)
+#pragma unroll
+        for (int r = 0; r < RTW; ++r) {
+            const uint32_t n = 16 * (rt0 + r) + (lane & 15);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t m = 16 * (tt0 + t) + 4 * g + e;
+                if (m < M && n < N && tt0 + t < n_tt && rt0 + r < n_rt) {
+                    float* dst = y + (size_t)m * ldy + n;
+                    *dst = accumulate ? *dst + acc[t][r][e] : acc[t][r][e];
+                }
+            }
+        }
+}
+
+// ------------------------------------------------------------------ Q4_K
+__device__ __forceinline__ void q4k_sm(const uint32_t (&q)[3], int s, uint32_t& sc, uint32_t& mn) {
+    auto byte = [&](int i) -> uint32_t { return (q[i >> 2] >> (8 * (i & 3))) & 0xFFu; };
+    if (s < 4) {
+        sc = byte(s) & 63u;
+        mn = byte(s + 4) & 63u;
+    } else {
+        sc = (byte(s + 4) & 0x0Fu) | ((byte(s - 4) >> 6) << 4);
+        mn = (byte(s + 4) >> 4) | ((byte(s) >> 6) << 4);
+    }
+}
+
+template <int RTW>
+__global__ __launch_bounds__(256) void k_gemm_q4_K(const uint8_t* __restrict__ W, const uint8_t* __restrict__ xt,
+                                                   float* __restrict__ y, uint32_t M, uint32_t N, uint32_t n_tt,
+                                                   uint32_t n_rt, uint32_t nB, uint32_t nbp, size_t xd_off,
+                                                   size_t dxs_off, uint32_t ldy, int accumulate) {
+    constexpr int TTW = 2;
+    __shared__ float dx_s[2][8][64], dm_s[2][8][64];  // [buffer][sub-block][token]
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4;
+    const uint32_t wt = w & 1, wr = w >> 1;
+    const uint32_t tt0 = blockIdx.y * 4 + wt * TTW;
+    const uint32_t rt0 = blockIdx.x * (2 * RTW) + wr * RTW;
+    const float* xd = (const float*)(xt + xd_off);
+    const float* dxs = (const float*)(xt + dxs_off);
+    const uint32_t tok = blockIdx.y * 64 + (threadIdx.x & 63), sq = threadIdx.x >> 6;  // stages s = sq, sq+4
+
+    float acc[TTW][RTW][4];
+#pragma unroll
+    for (int t = 0; t < TTW; ++t)
+#pragma unroll
+        for (int r = 0; r < RTW; ++r)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[t][r][e] = 0.0f;
+
+    u32x4 a[2][TTW][4], b[2][RTW][2], hd[2][RTW];
+    float sv[2][4];
+    auto load = [&](int buf, uint32_t B) {
+#pragma unroll
+        for (int t = 0; t < TTW; ++t) {
+            const uint32_t T = min(tt0 + t, n_tt - 1);
+            const uint8_t* p = xt + ((size_t)T * nB + B) * 4096 + 16 * lane;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[buf][t][i] = *(const u32x4*)(p + 1024 * i);
+        }
+#pragma unroll
+        for (int r = 0; r < RTW; ++r) {
+            const uint32_t R = min(rt0 + r, n_rt - 1);
+            const uint8_t* p = W + ((size_t)R * nB + B) * kQ4TChunk;
+            b[buf][r][0] = *(const u32x4*)(p + 16 * lane);
+            b[buf][r][1] = *(const u32x4*)(p + 1024 + 16 * lane);
+            hd[buf][r] = *(const u32x4*)(p + 2048 + 16 * (lane & 15));
+        }
+        const bool ok = tok < n_tt * 16;
+        const size_t base = (size_t)(ok ? tok : 0) * nbp + 8 * B;
+        sv[buf][0] = ok ? xd[base + sq] : 0.0f;
+        sv[buf][1] = ok ? xd[base + sq + 4] : 0.0f;
+        sv[buf][2] = ok ? dxs[base + sq] : 0.0f;
+        sv[buf][3] = ok ? dxs[base + sq + 4] : 0.0f;
+    };
+
+    auto step = [&](auto bufc, uint32_t B) {
+        constexpr int cur = decltype(bufc)::value;
+        dx_s[cur][sq][threadIdx.x & 63] = sv[cur][0];
+        dx_s[cur][sq + 4][threadIdx.x & 63] = sv[cur][1];
+        dm_s[cur][sq][threadIdx.x & 63] = sv[cur][2];
+        dm_s[cur][sq + 4][threadIdx.x & 63] = sv[cur][3];
+        __syncthreads();
+        if (B + 1 < nB) load(cur ^ 1, B + 1);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            long A[TTW], Bq[RTW];
+            float dsc[RTW], dmn[RTW];
+#pragma unroll
+            for (int r = 0; r < RTW; ++r) {
+                const uint32_t scb[3] = {hd[cur][r].y, hd[cur][r].z, hd[cur][r].w};
+                uint32_t sc, mn;
+                q4k_sm(scb, s, sc, mn);
+                dsc[r] = h2f(hd[cur][r].x & 0xFFFF) * (float)sc;
+                dmn[r] = h2f(hd[cur][r].x >> 16) * (float)mn;
+            }
+#pragma unroll
+            for (int t = 0; t < TTW; ++t) {
+                const u32x4 v = a[cur][t][s >> 1];
+                A[t] = (s & 1) ? gpack2(v.z, v.w) : gpack2(v.x, v.y);
+            }
+#pragma unroll
+            for (int r = 0; r < RTW; ++r) {
+                const u32x4 v = b[cur][r][s >> 2];
+                const uint32_t q = (s & 3) == 0 ? v.x : (s & 3) == 1 ? v.y : (s & 3) == 2 ? v.z : v.w;
+                Bq[r] = gpack2(q & 0x0F0F0F0Fu, (q >> 4) & 0x0F0F0F0Fu);
+            }
+#pragma unroll
+            for (int t = 0; t < TTW; ++t) {
+                const int tb = (wt * TTW + t) * 16 + 4 * g;
+                const float4 d4 = *(const float4*)&dx_s[cur][s][tb];
+                const float4 m4 = *(const float4*)&dm_s[cur][s][tb];
+                const float dxe[4] = {d4.x, d4.y, d4.z, d4.w};
+                const float dme[4] = {m4.x, m4.y, m4.z, m4.w};
+#pragma unroll
+                for (int r = 0; r < RTW; ++r) {
+                    const v4i z = {0, 0, 0, 0};
+                    const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[t], Bq[r], z, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        acc[t][r][e] = fmaf((float)c[e], dxe[e] * dsc[r], acc[t][r][e]);
+                        acc[t][r][e] = fmaf(-dmn[r], dme[e], acc[t][r][e]);
+                    }
+                }
+            }
+        }
+    };
+    load(0, 0);
+    for (uint32_t B = 0; B < nB; B += 2) {
+        step(std::integral_constant<int, 0>{}, B);
+        if (B + 1 < nB) step(std::integral_constant<int, 1>{}, B + 1);
+    }
+#pragma unroll
+    for (int t = 0; t < TTW; ++t)
+#pragma unroll
+        for (int r = 0; r < RTW; ++r) {
+            const uint32_t n = 16 * (rt0 + r) + (lane & 15);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t m = 16 * (tt0 + t) + 4 * g + e;
+                if (m < M && n < N && tt0 + t < n_tt && rt0 + r < n_rt) {
+                    float* dst = y + (size_t)m * ldy + n;
+                    *dst = accumulate ? *dst + acc[t][r][e] : acc[t][r][e];
+                }
+            }
+        }
+}
+
+}  // namespace ec
+
+using namespace ec;
+
+extern "C" size_t ec_gemm_act_bytes(int fmt, uint32_t M, uint32_t K) {
+    if (fmt != EC_Q8_0 && fmt != EC_Q4_K) return 0;
+    return xt_layout(fmt, M, K).total;
+}
+
+extern "C" int ec_gemm_quantize_act(int fmt, const float* x, void* act, uint32_t M, uint32_t K, void* stream) {
+    if (M == 0) return EC_OK;
+    if (!x || !act || (fmt != EC_Q8_0 && fmt != EC_Q4_K) || K == 0 || K % 32 || (fmt == EC_Q4_K && K % 256))
+        return ec_set_error(EC_ERR_ARG, "ec_gemm_quantize_act: bad argument (Q8_0: K % 32 == 0, Q4_K: K % 256 == 0)");
+    const XtLayout L = xt_layout(fmt, M, K);
+    const uint32_t nbp = L.Kp / 32;
+    if (fmt == EC_Q8_0)
+        hipLaunchKernelGGL(k_gemm_quantize_x<false>, dim3(nbp, L.Mp), dim3(32), 0, (hipStream_t)stream, x,
+                           (uint8_t*)act, M, K, K, L.nch, nbp, L.xd_off, L.dxs_off);
+    else
+        hipLaunchKernelGGL(k_gemm_quantize_x<true>, dim3(nbp, L.Mp), dim3(32), 0, (hipStream_t)stream, x,
+                           (uint8_t*)act, M, K, K, L.nch, nbp, L.xd_off, L.dxs_off);
+    EC_CHECK_LAUNCH();
+    return EC_OK;
+}
+
+extern "C" int ec_gemm(int fmt, const void* tiled, const void* act, float* y, uint32_t M, uint32_t N, uint32_t K,
+                       uint32_t ldy, int accumulate, void* stream) {
+    if (M == 0 || N == 0) return EC_OK;
+    if (!tiled || !act || !y || ldy < N || (fmt != EC_Q8_0 && fmt != EC_Q4_K) || K == 0 ||
+        (fmt == EC_Q4_K && K % 256) || K % 32)
+        return ec_set_error(EC_ERR_ARG, "ec_gemm: bad argument");
+    const XtLayout L = xt_layout(fmt, M, K);
+    const uint32_t n_tt = L.Mp / 16, n_rt = round_up(N, 16) / 16, nbp = L.Kp / 32;
+    const uint32_t gy = (n_tt + 3) / 4;
+    // 128-row workgroups when that still gives >= 512 workgroups, else 64-row
+    const bool wide = (size_t)((n_rt + 7) / 8) * gy >= 512;
+    hipStream_t st = (hipStream_t)stream;
+    if (fmt == EC_Q8_0) {
+        if (wide)
+            hipLaunchKernelGGL(k_gemm_q8_0<4>, dim3((n_rt + 7) / 8, gy), dim3(256), 0, st, (const uint8_t*)tiled,
+                               (const uint8_t*)act, y, M, N, n_tt, n_rt, L.nch, nbp, L.xd_off, ldy, accumulate);
+        else
+            hipLaunchKernelGGL(k_gemm_q8_0<2>, dim3((n_rt + 3) / 4, gy), dim3(256), 0, st, (const uint8_t*)tiled,
+                               (const uint8_t*)act, y, M, N, n_tt, n_rt, L.nch, nbp, L.xd_off, ldy, accumulate);
+    } else {  // 64-row workgroups only: 128 rows of Q4_K operands and scales exceed the register file
+        hipLaunchKernelGGL(k_gemm_q4_K<2>, dim3((n_rt + 3) / 4, gy), dim3(256), 0, st, (const uint8_t*)tiled,
+                           (const uint8_t*)act, y, M, N, n_tt, n_rt, L.nch, nbp, L.xd_off, L.dxs_off, ldy,
+                           accumulate);
+    }
+    EC_CHECK_LAUNCH();
+    return EC_OK;
+}

@@ -165,6 +165,43 @@ def deltanet_case(hip, T=1024, n_v=32, d=128, iters=5, seed=0):
             "TFLOPs": round(tf, 2), "frac": round(tf / FP32_PEAK_TFLOPS, 4)}
 
 
+INT8_PEAK_TOPS = 5000.0
+
+
+def gemm_case(hip, fmt, N, K, M=512, iters=20, seed=0):
+    """Prefill GEMM (M tokens x N rows x K) on int8 MFMA over a >= 512 MB weight
+    rotation; reports int8 TOP/s (2*M*N*K ops) and the fraction of the dense
+    int8 MFMA peak."""
+    st = torch.cuda.current_stream().cuda_stream
+    if fmt == L.Q8_0:
+        Wd = torch.empty(N * K // 32 * 34, dtype=torch.uint8, device="cuda")
+        hip.fill_random(1, Wd, N * K // 32, seed, 0.02, stream=st)
+    else:
+        Wd = torch.from_numpy(synth.q4_K_blocks(seed, N, K)).cuda()
+    tb = hip.tiled_bytes(fmt, N, K)
+    n_copies = max(2, math.ceil(ROTATE_BYTES / tb) + 1)
+    tiled = torch.empty((n_copies, tb), dtype=torch.uint8, device="cuda")
+    hip.repack(fmt, Wd, tiled[0], N, K, stream=st)
+    for i in range(1, n_copies):
+        tiled[i].copy_(tiled[0])
+    del Wd
+    x = torch.from_numpy(synth.activations(seed + 1, M * K)).cuda()
+    act = torch.empty(hip.gemm_act_bytes(fmt, M, K), dtype=torch.uint8, device="cuda")
+    hip.gemm_quantize_act(fmt, x, act, M, K, stream=st)
+    y = torch.empty(M * N, dtype=torch.float32, device="cuda")
+
+    def launch(i, stream):
+        hip.gemm(fmt, tiled[i], act, y, M, N, K, stream=stream)
+
+    mean_us, best_us = _events_mean_us(launch, n_copies, iters)
+    ops = 2.0 * M * N * K
+    tops = ops / (mean_us * 1e-6) / 1e12
+    del tiled
+    torch.cuda.empty_cache()
+    return {"kernel": "k_gemm_q8_0" if fmt == L.Q8_0 else "k_gemm_q4_K", "M": M, "N": N, "K": K,
+            "us": round(mean_us, 2), "TOPs": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4)}
+
+
 def run_all(hip, quick=False):
     res = {}
     res["q8_0_9216x2560_m1"] = matvec_case(hip, L.Q8_0, 9216, 2560)
@@ -178,6 +215,9 @@ def run_all(hip, quick=False):
     ctxs = (synth.randint(synth.stream_seed(5, 0), 8, 128, 4096) + 128).tolist()
     res["attn_batch8"] = attention_case(hip, ctxs)
     res["deltanet_1024"] = deltanet_case(hip)
+    for fmt, tag in ((L.Q4_K, "q4_K"), (L.Q8_0, "q8_0")):
+        res[f"gemm_{tag}_512x9216x2560"] = gemm_case(hip, fmt, 9216, 2560)
+        res[f"gemm_{tag}_512x2560x9216"] = gemm_case(hip, fmt, 2560, 9216)
     return res
 
 

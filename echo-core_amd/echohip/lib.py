@@ -40,6 +40,8 @@ _SIGS = {
     "ec_attn_decode_packed": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u64, _u32, _u32, _u32, _vp, _vp],
     "ec_deltanet": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp, _vp],
     "ec_fill_random": [C.c_int, _vp, _u64, _u64, C.c_float, _u32, _vp],
+    "ec_gemm_quantize_act": [C.c_int, _vp, _vp, _u32, _u32, _vp],
+    "ec_gemm": [C.c_int, _vp, _vp, _vp, _u32, _u32, _u32, _u32, C.c_int, _vp],
     "ec_delta_step": [_vp, _u32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp],
     "ec_glue_conv_gates": [_vp, _u32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
                            _vp],
@@ -53,6 +55,7 @@ _SIZE_FNS = {
     "ec_act_bytes": [C.c_int, _u32, _u32],
     "ec_attn_ws_bytes": [_u32, _u32, _u32, _u32],
     "ec_attn_qa_bytes": [_u32, _u32],
+    "ec_gemm_act_bytes": [C.c_int, _u32, _u32],
 }
 
 
@@ -190,6 +193,16 @@ class Lib:
 
     def swiglu_quant(self, gu, act, M, F, stream=None):
         self._call("ec_glue_swiglu_quant", _ptr(gu), _ptr(act), M, F, self._stream(stream))
+
+    def gemm_act_bytes(self, fmt, M, K):
+        return self.L.ec_gemm_act_bytes(fmt, M, K)
+
+    def gemm_quantize_act(self, fmt, x, act, M, K, stream=None):
+        self._call("ec_gemm_quantize_act", fmt, _ptr(x), _ptr(act), M, K, self._stream(stream))
+
+    def gemm(self, fmt, tiled, act, y, M, N, K, ldy=None, accumulate=False, stream=None):
+        self._call("ec_gemm", fmt, _ptr(tiled), _ptr(act), _ptr(y), M, N, K, N if ldy is None else ldy,
+                   int(bool(accumulate)), self._stream(stream))
 
     def copy(self, dst, src, nbytes):
         """Synchronous copy between host (numpy) and device buffers / raw addresses."""

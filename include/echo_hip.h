@@ -108,6 +108,19 @@ int ec_kv_append(const float* k, const float* v, int8_t* keys, int8_t* vals, flo
                  const int32_t* pos, uint32_t n_seq, uint64_t seq_stride, uint32_t n_kv, uint32_t head_dim,
                  void* stream);
 
+/* ------------------------------------------------------------- prefill GEMM
+ * Y[m][n] (+)= sum_k X[m][k] * W[n][k] for M tokens (any M; prefill chunks of
+ * 512) on int8 MFMA.  ec_gemm_quantize_act quantizes X (fp32 [M][K], row
+ * stride K) per 32-element block with the reference quantizer into the tiled
+ * token layout of gemm.hip (Q4_K: per sub-block of the reference's position
+ * order); W is the tiled weight of ec_repack.  Exact int32 block dots, fp32
+ * scaling: Q8_0 Y += dx*dw*isum; Q4_K Y += dx*(d*sc*isum - dmin*m*xsum).
+ * ldy >= N; accumulate != 0 adds to Y. */
+size_t ec_gemm_act_bytes(int fmt, uint32_t M, uint32_t K);
+int ec_gemm_quantize_act(int fmt, const float* x, void* act, uint32_t M, uint32_t K, void* stream);
+int ec_gemm(int fmt, const void* tiled, const void* act, float* y, uint32_t M, uint32_t N, uint32_t K, uint32_t ldy,
+            int accumulate, void* stream);
+
 /* ------------------------------------------------------- INT8 attention decode
  * out[s][h][:] = softmax_p(q[s][h].K[p, h%n_kv] * ks / sqrt(head_dim)) . V[p, h%n_kv] * vs
  * over p < ctx[s] (ctx[s] <= 0: output zeros).  q, out: [n_seq][n_heads*head_dim].
