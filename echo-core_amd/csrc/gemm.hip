@@ -115,7 +115,7 @@ __global__ __launch_bounds__(32) void k_gemm_quantize_x(const float* __restrict_
 
 // ------------------------------------------------------------------ Q8_0
 template <int RTW>
-__global__ __launch_bounds__(256) void k_gemm_q8_0(const uint8_t* __restrict__ W, const uint8_t* __restrict__ xt,
+__global__ __launch_bounds__(256, 2) void k_gemm_q8_0(const uint8_t* __restrict__ W, const uint8_t* __restrict__ xt,
                                                    float* __restrict__ y, uint32_t M, uint32_t N, uint32_t n_tt,
                                                    uint32_t n_rt, uint32_t nG, uint32_t nbp, size_t xd_off,
                                                    uint32_t ldy, int accumulate) {
@@ -384,17 +384,13 @@ extern "C" int ec_gemm(int fmt, const void* tiled, const void* act, float* y, ui
     const XtLayout L = xt_layout(fmt, M, K);
     const uint32_t n_tt = L.Mp / 16, n_rt = round_up(N, 16) / 16, nbp = L.Kp / 32;
     const uint32_t gy = (n_tt + 3) / 4;
-    // 128-row workgroups when that still gives >= 512 workgroups, else 64-row
-    const bool wide = (size_t)((n_rt + 7) / 8) * gy >= 512;
     hipStream_t st = (hipStream_t)stream;
+    // 64 tokens x 64 rows per workgroup: with the epilogue as the bottleneck,
+    // two waves per SIMD (<= 256 registers) beat larger register tiles
     if (fmt == EC_Q8_0) {
-        if (wide)
-            hipLaunchKernelGGL(k_gemm_q8_0<4>, dim3((n_rt + 7) / 8, gy), dim3(256), 0, st, (const uint8_t*)tiled,
-                               (const uint8_t*)act, y, M, N, n_tt, n_rt, L.nch, nbp, L.xd_off, ldy, accumulate);
-        else
-            hipLaunchKernelGGL(k_gemm_q8_0<2>, dim3((n_rt + 3) / 4, gy), dim3(256), 0, st, (const uint8_t*)tiled,
-                               (const uint8_t*)act, y, M, N, n_tt, n_rt, L.nch, nbp, L.xd_off, ldy, accumulate);
-    } else {  // 64-row workgroups only: 128 rows of Q4_K operands and scales exceed the register file
+        hipLaunchKernelGGL(k_gemm_q8_0<2>, dim3((n_rt + 3) / 4, gy), dim3(256), 0, st, (const uint8_t*)tiled,
+                           (const uint8_t*)act, y, M, N, n_tt, n_rt, L.nch, nbp, L.xd_off, ldy, accumulate);
+    } else {
         hipLaunchKernelGGL(k_gemm_q4_K<2>, dim3((n_rt + 3) / 4, gy), dim3(256), 0, st, (const uint8_t*)tiled,
                            (const uint8_t*)act, y, M, N, n_tt, n_rt, L.nch, nbp, L.xd_off, L.dxs_off, ldy,
                            accumulate);
