@@ -31,29 +31,36 @@ __device__ __forceinline__ v4i mfma_i8(long a, long b) {
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
 }
 
-// Cross-wave reduction of acc[4] and the store of y / accumulate.
+// Cross-wave reduction of acc[4] and the store of y / accumulate.  Each
+// wave parks its partials in LDS; then thread s (s < 256) sums slot s over the
+// waves in wave order (deterministic) and stores it: slot s = lane*4 + r of
+// the MFMA D layout, i.e. weight row 16t + lane%16, token 4*(lane/16) + r.
 template <int R>
 __device__ __forceinline__ void reduce_store(float (&acc)[4], float* red, float* __restrict__ y, uint32_t t,
                                              uint32_t M, uint32_t N, uint32_t ldy, int accumulate) {
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    if (nw > 1) {
-        for (int r = 0; r < R; ++r) red[(w * 64 + lane) * 4 + r] = acc[r];
-        __syncthreads();
-        if (w != 0) return;
+    if (nw == 1) {
+        const uint32_t row = lane & 15, g = lane >> 4, n = 16 * t + row;
+        if (n >= N) return;
         for (int r = 0; r < R; ++r) {
-            float s = red[lane * 4 + r];
-            for (uint32_t v = 1; v < nw; ++v) s += red[(v * 64 + lane) * 4 + r];
-            acc[r] = s;
+            const uint32_t m = 4 * g + r;
+            if (m < M) {
+                float* dst = y + (size_t)m * ldy + n;
+                *dst = accumulate ? *dst + acc[r] : acc[r];
+            }
         }
+        return;
     }
-    const uint32_t row = lane & 15, g = lane >> 4, n = 16 * t + row;
-    if (n >= N) return;
-    for (int r = 0; r < R; ++r) {
-        uint32_t m = 4 * g + r;
-        if (m < M) {
-            float* dst = y + (size_t)m * ldy + n;
-            *dst = accumulate ? *dst + acc[r] : acc[r];
-        }
+    for (int r = 0; r < R; ++r) red[(w * 64 + lane) * 4 + r] = acc[r];
+    __syncthreads();
+    for (uint32_t sl = threadIdx.x; sl < 256; sl += blockDim.x) {  // slot = lane' * 4 + r'
+        const uint32_t ln = sl >> 2, r = sl & 3;
+        const uint32_t m = 4 * (ln >> 4) + r, n = 16 * t + (ln & 15);
+        if ((int)r >= R || m >= M || n >= N) continue;
+        float s = red[sl];
+        for (uint32_t v = 1; v < nw; ++v) s += red[v * 256 + sl];
+        float* dst = y + (size_t)m * ldy + n;
+        *dst = accumulate ? *dst + s : s;
     }
 }
 
