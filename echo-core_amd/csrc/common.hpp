@@ -62,6 +62,21 @@ __device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x));
 __device__ __forceinline__ float conv_ring(const float* __restrict__ st, const float* __restrict__ w, float xin,
                                            uint32_t p, uint32_t kern, uint32_t conv_dim, uint32_t c) {
     float acc = xin * w[(size_t)(kern - 1) * conv_dim + c];
+    if (kern <= 4) {
+        // all taps loaded before the first use (one memory round trip); a tap
+        // k >= kern reads slot 0 / tap 0 and is multiplied by zero
+        float sv[3], wv[3];
+#pragma unroll
+        for (uint32_t k = 1; k < 4; ++k) {
+            const bool ok = k < kern;
+            sv[k - 1] = st[(size_t)(ok ? (p + kern - k) % kern : 0) * conv_dim + c];
+            const float wk = w[(size_t)(ok ? kern - 1 - k : 0) * conv_dim + c];
+            wv[k - 1] = ok ? wk : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < 3; ++k) acc += sv[k] * wv[k];
+        return acc;
+    }
     for (uint32_t k = 1; k < kern; ++k)
         acc += st[(size_t)((p + kern - k) % kern) * conv_dim + c] * w[(size_t)(kern - 1 - k) * conv_dim + c];
     return acc;

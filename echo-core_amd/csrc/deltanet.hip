@@ -91,8 +91,8 @@ __global__ __launch_bounds__(256) void k_deltanet(float* __restrict__ state, con
 //   the delta-rule update of the head's 128x128 state, gated RMSNorm of the
 //   128 outputs and Q8_0 quantization into act (K = n_v*128).
 // grid (n_v, n_seq), block 1024: thread t owns column t/8 of the transposed
-// state S[v][k] and k-entries 16*(t%8) .. +15 (the state is loaded first, so
-// its latency overlaps the conv work).  The q/k conv state of a k-head shared
+// state S[v][k] and k-entries 32u + 4*(t%8) + e (u, e < 4); the state is
+// loaded first, so its latency overlaps the conv work.  The q/k conv state of a k-head shared
 // by rep value heads is written by the block with h % rep == 0; the others
 // only read slots that step leaves untouched.
 __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ proj, uint32_t Nin,
@@ -113,14 +113,21 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
     const uint32_t rep = n_v / n_k, qh = h / rep;
     const float* pr = proj + (size_t)s * Nin;
 
-    // state column (loaded first)
+    // state column (loaded first): thread (col, ks) holds k = 32u + 4ks + e,
+    // so each load instruction reads whole 128-byte runs of 8 columns
     const uint32_t col = t >> 3, ks = t & 7;
-    float* sp = state + (((size_t)s * n_v + h) * 128 + col) * 128 + 16 * ks;
+    float* sp = state + (((size_t)s * n_v + h) * 128 + col) * 128 + 4 * ks;
     float S[16];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-        const float4 v4 = *(const float4*)(sp + 4 * u);
+        const float4 v4 = *(const float4*)(sp + 32 * u);
         S[4 * u] = v4.x, S[4 * u + 1] = v4.y, S[4 * u + 2] = v4.z, S[4 * u + 3] = v4.w;
+    }
+    // gated-norm inputs of output channel t, loaded now rather than after the update
+    float zg = 0.0f, nwt = 0.0f;
+    if (t < 128) {
+        zg = pr[conv_dim + h * 128 + t];
+        nwt = norm_w[t];
     }
 
     // conv: threads 0..127 q channels, 128..255 k channels, 256..383 v channels; 384 gates
@@ -157,8 +164,8 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
     float kk[16], qq[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        kk[i] = k_s[16 * ks + i] * inv_k;
-        qq[i] = q_s[16 * ks + i] * inv_q;
+        kk[i] = k_s[32 * (i >> 2) + 4 * ks + (i & 3)] * inv_k;
+        qq[i] = q_s[32 * (i >> 2) + 4 * ks + (i & 3)] * inv_q;
     }
     float kvp = 0.0f;
 #pragma unroll
@@ -180,7 +187,7 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
     op += __shfl_xor(op, 2);
     op += __shfl_xor(op, 4);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) *(float4*)(sp + 4 * u) = make_float4(S[4 * u], S[4 * u + 1], S[4 * u + 2], S[4 * u + 3]);
+    for (int u = 0; u < 4; ++u) *(float4*)(sp + 32 * u) = make_float4(S[4 * u], S[4 * u + 1], S[4 * u + 2], S[4 * u + 3]);
     if (ks == 0) o_s[col] = op;
     __syncthreads();
 
@@ -195,7 +202,7 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
     if (t < 128) {
         const float rms = sqrtf((red2[0] + red2[1]) / 128.0f + 1e-6f);
         const float inv = 1.0f / rms;
-        const float val = o * inv * norm_w[t] * silu(pr[conv_dim + h * 128 + t]);
+        const float val = o * inv * nwt * silu(zg);
         store_act_q8_lane(val, act, (float*)(act + xd_off), M, value_dim / 32, s, h * 128 + t);
     }
 }
