@@ -92,9 +92,11 @@ __global__ __launch_bounds__(256) void k_deltanet(float* __restrict__ state, con
 //   128 outputs and Q8_0 quantization into act (K = n_v*128).
 // grid (n_v, n_seq), block 1024: thread t owns column t/8 of the transposed
 // state S[v][k] and k-entries 32u + 4*(t%8) + e (u, e < 4); the state is
-// loaded first, so its latency overlaps the conv work.  The q/k conv state of a k-head shared
-// by rep value heads is written by the block with h % rep == 0; the others
-// only read slots that step leaves untouched.
+// loaded first, so its latency overlaps the conv work.  The q/k conv state of
+// a k-head shared by rep value heads is written by the block with h % rep == 0;
+// the others only use slots that step leaves untouched (with kern == 4 every
+// block loads all four slots before it knows the position, and the slot being
+// rewritten is never selected).
 __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ proj, uint32_t Nin,
                                                      float* __restrict__ conv_state,
                                                      const float* __restrict__ conv_w,
@@ -107,14 +109,13 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
     __shared__ float q_s[128], k_s[128], v_s[128], o_s[128];
     __shared__ float red[4], red2[2], gate_s[2];
     const uint32_t h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
-    const int32_t p = pos[s];
-    if (p < 0) return;
     const uint32_t key_dim = n_k * 128, value_dim = n_v * 128, conv_dim = 2 * key_dim + value_dim;
     const uint32_t rep = n_v / n_k, qh = h / rep;
     const float* pr = proj + (size_t)s * Nin;
 
-    // state column (loaded first): thread (col, ks) holds k = 32u + 4ks + e,
-    // so each load instruction reads whole 128-byte runs of 8 columns
+    // Every load that does not depend on the position is issued before pos[s]
+    // arrives.  State column first: thread (col, ks) holds k = 32u + 4ks + e,
+    // so each load instruction reads whole 128-byte runs of 8 columns.
     const uint32_t col = t >> 3, ks = t & 7;
     float* sp = state + (((size_t)s * n_v + h) * 128 + col) * 128 + 4 * ks;
     float S[16];
@@ -123,20 +124,53 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
         const float4 v4 = *(const float4*)(sp + 32 * u);
         S[4 * u] = v4.x, S[4 * u + 1] = v4.y, S[4 * u + 2] = v4.z, S[4 * u + 3] = v4.w;
     }
-    // gated-norm inputs of output channel t, loaded now rather than after the update
+    // gated-norm inputs of output channel t
     float zg = 0.0f, nwt = 0.0f;
     if (t < 128) {
         zg = pr[conv_dim + h * 128 + t];
         nwt = norm_w[t];
     }
-
-    // conv: threads 0..127 q channels, 128..255 k channels, 256..383 v channels; 384 gates
+    // conv inputs: threads 0..127 q channels, 128..255 k channels, 256..383 v
+    // channels (with kern == 4 all four ring slots and taps); thread 384 the gates
     float* cst = conv_state + (size_t)s * kern * conv_dim;
+    const uint32_t part = t >> 7, i = t & 127;
+    const uint32_t c = part == 2 ? 2 * key_dim + h * 128 + i : part * key_dim + qh * 128 + i;
+    const bool ring4 = kern == 4;
+    float xin = 0.0f, r4[4] = {0.f, 0.f, 0.f, 0.f}, w4[4] = {0.f, 0.f, 0.f, 0.f};
     if (t < 384) {
-        const uint32_t part = t >> 7, i = t & 127;
-        const uint32_t c = part == 2 ? 2 * key_dim + h * 128 + i : part * key_dim + qh * 128 + i;
-        const float xin = pr[c];
-        const float a = silu(conv_ring(cst, conv_w, xin, (uint32_t)p, kern, conv_dim, c));
+        xin = pr[c];
+        if (ring4) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                r4[q] = cst[(size_t)q * conv_dim + c];
+                w4[q] = conv_w[(size_t)q * conv_dim + c];
+            }
+        }
+    }
+    float al = 0.0f, br = 0.0f, dtb = 0.0f, alog = 0.0f;
+    if (t == 384) {
+        al = pr[conv_dim + value_dim + h];
+        br = pr[conv_dim + value_dim + n_v + h];
+        dtb = dt_bias[h];
+        alog = a_log[h];
+    }
+    const int32_t p = pos[s];
+    if (p < 0) return;
+
+    if (t < 384) {
+        float acc;
+        if (ring4) {  // conv_ring's sum with the slots already in registers
+            acc = xin * w4[3];
+#pragma unroll
+            for (uint32_t k = 1; k < 4; ++k) {
+                const uint32_t q = ((uint32_t)p + 4 - k) & 3;
+                const float rv = q == 0 ? r4[0] : (q == 1 ? r4[1] : (q == 2 ? r4[2] : r4[3]));
+                acc += rv * w4[3 - k];
+            }
+        } else {
+            acc = conv_ring(cst, conv_w, xin, (uint32_t)p, kern, conv_dim, c);
+        }
+        const float a = silu(acc);
         if (part == 2 || h % rep == 0) cst[(size_t)((uint32_t)p % kern) * conv_dim + c] = xin;
         if (part == 2) {
             v_s[i] = a;
@@ -146,11 +180,9 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
             (part == 0 ? q_s : k_s)[i] = a;  // normalized after the barrier
         }
     } else if (t == 384) {
-        const float al = pr[conv_dim + value_dim + h];
-        const float br = pr[conv_dim + value_dim + n_v + h];
-        const float sp_in = al + dt_bias[h];
+        const float sp_in = al + dtb;
         const float spl = sp_in > 20.0f ? sp_in : log1pf(expf(sp_in));
-        const float g = -expf(a_log[h]) * spl;
+        const float g = -expf(alog) * spl;
         gate_s[0] = expf(g);
         gate_s[1] = 1.0f / (1.0f + expf(-br));
     }
