@@ -130,28 +130,22 @@ struct ByteStage {
 };
 
 // --------------------------------------------------------------------- Q8_0
+// One wave's share of 16-row tile t: chunks gbeg, gbeg+1, ... (GPW per pass,
+// passes gstep apart), accumulated into acc (D layout).  xs / as: the wave's
+// LDS slice for staged scales and activation bytes.
 template <int MT, bool DOTS, int GPW>
-__global__ __launch_bounds__(1024) void k_mv_q8_0(const uint8_t* __restrict__ W, const uint8_t* __restrict__ act,
-                                                  float* __restrict__ y, int32_t* __restrict__ dots, uint32_t M,
-                                                  uint32_t N, uint32_t K, uint32_t nG, uint32_t xd_off, uint32_t ldy,
-                                                  int accumulate) {
-    extern __shared__ float lds[];
+__device__ __forceinline__ void q8_0_wave(const uint8_t* __restrict__ wt, const uint8_t* __restrict__ act,
+                                          int32_t* __restrict__ dots, uint32_t t, uint32_t M, uint32_t N, uint32_t K,
+                                          uint32_t nG, uint32_t xd_off, uint32_t gbeg, uint32_t gstep, float* xs,
+                                          uint8_t* as, float (&acc)[4]) {
     constexpr int R = MT < 4 ? MT : 4;
     constexpr int S = slots<MT>();
     constexpr int NB = 4 * GPW;
-    const uint32_t t = blockIdx.x, lane = threadIdx.x & 63, row = lane & 15, g = lane >> 4;
-    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t nw = blockDim.x >> 6;
     constexpr int ACT_MAX = GPW * 128 * S;  // act bytes per wave pass (M <= S tokens)
-    float* red = lds;
-    float* xs = lds + nw * 256 + w * (NB * S + ACT_MAX / 4);
-    uint8_t* as = (uint8_t*)(xs + NB * S);
-    const uint8_t* wt = W + (size_t)t * nG * kQ8TChunk;
+    const uint32_t lane = threadIdx.x & 63, row = lane & 15, g = lane >> 4;
     const bool aval = row < M;
     const size_t act_bytes = (size_t)nG * 128 * M;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-
-    for (uint32_t G0 = w * GPW; G0 < nG; G0 += nw * GPW) {
+    for (uint32_t G0 = gbeg; G0 < nG; G0 += gstep) {
         ScaleStage<NB, S> sc;
         ByteStage<ACT_MAX> ast;
         if constexpr (!DOTS) sc.load((const float*)(act + xd_off), nG * 4, 4 * G0, M, lane);
@@ -202,6 +196,30 @@ __global__ __launch_bounds__(1024) void k_mv_q8_0(const uint8_t* __restrict__ W,
             }
         }
     }
+}
+
+// LDS floats of one wave's slice (scales + activation bytes).
+template <int MT, int GPW>
+constexpr uint32_t q8_wave_lds() { return 4 * GPW * slots<MT>() + GPW * 128 * slots<MT>() / 4; }
+
+// grid = one workgroup per 16-row tile; the tile's K range is split over the
+// nw waves of the workgroup.
+template <int MT, bool DOTS, int GPW>
+__global__ __launch_bounds__(1024) void k_mv_q8_0(const uint8_t* __restrict__ W, const uint8_t* __restrict__ act,
+                                                  float* __restrict__ y, int32_t* __restrict__ dots, uint32_t M,
+                                                  uint32_t N, uint32_t K, uint32_t nG, uint32_t xd_off, uint32_t ldy,
+                                                  int accumulate) {
+    extern __shared__ float lds[];
+    constexpr int R = MT < 4 ? MT : 4;
+    const uint32_t t = blockIdx.x;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nw = blockDim.x >> 6;
+    float* red = lds;
+    float* xs = lds + nw * 256 + w * q8_wave_lds<MT, GPW>();
+    uint8_t* as = (uint8_t*)(xs + 4 * GPW * slots<MT>());
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    q8_0_wave<MT, DOTS, GPW>(W + (size_t)t * nG * kQ8TChunk, act, dots, t, M, N, K, nG, xd_off, w * GPW, nw * GPW, xs,
+                             as, acc);
     if constexpr (!DOTS) reduce_store<R>(acc, red, y, t, M, N, ldy, accumulate);
 }
 
@@ -464,13 +482,18 @@ static void plan(uint32_t n_tiles, uint32_t n_chunks, int max_gpw, int& gpw, uin
     if (nw > 16) nw = 16;  // larger K: several passes per wave
 }
 
+// LDS per workgroup is 160 KB on gfx950: cap the waves of a workgroup so that
+// nw * (reduction slice + wave slice) fits (more passes per wave instead).
+constexpr size_t kLdsBytes = 160 * 1024;
+static uint32_t lds_cap_waves(uint32_t wave_floats) { return (uint32_t)(kLdsBytes / ((256 + wave_floats) * 4)); }
+
 template <int MT, bool DOTS, int GPW>
 static void launch_q8_g(const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N, uint32_t K,
                         uint32_t ldy, int accumulate, uint32_t nw, hipStream_t st) {
     const ActLayout L = act_layout(EC_Q8_0, M, K);
     const uint32_t nT = round_up(N, 16) / 16, nG = L.Kp / 128;
-    const size_t lds = ((size_t)nw * 256 + (size_t)nw * (4 * GPW * slots<MT>() + GPW * 128 * slots<MT>() / 4)) *
-                       sizeof(float);
+    nw = min(nw, lds_cap_waves(q8_wave_lds<MT, GPW>()));
+    const size_t lds = ((size_t)nw * 256 + (size_t)nw * q8_wave_lds<MT, GPW>()) * sizeof(float);
     hipLaunchKernelGGL((k_mv_q8_0<MT, DOTS, GPW>), dim3(nT), dim3(64 * nw), lds, st, (const uint8_t*)W,
                        (const uint8_t*)act, y, dots, M, N, K, nG, (uint32_t)L.xd_off, ldy, accumulate);
 }
@@ -496,8 +519,9 @@ static void launch_q4_g(const void* W, const void* act, float* y, int32_t* dots,
                         uint32_t ldy, int accumulate, uint32_t nw, hipStream_t st) {
     const ActLayout L = act_layout(EC_Q4_K, M, K);
     const uint32_t nT = round_up(N, 16) / 16, nB = L.Kp / 256;
-    const size_t lds =
-        ((size_t)nw * 256 + (size_t)nw * (2 * 8 * GPW * slots<MT>() + GPW * 256 * slots<MT>() / 4)) * sizeof(float);
+    const uint32_t wave_floats = 2 * 8 * GPW * slots<MT>() + GPW * 256 * slots<MT>() / 4;
+    nw = min(nw, lds_cap_waves(wave_floats));
+    const size_t lds = ((size_t)nw * 256 + (size_t)nw * wave_floats) * sizeof(float);
     hipLaunchKernelGGL((k_mv_q4_K<MT, DOTS, GPW>), dim3(nT), dim3(64 * nw), lds, st, (const uint8_t*)W,
                        (const uint8_t*)act, y, dots, M, N, K, nB, (uint32_t)L.xd_off, (uint32_t)L.dxs_off, ldy,
                        accumulate);
