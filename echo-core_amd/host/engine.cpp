@@ -91,7 +91,15 @@ struct ec_engine {
     float* q_scales = nullptr;
     bool packed_attn = false;  // int8-MFMA attention with q packed by the rope kernel
     int32_t *tok = nullptr, *pos = nullptr, *gen = nullptr, *ctx = nullptr;
+    // pinned staging for ec_engine_set_inputs: a ring of slots (tok[16],
+    // pos[16]), each reused only after the event recorded behind its copies
+    // has completed, so the host never overwrites inputs a queued copy has
+    // not read yet
+    static constexpr uint32_t kIoSlots = 64;
     int32_t* h_io = nullptr;
+    hipEvent_t io_ev[kIoSlots] = {};
+    bool io_pending[kIoSlots] = {};
+    uint32_t io_next = 0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     std::vector<void*> allocs;
@@ -320,8 +328,11 @@ extern "C" int ec_engine_create(const ec_engine_cfg* cfg, ec_engine** out) {
     if (e->packed_attn && ((rc = dalloc(e, &e->q_packed, ec_attn_qa_bytes(B, c.n_heads))) ||
                            (rc = dalloc(e, &e->q_scales, (size_t)B * c.n_heads * 3))))
         return fail(rc);
-    if (hipHostMalloc((void**)&e->h_io, 4 * 16 * sizeof(int32_t)) != hipSuccess)
+    if (hipHostMalloc((void**)&e->h_io, (size_t)ec_engine::kIoSlots * 32 * sizeof(int32_t)) != hipSuccess)
         return fail(ec_set_error(EC_ERR_HIP, "ec_engine_create: pinned buffer"));
+    for (hipEvent_t& ev : e->io_ev)
+        if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess)
+            return fail(ec_set_error(EC_ERR_HIP, "ec_engine_create: event"));
     // RoPE inverse frequencies, 1/pow(base, i/head_dim) in fp32 (engine.zig:476)
     std::vector<float> inv(c.head_dim / 2);
     for (uint32_t i = 0; i < c.head_dim; i += 2)
@@ -341,6 +352,8 @@ extern "C" void ec_engine_destroy(ec_engine* e) {
     destroy_graph(e);
     for (void* p : e->allocs) (void)hipFree(p);
     if (e->h_io) (void)hipHostFree(e->h_io);
+    for (hipEvent_t ev : e->io_ev)
+        if (ev) (void)hipEventDestroy(ev);
     if (e->st) (void)hipStreamDestroy(e->st);
     delete e;
 }
@@ -566,15 +579,23 @@ extern "C" int ec_engine_set_inputs(ec_engine* e, const int32_t* tok, const int3
     if (!e || !tok || !pos || n > e->B) return ec_set_error(EC_ERR_ARG, "ec_engine_set_inputs: bad argument");
     for (uint32_t i = 0; i < e->B; ++i) {
         const bool in = i < n;
-        int32_t t = in ? tok[i] : 0;
+        const int32_t t = in ? tok[i] : 0;
         if (t < 0 || (uint32_t)t >= e->c.vocab) return ec_set_error(EC_ERR_ARG, "ec_engine_set_inputs: token id");
-        int32_t p = in ? pos[i] : -1;
+        const int32_t p = in ? pos[i] : -1;
         if (p >= 0 && (uint32_t)p >= e->c.max_ctx) return ec_set_error(EC_ERR_ARG, "ec_engine_set_inputs: KV cache full");
-        e->h_io[i] = t;
-        e->h_io[16 + i] = p;
     }
-    EC_HIP(hipMemcpyAsync(e->tok, e->h_io, e->B * 4, hipMemcpyHostToDevice, e->st));
-    EC_HIP(hipMemcpyAsync(e->pos, e->h_io + 16, e->B * 4, hipMemcpyHostToDevice, e->st));
+    const uint32_t slot = e->io_next;
+    e->io_next = (slot + 1) % ec_engine::kIoSlots;
+    if (e->io_pending[slot]) EC_HIP(hipEventSynchronize(e->io_ev[slot]));
+    int32_t* h = e->h_io + (size_t)slot * 32;
+    for (uint32_t i = 0; i < e->B; ++i) {
+        h[i] = i < n ? tok[i] : 0;
+        h[16 + i] = i < n ? pos[i] : -1;
+    }
+    EC_HIP(hipMemcpyAsync(e->tok, h, e->B * 4, hipMemcpyHostToDevice, e->st));
+    EC_HIP(hipMemcpyAsync(e->pos, h + 16, e->B * 4, hipMemcpyHostToDevice, e->st));
+    EC_HIP(hipEventRecord(e->io_ev[slot], e->st));
+    e->io_pending[slot] = true;
     return EC_OK;
 }
 

@@ -127,3 +127,44 @@ def test_decoder_graph_replay_matches_eager(oc):
     b, _, _ = _run(oc, graph=True)
     for x, y in zip(a, b):
         assert np.array_equal(x, y)
+
+
+def _teacher_forced(cfg, m, steps, sync_each):
+    """Ragged prompts fed by set_inputs + graph step with no host wait in
+    between (the host runs ahead of the GPU), or with a sync after every step."""
+    from echohip.engine import Engine
+    eng = Engine(cfg)
+    upload(eng, m)
+    eng.reset()
+    rng = np.random.default_rng(5)
+    start = [0, 3, 9]
+    prompts = [rng.integers(0, cfg.vocab, steps) for _ in range(3)]
+    for step in range(steps):
+        tok = np.zeros(3, np.int32)
+        pos = np.full(3, -1, np.int32)
+        for s in range(3):
+            if step >= start[s]:
+                tok[s] = prompts[s][step - start[s]]
+                pos[s] = step - start[s]
+        eng.set_inputs(tok, pos)
+        eng.step(graph=True)
+        if sync_each:
+            eng.sync()
+    gen, gpos = eng.tokens()
+    out = [eng.logits(s) for s in range(3)], gen, gpos
+    eng.close()
+    return out
+
+
+def test_queued_inputs_match_synchronous_feeding():
+    """Inputs staged while earlier steps are still queued on the GPU reach each
+    step intact (more steps than the engine's staging slots)."""
+    cfg = small_config(max_batch=3, max_ctx=96)
+    m = make_model(cfg, seed=9)
+    steps = 80
+    la, ga, pa = _teacher_forced(cfg, m, steps, sync_each=False)
+    lb, gb, pb = _teacher_forced(cfg, m, steps, sync_each=True)
+    assert np.array_equal(pa, pb) and pa.tolist() == [steps, steps - 3, steps - 9]
+    assert np.array_equal(ga, gb)
+    for x, y in zip(la, lb):
+        assert np.array_equal(x, y)
