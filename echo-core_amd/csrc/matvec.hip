@@ -21,6 +21,18 @@
 namespace ec {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Weight loads are streaming (each byte is used once per step): non-temporal.
+__device__ __forceinline__ uint4 ld_stream16(const uint8_t* p) {
+    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ld_stream8(const uint8_t* p) {
+    const u32x2 v = __builtin_nontemporal_load((const u32x2*)p);
+    return make_uint2(v.x, v.y);
+}
 
 __device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) {
     return (long)(((uint64_t)hi << 32) | (uint64_t)lo);
@@ -156,9 +168,9 @@ __device__ __forceinline__ void q8_0_wave(const uint8_t* __restrict__ wt, const 
         for (int u = 0; u < GPW; ++u) {
             const uint32_t G = min(G0 + u, nG - 1);
             const uint8_t* ch = wt + (size_t)G * kQ8TChunk;
-            b01[u] = *(const uint4*)(ch + lane * 16);
-            b23[u] = *(const uint4*)(ch + 1024 + lane * 16);
-            dw[u] = *(const uint2*)(ch + 2048 + row * 8);
+            b01[u] = ld_stream16(ch + lane * 16);
+            b23[u] = ld_stream16(ch + 1024 + lane * 16);
+            dw[u] = ld_stream8(ch + 2048 + row * 8);
         }
         if constexpr (!DOTS) sc.store(xs, lane);
         ast.store(as, (size_t)GPW * 128 * M, lane);
