@@ -350,6 +350,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(const uint8_t* __restrict__ qa
 // with lane = 4 dims (1 KB per wave load), and the eight wave sums are added
 // in LDS.
 constexpr uint32_t kMergeWaves = 8;
+constexpr uint32_t kMergeRegs = 8;  // chunk records per wave held in registers (contexts up to 8*8*64 = 4096)
 
 // With act != nullptr the merged rows are also quantized into the Q8_0
 // activation layout (M = n_seq rows, K = n_heads*256; quantize_act's format).
@@ -375,6 +376,14 @@ __global__ __launch_bounds__(512) void k_attn_merge(const float* __restrict__ ws
     const uint32_t nc = ((uint32_t)L + chunk - 1) / chunk;
     const float* base = ws + ((size_t)s * n_chunks_max * n_heads + h) * kRec64;
     const size_t cs = (size_t)n_heads * kRec64;
+    // the partial outputs of this wave's first kMergeRegs chunks (wv, wv+8, ...)
+    // are loaded together with the chunk maxima, before any reduction
+    float4 ov[kMergeRegs];
+#pragma unroll
+    for (int i = 0; i < (int)kMergeRegs; ++i) {
+        const uint32_t c = wv + kMergeWaves * i;
+        ov[i] = c < nc ? *(const float4*)(base + c * cs + 4 + 4 * lane) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
     float M = -INFINITY;
     for (uint32_t c = tid; c < nc; c += 512) M = fmaxf(M, base[c * cs]);
     M = wave_max(M);
@@ -393,21 +402,23 @@ __global__ __launch_bounds__(512) void k_attn_merge(const float* __restrict__ ws
     den = wave_sum(den);
     if (lane == 0) red[wv] = den;
     __syncthreads();
-    float4 a0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), a1 = a0;
-    uint32_t c = wv;
-    for (; c + kMergeWaves < nc; c += 2 * kMergeWaves) {
-        const float4 o0 = *(const float4*)(base + c * cs + 4 + 4 * lane);
-        const float4 o1 = *(const float4*)(base + (c + kMergeWaves) * cs + 4 + 4 * lane);
-        const float w0 = w_s[c], w1 = w_s[c + kMergeWaves];
-        a0.x = fmaf(w0, o0.x, a0.x), a0.y = fmaf(w0, o0.y, a0.y), a0.z = fmaf(w0, o0.z, a0.z), a0.w = fmaf(w0, o0.w, a0.w);
-        a1.x = fmaf(w1, o1.x, a1.x), a1.y = fmaf(w1, o1.y, a1.y), a1.z = fmaf(w1, o1.z, a1.z), a1.w = fmaf(w1, o1.w, a1.w);
+    // chunks in order wv, wv+8, ...: the first kMergeRegs from registers
+    float4 a0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int i = 0; i < (int)kMergeRegs; ++i) {
+        const uint32_t c = wv + kMergeWaves * i;
+        if (c < nc) {
+            const float w0 = w_s[c];
+            const float4 o0 = ov[i];
+            a0.x = fmaf(w0, o0.x, a0.x), a0.y = fmaf(w0, o0.y, a0.y), a0.z = fmaf(w0, o0.z, a0.z), a0.w = fmaf(w0, o0.w, a0.w);
+        }
     }
-    if (c < nc) {
+    for (uint32_t c = wv + kMergeWaves * kMergeRegs; c < nc; c += kMergeWaves) {
         const float4 o0 = *(const float4*)(base + c * cs + 4 + 4 * lane);
         const float w0 = w_s[c];
         a0.x = fmaf(w0, o0.x, a0.x), a0.y = fmaf(w0, o0.y, a0.y), a0.z = fmaf(w0, o0.z, a0.z), a0.w = fmaf(w0, o0.w, a0.w);
     }
-    acc_s[wv][lane] = make_float4(a0.x + a1.x, a0.y + a1.y, a0.z + a1.z, a0.w + a1.w);
+    acc_s[wv][lane] = a0;
     __syncthreads();
     if (tid < HD) {
         float dn = red[0], o = 0.0f;

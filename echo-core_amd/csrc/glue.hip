@@ -207,22 +207,26 @@ __global__ __launch_bounds__(256) void k_qk_rope_append(const float* __restrict_
     __shared__ float sh[4];
     const uint32_t HD = 256;
     const uint32_t head = blockIdx.x, s = blockIdx.y, d = threadIdx.x;
-    const int32_t p = pos[s];
-    if (head == 0 && d == 0) ctx[s] = (p >= 0 && (uint32_t)p < max_ctx) ? p + 1 : 0;
-    if (p < 0 || (uint32_t)p >= max_ctx) return;
     const float* pr = proj + (size_t)s * Nin;
     const bool is_q = head < n_heads, is_k = !is_q && head < n_heads + n_kv;
     const uint32_t off = is_q ? head * HD : (is_k ? n_heads * HD + (head - n_heads) * HD
                                                   : n_heads * HD + n_kv * HD + (head - n_heads - n_kv) * HD);
+    // inputs first: none of these loads depends on the position
+    const bool norm = (is_q && use_qn) || (is_k && use_kn);
     float val = pr[off + d];
-    if ((is_q && use_qn) || (is_k && use_kn)) {
+    const float nw = norm ? (is_q ? q_norm : k_norm)[d] : 1.0f;
+    const float ifr = (is_q || is_k) ? inv_freq[d / 2] : 0.0f;
+    const int32_t p = pos[s];
+    if (head == 0 && d == 0) ctx[s] = (p >= 0 && (uint32_t)p < max_ctx) ? p + 1 : 0;
+    if (p < 0 || (uint32_t)p >= max_ctx) return;
+    if (norm) {
         const float ss = block_sum256(val * val, sh);
         const float inv = 1.0f / sqrtf(ss / (float)HD + 1e-6f);
-        val = val * inv * (is_q ? q_norm : k_norm)[d];
+        val = val * inv * nw;
     }
     if (is_q || is_k) {
         const float other = __shfl_xor(val, 1);
-        const float ang = (float)p * inv_freq[d / 2];
+        const float ang = (float)p * ifr;
         float sn, cs;
         sincosf(ang, &sn, &cs);
         val = (d & 1) ? other * sn + val * cs : val * cs - other * sn;
