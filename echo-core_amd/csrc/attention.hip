@@ -267,14 +267,14 @@ __global__ __launch_bounds__(64) void k_attn_mfma(const uint8_t* __restrict__ qa
         const uint32_t t = 16 * st + r16;
         const int8_t* kr = kb + (size_t)(c0 + (t < ntok ? t : 0)) * row + 16 * gq;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) kw[st][i] = *(const u32x4*)(kr + 64 * i);
+        for (int i = 0; i < 4; ++i) kw[st][i] = __builtin_nontemporal_load((const u32x4*)(kr + 64 * i));
     }
     // V: instruction j brings positions 4j .. 4j+3 (256 bytes each, lane = 16 bytes)
     u32x4 vv[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
         const uint32_t t = 4 * j + (lane >> 4);
-        vv[j] = *(const u32x4*)(vb + (size_t)(c0 + (t < ntok ? t : 0)) * row + 16 * (lane & 15));
+        vv[j] = __builtin_nontemporal_load((const u32x4*)(vb + (size_t)(c0 + (t < ntok ? t : 0)) * row + 16 * (lane & 15)));
     }
 
     // ---- scores: 8 accumulating MFMAs per 16 positions; C row r = 4*gq + c

@@ -18,6 +18,8 @@
 
 namespace ec {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 struct DnIn {
     float4 q0, q1, k0, k1;
     float v, dec, bt;
@@ -121,7 +123,7 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
     float S[16];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-        const float4 v4 = *(const float4*)(sp + 32 * u);
+        const f32x4 v4 = __builtin_nontemporal_load((const f32x4*)(sp + 32 * u));
         S[4 * u] = v4.x, S[4 * u + 1] = v4.y, S[4 * u + 2] = v4.z, S[4 * u + 3] = v4.w;
     }
     // gated-norm inputs of output channel t
@@ -219,7 +221,10 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
     op += __shfl_xor(op, 2);
     op += __shfl_xor(op, 4);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) *(float4*)(sp + 32 * u) = make_float4(S[4 * u], S[4 * u + 1], S[4 * u + 2], S[4 * u + 3]);
+    for (int u = 0; u < 4; ++u) {
+        const f32x4 v4 = {S[4 * u], S[4 * u + 1], S[4 * u + 2], S[4 * u + 3]};
+        __builtin_nontemporal_store(v4, (f32x4*)(sp + 32 * u));
+    }
     if (ks == 0) o_s[col] = op;
     __syncthreads();
 
