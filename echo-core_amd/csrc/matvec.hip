@@ -283,9 +283,9 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
         for (int u = 0; u < GPW; ++u) {
             const uint32_t b = min(B0 + u, nB - 1);
             const uint8_t* ch = wt + (size_t)b * kQ4TChunk;
-            q0[u] = *(const uint4*)(ch + lane * 16);
-            q1[u] = *(const uint4*)(ch + 1024 + lane * 16);
-            hdr[u] = *(const uint4*)(ch + 2048 + row * 16);
+            q0[u] = ld_stream16(ch + lane * 16);
+            q1[u] = ld_stream16(ch + 1024 + lane * 16);
+            hdr[u] = ld_stream16(ch + 2048 + row * 16);
         }
         if constexpr (!DOTS) {
             sd.store(xs, lane);

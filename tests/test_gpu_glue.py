@@ -34,7 +34,7 @@ def _check_q8(xq, xd, xq_r, xd_r):
     assert (diff != 0).mean() < 1e-3, (diff != 0).sum()
 
 
-@pytest.mark.parametrize("M,H", [(8, 2560), (3, 256), (1, 384), (16, 128)])
+@pytest.mark.parametrize("M,H", [(8, 2560), (3, 256), (1, 384), (16, 128), (2, 5120)])
 def test_rmsnorm_quant(hip, oc, M, H):
     import torch
     x = (3.0 * synth.normal(synth.stream_seed(1, H), M * H)).astype(np.float32).reshape(M, H)
