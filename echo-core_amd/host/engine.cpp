@@ -346,6 +346,12 @@ extern "C" int ec_engine_create(const ec_engine_cfg* cfg, ec_engine** out) {
     return EC_OK;
 }
 
+extern "C" int ec_engine_get_config(const ec_engine* e, ec_engine_cfg* out) {
+    if (!e || !out) return ec_set_error(EC_ERR_ARG, "ec_engine_get_config: null argument");
+    *out = e->c;
+    return EC_OK;
+}
+
 extern "C" void ec_engine_destroy(ec_engine* e) {
     if (!e) return;
     if (e->st) (void)hipStreamSynchronize(e->st);

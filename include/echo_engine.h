@@ -72,6 +72,8 @@ enum ec_tensor {
 };
 
 int ec_engine_create(const ec_engine_cfg* cfg, ec_engine** out);
+/* The configuration the engine was created with. */
+int ec_engine_get_config(const ec_engine* e, ec_engine_cfg* out);
 void ec_engine_destroy(ec_engine* e);
 /* Copy one tensor from host memory (layer ignored for global tensors). */
 int ec_engine_set_tensor(ec_engine* e, int layer, int tensor, const void* host, size_t bytes);

@@ -1,6 +1,6 @@
 """The drop-in library exports what the headers in include/ declare.
 
-* C ABI (echo_hip.h, echo_engine.h): every `ec_*` function declared there is
+* C ABI (echo_hip.h, echo_engine.h, echo_gguf.h): every `ec_*` function declared there is
   found by the dynamic loader in libechohip.so (loaded with ctypes; no GPU call
   is made).
 * Reference-signature C++ interface (include/kernels/*.h, include/kv_cache.h):
@@ -28,7 +28,7 @@ pytestmark = pytest.mark.skipif(not LIB.exists(), reason="libechohip.so not buil
 
 def _declared_c_functions():
     names = set()
-    for h in ("echo_hip.h", "echo_engine.h"):
+    for h in ("echo_hip.h", "echo_engine.h", "echo_gguf.h"):
         text = (INC / h).read_text()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         names |= set(re.findall(r"^[A-Za-z_][\w\s\*]*?\b(ec_\w+)\s*\(", text, flags=re.M))
