@@ -502,7 +502,7 @@ extern "C" int ec_attn_decode(const float* q, const int8_t* keys, const int8_t* 
                               uint32_t max_ctx, void* ws, void* stream) {
     if (n_seq == 0) return EC_OK;
     if (!q || !keys || !vals || !kscales || !vscales || !out || !ctx || !ws || n_kv == 0 || n_heads % n_kv ||
-        max_ctx == 0 || seq_stride < (uint64_t)max_ctx * n_kv * head_dim)
+        max_ctx == 0 || (seq_stride != 0 && seq_stride < (uint64_t)max_ctx * n_kv * head_dim))
         return ec_set_error(EC_ERR_ARG, "ec_attn_decode: bad argument");
     const uint32_t G = n_heads / n_kv;
     const uint32_t ncm = (max_ctx + kAttnChunk - 1) / kAttnChunk;
@@ -546,7 +546,8 @@ extern "C" int ec_attn_decode_packed(const void* qa, const float* qsc, const int
                                      uint32_t n_kv, uint32_t max_ctx, void* ws, void* stream) {
     if (n_seq == 0) return EC_OK;
     if (!qa || !qsc || !keys || !vals || !kscales || !vscales || !out || !ctx || !ws || n_kv == 0 ||
-        n_heads % n_kv || max_ctx == 0 || seq_stride < (uint64_t)max_ctx * n_kv * 256 || (act_q8 && n_seq > 16))
+        n_heads % n_kv || max_ctx == 0 || (seq_stride != 0 && seq_stride < (uint64_t)max_ctx * n_kv * 256) ||
+        (act_q8 && n_seq > 16))
         return ec_set_error(EC_ERR_ARG, "ec_attn_decode_packed: bad argument");
     int rc = mfma_dispatch(n_heads / n_kv, (const uint8_t*)qa, qsc, keys, vals, kscales, vscales, out,
                            (uint8_t*)act_q8, ctx, n_seq, seq_stride, n_kv, max_ctx, (float*)ws, (hipStream_t)stream);

@@ -170,6 +170,106 @@ __global__ __launch_bounds__(128) void k_conv_gates(const float* __restrict__ pr
     (is_q ? q_out : k_out)[((size_t)s * n_k + h) * 128 + i] = a * inv;
 }
 
+// ------------------------------------- chunked prefill: conv + gates, T tokens
+// One sequence, T consecutive tokens at positions p0 .. p0+T-1 (proj rows
+// [T][Nin]).  grid (2*n_k + n_v, T), block 128: token t of one 128-channel
+// head, the same sums as k_conv_gates (conv_ring's tap order) with the taps of
+// positions >= p0 read from earlier rows of the chunk and older ones from the
+// ring.  The ring is updated afterwards by k_conv_ring_chunk.
+__global__ __launch_bounds__(128) void k_conv_gates_chunk(const float* __restrict__ proj, uint32_t Nin,
+                                                          const float* __restrict__ ring,
+                                                          const float* __restrict__ conv_w,
+                                                          const float* __restrict__ a_log,
+                                                          const float* __restrict__ dt_bias, float* __restrict__ q_out,
+                                                          float* __restrict__ k_out, float* __restrict__ v_out,
+                                                          float* __restrict__ dec, float* __restrict__ beta,
+                                                          uint32_t p0, uint32_t n_k, uint32_t n_v, uint32_t kern) {
+    __shared__ float sh[2];
+    const uint32_t hb = blockIdx.x, t = blockIdx.y, i = threadIdx.x;
+    const uint32_t key_dim = n_k * 128, value_dim = n_v * 128, conv_dim = 2 * key_dim + value_dim;
+    const float* pr = proj + (size_t)t * Nin;
+    const uint32_t c = hb * 128 + i;
+    const uint32_t p = p0 + t;
+    float acc = pr[c] * conv_w[(size_t)(kern - 1) * conv_dim + c];
+    for (uint32_t k = 1; k < kern; ++k) {
+        float x = 0.0f;
+        if (k <= t) x = proj[(size_t)(t - k) * Nin + c];
+        else if (k <= p) x = ring[(size_t)((p - k) % kern) * conv_dim + c];
+        acc += x * conv_w[(size_t)(kern - 1 - k) * conv_dim + c];
+    }
+    const float a = silu(acc);
+    if (c >= 2 * key_dim) {  // v head
+        const uint32_t h = hb - 2 * n_k;
+        v_out[((size_t)t * n_v + h) * 128 + i] = a;
+        if (i == 0) {
+            const float al = pr[conv_dim + value_dim + h];
+            const float br = pr[conv_dim + value_dim + n_v + h];
+            const float sp_in = al + dt_bias[h];
+            const float sp = sp_in > 20.0f ? sp_in : log1pf(expf(sp_in));
+            const float g = -expf(a_log[h]) * sp;
+            dec[(size_t)t * n_v + h] = expf(g);
+            beta[(size_t)t * n_v + h] = 1.0f / (1.0f + expf(-br));
+        }
+        return;
+    }
+    const float ss = wave_sum(a * a);
+    if ((i & 63) == 0) sh[i >> 6] = ss;
+    __syncthreads();
+    const float inv = 1.0f / sqrtf((sh[0] + sh[1]) + 1e-6f);
+    const bool is_q = c < key_dim;
+    const uint32_t h = is_q ? hb : hb - n_k;
+    (is_q ? q_out : k_out)[((size_t)t * n_k + h) * 128 + i] = a * inv;
+}
+
+// Ring update after a chunk: the inputs of the last min(T, kern) positions.
+// grid (ceil(conv_dim/256), min(T, kern)), block 256.
+__global__ __launch_bounds__(256) void k_conv_ring_chunk(const float* __restrict__ proj, uint32_t Nin,
+                                                         float* __restrict__ ring, uint32_t conv_dim, uint32_t T,
+                                                         uint32_t p0, uint32_t kern) {
+    const uint32_t c = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t t = T - 1 - blockIdx.y;  // chunk row
+    if (c >= conv_dim) return;
+    ring[(size_t)((p0 + t) % kern) * conv_dim + c] = proj[(size_t)t * Nin + c];
+}
+
+// --------------------------------------------- fp32 row ops (chunked prefill)
+// RMSNorm rows: y[i] = x[i] * 1/sqrt(mean(x[i]^2) + 1e-6) * w.  grid (M), block 256.
+__global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* __restrict__ x, const float* __restrict__ w,
+                                                      float* __restrict__ y, uint32_t H) {
+    __shared__ float sh[4];
+    const uint32_t i = blockIdx.x;
+    const float* xr = x + (size_t)i * H;
+    float ss = 0.0f;
+    for (uint32_t k = threadIdx.x; k < H; k += 256) ss = fmaf(xr[k], xr[k], ss);
+    ss = block_sum256(ss, sh);
+    const float inv = 1.0f / sqrtf(ss / (float)H + 1e-6f);
+    for (uint32_t k = threadIdx.x; k < H; k += 256) y[(size_t)i * H + k] = xr[k] * inv * w[k];
+}
+
+// SwiGLU rows: gu [M][2F] (gate | up) -> y [M][F].  grid (ceil(F/256), M).
+__global__ __launch_bounds__(256) void k_swiglu_rows(const float* __restrict__ gu, float* __restrict__ y, uint32_t F) {
+    const uint32_t i = blockIdx.y, k = blockIdx.x * 256 + threadIdx.x;
+    if (k >= F) return;
+    const float* g = gu + (size_t)i * 2 * F;
+    y[(size_t)i * F + k] = silu(g[k]) * g[F + k];
+}
+
+// Gated RMSNorm rows: core [M][n_v][128] -> y [M][n_v*128] (k_gated_norm_quant's
+// value before quantization).  grid (n_v, M), block 128.
+__global__ __launch_bounds__(128) void k_gated_norm_rows(const float* __restrict__ core, const float* __restrict__ proj,
+                                                         uint32_t Nin, uint32_t z_off, const float* __restrict__ norm_w,
+                                                         float* __restrict__ y, uint32_t n_v) {
+    __shared__ float sh[2];
+    const uint32_t h = blockIdx.x, s = blockIdx.y, i = threadIdx.x;
+    const float o = core[((size_t)s * n_v + h) * 128 + i];
+    const float ss = wave_sum(o * o);
+    if ((i & 63) == 0) sh[i >> 6] = ss;
+    __syncthreads();
+    const float rms = sqrtf((sh[0] + sh[1]) / 128.0f + 1e-6f);
+    const float inv = 1.0f / rms;
+    y[((size_t)s * n_v + h) * 128 + i] = o * inv * norm_w[i] * silu(proj[(size_t)s * Nin + z_off + h * 128 + i]);
+}
+
 // ------------------------------------------------ gated RMSNorm + quantize
 // grid (n_v, M), block 128: core [M][n_v][128], z at proj[s][z_off + h*128 + i]
 // -> act (K = n_v*128).  The head's 128 outputs are 4 whole 32-blocks.
@@ -363,6 +463,43 @@ extern "C" int ec_glue_conv_gates(const float* proj, uint32_t Nin, float* conv_s
                    conv_state, conv_w, a_log, dt_bias, q, k, v, dec, beta, pos, n_k, n_v, kern);
 }
 
+extern "C" int ec_glue_conv_gates_chunk(const float* proj, uint32_t Nin, float* ring, const float* conv_w,
+                                        const float* a_log, const float* dt_bias, float* q, float* k, float* v,
+                                        float* dec, float* beta, uint32_t T, uint32_t p0, uint32_t n_k, uint32_t n_v,
+                                        uint32_t kern, void* stream) {
+    if (T == 0) return EC_OK;
+    if (!proj || !ring || !conv_w || !a_log || !dt_bias || !q || !k || !v || !dec || !beta || n_k == 0 || n_v == 0 ||
+        kern == 0 || Nin < 2 * n_k * 128 + 2 * n_v * 128 + 2 * n_v)
+        return ec_set_error(EC_ERR_ARG, "ec_glue_conv_gates_chunk: bad argument");
+    const uint32_t conv_dim = 2 * n_k * 128 + n_v * 128;
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(k_conv_gates_chunk, dim3(2 * n_k + n_v, T), dim3(128), 0, st, proj, Nin, ring, conv_w, a_log,
+                       dt_bias, q, k, v, dec, beta, p0, n_k, n_v, kern);
+    EC_CHECK_LAUNCH();
+    EC_GLUE_LAUNCH(k_conv_ring_chunk, dim3((conv_dim + 255) / 256, T < kern ? T : kern), dim3(256), 0, st, proj, Nin,
+                   ring, conv_dim, T, p0, kern);
+}
+
+extern "C" int ec_glue_rmsnorm_rows(const float* x, const float* w, float* y, uint32_t M, uint32_t H, void* stream) {
+    if (M == 0) return EC_OK;
+    if (!x || !w || !y || H == 0) return ec_set_error(EC_ERR_ARG, "ec_glue_rmsnorm_rows: bad argument");
+    EC_GLUE_LAUNCH(k_rmsnorm_rows, dim3(M), dim3(256), 0, (hipStream_t)stream, x, w, y, H);
+}
+
+extern "C" int ec_glue_swiglu_rows(const float* gu, float* y, uint32_t M, uint32_t F, void* stream) {
+    if (M == 0) return EC_OK;
+    if (!gu || !y || F == 0) return ec_set_error(EC_ERR_ARG, "ec_glue_swiglu_rows: bad argument");
+    EC_GLUE_LAUNCH(k_swiglu_rows, dim3((F + 255) / 256, M), dim3(256), 0, (hipStream_t)stream, gu, y, F);
+}
+
+extern "C" int ec_glue_gated_norm_rows(const float* core, const float* proj, uint32_t Nin, uint32_t z_off,
+                                       const float* norm_w, float* y, uint32_t M, uint32_t n_v, void* stream) {
+    if (M == 0) return EC_OK;
+    if (!core || !proj || !norm_w || !y || n_v == 0) return ec_set_error(EC_ERR_ARG, "ec_glue_gated_norm_rows");
+    EC_GLUE_LAUNCH(k_gated_norm_rows, dim3(n_v, M), dim3(128), 0, (hipStream_t)stream, core, proj, Nin, z_off, norm_w,
+                   y, n_v);
+}
+
 extern "C" int ec_glue_gated_norm_quant(const float* core, const float* proj, uint32_t Nin, uint32_t z_off,
                                         const float* norm_w, void* act, uint32_t M, uint32_t n_v, void* stream) {
     if (!core || !proj || !norm_w || !act || M == 0 || M > 16) return ec_set_error(EC_ERR_ARG, "ec_glue_gated_norm");
@@ -379,7 +516,8 @@ extern "C" int ec_glue_qk_rope_append(const float* proj, uint32_t Nin, const flo
                                       void* stream) {
     if (head_dim != 256) return ec_set_error(EC_ERR_UNSUPPORTED, "ec_glue_qk_rope_append: head_dim must be 256");
     if (!proj || !inv_freq || !pos || (!q_out && !(q_packed && q_scales)) || !keys || !vals || !kscales ||
-        !vscales || !ctx || n_kv == 0 || n_heads % n_kv || seq_stride < (uint64_t)max_ctx * n_kv * head_dim)
+        !vscales || !ctx || n_kv == 0 || n_heads % n_kv ||
+        (seq_stride != 0 && seq_stride < (uint64_t)max_ctx * n_kv * head_dim))
         return ec_set_error(EC_ERR_ARG, "ec_glue_qk_rope_append: bad argument");
     EC_GLUE_LAUNCH(k_qk_rope_append, dim3(n_heads + 2 * n_kv, n_seq), dim3(256), 0, (hipStream_t)stream, proj, Nin,
                    q_norm, k_norm, use_qn, use_kn, inv_freq, pos, q_out, (uint8_t*)q_packed, q_scales, keys, vals,

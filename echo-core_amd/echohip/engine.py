@@ -73,6 +73,7 @@ class Engine:
         L.ec_engine_reset.argtypes = [vp]
         L.ec_engine_set_inputs.argtypes = [vp, vp, vp, u32]
         L.ec_engine_step.argtypes = [vp, i32]
+        L.ec_engine_prefill.argtypes = [vp, u32, vp, u32, i32]
         L.ec_engine_sync.argtypes = [vp]
         L.ec_engine_get_tokens.argtypes = [vp, vp, vp]
         L.ec_engine_get_logits.argtypes = [vp, vp, u32]
@@ -132,6 +133,11 @@ class Engine:
         p = np.ascontiguousarray(pos, np.int32)
         assert t.size == p.size
         self._check(self.L.ec_engine_set_inputs(self.h, t.ctypes.data, p.ctypes.data, t.size), "set_inputs")
+
+    def prefill(self, seq: int, tokens, pos0: int):
+        """Chunked prefill of one sequence (ec_engine_prefill): tokens at positions pos0 .. pos0+n-1."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        self._check(self.L.ec_engine_prefill(self.h, seq, t.ctypes.data, t.size, pos0), "prefill")
 
     def step(self, graph: bool = True):
         self._check(self.L.ec_engine_step(self.h, int(graph)), "step")

@@ -48,6 +48,11 @@ _SIGS = {
     "ec_glue_gated_norm_quant": [_vp, _vp, _u32, _u32, _vp, _vp, _u32, _u32, _vp],
     "ec_glue_rmsnorm_quant": [_vp, _vp, _vp, _u32, _u32, _vp],
     "ec_glue_swiglu_quant": [_vp, _vp, _u32, _u32, _vp],
+    "ec_glue_conv_gates_chunk": [_vp, _u32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32,
+                                 _vp],
+    "ec_glue_rmsnorm_rows": [_vp, _vp, _vp, _u32, _u32, _vp],
+    "ec_glue_swiglu_rows": [_vp, _vp, _u32, _u32, _vp],
+    "ec_glue_gated_norm_rows": [_vp, _vp, _u32, _u32, _vp, _vp, _u32, _u32, _vp],
     "ec_stream_read": [_vp, _sz, _vp, _u32, _vp],
 }
 _SIZE_FNS = {
@@ -186,6 +191,21 @@ class Lib:
 
     def gated_norm_quant(self, core, proj, Nin, z_off, norm_w, act, M, n_v, stream=None):
         self._call("ec_glue_gated_norm_quant", _ptr(core), _ptr(proj), Nin, z_off, _ptr(norm_w), _ptr(act), M, n_v,
+                   self._stream(stream))
+
+    def conv_gates_chunk(self, proj, Nin, ring, conv_w, a_log, dt_bias, q, k, v, dec, beta, T, p0, n_k, n_v, kern,
+                         stream=None):
+        self._call("ec_glue_conv_gates_chunk", _ptr(proj), Nin, _ptr(ring), _ptr(conv_w), _ptr(a_log), _ptr(dt_bias),
+                   _ptr(q), _ptr(k), _ptr(v), _ptr(dec), _ptr(beta), T, p0, n_k, n_v, kern, self._stream(stream))
+
+    def rmsnorm_rows(self, x, w, y, M, H, stream=None):
+        self._call("ec_glue_rmsnorm_rows", _ptr(x), _ptr(w), _ptr(y), M, H, self._stream(stream))
+
+    def swiglu_rows(self, gu, y, M, F, stream=None):
+        self._call("ec_glue_swiglu_rows", _ptr(gu), _ptr(y), M, F, self._stream(stream))
+
+    def gated_norm_rows(self, core, proj, Nin, z_off, norm_w, y, M, n_v, stream=None):
+        self._call("ec_glue_gated_norm_rows", _ptr(core), _ptr(proj), Nin, z_off, _ptr(norm_w), _ptr(y), M, n_v,
                    self._stream(stream))
 
     def rmsnorm_quant(self, x, w, act, M, H, stream=None):

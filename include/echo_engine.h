@@ -106,6 +106,14 @@ int ec_engine_init_random(ec_engine* e, uint64_t seed, float w_scale);
 int ec_engine_reset(ec_engine* e);
 /* Set this step's inputs for n <= max_batch sequences (host arrays). */
 int ec_engine_set_inputs(ec_engine* e, const int32_t* tok, const int32_t* pos, uint32_t n);
+/* Chunked prefill of one sequence: feed n tokens at positions pos0 ..
+ * pos0+n-1 (the sequence's next position; pos0 + n <= max_ctx) in chunks of up
+ * to 512 tokens, each block computed for the whole chunk (int8-MFMA GEMMs,
+ * the delta rule over the chunk's tokens, causal attention of every token over
+ * the sequence's cache).  Leaves the sequence as n decode steps would
+ * (conv/recurrent state, KV cache, position pos0 + n, greedy next token in
+ * `gen`, the last token's logits); other sequences are untouched.  Synchronous. */
+int ec_engine_prefill(ec_engine* e, uint32_t seq, const int32_t* tokens, uint32_t n, int32_t pos0);
 /* Run one decode step (graph-captured after the first call when use_graph). */
 int ec_engine_step(ec_engine* e, int use_graph);
 int ec_engine_sync(ec_engine* e);

@@ -193,6 +193,27 @@ int ec_glue_qk_rope_append(const float* proj, uint32_t Nin, const float* q_norm,
 int ec_glue_argmax_advance(const float* logits, uint32_t vocab, int32_t* gen, int32_t* next, int32_t* pos,
                            uint32_t n_seq, void* stream);
 
+/* ------------------------------------------------- chunked prefill glue
+ * T consecutive tokens of ONE sequence at positions p0 .. p0+T-1.
+ * conv_gates_chunk: as ec_glue_conv_gates for every token of the chunk (taps
+ * of positions >= p0 from earlier proj rows, older ones from the ring, whose
+ * slots are then overwritten with the chunk's last min(T, kern) inputs); ring
+ * is the sequence's [kern][conv_dim] conv state; q, k, v, dec, beta are the
+ * ec_deltanet inputs for n_seq = 1.  The _rows ops are the fp32 values of
+ * ec_glue_rmsnorm_quant / ec_glue_swiglu_quant / ec_glue_gated_norm_quant
+ * before quantization (quantize with ec_gemm_quantize_act for the GEMM).
+ * ec_glue_qk_rope_append and ec_attn_decode[_packed] with seq_stride == 0
+ * treat their n_seq slots as tokens of one sequence sharing one cache (slot s
+ * at position pos[s], attending over ctx[s] positions): causal attention of a
+ * chunk when ctx[s] = pos[s] + 1. */
+int ec_glue_conv_gates_chunk(const float* proj, uint32_t Nin, float* ring, const float* conv_w, const float* a_log,
+                             const float* dt_bias, float* q, float* k, float* v, float* dec, float* beta, uint32_t T,
+                             uint32_t p0, uint32_t n_k, uint32_t n_v, uint32_t kern, void* stream);
+int ec_glue_rmsnorm_rows(const float* x, const float* w, float* y, uint32_t M, uint32_t H, void* stream);
+int ec_glue_swiglu_rows(const float* gu, float* y, uint32_t M, uint32_t F, void* stream);
+int ec_glue_gated_norm_rows(const float* core, const float* proj, uint32_t Nin, uint32_t z_off, const float* norm_w,
+                            float* y, uint32_t M, uint32_t n_v, void* stream);
+
 /* Plain streaming read of `bytes` (multiple of 16) with `blocks` workgroups of
  * 256 threads: the HBM-bandwidth calibration used by the benchmarks. */
 int ec_stream_read(const void* src, size_t bytes, uint32_t* out, uint32_t blocks, void* stream);
