@@ -5,9 +5,11 @@ Workload: 32 blocks (24 gated-delta-net + 8 full-attention, GQA 16q/4kv,
 head_dim 256, INT8 KV), hidden 2560, FFN 9216 SwiGLU, vocab 151936, all
 matrices Q8_0 with seeded random weights generated on the device.  A ragged
 batch of 8 sequences with prompt lengths drawn uniformly from [128, 4096]
-(uniform random token ids) is prefilled (untimed; token by token through the
-same decode graph, as the reference's own prefill loops tokens), then W
-warm-up and K timed greedy decode steps run as HIP-graph replays.
+(uniform random token ids) is prefilled (chunked prefill, 512-token chunks of
+int8-MFMA GEMMs; timed separately and reported as config.prefill_tok_s, not
+part of `value`), then W warm-up and K timed greedy decode steps run as
+HIP-graph replays.  --prefill loop feeds the prompts token by token through
+the decode graph instead.
 
 value = 8 * K / (time of the K steps): decode tokens per second.
 roofline: the Q8_0 matvec (the dominant kernel) — algorithmic bytes of the
@@ -113,6 +115,8 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true",
                     help="launch every step's kernels directly instead of replaying the captured HIP graph "
                          "(rocprofv3 counter collection does not follow graph launches)")
+    ap.add_argument("--prefill", choices=("chunked", "loop"), default="chunked",
+                    help="chunked: ec_engine_prefill per sequence; loop: token by token through the decode graph")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="after the run, one device-to-device copy of this many MiB (a kernel of known "
                          "traffic, for calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -142,22 +146,35 @@ def main() -> int:
     prompts = [synth.randint(synth.stream_seed(args.seed, 2000 + s), int(lens[s]), 0, cfg.vocab - 1).astype(np.int32)
                for s in range(B)]
 
-    # ---- prefill (untimed): token loop through the decode graph, ragged
+    # ---- prefill (not part of `value`); a one-token prefill first allocates the
+    # engine's prefill buffers, then the state is reset
+    if args.prefill == "chunked":
+        eng.prefill(0, prompts[0][:1], 0)
+        eng.reset()
     t0 = time.perf_counter()
     T = int(lens.max())
-    for t in range(T):
-        tok = np.array([prompts[s][t] if t < lens[s] else 0 for s in range(B)], np.int32)
-        pos = np.array([t if t < lens[s] else -1 for s in range(B)], np.int32)
-        eng.set_inputs(tok, pos)
-        eng.step(graph=not args.no_graph)
-        if t % 512 == 0:
-            eng.sync()
-            log(f"prefill step {t}/{T}")
-    eng.sync()
+    if args.prefill == "chunked":
+        for s in range(B):
+            eng.prefill(s, prompts[s], 0)
+        eng.sync()
+    else:  # token loop through the decode graph, ragged
+        for t in range(T):
+            tok = np.array([prompts[s][t] if t < lens[s] else 0 for s in range(B)], np.int32)
+            pos = np.array([t if t < lens[s] else -1 for s in range(B)], np.int32)
+            eng.set_inputs(tok, pos)
+            eng.step(graph=not args.no_graph)
+            if t % 512 == 0:
+                eng.sync()
+                log(f"prefill step {t}/{T}")
+        eng.sync()
+    prefill_s = time.perf_counter() - t0
     gen, last_pos = eng.tokens()  # gen[s]: greedy token after sequence s's last prompt token
-    assert last_pos[int(np.argmax(lens))] == T
+    if args.prefill == "chunked":
+        assert np.array_equal(last_pos, lens)
     pos = lens.astype(np.int32)  # next position of every sequence
-    log(f"prefill {int(lens.sum())} tokens ({T} steps) in {time.perf_counter() - t0:.1f} s; prompts {lens.tolist()}")
+    prefill_tps = int(lens.sum()) / prefill_s
+    log(f"prefill ({args.prefill}) {int(lens.sum())} tokens in {prefill_s:.2f} s -> {prefill_tps:.0f} tok/s; "
+        f"prompts {lens.tolist()}")
 
     # ---- decode: warm-up then timed graph replays
     eng.set_inputs(gen, pos)
@@ -229,7 +246,9 @@ def main() -> int:
         "config": {"workload": "hybrid 4B-class Q8_0 decoder: 24 delta-net + 8 attention blocks, hidden 2560, "
                                "ffn 9216, vocab 151936; ragged batch of 8, greedy decode",
                    "global_batch": B, "prompt_lens": lens.tolist(), "decode_steps": W + K,
-                   "prefill": "token loop through the decode graph (untimed)",
+                   "prefill": ("chunked (512-token int8-MFMA GEMM chunks per sequence)" if args.prefill == "chunked"
+                               else "token loop through the decode graph"),
+                   "prefill_tok_s": round(prefill_tps, 1),
                    "step_hbm_bytes": int(step_bytes),
                    "step_hbm_frac": round(step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(mv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
