@@ -11,8 +11,8 @@
 // 4 xor-shuffle adds inside the row, no LDS and no barrier.  A wave holds 4
 // columns (2 KB of state, two 16-byte loads per lane), a 256-thread workgroup
 // 16 columns of one head.  Across the T tokens of one launch the state never
-// leaves the VGPRs; q/k/v/decay/beta for the next token are loaded while the
-// current one is computed.
+// leaves the VGPRs; the inputs (which do not depend on the recurrence) are
+// staged through LDS in double-buffered blocks of 32 tokens.
 #include "common.hpp"
 #include "layout.hpp"
 
@@ -20,26 +20,18 @@ namespace ec {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-struct DnIn {
-    float4 q0, q1, k0, k1;
-    float v, dec, bt;
-};
+// Token blocks of kDnBlock tokens: the workgroup's 256 threads load the next
+// block's q, k (one 128-float head each per token), the group's 16 v channels,
+// decay and beta with coalesced loads into registers while the current block
+// is computed from LDS, then store them into the other LDS buffer (double
+// buffering).  The per-token recurrence never waits on global memory.
+constexpr uint32_t kDnBlock = 32;
 
-__device__ __forceinline__ void dn_load(DnIn& in, const float* __restrict__ q, const float* __restrict__ k,
-                                        const float* __restrict__ v, const float* __restrict__ decay,
-                                        const float* __restrict__ beta, uint32_t t, uint32_t s, uint32_t n_seq,
-                                        uint32_t n_v, uint32_t n_k, uint32_t d_v, uint32_t h, uint32_t qh,
-                                        uint32_t col, uint32_t ks) {
-    const size_t qk = (((size_t)t * n_seq + s) * n_k + qh) * 128 + 8 * ks;
-    in.q0 = *(const float4*)(q + qk);
-    in.q1 = *(const float4*)(q + qk + 4);
-    in.k0 = *(const float4*)(k + qk);
-    in.k1 = *(const float4*)(k + qk + 4);
-    const size_t hv = ((size_t)t * n_seq + s) * n_v + h;
-    in.v = v[hv * d_v + col];
-    in.dec = decay[hv];
-    in.bt = beta[hv];
-}
+struct DnLds {
+    f32x4 q[2][kDnBlock][32], k[2][kDnBlock][32];
+    float v[2][kDnBlock][16];
+    float dec[2][kDnBlock], bt[2][kDnBlock];
+};
 
 // grid (n_v * d_v/16, n_seq), block 256: threadIdx/16 = column in the group, %16 = k slice.
 __global__ __launch_bounds__(256) void k_deltanet(float* __restrict__ state, const float* __restrict__ q,
@@ -47,39 +39,91 @@ __global__ __launch_bounds__(256) void k_deltanet(float* __restrict__ state, con
                                                   const float* __restrict__ decay, const float* __restrict__ beta,
                                                   float* __restrict__ out, uint32_t T, uint32_t n_seq, uint32_t n_v,
                                                   uint32_t n_k, uint32_t d_v, const int32_t* __restrict__ seq_pos) {
+    __shared__ DnLds L;
     const uint32_t groups = d_v / 16;
     const uint32_t h = blockIdx.x / groups, s = blockIdx.y;
     if (seq_pos && seq_pos[s] < 0) return;
-    const uint32_t col = 16 * (blockIdx.x % groups) + threadIdx.x / 16, ks = threadIdx.x % 16;
+    const uint32_t row = threadIdx.x / 16, ks = threadIdx.x % 16;
+    const uint32_t col0 = 16 * (blockIdx.x % groups), col = col0 + row;
     const uint32_t qh = h / (n_v / n_k);
     const float scale = 1.0f / sqrtf(128.0f);
     float* sp = state + (((size_t)s * n_v + h) * d_v + col) * 128 + 8 * ks;
     float4 s0 = *(float4*)sp, s1 = *(float4*)(sp + 4);
     float S[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 
-    DnIn cur, nxt;
-    dn_load(cur, q, k, v, decay, beta, 0, s, n_seq, n_v, n_k, d_v, h, qh, col, ks);
-    for (uint32_t t = 0; t < T; ++t) {
-        if (t + 1 < T) dn_load(nxt, q, k, v, decay, beta, t + 1, s, n_seq, n_v, n_k, d_v, h, qh, col, ks);
-        const float kk[8] = {cur.k0.x, cur.k0.y, cur.k0.z, cur.k0.w, cur.k1.x, cur.k1.y, cur.k1.z, cur.k1.w};
-        const float qq[8] = {cur.q0.x, cur.q0.y, cur.q0.z, cur.q0.w, cur.q1.x, cur.q1.y, cur.q1.z, cur.q1.w};
-        float kvp = 0.0f;
+    // staging registers of the next block (256 threads: 32 float4 of q and of
+    // k per token, 16 v channels per token, decay / beta)
+    constexpr uint32_t NQ = kDnBlock / 8, NV = kDnBlock * 16 / 256;
+    f32x4 rq[NQ], rk[NQ];  // ext_vector_type: arrays of it stay in registers
+    float rv[NV], rdb;
+    const uint32_t tid = threadIdx.x;
+    auto stage_load = [&](uint32_t t0) {
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            S[i] *= cur.dec;
-            kvp = fmaf(S[i], kk[i], kvp);
+        for (uint32_t u = 0; u < NQ; ++u) {
+            const uint32_t id = tid + 256 * u, t = t0 + id / 32;
+            const size_t off = (((size_t)t * n_seq + s) * n_k + qh) * 128 + 4 * (id % 32);
+            rq[u] = t < T ? *(const f32x4*)(q + off) : z;
+            rk[u] = t < T ? *(const f32x4*)(k + off) : z;
         }
-        const float kv = row16_sum(kvp);
-        const float delta = (cur.v - kv) * cur.bt;
-        float op = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            S[i] = fmaf(kk[i], delta, S[i]);
-            op = fmaf(S[i], qq[i] * scale, op);
+        for (uint32_t u = 0; u < NV; ++u) {
+            const uint32_t id = tid + 256 * u, t = t0 + id / 16;
+            rv[u] = t < T ? v[(((size_t)t * n_seq + s) * n_v + h) * d_v + col0 + id % 16] : 0.0f;
         }
-        const float o = row16_sum(op);
-        if (ks == 0) out[(((size_t)t * n_seq + s) * n_v + h) * d_v + col] = o;
-        cur = nxt;
+        const uint32_t t = t0 + tid % kDnBlock;
+        const size_t hv = ((size_t)t * n_seq + s) * n_v + h;
+        rdb = (tid < 2 * kDnBlock && t < T) ? (tid < kDnBlock ? decay[hv] : beta[hv]) : 0.0f;
+    };
+    auto stage_store = [&](uint32_t buf) {
+#pragma unroll
+        for (uint32_t u = 0; u < NQ; ++u) {
+            const uint32_t id = tid + 256 * u;
+            L.q[buf][id / 32][id % 32] = rq[u];
+            L.k[buf][id / 32][id % 32] = rk[u];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < NV; ++u) {
+            const uint32_t id = tid + 256 * u;
+            L.v[buf][id / 16][id % 16] = rv[u];
+        }
+        if (tid < kDnBlock) L.dec[buf][tid] = rdb;
+        else if (tid < 2 * kDnBlock) L.bt[buf][tid - kDnBlock] = rdb;
+    };
+
+    stage_load(0);
+    stage_store(0);
+    __syncthreads();
+    const uint32_t nb = (T + kDnBlock - 1) / kDnBlock;
+    for (uint32_t b = 0; b < nb; ++b) {
+        const uint32_t buf = b & 1, t0 = b * kDnBlock;
+        stage_load(t0 + kDnBlock);  // past T: zeros, no memory access
+        const uint32_t nt = min(kDnBlock, T - t0);
+        for (uint32_t j = 0; j < nt; ++j) {
+            const f32x4 k0 = L.k[buf][j][2 * ks], k1 = L.k[buf][j][2 * ks + 1];
+            const f32x4 q0 = L.q[buf][j][2 * ks], q1 = L.q[buf][j][2 * ks + 1];
+            const float vv = L.v[buf][j][row], dec = L.dec[buf][j], bt = L.bt[buf][j];
+            const float kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+            const float qq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+            float kvp = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                S[i] *= dec;
+                kvp = fmaf(S[i], kk[i], kvp);
+            }
+            const float kv = row16_sum(kvp);
+            const float delta = (vv - kv) * bt;
+            float op = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                S[i] = fmaf(kk[i], delta, S[i]);
+                op = fmaf(S[i], qq[i] * scale, op);
+            }
+            const float o = row16_sum(op);
+            if (ks == 0) out[(((size_t)(t0 + j) * n_seq + s) * n_v + h) * d_v + col] = o;
+        }
+        stage_store(buf ^ 1);
+        __syncthreads();
     }
     *(float4*)sp = make_float4(S[0], S[1], S[2], S[3]);
     *(float4*)(sp + 4) = make_float4(S[4], S[5], S[6], S[7]);
