@@ -250,12 +250,15 @@ int destroy_graph(ec_engine* e) {
 extern "C" int ec_engine_create(const ec_engine_cfg* cfg, ec_engine** out) {
     if (!cfg || !out) return ec_set_error(EC_ERR_ARG, "ec_engine_create: null argument");
     const ec_engine_cfg& c = *cfg;
-    if (c.hidden % 128 || c.ffn % 128 || c.head_dim != 256 || c.n_kv == 0 || c.n_heads % c.n_kv ||
-        c.ssm_heads == 0 || c.ssm_inner != c.ssm_heads * 128 || (c.ssm_heads / 2) % 1 || c.ssm_inner % 256 ||
-        c.max_batch == 0 || c.max_batch > 16 || c.max_ctx == 0 || c.conv_kernel == 0 || c.vocab == 0)
+    // ssm_heads == 0: no delta-net blocks (every block attention, attn_interval 1)
+    const bool delta_ok = c.ssm_heads == 0 ? (c.ssm_inner == 0 && c.attn_interval == 1)
+                                           : (c.ssm_inner == c.ssm_heads * 128 && c.ssm_inner % 256 == 0 &&
+                                              c.conv_kernel != 0 && c.attn_interval != 0);
+    if (c.hidden % 128 || c.ffn % 128 || c.head_dim != 256 || c.n_kv == 0 || c.n_heads % c.n_kv || !delta_ok ||
+        c.max_batch == 0 || c.max_batch > 16 || c.max_ctx == 0 || c.vocab == 0)
         return ec_set_error(EC_ERR_ARG,
-                            "ec_engine_create: need hidden, ffn % 128 == 0, head_dim 256, ssm_inner = 128*ssm_heads, "
-                            "1 <= max_batch <= 16");
+                            "ec_engine_create: need hidden, ffn % 128 == 0, head_dim 256, ssm_inner = 128*ssm_heads "
+                            "(or both 0 with attn_interval 1), 1 <= max_batch <= 16");
     ec_engine* e = new ec_engine();
     e->c = c;
     e->B = c.max_batch;

@@ -266,11 +266,22 @@ GGUFReader::GGUFReader(const std::string& path) {
         if (tok != metadata_.end())
             if (auto p = std::get_if<std::vector<std::string>>(&tok->second)) tokens_ = *p;
         if (!vocab) vocab = tokens_.size();
+        if (!vocab) {  // the embedding's row count when the metadata names none
+            auto emb = tensors_.find("token_embd.weight");
+            if (emb != tensors_.end() && emb->second.shape.size() >= 2) vocab = emb->second.shape[1];
+        }
         config_.vocab_size = (uint32_t)vocab;
         config_.ffn_type = config_.ffn_hidden_dim ? ModelConfig::FFNType::GatedSwiGLU : ModelConfig::FFNType::Dense;
         config_.norm_type = ModelConfig::NormType::RMSNorm;
         config_.pos_encoding = ModelConfig::PosEncoding::RoPE;
         config_.use_kv_quantization = false;
+        config_.ssm_inner_size = (uint32_t)u("ssm.inner_size");
+        config_.ssm_num_heads = (uint32_t)u("ssm.time_step_rank");
+        config_.ssm_conv_kernel = (uint32_t)u("ssm.conv_kernel");
+        config_.full_attention_interval = (uint32_t)u("full_attention_interval");
+        auto rb = metadata_.find(model_prefix_ + "rope.freq_base");
+        if (rb != metadata_.end())
+            if (auto p = std::get_if<double>(&rb->second)) config_.rope_base = (float)*p;
     } catch (...) {
         ::munmap((void*)map_, size_);
         map_ = nullptr;
@@ -497,12 +508,12 @@ extern "C" int ec_gguf_engine_config(const ec_gguf* g, uint32_t max_batch, uint3
     }
 }
 
-extern "C" int ec_engine_load_gguf(ec_engine* e, const ec_gguf* g) {
-    if (!e || !g) return ec_set_error(EC_ERR_ARG, "ec_engine_load_gguf: null argument");
+// Upload the decoder's tensors from a parsed file (shared by the C ABI and the
+// InferenceEngine facade); throws on a missing or mis-shaped tensor.
+void ec_load_gguf_tensors(ec_engine* e, const GGUFReader& r) {
     ec_engine_cfg c;
-    if (int rc = ec_engine_get_config(e, &c)) return rc;
-    try {
-        const GGUFReader& r = *g->r;
+    if (ec_engine_get_config(e, &c) != EC_OK) throw std::runtime_error(ec_last_error());
+    {
         Loader L{r, e};
         const uint64_t H = c.hidden, F = c.ffn, V = c.vocab;
         const uint64_t q_dim = (uint64_t)c.n_heads * c.head_dim, kv_dim = (uint64_t)c.n_kv * c.head_dim;
@@ -543,6 +554,13 @@ extern "C" int ec_engine_load_gguf(ec_engine* e, const ec_gguf* g) {
                 L.put(l, EC_T_SSM_NORM, blk(l, "ssm_norm.weight"), GGMLType::F32, 128, 1);
             }
         }
+    }
+}
+
+extern "C" int ec_engine_load_gguf(ec_engine* e, const ec_gguf* g) {
+    if (!e || !g) return ec_set_error(EC_ERR_ARG, "ec_engine_load_gguf: null argument");
+    try {
+        ec_load_gguf_tensors(e, *g->r);
         return EC_OK;
     } catch (const std::exception& ex) {
         return fail(ex);

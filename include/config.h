@@ -1,8 +1,9 @@
 /* config.h — model configuration of the reference-signature interface.
  *
- * Same struct layout as the echo-core interface include/config.h:6-26 (field
- * order and enum values unchanged: callers pass it by reference across the
- * library boundary).  The cache-tile helpers of the reference
+ * Same fields, order and enum values as the echo-core interface
+ * include/config.h:6-26, followed by the hybrid-model fields the device
+ * engine needs (defaulting to zero; code compiled against this header passes
+ * it by reference across the library boundary).  The cache-tile helpers of the reference
  * (include/config.h:28-60) tune a CPU L3 tiling; they are kept so that code
  * naming them compiles, and have no effect on the GPU kernels. */
 #pragma once
@@ -30,6 +31,15 @@ struct ModelConfig {
     PosEncoding pos_encoding;
 
     bool use_kv_quantization;
+
+    // Appended for hybrid delta-net / attention models (echo-core-zig
+    // src/core/config.zig:19-23); the fields above keep the reference's order.
+    // All zero = every block is attention (the reference C++ engine's model).
+    uint32_t ssm_inner_size = 0;           // delta-net value dim (ssm.inner_size)
+    uint32_t ssm_num_heads = 0;            // delta-net value heads (ssm.time_step_rank)
+    uint32_t ssm_conv_kernel = 0;          // causal conv taps (ssm.conv_kernel); 0 = 4
+    uint32_t full_attention_interval = 0;  // block i is attention iff (i+1) % interval == 0
+    float rope_base = 0.0f;                // RoPE base (rope.freq_base); 0 = 10000
 };
 
 template <uint64_t L3_SIZE_BYTES>

@@ -464,8 +464,9 @@ void oc_decoder_token(const oc_model_cfg* c, const oc_model_w* w, oc_seq_state* 
                       uint32_t token, float* logits, int quant_act) {
     const uint32_t H = c->hidden;
     const uint32_t q_dim = c->n_heads * c->head_dim, kv_dim = c->n_kv * c->head_dim;
-    const uint32_t value_dim = c->ssm_inner, n_v = c->ssm_heads, d_v = value_dim / n_v;
-    const uint32_t key_dim = value_dim / 2, d_k = d_v, n_k = key_dim / d_k;
+    /* ssm_heads == 0: a model without delta-net blocks (every block attention) */
+    const uint32_t value_dim = c->ssm_inner, n_v = c->ssm_heads, d_v = n_v ? value_dim / n_v : 0;
+    const uint32_t key_dim = value_dim / 2, d_k = d_v, n_k = d_k ? key_dim / d_k : 0;
     const uint32_t conv_dim = 2 * key_dim + value_dim;
     uint32_t maxK = H;
     if (c->ffn > maxK) maxK = c->ffn;
