@@ -19,6 +19,7 @@ namespace ec {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) {
     return (long)(((uint64_t)hi << 32) | (uint64_t)lo);
 }
@@ -193,10 +194,12 @@ __global__ __launch_bounds__(64) void k_attn_combine(const float* __restrict__ w
 // the pieces occupy A rows g, G+g and 2G+g.  K stays int8 (B operand), every
 // dot product is an exact int32 and
 //   score = ks * (s0*dot0 + s1*dot1 + s2*dot2) / sqrt(256).
-// One wave owns a 64-position chunk of one kv head for all G query heads of
-// its GQA group, keeps the chunk's max / sum / output per head and writes one
-// partial; softmax(.)V runs on the VALU from probabilities (times the V row
-// scale) broadcast through LDS, with the chunk's V rows staged in LDS.
+// One workgroup of four waves owns a 64-position chunk of one kv head for all
+// G query heads of its GQA group and writes one partial (max / sum / output)
+// per head.  Wave w scores positions 16w .. 16w+15 and stages their V rows in
+// LDS; wave 0 takes the softmax over the chunk; softmax(.)V runs on the VALU,
+// wave w producing dims 64w .. 64w+63 from probabilities (times the V row
+// scale) broadcast through LDS.
 //
 // Packed q layout: layout.hpp (store_q_pieces).
 constexpr uint32_t kChunk64 = 64;
@@ -216,17 +219,19 @@ __global__ __launch_bounds__(256) void k_pack_q(const float* __restrict__ q, uin
 }
 
 template <int G>
-__global__ __launch_bounds__(64) void k_attn_mfma(const uint8_t* __restrict__ qa, const float* __restrict__ qsc,
-                                                  const int8_t* __restrict__ keys, const int8_t* __restrict__ vals,
-                                                  const float* __restrict__ kscales, const float* __restrict__ vscales,
-                                                  const int32_t* __restrict__ ctx, uint64_t seq_stride, uint32_t n_kv,
-                                                  uint32_t n_chunks_max, uint32_t max_ctx, float* __restrict__ ws) {
+__global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ qa, const float* __restrict__ qsc,
+                                                   const int8_t* __restrict__ keys, const int8_t* __restrict__ vals,
+                                                   const float* __restrict__ kscales, const float* __restrict__ vscales,
+                                                   const int32_t* __restrict__ ctx, uint64_t seq_stride, uint32_t n_kv,
+                                                   uint32_t n_chunks_max, uint32_t max_ctx, float* __restrict__ ws) {
     static_assert(G == 1 || G == 2 || G == 4, "3G A rows must fit the 16 MFMA rows");
     constexpr uint32_t HD = 256;
-    __shared__ float part_s[kQPieces * G][64];  // per-piece scores (times the K row scale)
-    __shared__ float p_s[64][4];
-    __shared__ u32x4 v_s[64 * 16];  // the chunk's V rows, [position][256 bytes]
-    const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z, lane = threadIdx.x;
+    constexpr uint32_t NR = kQPieces * G;  // A rows in use
+    __shared__ float part_s[NR][64];       // per-piece scores (times the K row scale)
+    __shared__ f32x4 p_s[64];              // [position] probabilities x V row scale, one per head
+    __shared__ u32x4 v_s[64 * 16];         // the chunk's V rows, [position][256 bytes]
+    const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int32_t L = min(ctx[s], (int32_t)max_ctx);
     const uint32_t c0 = chunk * kChunk64;
     if (L <= 0 || c0 >= (uint32_t)L) return;
@@ -240,8 +245,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(const uint8_t* __restrict__ qa
     const uint32_t r16 = lane & 15, gq = lane >> 4;
 
     // ---- loads, in the order they are consumed (waitcnt retires them in order):
-    // A operand (packed q) and scales, K for 4 x 16 positions, then V.
-    constexpr uint32_t NR = kQPieces * G;  // A rows in use
+    // A operand (packed q) and scales, K of this wave's 16 positions, then their V.
     const bool arow = r16 < NR;
     const uint8_t* qp = qa + ((((size_t)s * n_kv + kvh) * NR + (arow ? r16 : 0)) * 4 + gq) * 64;
     u32x4 aq[4];
@@ -254,94 +258,102 @@ __global__ __launch_bounds__(64) void k_attn_mfma(const uint8_t* __restrict__ qa
         const uint32_t r = 4 * gq + c;
         rs[c] = scq[r < NR ? r : 0];
     }
-    float ksv[4];
+    const uint32_t t = 16 * wv + r16;  // position of this lane's B column
+    const uint32_t tc = t < ntok ? t : 0;
+    const float ksv = ksb[(size_t)(c0 + tc) * n_kv];
+    const float vsv = vsb[(size_t)(c0 + (lane < ntok ? lane : 0)) * n_kv];  // used by wave 0 (lane = position)
+    u32x4 kw[4];
+    const int8_t* kr = kb + (size_t)(c0 + tc) * row + 16 * gq;
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-        const uint32_t t = 16 * st + r16;
-        ksv[st] = ksb[(size_t)(c0 + (t < ntok ? t : 0)) * n_kv];
-    }
-    const float vsv = vsb[(size_t)(c0 + (lane < ntok ? lane : 0)) * n_kv];
-    u32x4 kw[4][4];
+    for (int i = 0; i < 4; ++i) kw[i] = __builtin_nontemporal_load((const u32x4*)(kr + 64 * i));
+    // V: instruction j brings positions 16*wv + 4j .. +3 (256 bytes each, lane = 16 bytes)
+    u32x4 vv[4];
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-        const uint32_t t = 16 * st + r16;
-        const int8_t* kr = kb + (size_t)(c0 + (t < ntok ? t : 0)) * row + 16 * gq;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kw[st][i] = __builtin_nontemporal_load((const u32x4*)(kr + 64 * i));
-    }
-    // V: instruction j brings positions 4j .. 4j+3 (256 bytes each, lane = 16 bytes)
-    u32x4 vv[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const uint32_t t = 4 * j + (lane >> 4);
-        vv[j] = __builtin_nontemporal_load((const u32x4*)(vb + (size_t)(c0 + (t < ntok ? t : 0)) * row + 16 * (lane & 15)));
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t tv = 16 * wv + 4 * j + (lane >> 4);
+        vv[j] = __builtin_nontemporal_load(
+            (const u32x4*)(vb + (size_t)(c0 + (tv < ntok ? tv : 0)) * row + 16 * (lane & 15)));
     }
 
-    // ---- scores: 8 accumulating MFMAs per 16 positions; C row r = 4*gq + c
-    long A[8];
+    // ---- scores of 16 positions: 8 accumulating MFMAs; C row r = 4*gq + c
+    v4i C = {0, 0, 0, 0};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        A[2 * i] = arow ? pack2(aq[i].x, aq[i].y) : 0l;
-        A[2 * i + 1] = arow ? pack2(aq[i].z, aq[i].w) : 0l;
+    for (int m = 0; m < 8; ++m) {
+        const long A = arow ? ((m & 1) ? pack2(aq[m / 2].z, aq[m / 2].w) : pack2(aq[m / 2].x, aq[m / 2].y)) : 0l;
+        const u32x4 w = kw[m / 2];
+        const long B = (m & 1) ? pack2(w.z, w.w) : pack2(w.x, w.y);
+        C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, C, 0, 0, 0);
     }
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-        v4i C = {0, 0, 0, 0};
+    for (int c = 0; c < 4; ++c)
+        if (4 * gq + c < NR) part_s[4 * gq + c][t] = (float)C[c] * rs[c] * ksv;
 #pragma unroll
-        for (int m = 0; m < 8; ++m) {
-            const u32x4 w = kw[st][m / 2];
-            const long B = (m & 1) ? pack2(w.z, w.w) : pack2(w.x, w.y);
-            C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[m], B, C, 0, 0, 0);
-        }
-        const uint32_t t = 16 * st + r16;
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-            if (4 * gq + c < NR) part_s[4 * gq + c][t] = (float)C[c] * rs[c] * ksv[st];
-    }
-#pragma unroll
-    for (int j = 0; j < 16; ++j) v_s[64 * j + lane] = vv[j];
+    for (int j = 0; j < 4; ++j) v_s[64 * (4 * wv + j) + lane] = vv[j];
     __syncthreads();
 
-    // ---- softmax over the chunk (lane = position)
+    // ---- softmax over the chunk (wave 0, lane = position)
     constexpr float scale = 1.0f / 16.0f;  // 1/sqrt(256)
-    float m[G], l[G];
+    if (wv == 0) {
+        float m[G], l[G];
+        f32x4 pr = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const float raw = (part_s[g][lane] + part_s[G + g][lane]) + part_s[2 * G + g][lane];
-        const float sc = lane < ntok ? raw * scale : -INFINITY;
-        m[g] = wave_max(sc);
-        const float e = lane < ntok ? __expf(sc - m[g]) : 0.0f;
-        l[g] = wave_sum(e);
-        p_s[lane][g] = e * vsv;
+        for (int g = 0; g < G; ++g) {
+            const float raw = (part_s[g][lane] + part_s[G + g][lane]) + part_s[2 * G + g][lane];
+            const float sc = lane < ntok ? raw * scale : -INFINITY;
+            m[g] = wave_max(sc);
+            const float e = lane < ntok ? __expf(sc - m[g]) : 0.0f;
+            l[g] = wave_sum(e);
+            pr[g] = e * vsv;
+        }
+        p_s[lane] = pr;
+        if (lane == 0) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float* rec = ws + (((size_t)s * n_chunks_max + chunk) * n_heads + kvh + n_kv * g) * kRec64;
+                *(float4*)rec = make_float4(m[g], l[g], 0.0f, 0.0f);
+            }
+        }
     }
     __syncthreads();
 
-    // ---- softmax . V (lane = 4 dims)
+    // ---- softmax . V: wave wv owns dims 64*wv .. +63 (lane = one 4-dim word),
+    // lane group pg sums positions 16*pg .. +15; the four group sums are added
+    // by cross-lane exchange.  Positions past the chunk end carry p = 0 (their
+    // clamped V rows add nothing).
+    const uint32_t word = 16 * wv + r16, pg = gq;
+    const uint32_t* vrow = (const uint32_t*)v_s;
     float o[G][4];
 #pragma unroll
     for (int g = 0; g < G; ++g)
         for (int e = 0; e < 4; ++e) o[g][e] = 0.0f;
-    // positions past the chunk end carry p = 0 (their clamped V rows add nothing)
-    const uint32_t* vrow = (const uint32_t*)v_s;
-#pragma unroll 8
-    for (uint32_t t = 0; t < 64; ++t) {
-        const uint32_t w = vrow[64 * t + lane];
+#pragma unroll
+    for (uint32_t i = 0; i < 16; ++i) {
+        const uint32_t tp = 16 * pg + i;
+        const uint32_t w = vrow[64 * tp + word];
+        const f32x4 p = p_s[tp];
         const float v0 = (float)(int8_t)(w & 0xFF), v1 = (float)(int8_t)((w >> 8) & 0xFF);
         const float v2 = (float)(int8_t)((w >> 16) & 0xFF), v3 = (float)(int8_t)(w >> 24);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            const float pg = p_s[t][g];
-            o[g][0] = fmaf(pg, v0, o[g][0]);
-            o[g][1] = fmaf(pg, v1, o[g][1]);
-            o[g][2] = fmaf(pg, v2, o[g][2]);
-            o[g][3] = fmaf(pg, v3, o[g][3]);
+            o[g][0] = fmaf(p[g], v0, o[g][0]);
+            o[g][1] = fmaf(p[g], v1, o[g][1]);
+            o[g][2] = fmaf(p[g], v2, o[g][2]);
+            o[g][3] = fmaf(p[g], v3, o[g][3]);
         }
     }
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float* rec = ws + (((size_t)s * n_chunks_max + chunk) * n_heads + kvh + n_kv * g) * kRec64;
-        if (lane == 0) *(float4*)rec = make_float4(m[g], l[g], 0.0f, 0.0f);
-        *(float4*)(rec + 4 + 4 * lane) = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            o[g][e] += __shfl_xor(o[g][e], 16);
+            o[g][e] += __shfl_xor(o[g][e], 32);
+        }
+    if (pg == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float* rec = ws + (((size_t)s * n_chunks_max + chunk) * n_heads + kvh + n_kv * g) * kRec64;
+            *(float4*)(rec + 4 + 4 * word) = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
+        }
     }
 }
 
@@ -450,7 +462,7 @@ static void launch_mfma(const uint8_t* qa, const float* qsc, const int8_t* keys,
                         const float* vs, float* out, uint8_t* act, const int32_t* ctx, uint32_t n_seq,
                         uint64_t seq_stride, uint32_t n_kv, uint32_t max_ctx, float* ws, hipStream_t st) {
     const uint32_t ncm = (max_ctx + kChunk64 - 1) / kChunk64;
-    hipLaunchKernelGGL((k_attn_mfma<G>), dim3(ncm, n_kv, n_seq), dim3(64), 0, st, qa, qsc, keys, vals, ks, vs, ctx,
+    hipLaunchKernelGGL((k_attn_mfma<G>), dim3(ncm, n_kv, n_seq), dim3(256), 0, st, qa, qsc, keys, vals, ks, vs, ctx,
                        seq_stride, n_kv, ncm, max_ctx, ws);
     const uint32_t xd_off = (uint32_t)act_layout(EC_Q8_0, n_seq, n_kv * G * 256).xd_off;
     hipLaunchKernelGGL(k_attn_merge, dim3(n_kv * G, n_seq), dim3(512), ncm * sizeof(float), st, ws, ctx, out, act,

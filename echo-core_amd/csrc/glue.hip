@@ -109,6 +109,62 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__
     store_act_q8_lane(xk * inv * wk, act, (float*)(act + xd_off), M, Kp / 32, i, k);
 }
 
+// Residual add of split-K partial sums fused with RMSNorm + quantize:
+// x_out = ((x + parts[0]) + parts[1]) + ... (fixed order), then x_out's
+// RMSNorm quantized like k_rmsnorm_quant.  Every block recomputes the whole row
+// of x_out for the sum (the same operations in the same order as the element it
+// writes), so blocks never read what another block writes; x_out != x.
+// parts: [NP][M][H].  grid (ceil(Kp/256), M), thread = element.
+template <int NP>
+__global__ __launch_bounds__(256) void k_add_rmsnorm_quant(const float* __restrict__ x, const float* __restrict__ parts,
+                                                           float* __restrict__ x_out, const float* __restrict__ w,
+                                                           uint8_t* __restrict__ act, uint32_t M, uint32_t H,
+                                                           uint32_t xd_off) {
+    __shared__ float sh[4];
+    const uint32_t i = blockIdx.y, t = threadIdx.x, k = blockIdx.x * 256 + t;
+    const size_t ps = (size_t)M * H;
+    const float* xr = x + (size_t)i * H;
+    const float* pr = parts + (size_t)i * H;
+    const uint32_t Kp = round_up(H, 128);
+    float xk = 0.0f;
+    if (k < H) {
+        float pk[NP];
+#pragma unroll
+        for (int p = 0; p < NP; ++p) pk[p] = pr[p * ps + k];
+        xk = xr[k];
+#pragma unroll
+        for (int p = 0; p < NP; ++p) xk += pk[p];
+    }
+    const float wk = k < H ? w[k] : 0.0f;
+    float ss = 0.0f;
+    // the row's float4s, 1024 per pass with every load of a pass issued
+    // before the first add (H = 2560: one pass)
+    constexpr uint32_t U = 4;
+    for (uint32_t c0 = 0; c0 < H / 4; c0 += 256 * U) {
+        float4 v[U], pv[U][NP];
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            const uint32_t c = c0 + t + 256 * u;
+            const bool ok = c < H / 4;
+            v[u] = ok ? ((const float4*)xr)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int p = 0; p < NP; ++p) pv[u][p] = ok ? ((const float4*)(pr + p * ps))[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            float4 a = v[u];
+#pragma unroll
+            for (int p = 0; p < NP; ++p) a.x += pv[u][p].x, a.y += pv[u][p].y, a.z += pv[u][p].z, a.w += pv[u][p].w;
+            ss = fmaf(a.x, a.x, fmaf(a.y, a.y, fmaf(a.z, a.z, fmaf(a.w, a.w, ss))));
+        }
+    }
+    ss = block_sum256(ss, sh);
+    const float inv = 1.0f / sqrtf(ss / (float)H + 1e-6f);
+    if (k >= Kp) return;  // whole 32-lane blocks leave together
+    if (k < H) x_out[(size_t)i * H + k] = xk;
+    store_act_q8_lane(xk * inv * wk, act, (float*)(act + xd_off), M, Kp / 32, i, k);
+}
+
 // ------------------------------------------------------- SwiGLU + quantize
 // gu [M][2F] (gate rows then up rows) -> act (K = F).  grid (ceil(Kp/256), M),
 // thread = element.
@@ -443,6 +499,28 @@ extern "C" int ec_glue_rmsnorm_quant(const float* x, const float* w, void* act, 
     const ActLayout L = act_layout(EC_Q8_0, M, H);
     EC_GLUE_LAUNCH(k_rmsnorm_quant, dim3((L.Kp + 255) / 256, M), dim3(256), 0, (hipStream_t)stream, x, w,
                    (uint8_t*)act, M, H, (uint32_t)L.xd_off);
+}
+
+extern "C" int ec_glue_add_rmsnorm_quant(const float* x, const float* parts, uint32_t nparts, float* x_out,
+                                         const float* w, void* act, uint32_t M, uint32_t H, void* stream) {
+    if (!x || !parts || !x_out || !w || !act || x == x_out || M == 0 || M > 16 || H % 32 || nparts == 0 ||
+        nparts > 8 || ((uintptr_t)x & 15) || ((uintptr_t)parts & 15))
+        return ec_set_error(EC_ERR_ARG, "ec_glue_add_rmsnorm_quant: bad argument");
+    const ActLayout L = act_layout(EC_Q8_0, M, H);
+    const dim3 grid((L.Kp + 255) / 256, M);
+    const hipStream_t st = (hipStream_t)stream;
+    uint8_t* a = (uint8_t*)act;
+    const uint32_t xo = (uint32_t)L.xd_off;
+    switch (nparts) {
+        case 1: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<1>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo);
+        case 2: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<2>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo);
+        case 3: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<3>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo);
+        case 4: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<4>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo);
+        case 5: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<5>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo);
+        case 6: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<6>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo);
+        case 7: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<7>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo);
+        default: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<8>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo);
+    }
 }
 
 extern "C" int ec_glue_swiglu_quant(const float* gu, void* act, uint32_t M, uint32_t F, void* stream) {

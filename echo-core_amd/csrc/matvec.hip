@@ -148,8 +148,8 @@ struct ByteStage {
 template <int MT, bool DOTS, int GPW>
 __device__ __forceinline__ void q8_0_wave(const uint8_t* __restrict__ wt, const uint8_t* __restrict__ act,
                                           int32_t* __restrict__ dots, uint32_t t, uint32_t M, uint32_t N, uint32_t K,
-                                          uint32_t nG, uint32_t xd_off, uint32_t gbeg, uint32_t gstep, float* xs,
-                                          uint8_t* as, float (&acc)[4]) {
+                                          uint32_t nG, uint32_t xd_off, uint32_t gbeg, uint32_t gstep, uint32_t gend,
+                                          float* xs, uint8_t* as, float (&acc)[4]) {
     constexpr int R = MT < 4 ? MT : 4;
     constexpr int S = slots<MT>();
     constexpr int NB = 4 * GPW;
@@ -157,7 +157,7 @@ __device__ __forceinline__ void q8_0_wave(const uint8_t* __restrict__ wt, const 
     const uint32_t lane = threadIdx.x & 63, row = lane & 15, g = lane >> 4;
     const bool aval = row < M;
     const size_t act_bytes = (size_t)nG * 128 * M;
-    for (uint32_t G0 = gbeg; G0 < nG; G0 += gstep) {
+    for (uint32_t G0 = gbeg; G0 < gend; G0 += gstep) {
         ScaleStage<NB, S> sc;
         ByteStage<ACT_MAX> ast;
         if constexpr (!DOTS) sc.load((const float*)(act + xd_off), nG * 4, 4 * G0, M, lane);
@@ -166,7 +166,7 @@ __device__ __forceinline__ void q8_0_wave(const uint8_t* __restrict__ wt, const 
         uint2 dw[GPW];
 #pragma unroll
         for (int u = 0; u < GPW; ++u) {
-            const uint32_t G = min(G0 + u, nG - 1);
+            const uint32_t G = min(G0 + u, gend - 1);
             const uint8_t* ch = wt + (size_t)G * kQ8TChunk;
             b01[u] = ld_stream16(ch + lane * 16);
             b23[u] = ld_stream16(ch + 1024 + lane * 16);
@@ -177,7 +177,7 @@ __device__ __forceinline__ void q8_0_wave(const uint8_t* __restrict__ wt, const 
 #pragma unroll
         for (int u = 0; u < GPW; ++u) {
             const uint32_t G = G0 + u;
-            if (G >= nG) break;
+            if (G >= gend) break;
             const uint8_t* ap = as + (((size_t)u * 4 + g) * M + (aval ? row : 0)) * 32;
             const uint4 a01 = *(const uint4*)ap;
             const uint4 a23 = *(const uint4*)(ap + 16);
@@ -214,25 +214,28 @@ __device__ __forceinline__ void q8_0_wave(const uint8_t* __restrict__ wt, const 
 template <int MT, int GPW>
 constexpr uint32_t q8_wave_lds() { return 4 * GPW * slots<MT>() + GPW * 128 * slots<MT>() / 4; }
 
-// grid = one workgroup per 16-row tile; the tile's K range is split over the
-// nw waves of the workgroup.
+// grid = (16-row tiles, K splits): workgroup (t, sp) covers chunks
+// [sp*nG/ns, (sp+1)*nG/ns) of tile t (ns = gridDim.y), split over its nw
+// waves, and writes its sums to y + sp*split_stride (one partial result per
+// split; ns = 1: the whole K range).
 template <int MT, bool DOTS, int GPW>
 __global__ __launch_bounds__(1024) void k_mv_q8_0(const uint8_t* __restrict__ W, const uint8_t* __restrict__ act,
                                                   float* __restrict__ y, int32_t* __restrict__ dots, uint32_t M,
                                                   uint32_t N, uint32_t K, uint32_t nG, uint32_t xd_off, uint32_t ldy,
-                                                  int accumulate) {
+                                                  int accumulate, size_t split_stride) {
     extern __shared__ float lds[];
     constexpr int R = MT < 4 ? MT : 4;
-    const uint32_t t = blockIdx.x;
+    const uint32_t t = blockIdx.x, sp = blockIdx.y;
     const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t nw = blockDim.x >> 6;
+    const uint32_t g0 = sp * nG / gridDim.y, g1 = (sp + 1) * nG / gridDim.y;
     float* red = lds;
     float* xs = lds + nw * 256 + w * q8_wave_lds<MT, GPW>();
     uint8_t* as = (uint8_t*)(xs + 4 * GPW * slots<MT>());
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    q8_0_wave<MT, DOTS, GPW>(W + (size_t)t * nG * kQ8TChunk, act, dots, t, M, N, K, nG, xd_off, w * GPW, nw * GPW, xs,
-                             as, acc);
-    if constexpr (!DOTS) reduce_store<R>(acc, red, y, t, M, N, ldy, accumulate);
+    q8_0_wave<MT, DOTS, GPW>(W + (size_t)t * nG * kQ8TChunk, act, dots, t, M, N, K, nG, xd_off, g0 + w * GPW, nw * GPW,
+                             g1, xs, as, acc);
+    if constexpr (!DOTS) reduce_store<R>(acc, red, y + sp * split_stride, t, M, N, ldy, accumulate);
 }
 
 // --------------------------------------------------------------------- Q4_K
@@ -501,28 +504,33 @@ static uint32_t lds_cap_waves(uint32_t wave_floats) { return (uint32_t)(kLdsByte
 
 template <int MT, bool DOTS, int GPW>
 static void launch_q8_g(const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N, uint32_t K,
-                        uint32_t ldy, int accumulate, uint32_t nw, hipStream_t st) {
+                        uint32_t ldy, int accumulate, uint32_t nw, uint32_t nsplit, hipStream_t st) {
     const ActLayout L = act_layout(EC_Q8_0, M, K);
     const uint32_t nT = round_up(N, 16) / 16, nG = L.Kp / 128;
     nw = min(nw, lds_cap_waves(q8_wave_lds<MT, GPW>()));
     const size_t lds = ((size_t)nw * 256 + (size_t)nw * q8_wave_lds<MT, GPW>()) * sizeof(float);
-    hipLaunchKernelGGL((k_mv_q8_0<MT, DOTS, GPW>), dim3(nT), dim3(64 * nw), lds, st, (const uint8_t*)W,
-                       (const uint8_t*)act, y, dots, M, N, K, nG, (uint32_t)L.xd_off, ldy, accumulate);
+    hipLaunchKernelGGL((k_mv_q8_0<MT, DOTS, GPW>), dim3(nT, nsplit), dim3(64 * nw), lds, st, (const uint8_t*)W,
+                       (const uint8_t*)act, y, dots, M, N, K, nG, (uint32_t)L.xd_off, ldy, accumulate,
+                       (size_t)M * ldy);
 }
 
+// nsplit > 1 (<= the 128-element chunks of K): the K range is cut into
+// nsplit balanced chunk ranges, one workgroup per (tile, range), partial sums
+// to y + sp*M*ldy.
 template <int MT, bool DOTS>
 static void launch_q8(const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N, uint32_t K,
-                      uint32_t ldy, int accumulate, hipStream_t st) {
+                      uint32_t ldy, int accumulate, hipStream_t st, uint32_t nsplit = 1) {
     const uint32_t nT = round_up(N, 16) / 16, nG = round_up(K, 128) / 128;
+    const uint32_t cps = (nG + nsplit - 1) / nsplit;  // longest range
     int gpw;
     uint32_t nw;
-    plan(nT, nG, 5, gpw, nw);  // GPW <= 5 keeps every variant under 128 VGPRs (1024 threads)
+    plan(nT * nsplit, cps, 5, gpw, nw);  // GPW <= 5 keeps every variant under 128 VGPRs (1024 threads)
     switch (gpw) {
-        case 1: launch_q8_g<MT, DOTS, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
-        case 2: launch_q8_g<MT, DOTS, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
-        case 3: launch_q8_g<MT, DOTS, 3>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
-        case 4: launch_q8_g<MT, DOTS, 4>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
-        default: launch_q8_g<MT, DOTS, 5>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
+        case 1: launch_q8_g<MT, DOTS, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
+        case 2: launch_q8_g<MT, DOTS, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
+        case 3: launch_q8_g<MT, DOTS, 3>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
+        case 4: launch_q8_g<MT, DOTS, 4>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
+        default: launch_q8_g<MT, DOTS, 5>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
     }
 }
 
@@ -611,6 +619,22 @@ extern "C" int ec_matvec(int fmt, const void* tiled, const void* act, float* y, 
     if (rc) return rc;
     if (ldy < N) return ec_set_error(EC_ERR_ARG, "ec_matvec: ldy < N");
     dispatch<false>(fmt, tiled, act, y, nullptr, M, N, K, ldy, accumulate, (hipStream_t)stream);
+    EC_CHECK_LAUNCH();
+    return EC_OK;
+}
+
+extern "C" int ec_matvec_split(int fmt, const void* tiled, const void* act, float* parts, uint32_t M, uint32_t N,
+                               uint32_t K, uint32_t nsplit, void* stream) {
+    int rc = check_mv(fmt, tiled, act, parts, M, N, K, "ec_matvec_split");
+    if (rc) return rc;
+    if (fmt != EC_Q8_0) return ec_set_error(EC_ERR_UNSUPPORTED, "ec_matvec_split: Q8_0 weights only");
+    if (nsplit == 0 || nsplit > round_up(K, 128) / 128)
+        return ec_set_error(EC_ERR_ARG, "ec_matvec_split: nsplit must be in [1, ceil(K/128)]");
+    const hipStream_t st = (hipStream_t)stream;
+    if (M == 1) launch_q8<1, false>(tiled, act, parts, nullptr, M, N, K, N, 0, st, nsplit);
+    else if (M <= 4) launch_q8<4, false>(tiled, act, parts, nullptr, M, N, K, N, 0, st, nsplit);
+    else if (M <= 8) launch_q8<8, false>(tiled, act, parts, nullptr, M, N, K, N, 0, st, nsplit);
+    else launch_q8<16, false>(tiled, act, parts, nullptr, M, N, K, N, 0, st, nsplit);
     EC_CHECK_LAUNCH();
     return EC_OK;
 }

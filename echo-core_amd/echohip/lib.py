@@ -32,6 +32,7 @@ _SIGS = {
     "ec_act_unpack": [C.c_int, _vp, _vp, _vp, _u32, _u32, _vp],
     "ec_matvec": [C.c_int, _vp, _vp, _vp, _u32, _u32, _u32, _u32, C.c_int, _vp],
     "ec_block_dots": [C.c_int, _vp, _vp, _vp, _u32, _u32, _u32, _vp],
+    "ec_matvec_split": [C.c_int, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp],
     "ec_matvec_gguf_f32": [C.c_int, _vp, _vp, _vp, _u32, _u32, _vp],
     "ec_dequant_dot_int8": [_vp, _vp, _vp, _vp, _u32, _u32, _vp],
     "ec_dequantize_to_fp16": [C.c_int, _vp, _vp, _sz, _vp],
@@ -47,6 +48,7 @@ _SIGS = {
                            _vp],
     "ec_glue_gated_norm_quant": [_vp, _vp, _u32, _u32, _vp, _vp, _u32, _u32, _vp],
     "ec_glue_rmsnorm_quant": [_vp, _vp, _vp, _u32, _u32, _vp],
+    "ec_glue_add_rmsnorm_quant": [_vp, _vp, _u32, _vp, _vp, _vp, _u32, _u32, _vp],
     "ec_glue_swiglu_quant": [_vp, _vp, _u32, _u32, _vp],
     "ec_glue_conv_gates_chunk": [_vp, _u32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32,
                                  _vp],
@@ -147,6 +149,10 @@ class Lib:
         self._call("ec_matvec", fmt, _ptr(tiled), _ptr(act), _ptr(y), M, N, K, N if ldy is None else ldy,
                    int(bool(accumulate)), self._stream(stream))
 
+    def matvec_split(self, fmt, tiled, act, parts, M, N, K, nsplit, stream=None):
+        self._call("ec_matvec_split", fmt, _ptr(tiled), _ptr(act), _ptr(parts), M, N, K, nsplit,
+                   self._stream(stream))
+
     def block_dots(self, fmt, tiled, act, out, M, N, K, stream=None):
         self._call("ec_block_dots", fmt, _ptr(tiled), _ptr(act), _ptr(out), M, N, K, self._stream(stream))
 
@@ -210,6 +216,10 @@ class Lib:
 
     def rmsnorm_quant(self, x, w, act, M, H, stream=None):
         self._call("ec_glue_rmsnorm_quant", _ptr(x), _ptr(w), _ptr(act), M, H, self._stream(stream))
+
+    def add_rmsnorm_quant(self, x, parts, nparts, x_out, w, act, M, H, stream=None):
+        self._call("ec_glue_add_rmsnorm_quant", _ptr(x), _ptr(parts), nparts, _ptr(x_out), _ptr(w), _ptr(act), M, H,
+                   self._stream(stream))
 
     def swiglu_quant(self, gu, act, M, F, stream=None):
         self._call("ec_glue_swiglu_quant", _ptr(gu), _ptr(act), M, F, self._stream(stream))

@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
+#include <utility>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -85,6 +87,9 @@ struct ec_engine {
     uint32_t nin_delta = 0, nin_attn = 0, nin_max = 0;
     uint64_t seq_stride = 0;
     float *x = nullptr, *proj = nullptr, *gu = nullptr, *core = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
+    // decode residual stream: x and x2 alternate (each fused residual add
+    // writes the other one); parts holds a split-K projection's partial sums
+    float *x2 = nullptr, *parts = nullptr;
     float *dec = nullptr, *beta = nullptr, *qbuf = nullptr, *attn_out = nullptr, *logits = nullptr;
     float* inv_freq = nullptr;
     void *act_h = nullptr, *act_v = nullptr, *act_f = nullptr, *act_q = nullptr, *attn_ws = nullptr;
@@ -182,6 +187,35 @@ int mv(ec_engine* e, const Mat& m, const void* act, float* y, uint32_t ldy, int 
     return ec_matvec(EC_Q8_0, m.tiled, act, y, e->B, m.N, m.K, ldy, acc, e->st);
 }
 
+// K splits of a residual-adding projection (N = hidden): with N/16 tiles
+// alone too few workgroups cover the GPU, so the K range is split and the
+// partial sums are added by the next RMSNorm (ec_glue_add_rmsnorm_quant).
+// Measured on MI355X for N = 2560, M = 8: K 4096 5.75 -> 4.92 us (3 splits),
+// K 9216 8.43 -> 6.99 us (3 splits); more splits shorten the matvec further
+// but each partial adds a 10 KB row read to every RMSNorm block, and the
+// decode step was fastest at 3 and 3 (EC_RESID_SPLIT="a,b" overrides the
+// splits for K < 8192 and K >= 8192).
+constexpr uint32_t kMaxResidSplit = 8;
+uint32_t resid_split(uint32_t N, uint32_t K) {
+    static const std::pair<uint32_t, uint32_t> sp = [] {
+        uint32_t a = 3, b = 3;
+        if (const char* v = getenv("EC_RESID_SPLIT")) sscanf(v, "%u,%u", &a, &b);
+        return std::make_pair(std::clamp(a, 1u, kMaxResidSplit), std::clamp(b, 1u, kMaxResidSplit));
+    }();
+    const uint32_t tiles = (N + 15) / 16, nG = (K + 127) / 128;
+    if (tiles >= 256) return 1;
+    return std::min(nG >= 64 ? sp.second : sp.first, nG);
+}
+
+// Residual projection: partial sums into e->parts; returns the split count.
+int mv_resid(ec_engine* e, const Mat& m, const void* act, uint32_t& ns) {
+    ns = resid_split(m.N, m.K);
+    if (e->mv_bytes)
+        e->mv_bytes->push_back((double)gguf_bytes(m.N, m.K) + (double)e->B * (m.K + m.K / 32 * 4) +
+                               (double)e->B * m.N * 4 * ns);
+    return ec_matvec_split(EC_Q8_0, m.tiled, act, e->parts, e->B, m.N, m.K, ns, e->st);
+}
+
 // The decode step (stream-ordered; captured once into a graph).
 int record_step(ec_engine* e) {
     const ec_engine_cfg& c = e->c;
@@ -191,17 +225,29 @@ int record_step(ec_engine* e) {
     do {                               \
         if (!e->mv_only) EC_TRY(call); \
     } while (0)
+    // xc: the current residual; ns > 0: e->parts holds ns partial sums still
+    // to be added to it (by the next norm, which then moves xc to the other buffer)
+    float* xc = e->x;
+    uint32_t ns = 0;
+    auto norm = [&](const float* w) -> int {
+        if (ns == 0) return ec_glue_rmsnorm_quant(xc, w, e->act_h, B, H, st);
+        float* xn = xc == e->x ? e->x2 : e->x;
+        const int rc = ec_glue_add_rmsnorm_quant(xc, e->parts, ns, xn, w, e->act_h, B, H, st);
+        xc = xn;
+        ns = 0;
+        return rc;
+    };
     EC_GLUE(ec_glue_embed(e->embed, e->tok, e->x, B, H, c.vocab, st));
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         Layer& y = e->L[l];
-        EC_GLUE(ec_glue_rmsnorm_quant(e->x, y.attn_norm, e->act_h, B, H, st));
+        EC_GLUE(norm(y.attn_norm));
         if (!y.attn) {
             const uint32_t Nin = e->nin_delta;
             EC_TRY(mv(e, y.w_in, e->act_h, e->proj, Nin, 0));
             // conv + gates + delta rule + gated norm + quantize in one launch
             EC_GLUE(ec_delta_step(e->proj, Nin, y.conv_state, y.conv_w, y.a_log, y.dt_bias, y.ssm_norm, y.ssm_state,
                                  e->act_v, e->pos, B, e->n_k, e->n_v, c.conv_kernel, st));
-            EC_TRY(mv(e, y.w_out, e->act_v, e->x, H, 1));
+            EC_TRY(mv_resid(e, y.w_out, e->act_v, ns));
         } else {
             const uint32_t Nin = e->nin_attn;
             EC_TRY(mv(e, y.w_in, e->act_h, e->proj, Nin, 0));
@@ -223,14 +269,14 @@ int record_step(ec_engine* e) {
                                       c.n_heads, c.n_kv, c.head_dim, c.max_ctx, e->attn_ws, st));
                 EC_GLUE(ec_quantize_act(EC_Q8_0, e->attn_out, e->act_q, B, e->q_dim, st));
             }
-            EC_TRY(mv(e, y.w_out, e->act_q, e->x, H, 1));
+            EC_TRY(mv_resid(e, y.w_out, e->act_q, ns));
         }
-        EC_GLUE(ec_glue_rmsnorm_quant(e->x, y.ffn_norm, e->act_h, B, H, st));
+        EC_GLUE(norm(y.ffn_norm));
         EC_TRY(mv(e, y.w_gu, e->act_h, e->gu, 2 * F, 0));
         EC_GLUE(ec_glue_swiglu_quant(e->gu, e->act_f, B, F, st));
-        EC_TRY(mv(e, y.w_down, e->act_f, e->x, H, 1));
+        EC_TRY(mv_resid(e, y.w_down, e->act_f, ns));
     }
-    EC_GLUE(ec_glue_rmsnorm_quant(e->x, e->final_norm, e->act_h, B, H, st));
+    EC_GLUE(norm(e->final_norm));
     EC_TRY(mv(e, e->lm_head, e->act_h, e->logits, c.vocab, 0));
     EC_GLUE(ec_glue_argmax_advance(e->logits, c.vocab, e->gen, e->tok, e->pos, B, st));
     return EC_OK;
@@ -321,6 +367,7 @@ extern "C" int ec_engine_create(const ec_engine_cfg* cfg, ec_engine** out) {
     (void)maxK;
     if ((rc = dalloc(e, &e->embed, gguf_bytes(c.vocab, H))) || (rc = dalloc(e, &e->final_norm, H)) ||
         (rc = alloc_mat(e, e->lm_head, c.vocab, H)) || (rc = dalloc(e, &e->x, (size_t)B * H)) ||
+        (rc = dalloc(e, &e->x2, (size_t)B * H)) || (rc = dalloc(e, &e->parts, (size_t)kMaxResidSplit * B * H)) ||
         (rc = dalloc(e, &e->proj, (size_t)B * e->nin_max)) || (rc = dalloc(e, &e->gu, (size_t)B * 2 * e->F)) ||
         (rc = dalloc(e, &e->core, (size_t)B * e->value_dim)) || (rc = dalloc(e, &e->q, (size_t)B * e->key_dim)) ||
         (rc = dalloc(e, &e->k, (size_t)B * e->key_dim)) || (rc = dalloc(e, &e->v, (size_t)B * e->value_dim)) ||

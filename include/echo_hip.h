@@ -83,6 +83,13 @@ int ec_act_unpack(int fmt, const void* act, int8_t* xq, float* xd, uint32_t M, u
  * (the reference's y += W x), else y is overwritten.  y is [M][ldy] fp32. */
 int ec_matvec(int fmt, const void* tiled, const void* act, float* y, uint32_t M, uint32_t N, uint32_t K,
               uint32_t ldy, int accumulate, void* stream);
+/* Split-K form of ec_matvec for Q8_0 (no counterpart in the reference: the
+ * decode step's output projections use it to fill the GPU when N is small).
+ * The K range is cut into nsplit (1 .. ceil(K/128)) balanced ranges of
+ * 128-element chunks; parts[sp][M][N] receives range sp's partial sums.
+ * sum over sp of parts == ec_matvec's y up to fp32 summation order. */
+int ec_matvec_split(int fmt, const void* tiled, const void* act, float* parts, uint32_t M, uint32_t N, uint32_t K,
+                    uint32_t nsplit, void* stream);
 /* The int32 block dots themselves: out[m][n][K/32] (parity contract). */
 int ec_block_dots(int fmt, const void* tiled, const void* act, int32_t* out, uint32_t M, uint32_t N, uint32_t K,
                   void* stream);
@@ -177,6 +184,11 @@ int ec_delta_step(const float* proj, uint32_t Nin, float* conv_state, const floa
 int ec_glue_embed(const void* emb, const int32_t* tok, float* x, uint32_t n_seq, uint32_t H, uint32_t vocab,
                   void* stream);
 int ec_glue_rmsnorm_quant(const float* x, const float* w, void* act, uint32_t M, uint32_t H, void* stream);
+/* x_out = x + parts[0] + ... + parts[nparts-1] (added in that order; parts is
+ * [nparts][M][H], the output of ec_matvec_split), then RMSNorm + quantize of
+ * x_out as ec_glue_rmsnorm_quant.  1 <= nparts <= 8; x_out must not be x. */
+int ec_glue_add_rmsnorm_quant(const float* x, const float* parts, uint32_t nparts, float* x_out, const float* w,
+                              void* act, uint32_t M, uint32_t H, void* stream);
 int ec_glue_swiglu_quant(const float* gu, void* act, uint32_t M, uint32_t F, void* stream);
 /* conv_state [n_seq][kern][conv_dim] is a ring over positions: slot p % kern
  * holds the conv input of position p (all zero before position 0). */

@@ -49,6 +49,38 @@ def test_rmsnorm_quant(hip, oc, M, H):
         _check_q8(xq[i], xd[i], xq_r, xd_r)
 
 
+@pytest.mark.parametrize("M,H,ns", [(8, 2560, 6), (8, 2560, 4), (3, 256, 1), (16, 128, 8), (2, 5120, 3)])
+def test_add_rmsnorm_quant(hip, oc, M, H, ns):
+    """x_out = ((x + p0) + p1) + ... in fp32 (exact order), then RMSNorm + quantize of x_out."""
+    import torch
+    x = (3.0 * synth.normal(synth.stream_seed(4, H), M * H)).astype(np.float32).reshape(M, H)
+    parts = synth.normal(synth.stream_seed(5, ns), ns * M * H).astype(np.float32).reshape(ns, M, H)
+    w = (1.0 + 0.1 * synth.normal(synth.stream_seed(2, H), H)).astype(np.float32)
+    act = empty(hip.act_bytes(Q8_0, M, H), torch.uint8)
+    x_out = empty(M * H, torch.float32)
+    hip.add_rmsnorm_quant(dev(x), dev(parts), ns, x_out, dev(w), act, M, H)
+    want = x.copy()
+    for p in range(ns):
+        want = want + parts[p]
+    assert np.array_equal(host(x_out).reshape(M, H).view(np.uint32), want.view(np.uint32))
+    xq, xd = _unpack(hip, act, M, H)
+    for i in range(M):
+        y = np.zeros(H, np.float32)
+        oc.lib.oc_rmsnorm(want[i], w, y, H)
+        xq_r, xd_r = oc.quantize_act_q8_0(y)
+        _check_q8(xq[i], xd[i], xq_r, xd_r)
+
+
+def test_add_rmsnorm_quant_rejects_in_place(hip):
+    import torch
+    from echohip.lib import EchoHipError
+    x = dev(np.ones((2, 128), np.float32))
+    act = empty(hip.act_bytes(Q8_0, 2, 128), torch.uint8)
+    with pytest.raises(EchoHipError):
+        hip.add_rmsnorm_quant(x, dev(np.ones((1, 2, 128), np.float32)), 1, x, dev(np.ones(128, np.float32)), act, 2,
+                              128)
+
+
 @pytest.mark.parametrize("M,F", [(8, 9216), (2, 512), (5, 384)])
 def test_swiglu_quant(hip, oc, M, F):
     import torch

@@ -123,6 +123,45 @@ def test_q8_0_matvec(hip, oc, M, N, K):
     assert np.allclose(host(y2), y - y0, rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("M,N,K,ns", [(8, 40, 4096, 4), (8, 64, 9216, 6), (3, 33, 992, 8), (1, 48, 512, 1),
+                                      (16, 16, 384, 3), (5, 20, 2560, 20)])
+def test_q8_0_matvec_split(hip, oc, M, N, K, ns):
+    """parts[sp] = the matvec over 128-element chunks [sp*nG/ns, (sp+1)*nG/ns) of K."""
+    import torch
+    W = synth.q8_0_blocks(6000 + K, N, K)
+    X = synth.activations(7000 + M, M * K).reshape(M, K)
+    tiled, act = _prep(hip, 6, W, X)
+    parts = dev(np.full((ns, M, N), 3.0, np.float32))
+    hip.matvec_split(6, tiled, act, parts, M, N, K, ns)
+    parts = host(parts).reshape(ns, M, N)
+    nG = -(-K // 128)
+    Wb = W.reshape(N, K // 32, 34)
+    for m in range(M):
+        rq, rd = oc.quantize_act_q8_0(X[m])
+        xdq = oc.dequant_act_q8_0(rq, rd)
+        for sp in range(ns):
+            b0, b1 = 4 * (sp * nG // ns), min(K // 32, 4 * ((sp + 1) * nG // ns))
+            ref = oc.matvec_q8_0(np.ascontiguousarray(Wb[:, b0:b1]).reshape(N, -1), xdq[32 * b0:32 * b1])
+            assert rel_l2(parts[sp, m], ref) < 1e-5, (m, sp)
+    y = empty(M * N, torch.float32)
+    hip.matvec(6, tiled, act, y, M, N, K)
+    assert rel_l2(parts.sum(0), host(y).reshape(M, N)) < 1e-6
+
+
+def test_q8_0_matvec_split_rejects_bad_arguments(hip):
+    import torch
+    from echohip.lib import EchoHipError
+    W = synth.q8_0_blocks(1, 16, 256)
+    tiled, act = _prep(hip, 6, W, synth.activations(2, 256).reshape(1, 256))
+    parts = empty(4 * 16, torch.float32)
+    with pytest.raises(EchoHipError):
+        hip.matvec_split(6, tiled, act, parts, 1, 16, 256, 3)  # 2 chunks of 128
+    with pytest.raises(EchoHipError):
+        hip.matvec_split(6, tiled, act, parts, 1, 16, 256, 0)
+    with pytest.raises(EchoHipError):
+        hip.matvec_split(10, tiled, act, parts, 1, 16, 256, 1)  # Q4_K
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 48, 512), (3, 40, 768), (8, 64, 2560), (16, 16, 256)])
 def test_q4_K_act_and_block_dots_bit_exact(hip, oc, M, N, K):
     import torch
