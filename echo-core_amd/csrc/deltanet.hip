@@ -143,6 +143,20 @@ __global__ __launch_bounds__(256) void k_deltanet(float* __restrict__ state, con
 // the others only use slots that step leaves untouched (with kern == 4 every
 // block loads all four slots before it knows the position, and the slot being
 // rewritten is never selected).
+// proj holds NP partial sums of the input projection, [NP][n_seq][Nin] (a
+// split-K matvec's output); every element read is their sum in part order.
+template <int NP>
+__device__ __forceinline__ float proj_at(const float* __restrict__ pr, size_t pstride, size_t i) {
+    float v[NP];
+#pragma unroll
+    for (int q = 0; q < NP; ++q) v[q] = pr[q * pstride + i];
+    float a = v[0];
+#pragma unroll
+    for (int q = 1; q < NP; ++q) a += v[q];
+    return a;
+}
+
+template <int NP>
 __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ proj, uint32_t Nin,
                                                      float* __restrict__ conv_state,
                                                      const float* __restrict__ conv_w,
@@ -158,6 +172,7 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
     const uint32_t key_dim = n_k * 128, value_dim = n_v * 128, conv_dim = 2 * key_dim + value_dim;
     const uint32_t rep = n_v / n_k, qh = h / rep;
     const float* pr = proj + (size_t)s * Nin;
+    const size_t pstride = (size_t)M * Nin;
 
     // Every load that does not depend on the position is issued before pos[s]
     // arrives.  State column first: thread (col, ks) holds k = 32u + 4ks + e,
@@ -173,7 +188,7 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
     // gated-norm inputs of output channel t
     float zg = 0.0f, nwt = 0.0f;
     if (t < 128) {
-        zg = pr[conv_dim + h * 128 + t];
+        zg = proj_at<NP>(pr, pstride, conv_dim + h * 128 + t);
         nwt = norm_w[t];
     }
     // conv inputs: threads 0..127 q channels, 128..255 k channels, 256..383 v
@@ -184,7 +199,7 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
     const bool ring4 = kern == 4;
     float xin = 0.0f, r4[4] = {0.f, 0.f, 0.f, 0.f}, w4[4] = {0.f, 0.f, 0.f, 0.f};
     if (t < 384) {
-        xin = pr[c];
+        xin = proj_at<NP>(pr, pstride, c);
         if (ring4) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -195,8 +210,8 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
     }
     float al = 0.0f, br = 0.0f, dtb = 0.0f, alog = 0.0f;
     if (t == 384) {
-        al = pr[conv_dim + value_dim + h];
-        br = pr[conv_dim + value_dim + n_v + h];
+        al = proj_at<NP>(pr, pstride, conv_dim + value_dim + h);
+        br = proj_at<NP>(pr, pstride, conv_dim + value_dim + n_v + h);
         dtb = dt_bias[h];
         alog = a_log[h];
     }
@@ -305,18 +320,40 @@ extern "C" int ec_deltanet(float* state, const float* q, const float* k, const f
     return EC_OK;
 }
 
+extern "C" int ec_delta_step_split(const float* proj, uint32_t nparts, uint32_t Nin, float* conv_state,
+                                   const float* conv_w, const float* a_log, const float* dt_bias, const float* norm_w,
+                                   float* state, void* act, const int32_t* pos, uint32_t n_seq, uint32_t n_k,
+                                   uint32_t n_v, uint32_t kern, void* stream) {
+    if (n_seq == 0) return EC_OK;
+    if (!proj || !conv_state || !conv_w || !a_log || !dt_bias || !norm_w || !state || !act || !pos || n_k == 0 ||
+        n_v == 0 || n_v % n_k || kern == 0 || n_seq > 16 || nparts == 0 || nparts > 8 ||
+        Nin < 2 * n_k * 128 + 2 * n_v * 128 + 2 * n_v)
+        return ec_set_error(EC_ERR_ARG, "ec_delta_step: bad argument");
+    const ActLayout L = act_layout(EC_Q8_0, n_seq, n_v * 128);
+    const dim3 grid(n_v, n_seq);
+    const hipStream_t st = (hipStream_t)stream;
+#define EC_DSTEP(NP)                                                                                               \
+    hipLaunchKernelGGL(k_delta_step<NP>, grid, dim3(1024), 0, st, proj, Nin, conv_state, conv_w, a_log, dt_bias, \
+                       norm_w, state, (uint8_t*)act, (uint32_t)L.xd_off, n_seq, pos, n_k, n_v, kern)
+    switch (nparts) {
+        case 1: EC_DSTEP(1); break;
+        case 2: EC_DSTEP(2); break;
+        case 3: EC_DSTEP(3); break;
+        case 4: EC_DSTEP(4); break;
+        case 5: EC_DSTEP(5); break;
+        case 6: EC_DSTEP(6); break;
+        case 7: EC_DSTEP(7); break;
+        default: EC_DSTEP(8); break;
+    }
+#undef EC_DSTEP
+    EC_CHECK_LAUNCH();
+    return EC_OK;
+}
+
 extern "C" int ec_delta_step(const float* proj, uint32_t Nin, float* conv_state, const float* conv_w,
                              const float* a_log, const float* dt_bias, const float* norm_w, float* state, void* act,
                              const int32_t* pos, uint32_t n_seq, uint32_t n_k, uint32_t n_v, uint32_t kern,
                              void* stream) {
-    if (n_seq == 0) return EC_OK;
-    if (!proj || !conv_state || !conv_w || !a_log || !dt_bias || !norm_w || !state || !act || !pos || n_k == 0 ||
-        n_v == 0 || n_v % n_k || kern == 0 || n_seq > 16 || Nin < 2 * n_k * 128 + 2 * n_v * 128 + 2 * n_v)
-        return ec_set_error(EC_ERR_ARG, "ec_delta_step: bad argument");
-    const ActLayout L = act_layout(EC_Q8_0, n_seq, n_v * 128);
-    hipLaunchKernelGGL(k_delta_step, dim3(n_v, n_seq), dim3(1024), 0, (hipStream_t)stream, proj, Nin, conv_state,
-                       conv_w, a_log, dt_bias, norm_w, state, (uint8_t*)act, (uint32_t)L.xd_off, n_seq, pos, n_k,
-                       n_v, kern);
-    EC_CHECK_LAUNCH();
-    return EC_OK;
+    return ec_delta_step_split(proj, 1, Nin, conv_state, conv_w, a_log, dt_bias, norm_w, state, act, pos, n_seq, n_k,
+                               n_v, kern, stream);
 }

@@ -168,13 +168,26 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm_quant(const float* __restri
 // ------------------------------------------------------- SwiGLU + quantize
 // gu [M][2F] (gate rows then up rows) -> act (K = F).  grid (ceil(Kp/256), M),
 // thread = element.
+// NP > 1: gu holds NP partial sums [NP][M][2F] (a split-K matvec's output),
+// added in part order.
+template <int NP>
 __global__ __launch_bounds__(256) void k_swiglu_quant(const float* __restrict__ gu, uint8_t* __restrict__ act,
                                                       uint32_t M, uint32_t F, uint32_t xd_off) {
     const uint32_t Kp = round_up(F, 128);
     const uint32_t i = blockIdx.y, k = blockIdx.x * 256 + threadIdx.x;
     if (k >= Kp) return;  // whole 32-lane blocks leave together (Kp % 32 == 0)
     const float* g = gu + (size_t)i * 2 * F;
-    const float v = k < F ? silu(g[k]) * g[F + k] : 0.0f;
+    const size_t ps = (size_t)M * 2 * F;
+    float v = 0.0f;
+    if (k < F) {
+        float gp[NP], up[NP];
+#pragma unroll
+        for (int q = 0; q < NP; ++q) gp[q] = g[q * ps + k], up[q] = g[q * ps + F + k];
+        float a = gp[0], b = up[0];
+#pragma unroll
+        for (int q = 1; q < NP; ++q) a += gp[q], b += up[q];
+        v = silu(a) * b;
+    }
     store_act_q8_lane(v, act, (float*)(act + xd_off), M, Kp / 32, i, k);
 }
 
@@ -523,11 +536,29 @@ extern "C" int ec_glue_add_rmsnorm_quant(const float* x, const float* parts, uin
     }
 }
 
-extern "C" int ec_glue_swiglu_quant(const float* gu, void* act, uint32_t M, uint32_t F, void* stream) {
-    if (!gu || !act || M == 0 || M > 16 || F % 32) return ec_set_error(EC_ERR_ARG, "ec_glue_swiglu_quant");
+extern "C" int ec_glue_swiglu_quant_split(const float* gu, uint32_t nparts, void* act, uint32_t M, uint32_t F,
+                                          void* stream) {
+    if (!gu || !act || M == 0 || M > 16 || F % 32 || nparts == 0 || nparts > 8)
+        return ec_set_error(EC_ERR_ARG, "ec_glue_swiglu_quant");
     const ActLayout L = act_layout(EC_Q8_0, M, F);
-    EC_GLUE_LAUNCH(k_swiglu_quant, dim3((L.Kp + 255) / 256, M), dim3(256), 0, (hipStream_t)stream, gu,
-                   (uint8_t*)act, M, F, (uint32_t)L.xd_off);
+    const dim3 grid((L.Kp + 255) / 256, M);
+    const hipStream_t st = (hipStream_t)stream;
+    uint8_t* a = (uint8_t*)act;
+    const uint32_t xo = (uint32_t)L.xd_off;
+    switch (nparts) {
+        case 1: EC_GLUE_LAUNCH(k_swiglu_quant<1>, grid, dim3(256), 0, st, gu, a, M, F, xo);
+        case 2: EC_GLUE_LAUNCH(k_swiglu_quant<2>, grid, dim3(256), 0, st, gu, a, M, F, xo);
+        case 3: EC_GLUE_LAUNCH(k_swiglu_quant<3>, grid, dim3(256), 0, st, gu, a, M, F, xo);
+        case 4: EC_GLUE_LAUNCH(k_swiglu_quant<4>, grid, dim3(256), 0, st, gu, a, M, F, xo);
+        case 5: EC_GLUE_LAUNCH(k_swiglu_quant<5>, grid, dim3(256), 0, st, gu, a, M, F, xo);
+        case 6: EC_GLUE_LAUNCH(k_swiglu_quant<6>, grid, dim3(256), 0, st, gu, a, M, F, xo);
+        case 7: EC_GLUE_LAUNCH(k_swiglu_quant<7>, grid, dim3(256), 0, st, gu, a, M, F, xo);
+        default: EC_GLUE_LAUNCH(k_swiglu_quant<8>, grid, dim3(256), 0, st, gu, a, M, F, xo);
+    }
+}
+
+extern "C" int ec_glue_swiglu_quant(const float* gu, void* act, uint32_t M, uint32_t F, void* stream) {
+    return ec_glue_swiglu_quant_split(gu, 1, act, M, F, stream);
 }
 
 extern "C" int ec_glue_conv_gates(const float* proj, uint32_t Nin, float* conv_state, const float* conv_w,

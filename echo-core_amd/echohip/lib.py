@@ -50,6 +50,8 @@ _SIGS = {
     "ec_glue_rmsnorm_quant": [_vp, _vp, _vp, _u32, _u32, _vp],
     "ec_glue_add_rmsnorm_quant": [_vp, _vp, _u32, _vp, _vp, _vp, _u32, _u32, _vp],
     "ec_glue_swiglu_quant": [_vp, _vp, _u32, _u32, _vp],
+    "ec_glue_swiglu_quant_split": [_vp, _u32, _vp, _u32, _u32, _vp],
+    "ec_delta_step_split": [_vp, _u32, _u32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp],
     "ec_glue_conv_gates_chunk": [_vp, _u32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32,
                                  _vp],
     "ec_glue_rmsnorm_rows": [_vp, _vp, _vp, _u32, _u32, _vp],
@@ -189,6 +191,12 @@ class Lib:
         self._call("ec_delta_step", _ptr(proj), Nin, _ptr(conv_state), _ptr(conv_w), _ptr(a_log), _ptr(dt_bias),
                    _ptr(norm_w), _ptr(state), _ptr(act), _ptr(pos), n_seq, n_k, n_v, kern, self._stream(stream))
 
+    def delta_step_split(self, proj, nparts, Nin, conv_state, conv_w, a_log, dt_bias, norm_w, state, act, pos, n_seq,
+                         n_k, n_v, kern, stream=None):
+        self._call("ec_delta_step_split", _ptr(proj), nparts, Nin, _ptr(conv_state), _ptr(conv_w), _ptr(a_log),
+                   _ptr(dt_bias), _ptr(norm_w), _ptr(state), _ptr(act), _ptr(pos), n_seq, n_k, n_v, kern,
+                   self._stream(stream))
+
     def conv_gates(self, proj, Nin, conv_state, conv_w, a_log, dt_bias, q, k, v, dec, beta, pos, n_seq, n_k, n_v,
                    kern, stream=None):
         self._call("ec_glue_conv_gates", _ptr(proj), Nin, _ptr(conv_state), _ptr(conv_w), _ptr(a_log),
@@ -223,6 +231,9 @@ class Lib:
 
     def swiglu_quant(self, gu, act, M, F, stream=None):
         self._call("ec_glue_swiglu_quant", _ptr(gu), _ptr(act), M, F, self._stream(stream))
+
+    def swiglu_quant_split(self, gu, nparts, act, M, F, stream=None):
+        self._call("ec_glue_swiglu_quant_split", _ptr(gu), nparts, _ptr(act), M, F, self._stream(stream))
 
     def gemm_act_bytes(self, fmt, M, K):
         return self.L.ec_gemm_act_bytes(fmt, M, K)

@@ -207,6 +207,32 @@ uint32_t resid_split(uint32_t N, uint32_t K) {
     return std::min(nG >= 64 ? sp.second : sp.first, nG);
 }
 
+// K splits of the input projection of a delta-net block and of gate/up
+// (their consumers, the fused delta step and SwiGLU, add the partial sums).
+// Decode step on MI355X (4B-class, batch 8): 1.867 ms unsplit, 1.860 ms with
+// 4 and 2 (EC_IN_SPLIT / EC_GU_SPLIT override).
+uint32_t env_split(const char* name, uint32_t dflt) {
+    const char* v = getenv(name);
+    return std::clamp(v ? (uint32_t)atoi(v) : dflt, 1u, kMaxResidSplit);
+}
+uint32_t in_split() {
+    static const uint32_t v = env_split("EC_IN_SPLIT", 4);
+    return v;
+}
+uint32_t gu_split() {
+    static const uint32_t v = env_split("EC_GU_SPLIT", 2);
+    return v;
+}
+
+// A split-K projection into y ([ns][B][N]); ns is clamped to the K chunks.
+int mv_split(ec_engine* e, const Mat& m, const void* act, float* y, uint32_t& ns) {
+    ns = std::min(ns, (m.K + 127) / 128);
+    if (e->mv_bytes)
+        e->mv_bytes->push_back((double)gguf_bytes(m.N, m.K) + (double)e->B * (m.K + m.K / 32 * 4) +
+                               (double)e->B * m.N * 4 * ns);
+    return ec_matvec_split(EC_Q8_0, m.tiled, act, y, e->B, m.N, m.K, ns, e->st);
+}
+
 // Residual projection: partial sums into e->parts; returns the split count.
 int mv_resid(ec_engine* e, const Mat& m, const void* act, uint32_t& ns) {
     ns = resid_split(m.N, m.K);
@@ -243,10 +269,11 @@ int record_step(ec_engine* e) {
         EC_GLUE(norm(y.attn_norm));
         if (!y.attn) {
             const uint32_t Nin = e->nin_delta;
-            EC_TRY(mv(e, y.w_in, e->act_h, e->proj, Nin, 0));
+            uint32_t nsi = in_split();
+            EC_TRY(mv_split(e, y.w_in, e->act_h, e->proj, nsi));
             // conv + gates + delta rule + gated norm + quantize in one launch
-            EC_GLUE(ec_delta_step(e->proj, Nin, y.conv_state, y.conv_w, y.a_log, y.dt_bias, y.ssm_norm, y.ssm_state,
-                                 e->act_v, e->pos, B, e->n_k, e->n_v, c.conv_kernel, st));
+            EC_GLUE(ec_delta_step_split(e->proj, nsi, Nin, y.conv_state, y.conv_w, y.a_log, y.dt_bias, y.ssm_norm,
+                                       y.ssm_state, e->act_v, e->pos, B, e->n_k, e->n_v, c.conv_kernel, st));
             EC_TRY(mv_resid(e, y.w_out, e->act_v, ns));
         } else {
             const uint32_t Nin = e->nin_attn;
@@ -272,8 +299,9 @@ int record_step(ec_engine* e) {
             EC_TRY(mv_resid(e, y.w_out, e->act_q, ns));
         }
         EC_GLUE(norm(y.ffn_norm));
-        EC_TRY(mv(e, y.w_gu, e->act_h, e->gu, 2 * F, 0));
-        EC_GLUE(ec_glue_swiglu_quant(e->gu, e->act_f, B, F, st));
+        uint32_t nsg = gu_split();
+        EC_TRY(mv_split(e, y.w_gu, e->act_h, e->gu, nsg));
+        EC_GLUE(ec_glue_swiglu_quant_split(e->gu, nsg, e->act_f, B, F, st));
         EC_TRY(mv_resid(e, y.w_down, e->act_f, ns));
     }
     EC_GLUE(norm(e->final_norm));
@@ -368,7 +396,8 @@ extern "C" int ec_engine_create(const ec_engine_cfg* cfg, ec_engine** out) {
     if ((rc = dalloc(e, &e->embed, gguf_bytes(c.vocab, H))) || (rc = dalloc(e, &e->final_norm, H)) ||
         (rc = alloc_mat(e, e->lm_head, c.vocab, H)) || (rc = dalloc(e, &e->x, (size_t)B * H)) ||
         (rc = dalloc(e, &e->x2, (size_t)B * H)) || (rc = dalloc(e, &e->parts, (size_t)kMaxResidSplit * B * H)) ||
-        (rc = dalloc(e, &e->proj, (size_t)B * e->nin_max)) || (rc = dalloc(e, &e->gu, (size_t)B * 2 * e->F)) ||
+        (rc = dalloc(e, &e->proj, (size_t)kMaxResidSplit * B * e->nin_max)) ||
+        (rc = dalloc(e, &e->gu, (size_t)kMaxResidSplit * B * 2 * e->F)) ||
         (rc = dalloc(e, &e->core, (size_t)B * e->value_dim)) || (rc = dalloc(e, &e->q, (size_t)B * e->key_dim)) ||
         (rc = dalloc(e, &e->k, (size_t)B * e->key_dim)) || (rc = dalloc(e, &e->v, (size_t)B * e->value_dim)) ||
         (rc = dalloc(e, &e->dec, (size_t)B * e->n_v)) || (rc = dalloc(e, &e->beta, (size_t)B * e->n_v)) ||

@@ -177,6 +177,11 @@ int ec_delta_step(const float* proj, uint32_t Nin, float* conv_state, const floa
                   uint32_t n_seq, uint32_t n_k, uint32_t n_v, uint32_t kern, void* stream);
 /* seq_pos (may be NULL): sequence s is skipped entirely (state untouched, no
  * output written) when seq_pos[s] < 0. */
+/* ec_delta_step with the input projection given as nparts (1..8) partial sums
+ * proj[nparts][n_seq][Nin] (ec_matvec_split's output), added in part order. */
+int ec_delta_step_split(const float* proj, uint32_t nparts, uint32_t Nin, float* conv_state, const float* conv_w,
+                        const float* a_log, const float* dt_bias, const float* norm_w, float* state, void* act,
+                        const int32_t* pos, uint32_t n_seq, uint32_t n_k, uint32_t n_v, uint32_t kern, void* stream);
 
 /* ------------------------------------------------------------ decode-step glue
  * Fused per-token ops of the hybrid decoder (semantics in glue.hip); every
@@ -190,6 +195,8 @@ int ec_glue_rmsnorm_quant(const float* x, const float* w, void* act, uint32_t M,
 int ec_glue_add_rmsnorm_quant(const float* x, const float* parts, uint32_t nparts, float* x_out, const float* w,
                               void* act, uint32_t M, uint32_t H, void* stream);
 int ec_glue_swiglu_quant(const float* gu, void* act, uint32_t M, uint32_t F, void* stream);
+/* ec_glue_swiglu_quant over nparts (1..8) partial sums gu[nparts][M][2F], added in part order. */
+int ec_glue_swiglu_quant_split(const float* gu, uint32_t nparts, void* act, uint32_t M, uint32_t F, void* stream);
 /* conv_state [n_seq][kern][conv_dim] is a ring over positions: slot p % kern
  * holds the conv input of position p (all zero before position 0). */
 int ec_glue_conv_gates(const float* proj, uint32_t Nin, float* conv_state, const float* conv_w, const float* a_log,

@@ -49,6 +49,51 @@ def test_rmsnorm_quant(hip, oc, M, H):
         _check_q8(xq[i], xd[i], xq_r, xd_r)
 
 
+@pytest.mark.parametrize("ns", [2, 5])
+def test_split_inputs_equal_summed_inputs(hip, ns):
+    """ec_delta_step_split / ec_glue_swiglu_quant_split over ns partial sums ==
+    the one-part entry on the parts added in order in fp32, bit for bit."""
+    import torch
+    n_seq, n_k, n_v, kern = 3, 2, 4, 4
+    key_dim, value_dim = 128 * n_k, 128 * n_v
+    conv_dim = 2 * key_dim + value_dim
+    Nin = conv_dim + value_dim + 2 * n_v
+    rng = np.random.default_rng(9)
+    conv_w = dev((0.5 * rng.standard_normal(kern * conv_dim)).astype(np.float32))
+    a_log = dev(np.log(1 + 15 * rng.random(n_v)).astype(np.float32))
+    dt_bias = dev((0.1 * rng.standard_normal(n_v)).astype(np.float32))
+    norm_w = dev((1 + 0.1 * rng.standard_normal(128)).astype(np.float32))
+    S0 = (0.02 * rng.standard_normal(n_seq * n_v * 128 * 128)).astype(np.float32)
+    ring0 = (0.3 * rng.standard_normal(n_seq * kern * conv_dim)).astype(np.float32)
+    parts = rng.standard_normal((ns, n_seq, Nin)).astype(np.float32)
+    total = parts[0].copy()
+    for q in range(1, ns):
+        total = total + parts[q]
+    pos = dev(np.array([5, -1, 2], np.int32))
+    out = []
+    for split in (True, False):
+        st, ring = dev(S0), dev(ring0)
+        act = empty(hip.act_bytes(Q8_0, n_seq, value_dim), torch.uint8)
+        if split:
+            hip.delta_step_split(dev(parts), ns, Nin, ring, conv_w, a_log, dt_bias, norm_w, st, act, pos, n_seq, n_k,
+                                 n_v, kern)
+        else:
+            hip.delta_step(dev(total), Nin, ring, conv_w, a_log, dt_bias, norm_w, st, act, pos, n_seq, n_k, n_v, kern)
+        out.append([host(st).view(np.uint32), host(ring).view(np.uint32), host(act)])
+    for a, b in zip(*out):
+        assert np.array_equal(a, b)
+    M, F = 5, 384
+    gu = rng.standard_normal((ns, M, 2 * F)).astype(np.float32)
+    gsum = gu[0].copy()
+    for q in range(1, ns):
+        gsum = gsum + gu[q]
+    a1 = empty(hip.act_bytes(Q8_0, M, F), torch.uint8)
+    a2 = empty(hip.act_bytes(Q8_0, M, F), torch.uint8)
+    hip.swiglu_quant_split(dev(gu), ns, a1, M, F)
+    hip.swiglu_quant(dev(gsum), a2, M, F)
+    assert np.array_equal(host(a1), host(a2))
+
+
 @pytest.mark.parametrize("M,H,ns", [(8, 2560, 6), (8, 2560, 4), (3, 256, 1), (16, 128, 8), (2, 5120, 3)])
 def test_add_rmsnorm_quant(hip, oc, M, H, ns):
     """x_out = ((x + p0) + p1) + ... in fp32 (exact order), then RMSNorm + quantize of x_out."""
