@@ -224,9 +224,14 @@ def run_all(hip, quick=False):
 # ---------------------------------------------------------------- PMC traffic
 # Matvec shapes of one decode step of the 4B-class hybrid decoder (M = 8 token
 # rows): (name, N output rows, K, launches per step).
-DECODE_STEP_MATVECS = [("delta_in", 12352, 2560, 24), ("delta_out", 2560, 4096, 24), ("attn_in", 6144, 2560, 8),
-                       ("attn_out", 2560, 4096, 8), ("ffn_gate_up", 18432, 2560, 32), ("ffn_down", 2560, 9216, 32),
-                       ("lm_head", 151936, 2560, 1)]
+# (name, N, K, launches per step, K splits): the decode step of the 4B-class
+# decoder at batch 8, with the split-K counts the engine uses (host/engine.cpp:
+# 4 for the delta-net input projection, 2 for gate/up, 3 for the projections
+# that add into the residual; a split writes one partial output per split).
+DECODE_STEP_MATVECS = [("delta_in", 12352, 2560, 24, 4), ("delta_out", 2560, 4096, 24, 3),
+                       ("attn_in", 6144, 2560, 8, 1), ("attn_out", 2560, 4096, 8, 3),
+                       ("ffn_gate_up", 18432, 2560, 32, 2), ("ffn_down", 2560, 9216, 32, 3),
+                       ("lm_head", 151936, 2560, 1, 1)]
 PMC_LAUNCHES = 3
 CALIB_BYTES = 256 << 20
 
@@ -238,7 +243,7 @@ def pmc_workload(hip, M=8):
     traffic: k_stream_read of CALIB_BYTES twice (reads) and a CALIB_BYTES
     fill twice (writes)."""
     st = torch.cuda.current_stream().cuda_stream
-    for name, N, K, _ in DECODE_STEP_MATVECS:
+    for name, N, K, _, ns in DECODE_STEP_MATVECS:
         tb = hip.tiled_bytes(L.Q8_0, N, K)
         n_copies = max(PMC_LAUNCHES, math.ceil(ROTATE_BYTES / tb) + 1)
         Wd = torch.empty(N * K // 32 * 34, dtype=torch.uint8, device="cuda")
@@ -251,10 +256,10 @@ def pmc_workload(hip, M=8):
         x = torch.from_numpy(synth.activations(1, M * K)).cuda()
         act = torch.empty(hip.act_bytes(L.Q8_0, M, K), dtype=torch.uint8, device="cuda")
         hip.quantize_act(L.Q8_0, x, act, M, K, stream=st)
-        y = torch.empty(M * N, dtype=torch.float32, device="cuda")
+        y = torch.empty(ns * M * N, dtype=torch.float32, device="cuda")
         torch.cuda.synchronize()
         for i in range(PMC_LAUNCHES):
-            hip.matvec(L.Q8_0, tiled[(i * 7919) % n_copies], act, y, M, N, K, stream=st)
+            hip.matvec_split(L.Q8_0, tiled[(i * 7919) % n_copies], act, y, M, N, K, ns, stream=st)
             torch.cuda.synchronize()
         del tiled
         torch.cuda.empty_cache()
@@ -281,9 +286,9 @@ def pmc_summary(csv_path, counter):
     fl = [float(r["Counter_Value"]) for r in rows if "FillFunctor<unsigned char>" in r["Kernel_Name"]][-2:]
     assert len(mv) == PMC_LAUNCHES * len(DECODE_STEP_MATVECS), len(mv)
     res = {"counter": counter, "shapes": {}}
-    for j, (name, N, K, per_step) in enumerate(DECODE_STEP_MATVECS):
+    for j, (name, N, K, per_step, ns) in enumerate(DECODE_STEP_MATVECS):
         v = mv[j * PMC_LAUNCHES:(j + 1) * PMC_LAUNCHES]
-        res["shapes"][name] = {"N": N, "K": K, "per_step": per_step, "KiB": [round(x, 1) for x in v]}
+        res["shapes"][name] = {"N": N, "K": K, "per_step": per_step, "splits": ns, "KiB": [round(x, 1) for x in v]}
     res["calib_read_KiB"] = [round(x, 1) for x in rd]
     res["calib_fill_KiB"] = [round(x, 1) for x in fl]
     res["calib_bytes"] = CALIB_BYTES

@@ -227,18 +227,18 @@ uint32_t gu_split() {
 // A split-K projection into y ([ns][B][N]); ns is clamped to the K chunks.
 int mv_split(ec_engine* e, const Mat& m, const void* act, float* y, uint32_t& ns) {
     ns = std::min(ns, (m.K + 127) / 128);
-    if (e->mv_bytes)
+    if (e->mv_bytes)  // the output counted once (the extra partial sums are not algorithmic bytes)
         e->mv_bytes->push_back((double)gguf_bytes(m.N, m.K) + (double)e->B * (m.K + m.K / 32 * 4) +
-                               (double)e->B * m.N * 4 * ns);
+                               (double)e->B * m.N * 4);
     return ec_matvec_split(EC_Q8_0, m.tiled, act, y, e->B, m.N, m.K, ns, e->st);
 }
 
 // Residual projection: partial sums into e->parts; returns the split count.
 int mv_resid(ec_engine* e, const Mat& m, const void* act, uint32_t& ns) {
     ns = resid_split(m.N, m.K);
-    if (e->mv_bytes)
+    if (e->mv_bytes)  // the output counted once, as in mv_split
         e->mv_bytes->push_back((double)gguf_bytes(m.N, m.K) + (double)e->B * (m.K + m.K / 32 * 4) +
-                               (double)e->B * m.N * 4 * ns);
+                               (double)e->B * m.N * 4);
     return ec_matvec_split(EC_Q8_0, m.tiled, act, e->parts, e->B, m.N, m.K, ns, e->st);
 }
 
