@@ -27,6 +27,15 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
+// x*x rounded on its own, never contracted into a following add: summed by a
+// butterfly reduction, a contracted square would make the first level an FMA
+// in one lane of each pair and a separately rounded sum in the other, so the
+// lanes' totals could differ in the last bit.
+__device__ __forceinline__ float sq_rn(float x) {
+#pragma clang fp contract(off)
+    return x * x;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
     return v;
@@ -55,6 +64,20 @@ __device__ __forceinline__ int8_t q_tail(float x, float scale) {
 }
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+// RoPE of element d paired with its neighbour d^1 (value `other`) at angle
+// ang: even d -> x cos - other sin, odd d -> other sin + x cos.  Products and
+// the sum are rounded separately (never contracted into an FMA), so every
+// kernel that rotates rounds the same way.
+__device__ __forceinline__ float rope_rot(float x, float other, uint32_t d, float sn, float cs) {
+#pragma clang fp contract(off)
+    return (d & 1) ? other * sn + x * cs : x * cs - other * sn;
+}
+__device__ __forceinline__ float rope_pair(float x, float other, uint32_t d, float ang) {
+    float sn, cs;
+    sincosf(ang, &sn, &cs);
+    return rope_rot(x, other, d, sn, cs);
+}
 
 // Causal depthwise conv of channel c at position p over a ring state
 // [kern][conv_dim] (slot q % kern = input of position q, zeros before 0):

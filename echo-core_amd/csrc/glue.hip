@@ -389,16 +389,13 @@ __global__ __launch_bounds__(256) void k_qk_rope_append(const float* __restrict_
     if (head == 0 && d == 0) ctx[s] = (p >= 0 && (uint32_t)p < max_ctx) ? p + 1 : 0;
     if (p < 0 || (uint32_t)p >= max_ctx) return;
     if (norm) {
-        const float ss = block_sum256(val * val, sh);
+        const float ss = block_sum256(sq_rn(val), sh);
         const float inv = 1.0f / sqrtf(ss / (float)HD + 1e-6f);
         val = val * inv * nw;
     }
     if (is_q || is_k) {
         const float other = __shfl_xor(val, 1);
-        const float ang = (float)p * ifr;
-        float sn, cs;
-        sincosf(ang, &sn, &cs);
-        val = (d & 1) ? other * sn + val * cs : val * cs - other * sn;
+        val = rope_pair(val, other, d, (float)p * ifr);
     }
     if (is_q) {
         if (qa) {

@@ -49,6 +49,66 @@ def test_rmsnorm_quant(hip, oc, M, H):
         _check_q8(xq[i], xd[i], xq_r, xd_r)
 
 
+@pytest.mark.parametrize("use_norms", [True, False])
+def test_qk_rope_append_matches_oracle(hip, oc, use_norms):
+    """ec_glue_qk_rope_append (fp32 q output): head RMSNorm + RoPE of q and k
+    (engine.zig head norms / rope, oracle oc_head_rmsnorm + oc_rope) within
+    fp32 rounding (sincosf vs libm, norm summation order); V rows appended bit
+    for bit as the oracle's per-token quantizer; K rows within one quantum;
+    ctx = pos + 1, and nothing appended for pos < 0 or pos >= max_ctx."""
+    import torch
+    n_heads, n_kv, HD, max_ctx = 8, 2, 256, 40
+    pos = np.array([0, 17, 39, -1, 40], np.int32)
+    n_seq = pos.size
+    Nin = (n_heads + 2 * n_kv) * HD
+    seq_stride = max_ctx * n_kv * HD
+    rng = np.random.default_rng(3)
+    proj = (2 * rng.standard_normal((n_seq, Nin))).astype(np.float32)
+    qn = (1 + 0.1 * rng.standard_normal(HD)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(HD)).astype(np.float32)
+    inv = np.zeros(HD // 2, np.float32)
+    oc.lib.oc_rope_inv_freq(inv, HD, 10000.0)
+    keys = empty(n_seq * seq_stride, torch.int8)
+    vals = empty(n_seq * seq_stride, torch.int8)
+    ks = empty(n_seq * max_ctx * n_kv, torch.float32)
+    vs = empty(n_seq * max_ctx * n_kv, torch.float32)
+    ctx = dev(np.full(n_seq, 9, np.int32))
+    q_out = empty(n_seq * n_heads * HD, torch.float32)
+    hip.qk_rope_append(dev(proj), Nin, dev(qn), dev(kn), use_norms, use_norms, dev(inv), dev(pos), q_out, None, None,
+                       keys, vals, ks, vs, ctx, n_seq, seq_stride, max_ctx, n_heads, n_kv, HD)
+    assert host(ctx).tolist() == [1, 18, 40, 0, 0]
+    qo = host(q_out).reshape(n_seq, n_heads * HD)
+    kh = host(keys).reshape(n_seq, max_ctx, n_kv * HD)
+    vh = host(vals).reshape(n_seq, max_ctx, n_kv * HD)
+    ksh = host(ks).reshape(n_seq, max_ctx, n_kv)
+    vsh = host(vs).reshape(n_seq, max_ctx, n_kv)
+    for s, p in enumerate(pos.tolist()):
+        if p < 0 or p >= max_ctx:
+            assert not kh[s].any() and not vh[s].any() and not ksh[s].any()
+            continue
+        q = proj[s, :n_heads * HD].copy()
+        k = proj[s, n_heads * HD:(n_heads + n_kv) * HD].copy()
+        v = proj[s, (n_heads + n_kv) * HD:].copy()
+        if use_norms:
+            oc.lib.oc_head_rmsnorm(q, qn, n_heads, HD)
+            oc.lib.oc_head_rmsnorm(k, kn, n_kv, HD)
+        oc.lib.oc_rope(q, n_heads, HD, p, inv)
+        oc.lib.oc_rope(k, n_kv, HD, p, inv)
+        assert rel_l2(qo[s], q) < 2e-6, (s, rel_l2(qo[s], q))
+        kr = np.zeros(max_ctx * n_kv * HD, np.int8)
+        vr = np.zeros(max_ctx * n_kv * HD, np.int8)
+        ksr = np.zeros(max_ctx * n_kv, np.float32)
+        vsr = np.zeros(max_ctx * n_kv, np.float32)
+        oc.kv_append(k, v, kr, vr, ksr, vsr, p, n_kv, HD)
+        kr, vr = kr.reshape(max_ctx, -1), vr.reshape(max_ctx, -1)
+        ksr, vsr = ksr.reshape(max_ctx, -1), vsr.reshape(max_ctx, -1)
+        assert np.array_equal(vh[s, p], vr[p]) and np.array_equal(vsh[s, p].view(np.uint32), vsr[p].view(np.uint32))
+        assert np.abs(kh[s, p].astype(np.int32) - kr[p].astype(np.int32)).max() <= 1
+        assert np.max(np.abs(ksh[s, p] - ksr[p]) / ksr[p]) < 1e-5
+        others = [t for t in range(max_ctx) if t != p]
+        assert not kh[s, others].any() and not vh[s, others].any()
+
+
 @pytest.mark.parametrize("ns", [2, 5])
 def test_split_inputs_equal_summed_inputs(hip, ns):
     """ec_delta_step_split / ec_glue_swiglu_quant_split over ns partial sums ==
