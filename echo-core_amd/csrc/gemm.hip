@@ -63,14 +63,17 @@ __host__ __device__ inline XtLayout xt_layout(int fmt, uint32_t M, uint32_t K) {
 }
 
 // ----------------------------------------------------------- activation prep
-// grid (Kp/32 blocks, Mp tokens), block 32: one lane per element of a block.
-// Q8_0: block b holds x[m][32b .. 32b+32); Q4_K: sub-block s of super-block
-// b/8 holds the 32 positions pos(s, i) (reference order, oc_q4k_pos).
+// grid (ceil(Kp/32 / 8), Mp tokens), block 256: eight 32-lane groups, one
+// quantization block each, one lane per element.  Q8_0: block b holds
+// x[m][32b .. 32b+32); Q4_K: sub-block s of super-block b/8 holds the 32
+// positions pos(s, i) (reference order, oc_q4k_pos).  Each run of 8 bytes of
+// the tiled layout is gathered with shuffles and stored by one lane.
 template <bool Q4>
-__global__ __launch_bounds__(32) void k_gemm_quantize_x(const float* __restrict__ x, uint8_t* __restrict__ xt,
-                                                        uint32_t M, uint32_t K, uint32_t ldx, uint32_t nch,
-                                                        uint32_t nbp, size_t xd_off, size_t dxs_off) {
-    const uint32_t b = blockIdx.x, m = blockIdx.y, i = threadIdx.x;
+__global__ __launch_bounds__(256) void k_gemm_quantize_x(const float* __restrict__ x, uint8_t* __restrict__ xt,
+                                                         uint32_t M, uint32_t K, uint32_t ldx, uint32_t nch,
+                                                         uint32_t nbp, size_t xd_off, size_t dxs_off) {
+    const uint32_t b = blockIdx.x * 8 + (threadIdx.x >> 5), m = blockIdx.y, i = threadIdx.x & 31;
+    if (b >= nbp) return;  // whole 32-lane groups leave together
     uint32_t k;
     if constexpr (Q4) {
         const uint32_t s = b % 8;  // sub-block of super-block b/8
@@ -88,19 +91,27 @@ __global__ __launch_bounds__(32) void k_gemm_quantize_x(const float* __restrict_
     const float inv = __fdiv_rn(1.0f, scale);
     const int8_t q = q_body(v, inv);  // a 32-element row: all elements are in whole 8-chunks
     const uint32_t T = m / 16, r = m % 16;
-    uint8_t* dst;
+    // 4 consecutive elements' bytes, gathered at the first lane of each 4
+    const uint32_t qb = (uint8_t)q;
+    const uint32_t w4 = qb | (__shfl_down(qb, 1, 32) << 8) | (__shfl_down(qb, 2, 32) << 16) |
+                        (__shfl_down(qb, 3, 32) << 24);
     if constexpr (Q4) {
-        // element e = i of the sub-block: lane group g and byte within the lane's 8 bytes
-        const uint32_t s = b % 8, e = i;
-        const uint32_t g = (e % 16) / 4, byte = (e < 16) ? e % 4 : 4 + e % 4;
-        const uint32_t l = r + 16 * g;
-        dst = xt + ((size_t)T * nch + b / 8) * 4096 + (s / 2) * 1024 + 16 * l + 8 * (s % 2) + byte;
+        // elements 4g..4g+3 are bytes 0..3 and elements 16+4g..16+4g+3 bytes
+        // 4..7 of lane r + 16g of sub-block pair s/2
+        const uint32_t hi = __shfl_down(w4, 16, 32);
+        if (i < 16 && (i & 3) == 0) {
+            const uint32_t s = b % 8, l = r + 16 * (i / 4);
+            *(uint2*)(xt + ((size_t)T * nch + b / 8) * 4096 + (s / 2) * 1024 + 16 * l + 8 * (s % 2)) =
+                make_uint2(w4, hi);
+        }
     } else {
-        const uint32_t G = b / 4, j = b % 4, g = i / 8;
-        const uint32_t l = r + 16 * g;
-        dst = xt + ((size_t)T * nch + G) * 2048 + (j / 2) * 1024 + 16 * l + 8 * (j % 2) + i % 8;
+        // elements 8g..8g+7 are the 8 bytes of lane r + 16g
+        const uint32_t hi = __shfl_down(w4, 4, 32);
+        if ((i & 7) == 0) {
+            const uint32_t G = b / 4, j = b % 4, l = r + 16 * (i / 8);
+            *(uint2*)(xt + ((size_t)T * nch + G) * 2048 + (j / 2) * 1024 + 16 * l + 8 * (j % 2)) = make_uint2(w4, hi);
+        }
     }
-    *dst = (uint8_t)q;
     int sum = q;
     if constexpr (Q4) {
 #pragma unroll
@@ -366,10 +377,10 @@ extern "C" int ec_gemm_quantize_act(int fmt, const float* x, void* act, uint32_t
     const XtLayout L = xt_layout(fmt, M, K);
     const uint32_t nbp = L.Kp / 32;
     if (fmt == EC_Q8_0)
-        hipLaunchKernelGGL(k_gemm_quantize_x<false>, dim3(nbp, L.Mp), dim3(32), 0, (hipStream_t)stream, x,
+        hipLaunchKernelGGL(k_gemm_quantize_x<false>, dim3((nbp + 7) / 8, L.Mp), dim3(256), 0, (hipStream_t)stream, x,
                            (uint8_t*)act, M, K, K, L.nch, nbp, L.xd_off, L.dxs_off);
     else
-        hipLaunchKernelGGL(k_gemm_quantize_x<true>, dim3(nbp, L.Mp), dim3(32), 0, (hipStream_t)stream, x,
+        hipLaunchKernelGGL(k_gemm_quantize_x<true>, dim3((nbp + 7) / 8, L.Mp), dim3(256), 0, (hipStream_t)stream, x,
                            (uint8_t*)act, M, K, K, L.nch, nbp, L.xd_off, L.dxs_off);
     EC_CHECK_LAUNCH();
     return EC_OK;
