@@ -146,16 +146,15 @@ def main() -> int:
     prompts = [synth.randint(synth.stream_seed(args.seed, 2000 + s), int(lens[s]), 0, cfg.vocab - 1).astype(np.int32)
                for s in range(B)]
 
-    # ---- prefill (not part of `value`); a one-token prefill first allocates the
-    # engine's prefill buffers, then the state is reset
+    # ---- prefill (not part of `value`); a two-sequence prefill first allocates
+    # the engine's prefill lanes, then the state is reset
     if args.prefill == "chunked":
-        eng.prefill(0, prompts[0][:1], 0)
+        eng.prefill_batch([(0, prompts[0][:1], 0), (1, prompts[1][:1], 0)])
         eng.reset()
     t0 = time.perf_counter()
     T = int(lens.max())
-    if args.prefill == "chunked":
-        for s in range(B):
-            eng.prefill(s, prompts[s], 0)
+    if args.prefill == "chunked":  # all prompts, two sequences' chunks in flight at a time
+        eng.prefill_batch([(s, prompts[s], 0) for s in range(B)])
         eng.sync()
     else:  # token loop through the decode graph, ragged
         for t in range(T):
@@ -246,7 +245,7 @@ def main() -> int:
         "config": {"workload": "hybrid 4B-class Q8_0 decoder: 24 delta-net + 8 attention blocks, hidden 2560, "
                                "ffn 9216, vocab 151936; ragged batch of 8, greedy decode",
                    "global_batch": B, "prompt_lens": lens.tolist(), "decode_steps": W + K,
-                   "prefill": ("chunked (512-token int8-MFMA GEMM chunks per sequence)" if args.prefill == "chunked"
+                   "prefill": ("chunked (512-token int8-MFMA GEMM chunks per sequence, two sequences in flight)" if args.prefill == "chunked"
                                else "token loop through the decode graph"),
                    "prefill_tok_s": round(prefill_tps, 1),
                    "step_hbm_bytes": int(step_bytes),

@@ -74,6 +74,7 @@ class Engine:
         L.ec_engine_set_inputs.argtypes = [vp, vp, vp, u32]
         L.ec_engine_step.argtypes = [vp, i32]
         L.ec_engine_prefill.argtypes = [vp, u32, vp, u32, i32]
+        L.ec_engine_prefill_batch.argtypes = [vp, u32, vp, vp, vp, vp]
         L.ec_engine_sync.argtypes = [vp]
         L.ec_engine_get_tokens.argtypes = [vp, vp, vp]
         L.ec_engine_get_logits.argtypes = [vp, vp, u32]
@@ -138,6 +139,16 @@ class Engine:
         """Chunked prefill of one sequence (ec_engine_prefill): tokens at positions pos0 .. pos0+n-1."""
         t = np.ascontiguousarray(tokens, dtype=np.int32)
         self._check(self.L.ec_engine_prefill(self.h, seq, t.ctypes.data, t.size, pos0), "prefill")
+
+    def prefill_batch(self, jobs):
+        """ec_engine_prefill_batch: jobs = [(seq, tokens, pos0), ...], distinct sequences."""
+        toks = [np.ascontiguousarray(t, dtype=np.int32) for _, t, _ in jobs]
+        seqs = np.array([j[0] for j in jobs], np.uint32)
+        lens = np.array([t.size for t in toks], np.uint32)
+        pos0 = np.array([j[2] for j in jobs], np.int32)
+        ptrs = (C.c_void_p * len(toks))(*[t.ctypes.data for t in toks])
+        self._check(self.L.ec_engine_prefill_batch(self.h, len(toks), seqs.ctypes.data, C.cast(ptrs, C.c_void_p),
+                                                   lens.ctypes.data, pos0.ctypes.data), "prefill_batch")
 
     def step(self, graph: bool = True):
         self._check(self.L.ec_engine_step(self.h, int(graph)), "step")

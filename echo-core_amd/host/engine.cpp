@@ -114,14 +114,20 @@ struct ec_engine {
     // matvec-only recording (profiling): skip every other launch, collect bytes
     bool mv_only = false;
     std::vector<double>* mv_bytes = nullptr;
-    // chunked prefill buffers (allocated on the first ec_engine_prefill):
-    // rows of up to kPrefillChunk tokens of one sequence
-    static constexpr uint32_t kPrefillChunk = 512, kPrefillAttnSlots = 128;
-    bool pf_ready = false;
-    float *pf_x = nullptr, *pf_n = nullptr, *pf_proj = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
-    float *pf_dec = nullptr, *pf_beta = nullptr, *pf_core = nullptr, *pf_gu = nullptr, *pf_attn = nullptr;
-    void *pf_act = nullptr, *pf_ws = nullptr;
-    int32_t *pf_tok = nullptr, *pf_pos = nullptr, *pf_ctx = nullptr;
+    // chunked prefill: lanes of scratch rows (up to kPrefillChunk tokens of
+    // one sequence each) with their own stream, allocated on first use; lane
+    // 0 runs on st.  Several sequences' chunks run concurrently on the lanes.
+    static constexpr uint32_t kPrefillChunk = 512, kPrefillAttnSlots = 128, kPrefillLanes = 2;
+    struct PrefillLane {
+        bool ready = false;
+        hipStream_t st = nullptr;
+        float *x = nullptr, *n = nullptr, *proj = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
+        float *dec = nullptr, *beta = nullptr, *core = nullptr, *gu = nullptr, *attn = nullptr;
+        void *act = nullptr, *ws = nullptr, *act1 = nullptr;  // act1: one row, for the last token's logits
+        int32_t *tok = nullptr, *pos = nullptr, *ctx = nullptr;
+        std::vector<int32_t> h_pos;
+    };
+    PrefillLane pf[kPrefillLanes];
 };
 
 namespace {
@@ -443,6 +449,11 @@ extern "C" int ec_engine_get_config(const ec_engine* e, ec_engine_cfg* out) {
 extern "C" void ec_engine_destroy(ec_engine* e) {
     if (!e) return;
     if (e->st) (void)hipStreamSynchronize(e->st);
+    for (uint32_t i = 1; i < ec_engine::kPrefillLanes; ++i)
+        if (e->pf[i].st) {
+            (void)hipStreamSynchronize(e->pf[i].st);
+            (void)hipStreamDestroy(e->pf[i].st);
+        }
     destroy_graph(e);
     for (void* p : e->allocs) (void)hipFree(p);
     if (e->h_io) (void)hipHostFree(e->h_io);
@@ -740,115 +751,181 @@ extern "C" size_t ec_engine_weight_bytes(const ec_engine* e) { return e ? e->wei
 
 // ------------------------------------------------------------ chunked prefill
 namespace {
-int prefill_alloc(ec_engine* e) {
-    if (e->pf_ready) return EC_OK;
+using Lane = ec_engine::PrefillLane;
+
+int prefill_alloc(ec_engine* e, Lane& L, uint32_t i) {
+    if (L.ready) return EC_OK;
     const size_t C = ec_engine::kPrefillChunk;
     const size_t wide = std::max({(size_t)e->H, (size_t)e->F, (size_t)e->value_dim, (size_t)e->q_dim});
     int rc;
-    if ((rc = dalloc(e, &e->pf_x, C * e->H)) || (rc = dalloc(e, &e->pf_n, C * wide)) ||
-        (rc = dalloc(e, &e->pf_proj, C * e->nin_max)) || (rc = dalloc(e, &e->pf_gu, C * 2 * (size_t)e->F)) ||
-        (rc = dalloc(e, &e->pf_act, ec_gemm_act_bytes(EC_Q8_0, (uint32_t)C, (uint32_t)wide))) ||
-        (rc = dalloc(e, &e->pf_tok, C)) || (rc = dalloc(e, &e->pf_pos, C)) || (rc = dalloc(e, &e->pf_ctx, C)))
+    if (i == 0) {
+        L.st = e->st;
+    } else if (!L.st) {
+        EC_HIP(hipStreamCreateWithFlags(&L.st, hipStreamNonBlocking));
+    }
+    if ((rc = dalloc(e, &L.x, C * e->H)) || (rc = dalloc(e, &L.n, C * wide)) ||
+        (rc = dalloc(e, &L.proj, C * e->nin_max)) || (rc = dalloc(e, &L.gu, C * 2 * (size_t)e->F)) ||
+        (rc = dalloc(e, &L.act, ec_gemm_act_bytes(EC_Q8_0, (uint32_t)C, (uint32_t)wide))) ||
+        (rc = dalloc(e, &L.act1, ec_act_bytes(EC_Q8_0, 1, e->H))) || (rc = dalloc(e, &L.tok, C)) ||
+        (rc = dalloc(e, &L.pos, C)) || (rc = dalloc(e, &L.ctx, C)))
         return rc;
     if (e->value_dim &&
-        ((rc = dalloc(e, &e->pf_q, C * e->key_dim)) || (rc = dalloc(e, &e->pf_k, C * e->key_dim)) ||
-         (rc = dalloc(e, &e->pf_v, C * e->value_dim)) || (rc = dalloc(e, &e->pf_dec, C * e->n_v)) ||
-         (rc = dalloc(e, &e->pf_beta, C * e->n_v)) || (rc = dalloc(e, &e->pf_core, C * e->value_dim))))
+        ((rc = dalloc(e, &L.q, C * e->key_dim)) || (rc = dalloc(e, &L.k, C * e->key_dim)) ||
+         (rc = dalloc(e, &L.v, C * e->value_dim)) || (rc = dalloc(e, &L.dec, C * e->n_v)) ||
+         (rc = dalloc(e, &L.beta, C * e->n_v)) || (rc = dalloc(e, &L.core, C * e->value_dim))))
         return rc;
-    if ((rc = dalloc(e, &e->pf_attn, C * e->q_dim)) ||
-        (rc = dalloc(e, &e->pf_ws, ec_attn_ws_bytes(ec_engine::kPrefillAttnSlots, e->c.n_heads, e->c.head_dim,
-                                                    e->c.max_ctx))))
+    if ((rc = dalloc(e, &L.attn, C * e->q_dim)) ||
+        (rc = dalloc(e, &L.ws, ec_attn_ws_bytes(ec_engine::kPrefillAttnSlots, e->c.n_heads, e->c.head_dim,
+                                                e->c.max_ctx))))
         return rc;
-    e->pf_ready = true;
+    L.h_pos.resize(C);
+    L.ready = true;
     return EC_OK;
 }
 
 // y[T][N] (+)= act(x rows) . W  on int8 MFMA (x fp32 [T][K] quantized per 32-block)
-int gemm_rows(ec_engine* e, const Mat& m, const float* x, float* y, uint32_t T, uint32_t ldy, int acc) {
-    EC_TRY(ec_gemm_quantize_act(EC_Q8_0, x, e->pf_act, T, m.K, e->st));
-    return ec_gemm(EC_Q8_0, m.tiled, e->pf_act, y, T, m.N, m.K, ldy, acc, e->st);
+int gemm_rows(Lane& L, const Mat& m, const float* x, float* y, uint32_t T, uint32_t ldy, int acc) {
+    EC_TRY(ec_gemm_quantize_act(EC_Q8_0, x, L.act, T, m.K, L.st));
+    return ec_gemm(EC_Q8_0, m.tiled, L.act, y, T, m.N, m.K, ldy, acc, L.st);
 }
 
-// One chunk of T tokens of sequence s at positions p .. p+T-1 through every block.
-int prefill_chunk(ec_engine* e, uint32_t s, uint32_t T, uint32_t p) {
+// One chunk of T tokens of sequence s at positions p .. p+T-1 through every
+// block, on the lane's stream (L.tok / L.pos already hold the chunk).
+int prefill_chunk(ec_engine* e, Lane& L, uint32_t s, uint32_t T, uint32_t p) {
     const ec_engine_cfg& c = e->c;
     const uint32_t H = e->H, F = e->F;
-    hipStream_t st = e->st;
-    EC_TRY(ec_glue_embed(e->embed, e->pf_tok, e->pf_x, T, H, c.vocab, st));
+    hipStream_t st = L.st;
+    EC_TRY(ec_glue_embed(e->embed, L.tok, L.x, T, H, c.vocab, st));
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         Layer& y = e->L[l];
-        EC_TRY(ec_glue_rmsnorm_rows(e->pf_x, y.attn_norm, e->pf_n, T, H, st));
+        EC_TRY(ec_glue_rmsnorm_rows(L.x, y.attn_norm, L.n, T, H, st));
         if (!y.attn) {
             const uint32_t Nin = e->nin_delta;
-            EC_TRY(gemm_rows(e, y.w_in, e->pf_n, e->pf_proj, T, Nin, 0));
+            EC_TRY(gemm_rows(L, y.w_in, L.n, L.proj, T, Nin, 0));
             float* ring = y.conv_state + (size_t)s * c.conv_kernel * e->conv_dim;
             float* state = y.ssm_state + (size_t)s * e->n_v * 128 * 128;
-            EC_TRY(ec_glue_conv_gates_chunk(e->pf_proj, Nin, ring, y.conv_w, y.a_log, y.dt_bias, e->pf_q, e->pf_k,
-                                            e->pf_v, e->pf_dec, e->pf_beta, T, p, e->n_k, e->n_v, c.conv_kernel, st));
-            EC_TRY(ec_deltanet(state, e->pf_q, e->pf_k, e->pf_v, e->pf_dec, e->pf_beta, e->pf_core, T, 1, e->n_v,
-                               e->n_k, 128, 128, nullptr, st));
-            EC_TRY(ec_glue_gated_norm_rows(e->pf_core, e->pf_proj, Nin, e->conv_dim, y.ssm_norm, e->pf_n, T, e->n_v,
-                                           st));
-            EC_TRY(gemm_rows(e, y.w_out, e->pf_n, e->pf_x, T, H, 1));
+            EC_TRY(ec_glue_conv_gates_chunk(L.proj, Nin, ring, y.conv_w, y.a_log, y.dt_bias, L.q, L.k, L.v, L.dec,
+                                            L.beta, T, p, e->n_k, e->n_v, c.conv_kernel, st));
+            EC_TRY(ec_deltanet(state, L.q, L.k, L.v, L.dec, L.beta, L.core, T, 1, e->n_v, e->n_k, 128, 128, nullptr,
+                               st));
+            EC_TRY(ec_glue_gated_norm_rows(L.core, L.proj, Nin, e->conv_dim, y.ssm_norm, L.n, T, e->n_v, st));
+            EC_TRY(gemm_rows(L, y.w_out, L.n, L.x, T, H, 1));
         } else {
             const uint32_t Nin = e->nin_attn;
-            EC_TRY(gemm_rows(e, y.w_in, e->pf_n, e->pf_proj, T, Nin, 0));
+            EC_TRY(gemm_rows(L, y.w_in, L.n, L.proj, T, Nin, 0));
             int8_t* keys = y.keys + (size_t)s * e->seq_stride;
             int8_t* vals = y.vals + (size_t)s * e->seq_stride;
             float* ks = y.ks + (size_t)s * c.max_ctx * c.n_kv;
             float* vs = y.vs + (size_t)s * c.max_ctx * c.n_kv;
             // slots = the chunk's tokens sharing sequence s's cache (seq_stride 0)
-            EC_TRY(ec_glue_qk_rope_append(e->pf_proj, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn, e->inv_freq,
-                                          e->pf_pos, e->pf_n, nullptr, nullptr, keys, vals, ks, vs, e->pf_ctx, T, 0,
-                                          c.max_ctx, c.n_heads, c.n_kv, c.head_dim, st));
+            EC_TRY(ec_glue_qk_rope_append(L.proj, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn, e->inv_freq, L.pos,
+                                          L.n, nullptr, nullptr, keys, vals, ks, vs, L.ctx, T, 0, c.max_ctx,
+                                          c.n_heads, c.n_kv, c.head_dim, st));
             for (uint32_t s0 = 0; s0 < T; s0 += ec_engine::kPrefillAttnSlots) {
                 const uint32_t n = std::min(T - s0, ec_engine::kPrefillAttnSlots);
-                EC_TRY(ec_attn_decode(e->pf_n + (size_t)s0 * e->q_dim, keys, vals, ks, vs,
-                                      e->pf_attn + (size_t)s0 * e->q_dim, e->pf_ctx + s0, n, 0, c.n_heads, c.n_kv,
-                                      c.head_dim, c.max_ctx, e->pf_ws, st));
+                EC_TRY(ec_attn_decode(L.n + (size_t)s0 * e->q_dim, keys, vals, ks, vs, L.attn + (size_t)s0 * e->q_dim,
+                                      L.ctx + s0, n, 0, c.n_heads, c.n_kv, c.head_dim, c.max_ctx, L.ws, st));
             }
-            EC_TRY(gemm_rows(e, y.w_out, e->pf_attn, e->pf_x, T, H, 1));
+            EC_TRY(gemm_rows(L, y.w_out, L.attn, L.x, T, H, 1));
         }
-        EC_TRY(ec_glue_rmsnorm_rows(e->pf_x, y.ffn_norm, e->pf_n, T, H, st));
-        EC_TRY(gemm_rows(e, y.w_gu, e->pf_n, e->pf_gu, T, 2 * F, 0));
-        EC_TRY(ec_glue_swiglu_rows(e->pf_gu, e->pf_n, T, F, st));
-        EC_TRY(gemm_rows(e, y.w_down, e->pf_n, e->pf_x, T, H, 1));
+        EC_TRY(ec_glue_rmsnorm_rows(L.x, y.ffn_norm, L.n, T, H, st));
+        EC_TRY(gemm_rows(L, y.w_gu, L.n, L.gu, T, 2 * F, 0));
+        EC_TRY(ec_glue_swiglu_rows(L.gu, L.n, T, F, st));
+        EC_TRY(gemm_rows(L, y.w_down, L.n, L.x, T, H, 1));
     }
+    return EC_OK;
+}
+
+// Prefill job of one sequence on a lane: the next chunk to run.
+struct PrefillJob {
+    uint32_t seq, n;
+    const int32_t* tokens;
+    int32_t pos0;
+    uint32_t done = 0;  // tokens already enqueued
+};
+
+// Enqueue the job's next chunk on lane L (the lane's previous chunk must have
+// completed: its token / position rows are overwritten).
+int prefill_step(ec_engine* e, Lane& L, PrefillJob& j) {
+    const uint32_t C = ec_engine::kPrefillChunk;
+    const uint32_t T = std::min(j.n - j.done, C), p = (uint32_t)j.pos0 + j.done;
+    for (uint32_t t = 0; t < T; ++t) L.h_pos[t] = (int32_t)(p + t);
+    EC_HIP(hipMemcpyAsync(L.tok, j.tokens + j.done, T * 4, hipMemcpyHostToDevice, L.st));
+    EC_HIP(hipMemcpyAsync(L.pos, L.h_pos.data(), T * 4, hipMemcpyHostToDevice, L.st));
+    EC_HIP(hipStreamSynchronize(L.st));  // pageable sources: the copies are complete before h_pos is reused
+    EC_TRY(prefill_chunk(e, L, j.seq, T, p));
+    j.done += T;
+    if (j.done < j.n) return EC_OK;
+    // the last token's logits and greedy next token; pos[seq] = pos0 + n
+    const int32_t last = j.pos0 + (int32_t)j.n - 1;
+    EC_TRY(ec_glue_rmsnorm_quant(L.x + (size_t)(T - 1) * e->H, e->final_norm, L.act1, 1, e->H, L.st));
+    EC_TRY(ec_matvec(EC_Q8_0, e->lm_head.tiled, L.act1, e->logits + (size_t)j.seq * e->c.vocab, 1, e->c.vocab, e->H,
+                     e->c.vocab, 0, L.st));
+    EC_HIP(hipMemcpyAsync(e->pos + j.seq, &last, 4, hipMemcpyHostToDevice, L.st));
+    EC_TRY(ec_glue_argmax_advance(e->logits + (size_t)j.seq * e->c.vocab, e->c.vocab, e->gen + j.seq,
+                                  e->tok + j.seq, e->pos + j.seq, 1, L.st));
+    EC_HIP(hipStreamSynchronize(L.st));  // `last` lives on this frame
+    return EC_OK;
+}
+
+// Run the jobs over `lanes` lanes: each lane takes the next unstarted job when
+// its current one is done; lanes alternate so that one lane's chunk is queued
+// while the other's runs.
+int prefill_run(ec_engine* e, std::vector<PrefillJob>& jobs, uint32_t lanes) {
+    lanes = std::max(1u, std::min({lanes, ec_engine::kPrefillLanes, (uint32_t)jobs.size()}));
+    for (uint32_t i = 0; i < lanes; ++i) EC_TRY(prefill_alloc(e, e->pf[i], i));
+    EC_HIP(hipStreamSynchronize(e->st));  // whatever the decode stream queued before
+    std::vector<int> cur(lanes, -1);
+    uint32_t next = 0;
+    for (;;) {
+        bool any = false;
+        for (uint32_t i = 0; i < lanes; ++i) {
+            if (cur[i] < 0 || jobs[cur[i]].done == jobs[cur[i]].n) cur[i] = next < jobs.size() ? (int)next++ : -1;
+            if (cur[i] < 0) continue;
+            any = true;
+            EC_TRY(prefill_step(e, e->pf[i], jobs[cur[i]]));
+        }
+        if (!any) break;
+    }
+    for (uint32_t i = 0; i < lanes; ++i) EC_HIP(hipStreamSynchronize(e->pf[i].st));
+    return EC_OK;
+}
+
+int check_prefill_args(ec_engine* e, uint32_t seq, const int32_t* tokens, uint32_t n, int32_t pos0, const char* who) {
+    if (!e || !tokens || n == 0 || seq >= e->B || pos0 < 0 || (uint64_t)pos0 + n > e->c.max_ctx) {
+        char buf[160];
+        snprintf(buf, sizeof buf, "%s: bad argument (seq < max_batch, pos0 + n <= max_ctx)", who);
+        return ec_set_error(EC_ERR_ARG, buf);
+    }
+    for (uint32_t i = 0; i < n; ++i)
+        if (tokens[i] < 0 || (uint32_t)tokens[i] >= e->c.vocab) {
+            char buf[96];
+            snprintf(buf, sizeof buf, "%s: token id", who);
+            return ec_set_error(EC_ERR_ARG, buf);
+        }
+    if (e->c.head_dim != 256) return ec_set_error(EC_ERR_UNSUPPORTED, "ec_engine_prefill: head_dim must be 256");
     return EC_OK;
 }
 }  // namespace
 
 extern "C" int ec_engine_prefill(ec_engine* e, uint32_t seq, const int32_t* tokens, uint32_t n, int32_t pos0) {
-    if (!e || !tokens || n == 0 || seq >= e->B || pos0 < 0 || (uint64_t)pos0 + n > e->c.max_ctx)
-        return ec_set_error(EC_ERR_ARG, "ec_engine_prefill: bad argument (seq < max_batch, pos0 + n <= max_ctx)");
-    for (uint32_t i = 0; i < n; ++i)
-        if (tokens[i] < 0 || (uint32_t)tokens[i] >= e->c.vocab)
-            return ec_set_error(EC_ERR_ARG, "ec_engine_prefill: token id");
-    if (e->c.head_dim != 256) return ec_set_error(EC_ERR_UNSUPPORTED, "ec_engine_prefill: head_dim must be 256");
-    EC_TRY(prefill_alloc(e));
-    const uint32_t C = ec_engine::kPrefillChunk;
-    std::vector<int32_t> pos(C);
-    for (uint32_t t0 = 0; t0 < n; t0 += C) {
-        const uint32_t T = std::min(n - t0, C), p = (uint32_t)pos0 + t0;
-        for (uint32_t t = 0; t < T; ++t) pos[t] = (int32_t)(p + t);
-        // synchronous copies: the host vectors are reused by the next chunk
-        EC_HIP(hipStreamSynchronize(e->st));
-        EC_HIP(hipMemcpy(e->pf_tok, tokens + t0, T * 4, hipMemcpyHostToDevice));
-        EC_HIP(hipMemcpy(e->pf_pos, pos.data(), T * 4, hipMemcpyHostToDevice));
-        EC_TRY(prefill_chunk(e, seq, T, p));
+    EC_TRY(check_prefill_args(e, seq, tokens, n, pos0, "ec_engine_prefill"));
+    std::vector<PrefillJob> jobs{PrefillJob{seq, n, tokens, pos0}};
+    return prefill_run(e, jobs, 1);
+}
+
+extern "C" int ec_engine_prefill_batch(ec_engine* e, uint32_t n_seqs, const uint32_t* seqs,
+                                       const int32_t* const* tokens, const uint32_t* lens, const int32_t* pos0) {
+    if (!e || !seqs || !tokens || !lens || !pos0) return ec_set_error(EC_ERR_ARG, "ec_engine_prefill_batch: null argument");
+    std::vector<PrefillJob> jobs;
+    for (uint32_t i = 0; i < n_seqs; ++i) {
+        EC_TRY(check_prefill_args(e, seqs[i], tokens[i], lens[i], pos0[i], "ec_engine_prefill_batch"));
+        for (uint32_t k = 0; k < i; ++k)
+            if (seqs[k] == seqs[i]) return ec_set_error(EC_ERR_ARG, "ec_engine_prefill_batch: a sequence appears twice");
+        jobs.push_back(PrefillJob{seqs[i], lens[i], tokens[i], pos0[i]});
     }
-    // the last token's logits and greedy next token; pos[seq] = pos0 + n
-    const uint32_t T = (n - 1) % C + 1;
-    const int32_t last = pos0 + (int32_t)n - 1;
-    EC_TRY(ec_glue_rmsnorm_quant(e->pf_x + (size_t)(T - 1) * e->H, e->final_norm, e->act_h, 1, e->H, e->st));
-    EC_TRY(ec_matvec(EC_Q8_0, e->lm_head.tiled, e->act_h, e->logits + (size_t)seq * e->c.vocab, 1, e->c.vocab, e->H,
-                     e->c.vocab, 0, e->st));
-    EC_HIP(hipStreamSynchronize(e->st));
-    EC_HIP(hipMemcpy(e->pos + seq, &last, 4, hipMemcpyHostToDevice));
-    EC_TRY(ec_glue_argmax_advance(e->logits + (size_t)seq * e->c.vocab, e->c.vocab, e->gen + seq, e->tok + seq,
-                                  e->pos + seq, 1, e->st));
-    EC_HIP(hipStreamSynchronize(e->st));
-    return EC_OK;
+    if (jobs.empty()) return EC_OK;
+    return prefill_run(e, jobs, ec_engine::kPrefillLanes);
 }
 
 extern "C" int ec_engine_profile_matvecs(ec_engine* e, uint32_t reps, uint32_t* launches, double* bytes_per_step,

@@ -166,6 +166,53 @@ def test_prefill_matches_token_loop(lens):
     b.close()
 
 
+def test_prefill_batch_equals_one_by_one():
+    """ec_engine_prefill_batch (sequences on two streams) == ec_engine_prefill per
+    sequence, bit for bit: logits, greedy tokens, positions, every state;
+    ragged lengths across chunk boundaries, a nonzero start position."""
+    from echohip.engine import Engine
+    cfg = small_config(max_batch=4, max_ctx=700)
+    m = make_model(cfg, seed=25)
+    rng = np.random.default_rng(4)
+    lens = [600, 7, 513, 40]
+    prompts = [rng.integers(0, cfg.vocab, n).astype(np.int32) for n in lens]
+    a, b = Engine(cfg), Engine(cfg)
+    upload(a, m)
+    upload(b, m)
+    a.reset()
+    b.reset()
+    a.prefill(3, prompts[3][:10], 0)
+    b.prefill(3, prompts[3][:10], 0)
+    for s in range(3):
+        a.prefill(s, prompts[s], 0)
+    a.prefill(3, prompts[3][10:], 10)
+    b.prefill_batch([(s, prompts[s], 0) for s in range(3)] + [(3, prompts[3][10:], 10)])
+    ga, pa = a.tokens()
+    gb, pb = b.tokens()
+    assert ga.tolist() == gb.tolist() and pa.tolist() == pb.tolist() == [600, 7, 513, 40]
+    for s in range(4):
+        assert np.array_equal(a.logits(s).view(np.uint32), b.logits(s).view(np.uint32))
+        sa, sb = _states(a, cfg, s), _states(b, cfg, s)
+        for key in sa:
+            assert np.array_equal(sa[key].view(np.uint8), sb[key].view(np.uint8)), (s, key)
+    a.close()
+    b.close()
+
+
+def test_prefill_batch_rejects_bad_arguments():
+    from echohip.engine import Engine
+    from echohip.lib import EchoHipError
+    cfg = small_config(max_batch=2, max_ctx=16)
+    e = Engine(cfg)
+    upload(e, make_model(cfg, seed=1))
+    e.reset()
+    with pytest.raises(EchoHipError):
+        e.prefill_batch([(0, [1, 2], 0), (0, [3], 2)])  # the same sequence twice
+    with pytest.raises(EchoHipError):
+        e.prefill_batch([(0, [1, 2], 0), (1, list(range(20)), 0)])  # past max_ctx
+    e.close()
+
+
 def test_prefill_rejects_bad_arguments():
     from echohip.engine import Engine
     from echohip.lib import EchoHipError
