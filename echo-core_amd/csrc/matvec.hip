@@ -474,18 +474,22 @@ __global__ void k_dequant_fp16(int fmt, const uint8_t* __restrict__ src, uint16_
 }
 
 // Chunks per wave (GPW, compile-time) and waves per 16-row tile (nw <= 16):
-// aim for EC_MV_TARGET_WAVES waves in total (default 4096) with every tile's K
-// range covered by one pass where possible.
-static uint32_t target_waves() {
+// aim for a total wave count with every tile's K range covered by one pass
+// where possible.  Q8_0: 12288 waves (EC_MV_TARGET_WAVES overrides; with the
+// decode step's split-K projections 12288 measured best of 2048 .. 32768:
+// 1.92 ms/step at 2048, 1.86 at 4096, 1.80 at 12288, 1.86 at 24576); Q4_K:
+// 4096.
+static uint32_t target_waves_q8() {
     static uint32_t v = [] {
         const char* e = getenv("EC_MV_TARGET_WAVES");
-        return e ? (uint32_t)atoi(e) : 4096u;
+        return e ? (uint32_t)atoi(e) : 12288u;
     }();
     return v;
 }
+constexpr uint32_t kTargetWavesQ4 = 4096;
 
-static void plan(uint32_t n_tiles, uint32_t n_chunks, int max_gpw, int& gpw, uint32_t& nw) {
-    const uint32_t want = (target_waves() + n_tiles - 1) / n_tiles;  // waves per tile wanted
+static void plan(uint32_t n_tiles, uint32_t n_chunks, int max_gpw, int& gpw, uint32_t& nw, uint32_t target) {
+    const uint32_t want = (target + n_tiles - 1) / n_tiles;  // waves per tile wanted
     gpw = (int)((n_chunks + want - 1) / (want ? want : 1));
     // one pass per wave where 16 waves can cover the tile's K: a second pass
     // would issue its loads only after the first pass's compute
@@ -524,7 +528,7 @@ static void launch_q8(const void* W, const void* act, float* y, int32_t* dots, u
     const uint32_t cps = (nG + nsplit - 1) / nsplit;  // longest range
     int gpw;
     uint32_t nw;
-    plan(nT * nsplit, cps, 5, gpw, nw);  // GPW <= 5 keeps every variant under 128 VGPRs (1024 threads)
+    plan(nT * nsplit, cps, 5, gpw, nw, target_waves_q8());  // GPW <= 5: every variant under 128 VGPRs
     switch (gpw) {
         case 1: launch_q8_g<MT, DOTS, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
         case 2: launch_q8_g<MT, DOTS, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
@@ -553,7 +557,7 @@ static void launch_q4(const void* W, const void* act, float* y, int32_t* dots, u
     const uint32_t nT = round_up(N, 16) / 16, nB = round_up(K, 256) / 256;
     int gpw;
     uint32_t nw;
-    plan(nT, nB, MT == 1 ? 3 : 1, gpw, nw);
+    plan(nT, nB, MT == 1 ? 3 : 1, gpw, nw, kTargetWavesQ4);
     switch (gpw) {
         case 1: launch_q4_g<MT, DOTS, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
         case 2: launch_q4_g<MT, DOTS, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;

@@ -226,9 +226,9 @@ def run_all(hip, quick=False):
 # rows): (name, N output rows, K, launches per step).
 # (name, N, K, launches per step, K splits): the decode step of the 4B-class
 # decoder at batch 8, with the split-K counts the engine uses (host/engine.cpp:
-# 4 for the delta-net input projection, 2 for gate/up, 3 for the projections
-# that add into the residual; a split writes one partial output per split).
-DECODE_STEP_MATVECS = [("delta_in", 12352, 2560, 24, 4), ("delta_out", 2560, 4096, 24, 3),
+# 2 for the delta-net input projection and gate/up, 3 for the projections that
+# add into the residual; a split writes one partial output per split).
+DECODE_STEP_MATVECS = [("delta_in", 12352, 2560, 24, 2), ("delta_out", 2560, 4096, 24, 3),
                        ("attn_in", 6144, 2560, 8, 1), ("attn_out", 2560, 4096, 8, 3),
                        ("ffn_gate_up", 18432, 2560, 32, 2), ("ffn_down", 2560, 9216, 32, 3),
                        ("lm_head", 151936, 2560, 1, 1)]

@@ -215,14 +215,14 @@ uint32_t resid_split(uint32_t N, uint32_t K) {
 
 // K splits of the input projection of a delta-net block and of gate/up
 // (their consumers, the fused delta step and SwiGLU, add the partial sums).
-// Decode step on MI355X (4B-class, batch 8): 1.867 ms unsplit, 1.860 ms with
-// 4 and 2 (EC_IN_SPLIT / EC_GU_SPLIT override).
+// Decode step on MI355X (4B-class, batch 8, ~12k matvec waves per launch):
+// best at 2 and 2 (EC_IN_SPLIT / EC_GU_SPLIT override).
 uint32_t env_split(const char* name, uint32_t dflt) {
     const char* v = getenv(name);
     return std::clamp(v ? (uint32_t)atoi(v) : dflt, 1u, kMaxResidSplit);
 }
 uint32_t in_split() {
-    static const uint32_t v = env_split("EC_IN_SPLIT", 4);
+    static const uint32_t v = env_split("EC_IN_SPLIT", 2);
     return v;
 }
 uint32_t gu_split() {
