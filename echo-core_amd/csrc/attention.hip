@@ -218,24 +218,26 @@ __global__ __launch_bounds__(256) void k_pack_q(const float* __restrict__ q, uin
     store_q_pieces(val, amax, d, s, head, n_heads, n_kv, qa, qsc);
 }
 
-template <int G>
+template <int G, int CH>
 __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ qa, const float* __restrict__ qsc,
                                                    const int8_t* __restrict__ keys, const int8_t* __restrict__ vals,
                                                    const float* __restrict__ kscales, const float* __restrict__ vscales,
                                                    const int32_t* __restrict__ ctx, uint64_t seq_stride, uint32_t n_kv,
                                                    uint32_t n_chunks_max, uint32_t max_ctx, float* __restrict__ ws) {
     static_assert(G == 1 || G == 2 || G == 4, "3G A rows must fit the 16 MFMA rows");
+    static_assert(CH == 64 || CH == 128, "chunk of 64 or 128 positions");
     constexpr uint32_t HD = 256;
     constexpr uint32_t NR = kQPieces * G;  // A rows in use
-    __shared__ float part_s[NR][64];       // per-piece scores (times the K row scale)
-    __shared__ f32x4 p_s[64];              // [position] probabilities x V row scale, one per head
-    __shared__ u32x4 v_s[64 * 16];         // the chunk's V rows, [position][256 bytes]
+    constexpr int NPW = CH / 64;           // 16-position groups per wave
+    __shared__ float part_s[NR][CH];       // per-piece scores (times the K row scale)
+    __shared__ f32x4 p_s[CH];              // [position] probabilities x V row scale, one per head
+    __shared__ u32x4 v_s[CH * 16];         // the chunk's V rows, [position][256 bytes]
     const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int32_t L = min(ctx[s], (int32_t)max_ctx);
-    const uint32_t c0 = chunk * kChunk64;
+    const uint32_t c0 = chunk * CH;
     if (L <= 0 || c0 >= (uint32_t)L) return;
-    const uint32_t ntok = min((uint32_t)L - c0, kChunk64);
+    const uint32_t ntok = min((uint32_t)L - c0, (uint32_t)CH);
     const uint32_t n_heads = n_kv * G;
     const size_t row = (size_t)n_kv * HD;
     const int8_t* kb = keys + s * seq_stride + (size_t)kvh * HD;
@@ -245,7 +247,8 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ q
     const uint32_t r16 = lane & 15, gq = lane >> 4;
 
     // ---- loads, in the order they are consumed (waitcnt retires them in order):
-    // A operand (packed q) and scales, K of this wave's 16 positions, then their V.
+    // A operand (packed q) and scales, K of this wave's 16-position groups
+    // (group q: positions 64q + 16*wv ..), then their V.
     const bool arow = r16 < NR;
     const uint8_t* qp = qa + ((((size_t)s * n_kv + kvh) * NR + (arow ? r16 : 0)) * 4 + gq) * 64;
     u32x4 aq[4];
@@ -258,54 +261,81 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ q
         const uint32_t r = 4 * gq + c;
         rs[c] = scq[r < NR ? r : 0];
     }
-    const uint32_t t = 16 * wv + r16;  // position of this lane's B column
-    const uint32_t tc = t < ntok ? t : 0;
-    const float ksv = ksb[(size_t)(c0 + tc) * n_kv];
-    const float vsv = vsb[(size_t)(c0 + (lane < ntok ? lane : 0)) * n_kv];  // used by wave 0 (lane = position)
-    u32x4 kw[4];
-    const int8_t* kr = kb + (size_t)(c0 + tc) * row + 16 * gq;
+    float ksv[NPW], vsv[NPW];
+    u32x4 kw[NPW][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) kw[i] = __builtin_nontemporal_load((const u32x4*)(kr + 64 * i));
-    // V: instruction j brings positions 16*wv + 4j .. +3 (256 bytes each, lane = 16 bytes)
-    u32x4 vv[4];
+    for (int q = 0; q < NPW; ++q) {
+        const uint32_t t = 64 * q + 16 * wv + r16;  // position of this lane's B column
+        const uint32_t tc = t < ntok ? t : 0;
+        ksv[q] = ksb[(size_t)(c0 + tc) * n_kv];
+        const uint32_t tl = 64 * q + lane;  // used by wave 0 (lane = position)
+        vsv[q] = vsb[(size_t)(c0 + (tl < ntok ? tl : 0)) * n_kv];
+        const int8_t* kr = kb + (size_t)(c0 + tc) * row + 16 * gq;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t tv = 16 * wv + 4 * j + (lane >> 4);
-        vv[j] = __builtin_nontemporal_load(
-            (const u32x4*)(vb + (size_t)(c0 + (tv < ntok ? tv : 0)) * row + 16 * (lane & 15)));
+        for (int i = 0; i < 4; ++i) kw[q][i] = __builtin_nontemporal_load((const u32x4*)(kr + 64 * i));
     }
+    // V: instruction (q, j) brings positions 64q + 16*wv + 4j .. +3 (256 bytes each, lane = 16 bytes)
+    u32x4 vv[NPW][4];
+#pragma unroll
+    for (int q = 0; q < NPW; ++q)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t tv = 64 * q + 16 * wv + 4 * j + (lane >> 4);
+            vv[q][j] = __builtin_nontemporal_load(
+                (const u32x4*)(vb + (size_t)(c0 + (tv < ntok ? tv : 0)) * row + 16 * (lane & 15)));
+        }
 
-    // ---- scores of 16 positions: 8 accumulating MFMAs; C row r = 4*gq + c
-    v4i C = {0, 0, 0, 0};
+    // ---- scores of 16 positions per group: 8 accumulating MFMAs; C row r = 4*gq + c
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-        const long A = arow ? ((m & 1) ? pack2(aq[m / 2].z, aq[m / 2].w) : pack2(aq[m / 2].x, aq[m / 2].y)) : 0l;
-        const u32x4 w = kw[m / 2];
-        const long B = (m & 1) ? pack2(w.z, w.w) : pack2(w.x, w.y);
-        C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, C, 0, 0, 0);
+    for (int q = 0; q < NPW; ++q) {
+        v4i C = {0, 0, 0, 0};
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const long A = arow ? ((m & 1) ? pack2(aq[m / 2].z, aq[m / 2].w) : pack2(aq[m / 2].x, aq[m / 2].y)) : 0l;
+            const u32x4 w = kw[q][m / 2];
+            const long B = (m & 1) ? pack2(w.z, w.w) : pack2(w.x, w.y);
+            C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, C, 0, 0, 0);
+        }
+        const uint32_t t = 64 * q + 16 * wv + r16;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (4 * gq + c < NR) part_s[4 * gq + c][t] = (float)C[c] * rs[c] * ksv[q];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v_s[64 * (16 * q + 4 * wv + j) + lane] = vv[q][j];
     }
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-        if (4 * gq + c < NR) part_s[4 * gq + c][t] = (float)C[c] * rs[c] * ksv;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v_s[64 * (4 * wv + j) + lane] = vv[j];
     __syncthreads();
 
-    // ---- softmax over the chunk (wave 0, lane = position)
+    // ---- softmax over the chunk (wave 0, lane = positions lane + 64q)
     constexpr float scale = 1.0f / 16.0f;  // 1/sqrt(256)
     if (wv == 0) {
         float m[G], l[G];
-        f32x4 pr = {0.0f, 0.0f, 0.0f, 0.0f};
+        f32x4 pr[NPW];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            const float raw = (part_s[g][lane] + part_s[G + g][lane]) + part_s[2 * G + g][lane];
-            const float sc = lane < ntok ? raw * scale : -INFINITY;
-            m[g] = wave_max(sc);
-            const float e = lane < ntok ? __expf(sc - m[g]) : 0.0f;
-            l[g] = wave_sum(e);
-            pr[g] = e * vsv;
+            float sc[NPW], mx = -INFINITY;
+#pragma unroll
+            for (int q = 0; q < NPW; ++q) {
+                const uint32_t tl = 64 * q + lane;
+                const float raw = (part_s[g][tl] + part_s[G + g][tl]) + part_s[2 * G + g][tl];
+                sc[q] = tl < ntok ? raw * scale : -INFINITY;
+                mx = fmaxf(mx, sc[q]);
+            }
+            m[g] = wave_max(mx);
+            float es = 0.0f;
+#pragma unroll
+            for (int q = 0; q < NPW; ++q) {
+                const float e = 64 * q + lane < ntok ? __expf(sc[q] - m[g]) : 0.0f;
+                es += e;
+                pr[q][g] = e * vsv[q];
+            }
+            l[g] = wave_sum(es);
         }
-        p_s[lane] = pr;
+#pragma unroll
+        for (int q = 0; q < NPW; ++q) {
+#pragma unroll
+            for (int g = G; g < 4; ++g) pr[q][g] = 0.0f;
+            p_s[64 * q + lane] = pr[q];
+        }
         if (lane == 0) {
 #pragma unroll
             for (int g = 0; g < G; ++g) {
@@ -317,9 +347,9 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ q
     __syncthreads();
 
     // ---- softmax . V: wave wv owns dims 64*wv .. +63 (lane = one 4-dim word),
-    // lane group pg sums positions 16*pg .. +15; the four group sums are added
-    // by cross-lane exchange.  Positions past the chunk end carry p = 0 (their
-    // clamped V rows add nothing).
+    // lane group pg sums positions (CH/4)*pg .. +CH/4-1; the four group sums
+    // are added by cross-lane exchange.  Positions past the chunk end carry
+    // p = 0 (their clamped V rows add nothing).
     const uint32_t word = 16 * wv + r16, pg = gq;
     const uint32_t* vrow = (const uint32_t*)v_s;
     float o[G][4];
@@ -327,8 +357,8 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ q
     for (int g = 0; g < G; ++g)
         for (int e = 0; e < 4; ++e) o[g][e] = 0.0f;
 #pragma unroll
-    for (uint32_t i = 0; i < 16; ++i) {
-        const uint32_t tp = 16 * pg + i;
+    for (uint32_t i = 0; i < CH / 4; ++i) {
+        const uint32_t tp = (CH / 4) * pg + i;
         const uint32_t w = vrow[64 * tp + word];
         const f32x4 p = p_s[tp];
         const float v0 = (float)(int8_t)(w & 0xFF), v1 = (float)(int8_t)((w >> 8) & 0xFF);
@@ -473,16 +503,31 @@ static void launch_attn(const float* q, const int8_t* keys, const int8_t* vals, 
 }
 
 
+// Positions per attention workgroup: 64, or 128 once 64-position chunks
+// would need more workgroups than the GPU holds at once (~2048 at 7 waves per
+// SIMD).  Measured on MI355X (16 heads / 4 kv heads): one sequence of 32768
+// positions 34.2 -> 28.1 us with 128; 512 and 4096 positions 11.0 / 12.3 us
+// with 64 vs 12.6 / 13.5 with 128.
+static uint32_t attn_chunk(uint32_t max_ctx, uint32_t n_kv, uint32_t n_seq) {
+    const uint64_t wgs64 = (uint64_t)((max_ctx + 63) / 64) * n_kv * n_seq;
+    return wgs64 >= 2048 ? 128u : 64u;
+}
+
 template <int G>
 static void launch_mfma(const uint8_t* qa, const float* qsc, const int8_t* keys, const int8_t* vals, const float* ks,
                         const float* vs, float* out, uint8_t* act, const int32_t* ctx, uint32_t n_seq,
                         uint64_t seq_stride, uint32_t n_kv, uint32_t max_ctx, float* ws, hipStream_t st) {
-    const uint32_t ncm = (max_ctx + kChunk64 - 1) / kChunk64;
-    hipLaunchKernelGGL((k_attn_mfma<G>), dim3(ncm, n_kv, n_seq), dim3(256), 0, st, qa, qsc, keys, vals, ks, vs, ctx,
-                       seq_stride, n_kv, ncm, max_ctx, ws);
+    const uint32_t CH = attn_chunk(max_ctx, n_kv, n_seq);
+    const uint32_t ncm = (max_ctx + CH - 1) / CH;
+    if (CH == 128)
+        hipLaunchKernelGGL((k_attn_mfma<G, 128>), dim3(ncm, n_kv, n_seq), dim3(256), 0, st, qa, qsc, keys, vals, ks, vs,
+                           ctx, seq_stride, n_kv, ncm, max_ctx, ws);
+    else
+        hipLaunchKernelGGL((k_attn_mfma<G, 64>), dim3(ncm, n_kv, n_seq), dim3(256), 0, st, qa, qsc, keys, vals, ks, vs,
+                           ctx, seq_stride, n_kv, ncm, max_ctx, ws);
     const uint32_t xd_off = (uint32_t)act_layout(EC_Q8_0, n_seq, n_kv * G * 256).xd_off;
-    hipLaunchKernelGGL(k_attn_merge, dim3(n_kv * G, n_seq), dim3(kMergeThreads), ncm * sizeof(float), st, ws, ctx, out, act,
-                       xd_off, n_seq, n_kv * G, ncm, max_ctx, kChunk64);
+    hipLaunchKernelGGL(k_attn_merge, dim3(n_kv * G, n_seq), dim3(kMergeThreads), ncm * sizeof(float), st, ws, ctx, out,
+                       act, xd_off, n_seq, n_kv * G, ncm, max_ctx, CH);
 }
 
 static int mfma_dispatch(uint32_t G, const uint8_t* qa, const float* qsc, const int8_t* keys, const int8_t* vals,

@@ -877,18 +877,22 @@ int prefill_run(ec_engine* e, std::vector<PrefillJob>& jobs, uint32_t lanes) {
     EC_HIP(hipStreamSynchronize(e->st));  // whatever the decode stream queued before
     std::vector<int> cur(lanes, -1);
     uint32_t next = 0;
-    for (;;) {
-        bool any = false;
-        for (uint32_t i = 0; i < lanes; ++i) {
+    int rc = EC_OK;
+    for (bool any = true; any && rc == EC_OK;) {
+        any = false;
+        for (uint32_t i = 0; i < lanes && rc == EC_OK; ++i) {
             if (cur[i] < 0 || jobs[cur[i]].done == jobs[cur[i]].n) cur[i] = next < jobs.size() ? (int)next++ : -1;
             if (cur[i] < 0) continue;
             any = true;
-            EC_TRY(prefill_step(e, e->pf[i], jobs[cur[i]]));
+            rc = prefill_step(e, e->pf[i], jobs[cur[i]]);
         }
-        if (!any) break;
     }
-    for (uint32_t i = 0; i < lanes; ++i) EC_HIP(hipStreamSynchronize(e->pf[i].st));
-    return EC_OK;
+    // every lane drained, also after an error (no work left in flight)
+    for (uint32_t i = 0; i < lanes; ++i) {
+        const hipError_t se = hipStreamSynchronize(e->pf[i].st);
+        if (rc == EC_OK && se != hipSuccess) rc = ec_set_hip_error_host(se, "ec_engine_prefill: stream");
+    }
+    return rc;
 }
 
 int check_prefill_args(ec_engine* e, uint32_t seq, const int32_t* tokens, uint32_t n, int32_t pos0, const char* who) {
