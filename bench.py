@@ -53,6 +53,18 @@ def step_traffic_bytes(cfg, eng_weight_bytes, ctx_sum, batch):
     return eng_weight_bytes + state + conv + kv
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or 'unknown'."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(eng, cfg, n_tokens, threads):
     """Time the oracle's AVX2 decoder on the engine's own weights (host copy)."""
     import numpy as np
@@ -235,7 +247,8 @@ def main() -> int:
         cpu = {"value": round(res[threads], 4), "unit": "tok/s", "cores": threads, "kind": "port",
                "sample": f"{args.cpu_tokens} single-sequence decode tokens of the same 4B-class model and weights "
                          f"(oracle AVX2 decoder, fp32 activations, OpenMP over matvec rows, {threads} threads, "
-                         f"context < {args.cpu_tokens + 2}); 1 thread: {res[1]:.4f} tok/s"}
+                         f"context < {args.cpu_tokens + 2}); 1 thread: {res[1]:.4f} tok/s; host CPU: {cpu_model()}, "
+                         f"{os.cpu_count()} hardware threads visible"}
 
     line = {
         "metric": "decode tok/s (4B-class Q8_0, 1 GPU); matvec HBM GB/s as % of peak",
