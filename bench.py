@@ -67,40 +67,14 @@ def cpu_model():
 
 def cpu_baseline(eng, cfg, n_tokens, threads):
     """Time the oracle's AVX2 decoder on the engine's own weights (host copy)."""
-    import numpy as np
-
-    from echohip.engine import (EngineConfig, T_A_LOG, T_ATTN_NORM, T_CONV_W, T_DT_BIAS, T_EMBED, T_FFN_NORM,
-                                T_FINAL_NORM, T_K_NORM, T_LM_HEAD, T_Q_NORM, T_SSM_NORM, T_W_DOWN, T_W_GATE, T_W_IN,
-                                T_W_OUT, T_W_UP)
+    from echohip.engine import EngineConfig
     from oracle import Baseline, Decoder
 
-    H, F = cfg.hidden, cfg.ffn
-    q8 = lambda rows, K: rows * (K // 32) * 34  # noqa: E731
-    f32 = lambda n: (n * 4, np.float32)  # noqa: E731
-    m = {"embed": eng.get_tensor(0, T_EMBED, q8(cfg.vocab, H)),
-         "final_norm": eng.get_tensor(0, T_FINAL_NORM, H * 4, np.float32),
-         "lm_head": eng.get_tensor(0, T_LM_HEAD, q8(cfg.vocab, H)), "layers": []}
-    for l in range(cfg.n_layers):
-        attn = cfg.is_attn(l)
-        nin = cfg.nin_attn if attn else cfg.nin_delta
-        kout = cfg.n_heads * cfg.head_dim if attn else cfg.ssm_inner
-        y = {"attn": attn, "w_in": eng.get_tensor(l, T_W_IN, q8(nin, H)), "w_out": eng.get_tensor(l, T_W_OUT, q8(H, kout)),
-             "w_gate": eng.get_tensor(l, T_W_GATE, q8(F, H)), "w_up": eng.get_tensor(l, T_W_UP, q8(F, H)),
-             "w_down": eng.get_tensor(l, T_W_DOWN, q8(H, F)),
-             "attn_norm": eng.get_tensor(l, T_ATTN_NORM, *f32(H)), "ffn_norm": eng.get_tensor(l, T_FFN_NORM, *f32(H))}
-        if attn:
-            y["q_norm"] = eng.get_tensor(l, T_Q_NORM, *f32(cfg.head_dim))
-            y["k_norm"] = eng.get_tensor(l, T_K_NORM, *f32(cfg.head_dim))
-        else:
-            y["conv_w"] = eng.get_tensor(l, T_CONV_W, *f32(cfg.conv_kernel * cfg.conv_dim))
-            y["a_log"] = eng.get_tensor(l, T_A_LOG, *f32(cfg.ssm_heads))
-            y["dt_bias"] = eng.get_tensor(l, T_DT_BIAS, *f32(cfg.ssm_heads))
-            y["ssm_norm"] = eng.get_tensor(l, T_SSM_NORM, *f32(128))
-        m["layers"].append(y)
+    m = eng.export_model()
     ccfg = EngineConfig(max_batch=1, max_ctx=n_tokens + 4)
     bl = Baseline()
     res = {}
-    for nthr, ntok in ((1, 1), (threads, n_tokens)):
+    for nthr, ntok in ((1, max(1, n_tokens // 10)), (threads, n_tokens)):
         bl.threads(nthr)
         dec = Decoder(bl, ccfg, m, n_seq=1, quant_act=False)
         dec.token(0, 1)  # warm-up (page-in)
@@ -121,7 +95,8 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=8)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--max-prompt", type=int, default=4096, help="upper bound of the prompt-length draw")
-    ap.add_argument("--cpu-tokens", type=int, default=8, help="all-core CPU baseline sample (tokens)")
+    ap.add_argument("--cpu-tokens", type=int, default=256,
+                    help="all-core CPU baseline sample (tokens; ~10 s on 16 cores); the 1-thread leg runs 1/10 of it")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
@@ -245,7 +220,8 @@ def main() -> int:
         threads = min(os.cpu_count() or 1, 16)
         res = cpu_baseline(eng, cfg, args.cpu_tokens, threads)
         cpu = {"value": round(res[threads], 4), "unit": "tok/s", "cores": threads, "kind": "port",
-               "sample": f"{args.cpu_tokens} single-sequence decode tokens of the same 4B-class model and weights "
+               "sample": f"{args.cpu_tokens} single-sequence decode tokens ({max(1, args.cpu_tokens // 10)} on 1 thread) "
+                         f"of the same 4B-class model and weights "
                          f"(oracle AVX2 decoder, fp32 activations, OpenMP over matvec rows, {threads} threads, "
                          f"context < {args.cpu_tokens + 2}); 1 thread: {res[1]:.4f} tok/s; host CPU: {cpu_model()}, "
                          f"{os.cpu_count()} hardware threads visible"}

@@ -122,6 +122,37 @@ class Engine:
         self._check(self.L.ec_engine_get_state(self.h, layer, which, seq, out.ctypes.data, out.nbytes), "get_state")
         return out
 
+    def export_model(self) -> dict:
+        """Copy the weights back to the host in the oracle decoder's weight
+        dict: GGUF Q8_0 matrices (w_in = the fused input-projection rows),
+        fp32 vectors."""
+        cfg = self.cfg
+        H, F = cfg.hidden, cfg.ffn
+        q8 = lambda rows, K: rows * (K // 32) * 34  # noqa: E731
+        f32 = lambda n: (n * 4, np.float32)  # noqa: E731
+        m = {"embed": self.get_tensor(0, T_EMBED, q8(cfg.vocab, H)),
+             "final_norm": self.get_tensor(0, T_FINAL_NORM, *f32(H)),
+             "lm_head": self.get_tensor(0, T_LM_HEAD, q8(cfg.vocab, H)), "layers": []}
+        for l in range(cfg.n_layers):
+            attn = cfg.is_attn(l)
+            nin = cfg.nin_attn if attn else cfg.nin_delta
+            kout = cfg.n_heads * cfg.head_dim if attn else cfg.ssm_inner
+            y = {"attn": attn, "w_in": self.get_tensor(l, T_W_IN, q8(nin, H)),
+                 "w_out": self.get_tensor(l, T_W_OUT, q8(H, kout)), "w_gate": self.get_tensor(l, T_W_GATE, q8(F, H)),
+                 "w_up": self.get_tensor(l, T_W_UP, q8(F, H)), "w_down": self.get_tensor(l, T_W_DOWN, q8(H, F)),
+                 "attn_norm": self.get_tensor(l, T_ATTN_NORM, *f32(H)),
+                 "ffn_norm": self.get_tensor(l, T_FFN_NORM, *f32(H))}
+            if attn:
+                y["q_norm"] = self.get_tensor(l, T_Q_NORM, *f32(cfg.head_dim))
+                y["k_norm"] = self.get_tensor(l, T_K_NORM, *f32(cfg.head_dim))
+            else:
+                y["conv_w"] = self.get_tensor(l, T_CONV_W, *f32(cfg.conv_kernel * cfg.conv_dim))
+                y["a_log"] = self.get_tensor(l, T_A_LOG, *f32(cfg.ssm_heads))
+                y["dt_bias"] = self.get_tensor(l, T_DT_BIAS, *f32(cfg.ssm_heads))
+                y["ssm_norm"] = self.get_tensor(l, T_SSM_NORM, *f32(128))
+            m["layers"].append(y)
+        return m
+
     def init_random(self, seed: int = 0, w_scale: float = 0.02 / 73.0):
         self._check(self.L.ec_engine_init_random(self.h, seed, w_scale), "init_random")
 
