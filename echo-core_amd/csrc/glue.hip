@@ -165,6 +165,51 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm_quant(const float* __restri
     store_act_q8_lane(xk * inv * wk, act, (float*)(act + xd_off), M, Kp / 32, i, k);
 }
 
+// Row variant: grid (M), block Kp/4 threads (Kp <= 4096), thread = 4
+// consecutive elements (one float4 of x and of each partial); the row is read
+// once.  Eight lanes form one Q8_0 block (max over 8 lanes), each stores its
+// 4 quantized bytes as one word.
+template <int NP>
+__global__ __launch_bounds__(1024) void k_add_rmsnorm_quant_row(const float* __restrict__ x,
+                                                               const float* __restrict__ parts,
+                                                               float* __restrict__ x_out, const float* __restrict__ w,
+                                                               uint8_t* __restrict__ act, uint32_t M, uint32_t H,
+                                                               uint32_t xd_off) {
+    __shared__ float sh[16];
+    const uint32_t i = blockIdx.x, t = threadIdx.x, k = 4 * t, lane = t & 63, wv = t >> 6;
+    const size_t ps = (size_t)M * H;
+    const uint32_t Kp = round_up(H, 128), nbp = Kp / 32;
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), wk = a;
+    if (k < H) {
+        float4 pv[NP];
+#pragma unroll
+        for (int p = 0; p < NP; ++p) pv[p] = *(const float4*)(parts + p * ps + (size_t)i * H + k);
+        a = *(const float4*)(x + (size_t)i * H + k);
+        wk = *(const float4*)(w + k);
+#pragma unroll
+        for (int p = 0; p < NP; ++p) a.x += pv[p].x, a.y += pv[p].y, a.z += pv[p].z, a.w += pv[p].w;
+        *(float4*)(x_out + (size_t)i * H + k) = a;
+    }
+    float ss = fmaf(a.x, a.x, fmaf(a.y, a.y, fmaf(a.z, a.z, a.w * a.w)));
+    ss = wave_sum(ss);
+    if (lane == 0) sh[wv] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (uint32_t v = 0; v < blockDim.x / 64; ++v) tot += sh[v];
+    const float inv = 1.0f / sqrtf(tot / (float)H + 1e-6f);
+    const float v0 = a.x * inv * wk.x, v1 = a.y * inv * wk.y, v2 = a.z * inv * wk.z, v3 = a.w * inv * wk.w;
+    float amax = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    const float scale = q_scale(amax);
+    const float iq = __fdiv_rn(1.0f, scale);
+    const uint32_t word = (uint32_t)(uint8_t)q_body(v0, iq) | ((uint32_t)(uint8_t)q_body(v1, iq) << 8) |
+                          ((uint32_t)(uint8_t)q_body(v2, iq) << 16) | ((uint32_t)(uint8_t)q_body(v3, iq) << 24);
+    const uint32_t sb = k / 32, e = k % 32, G = sb / 4, j = sb % 4;
+    *(uint32_t*)(act + (((size_t)G * 4 + e / 8) * M + i) * 32 + 8 * j + (e % 8)) = word;
+    if (e == 0) ((float*)(act + xd_off))[(size_t)i * nbp + sb] = scale;
+}
+
 // ------------------------------------------------------- SwiGLU + quantize
 // gu [M][2F] (gate rows then up rows) -> act (K = F).  grid (ceil(Kp/256), M),
 // thread = element.
@@ -486,6 +531,7 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float* __restrict
 
 }  // namespace ec
 
+
 using namespace ec;
 
 #define EC_GLUE_LAUNCH(...)                        \
@@ -521,6 +567,17 @@ extern "C" int ec_glue_add_rmsnorm_quant(const float* x, const float* parts, uin
     const hipStream_t st = (hipStream_t)stream;
     uint8_t* a = (uint8_t*)act;
     const uint32_t xo = (uint32_t)L.xd_off;
+    // one workgroup per row where it fits (rows up to 4096, 16-byte aligned rows): 2560-wide rows
+    // 3.9 -> ~3.5 us per call in the decode step; otherwise row-parallel blocks
+    if (nparts <= 4 && L.Kp <= 4096 && H % 4 == 0 && ((uintptr_t)x_out & 15) == 0 && ((uintptr_t)w & 15) == 0) {
+        const dim3 g1(M), b1(L.Kp / 4);
+        switch (nparts) {
+            case 1: EC_GLUE_LAUNCH(k_add_rmsnorm_quant_row<1>, g1, b1, 0, st, x, parts, x_out, w, a, M, H, xo);
+            case 2: EC_GLUE_LAUNCH(k_add_rmsnorm_quant_row<2>, g1, b1, 0, st, x, parts, x_out, w, a, M, H, xo);
+            case 3: EC_GLUE_LAUNCH(k_add_rmsnorm_quant_row<3>, g1, b1, 0, st, x, parts, x_out, w, a, M, H, xo);
+            default: EC_GLUE_LAUNCH(k_add_rmsnorm_quant_row<4>, g1, b1, 0, st, x, parts, x_out, w, a, M, H, xo);
+        }
+    }
     switch (nparts) {
         case 1: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<1>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo);
         case 2: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<2>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo);
