@@ -18,12 +18,38 @@ __device__ __forceinline__ float h2f(uint16_t h) {
     return __half2float(__ushort_as_half(h));
 }
 
-// Sum over the 16 lanes of a DPP row; every lane of the row receives the total.
+// Value of lane i ^ O.  Inside a 16-lane row (O < 16) this is DPP on the
+// VALU (a few cycles); across rows it is ds_bpermute (an LDS round trip).
+//   O = 1, 2: quad_perm [1,0,3,2] / [2,3,0,1]
+//   O = 4:    row_shl:4 into banks 0 and 2 (lane i reads i+4), row_shr:4 into
+//             banks 1 and 3 (lane i reads i-4)
+//   O = 8:    row_ror:8 (i+8 mod 16 == i^8)
+template <int CTRL, int BANKS>
+__device__ __forceinline__ int dpp_i(int old, int v) {
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, 0xF, BANKS, false);
+}
+template <int O>
+__device__ __forceinline__ int lane_xor_i(int v) {
+    static_assert(O == 1 || O == 2 || O == 4 || O == 8 || O == 16 || O == 32, "xor of 1 .. 32");
+    if constexpr (O == 1) return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);
+    else if constexpr (O == 2) return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);
+    else if constexpr (O == 4) return dpp_i<0x114, 0xA>(dpp_i<0x104, 0x5>(v, v), v);
+    else if constexpr (O == 8) return __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, true);
+    else return __shfl_xor(v, O);
+}
+template <int O>
+__device__ __forceinline__ float lane_xor(float v) {
+    return __int_as_float(lane_xor_i<O>(__float_as_int(v)));
+}
+
+// Sum over the 16 lanes of a DPP row; every lane of the row receives the total
+// (butterfly xor 1, 2, 4, 8: each level adds the same two partial sums in
+// every lane, so all lanes hold the identical total).
 __device__ __forceinline__ float row16_sum(float v) {
-    v += __shfl_xor(v, 1);
-    v += __shfl_xor(v, 2);
-    v += __shfl_xor(v, 4);
-    v += __shfl_xor(v, 8);
+    v += lane_xor<1>(v);
+    v += lane_xor<2>(v);
+    v += lane_xor<4>(v);
+    v += lane_xor<8>(v);
     return v;
 }
 
@@ -36,13 +62,24 @@ __device__ __forceinline__ float sq_rn(float x) {
     return x * x;
 }
 
+// Butterfly over the wave, xor 32 first (the same association in every lane).
 __device__ __forceinline__ float wave_sum(float v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    v += lane_xor<32>(v);
+    v += lane_xor<16>(v);
+    v += lane_xor<8>(v);
+    v += lane_xor<4>(v);
+    v += lane_xor<2>(v);
+    v += lane_xor<1>(v);
     return v;
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    v = fmaxf(v, lane_xor<32>(v));
+    v = fmaxf(v, lane_xor<16>(v));
+    v = fmaxf(v, lane_xor<8>(v));
+    v = fmaxf(v, lane_xor<4>(v));
+    v = fmaxf(v, lane_xor<2>(v));
+    v = fmaxf(v, lane_xor<1>(v));
     return v;
 }
 
@@ -114,8 +151,11 @@ __device__ __forceinline__ float conv_ring(const float* __restrict__ st, const f
 __device__ __forceinline__ void store_act_q8_lane(float v, uint8_t* __restrict__ act, float* __restrict__ xd,
                                                   uint32_t M, uint32_t nbp, uint32_t i, uint32_t k) {
     float amax = fabsf(v);
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    amax = fmaxf(amax, lane_xor<1>(amax));
+    amax = fmaxf(amax, lane_xor<2>(amax));
+    amax = fmaxf(amax, lane_xor<4>(amax));
+    amax = fmaxf(amax, lane_xor<8>(amax));
+    amax = fmaxf(amax, lane_xor<16>(amax));
     const float scale = q_scale(amax);
     const float inv = __fdiv_rn(1.0f, scale);
     const uint32_t b = (uint8_t)q_body(v, inv);

@@ -7,8 +7,11 @@
 // beta), so the work splits into n_seq*n_v*d_v columns of d_k = 128 floats.
 // The state is stored per head TRANSPOSED relative to the reference, S[v][k],
 // so one column is 512 contiguous bytes.  A DPP row of 16 lanes owns one
-// column, 8 k-entries per lane in VGPRs: both column reductions (kv and o) are
-// 4 xor-shuffle adds inside the row, no LDS and no barrier.  A wave holds 4
+// column, 8 k-entries per lane in VGPRs.  The multi-token kernel takes both
+// column dots of a token (S.k and S.q) from the state before its update and
+// reduces them together with 4 DPP adds each inside the row (no LDS, no
+// barrier): o = (decay*S.q + delta*(k.q))/sqrt(d_k) equals S'^T q/sqrt(d_k)
+// for the updated S', so one reduction latency per token.  A wave holds 4
 // columns (2 KB of state, two 16-byte loads per lane), a 256-thread workgroup
 // 16 columns of one head.  Across the T tokens of one launch the state never
 // leaves the VGPRs; the inputs (which do not depend on the recurrence) are
@@ -30,7 +33,7 @@ constexpr uint32_t kDnBlock = 32;
 struct DnLds {
     f32x4 q[2][kDnBlock][32], k[2][kDnBlock][32];
     float v[2][kDnBlock][16];
-    float dec[2][kDnBlock], bt[2][kDnBlock];
+    float dec[2][kDnBlock], bt[2][kDnBlock], kq[2][kDnBlock];
 };
 
 // grid (n_v * d_v/16, n_seq), block 256: threadIdx/16 = column in the group, %16 = k slice.
@@ -75,12 +78,21 @@ __global__ __launch_bounds__(256) void k_deltanet(float* __restrict__ state, con
         const size_t hv = ((size_t)t * n_seq + s) * n_v + h;
         rdb = (tid < 2 * kDnBlock && t < T) ? (tid < kDnBlock ? decay[hv] : beta[hv]) : 0.0f;
     };
+    // also k.q of each token (32 lanes hold one token's q and k): the output
+    // needs it, and it does not depend on the state
     auto stage_store = [&](uint32_t buf) {
 #pragma unroll
         for (uint32_t u = 0; u < NQ; ++u) {
             const uint32_t id = tid + 256 * u;
             L.q[buf][id / 32][id % 32] = rq[u];
             L.k[buf][id / 32][id % 32] = rk[u];
+            float kq = rq[u].x * rk[u].x + rq[u].y * rk[u].y + rq[u].z * rk[u].z + rq[u].w * rk[u].w;
+            kq += lane_xor<1>(kq);
+            kq += lane_xor<2>(kq);
+            kq += lane_xor<4>(kq);
+            kq += lane_xor<8>(kq);
+            kq += lane_xor<16>(kq);
+            if (id % 32 == 0) L.kq[buf][id / 32] = kq;
         }
 #pragma unroll
         for (uint32_t u = 0; u < NV; ++u) {
@@ -99,28 +111,46 @@ __global__ __launch_bounds__(256) void k_deltanet(float* __restrict__ state, con
         const uint32_t buf = b & 1, t0 = b * kDnBlock;
         stage_load(t0 + kDnBlock);  // past T: zeros, no memory access
         const uint32_t nt = min(kDnBlock, T - t0);
+        // Per token, both column dots come from the state before the update:
+        //   a = S.k, b = S.q  (one pair of row reductions),
+        //   kv = dec*a, delta = (v - kv)*beta,
+        //   o = (dec*S + k delta).q/sqrt(128) = (dec*b + delta*(k.q))/sqrt(128),
+        //   S <- dec*S + k delta.
+        // Token j+1's operands are read from LDS while token j is computed.
+        f32x4 k0 = L.k[buf][0][2 * ks], k1 = L.k[buf][0][2 * ks + 1];
+        f32x4 q0 = L.q[buf][0][2 * ks], q1 = L.q[buf][0][2 * ks + 1];
+        float vv = L.v[buf][0][row], dec = L.dec[buf][0], bt = L.bt[buf][0], kq = L.kq[buf][0];
         for (uint32_t j = 0; j < nt; ++j) {
-            const f32x4 k0 = L.k[buf][j][2 * ks], k1 = L.k[buf][j][2 * ks + 1];
-            const f32x4 q0 = L.q[buf][j][2 * ks], q1 = L.q[buf][j][2 * ks + 1];
-            const float vv = L.v[buf][j][row], dec = L.dec[buf][j], bt = L.bt[buf][j];
+            const uint32_t jn = j + 1 < nt ? j + 1 : j;
+            const f32x4 nk0 = L.k[buf][jn][2 * ks], nk1 = L.k[buf][jn][2 * ks + 1];
+            const f32x4 nq0 = L.q[buf][jn][2 * ks], nq1 = L.q[buf][jn][2 * ks + 1];
+            const float nvv = L.v[buf][jn][row], ndec = L.dec[buf][jn], nbt = L.bt[buf][jn], nkq = L.kq[buf][jn];
             const float kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
             const float qq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-            float kvp = 0.0f;
+            float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                S[i] *= dec;
-                kvp = fmaf(S[i], kk[i], kvp);
+            for (int i = 0; i < 4; ++i) {
+                a0 = fmaf(S[i], kk[i], a0);
+                b0 = fmaf(S[i], qq[i], b0);
+                a1 = fmaf(S[4 + i], kk[4 + i], a1);
+                b1 = fmaf(S[4 + i], qq[4 + i], b1);
             }
-            const float kv = row16_sum(kvp);
-            const float delta = (vv - kv) * bt;
-            float op = 0.0f;
+            float a = a0 + a1, bq = b0 + b1;
+            a += lane_xor<1>(a);
+            bq += lane_xor<1>(bq);
+            a += lane_xor<2>(a);
+            bq += lane_xor<2>(bq);
+            a += lane_xor<4>(a);
+            bq += lane_xor<4>(bq);
+            a += lane_xor<8>(a);
+            bq += lane_xor<8>(bq);
+            const float delta = (vv - dec * a) * bt;
+            const float o = (dec * bq + delta * kq) * scale;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                S[i] = fmaf(kk[i], delta, S[i]);
-                op = fmaf(S[i], qq[i] * scale, op);
-            }
-            const float o = row16_sum(op);
+            for (int i = 0; i < 8; ++i) S[i] = fmaf(kk[i], delta, S[i] * dec);
             if (ks == 0) out[(((size_t)(t0 + j) * n_seq + s) * n_v + h) * d_v + col] = o;
+            k0 = nk0, k1 = nk1, q0 = nq0, q1 = nq1;
+            vv = nvv, dec = ndec, bt = nbt, kq = nkq;
         }
         stage_store(buf ^ 1);
         __syncthreads();
@@ -266,9 +296,9 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
         S[i] *= dec;
         kvp = fmaf(S[i], kk[i], kvp);
     }
-    kvp += __shfl_xor(kvp, 1);
-    kvp += __shfl_xor(kvp, 2);
-    kvp += __shfl_xor(kvp, 4);
+    kvp += lane_xor<1>(kvp);
+    kvp += lane_xor<2>(kvp);
+    kvp += lane_xor<4>(kvp);
     const float delta = (v_s[col] - kvp) * bt;
     float op = 0.0f;
 #pragma unroll
@@ -276,9 +306,9 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
         S[i] = fmaf(kk[i], delta, S[i]);
         op = fmaf(S[i], qq[i] * scale, op);
     }
-    op += __shfl_xor(op, 1);
-    op += __shfl_xor(op, 2);
-    op += __shfl_xor(op, 4);
+    op += lane_xor<1>(op);
+    op += lane_xor<2>(op);
+    op += lane_xor<4>(op);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const f32x4 v4 = {S[4 * u], S[4 * u + 1], S[4 * u + 2], S[4 * u + 3]};
