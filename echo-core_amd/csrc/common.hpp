@@ -41,6 +41,13 @@ template <int O>
 __device__ __forceinline__ float lane_xor(float v) {
     return __int_as_float(lane_xor_i<O>(__float_as_int(v)));
 }
+// Value of lane i + N of the same 16-lane row (DPP row_shl:N, N = 1 .. 15);
+// a lane whose source lies past the row's end reads 0.
+template <int N>
+__device__ __forceinline__ uint32_t row_down(uint32_t v) {
+    static_assert(N >= 1 && N <= 15, "shift inside a row");
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x100 + N, 0xF, 0xF, true);
+}
 
 // Sum over the 16 lanes of a DPP row; every lane of the row receives the total
 // (butterfly xor 1, 2, 4, 8: each level adds the same two partial sums in
@@ -159,7 +166,7 @@ __device__ __forceinline__ void store_act_q8_lane(float v, uint8_t* __restrict__
     const float scale = q_scale(amax);
     const float inv = __fdiv_rn(1.0f, scale);
     const uint32_t b = (uint8_t)q_body(v, inv);
-    const uint32_t w = b | (__shfl_down(b, 1) << 8) | (__shfl_down(b, 2) << 16) | (__shfl_down(b, 3) << 24);
+    const uint32_t w = b | (row_down<1>(b) << 8) | (row_down<2>(b) << 16) | (row_down<3>(b) << 24);
     const uint32_t sb = k / 32, e = k % 32, G = sb / 4, j = sb % 4;
     if ((e & 3) == 0) *(uint32_t*)(act + (((size_t)G * 4 + e / 8) * M + i) * 32 + 8 * j + (e % 8)) = w;
     if (e == 0) xd[(size_t)i * nbp + sb] = scale;

@@ -116,17 +116,22 @@ __global__ __launch_bounds__(256) void k_deltanet(float* __restrict__ state, con
         //   kv = dec*a, delta = (v - kv)*beta,
         //   o = (dec*S + k delta).q/sqrt(128) = (dec*b + delta*(k.q))/sqrt(128),
         //   S <- dec*S + k delta.
-        // Token j+1's operands are read from LDS while token j is computed.
-        f32x4 k0 = L.k[buf][0][2 * ks], k1 = L.k[buf][0][2 * ks + 1];
-        f32x4 q0 = L.q[buf][0][2 * ks], q1 = L.q[buf][0][2 * ks + 1];
-        float vv = L.v[buf][0][row], dec = L.dec[buf][0], bt = L.bt[buf][0], kq = L.kq[buf][0];
-        for (uint32_t j = 0; j < nt; ++j) {
-            const uint32_t jn = j + 1 < nt ? j + 1 : j;
-            const f32x4 nk0 = L.k[buf][jn][2 * ks], nk1 = L.k[buf][jn][2 * ks + 1];
-            const f32x4 nq0 = L.q[buf][jn][2 * ks], nq1 = L.q[buf][jn][2 * ks + 1];
-            const float nvv = L.v[buf][jn][row], ndec = L.dec[buf][jn], nbt = L.bt[buf][jn], nkq = L.kq[buf][jn];
-            const float kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-            const float qq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        // Token j+1's operands are read from LDS while token j is computed (two
+        // register sets used in turn).
+        struct Ops {
+            f32x4 k0, k1, q0, q1;
+            float vv, dec, bt, kq;
+        };
+        auto read_ops = [&](uint32_t j) {
+            Ops o;
+            o.k0 = L.k[buf][j][2 * ks], o.k1 = L.k[buf][j][2 * ks + 1];
+            o.q0 = L.q[buf][j][2 * ks], o.q1 = L.q[buf][j][2 * ks + 1];
+            o.vv = L.v[buf][j][row], o.dec = L.dec[buf][j], o.bt = L.bt[buf][j], o.kq = L.kq[buf][j];
+            return o;
+        };
+        auto token = [&](const Ops& x, uint32_t j) {
+            const float kk[8] = {x.k0.x, x.k0.y, x.k0.z, x.k0.w, x.k1.x, x.k1.y, x.k1.z, x.k1.w};
+            const float qq[8] = {x.q0.x, x.q0.y, x.q0.z, x.q0.w, x.q1.x, x.q1.y, x.q1.z, x.q1.w};
             float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -144,13 +149,19 @@ __global__ __launch_bounds__(256) void k_deltanet(float* __restrict__ state, con
             bq += lane_xor<4>(bq);
             a += lane_xor<8>(a);
             bq += lane_xor<8>(bq);
-            const float delta = (vv - dec * a) * bt;
-            const float o = (dec * bq + delta * kq) * scale;
+            const float delta = (x.vv - x.dec * a) * x.bt;
+            const float o = (x.dec * bq + delta * x.kq) * scale;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) S[i] = fmaf(kk[i], delta, S[i] * dec);
+            for (int i = 0; i < 8; ++i) S[i] = fmaf(kk[i], delta, S[i] * x.dec);
             if (ks == 0) out[(((size_t)(t0 + j) * n_seq + s) * n_v + h) * d_v + col] = o;
-            k0 = nk0, k1 = nk1, q0 = nq0, q1 = nq1;
-            vv = nvv, dec = ndec, bt = nbt, kq = nkq;
+        };
+        Ops A = read_ops(0);
+        for (uint32_t j = 0; j < nt; j += 2) {
+            const Ops B = read_ops(j + 1 < nt ? j + 1 : j);
+            token(A, j);
+            if (j + 1 >= nt) break;
+            A = read_ops(j + 2 < nt ? j + 2 : j + 1);
+            token(B, j + 1);
         }
         stage_store(buf ^ 1);
         __syncthreads();

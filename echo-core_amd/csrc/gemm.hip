@@ -85,16 +85,18 @@ __global__ __launch_bounds__(256) void k_gemm_quantize_x(const float* __restrict
     const bool real = m < M && k < K;
     const float v = real ? x[(size_t)m * ldx + k] : 0.0f;
     float amax = fabsf(v);
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
+    amax = fmaxf(amax, lane_xor<1>(amax));
+    amax = fmaxf(amax, lane_xor<2>(amax));
+    amax = fmaxf(amax, lane_xor<4>(amax));
+    amax = fmaxf(amax, lane_xor<8>(amax));
+    amax = fmaxf(amax, lane_xor<16>(amax));
     const float scale = q_scale(amax);
     const float inv = __fdiv_rn(1.0f, scale);
     const int8_t q = q_body(v, inv);  // a 32-element row: all elements are in whole 8-chunks
     const uint32_t T = m / 16, r = m % 16;
     // 4 consecutive elements' bytes, gathered at the first lane of each 4
     const uint32_t qb = (uint8_t)q;
-    const uint32_t w4 = qb | (__shfl_down(qb, 1, 32) << 8) | (__shfl_down(qb, 2, 32) << 16) |
-                        (__shfl_down(qb, 3, 32) << 24);
+    const uint32_t w4 = qb | (row_down<1>(qb) << 8) | (row_down<2>(qb) << 16) | (row_down<3>(qb) << 24);
     if constexpr (Q4) {
         // elements 4g..4g+3 are bytes 0..3 and elements 16+4g..16+4g+3 bytes
         // 4..7 of lane r + 16g of sub-block pair s/2
@@ -106,7 +108,7 @@ __global__ __launch_bounds__(256) void k_gemm_quantize_x(const float* __restrict
         }
     } else {
         // elements 8g..8g+7 are the 8 bytes of lane r + 16g
-        const uint32_t hi = __shfl_down(w4, 4, 32);
+        const uint32_t hi = row_down<4>(w4);
         if ((i & 7) == 0) {
             const uint32_t G = b / 4, j = b % 4, l = r + 16 * (i / 8);
             *(uint2*)(xt + ((size_t)T * nch + G) * 2048 + (j / 2) * 1024 + 16 * l + 8 * (j % 2)) = make_uint2(w4, hi);
@@ -114,8 +116,11 @@ __global__ __launch_bounds__(256) void k_gemm_quantize_x(const float* __restrict
     }
     int sum = q;
     if constexpr (Q4) {
-#pragma unroll
-        for (int o = 1; o < 32; o <<= 1) sum += __shfl_xor(sum, o, 32);
+        sum += lane_xor_i<1>(sum);
+        sum += lane_xor_i<2>(sum);
+        sum += lane_xor_i<4>(sum);
+        sum += lane_xor_i<8>(sum);
+        sum += lane_xor_i<16>(sum);
     }
     if (i == 0) {
         float* xd = (float*)(xt + xd_off);

@@ -199,8 +199,9 @@ __global__ __launch_bounds__(1024) void k_add_rmsnorm_quant_row(const float* __r
     const float inv = 1.0f / sqrtf(tot / (float)H + 1e-6f);
     const float v0 = a.x * inv * wk.x, v1 = a.y * inv * wk.y, v2 = a.z * inv * wk.z, v3 = a.w * inv * wk.w;
     float amax = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    amax = fmaxf(amax, lane_xor<1>(amax));
+    amax = fmaxf(amax, lane_xor<2>(amax));
+    amax = fmaxf(amax, lane_xor<4>(amax));
     const float scale = q_scale(amax);
     const float iq = __fdiv_rn(1.0f, scale);
     const uint32_t word = (uint32_t)(uint8_t)q_body(v0, iq) | ((uint32_t)(uint8_t)q_body(v1, iq) << 8) |
@@ -439,7 +440,7 @@ __global__ __launch_bounds__(256) void k_qk_rope_append(const float* __restrict_
         val = val * inv * nw;
     }
     if (is_q || is_k) {
-        const float other = __shfl_xor(val, 1);
+        const float other = lane_xor<1>(val);
         val = rope_pair(val, other, d, (float)p * ifr);
     }
     if (is_q) {
@@ -501,14 +502,18 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float* __restrict
     } else {
         for (uint32_t k = t; k < vocab; k += 1024) take(l[k], k);
     }
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(best, o);
-        const int32_t oi = __shfl_xor(bi, o);
+    auto merge = [&](float ov, int32_t oi) {
         if (ov > best || (ov == best && oi < bi)) {
             best = ov;
             bi = oi;
         }
-    }
+    };
+    merge(lane_xor<32>(best), lane_xor_i<32>(bi));
+    merge(lane_xor<16>(best), lane_xor_i<16>(bi));
+    merge(lane_xor<8>(best), lane_xor_i<8>(bi));
+    merge(lane_xor<4>(best), lane_xor_i<4>(bi));
+    merge(lane_xor<2>(best), lane_xor_i<2>(bi));
+    merge(lane_xor<1>(best), lane_xor_i<1>(bi));
     if ((t & 63) == 0) {
         sv[t >> 6] = best;
         si[t >> 6] = bi;

@@ -42,7 +42,7 @@ __global__ __launch_bounds__(64) void k_quantize_rows(const float* __restrict__ 
     int8_t* qr = q + (size_t)r * width;
     float amax = 0.0f;
     for (uint32_t i = threadIdx.x; i < width; i += 64) amax = fmaxf(amax, fabsf(xr[i]));
-    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    amax = wave_max(amax);
     float scale = q_scale(amax);
     float inv = __fdiv_rn(1.0f, scale);
     uint32_t body = width & ~7u;
