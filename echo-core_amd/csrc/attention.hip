@@ -387,45 +387,55 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ q
     }
 }
 
-// grid (n_heads, n_seq), block 1024 (16 waves): merge chunk partials.  The
-// chunk weights exp(m_c - M) go through LDS; wave w then sums chunks w, w+16,
-// ... with lane = 4 dims (1 KB per wave load), and the sixteen wave sums are
-// added in LDS.  (16 waves instead of 8: 32k-position context 38.7 -> 34.4 us.)
+// grid (n_heads, n_seq, DS), block 1024 (16 waves): merge chunk partials.  The
+// chunk weights exp(m_c - M) go through LDS; workgroup z covers dims
+// [256/DS*z, 256/DS*(z+1)) with lane = 4 dims, so one wave load brings the
+// slice of DS chunk records (1 KB); wave w sums chunks DS*(w + 16i) + lane
+// group, and the wave sums are added in LDS.  DS = 4 when the heads and
+// sequences alone give few workgroups (one long sequence: every workgroup
+// otherwise streams 1 KB per chunk through one CU).  (16 waves instead of 8:
+// 32k-position context 38.7 -> 34.4 us.)
 constexpr uint32_t kMergeWaves = 16;
 constexpr uint32_t kMergeThreads = 64 * kMergeWaves;
 constexpr uint32_t kMergeRegs = 8;  // chunk records per wave loaded per batch (the first with the maxima)
 
 // With act != nullptr the merged rows are also quantized into the Q8_0
 // activation layout (M = n_seq rows, K = n_heads*256; quantize_act's format).
+template <int DS>
 __global__ __launch_bounds__(kMergeThreads) void k_attn_merge(const float* __restrict__ ws, const int32_t* __restrict__ ctx,
                                                     float* __restrict__ out, uint8_t* __restrict__ act,
                                                     uint32_t act_xd_off, uint32_t n_seq, uint32_t n_heads,
                                                     uint32_t n_chunks_max,
                                                     uint32_t max_ctx, uint32_t chunk) {
+    static_assert(DS == 1 || DS == 2 || DS == 4, "dim slices of 256, 128 or 64");
+    constexpr uint32_t HD = 256, SD = HD / DS, LPR = 64 / DS;  // slice dims, lanes per record
     extern __shared__ float w_s[];
     __shared__ float red[kMergeWaves];
     __shared__ float4 acc_s[kMergeWaves][64];
-    const uint32_t HD = 256;
-    const uint32_t h = blockIdx.x, s = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const uint32_t h = blockIdx.x, s = blockIdx.y, z = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const uint32_t sub = lane / LPR, d4 = lane % LPR;  // record within the wave load, 4-dim group in the slice
     const int32_t L = min(ctx[s], (int32_t)max_ctx);
-    float* dst = out + ((size_t)s * n_heads + h) * HD;
+    float* dst = out + ((size_t)s * n_heads + h) * HD + SD * z;
     if (L <= 0) {
-        if (tid < HD) {
+        if (tid < SD) {
             dst[tid] = 0.0f;
-            if (act) store_act_q8_lane(0.0f, act, (float*)(act + act_xd_off), n_seq, n_heads * HD / 32, s, h * HD + tid);
+            if (act)
+                store_act_q8_lane(0.0f, act, (float*)(act + act_xd_off), n_seq, n_heads * HD / 32, s,
+                                  h * HD + SD * z + tid);
         }
         return;
     }
     const uint32_t nc = ((uint32_t)L + chunk - 1) / chunk;
     const float* base = ws + ((size_t)s * n_chunks_max * n_heads + h) * kRec64;
     const size_t cs = (size_t)n_heads * kRec64;
-    // the partial outputs of this wave's first kMergeRegs chunks (wv, wv+8, ...)
-    // are loaded together with the chunk maxima, before any reduction
+    const uint32_t doff = 4 + SD * z + 4 * d4;  // this lane's 4 dims in a record
+    // the partial outputs of this lane's first kMergeRegs chunks are loaded
+    // together with the chunk maxima, before any reduction
     float4 ov[kMergeRegs];
 #pragma unroll
     for (int i = 0; i < (int)kMergeRegs; ++i) {
-        const uint32_t c = wv + kMergeWaves * i;
-        ov[i] = c < nc ? *(const float4*)(base + c * cs + 4 + 4 * lane) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const uint32_t c = DS * (wv + kMergeWaves * i) + sub;
+        ov[i] = c < nc ? *(const float4*)(base + c * cs + doff) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     float M = -INFINITY;
     for (uint32_t c = tid; c < nc; c += kMergeThreads) M = fmaxf(M, base[c * cs]);
@@ -445,49 +455,47 @@ __global__ __launch_bounds__(kMergeThreads) void k_attn_merge(const float* __res
     den = wave_sum(den);
     if (lane == 0) red[wv] = den;
     __syncthreads();
-    // chunks in order wv, wv+8, ...: the first kMergeRegs from registers
+    auto add = [](float4& a, float w, const float4& o) {
+        a.x = fmaf(w, o.x, a.x), a.y = fmaf(w, o.y, a.y), a.z = fmaf(w, o.z, a.z), a.w = fmaf(w, o.w, a.w);
+    };
+    // chunks in order i = 0, 1, ...: the first kMergeRegs from registers
     float4 a0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
     for (int i = 0; i < (int)kMergeRegs; ++i) {
-        const uint32_t c = wv + kMergeWaves * i;
-        if (c < nc) {
-            const float w0 = w_s[c];
-            const float4 o0 = ov[i];
-            a0.x = fmaf(w0, o0.x, a0.x), a0.y = fmaf(w0, o0.y, a0.y), a0.z = fmaf(w0, o0.z, a0.z), a0.w = fmaf(w0, o0.w, a0.w);
-        }
+        const uint32_t c = DS * (wv + kMergeWaves * i) + sub;
+        if (c < nc) add(a0, w_s[c], ov[i]);
     }
     // longer contexts: the rest in batches of kMergeRegs records, all loads of a
     // batch in flight before its first add (same order of additions)
-    for (uint32_t c0 = wv + kMergeWaves * kMergeRegs; c0 < nc; c0 += kMergeWaves * kMergeRegs) {
+    for (uint32_t i0 = kMergeRegs; DS * (wv + kMergeWaves * i0) < nc; i0 += kMergeRegs) {
         float4 ob[kMergeRegs];
 #pragma unroll
         for (int i = 0; i < (int)kMergeRegs; ++i) {
-            const uint32_t c = c0 + kMergeWaves * i;
-            ob[i] = c < nc ? *(const float4*)(base + c * cs + 4 + 4 * lane) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const uint32_t c = DS * (wv + kMergeWaves * (i0 + i)) + sub;
+            ob[i] = c < nc ? *(const float4*)(base + c * cs + doff) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
 #pragma unroll
         for (int i = 0; i < (int)kMergeRegs; ++i) {
-            const uint32_t c = c0 + kMergeWaves * i;
-            if (c < nc) {
-                const float w0 = w_s[c];
-                const float4 o0 = ob[i];
-                a0.x = fmaf(w0, o0.x, a0.x), a0.y = fmaf(w0, o0.y, a0.y), a0.z = fmaf(w0, o0.z, a0.z),
-                a0.w = fmaf(w0, o0.w, a0.w);
-            }
+            const uint32_t c = DS * (wv + kMergeWaves * (i0 + i)) + sub;
+            if (c < nc) add(a0, w_s[c], ob[i]);
         }
     }
     acc_s[wv][lane] = a0;
     __syncthreads();
-    if (tid < HD) {
+    if (tid < SD) {
         float dn = red[0], o = 0.0f;
 #pragma unroll
         for (int i = 1; i < (int)kMergeWaves; ++i) dn += red[i];
-        const float* col = (const float*)acc_s + tid;  // dim tid of every wave's sum
+        // dim tid of the slice: float tid of each record group's 64-float run
+        const float* col = (const float*)acc_s + tid;
 #pragma unroll
-        for (int i = 0; i < (int)kMergeWaves; ++i) o += col[i * 256];
+        for (int i = 0; i < (int)kMergeWaves; ++i)
+#pragma unroll
+            for (int r = 0; r < DS; ++r) o += col[i * 256 + r * SD];
         o = o / dn;
         dst[tid] = o;
-        if (act) store_act_q8_lane(o, act, (float*)(act + act_xd_off), n_seq, n_heads * HD / 32, s, h * HD + tid);
+        if (act)
+            store_act_q8_lane(o, act, (float*)(act + act_xd_off), n_seq, n_heads * HD / 32, s, h * HD + SD * z + tid);
     }
 }
 
@@ -526,8 +534,13 @@ static void launch_mfma(const uint8_t* qa, const float* qsc, const int8_t* keys,
         hipLaunchKernelGGL((k_attn_mfma<G, 64>), dim3(ncm, n_kv, n_seq), dim3(256), 0, st, qa, qsc, keys, vals, ks, vs,
                            ctx, seq_stride, n_kv, ncm, max_ctx, ws);
     const uint32_t xd_off = (uint32_t)act_layout(EC_Q8_0, n_seq, n_kv * G * 256).xd_off;
-    hipLaunchKernelGGL(k_attn_merge, dim3(n_kv * G, n_seq), dim3(kMergeThreads), ncm * sizeof(float), st, ws, ctx, out,
-                       act, xd_off, n_seq, n_kv * G, ncm, max_ctx, CH);
+    // few (head, sequence) pairs: four workgroups per pair, 64 dims each
+    if (n_kv * G * n_seq <= 32)
+        hipLaunchKernelGGL(k_attn_merge<4>, dim3(n_kv * G, n_seq, 4), dim3(kMergeThreads), ncm * sizeof(float), st, ws,
+                           ctx, out, act, xd_off, n_seq, n_kv * G, ncm, max_ctx, CH);
+    else
+        hipLaunchKernelGGL(k_attn_merge<1>, dim3(n_kv * G, n_seq), dim3(kMergeThreads), ncm * sizeof(float), st, ws,
+                           ctx, out, act, xd_off, n_seq, n_kv * G, ncm, max_ctx, CH);
 }
 
 static int mfma_dispatch(uint32_t G, const uint8_t* qa, const float* qsc, const int8_t* keys, const int8_t* vals,
