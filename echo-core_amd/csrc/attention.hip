@@ -218,8 +218,12 @@ __global__ __launch_bounds__(256) void k_pack_q(const float* __restrict__ q, uin
     store_q_pieces(val, amax, d, s, head, n_heads, n_kv, qa, qsc);
 }
 
-template <int G, int CH>
+// PQ: q arrives as fp32 [n_seq][n_heads][256] (qf) and the workgroup packs
+// its G heads itself (into LDS that the scores reuse); otherwise qa / qsc hold
+// the packed q.
+template <int G, int CH, bool PQ>
 __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ qa, const float* __restrict__ qsc,
+                                                   const float* __restrict__ qf,
                                                    const int8_t* __restrict__ keys, const int8_t* __restrict__ vals,
                                                    const float* __restrict__ kscales, const float* __restrict__ vscales,
                                                    const int32_t* __restrict__ ctx, uint64_t seq_stride, uint32_t n_kv,
@@ -229,7 +233,9 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ q
     constexpr uint32_t HD = 256;
     constexpr uint32_t NR = kQPieces * G;  // A rows in use
     constexpr int NPW = CH / 64;           // 16-position groups per wave
-    __shared__ float part_s[NR][CH];       // per-piece scores (times the K row scale)
+    __shared__ float part_s[NR][CH];       // per-piece scores (times the K row scale); PQ: packed q first
+    __shared__ float qsc_s[PQ ? NR : 1];
+    __shared__ float qmx_s[PQ ? G : 1][4];
     __shared__ f32x4 p_s[CH];              // [position] probabilities x V row scale, one per head
     __shared__ u32x4 v_s[CH * 16];         // the chunk's V rows, [position][256 bytes]
     const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
@@ -250,16 +256,22 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ q
     // A operand (packed q) and scales, K of this wave's 16-position groups
     // (group q: positions 64q + 16*wv ..), then their V.
     const bool arow = r16 < NR;
-    const uint8_t* qp = qa + ((((size_t)s * n_kv + kvh) * NR + (arow ? r16 : 0)) * 4 + gq) * 64;
     u32x4 aq[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) aq[i] = *(const u32x4*)(qp + 16 * i);
-    const float* scq = qsc + ((size_t)s * n_kv + kvh) * NR;
     float rs[4];  // scale of the A row of each C element this lane holds
+    float qv[G];  // PQ: dim tid of each head of the group
+    if constexpr (!PQ) {
+        const uint8_t* qp = qa + ((((size_t)s * n_kv + kvh) * NR + (arow ? r16 : 0)) * 4 + gq) * 64;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const uint32_t r = 4 * gq + c;
-        rs[c] = scq[r < NR ? r : 0];
+        for (int i = 0; i < 4; ++i) aq[i] = *(const u32x4*)(qp + 16 * i);
+        const float* scq = qsc + ((size_t)s * n_kv + kvh) * NR;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t r = 4 * gq + c;
+            rs[c] = scq[r < NR ? r : 0];
+        }
+    } else {
+#pragma unroll
+        for (int g = 0; g < G; ++g) qv[g] = qf[((size_t)s * n_heads + kvh + n_kv * g) * HD + tid];
     }
     float ksv[NPW], vsv[NPW];
     u32x4 kw[NPW][4];
@@ -284,6 +296,32 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ q
             vv[q][j] = __builtin_nontemporal_load(
                 (const u32x4*)(vb + (size_t)(c0 + (tv < ntok ? tv : 0)) * row + 16 * (lane & 15)));
         }
+
+    if constexpr (PQ) {
+        // pack q (its loads were issued before K and V), then take the A operand from LDS
+        uint8_t* qa_s = (uint8_t*)&part_s[0][0];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float m = wave_max(fabsf(qv[g]));
+            if (lane == 0) qmx_s[g][wv] = m;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float amax = fmaxf(fmaxf(qmx_s[g][0], qmx_s[g][1]), fmaxf(qmx_s[g][2], qmx_s[g][3]));
+            pack_q_pieces(qv[g], amax, tid, g, G, qa_s, qsc_s);
+        }
+        __syncthreads();
+        const uint8_t* qp = qa_s + ((arow ? r16 : 0) * 4 + gq) * 64;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) aq[i] = *(const u32x4*)(qp + 16 * i);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t r = 4 * gq + c;
+            rs[c] = qsc_s[r < NR ? r : 0];
+        }
+        __syncthreads();  // part_s is written below
+    }
 
     // ---- scores of 16 positions per group: 8 accumulating MFMAs; C row r = 4*gq + c
 #pragma unroll
@@ -522,17 +560,25 @@ static uint32_t attn_chunk(uint32_t max_ctx, uint32_t n_kv, uint32_t n_seq) {
 }
 
 template <int G>
-static void launch_mfma(const uint8_t* qa, const float* qsc, const int8_t* keys, const int8_t* vals, const float* ks,
+static void launch_mfma(const uint8_t* qa, const float* qsc, const float* qf, const int8_t* keys, const int8_t* vals,
+                        const float* ks,
                         const float* vs, float* out, uint8_t* act, const int32_t* ctx, uint32_t n_seq,
                         uint64_t seq_stride, uint32_t n_kv, uint32_t max_ctx, float* ws, hipStream_t st) {
     const uint32_t CH = attn_chunk(max_ctx, n_kv, n_seq);
     const uint32_t ncm = (max_ctx + CH - 1) / CH;
-    if (CH == 128)
-        hipLaunchKernelGGL((k_attn_mfma<G, 128>), dim3(ncm, n_kv, n_seq), dim3(256), 0, st, qa, qsc, keys, vals, ks, vs,
-                           ctx, seq_stride, n_kv, ncm, max_ctx, ws);
+    const dim3 grid(ncm, n_kv, n_seq);
+    if (qf && CH == 128)
+        hipLaunchKernelGGL((k_attn_mfma<G, 128, true>), grid, dim3(256), 0, st, qa, qsc, qf, keys, vals, ks, vs, ctx,
+                           seq_stride, n_kv, ncm, max_ctx, ws);
+    else if (qf)
+        hipLaunchKernelGGL((k_attn_mfma<G, 64, true>), grid, dim3(256), 0, st, qa, qsc, qf, keys, vals, ks, vs, ctx,
+                           seq_stride, n_kv, ncm, max_ctx, ws);
+    else if (CH == 128)
+        hipLaunchKernelGGL((k_attn_mfma<G, 128, false>), grid, dim3(256), 0, st, qa, qsc, qf, keys, vals, ks, vs, ctx,
+                           seq_stride, n_kv, ncm, max_ctx, ws);
     else
-        hipLaunchKernelGGL((k_attn_mfma<G, 64>), dim3(ncm, n_kv, n_seq), dim3(256), 0, st, qa, qsc, keys, vals, ks, vs,
-                           ctx, seq_stride, n_kv, ncm, max_ctx, ws);
+        hipLaunchKernelGGL((k_attn_mfma<G, 64, false>), grid, dim3(256), 0, st, qa, qsc, qf, keys, vals, ks, vs, ctx,
+                           seq_stride, n_kv, ncm, max_ctx, ws);
     const uint32_t xd_off = (uint32_t)act_layout(EC_Q8_0, n_seq, n_kv * G * 256).xd_off;
     // few (head, sequence) pairs: four workgroups per pair, 64 dims each
     if (n_kv * G * n_seq <= 32)
@@ -543,11 +589,12 @@ static void launch_mfma(const uint8_t* qa, const float* qsc, const int8_t* keys,
                            ctx, out, act, xd_off, n_seq, n_kv * G, ncm, max_ctx, CH);
 }
 
-static int mfma_dispatch(uint32_t G, const uint8_t* qa, const float* qsc, const int8_t* keys, const int8_t* vals,
+static int mfma_dispatch(uint32_t G, const uint8_t* qa, const float* qsc, const float* qf, const int8_t* keys,
+                         const int8_t* vals,
                          const float* ks, const float* vs, float* out, uint8_t* act, const int32_t* ctx,
                          uint32_t n_seq, uint64_t seq_stride, uint32_t n_kv, uint32_t max_ctx, float* ws,
                          hipStream_t st) {
-#define EC_MF(G_) launch_mfma<G_>(qa, qsc, keys, vals, ks, vs, out, act, ctx, n_seq, seq_stride, n_kv, max_ctx, ws, st)
+#define EC_MF(G_) launch_mfma<G_>(qa, qsc, qf, keys, vals, ks, vs, out, act, ctx, n_seq, seq_stride, n_kv, max_ctx, ws, st)
     switch (G) {
         case 1: EC_MF(1); break;
         case 2: EC_MF(2); break;
@@ -598,9 +645,13 @@ extern "C" int ec_attn_decode(const float* q, const int8_t* keys, const int8_t* 
         const size_t part = (size_t)n_seq * ((max_ctx + kChunk64 - 1) / kChunk64) * n_heads * kRec64 * 4;
         uint8_t* qa = (uint8_t*)ws + ((part + 255) & ~(size_t)255);
         float* qsc = (float*)(qa + qa_bytes(n_seq, n_heads));
-        hipLaunchKernelGGL(k_pack_q, dim3(n_heads, n_seq), dim3(256), 0, st, q, qa, qsc, n_heads, n_kv);
-        int rc = mfma_dispatch(G, qa, qsc, keys, vals, kscales, vscales, out, nullptr, ctx, n_seq, seq_stride, n_kv,
-                               max_ctx, w, st);
+        // few sequences: each attention workgroup packs its own query heads (no
+        // separate pass); many (prefill tokens): one packing pass, so that the
+        // chunk workgroups of a token do not all repeat it
+        const bool own = n_seq <= 16;
+        if (!own) hipLaunchKernelGGL(k_pack_q, dim3(n_heads, n_seq), dim3(256), 0, st, q, qa, qsc, n_heads, n_kv);
+        int rc = mfma_dispatch(G, qa, qsc, own ? q : nullptr, keys, vals, kscales, vscales, out, nullptr, ctx, n_seq,
+                               seq_stride, n_kv, max_ctx, w, st);
         if (rc) return rc;
         EC_CHECK_LAUNCH();
         return EC_OK;
@@ -635,7 +686,7 @@ extern "C" int ec_attn_decode_packed(const void* qa, const float* qsc, const int
         n_heads % n_kv || max_ctx == 0 || (seq_stride != 0 && seq_stride < (uint64_t)max_ctx * n_kv * 256) ||
         (act_q8 && n_seq > 16))
         return ec_set_error(EC_ERR_ARG, "ec_attn_decode_packed: bad argument");
-    int rc = mfma_dispatch(n_heads / n_kv, (const uint8_t*)qa, qsc, keys, vals, kscales, vscales, out,
+    int rc = mfma_dispatch(n_heads / n_kv, (const uint8_t*)qa, qsc, nullptr, keys, vals, kscales, vscales, out,
                            (uint8_t*)act_q8, ctx, n_seq, seq_stride, n_kv, max_ctx, (float*)ws, (hipStream_t)stream);
     if (rc) return rc;
     EC_CHECK_LAUNCH();

@@ -49,22 +49,29 @@ __host__ __device__ inline uint32_t qa_offset(uint32_t d) {
 }
 
 #ifdef __HIPCC__
-// Thread d of a 256-thread group stores dim d of (sequence s, head) given the head's max|q|.
-__device__ inline void store_q_pieces(float val, float amax, uint32_t d, uint32_t s, uint32_t head, uint32_t n_heads,
-                                      uint32_t n_kv, uint8_t* __restrict__ qa, float* __restrict__ qsc) {
-    const uint32_t G = n_heads / n_kv, kvh = head % n_kv, g = head / n_kv;
+// The kQPieces int8 pieces of dim d of query head g (of G per kv head) given
+// the head's max|q|: rows pc*G + g of one kv head's packed block at `rows`
+// ([kQPieces*G][4][64] bytes), piece scales at sc[pc*G + g] (written by d == 0).
+__device__ inline void pack_q_pieces(float val, float amax, uint32_t d, uint32_t g, uint32_t G,
+                                     uint8_t* __restrict__ rows, float* __restrict__ sc) {
     const uint32_t off = qa_offset(d), gq = off >> 16, at = off & 0xFFFF;
-    uint8_t* base = qa + ((size_t)s * n_kv + kvh) * (kQPieces * G) * 4 * 64;
-    float* sc = qsc + ((size_t)s * n_kv + kvh) * kQPieces * G;
     float r = val, step = amax > 0.0f ? amax / 127.0f : 1.0f;
 #pragma unroll
     for (uint32_t pc = 0; pc < kQPieces; ++pc) {
         const float qi = fminf(fmaxf(rintf(r / step), -127.0f), 127.0f);
-        base[((size_t)(pc * G + g) * 4 + gq) * 64 + at] = (uint8_t)(int8_t)qi;
+        rows[((size_t)(pc * G + g) * 4 + gq) * 64 + at] = (uint8_t)(int8_t)qi;
         if (d == 0) sc[pc * G + g] = step;
         r = fmaf(-qi, step, r);
         step = step / 254.0f;
     }
+}
+
+// Thread d of a 256-thread group stores dim d of (sequence s, head) given the head's max|q|.
+__device__ inline void store_q_pieces(float val, float amax, uint32_t d, uint32_t s, uint32_t head, uint32_t n_heads,
+                                      uint32_t n_kv, uint8_t* __restrict__ qa, float* __restrict__ qsc) {
+    const uint32_t G = n_heads / n_kv, kvh = head % n_kv, g = head / n_kv;
+    pack_q_pieces(val, amax, d, g, G, qa + ((size_t)s * n_kv + kvh) * (kQPieces * G) * 4 * 64,
+                  qsc + ((size_t)s * n_kv + kvh) * kQPieces * G);
 }
 #endif
 

@@ -131,7 +131,7 @@ def attention_case(hip, ctxs, n_heads=16, n_kv=4, hd=256, iters=100, seed=0):
     # bytes the path must read: K and V rows plus their scales for every live position, q, out
     alg = sum(ctxs) * n_kv * (2 * hd + 8) + 2 * n_seq * n_heads * hd * 4
     gbs = alg / (mean_us * 1e-6) / 1e9
-    return {"kernel": "k_pack_q+k_attn_mfma+k_attn_merge", "ctxs": ctxs if n_seq <= 8 else f"{n_seq} seqs",
+    return {"kernel": "k_attn_mfma+k_attn_merge", "ctxs": ctxs if n_seq <= 8 else f"{n_seq} seqs",
             "bytes": alg, "us": round(mean_us, 3), "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
             "copies": n_copies}
 
