@@ -236,8 +236,12 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ q
     __shared__ float part_s[NR][CH];       // per-piece scores (times the K row scale); PQ: packed q first
     __shared__ float qsc_s[PQ ? NR : 1];
     __shared__ float qmx_s[PQ ? G : 1][4];
-    __shared__ f32x4 p_s[CH];              // [position] probabilities x V row scale, one per head
-    __shared__ u32x4 v_s[CH * 16];         // the chunk's V rows, [position][256 bytes]
+    // the chunk's V transposed, [dim][position slots]: a dword holds 4 positions
+    // (slot s = 16q + 4w + r: positions 64q + 16w + r + 4e, e = 0..3), rows
+    // padded by one dword
+    constexpr uint32_t RS = CH / 4 + 1;
+    __shared__ uint32_t vT[256 * RS];
+    __shared__ float psc_s[4][4];          // per head: scales of the probability pieces
     const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int32_t L = min(ctx[s], (int32_t)max_ctx);
@@ -338,8 +342,19 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ q
 #pragma unroll
         for (int c = 0; c < 4; ++c)
             if (4 * gq + c < NR) part_s[4 * gq + c][t] = (float)C[c] * rs[c] * ksv[q];
+        // V: dword c of the lane's 16 bytes for positions +0, +4, +8, +12 (loads
+        // j = 0..3) -> four dims x those positions (4x4 byte transpose)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v_s[64 * (16 * q + 4 * wv + j) + lane] = vv[q][j];
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t w0 = vv[q][0][c], w1 = vv[q][1][c], w2 = vv[q][2][c], w3 = vv[q][3][c];
+            const uint32_t a0 = __builtin_amdgcn_perm(w1, w0, 0x05010400u), a1 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);
+            const uint32_t b0 = __builtin_amdgcn_perm(w3, w2, 0x05010400u), b1 = __builtin_amdgcn_perm(w3, w2, 0x07030602u);
+            const uint32_t tb[4] = {__builtin_amdgcn_perm(b0, a0, 0x05040100u), __builtin_amdgcn_perm(b0, a0, 0x07060302u),
+                                    __builtin_amdgcn_perm(b1, a1, 0x05040100u), __builtin_amdgcn_perm(b1, a1, 0x07060302u)};
+            const uint32_t slot = 16 * q + 4 * wv + gq;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) vT[(16 * r16 + 4 * c + b) * RS + slot] = tb[b];
+        }
     }
     __syncthreads();
 
@@ -347,7 +362,7 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ q
     constexpr float scale = 1.0f / 16.0f;  // 1/sqrt(256)
     if (wv == 0) {
         float m[G], l[G];
-        f32x4 pr[NPW];
+        float pr[NPW][G];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             float sc[NPW], mx = -INFINITY;
@@ -368,11 +383,28 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ q
             }
             l[g] = wave_sum(es);
         }
+        // probabilities x V row scale as three int8 pieces per head (as q):
+        // A rows 4g + piece, bytes in the slot order of vT (part_s is free now)
+        uint8_t* pA = (uint8_t*)&part_s[0][0];
+        const uint32_t rr = lane & 15;
 #pragma unroll
-        for (int q = 0; q < NPW; ++q) {
+        for (int g = 0; g < G; ++g) {
+            float mx = 0.0f;
 #pragma unroll
-            for (int g = G; g < 4; ++g) pr[q][g] = 0.0f;
-            p_s[64 * q + lane] = pr[q];
+            for (int q = 0; q < NPW; ++q) mx = fmaxf(mx, pr[q][g]);
+            mx = wave_max(mx);
+#pragma unroll
+            for (int q = 0; q < NPW; ++q) {
+                const uint32_t byte = 4 * (16 * q + 4 * (lane >> 4) + (rr & 3)) + (rr >> 2);
+                int8_t pcs[kQPieces];
+                float steps[kQPieces];
+                split_pieces(pr[q][g], mx, pcs, steps);
+#pragma unroll
+                for (uint32_t pc = 0; pc < kQPieces; ++pc) {
+                    pA[(4 * g + pc) * CH + byte] = (uint8_t)pcs[pc];
+                    if (lane == 0 && q == 0) psc_s[g][pc] = steps[pc];
+                }
+            }
         }
         if (lane == 0) {
 #pragma unroll
@@ -384,44 +416,29 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ q
     }
     __syncthreads();
 
-    // ---- softmax . V: wave wv owns dims 64*wv .. +63 (lane = one 4-dim word),
-    // lane group pg sums positions (CH/4)*pg .. +CH/4-1; the four group sums
-    // are added by cross-lane exchange.  Positions past the chunk end carry
-    // p = 0 (their clamped V rows add nothing).
-    const uint32_t word = 16 * wv + r16, pg = gq;
-    const uint32_t* vrow = (const uint32_t*)v_s;
-    float o[G][4];
+    // ---- softmax . V on v_mfma_i32_16x16x32_i8: A = the probability pieces (row
+    // 4g + piece), B = vT (wave wv: dims 64wv .. +63, four 16-dim tiles), K =
+    // positions in slot order; C element e of lane group g is piece e of head
+    // g, exact int32.  Positions past the chunk end carry p = 0.
+    const uint8_t* pA = (const uint8_t*)&part_s[0][0];
+    v4i Cv[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-        for (int e = 0; e < 4; ++e) o[g][e] = 0.0f;
+    for (uint32_t ks = 0; ks < CH / 32; ++ks) {
+        // rows 4G .. 15 feed only C rows that are not stored: read row 0 there
+        const uint32_t* ap = (const uint32_t*)(pA + (r16 < 4 * G ? r16 : 0) * CH + 32 * ks + 8 * gq);
+        const long A = pack2(ap[0], ap[1]);
 #pragma unroll
-    for (uint32_t i = 0; i < CH / 4; ++i) {
-        const uint32_t tp = (CH / 4) * pg + i;
-        const uint32_t w = vrow[64 * tp + word];
-        const f32x4 p = p_s[tp];
-        const float v0 = (float)(int8_t)(w & 0xFF), v1 = (float)(int8_t)((w >> 8) & 0xFF);
-        const float v2 = (float)(int8_t)((w >> 16) & 0xFF), v3 = (float)(int8_t)(w >> 24);
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            o[g][0] = fmaf(p[g], v0, o[g][0]);
-            o[g][1] = fmaf(p[g], v1, o[g][1]);
-            o[g][2] = fmaf(p[g], v2, o[g][2]);
-            o[g][3] = fmaf(p[g], v3, o[g][3]);
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t* bp = vT + (64 * wv + 16 * t + r16) * RS + 8 * ks + 2 * gq;
+            Cv[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, pack2(bp[0], bp[1]), Cv[t], 0, 0, 0);
         }
     }
+    if (gq < (uint32_t)G) {
+        const float s0 = psc_s[gq][0], s1 = psc_s[gq][1], s2 = psc_s[gq][2];
+        float* rec = ws + (((size_t)s * n_chunks_max + chunk) * n_heads + kvh + n_kv * gq) * kRec64;
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            o[g][e] += __shfl_xor(o[g][e], 16);
-            o[g][e] += __shfl_xor(o[g][e], 32);
-        }
-    if (pg == 0) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float* rec = ws + (((size_t)s * n_chunks_max + chunk) * n_heads + kvh + n_kv * g) * kRec64;
-            *(float4*)(rec + 4 + 4 * word) = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
-        }
+        for (int t = 0; t < 4; ++t)
+            rec[4 + 64 * wv + 16 * t + r16] = (s0 * (float)Cv[t][0] + s1 * (float)Cv[t][1]) + s2 * (float)Cv[t][2];
     }
 }
 

@@ -49,20 +49,39 @@ __host__ __device__ inline uint32_t qa_offset(uint32_t d) {
 }
 
 #ifdef __HIPCC__
+// Three int8 pieces of x for a group whose max |x| is amax:
+//   x ~ sum_pc piece_pc * step_pc,  step_0 = amax/127, step_{pc+1} = step_pc/254,
+// piece_pc = rint(r_pc / step_pc) (clamped), r_{pc+1} = r_pc - piece_pc*step_pc
+// (one rounding, fma); the divisions are products with 1/step_pc, so each
+// value costs one reciprocal per group (|x - sum| <= amax * 6.2e-8).
+__device__ inline void split_pieces(float x, float amax, int8_t (&pc_out)[kQPieces], float (&step_out)[kQPieces]) {
+    float step = amax > 0.0f ? amax * (1.0f / 127.0f) : 1.0f;
+    float inv = amax > 0.0f ? 127.0f / amax : 1.0f;
+    float r = x;
+#pragma unroll
+    for (uint32_t pc = 0; pc < kQPieces; ++pc) {
+        const float qi = fminf(fmaxf(rintf(r * inv), -127.0f), 127.0f);
+        pc_out[pc] = (int8_t)qi;
+        step_out[pc] = step;
+        r = fmaf(-qi, step, r);
+        step = step * (1.0f / 254.0f);
+        inv = inv * 254.0f;
+    }
+}
+
 // The kQPieces int8 pieces of dim d of query head g (of G per kv head) given
 // the head's max|q|: rows pc*G + g of one kv head's packed block at `rows`
 // ([kQPieces*G][4][64] bytes), piece scales at sc[pc*G + g] (written by d == 0).
 __device__ inline void pack_q_pieces(float val, float amax, uint32_t d, uint32_t g, uint32_t G,
                                      uint8_t* __restrict__ rows, float* __restrict__ sc) {
     const uint32_t off = qa_offset(d), gq = off >> 16, at = off & 0xFFFF;
-    float r = val, step = amax > 0.0f ? amax / 127.0f : 1.0f;
+    int8_t pcs[kQPieces];
+    float steps[kQPieces];
+    split_pieces(val, amax, pcs, steps);
 #pragma unroll
     for (uint32_t pc = 0; pc < kQPieces; ++pc) {
-        const float qi = fminf(fmaxf(rintf(r / step), -127.0f), 127.0f);
-        rows[((size_t)(pc * G + g) * 4 + gq) * 64 + at] = (uint8_t)(int8_t)qi;
-        if (d == 0) sc[pc * G + g] = step;
-        r = fmaf(-qi, step, r);
-        step = step / 254.0f;
+        rows[((size_t)(pc * G + g) * 4 + gq) * 64 + at] = (uint8_t)pcs[pc];
+        if (d == 0) sc[pc * G + g] = steps[pc];
     }
 }
 
