@@ -287,7 +287,12 @@ def test_kv_append_bit_exact(hip, oc):
     ([300, 1, 0, 777], 800, 16, 4, 256), ([65, 130], 200, 4, 4, 256), ([129, 64], 192, 8, 4, 256),
     ([333], 400, 32, 4, 256), ([200, 0], 256, 8, 2, 128),
     # 66 chunks of 64 x 4 kv heads x 8 sequences >= 2048 workgroups: 128-position chunks
-    ([4200, 1, 0, 129, 128, 127, 4000, 2050], 4200, 16, 4, 256)])
+    ([4200, 1, 0, 129, 128, 127, 4000, 2050], 4200, 16, 4, 256),
+    # more than 16 sequences: q packed by a separate pass, not by each workgroup
+    ([5 + 37 * i for i in range(20)], 720, 16, 4, 256),
+    # one long sequence: 516 chunks of 64 x 4 kv heads >= 2048 workgroups, so
+    # 128-position chunks, and the merge in four 64-dim slices (16 pairs)
+    ([33000], 33000, 16, 4, 256)])
 def test_attention_decode(hip, oc, ctxs, max_ctx, n_heads, n_kv, hd):
     """16/4 heads and 4/4, 8/4 run the int8-MFMA kernel; 32/4 and head_dim 128 the VALU kernel."""
     import torch
