@@ -418,7 +418,7 @@ __global__ __launch_bounds__(256) void k_qk_rope_append(const float* __restrict_
                                                         int8_t* __restrict__ vals, float* __restrict__ kscales,
                                                         float* __restrict__ vscales, int32_t* __restrict__ ctx,
                                                         uint64_t seq_stride, uint32_t max_ctx, uint32_t n_heads,
-                                                        uint32_t n_kv) {
+                                                        uint32_t n_kv, uint32_t nparts, size_t pstride) {
     __shared__ float sh[4];
     const uint32_t HD = 256;
     const uint32_t head = blockIdx.x, s = blockIdx.y, d = threadIdx.x;
@@ -428,7 +428,13 @@ __global__ __launch_bounds__(256) void k_qk_rope_append(const float* __restrict_
                                                   : n_heads * HD + n_kv * HD + (head - n_heads - n_kv) * HD);
     // inputs first: none of these loads depends on the position
     const bool norm = (is_q && use_qn) || (is_k && use_kn);
-    float val = pr[off + d];
+    float pv[8];  // the projection's partial sums (nparts <= 8), added in part order
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) pv[i] = i < nparts ? pr[i * pstride + off + d] : 0.0f;
+    float val = pv[0];
+#pragma unroll
+    for (uint32_t i = 1; i < 8; ++i)
+        if (i < nparts) val += pv[i];
     const float nw = norm ? (is_q ? q_norm : k_norm)[d] : 1.0f;
     const float ifr = (is_q || is_k) ? inv_freq[d / 2] : 0.0f;
     const int32_t p = pos[s];
@@ -676,20 +682,33 @@ extern "C" int ec_glue_gated_norm_quant(const float* core, const float* proj, ui
                    norm_w, (uint8_t*)act, M, n_v, (uint32_t)L.xd_off);
 }
 
-extern "C" int ec_glue_qk_rope_append(const float* proj, uint32_t Nin, const float* q_norm, const float* k_norm,
+extern "C" int ec_glue_qk_rope_append_split(const float* proj, uint32_t nparts, uint32_t Nin, const float* q_norm,
+                                            const float* k_norm,
                                       int use_qn, int use_kn, const float* inv_freq, const int32_t* pos, float* q_out,
                                       void* q_packed, float* q_scales, int8_t* keys, int8_t* vals, float* kscales,
                                       float* vscales, int32_t* ctx, uint32_t n_seq, uint64_t seq_stride,
                                       uint32_t max_ctx, uint32_t n_heads, uint32_t n_kv, uint32_t head_dim,
                                       void* stream) {
     if (head_dim != 256) return ec_set_error(EC_ERR_UNSUPPORTED, "ec_glue_qk_rope_append: head_dim must be 256");
-    if (!proj || !inv_freq || !pos || (!q_out && !(q_packed && q_scales)) || !keys || !vals || !kscales ||
+    if (!proj || nparts == 0 || nparts > 8 || !inv_freq || !pos || (!q_out && !(q_packed && q_scales)) || !keys ||
+        !vals || !kscales ||
         !vscales || !ctx || n_kv == 0 || n_heads % n_kv ||
         (seq_stride != 0 && seq_stride < (uint64_t)max_ctx * n_kv * head_dim))
         return ec_set_error(EC_ERR_ARG, "ec_glue_qk_rope_append: bad argument");
     EC_GLUE_LAUNCH(k_qk_rope_append, dim3(n_heads + 2 * n_kv, n_seq), dim3(256), 0, (hipStream_t)stream, proj, Nin,
                    q_norm, k_norm, use_qn, use_kn, inv_freq, pos, q_out, (uint8_t*)q_packed, q_scales, keys, vals,
-                   kscales, vscales, ctx, seq_stride, max_ctx, n_heads, n_kv);
+                   kscales, vscales, ctx, seq_stride, max_ctx, n_heads, n_kv, nparts, (size_t)n_seq * Nin);
+}
+
+extern "C" int ec_glue_qk_rope_append(const float* proj, uint32_t Nin, const float* q_norm, const float* k_norm,
+                                      int use_qn, int use_kn, const float* inv_freq, const int32_t* pos, float* q_out,
+                                      void* q_packed, float* q_scales, int8_t* keys, int8_t* vals, float* kscales,
+                                      float* vscales, int32_t* ctx, uint32_t n_seq, uint64_t seq_stride,
+                                      uint32_t max_ctx, uint32_t n_heads, uint32_t n_kv, uint32_t head_dim,
+                                      void* stream) {
+    return ec_glue_qk_rope_append_split(proj, 1, Nin, q_norm, k_norm, use_qn, use_kn, inv_freq, pos, q_out, q_packed,
+                                        q_scales, keys, vals, kscales, vscales, ctx, n_seq, seq_stride, max_ctx,
+                                        n_heads, n_kv, head_dim, stream);
 }
 
 extern "C" int ec_glue_argmax_advance(const float* logits, uint32_t vocab, int32_t* gen, int32_t* next, int32_t* pos,

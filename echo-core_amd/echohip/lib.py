@@ -41,6 +41,8 @@ _SIGS = {
     "ec_attn_decode_packed": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u64, _u32, _u32, _u32, _vp, _vp],
     "ec_glue_qk_rope_append": [_vp, _u32, _vp, _vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                _vp, _u32, _u64, _u32, _u32, _u32, _u32, _vp],
+    "ec_glue_qk_rope_append_split": [_vp, _u32, _u32, _vp, _vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                     _vp, _vp, _vp, _u32, _u64, _u32, _u32, _u32, _u32, _vp],
     "ec_deltanet": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp, _vp],
     "ec_fill_random": [C.c_int, _vp, _u64, _u64, C.c_float, _u32, _vp],
     "ec_gemm_quantize_act": [C.c_int, _vp, _vp, _u32, _u32, _vp],
@@ -190,6 +192,14 @@ class Lib:
         self._call("ec_glue_qk_rope_append", _ptr(proj), Nin, _ptr(q_norm), _ptr(k_norm), int(use_qn), int(use_kn),
                    _ptr(inv_freq), _ptr(pos), _ptr(q_out), _ptr(q_packed), _ptr(q_scales), _ptr(keys), _ptr(vals),
                    _ptr(ks), _ptr(vs), _ptr(ctx), n_seq, seq_stride, max_ctx, n_heads, n_kv, head_dim,
+                   self._stream(stream))
+
+    def qk_rope_append_split(self, proj, nparts, Nin, q_norm, k_norm, use_qn, use_kn, inv_freq, pos, q_out, q_packed,
+                             q_scales, keys, vals, ks, vs, ctx, n_seq, seq_stride, max_ctx, n_heads, n_kv, head_dim,
+                             stream=None):
+        self._call("ec_glue_qk_rope_append_split", _ptr(proj), nparts, Nin, _ptr(q_norm), _ptr(k_norm), int(use_qn),
+                   int(use_kn), _ptr(inv_freq), _ptr(pos), _ptr(q_out), _ptr(q_packed), _ptr(q_scales), _ptr(keys),
+                   _ptr(vals), _ptr(ks), _ptr(vs), _ptr(ctx), n_seq, seq_stride, max_ctx, n_heads, n_kv, head_dim,
                    self._stream(stream))
 
     def attn_qa_bytes(self, n_seq, n_heads):

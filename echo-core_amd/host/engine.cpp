@@ -229,6 +229,13 @@ uint32_t gu_split() {
     static const uint32_t v = env_split("EC_GU_SPLIT", 2);
     return v;
 }
+// attention input projection (q|k|v, 6144 x 2560), partials added by the rope
+// kernel.  Decode batch 8 on MI355X: 1 / 2 / 3 / 4 / 5 / 6 / 8 splits
+// 4623 / 4620 / 4631 / 4633 / 4633 / 4628 / 4625 tok/s.
+uint32_t attn_split() {
+    static const uint32_t v = env_split("EC_ATTN_SPLIT", 4);
+    return v;
+}
 
 // A split-K projection into y ([ns][B][N]); ns is clamped to the K chunks.
 int mv_split(ec_engine* e, const Mat& m, const void* act, float* y, uint32_t& ns) {
@@ -283,21 +290,23 @@ int record_step(ec_engine* e) {
             EC_TRY(mv_resid(e, y.w_out, e->act_v, ns));
         } else {
             const uint32_t Nin = e->nin_attn;
-            EC_TRY(mv(e, y.w_in, e->act_h, e->proj, Nin, 0));
+            uint32_t nsa = attn_split();
+            EC_TRY(mv_split(e, y.w_in, e->act_h, e->proj, nsa));
             if (e->packed_attn) {
                 // rope + KV append write q as int8 pieces; attention writes the
                 // Q8_0 activation of its output for the output projection
-                EC_GLUE(ec_glue_qk_rope_append(e->proj, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn, e->inv_freq,
-                                              e->pos, nullptr, e->q_packed, e->q_scales, y.keys, y.vals, y.ks, y.vs,
-                                              e->ctx, B, e->seq_stride, c.max_ctx, c.n_heads, c.n_kv, c.head_dim,
-                                              st));
+                EC_GLUE(ec_glue_qk_rope_append_split(e->proj, nsa, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn,
+                                                    e->inv_freq, e->pos, nullptr, e->q_packed, e->q_scales, y.keys,
+                                                    y.vals, y.ks, y.vs, e->ctx, B, e->seq_stride, c.max_ctx,
+                                                    c.n_heads, c.n_kv, c.head_dim, st));
                 EC_GLUE(ec_attn_decode_packed(e->q_packed, e->q_scales, y.keys, y.vals, y.ks, y.vs, e->attn_out,
                                              e->act_q, e->ctx, B, e->seq_stride, c.n_heads, c.n_kv, c.max_ctx,
                                              e->attn_ws, st));
             } else {
-                EC_GLUE(ec_glue_qk_rope_append(e->proj, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn, e->inv_freq,
-                                              e->pos, e->qbuf, nullptr, nullptr, y.keys, y.vals, y.ks, y.vs, e->ctx,
-                                              B, e->seq_stride, c.max_ctx, c.n_heads, c.n_kv, c.head_dim, st));
+                EC_GLUE(ec_glue_qk_rope_append_split(e->proj, nsa, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn,
+                                                    e->inv_freq, e->pos, e->qbuf, nullptr, nullptr, y.keys, y.vals,
+                                                    y.ks, y.vs, e->ctx, B, e->seq_stride, c.max_ctx, c.n_heads,
+                                                    c.n_kv, c.head_dim, st));
                 EC_GLUE(ec_attn_decode(e->qbuf, y.keys, y.vals, y.ks, y.vs, e->attn_out, e->ctx, B, e->seq_stride,
                                       c.n_heads, c.n_kv, c.head_dim, c.max_ctx, e->attn_ws, st));
                 EC_GLUE(ec_quantize_act(EC_Q8_0, e->attn_out, e->act_q, B, e->q_dim, st));

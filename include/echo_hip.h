@@ -209,6 +209,14 @@ int ec_glue_qk_rope_append(const float* proj, uint32_t Nin, const float* q_norm,
                            float* q_scales, int8_t* keys, int8_t* vals, float* kscales, float* vscales, int32_t* ctx,
                            uint32_t n_seq, uint64_t seq_stride, uint32_t max_ctx, uint32_t n_heads, uint32_t n_kv,
                            uint32_t head_dim, void* stream);
+/* ec_glue_qk_rope_append with the projection given as nparts (1..8) partial
+ * sums proj[nparts][n_seq][Nin] (ec_matvec_split's output), added in part order. */
+int ec_glue_qk_rope_append_split(const float* proj, uint32_t nparts, uint32_t Nin, const float* q_norm,
+                                 const float* k_norm, int use_qn, int use_kn, const float* inv_freq,
+                                 const int32_t* pos, float* q_out, void* q_packed, float* q_scales, int8_t* keys,
+                                 int8_t* vals, float* kscales, float* vscales, int32_t* ctx, uint32_t n_seq,
+                                 uint64_t seq_stride, uint32_t max_ctx, uint32_t n_heads, uint32_t n_kv,
+                                 uint32_t head_dim, void* stream);
 int ec_glue_argmax_advance(const float* logits, uint32_t vocab, int32_t* gen, int32_t* next, int32_t* pos,
                            uint32_t n_seq, void* stream);
 

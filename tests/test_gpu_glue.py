@@ -109,6 +109,45 @@ def test_qk_rope_append_matches_oracle(hip, oc, use_norms):
         assert not kh[s, others].any() and not vh[s, others].any()
 
 
+@pytest.mark.parametrize("ns", [2, 3, 8])
+def test_rope_append_split_equals_summed_input(hip, ns):
+    """ec_glue_qk_rope_append_split over ns partial projections == the one-part
+    entry on the parts added in order in fp32, bit for bit (packed q, K/V rows,
+    scales, ctx), including an inactive sequence."""
+    import torch
+    n_heads, n_kv, HD, max_ctx = 16, 4, 256, 24
+    pos = np.array([3, -1, 23, 0], np.int32)
+    n_seq = pos.size
+    Nin = (n_heads + 2 * n_kv) * HD
+    seq_stride = max_ctx * n_kv * HD
+    rng = np.random.default_rng(12 + ns)
+    parts = rng.standard_normal((ns, n_seq, Nin)).astype(np.float32)
+    total = parts[0].copy()
+    for q in range(1, ns):
+        total = total + parts[q]
+    qn = dev((1 + 0.1 * rng.standard_normal(HD)).astype(np.float32))
+    kn = dev((1 + 0.1 * rng.standard_normal(HD)).astype(np.float32))
+    inv = dev((1.0 / 10000.0 ** (np.arange(HD // 2) * 2.0 / HD)).astype(np.float32))
+    out = []
+    for split in (True, False):
+        keys = empty(n_seq * seq_stride, torch.int8)
+        vals = empty(n_seq * seq_stride, torch.int8)
+        ks = empty(n_seq * max_ctx * n_kv, torch.float32)
+        vs = empty(n_seq * max_ctx * n_kv, torch.float32)
+        ctx = empty(n_seq, torch.int32)
+        qa = empty(hip.attn_qa_bytes(n_seq, n_heads), torch.uint8)
+        qs = empty(n_seq * n_heads * 3, torch.float32)
+        if split:
+            hip.qk_rope_append_split(dev(parts), ns, Nin, qn, kn, 1, 1, inv, dev(pos), None, qa, qs, keys, vals, ks, vs,
+                                     ctx, n_seq, seq_stride, max_ctx, n_heads, n_kv, HD)
+        else:
+            hip.qk_rope_append(dev(total), Nin, qn, kn, 1, 1, inv, dev(pos), None, qa, qs, keys, vals, ks, vs, ctx,
+                               n_seq, seq_stride, max_ctx, n_heads, n_kv, HD)
+        out.append([host(t).view(np.uint8) for t in (keys, vals, ks, vs, ctx, qa, qs)])
+    for a, b in zip(*out):
+        assert np.array_equal(a, b)
+
+
 @pytest.mark.parametrize("ns", [2, 5])
 def test_split_inputs_equal_summed_inputs(hip, ns):
     """ec_delta_step_split / ec_glue_swiglu_quant_split over ns partial sums ==
