@@ -229,8 +229,8 @@ def run_all(hip, quick=False):
 # 2 for the delta-net input projection and gate/up, 3 for the projections that
 # add into the residual; a split writes one partial output per split).
 DECODE_STEP_MATVECS = [("delta_in", 12352, 2560, 24, 2), ("delta_out", 2560, 4096, 24, 3),
-                       ("attn_in", 6144, 2560, 8, 1), ("attn_out", 2560, 4096, 8, 3),
-                       ("ffn_gate_up", 18432, 2560, 32, 2), ("ffn_down", 2560, 9216, 32, 3),
+                       ("attn_in", 6144, 2560, 8, 4), ("attn_out", 2560, 4096, 8, 3),
+                       ("ffn_gate_up", 18432, 2560, 32, 3), ("ffn_down", 2560, 9216, 32, 3),
                        ("lm_head", 151936, 2560, 1, 1)]
 PMC_LAUNCHES = 3
 CALIB_BYTES = 256 << 20
