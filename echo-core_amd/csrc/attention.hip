@@ -194,12 +194,13 @@ __global__ __launch_bounds__(64) void k_attn_combine(const float* __restrict__ w
 // the pieces occupy A rows g, G+g and 2G+g.  K stays int8 (B operand), every
 // dot product is an exact int32 and
 //   score = ks * (s0*dot0 + s1*dot1 + s2*dot2) / sqrt(256).
-// One workgroup of four waves owns a 64-position chunk of one kv head for all
-// G query heads of its GQA group and writes one partial (max / sum / output)
-// per head.  Wave w scores positions 16w .. 16w+15 and stages their V rows in
-// LDS; wave 0 takes the softmax over the chunk; softmax(.)V runs on the VALU,
-// wave w producing dims 64w .. 64w+63 from probabilities (times the V row
-// scale) broadcast through LDS.
+// One workgroup of four waves owns a 64-position (or 128-position) chunk of
+// one kv head for all G query heads of its GQA group and writes one partial
+// (max / sum / output) per head.  Wave w scores positions 16w .. 16w+15 (+64q)
+// and stages their V rows in LDS, transposed to [dim][position]; wave 0 takes
+// the softmax over the chunk and splits probability x V row scale into three
+// int8 pieces per head the same way; softmax(.)V then runs on the same MFMA,
+// wave w producing dims 64w .. 64w+63 as exact int32 sums per piece.
 //
 // Packed q layout: layout.hpp (store_q_pieces).
 constexpr uint32_t kChunk64 = 64;
