@@ -471,7 +471,7 @@ __global__ __launch_bounds__(256) void k_qk_rope_append(const float* __restrict_
 // Active sequences write the token to gen and next and advance pos.
 __global__ __launch_bounds__(1024) void k_argmax_advance(const float* __restrict__ logits, uint32_t vocab,
                                                          int32_t* __restrict__ gen, int32_t* __restrict__ next,
-                                                         int32_t* __restrict__ pos) {
+                                                         int32_t* __restrict__ pos, uint32_t max_pos) {
     __shared__ float sv[16];
     __shared__ int32_t si[16];
     const uint32_t s = blockIdx.x, t = threadIdx.x;
@@ -535,7 +535,10 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float* __restrict
         if (pos[s] >= 0) {
             gen[s] = bi;
             next[s] = bi;
-            pos[s] += 1;
+            // a sequence whose next position would be past the cache ends here:
+            // it becomes inactive (pos -1) instead of decoding without attention
+            const int32_t np = pos[s] + 1;
+            pos[s] = (max_pos != 0 && (uint32_t)np >= max_pos) ? -1 : np;
         }
     }
 }
@@ -712,7 +715,8 @@ extern "C" int ec_glue_qk_rope_append(const float* proj, uint32_t Nin, const flo
 }
 
 extern "C" int ec_glue_argmax_advance(const float* logits, uint32_t vocab, int32_t* gen, int32_t* next, int32_t* pos,
-                                      uint32_t n_seq, void* stream) {
+                                      uint32_t n_seq, uint32_t max_pos, void* stream) {
     if (!logits || !gen || !next || !pos) return ec_set_error(EC_ERR_ARG, "ec_glue_argmax_advance: bad argument");
-    EC_GLUE_LAUNCH(k_argmax_advance, dim3(n_seq), dim3(1024), 0, (hipStream_t)stream, logits, vocab, gen, next, pos);
+    EC_GLUE_LAUNCH(k_argmax_advance, dim3(n_seq), dim3(1024), 0, (hipStream_t)stream, logits, vocab, gen, next, pos,
+                   max_pos);
 }

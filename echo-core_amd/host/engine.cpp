@@ -173,9 +173,22 @@ int random_rows(ec_engine* e, Mat& m, uint32_t row0, uint32_t N, uint64_t seed, 
     return ec_repack(EC_Q8_0, tmp, dst, N, m.K, e->st);
 }
 
-int upload_vec(ec_engine* e, float* dst, const std::vector<float>& v) {
-    EC_HIP(hipMemcpy(dst, v.data(), v.size() * sizeof(float), hipMemcpyHostToDevice));
+// Host <-> device copies on the engine stream, complete on return.  The
+// engine's buffers are zeroed and written by work queued on its non-blocking
+// stream, which a copy on the null stream would not wait for.
+int h2d(ec_engine* e, void* dst, const void* src, size_t bytes) {
+    EC_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, e->st));
+    EC_HIP(hipStreamSynchronize(e->st));
     return EC_OK;
+}
+int d2h(ec_engine* e, void* dst, const void* src, size_t bytes) {
+    EC_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, e->st));
+    EC_HIP(hipStreamSynchronize(e->st));
+    return EC_OK;
+}
+
+int upload_vec(ec_engine* e, float* dst, const std::vector<float>& v) {
+    return h2d(e, dst, v.data(), v.size() * sizeof(float));
 }
 
 std::vector<float> gen_vec(uint64_t seed, size_t n, double mean, double std) {
@@ -324,7 +337,7 @@ int record_step(ec_engine* e) {
     }
     EC_GLUE(norm(e->final_norm));
     EC_TRY(mv(e, e->lm_head, e->act_h, e->logits, c.vocab, 0));
-    EC_GLUE(ec_glue_argmax_advance(e->logits, c.vocab, e->gen, e->tok, e->pos, B, st));
+    EC_GLUE(ec_glue_argmax_advance(e->logits, c.vocab, e->gen, e->tok, e->pos, B, c.max_ctx, st));
     return EC_OK;
 #undef EC_GLUE
 }
@@ -445,9 +458,7 @@ extern "C" int ec_engine_create(const ec_engine_cfg* cfg, ec_engine** out) {
         inv[i / 2] = 1.0f / powf(c.rope_base, (float)i / (float)c.head_dim);
     if ((rc = upload_vec(e, e->inv_freq, inv))) return fail(rc);
     std::vector<int32_t> neg(B, -1);
-    if (hipMemcpy(e->pos, neg.data(), B * 4, hipMemcpyHostToDevice) != hipSuccess)
-        return fail(ec_set_error(EC_ERR_HIP, "ec_engine_create: pos"));
-    if (hipStreamSynchronize(e->st) != hipSuccess) return fail(ec_set_error(EC_ERR_HIP, "ec_engine_create: sync"));
+    if ((rc = h2d(e, e->pos, neg.data(), B * 4))) return fail(rc);
     *out = e;
     return EC_OK;
 }
@@ -489,13 +500,11 @@ extern "C" int ec_engine_set_tensor(ec_engine* e, int layer, int tensor, const v
     };
     auto vec = [&](float* dst, size_t n) -> int {
         EC_TRY(need(n * 4));
-        EC_HIP(hipMemcpy(dst, host, bytes, hipMemcpyHostToDevice));
-        return EC_OK;
+        return h2d(e, dst, host, bytes);
     };
     if (tensor == EC_T_EMBED) {
         EC_TRY(need(gguf_bytes(c.vocab, e->H)));
-        EC_HIP(hipMemcpy(e->embed, host, bytes, hipMemcpyHostToDevice));
-        return EC_OK;
+        return h2d(e, e->embed, host, bytes);
     }
     if (tensor == EC_T_FINAL_NORM) return vec(e->final_norm, e->H);
     if (tensor == EC_T_LM_HEAD) {
@@ -556,13 +565,11 @@ extern "C" int ec_engine_get_tensor(ec_engine* e, int layer, int tensor, void* h
     };
     auto vec = [&](const float* src, size_t n) -> int {
         EC_TRY(need(n * 4));
-        EC_HIP(hipMemcpy(host, src, bytes, hipMemcpyDeviceToHost));
-        return EC_OK;
+        return d2h(e, host, src, bytes);
     };
     if (tensor == EC_T_EMBED) {
         EC_TRY(need(gguf_bytes(c.vocab, e->H)));
-        EC_HIP(hipMemcpy(host, e->embed, bytes, hipMemcpyDeviceToHost));
-        return EC_OK;
+        return d2h(e, host, e->embed, bytes);
     }
     if (tensor == EC_T_FINAL_NORM) return vec(e->final_norm, e->H);
     if (tensor == EC_T_LM_HEAD) {
@@ -621,9 +628,7 @@ extern "C" int ec_engine_get_state(ec_engine* e, int layer, int which, uint32_t 
         return ec_set_error(EC_ERR_ARG, "ec_engine_get_state: state id not valid for this layer");
     }
     if (bytes != n) return ec_set_error(EC_ERR_ARG, "ec_engine_get_state: wrong byte count");
-    EC_HIP(hipStreamSynchronize(e->st));
-    EC_HIP(hipMemcpy(host, src, n, hipMemcpyDeviceToHost));
-    return EC_OK;
+    return d2h(e, host, src, n);
 }
 
 extern "C" int ec_engine_init_random(ec_engine* e, uint64_t seed, float w_scale) {
@@ -744,17 +749,14 @@ extern "C" int ec_engine_sync(ec_engine* e) {
 
 extern "C" int ec_engine_get_tokens(ec_engine* e, int32_t* gen, int32_t* pos) {
     if (!e) return ec_set_error(EC_ERR_ARG, "ec_engine_get_tokens: null engine");
-    EC_HIP(hipStreamSynchronize(e->st));
-    if (gen) EC_HIP(hipMemcpy(gen, e->gen, e->B * 4, hipMemcpyDeviceToHost));
-    if (pos) EC_HIP(hipMemcpy(pos, e->pos, e->B * 4, hipMemcpyDeviceToHost));
+    if (gen) EC_TRY(d2h(e, gen, e->gen, e->B * 4));
+    if (pos) EC_TRY(d2h(e, pos, e->pos, e->B * 4));
     return EC_OK;
 }
 
 extern "C" int ec_engine_get_logits(ec_engine* e, float* host, uint32_t seq) {
     if (!e || !host || seq >= e->B) return ec_set_error(EC_ERR_ARG, "ec_engine_get_logits: bad argument");
-    EC_HIP(hipStreamSynchronize(e->st));
-    EC_HIP(hipMemcpy(host, e->logits + (size_t)seq * e->c.vocab, (size_t)e->c.vocab * 4, hipMemcpyDeviceToHost));
-    return EC_OK;
+    return d2h(e, host, e->logits + (size_t)seq * e->c.vocab, (size_t)e->c.vocab * 4);
 }
 
 extern "C" void* ec_engine_stream(ec_engine* e) { return e ? (void*)e->st : nullptr; }
@@ -875,7 +877,7 @@ int prefill_step(ec_engine* e, Lane& L, PrefillJob& j) {
                      e->c.vocab, 0, L.st));
     EC_HIP(hipMemcpyAsync(e->pos + j.seq, &last, 4, hipMemcpyHostToDevice, L.st));
     EC_TRY(ec_glue_argmax_advance(e->logits + (size_t)j.seq * e->c.vocab, e->c.vocab, e->gen + j.seq,
-                                  e->tok + j.seq, e->pos + j.seq, 1, L.st));
+                                  e->tok + j.seq, e->pos + j.seq, 1, e->c.max_ctx, L.st));
     EC_HIP(hipStreamSynchronize(L.st));  // `last` lives on this frame
     return EC_OK;
 }

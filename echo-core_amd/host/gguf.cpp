@@ -225,6 +225,8 @@ GGUFReader::GGUFReader(const std::string& path) {
             uint64_t n = 1;
             for (uint32_t d = 0; d < nd; ++d) {
                 shape[d] = c.get<uint64_t>();
+                if (shape[d] != 0 && n > UINT64_MAX / shape[d])
+                    throw std::runtime_error("GGUF: tensor '" + name + "' has an element count that overflows");
                 n *= shape[d];
             }
             const GGMLType t = ggml_type_from_uint32(c.get<uint32_t>());
@@ -239,8 +241,10 @@ GGUFReader::GGUFReader(const std::string& path) {
         const uint64_t align = (uint64_t)alignment();
         if (align == 0) throw std::runtime_error("GGUF: general.alignment is 0");
         data_offset_ = (off_t)((c.at + align - 1) / align * align);
-        for (const auto& kv : tensors_)
-            if ((uint64_t)data_offset_ + kv.second.offset + kv.second.size > size_)
+        if ((uint64_t)data_offset_ > (uint64_t)size_) throw std::runtime_error("GGUF: data section past the end of the file");
+        const uint64_t data_bytes = (uint64_t)size_ - (uint64_t)data_offset_;
+        for (const auto& kv : tensors_)  // two comparisons: offset + size could wrap
+            if (kv.second.offset > data_bytes || kv.second.size > data_bytes - kv.second.offset)
                 throw std::runtime_error("GGUF: tensor '" + kv.first + "' extends past the end of the file");
         // model config (reference field semantics; head_dim from key_length when present)
         auto u = [&](const char* suffix) -> uint64_t {

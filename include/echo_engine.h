@@ -15,7 +15,10 @@
  * and position are untouched).  After a step the greedy next token of every
  * active sequence is in the engine's `gen` array and its position has
  * advanced by one; the next step consumes `gen` as input unless new inputs
- * are set.  A step runs as one captured HIP graph on the engine's stream.
+ * are set.  A sequence that has written the last slot of its KV cache
+ * (position max_ctx - 1) still gets its greedy token in `gen`, and its
+ * position becomes -1 (inactive) instead of max_ctx: it stops until new
+ * inputs are set.  A step runs as one captured HIP graph on the engine's stream.
  *
  * Differences from the reference, all deliberate:
  *  - activations entering a matvec are quantized per 32-element block with the

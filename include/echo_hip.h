@@ -217,8 +217,12 @@ int ec_glue_qk_rope_append_split(const float* proj, uint32_t nparts, uint32_t Ni
                                  int8_t* vals, float* kscales, float* vscales, int32_t* ctx, uint32_t n_seq,
                                  uint64_t seq_stride, uint32_t max_ctx, uint32_t n_heads, uint32_t n_kv,
                                  uint32_t head_dim, void* stream);
+/* Greedy pick (first maximum) of every active sequence (pos[s] >= 0):
+ * gen[s] = next[s] = argmax, pos[s] += 1; when the new position would be
+ * >= max_pos (the KV cache length; 0 = no limit) the sequence is instead
+ * made inactive, pos[s] = -1, after its last token is written to gen. */
 int ec_glue_argmax_advance(const float* logits, uint32_t vocab, int32_t* gen, int32_t* next, int32_t* pos,
-                           uint32_t n_seq, void* stream);
+                           uint32_t n_seq, uint32_t max_pos, void* stream);
 
 /* ------------------------------------------------- chunked prefill glue
  * T consecutive tokens of ONE sequence at positions p0 .. p0+T-1.

@@ -432,17 +432,104 @@ void ob_matvec_q8_0_avx2(const void* blocks, const float* x, float* y, uint32_t 
 #define OC_MV_IMPL oc_matvec_q8_0
 #endif
 
-/* Matvec with optional activation quantization: y = W * xin (y zeroed first). */
-static void mv(const uint8_t* W, const float* x, float* y, uint32_t M, uint32_t K, int quant_act, float* scratch_deq,
-               int8_t* scratch_q, float* scratch_d) {
+/* Embedding row of a Q8_0 table (engine.zig:41-50): x[i] = d_b * qs[i]. */
+void oc_embed_row_q8_0(const uint8_t* embed, uint32_t H, uint32_t token, float* x) {
+    uint32_t nb = H / 32;
+    const uint8_t* row = embed + (size_t)token * nb * 34;
+    for (uint32_t bb = 0; bb < nb; ++bb) {
+        float d = oc_fp16_to_fp32(rd16(row + 34 * bb));
+        const int8_t* qs = (const int8_t*)(row + 34 * bb + 2);
+        for (int j = 0; j < 32; ++j) x[32 * bb + j] = d * (float)qs[j];
+    }
+}
+
+/* echo-core-zig/src/kernels/qwen_linear.zig:215-219 (per value head h):
+ * beta = 1/(1+exp(-b)), g = -exp(A_log)*softplus(alpha + dt_bias), decay = exp(g). */
+void oc_deltanet_gates(const float* alpha, const float* beta_logit, const float* a_log, const float* dt_bias,
+                       float* decay, float* beta, uint32_t n_v) {
+    for (uint32_t h = 0; h < n_v; ++h) {
+        beta[h] = 1.0f / (1.0f + expf(-beta_logit[h]));
+        float g = -expf(a_log[h]) * oc_softplus(alpha[h] + dt_bias[h]);
+        decay[h] = expf(g);
+    }
+}
+
+/* echo-core-zig/src/kernels/qwen_linear.zig:244-257 (per value head h of d_v):
+ * core <- core * (1/sqrt(sum(core^2)/d_v + 1e-6)) * w[i] * silu(z), squares
+ * summed in index order as the readout loop accumulates them. */
+void oc_gated_rmsnorm(float* core, const float* z, const float* w, uint32_t n_v, uint32_t d_v) {
+    for (uint32_t h = 0; h < n_v; ++h) {
+        float* oh = core + (size_t)h * d_v;
+        float rms = 0.0f;
+        for (uint32_t vi = 0; vi < d_v; ++vi) rms += oh[vi] * oh[vi];
+        rms = sqrtf(rms / (float)d_v + 1e-6f);
+        float inv = 1.0f / rms;
+        for (uint32_t vi = 0; vi < d_v; ++vi) {
+            float nrm = oh[vi] * inv * w[vi];
+            oh[vi] = nrm * oc_silu(z[(size_t)h * d_v + vi]);
+        }
+    }
+}
+
+typedef struct {
+    uint32_t H, q_dim, kv_dim, value_dim, n_v, d_v, key_dim, d_k, n_k, conv_dim, maxK, big;
+} dims_t;
+
+static dims_t dims_of(const oc_model_cfg* c) {
+    dims_t d;
+    d.H = c->hidden;
+    d.q_dim = c->n_heads * c->head_dim;
+    d.kv_dim = c->n_kv * c->head_dim;
+    /* ssm_heads == 0: a model without delta-net blocks (every block attention) */
+    d.value_dim = c->ssm_inner;
+    d.n_v = c->ssm_heads;
+    d.d_v = d.n_v ? d.value_dim / d.n_v : 0;
+    d.key_dim = d.value_dim / 2; /* qwen_linear.zig:117-124 */
+    d.d_k = d.d_v;
+    d.n_k = d.d_k ? d.key_dim / d.d_k : 0;
+    d.conv_dim = 2 * d.key_dim + d.value_dim;
+    d.maxK = d.H;
+    if (c->ffn > d.maxK) d.maxK = c->ffn;
+    if (d.value_dim > d.maxK) d.maxK = d.value_dim;
+    if (d.q_dim > d.maxK) d.maxK = d.q_dim;
+    d.big = d.conv_dim;
+    if (c->ffn > d.big) d.big = c->ffn;
+    if (d.q_dim + 2 * d.kv_dim > d.big) d.big = d.q_dim + 2 * d.kv_dim;
+    return d;
+}
+
+/* Scratch for mv(): the quantized activation and its dequantized copy. */
+typedef struct {
+    float* deq;
+    int8_t* qq;
+    float* qd;
+} mv_scratch;
+
+static mv_scratch mv_alloc(uint32_t maxK) {
+    mv_scratch m;
+    m.deq = (float*)calloc(maxK, sizeof(float));
+    m.qq = (int8_t*)calloc(maxK, 1);
+    m.qd = (float*)calloc(maxK / 32 + 1, sizeof(float));
+    return m;
+}
+static void mv_free(mv_scratch* m) { free(m->deq); free(m->qq); free(m->qd); }
+
+/* Matvec with optional activation quantization: y = W * x (y zeroed first). */
+static void mv(const uint8_t* W, const float* x, float* y, uint32_t M, uint32_t K, int quant_act, mv_scratch* s) {
     memset(y, 0, sizeof(float) * M);
     if (quant_act) {
-        oc_quantize_act_q8_0(x, scratch_q, scratch_d, K);
-        oc_dequant_act_q8_0(scratch_q, scratch_d, scratch_deq, K);
-        OC_MV_IMPL(W, scratch_deq, y, M, K);
+        oc_quantize_act_q8_0(x, s->qq, s->qd, K);
+        oc_dequant_act_q8_0(s->qq, s->qd, s->deq, K);
+        OC_MV_IMPL(W, s->deq, y, M, K);
     } else {
         OC_MV_IMPL(W, x, y, M, K);
     }
+}
+
+void oc_matvec_act_q8_0(const void* W, const float* x, float* y, uint32_t M, uint32_t K, int quant_act) {
+    mv_scratch s = mv_alloc(K);
+    mv((const uint8_t*)W, x, y, M, K, quant_act, &s);
+    mv_free(&s);
 }
 
 static int is_attn_layer(const oc_model_cfg* c, uint32_t l) {
@@ -454,116 +541,108 @@ static int all_zero(const float* w, uint32_t n) {
     return 1;
 }
 
+/* qwen_linear.forward (echo-core-zig/src/kernels/qwen_linear.zig:103-271) of
+ * block l: projections :141-180, conv shift + conv + SiLU :182-201, q/k L2
+ * norms :203-204, gates :215-219, delta rule :221-249 (oc_deltanet_step),
+ * gated RMSNorm :252-257, out projection :260-270. */
+void oc_deltanet_block(const oc_model_cfg* c, const oc_model_w* w, uint32_t l, float* conv_state, float* ssm_state,
+                       const float* in, float* out, int quant_act) {
+    const dims_t d = dims_of(c);
+    mv_scratch s = mv_alloc(d.maxK);
+    float* a = (float*)calloc(d.conv_dim, sizeof(float));
+    float* b = (float*)calloc(d.conv_dim, sizeof(float));
+    float* z = (float*)calloc(d.value_dim, sizeof(float));
+    float* core = (float*)calloc(d.value_dim, sizeof(float));
+    float* ab = (float*)calloc(2 * d.n_v, sizeof(float));
+    float* dec = (float*)calloc(d.n_v, sizeof(float));
+    float* bet = (float*)calloc(d.n_v, sizeof(float));
+    mv(w->w_qkv[l], in, a, d.conv_dim, d.H, quant_act, &s);
+    mv(w->w_z[l], in, z, d.value_dim, d.H, quant_act, &s);
+    mv(w->w_ab[l], in, ab, 2 * d.n_v, d.H, quant_act, &s);
+    oc_conv_step(conv_state, a, w->conv_w[l], b, d.conv_dim, c->conv_kernel);
+    oc_l2norm_heads(b, d.n_k, d.d_k);
+    oc_l2norm_heads(b + d.key_dim, d.n_k, d.d_k);
+    oc_deltanet_gates(ab, ab + d.n_v, w->a_log[l], w->dt_bias[l], dec, bet, d.n_v);
+    oc_deltanet_step(ssm_state, b, b + d.key_dim, b + 2 * d.key_dim, dec, bet, core, d.n_v, d.n_k, d.d_k, d.d_v);
+    oc_gated_rmsnorm(core, z, w->ssm_norm[l], d.n_v, d.d_v);
+    mv(w->w_out[l], core, out, d.H, d.value_dim, quant_act, &s);
+    free(a); free(b); free(z); free(core); free(ab); free(dec); free(bet);
+    mv_free(&s);
+}
+
+/* Attention block l (echo-core-zig/src/inference/engine.zig:520-621): fused
+ * q|k|v projection :537-539, q/k head RMSNorm when the weight is not all zero
+ * :548-553, RoPE at position pos :556-558, KV append before attending :561,
+ * INT8 attention over pos+1 positions :563-616, output projection :619.  The
+ * block attends over its own layer's cache length (the reference reads layer
+ * 0's, cache.zig:131-134, which a hybrid stack never appends to). */
+void oc_attention_block(const oc_model_cfg* c, const oc_model_w* w, uint32_t l, int8_t* keys, int8_t* vals,
+                        float* kscales, float* vscales, uint32_t pos, const float* in, float* out, int quant_act) {
+    const dims_t d = dims_of(c);
+    mv_scratch s = mv_alloc(d.maxK);
+    float* a = (float*)calloc(d.q_dim + 2 * d.kv_dim, sizeof(float));
+    float* core = (float*)calloc(d.q_dim, sizeof(float));
+    float* inv_freq = (float*)calloc(c->head_dim / 2 + 1, sizeof(float));
+    oc_rope_inv_freq(inv_freq, c->head_dim, c->rope_base);
+    mv(w->w_qkv[l], in, a, d.q_dim + 2 * d.kv_dim, d.H, quant_act, &s);
+    float* q = a;
+    float* k = a + d.q_dim;
+    float* v = a + d.q_dim + d.kv_dim;
+    if (!all_zero(w->q_norm[l], c->head_dim)) oc_head_rmsnorm(q, w->q_norm[l], c->n_heads, c->head_dim);
+    if (!all_zero(w->k_norm[l], c->head_dim)) oc_head_rmsnorm(k, w->k_norm[l], c->n_kv, c->head_dim);
+    oc_rope(q, c->n_heads, c->head_dim, pos, inv_freq);
+    oc_rope(k, c->n_kv, c->head_dim, pos, inv_freq);
+    oc_kv_append(k, v, keys, vals, kscales, vscales, pos, c->n_kv, c->head_dim);
+    oc_attn_decode_int8(q, keys, vals, kscales, vscales, core, c->n_heads, c->n_kv, c->head_dim, pos + 1);
+    mv(w->w_out[l], core, out, d.H, d.q_dim, quant_act, &s);
+    free(a); free(core); free(inv_freq);
+    mv_free(&s);
+}
+
+/* SwiGLU FFN of block l (echo-core-zig/src/inference/engine.zig:748-781):
+ * out = W_down (silu(W_gate in) * (W_up in)). */
+void oc_ffn_block(const oc_model_cfg* c, const oc_model_w* w, uint32_t l, const float* in, float* out,
+                  int quant_act) {
+    const dims_t d = dims_of(c);
+    mv_scratch s = mv_alloc(d.maxK);
+    float* g = (float*)calloc(c->ffn, sizeof(float));
+    float* u = (float*)calloc(c->ffn, sizeof(float));
+    mv(w->w_gate[l], in, g, c->ffn, d.H, quant_act, &s);
+    mv(w->w_up[l], in, u, c->ffn, d.H, quant_act, &s);
+    for (uint32_t i = 0; i < c->ffn; ++i) g[i] = oc_silu(g[i]) * u[i];
+    mv(w->w_down[l], g, out, d.H, c->ffn, quant_act, &s);
+    free(g); free(u);
+    mv_free(&s);
+}
+
 /* echo-core-zig/src/inference/engine.zig:360-389 (forwardToken) with
- * layerForward :397-463, attention :520-621, ffn :748-781, norm :783-809 and
- * qwen_linear.forward (echo-core-zig/src/kernels/qwen_linear.zig:103-271).
- * The attention layer attends over its own layer's cache length after the
- * append (the reference reads layer 0's length, cache.zig:131-134, which a
- * hybrid stack never appends to). */
+ * layerForward :397-463 (qwen_linear and attention blocks: residual + norm +
+ * block, then residual + post-attention norm + FFN), final norm and the vocab
+ * projection :375-385. */
 void oc_decoder_token(const oc_model_cfg* c, const oc_model_w* w, oc_seq_state* st,
                       uint32_t token, float* logits, int quant_act) {
-    const uint32_t H = c->hidden;
-    const uint32_t q_dim = c->n_heads * c->head_dim, kv_dim = c->n_kv * c->head_dim;
-    /* ssm_heads == 0: a model without delta-net blocks (every block attention) */
-    const uint32_t value_dim = c->ssm_inner, n_v = c->ssm_heads, d_v = n_v ? value_dim / n_v : 0;
-    const uint32_t key_dim = value_dim / 2, d_k = d_v, n_k = d_k ? key_dim / d_k : 0;
-    const uint32_t conv_dim = 2 * key_dim + value_dim;
-    uint32_t maxK = H;
-    if (c->ffn > maxK) maxK = c->ffn;
-    if (value_dim > maxK) maxK = value_dim;
-    if (q_dim > maxK) maxK = q_dim;
-    uint32_t big = conv_dim;
-    if (c->ffn > big) big = c->ffn;
-    if (q_dim + 2 * kv_dim > big) big = q_dim + 2 * kv_dim;
-
+    const dims_t d = dims_of(c);
+    const uint32_t H = d.H;
     float* x = (float*)calloc(H, sizeof(float));
     float* hbuf = (float*)calloc(H, sizeof(float));
     float* tmp = (float*)calloc(H, sizeof(float));
-    float* a = (float*)calloc(big, sizeof(float));
-    float* b = (float*)calloc(big, sizeof(float));
-    float* z = (float*)calloc(value_dim ? value_dim : 1, sizeof(float));
-    float* core = (float*)calloc(maxK, sizeof(float));
-    float* ab = (float*)calloc(2 * (n_v ? n_v : 1), sizeof(float));
-    float* deq = (float*)calloc(maxK, sizeof(float));
-    int8_t* qq = (int8_t*)calloc(maxK, 1);
-    float* qd = (float*)calloc(maxK / 32 + 1, sizeof(float));
-    float* inv_freq = (float*)calloc(c->head_dim / 2 + 1, sizeof(float));
-    float* dec = (float*)calloc(n_v ? n_v : 1, sizeof(float));
-    float* bet = (float*)calloc(n_v ? n_v : 1, sizeof(float));
-    oc_rope_inv_freq(inv_freq, c->head_dim, c->rope_base);
-
-    /* embedding row, Q8_0 dequant (engine.zig:41-50) */
-    {
-        uint32_t nb = H / 32;
-        const uint8_t* row = w->embed + (size_t)token * nb * 34;
-        for (uint32_t bb = 0; bb < nb; ++bb) {
-            float d = oc_fp16_to_fp32(rd16(row + 34 * bb));
-            const int8_t* qs = (const int8_t*)(row + 34 * bb + 2);
-            for (int j = 0; j < 32; ++j) x[32 * bb + j] = d * (float)qs[j];
-        }
-    }
-
+    mv_scratch s = mv_alloc(d.maxK);
+    oc_embed_row_q8_0(w->embed, H, token, x);
     for (uint32_t l = 0; l < c->n_layers; ++l) {
         oc_rmsnorm(x, w->attn_norm[l], hbuf, H);
-        if (!is_attn_layer(c, l)) {
-            /* qwen_linear.forward :141-180 projections */
-            mv(w->w_qkv[l], hbuf, a, conv_dim, H, quant_act, deq, qq, qd);
-            mv(w->w_z[l], hbuf, z, value_dim, H, quant_act, deq, qq, qd);
-            mv(w->w_ab[l], hbuf, ab, 2 * n_v, H, quant_act, deq, qq, qd);
-            /* conv shift + conv + SiLU :182-201 */
-            oc_conv_step(st->conv_state[l], a, w->conv_w[l], b, conv_dim, c->conv_kernel);
-            /* L2 norm q and k :203-204 */
-            oc_l2norm_heads(b, n_k, d_k);
-            oc_l2norm_heads(b + key_dim, n_k, d_k);
-            /* gates :215-219 */
-            for (uint32_t h = 0; h < n_v; ++h) {
-                bet[h] = 1.0f / (1.0f + expf(-ab[n_v + h]));
-                float g = -expf(w->a_log[l][h]) * oc_softplus(ab[h] + w->dt_bias[l][h]);
-                dec[h] = expf(g);
-            }
-            oc_deltanet_step(st->ssm_state[l], b, b + key_dim, b + 2 * key_dim, dec, bet, core, n_v, n_k, d_k, d_v);
-            /* gated RMSNorm :252-257 */
-            for (uint32_t h = 0; h < n_v; ++h) {
-                float* oh = core + (size_t)h * d_v;
-                float rms = 0.0f;
-                for (uint32_t vi = 0; vi < d_v; ++vi) rms += oh[vi] * oh[vi];
-                rms = sqrtf(rms / (float)d_v + 1e-6f);
-                float inv = 1.0f / rms;
-                for (uint32_t vi = 0; vi < d_v; ++vi) {
-                    float nrm = oh[vi] * inv * w->ssm_norm[l][vi];
-                    oh[vi] = nrm * oc_silu(z[(size_t)h * d_v + vi]);
-                }
-            }
-            mv(w->w_out[l], core, tmp, H, value_dim, quant_act, deq, qq, qd);  /* :260-270 */
-        } else {
-            /* engine.zig:537-539 projections (fused q|k|v rows) */
-            mv(w->w_qkv[l], hbuf, a, q_dim + 2 * kv_dim, H, quant_act, deq, qq, qd);
-            float* q = a;
-            float* k = a + q_dim;
-            float* v = a + q_dim + kv_dim;
-            if (!all_zero(w->q_norm[l], c->head_dim)) oc_head_rmsnorm(q, w->q_norm[l], c->n_heads, c->head_dim);
-            if (!all_zero(w->k_norm[l], c->head_dim)) oc_head_rmsnorm(k, w->k_norm[l], c->n_kv, c->head_dim);
-            oc_rope(q, c->n_heads, c->head_dim, st->pos, inv_freq);
-            oc_rope(k, c->n_kv, c->head_dim, st->pos, inv_freq);
-            oc_kv_append(k, v, st->keys[l], st->vals[l], st->kscales[l], st->vscales[l], st->pos, c->n_kv,
-                         c->head_dim);
-            oc_attn_decode_int8(q, st->keys[l], st->vals[l], st->kscales[l], st->vscales[l], core, c->n_heads,
-                                c->n_kv, c->head_dim, st->pos + 1);
-            mv(w->w_out[l], core, tmp, H, q_dim, quant_act, deq, qq, qd);
-        }
+        if (!is_attn_layer(c, l))
+            oc_deltanet_block(c, w, l, st->conv_state[l], st->ssm_state[l], hbuf, tmp, quant_act);
+        else
+            oc_attention_block(c, w, l, st->keys[l], st->vals[l], st->kscales[l], st->vscales[l], st->pos, hbuf, tmp,
+                               quant_act);
         for (uint32_t i = 0; i < H; ++i) x[i] = x[i] + tmp[i];
-        /* FFN (engine.zig:748-781), post-attention norm */
         oc_rmsnorm(x, w->ffn_norm[l], hbuf, H);
-        mv(w->w_gate[l], hbuf, a, c->ffn, H, quant_act, deq, qq, qd);
-        mv(w->w_up[l], hbuf, b, c->ffn, H, quant_act, deq, qq, qd);
-        for (uint32_t i = 0; i < c->ffn; ++i) a[i] = oc_silu(a[i]) * b[i];
-        mv(w->w_down[l], a, tmp, H, c->ffn, quant_act, deq, qq, qd);
+        oc_ffn_block(c, w, l, hbuf, tmp, quant_act);
         for (uint32_t i = 0; i < H; ++i) x[i] = x[i] + tmp[i];
     }
     oc_rmsnorm(x, w->final_norm, hbuf, H);
-    mv(w->lm_head, hbuf, logits, c->vocab, H, quant_act, deq, qq, qd);
+    mv(w->lm_head, hbuf, logits, c->vocab, H, quant_act, &s);
     st->pos += 1;
-
-    free(x); free(hbuf); free(tmp); free(a); free(b); free(z); free(core); free(ab);
-    free(deq); free(qq); free(qd); free(inv_freq); free(dec); free(bet);
+    free(x); free(hbuf); free(tmp);
+    mv_free(&s);
 }

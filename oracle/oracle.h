@@ -23,6 +23,14 @@
  *                         orthonormal-key retrieval, column permutation), fp64
  *                         brute force
  *   decoder glue          fp64 brute force per op; RoPE rotation norm invariance
+ *   delta-net gates and   closed forms (softplus(0) = ln 2 gives decay
+ *   gated RMSNorm         2^-exp(A_log); softplus(x > 20) = x; sigmoid(0) = 1/2;
+ *                         z = 0 gives 0; a constant core gives w*c/sqrt(c^2+eps)*SiLU(z))
+ *   blocks / decoder      closed forms with unit-row Q8_0 projections (delta-net
+ *                         first token S = k (x) beta v, state decay, zero z; attention
+ *                         at position 0 returns V of kv head h % n_kv; FFN
+ *                         silu(gate)*up); oc_decoder_token equals the composition
+ *                         of the blocks bit for bit (tests/test_oracle_blocks.py)
  */
 #ifndef ECHO_ORACLE_H
 #define ECHO_ORACLE_H
@@ -173,6 +181,28 @@ typedef struct {
     uint32_t pos;        /* tokens already processed */
 } oc_seq_state;
 
+/* Q8_0 embedding row (engine.zig:41-50). */
+void oc_embed_row_q8_0(const uint8_t* embed, uint32_t H, uint32_t token, float* x);
+/* Delta-net gates (qwen_linear.zig:215-219) per value head:
+ * beta = sigmoid(beta_logit), decay = exp(-exp(a_log) * softplus(alpha + dt_bias)). */
+void oc_deltanet_gates(const float* alpha, const float* beta_logit, const float* a_log, const float* dt_bias,
+                       float* decay, float* beta, uint32_t n_v);
+/* Gated RMSNorm (qwen_linear.zig:244-257), in place on core [n_v][d_v]:
+ * core * (1/sqrt(mean(core^2) + 1e-6)) * w * silu(z). */
+void oc_gated_rmsnorm(float* core, const float* z, const float* w, uint32_t n_v, uint32_t d_v);
+/* y = W x (y zeroed), x first quantized per 32-block when quant_act != 0. */
+void oc_matvec_act_q8_0(const void* W, const float* x, float* y, uint32_t M, uint32_t K, int quant_act);
+/* qwen_linear.forward of block l (qwen_linear.zig:103-271): in = the block's
+ * normed input [hidden], out = its output [hidden] (before the residual). */
+void oc_deltanet_block(const oc_model_cfg* c, const oc_model_w* w, uint32_t l, float* conv_state, float* ssm_state,
+                       const float* in, float* out, int quant_act);
+/* Attention block l at position pos (engine.zig:520-621), appending to the
+ * layer's cache before attending over pos+1 positions. */
+void oc_attention_block(const oc_model_cfg* c, const oc_model_w* w, uint32_t l, int8_t* keys, int8_t* vals,
+                        float* kscales, float* vscales, uint32_t pos, const float* in, float* out, int quant_act);
+/* SwiGLU FFN of block l (engine.zig:748-781). */
+void oc_ffn_block(const oc_model_cfg* c, const oc_model_w* w, uint32_t l, const float* in, float* out,
+                  int quant_act);
 /* One token of one sequence: fills logits [vocab]; advances st->pos. */
 void oc_decoder_token(const oc_model_cfg* cfg, const oc_model_w* w, oc_seq_state* st,
                       uint32_t token, float* logits, int quant_act);

@@ -70,6 +70,33 @@ class Oracle:
         L.oc_conv_step.argtypes = [_f32p, _f32p, _f32p, _f32p, _u32, _u32]
         L.oc_argmax.argtypes = [_f32p, _u32]
         L.oc_argmax.restype = _u32
+        L.oc_embed_row_q8_0.argtypes = [_u8p, _u32, _u32, _f32p]
+        L.oc_deltanet_gates.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _u32]
+        L.oc_gated_rmsnorm.argtypes = [_f32p, _f32p, _f32p, _u32, _u32]
+        L.oc_matvec_act_q8_0.argtypes = [_u8p, _f32p, _f32p, _u32, _u32, C.c_int]
+
+    def deltanet_gates(self, alpha, beta_logit, a_log, dt_bias):
+        """(decay, beta) per value head (qwen_linear.zig:215-219)."""
+        f = lambda a: np.ascontiguousarray(a, np.float32).reshape(-1)  # noqa: E731
+        alpha, beta_logit, a_log, dt_bias = f(alpha), f(beta_logit), f(a_log), f(dt_bias)
+        n = alpha.size
+        dec, bet = np.zeros(n, np.float32), np.zeros(n, np.float32)
+        self.lib.oc_deltanet_gates(alpha, beta_logit, a_log, dt_bias, dec, bet, n)
+        return dec, bet
+
+    def gated_rmsnorm(self, core, z, w, n_v, d_v):
+        """core * rsqrt(mean(core^2) + 1e-6) * w * silu(z) per head (qwen_linear.zig:244-257)."""
+        out = np.array(core, np.float32).reshape(-1)
+        self.lib.oc_gated_rmsnorm(out, np.ascontiguousarray(z, np.float32).reshape(-1),
+                                  np.ascontiguousarray(w, np.float32).reshape(-1), n_v, d_v)
+        return out.reshape(n_v, d_v)
+
+    def matvec_act_q8_0(self, W, x, quant_act=True):
+        M = W.shape[0]
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        y = np.zeros(M, np.float32)
+        self.lib.oc_matvec_act_q8_0(np.ascontiguousarray(W).reshape(-1), x, y, M, x.size, int(quant_act))
+        return y
 
     # -- wrappers returning numpy arrays
     def quantize(self, x: np.ndarray, width: int):
@@ -305,6 +332,11 @@ class Decoder:
             self.seqs.append(s)
         oc.lib.oc_decoder_token.argtypes = [C.POINTER(_OcCfg), C.POINTER(_OcW), C.POINTER(_OcSeq), C.c_uint32,
                                             C.c_void_p, C.c_int]
+        oc.lib.oc_deltanet_block.argtypes = [C.POINTER(_OcCfg), C.POINTER(_OcW), _u32, _f32p, _f32p, _f32p, _f32p,
+                                             C.c_int]
+        oc.lib.oc_attention_block.argtypes = [C.POINTER(_OcCfg), C.POINTER(_OcW), _u32, _i8p, _i8p, _f32p, _f32p,
+                                              _u32, _f32p, _f32p, C.c_int]
+        oc.lib.oc_ffn_block.argtypes = [C.POINTER(_OcCfg), C.POINTER(_OcW), _u32, _f32p, _f32p, C.c_int]
 
     def token(self, seq: int, tok: int):
         logits = np.zeros(self.cfg.vocab, np.float32)
@@ -314,6 +346,30 @@ class Decoder:
 
     def pos(self, seq: int) -> int:
         return self.seqs[seq].pos
+
+    # -- the blocks oc_decoder_token composes, on one sequence's state
+    def deltanet_block(self, seq: int, layer: int, x):
+        """qwen_linear.forward of `layer` on the normed input x; advances the
+        sequence's conv and recurrent state of that layer."""
+        st = self.states[seq]
+        out = np.zeros(self.cfg.hidden, np.float32)
+        self.oc.lib.oc_deltanet_block(C.byref(self.c), C.byref(self.w), layer, st["conv"][layer], st["ssm"][layer],
+                                      np.ascontiguousarray(x, np.float32), out, self.quant_act)
+        return out
+
+    def attention_block(self, seq: int, layer: int, x, pos: int):
+        st = self.states[seq]
+        out = np.zeros(self.cfg.hidden, np.float32)
+        self.oc.lib.oc_attention_block(C.byref(self.c), C.byref(self.w), layer, st["k"][layer], st["v"][layer],
+                                       st["ks"][layer], st["vs"][layer], pos, np.ascontiguousarray(x, np.float32), out,
+                                       self.quant_act)
+        return out
+
+    def ffn_block(self, layer: int, x):
+        out = np.zeros(self.cfg.hidden, np.float32)
+        self.oc.lib.oc_ffn_block(C.byref(self.c), C.byref(self.w), layer, np.ascontiguousarray(x, np.float32), out,
+                                 self.quant_act)
+        return out
 
     def load_state(self, seq: int, pos: int, get):
         """Overwrite sequence `seq`'s state with another decoder's, at position
