@@ -12,6 +12,18 @@ T_EMBED, T_FINAL_NORM, T_LM_HEAD = 0, 1, 2
 T_ATTN_NORM, T_FFN_NORM, T_W_IN, T_W_OUT, T_W_GATE, T_W_UP, T_W_DOWN = 10, 11, 12, 13, 14, 15, 16
 T_CONV_W, T_A_LOG, T_DT_BIAS, T_SSM_NORM, T_Q_NORM, T_K_NORM = 17, 18, 19, 20, 21, 22
 S_CONV, S_SSM, S_KEYS, S_VALS, S_KSCALES, S_VSCALES = 0, 1, 2, 3, 4, 5
+# step trace operations and step buffers (echo_engine.h EC_OP_* / EC_B_*)
+(OP_EMBED, OP_NORM, OP_MV_IN, OP_DELTA_STEP, OP_MV_OUT, OP_ROPE_APPEND, OP_ATTN, OP_QUANT_ATTN, OP_MV_GU, OP_SWIGLU,
+ OP_MV_DOWN, OP_LM_HEAD, OP_ARGMAX) = range(13)
+(B_X, B_X2, B_PARTS, B_PROJ, B_GU, B_ACT_H, B_ACT_V, B_ACT_F, B_ACT_Q, B_ATTN_OUT, B_Q_PACKED, B_Q_SCALES, B_QBUF,
+ B_LOGITS, B_TOK, B_POS, B_GEN, B_CTX, B_INV_FREQ) = range(19)
+
+
+class TraceEvent(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("op", "layer", "phase", "nparts", "x_in", "x_out")]
+
+
+_TRACE_FN = C.CFUNCTYPE(None, C.c_void_p, C.POINTER(TraceEvent))
 
 
 @dataclass
@@ -84,6 +96,8 @@ class Engine:
         L.ec_engine_weight_bytes.restype = C.c_size_t
         L.ec_engine_profile_matvecs.argtypes = [vp, u32, C.POINTER(u32), C.POINTER(C.c_double),
                                                 C.POINTER(C.c_double)]
+        L.ec_engine_step_traced.argtypes = [vp, _TRACE_FN, vp]
+        L.ec_engine_buffer.argtypes = [vp, i32, C.POINTER(vp), C.POINTER(C.c_size_t)]
         c = _Cfg(**{f.name: getattr(cfg, f.name) for f in fields(cfg)})
         h = vp()
         self._check(L.ec_engine_create(C.byref(c), C.byref(h)), "ec_engine_create")
@@ -198,6 +212,55 @@ class Engine:
         out = np.zeros(self.cfg.vocab, np.float32)
         self._check(self.L.ec_engine_get_logits(self.h, out.ctypes.data, seq), "get_logits")
         return out
+
+    def step_traced(self, fn):
+        """One decode step launched eagerly with fn(event) called before (phase
+        0) and after (phase 1) every launch, the stream drained each time
+        (ec_engine_step_traced); fn reads buffers with read_buffer / get_state."""
+        err = []
+
+        def cb(_user, ev):
+            if err:
+                return
+            try:
+                e = ev.contents
+                fn(TraceEvent(e.op, e.layer, e.phase, e.nparts, e.x_in, e.x_out))
+            except BaseException as x:  # noqa: BLE001 (re-raised after the step)
+                err.append(x)
+        c_cb = _TRACE_FN(cb)
+        rc = self.L.ec_engine_step_traced(self.h, c_cb, None)
+        if err:
+            raise err[0]
+        self._check(rc, "step_traced")
+
+    def buffer(self, which: int):
+        """(device address, bytes) of a step buffer (ec_engine_buffer)."""
+        p, n = C.c_void_p(), C.c_size_t()
+        self._check(self.L.ec_engine_buffer(self.h, which, C.byref(p), C.byref(n)), "buffer")
+        return p.value or 0, n.value
+
+    def read_buffer(self, which: int, dtype=np.float32, offset: int = 0, count: int | None = None) -> np.ndarray:
+        """Copy (part of) a step buffer to the host: `count` elements of dtype from element `offset`."""
+        p, n = self.buffer(which)
+        isz = np.dtype(dtype).itemsize
+        count = n // isz - offset if count is None else count
+        assert 0 <= offset and offset + count <= n // isz, (which, offset, count, n)
+        out = np.empty(count, dtype)
+        if count:
+            self.hip.copy(out, p + offset * isz, out.nbytes)
+        return out
+
+    def read_act(self, which: int, K: int):
+        """An activation buffer (ec_quantize_act Q8_0 layout, M = max_batch) as
+        (xq int8 [B][K], xd fp32 [B][K/32])."""
+        import torch
+        p, _ = self.buffer(which)
+        B = self.cfg.max_batch
+        xq = torch.empty(B * K, dtype=torch.int8, device="cuda")
+        xd = torch.empty(B * (K // 32), dtype=torch.float32, device="cuda")
+        self.hip.act_unpack(6, p, xq, xd, B, K)
+        torch.cuda.synchronize()
+        return xq.cpu().numpy().reshape(B, K), xd.cpu().numpy().reshape(B, K // 32)
 
     @property
     def stream(self) -> int:

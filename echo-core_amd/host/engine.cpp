@@ -114,6 +114,9 @@ struct ec_engine {
     // matvec-only recording (profiling): skip every other launch, collect bytes
     bool mv_only = false;
     std::vector<double>* mv_bytes = nullptr;
+    // step tracing (ec_engine_step_traced): called around every launch
+    ec_trace_fn trace_cb = nullptr;
+    void* trace_user = nullptr;
     // chunked prefill: lanes of scratch rows (up to kPrefillChunk tokens of
     // one sequence each) with their own stream, allocated on first use; lane
     // 0 runs on st.  Several sequences' chunks run concurrently on the lanes.
@@ -253,22 +256,39 @@ uint32_t attn_split() {
     return v;
 }
 
-// A split-K projection into y ([ns][B][N]); ns is clamped to the K chunks.
-int mv_split(ec_engine* e, const Mat& m, const void* act, float* y, uint32_t& ns) {
-    ns = std::min(ns, (m.K + 127) / 128);
+// A split count clamped to the matrix's 128-element K chunks.
+uint32_t split_count(const Mat& m, uint32_t ns) { return std::min(ns, (m.K + 127) / 128); }
+
+// A split-K projection into y ([ns][B][N]); ns from split_count.
+int mv_split(ec_engine* e, const Mat& m, const void* act, float* y, uint32_t ns) {
     if (e->mv_bytes)  // the output counted once (the extra partial sums are not algorithmic bytes)
         e->mv_bytes->push_back((double)gguf_bytes(m.N, m.K) + (double)e->B * (m.K + m.K / 32 * 4) +
                                (double)e->B * m.N * 4);
     return ec_matvec_split(EC_Q8_0, m.tiled, act, y, e->B, m.N, m.K, ns, e->st);
 }
 
-// Residual projection: partial sums into e->parts; returns the split count.
-int mv_resid(ec_engine* e, const Mat& m, const void* act, uint32_t& ns) {
-    ns = resid_split(m.N, m.K);
+// Residual projection: ns = resid_split(N, K) partial sums into e->parts.
+int mv_resid(ec_engine* e, const Mat& m, const void* act, uint32_t ns) {
     if (e->mv_bytes)  // the output counted once, as in mv_split
         e->mv_bytes->push_back((double)gguf_bytes(m.N, m.K) + (double)e->B * (m.K + m.K / 32 * 4) +
                                (double)e->B * m.N * 4);
     return ec_matvec_split(EC_Q8_0, m.tiled, act, e->parts, e->B, m.N, m.K, ns, e->st);
+}
+
+// One launch of the decode step; with a trace callback installed, the stream
+// is drained and the callback called before and after it.
+template <class F>
+int launch(ec_engine* e, int op, int layer, int nparts, int x_in, int x_out, F&& f) {
+    if (!e->trace_cb) return f();
+    ec_trace_event ev{op, layer, 0, nparts, x_in, x_out};
+    EC_HIP(hipStreamSynchronize(e->st));
+    e->trace_cb(e->trace_user, &ev);
+    const int rc = f();
+    if (rc) return rc;
+    EC_HIP(hipStreamSynchronize(e->st));
+    ev.phase = 1;
+    e->trace_cb(e->trace_user, &ev);
+    return EC_OK;
 }
 
 // The decode step (stream-ordered; captured once into a graph).
@@ -276,70 +296,88 @@ int record_step(ec_engine* e) {
     const ec_engine_cfg& c = e->c;
     const uint32_t B = e->B, H = e->H, F = e->F;
     hipStream_t st = e->st;
-#define EC_GLUE(call)                  \
-    do {                               \
-        if (!e->mv_only) EC_TRY(call); \
+    // glue launches are left out when only the matvecs are recorded
+#define EC_GLUE(op, layer, nparts, xin, xout, call)                                        \
+    do {                                                                                  \
+        if (!e->mv_only) EC_TRY(launch(e, op, layer, (int)(nparts), xin, xout, [&] { return (call); })); \
     } while (0)
+#define EC_MV(op, layer, nparts, call) EC_TRY(launch(e, op, layer, (int)(nparts), -1, -1, [&] { return (call); }))
     // xc: the current residual; ns > 0: e->parts holds ns partial sums still
     // to be added to it (by the next norm, which then moves xc to the other buffer)
     float* xc = e->x;
     uint32_t ns = 0;
-    auto norm = [&](const float* w) -> int {
-        if (ns == 0) return ec_glue_rmsnorm_quant(xc, w, e->act_h, B, H, st);
+    auto xid = [&](const float* p) { return p == e->x ? EC_B_X : EC_B_X2; };
+    auto norm = [&](const float* w, int layer) -> int {
+        if (ns == 0) {
+            EC_GLUE(EC_OP_NORM, layer, 0, xid(xc), xid(xc), ec_glue_rmsnorm_quant(xc, w, e->act_h, B, H, st));
+            return EC_OK;
+        }
         float* xn = xc == e->x ? e->x2 : e->x;
-        const int rc = ec_glue_add_rmsnorm_quant(xc, e->parts, ns, xn, w, e->act_h, B, H, st);
+        EC_GLUE(EC_OP_NORM, layer, ns, xid(xc), xid(xn),
+                ec_glue_add_rmsnorm_quant(xc, e->parts, ns, xn, w, e->act_h, B, H, st));
         xc = xn;
         ns = 0;
-        return rc;
+        return EC_OK;
     };
-    EC_GLUE(ec_glue_embed(e->embed, e->tok, e->x, B, H, c.vocab, st));
+    EC_GLUE(EC_OP_EMBED, -1, 0, -1, EC_B_X, ec_glue_embed(e->embed, e->tok, e->x, B, H, c.vocab, st));
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         Layer& y = e->L[l];
-        EC_GLUE(norm(y.attn_norm));
+        const int li = (int)l;
+        EC_TRY(norm(y.attn_norm, li));
         if (!y.attn) {
             const uint32_t Nin = e->nin_delta;
-            uint32_t nsi = in_split();
-            EC_TRY(mv_split(e, y.w_in, e->act_h, e->proj, nsi));
+            const uint32_t nsi = split_count(y.w_in, in_split());
+            EC_MV(EC_OP_MV_IN, li, nsi, mv_split(e, y.w_in, e->act_h, e->proj, nsi));
             // conv + gates + delta rule + gated norm + quantize in one launch
-            EC_GLUE(ec_delta_step_split(e->proj, nsi, Nin, y.conv_state, y.conv_w, y.a_log, y.dt_bias, y.ssm_norm,
-                                       y.ssm_state, e->act_v, e->pos, B, e->n_k, e->n_v, c.conv_kernel, st));
-            EC_TRY(mv_resid(e, y.w_out, e->act_v, ns));
+            EC_GLUE(EC_OP_DELTA_STEP, li, nsi, -1, -1,
+                    ec_delta_step_split(e->proj, nsi, Nin, y.conv_state, y.conv_w, y.a_log, y.dt_bias, y.ssm_norm,
+                                        y.ssm_state, e->act_v, e->pos, B, e->n_k, e->n_v, c.conv_kernel, st));
+            ns = resid_split(y.w_out.N, y.w_out.K);
+            EC_MV(EC_OP_MV_OUT, li, ns, mv_resid(e, y.w_out, e->act_v, ns));
         } else {
             const uint32_t Nin = e->nin_attn;
-            uint32_t nsa = attn_split();
-            EC_TRY(mv_split(e, y.w_in, e->act_h, e->proj, nsa));
+            const uint32_t nsa = split_count(y.w_in, attn_split());
+            EC_MV(EC_OP_MV_IN, li, nsa, mv_split(e, y.w_in, e->act_h, e->proj, nsa));
             if (e->packed_attn) {
                 // rope + KV append write q as int8 pieces; attention writes the
                 // Q8_0 activation of its output for the output projection
-                EC_GLUE(ec_glue_qk_rope_append_split(e->proj, nsa, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn,
-                                                    e->inv_freq, e->pos, nullptr, e->q_packed, e->q_scales, y.keys,
-                                                    y.vals, y.ks, y.vs, e->ctx, B, e->seq_stride, c.max_ctx,
-                                                    c.n_heads, c.n_kv, c.head_dim, st));
-                EC_GLUE(ec_attn_decode_packed(e->q_packed, e->q_scales, y.keys, y.vals, y.ks, y.vs, e->attn_out,
-                                             e->act_q, e->ctx, B, e->seq_stride, c.n_heads, c.n_kv, c.max_ctx,
-                                             e->attn_ws, st));
+                EC_GLUE(EC_OP_ROPE_APPEND, li, nsa, -1, -1,
+                        ec_glue_qk_rope_append_split(e->proj, nsa, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn,
+                                                     e->inv_freq, e->pos, nullptr, e->q_packed, e->q_scales, y.keys,
+                                                     y.vals, y.ks, y.vs, e->ctx, B, e->seq_stride, c.max_ctx,
+                                                     c.n_heads, c.n_kv, c.head_dim, st));
+                EC_GLUE(EC_OP_ATTN, li, 0, -1, -1,
+                        ec_attn_decode_packed(e->q_packed, e->q_scales, y.keys, y.vals, y.ks, y.vs, e->attn_out,
+                                              e->act_q, e->ctx, B, e->seq_stride, c.n_heads, c.n_kv, c.max_ctx,
+                                              e->attn_ws, st));
             } else {
-                EC_GLUE(ec_glue_qk_rope_append_split(e->proj, nsa, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn,
-                                                    e->inv_freq, e->pos, e->qbuf, nullptr, nullptr, y.keys, y.vals,
-                                                    y.ks, y.vs, e->ctx, B, e->seq_stride, c.max_ctx, c.n_heads,
-                                                    c.n_kv, c.head_dim, st));
-                EC_GLUE(ec_attn_decode(e->qbuf, y.keys, y.vals, y.ks, y.vs, e->attn_out, e->ctx, B, e->seq_stride,
-                                      c.n_heads, c.n_kv, c.head_dim, c.max_ctx, e->attn_ws, st));
-                EC_GLUE(ec_quantize_act(EC_Q8_0, e->attn_out, e->act_q, B, e->q_dim, st));
+                EC_GLUE(EC_OP_ROPE_APPEND, li, nsa, -1, -1,
+                        ec_glue_qk_rope_append_split(e->proj, nsa, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn,
+                                                     e->inv_freq, e->pos, e->qbuf, nullptr, nullptr, y.keys, y.vals,
+                                                     y.ks, y.vs, e->ctx, B, e->seq_stride, c.max_ctx, c.n_heads,
+                                                     c.n_kv, c.head_dim, st));
+                EC_GLUE(EC_OP_ATTN, li, 0, -1, -1,
+                        ec_attn_decode(e->qbuf, y.keys, y.vals, y.ks, y.vs, e->attn_out, e->ctx, B, e->seq_stride,
+                                       c.n_heads, c.n_kv, c.head_dim, c.max_ctx, e->attn_ws, st));
+                EC_GLUE(EC_OP_QUANT_ATTN, li, 0, -1, -1, ec_quantize_act(EC_Q8_0, e->attn_out, e->act_q, B, e->q_dim, st));
             }
-            EC_TRY(mv_resid(e, y.w_out, e->act_q, ns));
+            ns = resid_split(y.w_out.N, y.w_out.K);
+            EC_MV(EC_OP_MV_OUT, li, ns, mv_resid(e, y.w_out, e->act_q, ns));
         }
-        EC_GLUE(norm(y.ffn_norm));
-        uint32_t nsg = gu_split();
-        EC_TRY(mv_split(e, y.w_gu, e->act_h, e->gu, nsg));
-        EC_GLUE(ec_glue_swiglu_quant_split(e->gu, nsg, e->act_f, B, F, st));
-        EC_TRY(mv_resid(e, y.w_down, e->act_f, ns));
+        EC_TRY(norm(y.ffn_norm, li));
+        const uint32_t nsg = split_count(y.w_gu, gu_split());
+        EC_MV(EC_OP_MV_GU, li, nsg, mv_split(e, y.w_gu, e->act_h, e->gu, nsg));
+        EC_GLUE(EC_OP_SWIGLU, li, nsg, -1, -1, ec_glue_swiglu_quant_split(e->gu, nsg, e->act_f, B, F, st));
+        ns = resid_split(y.w_down.N, y.w_down.K);
+        EC_MV(EC_OP_MV_DOWN, li, ns, mv_resid(e, y.w_down, e->act_f, ns));
     }
-    EC_GLUE(norm(e->final_norm));
-    EC_TRY(mv(e, e->lm_head, e->act_h, e->logits, c.vocab, 0));
-    EC_GLUE(ec_glue_argmax_advance(e->logits, c.vocab, e->gen, e->tok, e->pos, B, c.max_ctx, st));
+    EC_TRY(norm(e->final_norm, -1));
+    EC_MV(EC_OP_LM_HEAD, -1, 0, mv(e, e->lm_head, e->act_h, e->logits, c.vocab, 0));
+    EC_GLUE(EC_OP_ARGMAX, -1, 0, -1, -1,
+            ec_glue_argmax_advance(e->logits, c.vocab, e->gen, e->tok, e->pos, B, c.max_ctx, st));
     return EC_OK;
 #undef EC_GLUE
+#undef EC_MV
 }
 
 int destroy_graph(ec_engine* e) {
@@ -987,4 +1025,47 @@ extern "C" int ec_engine_profile_matvecs(ec_engine* e, uint32_t reps, uint32_t* 
     for (double v : by) t += v;
     *bytes_per_step = t;
     return rc;
+}
+
+extern "C" int ec_engine_step_traced(ec_engine* e, ec_trace_fn cb, void* user) {
+    if (!e || !cb) return ec_set_error(EC_ERR_ARG, "ec_engine_step_traced: null argument");
+    e->trace_cb = cb;
+    e->trace_user = user;
+    const int rc = record_step(e);
+    e->trace_cb = nullptr;
+    e->trace_user = nullptr;
+    return rc;
+}
+
+extern "C" int ec_engine_buffer(ec_engine* e, int which, void** dev, size_t* bytes) {
+    if (!e || !dev || !bytes) return ec_set_error(EC_ERR_ARG, "ec_engine_buffer: null argument");
+    const ec_engine_cfg& c = e->c;
+    const size_t B = e->B;
+    void* p = nullptr;
+    size_t n = 0;
+    switch (which) {
+        case EC_B_X: p = e->x, n = B * e->H * 4; break;
+        case EC_B_X2: p = e->x2, n = B * e->H * 4; break;
+        case EC_B_PARTS: p = e->parts, n = (size_t)kMaxResidSplit * B * e->H * 4; break;
+        case EC_B_PROJ: p = e->proj, n = (size_t)kMaxResidSplit * B * e->nin_max * 4; break;
+        case EC_B_GU: p = e->gu, n = (size_t)kMaxResidSplit * B * 2 * e->F * 4; break;
+        case EC_B_ACT_H: p = e->act_h, n = ec_act_bytes(EC_Q8_0, e->B, e->H); break;
+        case EC_B_ACT_V: p = e->act_v, n = ec_act_bytes(EC_Q8_0, e->B, e->value_dim); break;
+        case EC_B_ACT_F: p = e->act_f, n = ec_act_bytes(EC_Q8_0, e->B, e->F); break;
+        case EC_B_ACT_Q: p = e->act_q, n = ec_act_bytes(EC_Q8_0, e->B, e->q_dim); break;
+        case EC_B_ATTN_OUT: p = e->attn_out, n = B * e->q_dim * 4; break;
+        case EC_B_Q_PACKED: p = e->q_packed, n = e->q_packed ? ec_attn_qa_bytes(e->B, c.n_heads) : 0; break;
+        case EC_B_Q_SCALES: p = e->q_scales, n = e->q_scales ? B * c.n_heads * 3 * 4 : 0; break;
+        case EC_B_QBUF: p = e->qbuf, n = B * e->q_dim * 4; break;
+        case EC_B_LOGITS: p = e->logits, n = B * c.vocab * 4; break;
+        case EC_B_TOK: p = e->tok, n = B * 4; break;
+        case EC_B_POS: p = e->pos, n = B * 4; break;
+        case EC_B_GEN: p = e->gen, n = B * 4; break;
+        case EC_B_CTX: p = e->ctx, n = B * 4; break;
+        case EC_B_INV_FREQ: p = e->inv_freq, n = (size_t)c.head_dim / 2 * 4; break;
+        default: return ec_set_error(EC_ERR_ARG, "ec_engine_buffer: unknown buffer id");
+    }
+    *dev = p;
+    *bytes = n;
+    return EC_OK;
 }

@@ -143,6 +143,46 @@ size_t ec_engine_weight_bytes(const ec_engine* e);
 int ec_engine_profile_matvecs(ec_engine* e, uint32_t reps, uint32_t* launches, double* bytes_per_step,
                               double* us_per_step);
 
+/* ------------------------------------------------------------ step tracing
+ * For checking the decode step one operation at a time: the step's launches
+ * (the same kernels, buffers and order as ec_engine_step) run eagerly, and
+ * around every launch the engine stream is synchronized and cb is called
+ * twice, before (phase 0) and after (phase 1) the launch, so the callback
+ * can read the operation's inputs and outputs (ec_engine_buffer,
+ * ec_engine_get_state).  Not for production use: every launch waits. */
+enum {
+    EC_OP_EMBED = 0,       /* tok -> x */
+    EC_OP_NORM = 1,        /* x_in (+ nparts partial sums in PARTS) -> x_out, ACT_H; RMSNorm + quantize */
+    EC_OP_MV_IN = 2,       /* ACT_H -> PROJ [nparts][B][Nin] (delta: q|k|v|z|alpha|beta, attention: q|k|v) */
+    EC_OP_DELTA_STEP = 3,  /* PROJ, conv and recurrent state -> state, ACT_V */
+    EC_OP_MV_OUT = 4,      /* ACT_V or ACT_Q -> PARTS [nparts][B][H] */
+    EC_OP_ROPE_APPEND = 5, /* PROJ -> KV row at pos, Q_PACKED + Q_SCALES (or QBUF), CTX */
+    EC_OP_ATTN = 6,        /* Q_PACKED (or QBUF), KV cache, CTX -> ATTN_OUT (and ACT_Q when packed) */
+    EC_OP_QUANT_ATTN = 7,  /* ATTN_OUT -> ACT_Q (unpacked attention only) */
+    EC_OP_MV_GU = 8,       /* ACT_H -> GU [nparts][B][2F] (gate rows, then up rows) */
+    EC_OP_SWIGLU = 9,      /* GU -> ACT_F */
+    EC_OP_MV_DOWN = 10,    /* ACT_F -> PARTS [nparts][B][H] */
+    EC_OP_LM_HEAD = 11,    /* ACT_H -> LOGITS */
+    EC_OP_ARGMAX = 12,     /* LOGITS, POS -> GEN, TOK, POS */
+};
+typedef struct {
+    int op, layer;   /* layer -1: embedding, final norm, head, argmax */
+    int phase;       /* 0: before the launch, 1: after it completed */
+    int nparts;      /* partial sums the op writes (MV_*) or reads (NORM, DELTA_STEP, ROPE_APPEND, SWIGLU) */
+    int x_in, x_out; /* residual buffers (EC_B_X / EC_B_X2) an EMBED / NORM reads and writes, else -1 */
+} ec_trace_event;
+typedef void (*ec_trace_fn)(void* user, const ec_trace_event* ev);
+int ec_engine_step_traced(ec_engine* e, ec_trace_fn cb, void* user);
+
+/* Device address and size of one of the engine's step buffers (activation
+ * buffers in the ec_quantize_act layout, M = max_batch). */
+enum {
+    EC_B_X = 0, EC_B_X2 = 1, EC_B_PARTS = 2, EC_B_PROJ = 3, EC_B_GU = 4, EC_B_ACT_H = 5, EC_B_ACT_V = 6,
+    EC_B_ACT_F = 7, EC_B_ACT_Q = 8, EC_B_ATTN_OUT = 9, EC_B_Q_PACKED = 10, EC_B_Q_SCALES = 11, EC_B_QBUF = 12,
+    EC_B_LOGITS = 13, EC_B_TOK = 14, EC_B_POS = 15, EC_B_GEN = 16, EC_B_CTX = 17, EC_B_INV_FREQ = 18,
+};
+int ec_engine_buffer(ec_engine* e, int which, void** dev, size_t* bytes);
+
 #ifdef __cplusplus
 }
 #endif

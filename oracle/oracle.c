@@ -247,6 +247,31 @@ void oc_quantize_act_q4_K(const float* x, int8_t* xq, float* xd, int32_t* xsum, 
     }
 }
 
+/* Two-piece activation (design): piece 0 is the reference quantizer per
+ * 32-element block (scale s = amax/127, q0 = sat8(rne(x * (1/s)))); piece 1
+ * quantizes the residual r = fma(-q0, s, x) with the scale s/256:
+ * q1 = sat8(rne(r * ((1/s) * 256))).  x ~ q0*s + q1*(s/256), |error| <=
+ * s/512 except where q0 saturated.  xd holds s per block. */
+void oc_quantize_act2_q8_0(const float* x, int8_t* xq0, int8_t* xq1, float* xd, uint32_t K) {
+    oc_quantize_per_token_symmetric(x, xq0, xd, K / 32, 32);
+    for (uint32_t k = 0; k < K; ++k) {
+        const float sc = xd[k / 32];
+        const float inv1 = (1.0f / sc) * 256.0f;
+        const float r = fmaf(-(float)xq0[k], sc, x[k]);
+        int v = (int)rintf(r * inv1);
+        if (v > 127) v = 127;
+        if (v < -128) v = -128;
+        xq1[k] = (int8_t)v;
+    }
+}
+
+void oc_dequant_act2_q8_0(const int8_t* xq0, const int8_t* xq1, const float* xd, float* x_deq, uint32_t K) {
+    for (uint32_t k = 0; k < K; ++k) {
+        const float sc = xd[k / 32];
+        x_deq[k] = (float)xq0[k] * sc + (float)xq1[k] * (sc * (1.0f / 256.0f));
+    }
+}
+
 void oc_dequant_act_q8_0(const int8_t* xq, const float* xd, float* x_deq, uint32_t K) {
     for (uint32_t k = 0; k < K; ++k) x_deq[k] = (float)xq[k] * xd[k / 32];
 }
@@ -502,6 +527,7 @@ static dims_t dims_of(const oc_model_cfg* c) {
 typedef struct {
     float* deq;
     int8_t* qq;
+    int8_t* qq1;
     float* qd;
 } mv_scratch;
 
@@ -509,15 +535,22 @@ static mv_scratch mv_alloc(uint32_t maxK) {
     mv_scratch m;
     m.deq = (float*)calloc(maxK, sizeof(float));
     m.qq = (int8_t*)calloc(maxK, 1);
+    m.qq1 = (int8_t*)calloc(maxK, 1);
     m.qd = (float*)calloc(maxK / 32 + 1, sizeof(float));
     return m;
 }
-static void mv_free(mv_scratch* m) { free(m->deq); free(m->qq); free(m->qd); }
+static void mv_free(mv_scratch* m) { free(m->deq); free(m->qq); free(m->qq1); free(m->qd); }
 
-/* Matvec with optional activation quantization: y = W * x (y zeroed first). */
+/* Matvec with optional activation quantization: y = W * x (y zeroed first).
+ * quant_act 0: fp32 x (reference); 1: x quantized per 32-block; 2: x as two
+ * int8 pieces per 32-block (oc_quantize_act2_q8_0). */
 static void mv(const uint8_t* W, const float* x, float* y, uint32_t M, uint32_t K, int quant_act, mv_scratch* s) {
     memset(y, 0, sizeof(float) * M);
-    if (quant_act) {
+    if (quant_act == 2) {
+        oc_quantize_act2_q8_0(x, s->qq, s->qq1, s->qd, K);
+        oc_dequant_act2_q8_0(s->qq, s->qq1, s->qd, s->deq, K);
+        OC_MV_IMPL(W, s->deq, y, M, K);
+    } else if (quant_act) {
         oc_quantize_act_q8_0(x, s->qq, s->qd, K);
         oc_dequant_act_q8_0(s->qq, s->qd, s->deq, K);
         OC_MV_IMPL(W, s->deq, y, M, K);
@@ -599,6 +632,11 @@ void oc_attention_block(const oc_model_cfg* c, const oc_model_w* w, uint32_t l, 
     mv_free(&s);
 }
 
+/* engine.zig:769-772: out[i] = silu(gate[i]) * up[i] (out may alias gate). */
+void oc_swiglu(const float* gate, const float* up, float* out, uint32_t n) {
+    for (uint32_t i = 0; i < n; ++i) out[i] = oc_silu(gate[i]) * up[i];
+}
+
 /* SwiGLU FFN of block l (echo-core-zig/src/inference/engine.zig:748-781):
  * out = W_down (silu(W_gate in) * (W_up in)). */
 void oc_ffn_block(const oc_model_cfg* c, const oc_model_w* w, uint32_t l, const float* in, float* out,
@@ -609,7 +647,7 @@ void oc_ffn_block(const oc_model_cfg* c, const oc_model_w* w, uint32_t l, const 
     float* u = (float*)calloc(c->ffn, sizeof(float));
     mv(w->w_gate[l], in, g, c->ffn, d.H, quant_act, &s);
     mv(w->w_up[l], in, u, c->ffn, d.H, quant_act, &s);
-    for (uint32_t i = 0; i < c->ffn; ++i) g[i] = oc_silu(g[i]) * u[i];
+    oc_swiglu(g, u, g, c->ffn);
     mv(w->w_down[l], g, out, d.H, c->ffn, quant_act, &s);
     free(g); free(u);
     mv_free(&s);

@@ -83,6 +83,11 @@ uint32_t oc_q4k_pos(uint32_t s, uint32_t i);
  * block; xsum = sum of the block's int8 values (Q4_K min term). */
 void oc_quantize_act_q8_0(const float* x, int8_t* xq, float* xd, uint32_t K);
 void oc_quantize_act_q4_K(const float* x, int8_t* xq, float* xd, int32_t* xsum, uint32_t K);
+/* Two-piece Q8_0 activation (design): q0 = the reference quantizer per
+ * 32-block with scale s; q1 = sat8(rne(fma(-q0, s, x) * ((1/s)*256))) with
+ * scale s/256.  x ~ q0*s + q1*s/256; x_deq = q0*s + q1*(s/256). */
+void oc_quantize_act2_q8_0(const float* x, int8_t* xq0, int8_t* xq1, float* xd, uint32_t K);
+void oc_dequant_act2_q8_0(const int8_t* xq0, const int8_t* xq1, const float* xd, float* x_deq, uint32_t K);
 /* Dequantize back to natural order (x_deq[k] = xq*xd) for the reference matvec. */
 void oc_dequant_act_q8_0(const int8_t* xq, const float* xd, float* x_deq, uint32_t K);
 void oc_dequant_act_q4_K(const int8_t* xq, const float* xd, float* x_deq, uint32_t K);
@@ -136,9 +141,9 @@ void oc_conv_step(float* conv_state, const float* x, const float* w, float* out,
 /* ---- full hybrid decoder (engine.zig:360-463, qwen_linear.zig:103-271) ----
  * Small, self-contained restatement used as the decoder checker and as the
  * CPU baseline.  Weights are GGUF Q8_0 byte blocks; norms and small vectors
- * are fp32.  quant_act != 0 inserts the activation quantization the GPU
- * path uses before every matvec (design), 0 keeps fp32 activations
- * (reference semantics). */
+ * are fp32.  quant_act 1 inserts the one-piece int8 activation quantization
+ * before every matvec, 2 the two-piece one (design; oc_quantize_act2_q8_0),
+ * 0 keeps fp32 activations (reference semantics). */
 typedef struct {
     uint32_t hidden, ffn, n_layers, vocab;
     uint32_t n_heads, n_kv, head_dim;          /* full-attention layers */
@@ -200,6 +205,8 @@ void oc_deltanet_block(const oc_model_cfg* c, const oc_model_w* w, uint32_t l, f
  * layer's cache before attending over pos+1 positions. */
 void oc_attention_block(const oc_model_cfg* c, const oc_model_w* w, uint32_t l, int8_t* keys, int8_t* vals,
                         float* kscales, float* vscales, uint32_t pos, const float* in, float* out, int quant_act);
+/* out = silu(gate) * up elementwise (engine.zig:769-772); out may alias gate. */
+void oc_swiglu(const float* gate, const float* up, float* out, uint32_t n);
 /* SwiGLU FFN of block l (engine.zig:748-781). */
 void oc_ffn_block(const oc_model_cfg* c, const oc_model_w* w, uint32_t l, const float* in, float* out,
                   int quant_act);

@@ -74,6 +74,48 @@ class Oracle:
         L.oc_deltanet_gates.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _u32]
         L.oc_gated_rmsnorm.argtypes = [_f32p, _f32p, _f32p, _u32, _u32]
         L.oc_matvec_act_q8_0.argtypes = [_u8p, _f32p, _f32p, _u32, _u32, C.c_int]
+        L.oc_swiglu.argtypes = [_f32p, _f32p, _f32p, _u32]
+
+    def swiglu(self, gate, up):
+        g = np.ascontiguousarray(gate, np.float32).reshape(-1)
+        out = np.zeros(g.size, np.float32)
+        self.lib.oc_swiglu(g, np.ascontiguousarray(up, np.float32).reshape(-1), out, g.size)
+        return out
+
+    def rmsnorm(self, x, w):
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        out = np.zeros(x.size, np.float32)
+        self.lib.oc_rmsnorm(x, np.ascontiguousarray(w, np.float32).reshape(-1), out, x.size)
+        return out
+
+    def embed_row_q8_0(self, embed, H, tok):
+        out = np.zeros(H, np.float32)
+        self.lib.oc_embed_row_q8_0(np.ascontiguousarray(embed).reshape(-1), H, int(tok), out)
+        return out
+
+    def conv_step(self, state, x, w, C_, kernel):
+        """Advances state ([kernel][C] newest first) in place; returns silu(conv)."""
+        out = np.zeros(C_, np.float32)
+        self.lib.oc_conv_step(state.reshape(-1), np.ascontiguousarray(x, np.float32).reshape(-1),
+                              np.ascontiguousarray(w, np.float32).reshape(-1), out, C_, kernel)
+        return out
+
+    def l2norm_heads(self, x, n_heads, head_dim):
+        y = np.array(x, np.float32).reshape(-1)
+        self.lib.oc_l2norm_heads(y, n_heads, head_dim)
+        return y
+
+    def head_rmsnorm(self, x, w, n_heads, head_dim):
+        y = np.array(x, np.float32).reshape(-1)
+        self.lib.oc_head_rmsnorm(y, np.ascontiguousarray(w, np.float32), n_heads, head_dim)
+        return y
+
+    def rope(self, x, n_heads, head_dim, pos, base=10000.0):
+        inv = np.zeros(head_dim // 2, np.float32)
+        self.lib.oc_rope_inv_freq(inv, head_dim, base)
+        y = np.array(x, np.float32).reshape(-1)
+        self.lib.oc_rope(y, n_heads, head_dim, pos, inv)
+        return y
 
     def deltanet_gates(self, alpha, beta_logit, a_log, dt_bias):
         """(decay, beta) per value head (qwen_linear.zig:215-219)."""

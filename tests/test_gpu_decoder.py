@@ -1,130 +1,182 @@
-"""GPU hybrid decoder (echo_engine.h) vs the oracle's token-by-token decoder.
+"""GPU hybrid decoder (echo_engine.h) vs the oracle.
 
-Small config (hidden 256, 4 blocks: 3 delta-net + 1 attention, vocab 1000),
-three sequences entering at different steps (ragged batch), prompt tokens
-first, then each sequence's own greedy tokens.  The oracle quantizes matvec
-inputs exactly as the GPU path does (quant_act=1), so the two agree to fp32
-rounding (~1e-7 relative L2 of the logits) except where an activation lands on
-an int8 rounding boundary: the GPU's reduction orders (RMSNorm, matvec and
-delta-rule sums) differ from the reference's sequential sums by ~1e-6
-relative, which can move one element across a .5 boundary and change it by
-one quantum.  At hidden 256 one such flip moves that step's logits by
-4e-3 .. 2.5e-2 relative L2 (more when it happens in an early block: it then
-passes through the later blocks' quantizers), and when it lands in a cached
-quantity (a KV row, the recurrent state) it persists in later steps.
+Parity is checked one operation at a time (tests/decoder_ops.py): each
+decode step runs through ec_engine_step_traced, and every launch's output is
+compared with the oracle's restatement of that operation applied to the
+GPU's own inputs -- integer and copy work bit-exact, fp32 outputs within
+1e-5 relative L2, int8 activations equal to the reference quantizer of the
+oracle's fp32 value except at a rounding boundary.  A traced step equals an
+untraced eager step and the graph replay bit for bit, so the per-operation
+parity carries over to the production (graph) step.
 
-test_decoder_stepwise_matches_oracle removes the carry-over: before every
-step the oracle is loaded with the GPU's state (KV caches, conv and
-delta-rule states), so each step's logits reflect that step alone:
-  - most steps agree to 1e-5 (the exact-path case: a systematic error in any
-    op would show in every step);
-  - every step is within 5e-2 (single-quantum flips at most);
-  - greedy tokens agree wherever the oracle's top-2 margin is clear.
-test_decoder_free_run_tracks_oracle runs both decoders independently and
-checks that the carried differences stay at the flip level (no divergence).
+Small config: hidden 256, 4 blocks (3 delta-net + 1 attention), vocab 1000,
+three sequences entering at different steps (ragged batch).  The 4B-class
+shapes of the benchmark (hidden 2560, 32 blocks, vocab 151936) run the same
+checks for a few steps on a subset of matrix rows.
 """
 import numpy as np
 import pytest
 
 from conftest import rel_l2
+from decoder_ops import OpChecker
 from decoder_util import OracleDecoder, make_model, small_config, upload
 
 pytestmark = pytest.mark.gpu
 
 
-def _gpu_state(eng, cfg, seq, pos):
-    """The engine's state of `seq` in the oracle's layouts (conv: newest first, ssm: [h][k][v])."""
-    from echohip.engine import S_CONV, S_KEYS, S_KSCALES, S_SSM, S_VALS, S_VSCALES
-
-    def get(l, kind):
-        if kind == "conv":
-            ring = eng.get_state(l, S_CONV, seq).reshape(cfg.conv_kernel, cfg.conv_dim)
-            out = np.zeros_like(ring)
-            for t in range(cfg.conv_kernel):
-                if pos - 1 - t >= 0:
-                    out[t] = ring[(pos - 1 - t) % cfg.conv_kernel]
-            return out
-        if kind == "ssm":
-            return eng.get_state(l, S_SSM, seq).reshape(cfg.ssm_heads, 128, 128).transpose(0, 2, 1)
-        which = {"k": S_KEYS, "v": S_VALS, "ks": S_KSCALES, "vs": S_VSCALES}[kind]
-        return eng.get_state(l, which, seq)
-    return get
-
-
-def _run(oc, graph, sync=False):
+def _run_logits(graph):
+    """Logits of 12 ragged steps of the small model (eager or graph steps)."""
     from echohip.engine import Engine
     cfg = small_config(max_batch=3, max_ctx=64)
     m = make_model(cfg, seed=7)
     eng = Engine(cfg)
     upload(eng, m)
     eng.reset()
-    ref = OracleDecoder(oc, cfg, m, n_seq=3)
     start = [0, 2, 4]
     prompt = [[11, 523, 7, 999], [42, 0, 17], [300, 301, 302, 303, 304]]
     nxt = [None, None, None]
-    got, want, toks = [], [], []
+    got = []
     for step in range(12):
-        tok = np.zeros(3, np.int32)
-        pos = np.full(3, -1, np.int32)
-        for s in range(3):
-            i = step - start[s]
-            if i < 0:
-                continue
-            tok[s] = prompt[s][i] if i < len(prompt[s]) else nxt[s]
-            pos[s] = i
-        if sync:
-            for s in range(3):
-                if pos[s] >= 0:
-                    ref.load_state(s, int(pos[s]), _gpu_state(eng, cfg, s, int(pos[s])))
+        tok, pos = _ragged_inputs(step, prompt, start, nxt)
         eng.set_inputs(tok, pos)
         eng.step(graph=graph)
+        gen, _ = eng.tokens()
+        for s in range(3):
+            if pos[s] >= 0:
+                got.append(eng.logits(s))
+                nxt[s] = int(gen[s])
+    eng.close()
+    return got
+
+
+def _ragged_inputs(step, prompt, start, nxt):
+    tok = np.zeros(3, np.int32)
+    pos = np.full(3, -1, np.int32)
+    for s in range(3):
+        i = step - start[s]
+        if i < 0:
+            continue
+        tok[s] = prompt[s][i] if i < len(prompt[s]) else nxt[s]
+        pos[s] = i
+    return tok, pos
+
+
+def test_decoder_every_op_matches_oracle(oc):
+    """12 ragged steps of the small model, every launch of every step checked against the oracle."""
+    from echohip.engine import Engine
+    cfg = small_config(max_batch=3, max_ctx=64)
+    m = make_model(cfg, seed=7)
+    eng = Engine(cfg)
+    upload(eng, m)
+    eng.reset()
+    chk = OpChecker(oc, eng, cfg, m)
+    start = [0, 2, 4]
+    prompt = [[11, 523, 7, 999], [42, 0, 17], [300, 301, 302, 303, 304]]
+    nxt = [None, None, None]
+    for step in range(12):
+        tok, pos = _ragged_inputs(step, prompt, start, nxt)
+        print(f"step {step}: tokens {tok.tolist()} positions {pos.tolist()}", flush=True)
+        eng.set_inputs(tok, pos)
+        eng.step_traced(chk)
         gen, gpos = eng.tokens()
         for s in range(3):
-            if pos[s] < 0:
+            if pos[s] >= 0:
+                assert gpos[s] == pos[s] + 1
+                nxt[s] = int(gen[s])
+            else:
                 assert gpos[s] == -1
-                continue
-            assert gpos[s] == pos[s] + 1
-            lg = eng.logits(s)
-            lr = ref.token(s, int(tok[s]))
-            got.append(lg)
-            want.append(lr)
-            toks.append((int(gen[s]), lr))
-            nxt[s] = int(gen[s])
+    print(chk.summary())
+    assert chk.counts.get(3, 0) > 0 and chk.counts.get(6, 0) > 0  # delta steps and attention were checked
     eng.close()
-    return got, want, toks
 
 
-def _check_tokens(toks):
-    checked = 0
-    for g_tok, lr in toks:
-        top2 = np.sort(lr)[-2:]
-        if top2[1] - top2[0] > 1e-2 * max(1.0, abs(top2[1])):
-            assert g_tok == int(np.argmax(lr))
-            checked += 1
-    assert checked > len(toks) // 2
+def test_traced_step_equals_eager_and_graph(oc):
+    """The traced step launches the same kernels on the same buffers: logits, tokens and states bit-identical."""
+    from echohip.engine import S_KEYS, S_SSM, Engine
+    cfg = small_config(max_batch=3, max_ctx=64)
+    m = make_model(cfg, seed=8)
+    outs = []
+    for mode in ("traced", "eager", "graph"):
+        eng = Engine(cfg)
+        upload(eng, m)
+        eng.reset()
+        for step in range(5):
+            eng.set_inputs(np.array([3 + step, 70, 500], np.int32), np.array([step, step, -1 if step < 2 else step - 2],
+                                                                             np.int32))
+            if mode == "traced":
+                eng.step_traced(lambda ev: None)
+            else:
+                eng.step(graph=mode == "graph")
+        gen, pos = eng.tokens()
+        outs.append(([eng.logits(s) for s in range(3)], gen, pos, eng.get_state(0, S_SSM, 1),
+                     eng.get_state(3, S_KEYS, 2)))
+        eng.close()
+    for other in outs[1:]:
+        for a, b in zip(outs[0][0], other[0]):
+            assert np.array_equal(a, b)
+        for a, b in zip(outs[0][1:], other[1:]):
+            assert np.array_equal(a, b)
 
 
-def test_decoder_stepwise_matches_oracle(oc):
-    got, want, toks = _run(oc, graph=False, sync=True)
-    errs = np.array([rel_l2(g, w) for g, w in zip(got, want)])
-    print("per-step logits rel_l2:", " ".join(f"{e:.1e}" for e in errs))
-    assert (errs < 1e-5).mean() >= 0.75, errs
-    assert errs.max() < 5e-2, errs
-    _check_tokens(toks)
+def test_decoder_4b_shapes_every_op_matches_oracle(oc):
+    """The benchmark's 4B-class decoder (hidden 2560, ffn 9216, 24 delta-net + 8 attention blocks, GQA 16/4,
+    vocab 151936, seeded device weights), two sequences, three decode steps: every launch checked against the
+    oracle (matrices on 384 random rows each)."""
+    from echohip.engine import Engine, EngineConfig
+    cfg = EngineConfig(max_batch=2, max_ctx=16)
+    eng = Engine(cfg)
+    eng.init_random(seed=0)
+    eng.reset()
+    m = eng.export_model()
+    chk = OpChecker(oc, eng, cfg, m, rows_per_matrix=384, seed=1)
+    toks = [[1000, 77, 151935], [5, 123456, 42]]
+    for step in range(3):
+        tok = np.array([toks[0][step], toks[1][step]], np.int32)
+        pos = np.array([step, step], np.int32)
+        print(f"4B step {step}: tokens {tok.tolist()}", flush=True)
+        eng.set_inputs(tok, pos)
+        eng.step_traced(chk)
+    print(chk.summary())
+    eng.close()
 
 
-def test_decoder_free_run_tracks_oracle(oc):
-    got, want, toks = _run(oc, graph=False)
-    errs = np.array([rel_l2(g, w) for g, w in zip(got, want)])
-    print("per-step logits rel_l2:", " ".join(f"{e:.1e}" for e in errs))
-    assert (errs < 1e-5).mean() >= 0.5, errs
-    assert errs.max() < 5e-2, errs
-    _check_tokens(toks)
+def test_decoder_4b_end_to_end_vs_fp32_reference(oc):
+    """The quantized-activation decoder against the reference arithmetic (fp32 activations, oc_decoder_token
+    quant_act=0) on the 4B-class weights, one sequence, four tokens: the deviation and greedy-token agreement
+    are reported.  (Parity is the per-operation test above; this is the accumulated effect of int8 activations
+    over 32 blocks, also shown by the oracle itself run with quantized activations.)"""
+    from echohip.engine import Engine, EngineConfig
+    from oracle import Baseline
+    cfg = EngineConfig(max_batch=1, max_ctx=16)
+    eng = Engine(cfg)
+    eng.init_random(seed=0)
+    eng.reset()
+    m = eng.export_model()
+    bl = Baseline()
+    bl.threads(16)
+    ref = OracleDecoder(bl, cfg, m, n_seq=1, quant_act=False)
+    refq = OracleDecoder(bl, cfg, m, n_seq=1, quant_act=True)
+    errs, errq, same = [], [], []
+    for step, t in enumerate((1000, 77, 151935, 9)):
+        eng.set_inputs(np.array([t], np.int32), np.array([step], np.int32))
+        eng.step(graph=True)
+        g = eng.logits(0)
+        lr, lq = ref.token(0, t), refq.token(0, t)
+        errs.append(rel_l2(g, lr))
+        errq.append(rel_l2(g, lq))
+        same.append((int(np.argmax(g)) == int(np.argmax(lr)), int(np.argmax(lq)) == int(np.argmax(lr))))
+    eng.close()
+    print("4B logits rel_l2 vs fp32-activation reference:", " ".join(f"{e:.2e}" for e in errs))
+    print("4B logits rel_l2 vs oracle with quantized activations:", " ".join(f"{e:.2e}" for e in errq))
+    print("greedy token equal to the fp32 reference's (GPU, quantized oracle):", same)
+    # a report, not a parity bar (the per-operation test is): the logits must still be the same function
+    assert max(errs) < 0.5 and max(errq) < max(errs)
 
 
-def test_decoder_graph_replay_matches_eager(oc):
-    a, _, _ = _run(oc, graph=False)
-    b, _, _ = _run(oc, graph=True)
+def test_decoder_graph_replay_matches_eager():
+    a = _run_logits(graph=False)
+    b = _run_logits(graph=True)
+    assert len(a) == len(b) > 0
     for x, y in zip(a, b):
         assert np.array_equal(x, y)
 

@@ -253,3 +253,37 @@ def test_q4_K_integer_form_equals_reference(oc):
                    axis=(1, 2))
     y_ref = oc.matvec_q4_K(W, oc.dequant_act_q4_K(xq, xd))
     assert rel_l2(y_ref, y_int) < 1e-5
+
+
+def test_two_piece_activation_quantizer(oc):
+    """oc_quantize_act2_q8_0: piece 0 is the reference quantizer; piece 1 quantizes the residual with scale/256, so
+    |x - (q0*s + q1*s/256)| <= s/512 wherever q1 did not saturate, and exactly representable inputs come back
+    exactly."""
+    import ctypes as C
+    f32 = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+    i8 = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+    oc.lib.oc_quantize_act2_q8_0.argtypes = [f32, i8, i8, f32, C.c_uint32]
+    oc.lib.oc_dequant_act2_q8_0.argtypes = [i8, i8, f32, f32, C.c_uint32]
+    K = 4096
+    x = synth.activations(17, K) * 3
+    q0, q1 = np.zeros(K, np.int8), np.zeros(K, np.int8)
+    xd, xr = np.zeros(K // 32, np.float32), np.zeros(K, np.float32)
+    oc.lib.oc_quantize_act2_q8_0(x, q0, q1, xd, K)
+    oc.lib.oc_dequant_act2_q8_0(q0, q1, xd, xr, K)
+    rq, rs = oc.quantize_act_q8_0(x)
+    assert np.array_equal(q0, rq) and np.array_equal(xd, rs)
+    s = np.repeat(xd.astype(np.float64), 32)
+    ok = np.abs(q1) < 127
+    assert ok.mean() > 0.98
+    fp32_sum = 2.0 ** -22 * np.abs(x.astype(np.float64))  # the fp32 rounding of q0*s + q1*s/256 itself
+    assert np.all((np.abs(x.astype(np.float64) - xr) <= s / 512 + fp32_sum)[ok])
+    # values on the two-piece grid (q0*s + q1*s/256 with |q1| < 128) are reproduced exactly
+    s0 = np.float32(0.5)
+    g = np.zeros(32, np.float32)
+    g[0] = 127 * s0  # sets the block scale to exactly 0.5
+    g[1:] = (np.arange(1, 32) - 16) * s0 + (np.arange(1, 32) % 7 - 3) * (s0 / 256)
+    oc.lib.oc_quantize_act2_q8_0(g, q0[:32].copy(), q1[:32].copy(), xd[:1].copy(), 32)
+    a0, a1, ad, ar = np.zeros(32, np.int8), np.zeros(32, np.int8), np.zeros(1, np.float32), np.zeros(32, np.float32)
+    oc.lib.oc_quantize_act2_q8_0(g, a0, a1, ad, 32)
+    oc.lib.oc_dequant_act2_q8_0(a0, a1, ad, ar, 32)
+    assert ad[0] == s0 and np.array_equal(ar, g)
