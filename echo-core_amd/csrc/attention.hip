@@ -12,6 +12,8 @@
 // head (each K/V byte is read once for the whole GQA group), keeps a running
 // max / sum / output per head (online softmax) and writes one partial per
 // chunk; a second kernel merges the partials.
+#include <atomic>
+
 #include "common.hpp"
 #include "layout.hpp"
 
@@ -712,3 +714,60 @@ extern "C" int ec_attn_decode_packed(const void* qa, const float* qsc, const int
 }
 
 extern "C" size_t ec_attn_qa_bytes(uint32_t n_seq, uint32_t n_heads) { return qa_bytes(n_seq, n_heads); }
+
+// ------------------------------------------------ attention without allocation
+// ec_attn_decode_noalloc runs ec_attn_decode with its workspace in `scratch`, a
+// fixed device array that every GPU the library runs on holds until the
+// process ends.  In host code `scratch` names a host-side stand-in, so its
+// device address is looked up once per device (hipGetSymbolAddress, with that
+// device current) and only that address is passed to kernels.
+namespace {
+constexpr size_t kScratchBytes = (size_t)16 << 20;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+std::atomic<void*> g_scratch[kMaxDevices];
+
+int scratch_for_device(int dev, void** out) {
+    if (dev < 0 || dev >= kMaxDevices) return ec_set_error(EC_ERR_ARG, "attention scratch: device index >= 64");
+    void* p = g_scratch[dev].load(std::memory_order_acquire);
+    if (!p) {
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return ec_set_hip_error(e, "attention scratch: hipGetSymbolAddress");
+        g_scratch[dev].store(p, std::memory_order_release);  // a concurrent lookup stores the same address
+    }
+    *out = p;
+    return EC_OK;
+}
+}  // namespace
+
+// Called by ec_device_init with `device` current.
+extern "C" int ec_attn_scratch_init(int device) {
+    void* p = nullptr;
+    return scratch_for_device(device, &p);
+}
+
+extern "C" size_t ec_attn_noalloc_max_bytes(void) { return kScratchBytes; }
+
+extern "C" int ec_attn_decode_noalloc(const float* q, const int8_t* keys, const int8_t* vals, const float* kscales,
+                                      const float* vscales, float* out, const int32_t* ctx, uint32_t n_seq,
+                                      uint64_t seq_stride, uint32_t n_heads, uint32_t n_kv, uint32_t head_dim,
+                                      uint32_t max_ctx, void* stream) {
+    if (n_seq == 0) return EC_OK;
+    const size_t need = ec_attn_ws_bytes(n_seq, n_heads, head_dim, max_ctx);
+    if (need > kScratchBytes) {
+        char buf[192];
+        snprintf(buf, sizeof buf,
+                 "ec_attn_decode_noalloc: workspace of %zu bytes (n_seq %u, n_heads %u, max_ctx %u) exceeds the "
+                 "fixed %zu-byte scratch; use ec_attn_decode with a caller workspace",
+                 need, n_seq, n_heads, max_ctx, kScratchBytes);
+        return ec_set_error(EC_ERR_ARG, buf);
+    }
+    int dev = 0;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return ec_set_hip_error(e, "ec_attn_decode_noalloc: hipGetDevice");
+    void* ws = nullptr;
+    const int rc = scratch_for_device(dev, &ws);
+    if (rc) return rc;
+    return ec_attn_decode(q, keys, vals, kscales, vscales, out, ctx, n_seq, seq_stride, n_heads, n_kv, head_dim,
+                          max_ctx, ws, stream);
+}

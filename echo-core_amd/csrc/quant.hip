@@ -267,10 +267,12 @@ extern "C" int ec_set_hip_error(hipError_t e, const char* where) {
     return EC_ERR_HIP;
 }
 
+extern "C" int ec_attn_scratch_init(int device);
+
 extern "C" int ec_device_init(int device) {
     hipError_t e = hipSetDevice(device);
     if (e != hipSuccess) return ec_set_hip_error(e, "ec_device_init");
-    return EC_OK;
+    return ec_attn_scratch_init(device);  // the device address of ec_attn_decode_noalloc's scratch
 }
 
 extern "C" int ec_copy(void* dst, const void* src, size_t bytes) {

@@ -38,6 +38,7 @@ _SIGS = {
     "ec_dequantize_to_fp16": [C.c_int, _vp, _vp, _sz, _vp],
     "ec_kv_append": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u64, _u32, _u32, _vp],
     "ec_attn_decode": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u64, _u32, _u32, _u32, _u32, _vp, _vp],
+    "ec_attn_decode_noalloc": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u64, _u32, _u32, _u32, _u32, _vp],
     "ec_attn_decode_packed": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u64, _u32, _u32, _u32, _vp, _vp],
     "ec_glue_qk_rope_append": [_vp, _u32, _vp, _vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                _vp, _u32, _u64, _u32, _u32, _u32, _u32, _vp],
@@ -69,6 +70,7 @@ _SIZE_FNS = {
     "ec_attn_ws_bytes": [_u32, _u32, _u32, _u32],
     "ec_attn_qa_bytes": [_u32, _u32],
     "ec_gemm_act_bytes": [C.c_int, _u32, _u32],
+    "ec_attn_noalloc_max_bytes": [],
 }
 
 
@@ -180,6 +182,15 @@ class Lib:
                     stream=None):
         self._call("ec_attn_decode", _ptr(q), _ptr(keys), _ptr(vals), _ptr(ks), _ptr(vs), _ptr(out), _ptr(ctx),
                    n_seq, seq_stride, n_heads, n_kv, head_dim, max_ctx, _ptr(ws), self._stream(stream))
+
+    def attn_decode_noalloc(self, q, keys, vals, ks, vs, out, ctx, n_seq, seq_stride, n_heads, n_kv, head_dim,
+                            max_ctx, stream=None):
+        """ec_attn_decode with the library's fixed per-GPU scratch instead of a workspace (no allocation)."""
+        self._call("ec_attn_decode_noalloc", _ptr(q), _ptr(keys), _ptr(vals), _ptr(ks), _ptr(vs), _ptr(out),
+                   _ptr(ctx), n_seq, seq_stride, n_heads, n_kv, head_dim, max_ctx, self._stream(stream))
+
+    def attn_noalloc_max_bytes(self):
+        return self.L.ec_attn_noalloc_max_bytes()
 
     def attn_decode_packed(self, q_packed, q_scales, keys, vals, ks, vs, out, act_q8, ctx, n_seq, seq_stride, n_heads,
                            n_kv, max_ctx, ws, stream=None):

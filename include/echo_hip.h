@@ -140,6 +140,22 @@ int ec_attn_decode(const float* q, const int8_t* keys, const int8_t* vals, const
                    const float* vscales, float* out, const int32_t* ctx, uint32_t n_seq, uint64_t seq_stride,
                    uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t max_ctx, void* ws, void* stream);
 
+/* ec_attn_decode without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, serving loops that forbid
+ * hipMalloc).  No counterpart in the reference.  The workspace is a fixed
+ * device array of ec_attn_noalloc_max_bytes() = 16 MiB per GPU, held until
+ * the process ends; calls needing more (ec_attn_ws_bytes(n_seq, n_heads,
+ * head_dim, max_ctx) > 16 MiB, e.g. more than ~1M total context positions at
+ * 16 heads) fail with EC_ERR_ARG.  Nothing in it needs to start at zero.
+ * Every call on one GPU shares that array: calls that overlap on one GPU
+ * (different streams, or threads) race and must be serialized by the caller.
+ * The array's device address is looked up by ec_device_init, or on the
+ * first call on a device. */
+size_t ec_attn_noalloc_max_bytes(void);
+int ec_attn_decode_noalloc(const float* q, const int8_t* keys, const int8_t* vals, const float* kscales,
+                           const float* vscales, float* out, const int32_t* ctx, uint32_t n_seq, uint64_t seq_stride,
+                           uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t max_ctx, void* stream);
+
 /* Same computation from q already packed into the three-piece int8 layout
  * (ec_glue_qk_rope_append writes it; ec_attn_qa_bytes(n_seq, n_heads) bytes
  * plus n_seq*n_heads*3 fp32 scales), head_dim 256, n_heads/n_kv in {1,2,4}.
