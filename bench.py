@@ -207,6 +207,9 @@ def main() -> int:
         for name, fn in (("q8_0_9216x2560", lambda: kbench.matvec_case(hip, 6, 9216, 2560)),
                          ("q4_K_9216x2560", lambda: kbench.matvec_case(hip, 10, 9216, 2560)),
                          ("q4_K_2560x9216", lambda: kbench.matvec_case(hip, 10, 2560, 9216)),
+                         ("gguf_f32_q8_0_9216x2560", lambda: kbench.gguf_f32_case(hip, 6, 9216, 2560)),
+                         ("gguf_f32_q4_K_9216x2560", lambda: kbench.gguf_f32_case(hip, 10, 9216, 2560)),
+                         ("gguf_f32_q4_K_2560x9216", lambda: kbench.gguf_f32_case(hip, 10, 2560, 9216)),
                          ("attn_ctx512", lambda: kbench.attention_case(hip, 512)),
                          ("attn_ctx4096", lambda: kbench.attention_case(hip, 4096)),
                          ("attn_ctx32768", lambda: kbench.attention_case(hip, 32768)),

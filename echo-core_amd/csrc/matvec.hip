@@ -346,6 +346,8 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
 }
 
 // ------------------------------------------------ reference-semantics fp32 path
+int gguf_mv_fast(int fmt, const uint8_t* W, const float* x, float* y, uint32_t M, uint32_t K, hipStream_t st);
+
 // One wave per output row, fp32 activations, GGUF bytes read in place.
 // Q8_0 follows src/kernels/matvec.cpp:62-87 per block; Q4_K :92-142; Q2_K
 // :146-183; F16 :18-45.  The row sum is a wave reduction (order differs from
@@ -593,6 +595,25 @@ __global__ __launch_bounds__(256) void k_stream_read(const uint4* __restrict__ s
     if (acc == 0x9E3779B9u) out[blockIdx.x] = acc;  // keeps the loads live; practically never taken
 }
 
+// The same read with a chosen launch shape: U non-temporal 16-byte loads in
+// flight per thread per step (the single-launch read ceiling sweep).
+template <int U>
+__global__ __launch_bounds__(1024) void k_stream_read_u(const uint8_t* __restrict__ src, size_t n16, uint32_t* out) {
+    uint32_t acc = 0;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i0 = (size_t)blockIdx.x * blockDim.x * U + threadIdx.x; i0 < n16; i0 += stride * U) {
+        uint4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const size_t i = i0 + (size_t)u * blockDim.x;
+            v[u] = i < n16 ? ld_stream16(src + 16 * i) : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    if (acc == 0x9E3779B9u) out[blockIdx.x] = acc;
+}
+
 }  // namespace ec
 
 using namespace ec;
@@ -601,6 +622,23 @@ extern "C" int ec_stream_read(const void* src, size_t bytes, uint32_t* out, uint
     if (!src || !out || bytes % 16 || blocks == 0) return ec_set_error(EC_ERR_ARG, "ec_stream_read: bad argument");
     hipLaunchKernelGGL(k_stream_read, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const uint4*)src, bytes / 16,
                        out);
+    EC_CHECK_LAUNCH();
+    return EC_OK;
+}
+
+extern "C" int ec_stream_read_shape(const void* src, size_t bytes, uint32_t* out, uint32_t blocks, uint32_t threads,
+                                    uint32_t unroll, void* stream) {
+    if (!src || !out || bytes % 16 || blocks == 0 || (threads != 256 && threads != 512 && threads != 1024))
+        return ec_set_error(EC_ERR_ARG, "ec_stream_read_shape: bad argument");
+    const uint8_t* s = (const uint8_t*)src;
+    hipStream_t st = (hipStream_t)stream;
+    switch (unroll) {
+        case 1: hipLaunchKernelGGL(k_stream_read_u<1>, dim3(blocks), dim3(threads), 0, st, s, bytes / 16, out); break;
+        case 2: hipLaunchKernelGGL(k_stream_read_u<2>, dim3(blocks), dim3(threads), 0, st, s, bytes / 16, out); break;
+        case 4: hipLaunchKernelGGL(k_stream_read_u<4>, dim3(blocks), dim3(threads), 0, st, s, bytes / 16, out); break;
+        case 8: hipLaunchKernelGGL(k_stream_read_u<8>, dim3(blocks), dim3(threads), 0, st, s, bytes / 16, out); break;
+        default: return ec_set_error(EC_ERR_ARG, "ec_stream_read_shape: unroll must be 1, 2, 4 or 8");
+    }
     EC_CHECK_LAUNCH();
     return EC_OK;
 }
@@ -658,6 +696,11 @@ extern "C" int ec_matvec_gguf_f32(int fmt, const void* gguf, const float* x, flo
     if (!gguf || !x || !y) return ec_set_error(EC_ERR_ARG, "ec_matvec_gguf_f32: null pointer");
     if (fmt != EC_Q8_0 && fmt != EC_Q4_K && fmt != EC_Q2_K && fmt != EC_F16)
         return ec_set_error(EC_ERR_UNSUPPORTED, "ec_matvec_gguf_f32: unsupported format");
+    // Q8_0 / Q4_K weight stream (gguf_mv.hip) where the shape allows it
+    if (gguf_mv_fast(fmt, (const uint8_t*)gguf, x, y, M, K, (hipStream_t)stream) == EC_OK) {
+        EC_CHECK_LAUNCH();
+        return EC_OK;
+    }
     hipLaunchKernelGGL(k_matvec_gguf_f32, dim3(M), dim3(64), 0, (hipStream_t)stream, fmt, (const uint8_t*)gguf, x, y,
                        M, K);
     EC_CHECK_LAUNCH();

@@ -88,6 +88,68 @@ def matvec_case(hip, fmt, N, K, M=1, iters=200, seed=0):
             "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": n_copies}
 
 
+def gguf_f32_case(hip, fmt, N, K, iters=200, seed=0):
+    """The reference-signature matvec path (ec_matvec_gguf_f32: GGUF bytes read in
+    place, fp32 activations, y += W x) over a rotation of weight copies, device
+    pointers.  Algorithmic bytes: weights + fp32 x + y read and written."""
+    st = torch.cuda.current_stream().cuda_stream
+    if fmt == L.Q8_0:
+        wbytes = N * K // 32 * 34
+        W0 = torch.empty(wbytes, dtype=torch.uint8, device="cuda")
+        hip.fill_random(1, W0, N * K // 32, seed, 0.02, stream=st)
+    else:
+        wbytes = N * K // 256 * 144
+        W0 = torch.from_numpy(synth.q4_K_blocks(seed, N, K).reshape(-1)).cuda()
+    n_copies = max(2, math.ceil(ROTATE_BYTES / wbytes) + 1)
+    Ws = torch.empty((n_copies, wbytes), dtype=torch.uint8, device="cuda")
+    for i in range(n_copies):
+        Ws[i].copy_(W0)
+    del W0
+    x = torch.from_numpy(synth.activations(seed + 1, K)).cuda()
+    y = torch.zeros(N, dtype=torch.float32, device="cuda")
+
+    def launch(i, stream):
+        hip.matvec_gguf_f32(fmt, Ws[i], x, y, N, K, stream=stream)
+
+    mean_us, best_us = _events_mean_us(launch, n_copies, iters)
+    alg = wbytes + K * 4 + 2 * N * 4
+    gbs = alg / (mean_us * 1e-6) / 1e9
+    del Ws
+    torch.cuda.empty_cache()
+    return {"kernel": "k_gguf_q8_0_f32" if fmt == L.Q8_0 else "k_gguf_q4_K_f32", "M": 1, "N": N, "K": K,
+            "bytes": alg, "us": round(mean_us, 3), "us_best": round(best_us, 3), "GBs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": n_copies}
+
+
+def stream_read_sweep(hip, nbytes, iters=100):
+    """Fastest single launch of a plain non-temporal 16-byte read of `nbytes`
+    over launch shapes (256 .. 8192 workgroups of 256 / 512 / 1024 threads, 1 ..
+    8 loads in flight per thread), each timed over a >= 512 MB rotation: the
+    achievable ceiling for one kernel that must read that many bytes."""
+    n_copies = max(2, math.ceil(ROTATE_BYTES / nbytes) + 1)
+    buf = torch.empty((n_copies, nbytes), dtype=torch.uint8, device="cuda")
+    buf.fill_(1)
+    out = torch.zeros(8192, dtype=torch.int32, device="cuda")
+    best = None
+    for threads in (256, 512, 1024):
+        for unroll in (1, 2, 4, 8):
+            for blocks in (256, 512, 1024, 2048, 4096, 8192):
+                if blocks * threads * unroll * 16 > 4 * nbytes:  # most threads would have nothing to load
+                    continue
+
+                def launch(i, stream, b=blocks, t=threads, u=unroll):
+                    hip.stream_read_shape(buf[i], nbytes, out, b, t, u, stream=stream)
+
+                us, _ = _events_mean_us(launch, n_copies, iters, replays=3)
+                if best is None or us < best["us"]:
+                    best = {"blocks": blocks, "threads": threads, "unroll": unroll, "us": round(us, 3)}
+    del buf
+    torch.cuda.empty_cache()
+    gbs = nbytes / (best["us"] * 1e-6) / 1e9
+    return {"kernel": "k_stream_read_u", "bytes": nbytes, **best, "GBs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": n_copies}
+
+
 def stream_read_case(hip, nbytes, iters=100, blocks=4096):
     """Plain streaming read over a >= 512 MB rotation: the achievable-HBM reference."""
     n_copies = max(2, math.ceil(ROTATE_BYTES / nbytes) + 1)

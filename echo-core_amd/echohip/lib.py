@@ -63,6 +63,7 @@ _SIGS = {
     "ec_glue_swiglu_rows": [_vp, _vp, _u32, _u32, _vp],
     "ec_glue_gated_norm_rows": [_vp, _vp, _u32, _u32, _vp, _vp, _u32, _u32, _vp],
     "ec_stream_read": [_vp, _sz, _vp, _u32, _vp],
+    "ec_stream_read_shape": [_vp, _sz, _vp, _u32, _u32, _u32, _vp],
 }
 _SIZE_FNS = {
     "ec_tiled_bytes": [C.c_int, _u32, _u32],
@@ -282,6 +283,9 @@ class Lib:
     def deltanet(self, state, q, k, v, decay, beta, out, T, n_seq, n_v, n_k, d_k, d_v, seq_pos=None, stream=None):
         self._call("ec_deltanet", _ptr(state), _ptr(q), _ptr(k), _ptr(v), _ptr(decay), _ptr(beta), _ptr(out), T,
                    n_seq, n_v, n_k, d_k, d_v, _ptr(seq_pos), self._stream(stream))
+
+    def stream_read_shape(self, src, nbytes, out, blocks, threads, unroll, stream=None):
+        self._call("ec_stream_read_shape", _ptr(src), nbytes, _ptr(out), blocks, threads, unroll, self._stream(stream))
 
     def stream_read(self, src, nbytes, out, blocks, stream=None):
         self._call("ec_stream_read", _ptr(src), nbytes, _ptr(out), blocks, self._stream(stream))

@@ -264,6 +264,11 @@ int ec_glue_gated_norm_rows(const float* core, const float* proj, uint32_t Nin, 
 /* Plain streaming read of `bytes` (multiple of 16) with `blocks` workgroups of
  * 256 threads: the HBM-bandwidth calibration used by the benchmarks. */
 int ec_stream_read(const void* src, size_t bytes, uint32_t* out, uint32_t blocks, void* stream);
+/* The same read with `threads` (256/512/1024) per workgroup and `unroll`
+ * (1/2/4/8) non-temporal 16-byte loads in flight per thread: the sweep that
+ * finds the fastest single launch reading a buffer of a given size. */
+int ec_stream_read_shape(const void* src, size_t bytes, uint32_t* out, uint32_t blocks, uint32_t threads,
+                         uint32_t unroll, void* stream);
 
 /* ----------------------------------------------------------------- random
  * Fill device memory from the portable splitmix64 stream: element i gets

@@ -425,3 +425,18 @@ def test_deltanet_1024_tokens_32_heads(hip, oc):
     es = rel_l2(S, Sr)
     print(f"1024 tokens: worst per-token output rel_l2 {worst:.2e}, final state rel_l2 {es:.2e}")
     assert es < 1e-3
+
+
+@pytest.mark.parametrize("fmt,N,K", [(6, 9216, 2560), (6, 2560, 9216), (6, 1000, 4096), (6, 77, 96), (10, 9216, 2560),
+                                     (10, 2560, 9216), (10, 333, 512)])
+def test_gguf_f32_matvec_full_shapes(hip, oc, fmt, N, K):
+    """The reference-signature path (GGUF bytes in place, fp32 activations, y += W x) at the matvec workloads'
+    full shapes, ragged row counts and a K whose rows are not 16-byte aligned (K = 96: per-row kernel), against
+    the oracle's reference-order matvec: within 1e-5 relative L2 (fp32 summation order only)."""
+    W = synth.q8_0_blocks(fmt + N, N, K) if fmt == 6 else synth.q4_K_blocks(fmt + N, N, K)
+    x = synth.activations(N + 1, K)
+    y0 = synth.activations(N + 2, N)
+    y = dev(y0)
+    hip.matvec_gguf_f32(fmt, dev(W), dev(x), y, N, K)
+    ref = (oc.matvec_q8_0 if fmt == 6 else oc.matvec_q4_K)(W, x, y0)
+    assert rel_l2(host(y), ref) < 1e-5
