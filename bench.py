@@ -87,6 +87,86 @@ def cpu_baseline(eng, cfg, n_tokens, threads):
     return res
 
 
+def cpu_kernel_baselines(threads):
+    """The matvec, attention and delta-net workloads on the host CPU: the
+    oracle's AVX2 row kernels (reference structure, fp32 activations) and its
+    attention / delta-net restatements, OpenMP over rows / heads, on 1 thread
+    and on `threads`; one warm-up, then the best of 5 (the delta-net: 64 of
+    the 1024 tokens, per-token time reported)."""
+    import ctypes as C
+
+    import numpy as np
+
+    from echohip import synth
+    from oracle import Baseline
+
+    bl = Baseline()
+    L = bl.lib
+    res = {}
+
+    def best(fn, reps=5):
+        fn()
+        t = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            t.append(time.perf_counter() - t0)
+        return min(t)
+
+    p = lambda a: a.ctypes.data  # noqa: E731
+    for fmt, N, K in ((6, 9216, 2560), (10, 9216, 2560), (10, 2560, 9216)):
+        W = synth.q8_0_blocks(0, N, K) if fmt == 6 else synth.q4_K_blocks(0, N, K)
+        x = synth.activations(1, K)
+        y = np.zeros(N, np.float32)
+        fn = L.ob_matvec_q8_0_avx2 if fmt == 6 else L.ob_matvec_q4_K_avx2
+        name = f"{'q8_0' if fmt == 6 else 'q4_K'}_{N}x{K}"
+        row = {}
+        for nthr in (1, threads):
+            bl.threads(nthr)
+            s = best(lambda: fn(p(W), p(x), p(y), N, K))
+            row[f"us_{nthr}t"] = round(s * 1e6, 1)
+            row[f"GBs_{nthr}t"] = round(W.nbytes / s / 1e9, 2)
+        res[name] = row
+    n_heads, n_kv, hd = 16, 4, 256
+    for ctx in (512, 4096, 32768):
+        keys = synth.randint(3, ctx * n_kv * hd, -127, 127).astype(np.int8)
+        vals = synth.randint(4, ctx * n_kv * hd, -127, 127).astype(np.int8)
+        ks = (0.01 + 0.02 * synth.uniform01(5, ctx * n_kv)).astype(np.float32)
+        vs = (0.01 + 0.02 * synth.uniform01(6, ctx * n_kv)).astype(np.float32)
+        q = synth.activations(7, n_heads * hd)
+        out = np.zeros(n_heads * hd, np.float32)
+        row = {}
+        for nthr in (1, threads):
+            bl.threads(nthr)
+            s = best(lambda: L.oc_attn_decode_int8(p(q), p(keys), p(vals), p(ks), p(vs), p(out), n_heads, n_kv, hd,
+                                                   ctx))
+            row[f"us_{nthr}t"] = round(s * 1e6, 1)
+            row[f"GBs_{nthr}t"] = round((2080 * ctx + 32768) / s / 1e9, 2)
+        res[f"attn_ctx{ctx}"] = row
+    n_v, d, T = 32, 128, 64
+    rng = np.random.default_rng(0)
+    S0 = (rng.standard_normal((n_v, d, d)) * 0.02).astype(np.float32)
+    qk = rng.standard_normal((2, T, n_v, d)).astype(np.float32)
+    qk /= np.linalg.norm(qk, axis=-1, keepdims=True)
+    v = rng.standard_normal((T, n_v, d)).astype(np.float32)
+    dec = (1 / (1 + np.exp(-rng.normal(2, 0.5, (T, n_v))))).astype(np.float32)
+    bet = (1 / (1 + np.exp(-rng.normal(0, 1, (T, n_v))))).astype(np.float32)
+    o = np.zeros(n_v * d, np.float32)
+    row = {}
+    for nthr in (1, threads):
+        bl.threads(nthr)
+        S = S0.copy()
+
+        def run():
+            for t in range(T):
+                L.oc_deltanet_step(p(S), p(qk[0, t]), p(qk[1, t]), p(v[t]), p(dec[t]), p(bet[t]), p(o), n_v, n_v, d, d)
+        s = best(run) / T
+        row[f"us_per_token_{nthr}t"] = round(s * 1e6, 1)
+        row[f"GFLOPs_{nthr}t"] = round(7 * n_v * d * d / s / 1e9, 2)
+    res["deltanet_32h"] = row
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -222,12 +302,16 @@ def main() -> int:
     if not args.no_cpu:
         threads = min(os.cpu_count() or 1, 16)
         res = cpu_baseline(eng, cfg, args.cpu_tokens, threads)
+        log("cpu baseline: kernel workloads")
+        cpu_kernels = cpu_kernel_baselines(threads)
+        log(f"cpu kernels: {cpu_kernels}")
         cpu = {"value": round(res[threads], 4), "unit": "tok/s", "cores": threads, "kind": "port",
                "sample": f"{args.cpu_tokens} single-sequence decode tokens ({max(1, args.cpu_tokens // 10)} on 1 thread) "
                          f"of the same 4B-class model and weights "
                          f"(oracle AVX2 decoder, fp32 activations, OpenMP over matvec rows, {threads} threads, "
                          f"context < {args.cpu_tokens + 2}); 1 thread: {res[1]:.4f} tok/s; host CPU: {cpu_model()}, "
-                         f"{os.cpu_count()} hardware threads visible"}
+                         f"{os.cpu_count()} hardware threads visible",
+               "kernels": cpu_kernels}
 
     line = {
         "metric": "decode tok/s (4B-class Q8_0, 1 GPU); matvec HBM GB/s as % of peak",

@@ -357,14 +357,101 @@ def pmc_summary(csv_path, counter):
     return res
 
 
+def pmc_cases(hip, which):
+    """Eager launches for counter collection: `attention` runs the decode
+    attention at 512 / 4096 / 32768 positions (16 query heads, 4 KV heads,
+    head_dim 256, one sequence), `gemm` the M = 512 prefill GEMMs (Q8_0 and
+    Q4_K, 9216 x 2560 and 2560 x 9216), PMC_LAUNCHES times each on different
+    buffer copies of a >= 512 MB rotation; then the calibration kernels of
+    pmc_workload (a 256 MiB read, a 256 MiB fill)."""
+    st = torch.cuda.current_stream().cuda_stream
+    if which == "attention":
+        for ctx in (512, 4096, 32768):
+            n_kv, hd, n_heads = 4, 256, 16
+            kv = ctx * n_kv * hd
+            per = 2 * kv + 2 * ctx * n_kv * 4
+            n_copies = max(PMC_LAUNCHES, math.ceil(ROTATE_BYTES / per) + 1)
+            keys = torch.randint(-127, 128, (n_copies, kv), dtype=torch.int8, device="cuda")
+            vals = torch.randint(-127, 128, (n_copies, kv), dtype=torch.int8, device="cuda")
+            ks = torch.rand((n_copies, ctx * n_kv), device="cuda") * 0.02 + 0.01
+            vs = torch.rand((n_copies, ctx * n_kv), device="cuda") * 0.02 + 0.01
+            q = torch.from_numpy(synth.activations(0, n_heads * hd)).cuda()
+            out = torch.empty(n_heads * hd, dtype=torch.float32, device="cuda")
+            cl = torch.tensor([ctx], dtype=torch.int32, device="cuda")
+            ws = torch.empty(hip.attn_ws_bytes(1, n_heads, hd, ctx), dtype=torch.uint8, device="cuda")
+            torch.cuda.synchronize()
+            for i in range(PMC_LAUNCHES):
+                c = (i * 7919) % n_copies
+                hip.attn_decode(q, keys[c], vals[c], ks[c], vs[c], out, cl, 1, kv, n_heads, n_kv, hd, ctx, ws, stream=st)
+                torch.cuda.synchronize()
+            del keys, vals, ks, vs
+            torch.cuda.empty_cache()
+    elif which == "gemm":
+        for fmt in (L.Q8_0, L.Q4_K):
+            for N, K in ((9216, 2560), (2560, 9216)):
+                M = 512
+                if fmt == L.Q8_0:
+                    Wd = torch.empty(N * K // 32 * 34, dtype=torch.uint8, device="cuda")
+                    hip.fill_random(1, Wd, N * K // 32, 0, 0.02, stream=st)
+                else:
+                    Wd = torch.from_numpy(synth.q4_K_blocks(0, N, K).reshape(-1)).cuda()
+                tiled = torch.empty(hip.tiled_bytes(fmt, N, K), dtype=torch.uint8, device="cuda")
+                hip.repack(fmt, Wd, tiled, N, K, stream=st)
+                x = torch.from_numpy(synth.activations(1, M * K)).cuda()
+                act = torch.empty(hip.gemm_act_bytes(fmt, M, K), dtype=torch.uint8, device="cuda")
+                hip.gemm_quantize_act(fmt, x, act, M, K, stream=st)
+                y = torch.empty(M * N, dtype=torch.float32, device="cuda")
+                torch.cuda.synchronize()
+                for _ in range(PMC_LAUNCHES):
+                    hip.gemm(fmt, tiled, act, y, M, N, K, stream=st)
+                    torch.cuda.synchronize()
+                del Wd, tiled, x, act, y
+                torch.cuda.empty_cache()
+    else:
+        raise ValueError(which)
+    bufs = [torch.full((CALIB_BYTES,), 1, dtype=torch.uint8, device="cuda") for _ in range(3)]
+    out = torch.zeros(4096, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    for i in range(2):
+        hip.stream_read(bufs[i], CALIB_BYTES, out, 4096, stream=st)
+        torch.cuda.synchronize()
+    for i in range(2):
+        bufs[2 - i].fill_(2)
+        torch.cuda.synchronize()
+
+
+def pmc_kernel_means(csv_path, counters):
+    """Mean value per dispatch of each counter, per kernel name, from a
+    rocprofv3 counter_collection.csv (several counters of one pass)."""
+    import csv
+    acc = {}
+    for r in csv.DictReader(open(csv_path)):
+        if r.get("Counter_Name") not in counters:
+            continue
+        k = r["Kernel_Name"].split("(")[0]
+        d = acc.setdefault(k, {}).setdefault(r["Counter_Name"], [])
+        d.append(float(r["Counter_Value"]))
+    return {k: {c: round(sum(v) / len(v), 1) for c, v in cs.items()} | {"dispatches": len(next(iter(cs.values())))}
+            for k, cs in acc.items()}
+
+
 if __name__ == "__main__":
     import json
     import sys
     if len(sys.argv) > 1 and sys.argv[1] == "--pmc-workload":
         pmc_workload(L.load())
         print("pmc workload done", flush=True)
+    elif len(sys.argv) > 2 and sys.argv[1] == "--pmc-cases":
+        pmc_cases(L.load(), sys.argv[2])
+        print("pmc cases done", flush=True)
+    elif len(sys.argv) > 3 and sys.argv[1] == "--pmc-means":
+        print(json.dumps(pmc_kernel_means(sys.argv[2], sys.argv[3].split(",")), indent=1))
     elif len(sys.argv) > 3 and sys.argv[1] == "--pmc-summary":
         print(json.dumps(pmc_summary(sys.argv[2], sys.argv[3])))
+    elif len(sys.argv) > 1 and sys.argv[1] == "--ceiling":
+        hip = L.load()
+        for nbytes in (13271040, 25067520, 50135040, 436 << 20):
+            print(json.dumps(stream_read_sweep(hip, nbytes)), flush=True)
     else:
         hip = L.load()
         r = run_all(hip)
