@@ -206,7 +206,7 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
                                                      const float* __restrict__ norm_w, float* __restrict__ state,
                                                      uint8_t* __restrict__ act, uint32_t xd_off, uint32_t M,
                                                      const int32_t* __restrict__ pos, uint32_t n_k, uint32_t n_v,
-                                                     uint32_t kern) {
+                                                     uint32_t kern, float* __restrict__ yout) {
     __shared__ float q_s[128], k_s[128], v_s[128], o_s[128];
     __shared__ float red[4], red2[2], gate_s[2];
     const uint32_t h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
@@ -340,7 +340,8 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
         const float rms = sqrtf((red2[0] + red2[1]) / 128.0f + 1e-6f);
         const float inv = 1.0f / rms;
         const float val = o * inv * nwt * silu(zg);
-        store_act_q8_lane(val, act, (float*)(act + xd_off), M, value_dim / 32, s, h * 128 + t);
+        if (act) store_act_q8_lane(val, act, (float*)(act + xd_off), M, value_dim / 32, s, h * 128 + t);
+        if (yout) yout[(size_t)s * value_dim + h * 128 + t] = val;
     }
 }
 
@@ -361,12 +362,12 @@ extern "C" int ec_deltanet(float* state, const float* q, const float* k, const f
     return EC_OK;
 }
 
-extern "C" int ec_delta_step_split(const float* proj, uint32_t nparts, uint32_t Nin, float* conv_state,
-                                   const float* conv_w, const float* a_log, const float* dt_bias, const float* norm_w,
-                                   float* state, void* act, const int32_t* pos, uint32_t n_seq, uint32_t n_k,
-                                   uint32_t n_v, uint32_t kern, void* stream) {
+extern "C" int ec_delta_step_out(const float* proj, uint32_t nparts, uint32_t Nin, float* conv_state,
+                                 const float* conv_w, const float* a_log, const float* dt_bias, const float* norm_w,
+                                 float* state, void* act, float* out, const int32_t* pos, uint32_t n_seq, uint32_t n_k,
+                                 uint32_t n_v, uint32_t kern, void* stream) {
     if (n_seq == 0) return EC_OK;
-    if (!proj || !conv_state || !conv_w || !a_log || !dt_bias || !norm_w || !state || !act || !pos || n_k == 0 ||
+    if (!proj || !conv_state || !conv_w || !a_log || !dt_bias || !norm_w || !state || (!act && !out) || !pos || n_k == 0 ||
         n_v == 0 || n_v % n_k || kern == 0 || n_seq > 16 || nparts == 0 || nparts > 8 ||
         Nin < 2 * n_k * 128 + 2 * n_v * 128 + 2 * n_v)
         return ec_set_error(EC_ERR_ARG, "ec_delta_step: bad argument");
@@ -375,7 +376,7 @@ extern "C" int ec_delta_step_split(const float* proj, uint32_t nparts, uint32_t 
     const hipStream_t st = (hipStream_t)stream;
 #define EC_DSTEP(NP)                                                                                               \
     hipLaunchKernelGGL(k_delta_step<NP>, grid, dim3(1024), 0, st, proj, Nin, conv_state, conv_w, a_log, dt_bias, \
-                       norm_w, state, (uint8_t*)act, (uint32_t)L.xd_off, n_seq, pos, n_k, n_v, kern)
+                       norm_w, state, (uint8_t*)act, (uint32_t)L.xd_off, n_seq, pos, n_k, n_v, kern, out)
     switch (nparts) {
         case 1: EC_DSTEP(1); break;
         case 2: EC_DSTEP(2); break;
@@ -389,6 +390,15 @@ extern "C" int ec_delta_step_split(const float* proj, uint32_t nparts, uint32_t 
 #undef EC_DSTEP
     EC_CHECK_LAUNCH();
     return EC_OK;
+}
+
+extern "C" int ec_delta_step_split(const float* proj, uint32_t nparts, uint32_t Nin, float* conv_state,
+                                   const float* conv_w, const float* a_log, const float* dt_bias, const float* norm_w,
+                                   float* state, void* act, const int32_t* pos, uint32_t n_seq, uint32_t n_k,
+                                   uint32_t n_v, uint32_t kern, void* stream) {
+    if (!act && n_seq) return ec_set_error(EC_ERR_ARG, "ec_delta_step: bad argument");
+    return ec_delta_step_out(proj, nparts, Nin, conv_state, conv_w, a_log, dt_bias, norm_w, state, act, nullptr, pos,
+                             n_seq, n_k, n_v, kern, stream);
 }
 
 extern "C" int ec_delta_step(const float* proj, uint32_t Nin, float* conv_state, const float* conv_w,

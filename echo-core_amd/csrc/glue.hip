@@ -75,6 +75,19 @@ __global__ __launch_bounds__(256) void k_embed_q8_0(const uint8_t* __restrict__ 
     }
 }
 
+// F16 / F32 embedding rows (engine.zig:30-54 reads fp16, f32 and Q8_0 tables).
+template <typename T>
+__global__ __launch_bounds__(256) void k_embed_rows(const T* __restrict__ emb, const int32_t* __restrict__ tok,
+                                                    float* __restrict__ x, uint32_t H, uint32_t vocab) {
+    const uint32_t s = blockIdx.x;
+    int32_t t = tok[s];
+    t = t < 0 ? 0 : (t >= (int32_t)vocab ? (int32_t)vocab - 1 : t);
+    for (uint32_t i = threadIdx.x; i < H; i += 256) {
+        if constexpr (sizeof(T) == 2) x[(size_t)s * H + i] = h2f(emb[(size_t)t * H + i]);
+        else x[(size_t)s * H + i] = emb[(size_t)t * H + i];
+    }
+}
+
 // ---------------------------------------------------------- RMSNorm + quantize
 // grid (ceil(Kp/256), M), block 256: every block reads the whole row i of x
 // [M][H] for the sum of squares (float4 loads, all issued before the
@@ -559,6 +572,18 @@ extern "C" int ec_glue_embed(const void* emb, const int32_t* tok, float* x, uint
                              uint32_t vocab, void* stream) {
     if (!emb || !tok || !x || H % 32) return ec_set_error(EC_ERR_ARG, "ec_glue_embed: bad argument");
     EC_GLUE_LAUNCH(k_embed_q8_0, dim3(n_seq), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)emb, tok, x, H,
+                   vocab);
+}
+
+extern "C" int ec_glue_embed_fmt(int fmt, const void* emb, const int32_t* tok, float* x, uint32_t n_seq, uint32_t H,
+                                 uint32_t vocab, void* stream) {
+    if (fmt == EC_Q8_0) return ec_glue_embed(emb, tok, x, n_seq, H, vocab, stream);
+    if (!emb || !tok || !x || (fmt != EC_F16 && fmt != EC_F32))
+        return ec_set_error(EC_ERR_ARG, "ec_glue_embed_fmt: format must be Q8_0, F16 or F32");
+    if (fmt == EC_F16)
+        EC_GLUE_LAUNCH(k_embed_rows<uint16_t>, dim3(n_seq), dim3(256), 0, (hipStream_t)stream, (const uint16_t*)emb,
+                       tok, x, H, vocab);
+    EC_GLUE_LAUNCH(k_embed_rows<float>, dim3(n_seq), dim3(256), 0, (hipStream_t)stream, (const float*)emb, tok, x, H,
                    vocab);
 }
 

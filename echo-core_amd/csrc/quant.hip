@@ -109,6 +109,22 @@ __global__ void k_unpack_q8_0(const uint8_t* __restrict__ src, uint8_t* __restri
     }
 }
 
+// Inverse of k_repack_q4_K: tiled -> GGUF rows (only the N x K/256 real super-blocks).
+__global__ void k_unpack_q4_K(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint32_t N, uint32_t K,
+                              uint32_t Kp) {
+    const uint32_t nb = K / 256, nbp = Kp / 256;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)N * nb) return;
+    const uint32_t row = idx / nb, b = idx % nb, t = row / 16, r = row % 16;
+    const uint8_t* ch = src + ((size_t)t * nbp + b) * 2304;
+    uint8_t* o = dst + ((size_t)row * nb + b) * 144;
+    for (int i = 0; i < 16; ++i) o[i] = ch[2048 + r * 16 + i];
+    for (int g = 0; g < 4; ++g)
+        for (int sb = 0; sb < 8; ++sb)
+            for (int e = 0; e < 4; ++e)
+                o[16 + 16 * sb + 4 * g + e] = ch[(sb / 4) * 1024 + (size_t)(r + 16 * g) * 16 + 4 * (sb % 4) + e];
+}
+
 // ------------------------------------------------------- activation packing
 // One thread per (token slot i < 16, 32-block).  Slots >= M only zero scales.
 __global__ void k_quantize_act_q8_0(const float* __restrict__ x, uint8_t* __restrict__ act, uint32_t M, uint32_t K,
@@ -322,7 +338,16 @@ extern "C" int ec_repack(int fmt, const void* gguf, void* tiled, uint32_t N, uin
 }
 
 extern "C" int ec_unpack_tiled(int fmt, const void* tiled, void* gguf, uint32_t N, uint32_t K, void* stream) {
-    if (fmt != EC_Q8_0) return ec_set_error(EC_ERR_UNSUPPORTED, "ec_unpack_tiled: Q8_0 only");
+    if (fmt == EC_Q4_K) {
+        if (!tiled || !gguf || K % 256) return ec_set_error(EC_ERR_ARG, "ec_unpack_tiled: bad argument");
+        const size_t n = (size_t)N * (K / 256);
+        if (n == 0) return EC_OK;
+        hipLaunchKernelGGL(k_unpack_q4_K, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream,
+                           (const uint8_t*)tiled, (uint8_t*)gguf, N, K, round_up(K, 256));
+        EC_CHECK_LAUNCH();
+        return EC_OK;
+    }
+    if (fmt != EC_Q8_0) return ec_set_error(EC_ERR_UNSUPPORTED, "ec_unpack_tiled: Q8_0 or Q4_K");
     if (!tiled || !gguf || K % 32) return ec_set_error(EC_ERR_ARG, "ec_unpack_tiled: bad argument");
     const size_t n = (size_t)N * (K / 32);
     if (n == 0) return EC_OK;

@@ -12,11 +12,21 @@ T_EMBED, T_FINAL_NORM, T_LM_HEAD = 0, 1, 2
 T_ATTN_NORM, T_FFN_NORM, T_W_IN, T_W_OUT, T_W_GATE, T_W_UP, T_W_DOWN = 10, 11, 12, 13, 14, 15, 16
 T_CONV_W, T_A_LOG, T_DT_BIAS, T_SSM_NORM, T_Q_NORM, T_K_NORM = 17, 18, 19, 20, 21, 22
 S_CONV, S_SSM, S_KEYS, S_VALS, S_KSCALES, S_VSCALES = 0, 1, 2, 3, 4, 5
+# tensor formats (echo_hip.h ec_wfmt)
+F32, F16, Q8_0, Q4_K = 0, 1, 6, 10
+MATRICES = (T_W_IN, T_W_OUT, T_W_GATE, T_W_UP, T_W_DOWN)
 # step trace operations and step buffers (echo_engine.h EC_OP_* / EC_B_*)
-(OP_EMBED, OP_NORM, OP_MV_IN, OP_DELTA_STEP, OP_MV_OUT, OP_ROPE_APPEND, OP_ATTN, OP_QUANT_ATTN, OP_MV_GU, OP_SWIGLU,
- OP_MV_DOWN, OP_LM_HEAD, OP_ARGMAX) = range(13)
+(OP_EMBED, OP_NORM, OP_MV_IN, OP_DELTA_STEP, OP_MV_OUT, OP_ROPE_APPEND, OP_ATTN, OP_QUANT_ACT, OP_MV_GU, OP_SWIGLU,
+ OP_MV_DOWN, OP_LM_HEAD, OP_ARGMAX, OP_NORM_ROWS) = range(14)
 (B_X, B_X2, B_PARTS, B_PROJ, B_GU, B_ACT_H, B_ACT_V, B_ACT_F, B_ACT_Q, B_ATTN_OUT, B_Q_PACKED, B_Q_SCALES, B_QBUF,
- B_LOGITS, B_TOK, B_POS, B_GEN, B_CTX, B_INV_FREQ) = range(19)
+ B_LOGITS, B_TOK, B_POS, B_GEN, B_CTX, B_INV_FREQ, B_HN, B_CORE, B_FF, B_ACT4_H, B_ACT4_V, B_ACT4_Q,
+ B_ACT4_F) = range(26)
+ACT4_BUFFERS = (B_ACT4_H, B_ACT4_V, B_ACT4_Q, B_ACT4_F)
+
+
+def gguf_row_bytes(fmt: int, K: int) -> int:
+    """Bytes of one GGUF row of K elements."""
+    return {Q8_0: K // 32 * 34, Q4_K: K // 256 * 144, F16: 2 * K, F32: 4 * K}[fmt]
 
 
 class TraceEvent(C.Structure):
@@ -98,6 +108,8 @@ class Engine:
                                                 C.POINTER(C.c_double)]
         L.ec_engine_step_traced.argtypes = [vp, _TRACE_FN, vp]
         L.ec_engine_buffer.argtypes = [vp, i32, C.POINTER(vp), C.POINTER(C.c_size_t)]
+        L.ec_engine_set_format.argtypes = [vp, i32, i32, i32]
+        L.ec_engine_get_format.argtypes = [vp, i32, i32]
         c = _Cfg(**{f.name: getattr(cfg, f.name) for f in fields(cfg)})
         h = vp()
         self._check(L.ec_engine_create(C.byref(c), C.byref(h)), "ec_engine_create")
@@ -116,6 +128,13 @@ class Engine:
         self.close()
 
     # ---- weights
+    def set_format(self, layer: int, tensor: int, fmt: int):
+        """Storage format of a matrix (Q8_0 / Q4_K) or of the embedding (Q8_0 / F16 / F32)."""
+        self._check(self.L.ec_engine_set_format(self.h, layer, tensor, fmt), "set_format")
+
+    def get_format(self, layer: int, tensor: int) -> int:
+        return self.L.ec_engine_get_format(self.h, layer, tensor)
+
     def set_tensor(self, layer: int, tensor: int, arr: np.ndarray):
         a = np.ascontiguousarray(arr)
         self._check(self.L.ec_engine_set_tensor(self.h, layer, tensor, a.ctypes.data, a.nbytes), "set_tensor")
@@ -138,22 +157,34 @@ class Engine:
 
     def export_model(self) -> dict:
         """Copy the weights back to the host in the oracle decoder's weight
-        dict: GGUF Q8_0 matrices (w_in = the fused input-projection rows),
+        dict: GGUF matrices of their storage format (w_in = the fused
+        input-projection rows; the formats under "fmt" when not all Q8_0),
         fp32 vectors."""
         cfg = self.cfg
         H, F = cfg.hidden, cfg.ffn
-        q8 = lambda rows, K: rows * (K // 32) * 34  # noqa: E731
         f32 = lambda n: (n * 4, np.float32)  # noqa: E731
-        m = {"embed": self.get_tensor(0, T_EMBED, q8(cfg.vocab, H)),
-             "final_norm": self.get_tensor(0, T_FINAL_NORM, *f32(H)),
-             "lm_head": self.get_tensor(0, T_LM_HEAD, q8(cfg.vocab, H)), "layers": []}
+        fmts = {}
+
+        def mat(l, t, name, rows, K):
+            fmt = self.get_format(l, t)
+            if fmt != Q8_0:
+                fmts[(l, name)] = fmt
+            return self.get_tensor(l, t, rows * gguf_row_bytes(fmt, K))
+        emb_fmt = self.get_format(0, T_EMBED)
+        if emb_fmt != Q8_0:
+            fmts[(-1, "embed")] = emb_fmt
+        emb = self.get_tensor(0, T_EMBED, cfg.vocab * gguf_row_bytes(emb_fmt, H))
+        if emb_fmt in (F16, F32):
+            emb = emb.view(np.float16 if emb_fmt == F16 else np.float32)
+        m = {"embed": emb, "final_norm": self.get_tensor(0, T_FINAL_NORM, *f32(H)),
+             "lm_head": mat(-1, T_LM_HEAD, "lm_head", cfg.vocab, H), "layers": []}
         for l in range(cfg.n_layers):
             attn = cfg.is_attn(l)
             nin = cfg.nin_attn if attn else cfg.nin_delta
             kout = cfg.n_heads * cfg.head_dim if attn else cfg.ssm_inner
-            y = {"attn": attn, "w_in": self.get_tensor(l, T_W_IN, q8(nin, H)),
-                 "w_out": self.get_tensor(l, T_W_OUT, q8(H, kout)), "w_gate": self.get_tensor(l, T_W_GATE, q8(F, H)),
-                 "w_up": self.get_tensor(l, T_W_UP, q8(F, H)), "w_down": self.get_tensor(l, T_W_DOWN, q8(H, F)),
+            y = {"attn": attn, "w_in": mat(l, T_W_IN, "w_in", nin, H), "w_out": mat(l, T_W_OUT, "w_out", H, kout),
+                 "w_gate": mat(l, T_W_GATE, "w_gate", F, H), "w_up": mat(l, T_W_UP, "w_up", F, H),
+                 "w_down": mat(l, T_W_DOWN, "w_down", H, F),
                  "attn_norm": self.get_tensor(l, T_ATTN_NORM, *f32(H)),
                  "ffn_norm": self.get_tensor(l, T_FFN_NORM, *f32(H))}
             if attn:
@@ -165,6 +196,8 @@ class Engine:
                 y["dt_bias"] = self.get_tensor(l, T_DT_BIAS, *f32(cfg.ssm_heads))
                 y["ssm_norm"] = self.get_tensor(l, T_SSM_NORM, *f32(128))
             m["layers"].append(y)
+        if fmts:
+            m["fmt"] = fmts
         return m
 
     def init_random(self, seed: int = 0, w_scale: float = 0.02 / 73.0):
@@ -251,14 +284,16 @@ class Engine:
         return out
 
     def read_act(self, which: int, K: int):
-        """An activation buffer (ec_quantize_act Q8_0 layout, M = max_batch) as
-        (xq int8 [B][K], xd fp32 [B][K/32])."""
+        """An activation buffer (ec_quantize_act layout, M = max_batch; Q4_K for
+        the B_ACT4_* buffers, Q8_0 otherwise) as (xq int8 [B][K], xd fp32
+        [B][K/32]); Q4_K values in the quantizer's sub-block order."""
         import torch
-        p, _ = self.buffer(which)
+        p, n = self.buffer(which)
+        assert n, f"step buffer {which} is not allocated"
         B = self.cfg.max_batch
         xq = torch.empty(B * K, dtype=torch.int8, device="cuda")
         xd = torch.empty(B * (K // 32), dtype=torch.float32, device="cuda")
-        self.hip.act_unpack(6, p, xq, xd, B, K)
+        self.hip.act_unpack(Q4_K if which in ACT4_BUFFERS else Q8_0, p, xq, xd, B, K)
         torch.cuda.synchronize()
         return xq.cpu().numpy().reshape(B, K), xd.cpu().numpy().reshape(B, K // 32)
 

@@ -52,6 +52,7 @@ double normal_at(uint64_t seed, uint64_t i) {
 struct Mat {
     void* tiled = nullptr;
     uint32_t N = 0, K = 0;
+    int fmt = EC_Q8_0;  // EC_Q8_0 or EC_Q4_K (src/inference.cpp:526-545 dispatches per tensor)
 };
 
 struct Layer {
@@ -81,6 +82,7 @@ struct ec_engine {
     hipStream_t st = nullptr;
     std::vector<Layer> L;
     void* embed = nullptr;
+    int embed_fmt = EC_Q8_0;  // EC_Q8_0 (GGUF blocks), EC_F16 or EC_F32 rows
     float* final_norm = nullptr;
     Mat lm_head;
     uint32_t B = 0, H = 0, F = 0, q_dim = 0, kv_dim = 0, value_dim = 0, key_dim = 0, conv_dim = 0, n_v = 0, n_k = 0;
@@ -95,6 +97,11 @@ struct ec_engine {
     void *act_h = nullptr, *act_v = nullptr, *act_f = nullptr, *act_q = nullptr, *attn_ws = nullptr;
     void* q_packed = nullptr;
     float* q_scales = nullptr;
+    // inputs of Q4_K matrices (allocated with the first one): fp32 rows of the
+    // producing op and their Q4_K-grouped activation
+    bool q4 = false;
+    float *hn = nullptr, *core_f = nullptr, *ff = nullptr;
+    void *act4_h = nullptr, *act4_v = nullptr, *act4_q = nullptr, *act4_f = nullptr;
     bool packed_attn = false;  // int8-MFMA attention with q packed by the rope kernel
     int32_t *tok = nullptr, *pos = nullptr, *gen = nullptr, *ctx = nullptr;
     // pinned staging for ec_engine_set_inputs: a ring of slots (tok[16],
@@ -149,28 +156,36 @@ int dalloc(ec_engine* e, T** p, size_t count) {
 int alloc_mat(ec_engine* e, Mat& m, uint32_t N, uint32_t K) {
     m.N = N;
     m.K = K;
-    return dalloc(e, &m.tiled, ec_tiled_bytes(EC_Q8_0, N, K));
+    return dalloc(e, &m.tiled, ec_tiled_bytes(m.fmt, N, K));
 }
 
 bool is_attn(const ec_engine_cfg& c, uint32_t l) { return c.attn_interval && ((l + 1) % c.attn_interval) == 0; }
 
-size_t gguf_bytes(uint32_t N, uint32_t K) { return (size_t)N * (K / 32) * 34; }
+size_t gguf_bytes(int fmt, uint32_t N, uint32_t K) {
+    return fmt == EC_Q4_K ? (size_t)N * (K / 256) * 144 : (size_t)N * (K / 32) * 34;
+}
+size_t gguf_bytes(const Mat& m, uint32_t N) { return gguf_bytes(m.fmt, N, m.K); }
+size_t embed_bytes(const ec_engine* e) {
+    const size_t n = (size_t)e->c.vocab * e->H;
+    return e->embed_fmt == EC_F16 ? 2 * n : (e->embed_fmt == EC_F32 ? 4 * n : gguf_bytes(EC_Q8_0, e->c.vocab, e->H));
+}
 
 // Upload GGUF bytes (host) of rows [row0, row0+N) of matrix m's logical rows
 // and repack them into the tiled layout at that tile offset (row0 % 16 == 0).
 int upload_rows(ec_engine* e, Mat& m, uint32_t row0, const void* host, uint32_t N) {
     if (row0 % 16 || row0 + N > m.N) return ec_set_error(EC_ERR_ARG, "engine: bad row range");
     void* tmp = nullptr;
-    EC_HIP(hipMalloc(&tmp, gguf_bytes(N, m.K)));
-    EC_HIP(hipMemcpyAsync(tmp, host, gguf_bytes(N, m.K), hipMemcpyHostToDevice, e->st));
-    uint8_t* dst = (uint8_t*)m.tiled + ec_tiled_bytes(EC_Q8_0, row0, m.K);
-    int rc = ec_repack(EC_Q8_0, tmp, dst, N, m.K, e->st);
+    EC_HIP(hipMalloc(&tmp, gguf_bytes(m, N)));
+    EC_HIP(hipMemcpyAsync(tmp, host, gguf_bytes(m, N), hipMemcpyHostToDevice, e->st));
+    uint8_t* dst = (uint8_t*)m.tiled + ec_tiled_bytes(m.fmt, row0, m.K);
+    int rc = ec_repack(m.fmt, tmp, dst, N, m.K, e->st);
     EC_HIP(hipStreamSynchronize(e->st));
     EC_HIP(hipFree(tmp));
     return rc;
 }
 
 int random_rows(ec_engine* e, Mat& m, uint32_t row0, uint32_t N, uint64_t seed, float scale, void* tmp) {
+    if (m.fmt != EC_Q8_0) return ec_set_error(EC_ERR_UNSUPPORTED, "ec_engine_init_random: Q8_0 matrices only");
     EC_TRY(ec_fill_random(1, tmp, (uint64_t)N * (m.K / 32), seed, scale, m.K, e->st));
     uint8_t* dst = (uint8_t*)m.tiled + ec_tiled_bytes(EC_Q8_0, row0, m.K);
     return ec_repack(EC_Q8_0, tmp, dst, N, m.K, e->st);
@@ -200,13 +215,19 @@ std::vector<float> gen_vec(uint64_t seed, size_t n, double mean, double std) {
     return v;
 }
 
+// Activation bytes of one matvec input (int8 + fp32 block scales; Q4_K also
+// fp32 per-block sums).
+double act_alg_bytes(const ec_engine* e, const Mat& m) {
+    return (double)e->B * (m.K + m.K / 32 * 4 * (m.fmt == EC_Q4_K ? 2 : 1));
+}
+
 // One matvec launch; in profiling mode also its algorithmic bytes (weights,
 // activation bytes + scales, outputs written, and read too when accumulating).
 int mv(ec_engine* e, const Mat& m, const void* act, float* y, uint32_t ldy, int acc) {
     if (e->mv_bytes)
-        e->mv_bytes->push_back((double)gguf_bytes(m.N, m.K) + (double)e->B * (m.K + m.K / 32 * 4) +
+        e->mv_bytes->push_back((double)gguf_bytes(m, m.N) + act_alg_bytes(e, m) +
                                (double)e->B * m.N * 4 * (acc ? 2 : 1));
-    return ec_matvec(EC_Q8_0, m.tiled, act, y, e->B, m.N, m.K, ldy, acc, e->st);
+    return ec_matvec(m.fmt, m.tiled, act, y, e->B, m.N, m.K, ldy, acc, e->st);
 }
 
 // K splits of a residual-adding projection (N = hidden): with N/16 tiles
@@ -218,7 +239,8 @@ int mv(ec_engine* e, const Mat& m, const void* act, float* y, uint32_t ldy, int 
 // decode step was fastest at 3 and 3 (EC_RESID_SPLIT="a,b" overrides the
 // splits for K < 8192 and K >= 8192).
 constexpr uint32_t kMaxResidSplit = 8;
-uint32_t resid_split(uint32_t N, uint32_t K) {
+uint32_t resid_split(uint32_t N, uint32_t K, int fmt = EC_Q8_0) {
+    if (fmt != EC_Q8_0) return 1;
     static const std::pair<uint32_t, uint32_t> sp = [] {
         uint32_t a = 3, b = 3;
         if (const char* v = getenv("EC_RESID_SPLIT")) sscanf(v, "%u,%u", &a, &b);
@@ -256,24 +278,20 @@ uint32_t attn_split() {
     return v;
 }
 
-// A split count clamped to the matrix's 128-element K chunks.
-uint32_t split_count(const Mat& m, uint32_t ns) { return std::min(ns, (m.K + 127) / 128); }
+// A split count clamped to the matrix's 128-element K chunks (Q4_K: no split).
+uint32_t split_count(const Mat& m, uint32_t ns) { return m.fmt == EC_Q8_0 ? std::min(ns, (m.K + 127) / 128) : 1u; }
 
-// A split-K projection into y ([ns][B][N]); ns from split_count.
+// A split-K projection into y ([ns][B][N]); ns from split_count.  Q4_K: one
+// whole-K launch into y.
 int mv_split(ec_engine* e, const Mat& m, const void* act, float* y, uint32_t ns) {
     if (e->mv_bytes)  // the output counted once (the extra partial sums are not algorithmic bytes)
-        e->mv_bytes->push_back((double)gguf_bytes(m.N, m.K) + (double)e->B * (m.K + m.K / 32 * 4) +
-                               (double)e->B * m.N * 4);
+        e->mv_bytes->push_back((double)gguf_bytes(m, m.N) + act_alg_bytes(e, m) + (double)e->B * m.N * 4);
+    if (m.fmt != EC_Q8_0) return ec_matvec(m.fmt, m.tiled, act, y, e->B, m.N, m.K, m.N, 0, e->st);
     return ec_matvec_split(EC_Q8_0, m.tiled, act, y, e->B, m.N, m.K, ns, e->st);
 }
 
-// Residual projection: ns = resid_split(N, K) partial sums into e->parts.
-int mv_resid(ec_engine* e, const Mat& m, const void* act, uint32_t ns) {
-    if (e->mv_bytes)  // the output counted once, as in mv_split
-        e->mv_bytes->push_back((double)gguf_bytes(m.N, m.K) + (double)e->B * (m.K + m.K / 32 * 4) +
-                               (double)e->B * m.N * 4);
-    return ec_matvec_split(EC_Q8_0, m.tiled, act, e->parts, e->B, m.N, m.K, ns, e->st);
-}
+// Residual projection: ns = resid_split(m) partial sums into e->parts.
+int mv_resid(ec_engine* e, const Mat& m, const void* act, uint32_t ns) { return mv_split(e, m, act, e->parts, ns); }
 
 // One launch of the decode step; with a trace callback installed, the stream
 // is drained and the callback called before and after it.
@@ -291,7 +309,11 @@ int launch(ec_engine* e, int op, int layer, int nparts, int x_in, int x_out, F&&
     return EC_OK;
 }
 
-// The decode step (stream-ordered; captured once into a graph).
+// The decode step (stream-ordered; captured once into a graph).  Q8_0
+// matrices read the Q8_0 activations the fused glue kernels write; a Q4_K
+// matrix reads a Q4_K-grouped activation quantized from the fp32 output of its
+// producer (RMSNorm rows, the delta step's fp32 output, attention's output,
+// SwiGLU rows), one extra launch per such input.
 int record_step(ec_engine* e) {
     const ec_engine_cfg& c = e->c;
     const uint32_t B = e->B, H = e->H, F = e->F;
@@ -301,43 +323,62 @@ int record_step(ec_engine* e) {
     do {                                                                                  \
         if (!e->mv_only) EC_TRY(launch(e, op, layer, (int)(nparts), xin, xout, [&] { return (call); })); \
     } while (0)
-#define EC_MV(op, layer, nparts, call) EC_TRY(launch(e, op, layer, (int)(nparts), -1, -1, [&] { return (call); }))
+#define EC_MV(op, layer, nparts, actb, call) EC_TRY(launch(e, op, layer, (int)(nparts), actb, -1, [&] { return (call); }))
     // xc: the current residual; ns > 0: e->parts holds ns partial sums still
     // to be added to it (by the next norm, which then moves xc to the other buffer)
     float* xc = e->x;
     uint32_t ns = 0;
     auto xid = [&](const float* p) { return p == e->x ? EC_B_X : EC_B_X2; };
-    auto norm = [&](const float* w, int layer) -> int {
+    auto q4 = [](const Mat& m) { return m.fmt == EC_Q4_K; };
+    // RMSNorm of the residual (adding pending partial sums first) into act_h;
+    // with a Q4_K consumer also the fp32 rows and their Q4_K activation
+    auto norm = [&](const float* w, int layer, bool need4) -> int {
         if (ns == 0) {
             EC_GLUE(EC_OP_NORM, layer, 0, xid(xc), xid(xc), ec_glue_rmsnorm_quant(xc, w, e->act_h, B, H, st));
-            return EC_OK;
+        } else {
+            float* xn = xc == e->x ? e->x2 : e->x;
+            EC_GLUE(EC_OP_NORM, layer, ns, xid(xc), xid(xn),
+                    ec_glue_add_rmsnorm_quant(xc, e->parts, ns, xn, w, e->act_h, B, H, st));
+            xc = xn;
+            ns = 0;
         }
-        float* xn = xc == e->x ? e->x2 : e->x;
-        EC_GLUE(EC_OP_NORM, layer, ns, xid(xc), xid(xn),
-                ec_glue_add_rmsnorm_quant(xc, e->parts, ns, xn, w, e->act_h, B, H, st));
-        xc = xn;
-        ns = 0;
+        if (need4) {
+            EC_GLUE(EC_OP_NORM_ROWS, layer, 0, xid(xc), EC_B_HN, ec_glue_rmsnorm_rows(xc, w, e->hn, B, H, st));
+            EC_GLUE(EC_OP_QUANT_ACT, layer, 0, EC_B_HN, EC_B_ACT4_H, ec_quantize_act(EC_Q4_K, e->hn, e->act4_h, B, H, st));
+        }
         return EC_OK;
     };
-    EC_GLUE(EC_OP_EMBED, -1, 0, -1, EC_B_X, ec_glue_embed(e->embed, e->tok, e->x, B, H, c.vocab, st));
+    auto ain = [&](const Mat& m, void* a8, void* a4) { return q4(m) ? a4 : a8; };
+    auto aid = [&](const Mat& m, int b8, int b4) { return q4(m) ? b4 : b8; };
+    EC_GLUE(EC_OP_EMBED, -1, 0, -1, EC_B_X, ec_glue_embed_fmt(e->embed_fmt, e->embed, e->tok, e->x, B, H, c.vocab, st));
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         Layer& y = e->L[l];
         const int li = (int)l;
-        EC_TRY(norm(y.attn_norm, li));
+        EC_TRY(norm(y.attn_norm, li, q4(y.w_in)));
         if (!y.attn) {
             const uint32_t Nin = e->nin_delta;
             const uint32_t nsi = split_count(y.w_in, in_split());
-            EC_MV(EC_OP_MV_IN, li, nsi, mv_split(e, y.w_in, e->act_h, e->proj, nsi));
+            EC_MV(EC_OP_MV_IN, li, nsi, aid(y.w_in, EC_B_ACT_H, EC_B_ACT4_H),
+                  mv_split(e, y.w_in, ain(y.w_in, e->act_h, e->act4_h), e->proj, nsi));
             // conv + gates + delta rule + gated norm + quantize in one launch
-            EC_GLUE(EC_OP_DELTA_STEP, li, nsi, -1, -1,
-                    ec_delta_step_split(e->proj, nsi, Nin, y.conv_state, y.conv_w, y.a_log, y.dt_bias, y.ssm_norm,
-                                        y.ssm_state, e->act_v, e->pos, B, e->n_k, e->n_v, c.conv_kernel, st));
-            ns = resid_split(y.w_out.N, y.w_out.K);
-            EC_MV(EC_OP_MV_OUT, li, ns, mv_resid(e, y.w_out, e->act_v, ns));
+            // (fp32 output instead when the output projection is Q4_K)
+            const bool o4 = q4(y.w_out);
+            EC_GLUE(EC_OP_DELTA_STEP, li, nsi, -1, o4 ? EC_B_CORE : EC_B_ACT_V,
+                    ec_delta_step_out(e->proj, nsi, Nin, y.conv_state, y.conv_w, y.a_log, y.dt_bias, y.ssm_norm,
+                                      y.ssm_state, o4 ? nullptr : e->act_v, o4 ? e->core_f : nullptr, e->pos, B,
+                                      e->n_k, e->n_v, c.conv_kernel, st));
+            if (o4)
+                EC_GLUE(EC_OP_QUANT_ACT, li, 0, EC_B_CORE, EC_B_ACT4_V,
+                        ec_quantize_act(EC_Q4_K, e->core_f, e->act4_v, B, e->value_dim, st));
+            ns = resid_split(y.w_out.N, y.w_out.K, y.w_out.fmt);
+            EC_MV(EC_OP_MV_OUT, li, ns, aid(y.w_out, EC_B_ACT_V, EC_B_ACT4_V),
+                  mv_resid(e, y.w_out, ain(y.w_out, e->act_v, e->act4_v), ns));
         } else {
             const uint32_t Nin = e->nin_attn;
             const uint32_t nsa = split_count(y.w_in, attn_split());
-            EC_MV(EC_OP_MV_IN, li, nsa, mv_split(e, y.w_in, e->act_h, e->proj, nsa));
+            EC_MV(EC_OP_MV_IN, li, nsa, aid(y.w_in, EC_B_ACT_H, EC_B_ACT4_H),
+                  mv_split(e, y.w_in, ain(y.w_in, e->act_h, e->act4_h), e->proj, nsa));
+            const bool o4 = q4(y.w_out);
             if (e->packed_attn) {
                 // rope + KV append write q as int8 pieces; attention writes the
                 // Q8_0 activation of its output for the output projection
@@ -346,10 +387,10 @@ int record_step(ec_engine* e) {
                                                      e->inv_freq, e->pos, nullptr, e->q_packed, e->q_scales, y.keys,
                                                      y.vals, y.ks, y.vs, e->ctx, B, e->seq_stride, c.max_ctx,
                                                      c.n_heads, c.n_kv, c.head_dim, st));
-                EC_GLUE(EC_OP_ATTN, li, 0, -1, -1,
+                EC_GLUE(EC_OP_ATTN, li, 0, -1, o4 ? -1 : EC_B_ACT_Q,
                         ec_attn_decode_packed(e->q_packed, e->q_scales, y.keys, y.vals, y.ks, y.vs, e->attn_out,
-                                              e->act_q, e->ctx, B, e->seq_stride, c.n_heads, c.n_kv, c.max_ctx,
-                                              e->attn_ws, st));
+                                              o4 ? nullptr : e->act_q, e->ctx, B, e->seq_stride, c.n_heads, c.n_kv,
+                                              c.max_ctx, e->attn_ws, st));
             } else {
                 EC_GLUE(EC_OP_ROPE_APPEND, li, nsa, -1, -1,
                         ec_glue_qk_rope_append_split(e->proj, nsa, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn,
@@ -359,20 +400,36 @@ int record_step(ec_engine* e) {
                 EC_GLUE(EC_OP_ATTN, li, 0, -1, -1,
                         ec_attn_decode(e->qbuf, y.keys, y.vals, y.ks, y.vs, e->attn_out, e->ctx, B, e->seq_stride,
                                        c.n_heads, c.n_kv, c.head_dim, c.max_ctx, e->attn_ws, st));
-                EC_GLUE(EC_OP_QUANT_ATTN, li, 0, -1, -1, ec_quantize_act(EC_Q8_0, e->attn_out, e->act_q, B, e->q_dim, st));
+                if (!o4)
+                    EC_GLUE(EC_OP_QUANT_ACT, li, 0, EC_B_ATTN_OUT, EC_B_ACT_Q,
+                            ec_quantize_act(EC_Q8_0, e->attn_out, e->act_q, B, e->q_dim, st));
             }
-            ns = resid_split(y.w_out.N, y.w_out.K);
-            EC_MV(EC_OP_MV_OUT, li, ns, mv_resid(e, y.w_out, e->act_q, ns));
+            if (o4)
+                EC_GLUE(EC_OP_QUANT_ACT, li, 0, EC_B_ATTN_OUT, EC_B_ACT4_Q,
+                        ec_quantize_act(EC_Q4_K, e->attn_out, e->act4_q, B, e->q_dim, st));
+            ns = resid_split(y.w_out.N, y.w_out.K, y.w_out.fmt);
+            EC_MV(EC_OP_MV_OUT, li, ns, aid(y.w_out, EC_B_ACT_Q, EC_B_ACT4_Q),
+                  mv_resid(e, y.w_out, ain(y.w_out, e->act_q, e->act4_q), ns));
         }
-        EC_TRY(norm(y.ffn_norm, li));
-        const uint32_t nsg = split_count(y.w_gu, gu_split());
-        EC_MV(EC_OP_MV_GU, li, nsg, mv_split(e, y.w_gu, e->act_h, e->gu, nsg));
-        EC_GLUE(EC_OP_SWIGLU, li, nsg, -1, -1, ec_glue_swiglu_quant_split(e->gu, nsg, e->act_f, B, F, st));
-        ns = resid_split(y.w_down.N, y.w_down.K);
-        EC_MV(EC_OP_MV_DOWN, li, ns, mv_resid(e, y.w_down, e->act_f, ns));
+        EC_TRY(norm(y.ffn_norm, li, q4(y.w_gu)));
+        const bool d4 = q4(y.w_down);
+        // a Q4_K down projection reads SwiGLU rows, which take one gate/up part
+        const uint32_t nsg = d4 ? 1u : split_count(y.w_gu, gu_split());
+        EC_MV(EC_OP_MV_GU, li, nsg, aid(y.w_gu, EC_B_ACT_H, EC_B_ACT4_H),
+              mv_split(e, y.w_gu, ain(y.w_gu, e->act_h, e->act4_h), e->gu, nsg));
+        if (d4) {
+            EC_GLUE(EC_OP_SWIGLU, li, nsg, -1, EC_B_FF, ec_glue_swiglu_rows(e->gu, e->ff, B, F, st));
+            EC_GLUE(EC_OP_QUANT_ACT, li, 0, EC_B_FF, EC_B_ACT4_F, ec_quantize_act(EC_Q4_K, e->ff, e->act4_f, B, F, st));
+        } else {
+            EC_GLUE(EC_OP_SWIGLU, li, nsg, -1, EC_B_ACT_F, ec_glue_swiglu_quant_split(e->gu, nsg, e->act_f, B, F, st));
+        }
+        ns = resid_split(y.w_down.N, y.w_down.K, y.w_down.fmt);
+        EC_MV(EC_OP_MV_DOWN, li, ns, aid(y.w_down, EC_B_ACT_F, EC_B_ACT4_F),
+              mv_resid(e, y.w_down, ain(y.w_down, e->act_f, e->act4_f), ns));
     }
-    EC_TRY(norm(e->final_norm, -1));
-    EC_MV(EC_OP_LM_HEAD, -1, 0, mv(e, e->lm_head, e->act_h, e->logits, c.vocab, 0));
+    EC_TRY(norm(e->final_norm, -1, q4(e->lm_head)));
+    EC_MV(EC_OP_LM_HEAD, -1, 0, aid(e->lm_head, EC_B_ACT_H, EC_B_ACT4_H),
+          mv(e, e->lm_head, ain(e->lm_head, e->act_h, e->act4_h), e->logits, c.vocab, 0));
     EC_GLUE(EC_OP_ARGMAX, -1, 0, -1, -1,
             ec_glue_argmax_advance(e->logits, c.vocab, e->gen, e->tok, e->pos, B, c.max_ctx, st));
     return EC_OK;
@@ -437,8 +494,7 @@ extern "C" int ec_engine_create(const ec_engine_cfg* cfg, ec_engine** out) {
             (rc = alloc_mat(e, y.w_gu, 2 * e->F, H)) || (rc = alloc_mat(e, y.w_down, H, e->F)) ||
             (rc = dalloc(e, &y.attn_norm, H)) || (rc = dalloc(e, &y.ffn_norm, H)))
             break;
-        wb += ec_tiled_bytes(EC_Q8_0, Nin, H) + ec_tiled_bytes(EC_Q8_0, H, Kout) +
-              ec_tiled_bytes(EC_Q8_0, 2 * e->F, H) + ec_tiled_bytes(EC_Q8_0, H, e->F) + 2 * H * 4;
+        wb += 2 * H * 4;
         if (!y.attn) {
             if ((rc = dalloc(e, &y.conv_w, (size_t)c.conv_kernel * e->conv_dim)) ||
                 (rc = dalloc(e, &y.a_log, e->n_v)) || (rc = dalloc(e, &y.dt_bias, e->n_v)) ||
@@ -458,11 +514,9 @@ extern "C" int ec_engine_create(const ec_engine_cfg* cfg, ec_engine** out) {
         }
     }
     if (rc) return fail(rc);
-    wb += ec_tiled_bytes(EC_Q8_0, c.vocab, H) + H * 4;
-    e->weight_bytes = wb;
-    const size_t maxK = std::max(std::max(H, e->F), std::max(e->value_dim, e->q_dim));
-    (void)maxK;
-    if ((rc = dalloc(e, &e->embed, gguf_bytes(c.vocab, H))) || (rc = dalloc(e, &e->final_norm, H)) ||
+    wb += H * 4;
+    e->weight_bytes = wb;  // vectors; the matrices are counted by ec_engine_weight_bytes
+    if ((rc = dalloc(e, &e->embed, embed_bytes(e))) || (rc = dalloc(e, &e->final_norm, H)) ||
         (rc = alloc_mat(e, e->lm_head, c.vocab, H)) || (rc = dalloc(e, &e->x, (size_t)B * H)) ||
         (rc = dalloc(e, &e->x2, (size_t)B * H)) || (rc = dalloc(e, &e->parts, (size_t)kMaxResidSplit * B * H)) ||
         (rc = dalloc(e, &e->proj, (size_t)kMaxResidSplit * B * e->nin_max)) ||
@@ -507,6 +561,83 @@ extern "C" int ec_engine_get_config(const ec_engine* e, ec_engine_cfg* out) {
     return EC_OK;
 }
 
+namespace {
+
+// The matrix a (layer, tensor) names, or nullptr.
+Mat* find_mat(ec_engine* e, int layer, int tensor) {
+    if (tensor == EC_T_LM_HEAD) return &e->lm_head;
+    if (layer < 0 || layer >= (int)e->c.n_layers) return nullptr;
+    Layer& y = e->L[layer];
+    switch (tensor) {
+        case EC_T_W_IN: return &y.w_in;
+        case EC_T_W_OUT: return &y.w_out;
+        case EC_T_W_GATE:
+        case EC_T_W_UP: return &y.w_gu;
+        case EC_T_W_DOWN: return &y.w_down;
+        default: return nullptr;
+    }
+}
+
+// Buffers of Q4_K inputs, allocated with the first Q4_K matrix.
+int alloc_q4(ec_engine* e) {
+    if (e->q4) return EC_OK;
+    const uint32_t B = e->B;
+    EC_TRY(dalloc(e, &e->hn, (size_t)B * e->H));
+    EC_TRY(dalloc(e, &e->core_f, (size_t)B * std::max(e->value_dim, 1u)));
+    EC_TRY(dalloc(e, &e->ff, (size_t)B * e->F));
+    EC_TRY(dalloc(e, &e->act4_h, ec_act_bytes(EC_Q4_K, B, e->H)));
+    EC_TRY(dalloc(e, &e->act4_v, e->value_dim % 256 ? 16 : ec_act_bytes(EC_Q4_K, B, e->value_dim)));
+    EC_TRY(dalloc(e, &e->act4_q, ec_act_bytes(EC_Q4_K, B, e->q_dim)));
+    EC_TRY(dalloc(e, &e->act4_f, e->F % 256 ? 16 : ec_act_bytes(EC_Q4_K, B, e->F)));
+    e->q4 = true;
+    return EC_OK;
+}
+
+// Free one allocation the engine owns (and forget it).
+void dfree(ec_engine* e, void* p) {
+    auto it = std::find(e->allocs.begin(), e->allocs.end(), p);
+    if (it != e->allocs.end()) e->allocs.erase(it);
+    (void)hipFree(p);
+}
+
+}  // namespace
+
+extern "C" int ec_engine_set_format(ec_engine* e, int layer, int tensor, int fmt) {
+    if (!e) return ec_set_error(EC_ERR_ARG, "ec_engine_set_format: null engine");
+    EC_HIP(hipStreamSynchronize(e->st));
+    if (tensor == EC_T_EMBED) {
+        if (fmt != EC_Q8_0 && fmt != EC_F16 && fmt != EC_F32)
+            return ec_set_error(EC_ERR_UNSUPPORTED, "ec_engine_set_format: embedding is Q8_0, F16 or F32");
+        if (fmt == e->embed_fmt) return EC_OK;
+        dfree(e, e->embed);
+        e->embed = nullptr;
+        e->embed_fmt = fmt;
+        destroy_graph(e);
+        return dalloc(e, &e->embed, embed_bytes(e));
+    }
+    Mat* m = find_mat(e, layer, tensor);
+    if (!m) return ec_set_error(EC_ERR_ARG, "ec_engine_set_format: not a matrix tensor");
+    if (fmt != EC_Q8_0 && fmt != EC_Q4_K)
+        return ec_set_error(EC_ERR_UNSUPPORTED, "ec_engine_set_format: matrices are Q8_0 or Q4_K");
+    if (fmt == EC_Q4_K && m->K % 256)
+        return ec_set_error(EC_ERR_ARG, "ec_engine_set_format: Q4_K needs K % 256 == 0");
+    if (fmt == m->fmt) return EC_OK;
+    if (fmt == EC_Q4_K) EC_TRY(alloc_q4(e));
+    dfree(e, m->tiled);
+    m->tiled = nullptr;
+    m->fmt = fmt;
+    destroy_graph(e);
+    return dalloc(e, &m->tiled, ec_tiled_bytes(fmt, m->N, m->K));
+}
+
+extern "C" int ec_engine_get_format(const ec_engine* e, int layer, int tensor) {
+    if (!e) return ec_set_error(EC_ERR_ARG, "ec_engine_get_format: null engine");
+    if (tensor == EC_T_EMBED) return e->embed_fmt;
+    const Mat* m = find_mat(const_cast<ec_engine*>(e), layer, tensor);
+    if (!m) return ec_set_error(EC_ERR_ARG, "ec_engine_get_format: not a matrix tensor");
+    return m->fmt;
+}
+
 extern "C" void ec_engine_destroy(ec_engine* e) {
     if (!e) return;
     if (e->st) (void)hipStreamSynchronize(e->st);
@@ -541,12 +672,12 @@ extern "C" int ec_engine_set_tensor(ec_engine* e, int layer, int tensor, const v
         return h2d(e, dst, host, bytes);
     };
     if (tensor == EC_T_EMBED) {
-        EC_TRY(need(gguf_bytes(c.vocab, e->H)));
+        EC_TRY(need(embed_bytes(e)));
         return h2d(e, e->embed, host, bytes);
     }
     if (tensor == EC_T_FINAL_NORM) return vec(e->final_norm, e->H);
     if (tensor == EC_T_LM_HEAD) {
-        EC_TRY(need(gguf_bytes(c.vocab, e->H)));
+        EC_TRY(need(gguf_bytes(e->lm_head, c.vocab)));
         return upload_rows(e, e->lm_head, 0, host, c.vocab);
     }
     if (layer < 0 || (uint32_t)layer >= c.n_layers) return ec_set_error(EC_ERR_ARG, "ec_engine_set_tensor: layer");
@@ -555,11 +686,11 @@ extern "C" int ec_engine_set_tensor(ec_engine* e, int layer, int tensor, const v
     switch (tensor) {
         case EC_T_ATTN_NORM: return vec(y.attn_norm, e->H);
         case EC_T_FFN_NORM: return vec(y.ffn_norm, e->H);
-        case EC_T_W_IN: EC_TRY(need(gguf_bytes(y.w_in.N, e->H))); return upload_rows(e, y.w_in, 0, host, y.w_in.N);
-        case EC_T_W_OUT: EC_TRY(need(gguf_bytes(e->H, y.w_out.K))); return upload_rows(e, y.w_out, 0, host, e->H);
-        case EC_T_W_GATE: EC_TRY(need(gguf_bytes(e->F, e->H))); return upload_rows(e, y.w_gu, 0, host, e->F);
-        case EC_T_W_UP: EC_TRY(need(gguf_bytes(e->F, e->H))); return upload_rows(e, y.w_gu, e->F, host, e->F);
-        case EC_T_W_DOWN: EC_TRY(need(gguf_bytes(e->H, e->F))); return upload_rows(e, y.w_down, 0, host, e->H);
+        case EC_T_W_IN: EC_TRY(need(gguf_bytes(y.w_in, y.w_in.N))); return upload_rows(e, y.w_in, 0, host, y.w_in.N);
+        case EC_T_W_OUT: EC_TRY(need(gguf_bytes(y.w_out, e->H))); return upload_rows(e, y.w_out, 0, host, e->H);
+        case EC_T_W_GATE: EC_TRY(need(gguf_bytes(y.w_gu, e->F))); return upload_rows(e, y.w_gu, 0, host, e->F);
+        case EC_T_W_UP: EC_TRY(need(gguf_bytes(y.w_gu, e->F))); return upload_rows(e, y.w_gu, e->F, host, e->F);
+        case EC_T_W_DOWN: EC_TRY(need(gguf_bytes(y.w_down, e->H))); return upload_rows(e, y.w_down, 0, host, e->H);
         default: break;
     }
     if (!y.attn) {
@@ -584,10 +715,10 @@ extern "C" int ec_engine_set_tensor(ec_engine* e, int layer, int tensor, const v
 namespace {
 int download_rows(ec_engine* e, const Mat& m, uint32_t row0, void* host, uint32_t N) {
     void* tmp = nullptr;
-    EC_HIP(hipMalloc(&tmp, gguf_bytes(N, m.K)));
-    const uint8_t* src = (const uint8_t*)m.tiled + ec_tiled_bytes(EC_Q8_0, row0, m.K);
-    int rc = ec_unpack_tiled(EC_Q8_0, src, tmp, N, m.K, e->st);
-    if (!rc && hipMemcpyAsync(host, tmp, gguf_bytes(N, m.K), hipMemcpyDeviceToHost, e->st) != hipSuccess)
+    EC_HIP(hipMalloc(&tmp, gguf_bytes(m, N)));
+    const uint8_t* src = (const uint8_t*)m.tiled + ec_tiled_bytes(m.fmt, row0, m.K);
+    int rc = ec_unpack_tiled(m.fmt, src, tmp, N, m.K, e->st);
+    if (!rc && hipMemcpyAsync(host, tmp, gguf_bytes(m, N), hipMemcpyDeviceToHost, e->st) != hipSuccess)
         rc = ec_set_error(EC_ERR_HIP, "download_rows: copy");
     (void)hipStreamSynchronize(e->st);
     (void)hipFree(tmp);
@@ -606,12 +737,12 @@ extern "C" int ec_engine_get_tensor(ec_engine* e, int layer, int tensor, void* h
         return d2h(e, host, src, bytes);
     };
     if (tensor == EC_T_EMBED) {
-        EC_TRY(need(gguf_bytes(c.vocab, e->H)));
+        EC_TRY(need(embed_bytes(e)));
         return d2h(e, host, e->embed, bytes);
     }
     if (tensor == EC_T_FINAL_NORM) return vec(e->final_norm, e->H);
     if (tensor == EC_T_LM_HEAD) {
-        EC_TRY(need(gguf_bytes(c.vocab, e->H)));
+        EC_TRY(need(gguf_bytes(e->lm_head, c.vocab)));
         return download_rows(e, e->lm_head, 0, host, c.vocab);
     }
     if (layer < 0 || (uint32_t)layer >= c.n_layers) return ec_set_error(EC_ERR_ARG, "ec_engine_get_tensor: layer");
@@ -619,11 +750,11 @@ extern "C" int ec_engine_get_tensor(ec_engine* e, int layer, int tensor, void* h
     switch (tensor) {
         case EC_T_ATTN_NORM: return vec(y.attn_norm, e->H);
         case EC_T_FFN_NORM: return vec(y.ffn_norm, e->H);
-        case EC_T_W_IN: EC_TRY(need(gguf_bytes(y.w_in.N, e->H))); return download_rows(e, y.w_in, 0, host, y.w_in.N);
-        case EC_T_W_OUT: EC_TRY(need(gguf_bytes(e->H, y.w_out.K))); return download_rows(e, y.w_out, 0, host, e->H);
-        case EC_T_W_GATE: EC_TRY(need(gguf_bytes(e->F, e->H))); return download_rows(e, y.w_gu, 0, host, e->F);
-        case EC_T_W_UP: EC_TRY(need(gguf_bytes(e->F, e->H))); return download_rows(e, y.w_gu, e->F, host, e->F);
-        case EC_T_W_DOWN: EC_TRY(need(gguf_bytes(e->H, e->F))); return download_rows(e, y.w_down, 0, host, e->H);
+        case EC_T_W_IN: EC_TRY(need(gguf_bytes(y.w_in, y.w_in.N))); return download_rows(e, y.w_in, 0, host, y.w_in.N);
+        case EC_T_W_OUT: EC_TRY(need(gguf_bytes(y.w_out, e->H))); return download_rows(e, y.w_out, 0, host, e->H);
+        case EC_T_W_GATE: EC_TRY(need(gguf_bytes(y.w_gu, e->F))); return download_rows(e, y.w_gu, 0, host, e->F);
+        case EC_T_W_UP: EC_TRY(need(gguf_bytes(y.w_gu, e->F))); return download_rows(e, y.w_gu, e->F, host, e->F);
+        case EC_T_W_DOWN: EC_TRY(need(gguf_bytes(y.w_down, e->H))); return download_rows(e, y.w_down, 0, host, e->H);
         default: break;
     }
     if (!y.attn) {
@@ -673,9 +804,10 @@ extern "C" int ec_engine_init_random(ec_engine* e, uint64_t seed, float w_scale)
     if (!e) return ec_set_error(EC_ERR_ARG, "ec_engine_init_random: null engine");
     const ec_engine_cfg& c = e->c;
     destroy_graph(e);
-    size_t tmp_bytes = gguf_bytes(c.vocab, e->H);
+    if (e->embed_fmt != EC_Q8_0) return ec_set_error(EC_ERR_UNSUPPORTED, "ec_engine_init_random: Q8_0 tensors only");
+    size_t tmp_bytes = gguf_bytes(EC_Q8_0, c.vocab, e->H);
     for (const Layer& y : e->L)
-        tmp_bytes = std::max(tmp_bytes, std::max(gguf_bytes(y.w_in.N, e->H), gguf_bytes(e->F, e->H)));
+        tmp_bytes = std::max(tmp_bytes, std::max(gguf_bytes(EC_Q8_0, y.w_in.N, e->H), gguf_bytes(EC_Q8_0, e->F, e->H)));
     void* tmp = nullptr;
     EC_HIP(hipMalloc(&tmp, tmp_bytes));
     uint64_t stream_id = 0;
@@ -799,7 +931,13 @@ extern "C" int ec_engine_get_logits(ec_engine* e, float* host, uint32_t seq) {
 
 extern "C" void* ec_engine_stream(ec_engine* e) { return e ? (void*)e->st : nullptr; }
 
-extern "C" size_t ec_engine_weight_bytes(const ec_engine* e) { return e ? e->weight_bytes : 0; }
+extern "C" size_t ec_engine_weight_bytes(const ec_engine* e) {
+    if (!e) return 0;
+    size_t wb = e->weight_bytes + ec_tiled_bytes(e->lm_head.fmt, e->lm_head.N, e->lm_head.K);
+    for (const Layer& y : e->L)
+        for (const Mat* m : {&y.w_in, &y.w_out, &y.w_gu, &y.w_down}) wb += ec_tiled_bytes(m->fmt, m->N, m->K);
+    return wb;
+}
 
 // ------------------------------------------------------------ chunked prefill
 namespace {
@@ -809,6 +947,11 @@ int prefill_alloc(ec_engine* e, Lane& L, uint32_t i) {
     if (L.ready) return EC_OK;
     const size_t C = ec_engine::kPrefillChunk;
     const size_t wide = std::max({(size_t)e->H, (size_t)e->F, (size_t)e->value_dim, (size_t)e->q_dim});
+    // token activations of either matrix format (Q4_K for K % 256 == 0)
+    const size_t act_rows_bytes = std::max(ec_gemm_act_bytes(EC_Q8_0, (uint32_t)C, (uint32_t)wide),
+                                           ec_gemm_act_bytes(EC_Q4_K, (uint32_t)C, (uint32_t)(wide / 256 * 256)));
+    const size_t act1_bytes =
+        std::max(ec_act_bytes(EC_Q8_0, 1, e->H), e->H % 256 ? (size_t)0 : ec_act_bytes(EC_Q4_K, 1, e->H));
     int rc;
     if (i == 0) {
         L.st = e->st;
@@ -817,8 +960,7 @@ int prefill_alloc(ec_engine* e, Lane& L, uint32_t i) {
     }
     if ((rc = dalloc(e, &L.x, C * e->H)) || (rc = dalloc(e, &L.n, C * wide)) ||
         (rc = dalloc(e, &L.proj, C * e->nin_max)) || (rc = dalloc(e, &L.gu, C * 2 * (size_t)e->F)) ||
-        (rc = dalloc(e, &L.act, ec_gemm_act_bytes(EC_Q8_0, (uint32_t)C, (uint32_t)wide))) ||
-        (rc = dalloc(e, &L.act1, ec_act_bytes(EC_Q8_0, 1, e->H))) || (rc = dalloc(e, &L.tok, C)) ||
+        (rc = dalloc(e, &L.act, act_rows_bytes)) || (rc = dalloc(e, &L.act1, act1_bytes)) || (rc = dalloc(e, &L.tok, C)) ||
         (rc = dalloc(e, &L.pos, C)) || (rc = dalloc(e, &L.ctx, C)))
         return rc;
     if (e->value_dim &&
@@ -835,10 +977,11 @@ int prefill_alloc(ec_engine* e, Lane& L, uint32_t i) {
     return EC_OK;
 }
 
-// y[T][N] (+)= act(x rows) . W  on int8 MFMA (x fp32 [T][K] quantized per 32-block)
+// y[T][N] (+)= act(x rows) . W  on int8 MFMA (x fp32 [T][K] quantized per
+// 32-element block in the matrix's activation format)
 int gemm_rows(Lane& L, const Mat& m, const float* x, float* y, uint32_t T, uint32_t ldy, int acc) {
-    EC_TRY(ec_gemm_quantize_act(EC_Q8_0, x, L.act, T, m.K, L.st));
-    return ec_gemm(EC_Q8_0, m.tiled, L.act, y, T, m.N, m.K, ldy, acc, L.st);
+    EC_TRY(ec_gemm_quantize_act(m.fmt, x, L.act, T, m.K, L.st));
+    return ec_gemm(m.fmt, m.tiled, L.act, y, T, m.N, m.K, ldy, acc, L.st);
 }
 
 // One chunk of T tokens of sequence s at positions p .. p+T-1 through every
@@ -847,7 +990,7 @@ int prefill_chunk(ec_engine* e, Lane& L, uint32_t s, uint32_t T, uint32_t p) {
     const ec_engine_cfg& c = e->c;
     const uint32_t H = e->H, F = e->F;
     hipStream_t st = L.st;
-    EC_TRY(ec_glue_embed(e->embed, L.tok, L.x, T, H, c.vocab, st));
+    EC_TRY(ec_glue_embed_fmt(e->embed_fmt, e->embed, L.tok, L.x, T, H, c.vocab, st));
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         Layer& y = e->L[l];
         EC_TRY(ec_glue_rmsnorm_rows(L.x, y.attn_norm, L.n, T, H, st));
@@ -910,9 +1053,15 @@ int prefill_step(ec_engine* e, Lane& L, PrefillJob& j) {
     if (j.done < j.n) return EC_OK;
     // the last token's logits and greedy next token; pos[seq] = pos0 + n
     const int32_t last = j.pos0 + (int32_t)j.n - 1;
-    EC_TRY(ec_glue_rmsnorm_quant(L.x + (size_t)(T - 1) * e->H, e->final_norm, L.act1, 1, e->H, L.st));
-    EC_TRY(ec_matvec(EC_Q8_0, e->lm_head.tiled, L.act1, e->logits + (size_t)j.seq * e->c.vocab, 1, e->c.vocab, e->H,
-                     e->c.vocab, 0, L.st));
+    const float* xl = L.x + (size_t)(T - 1) * e->H;
+    if (e->lm_head.fmt == EC_Q4_K) {
+        EC_TRY(ec_glue_rmsnorm_rows(xl, e->final_norm, L.n, 1, e->H, L.st));
+        EC_TRY(ec_quantize_act(EC_Q4_K, L.n, L.act1, 1, e->H, L.st));
+    } else {
+        EC_TRY(ec_glue_rmsnorm_quant(xl, e->final_norm, L.act1, 1, e->H, L.st));
+    }
+    EC_TRY(ec_matvec(e->lm_head.fmt, e->lm_head.tiled, L.act1, e->logits + (size_t)j.seq * e->c.vocab, 1, e->c.vocab,
+                     e->H, e->c.vocab, 0, L.st));
     EC_HIP(hipMemcpyAsync(e->pos + j.seq, &last, 4, hipMemcpyHostToDevice, L.st));
     EC_TRY(ec_glue_argmax_advance(e->logits + (size_t)j.seq * e->c.vocab, e->c.vocab, e->gen + j.seq,
                                   e->tok + j.seq, e->pos + j.seq, 1, e->c.max_ctx, L.st));
@@ -1063,6 +1212,15 @@ extern "C" int ec_engine_buffer(ec_engine* e, int which, void** dev, size_t* byt
         case EC_B_GEN: p = e->gen, n = B * 4; break;
         case EC_B_CTX: p = e->ctx, n = B * 4; break;
         case EC_B_INV_FREQ: p = e->inv_freq, n = (size_t)c.head_dim / 2 * 4; break;
+        case EC_B_HN: p = e->hn, n = e->hn ? B * e->H * 4 : 0; break;
+        case EC_B_CORE: p = e->core_f, n = e->core_f ? B * e->value_dim * 4 : 0; break;
+        case EC_B_FF: p = e->ff, n = e->ff ? B * e->F * 4 : 0; break;
+        case EC_B_ACT4_H: p = e->act4_h, n = e->q4 ? ec_act_bytes(EC_Q4_K, e->B, e->H) : 0; break;
+        case EC_B_ACT4_V:
+            p = e->act4_v, n = e->q4 && e->value_dim % 256 == 0 ? ec_act_bytes(EC_Q4_K, e->B, e->value_dim) : 0;
+            break;
+        case EC_B_ACT4_Q: p = e->act4_q, n = e->q4 ? ec_act_bytes(EC_Q4_K, e->B, e->q_dim) : 0; break;
+        case EC_B_ACT4_F: p = e->act4_f, n = e->q4 && e->F % 256 == 0 ? ec_act_bytes(EC_Q4_K, e->B, e->F) : 0; break;
         default: return ec_set_error(EC_ERR_ARG, "ec_engine_buffer: unknown buffer id");
     }
     *dev = p;

@@ -7,7 +7,7 @@
  * (echo-core-zig/src/ports/inference.zig:135-140), otherwise a gated-delta-net
  * ("qwen_linear") block (echo-core-zig/src/kernels/qwen_linear.zig:103-271);
  * each block is followed by a SwiGLU FFN; RMSNorm before every sub-block,
- * greedy argmax at the end.  All matrices are GGUF Q8_0.
+ * greedy argmax at the end.  Matrices are GGUF Q8_0 or Q4_K (per tensor).
  *
  * The engine decodes a batch of up to max_batch sequences per step, each at
  * its own position (ragged).  Inputs of a step are, per sequence, a token and
@@ -52,12 +52,13 @@ typedef struct {
     float rope_base;
 } ec_engine_cfg;
 
-/* Tensor ids for ec_engine_set_tensor.  Matrices are GGUF Q8_0 bytes, rows x
- * (K/32*34); vectors are fp32.  Per-layer tensors: */
+/* Tensor ids for ec_engine_set_tensor.  Matrices are GGUF bytes of their
+ * format (ec_engine_set_format; Q8_0 by default): rows x (K/32*34) for Q8_0,
+ * rows x (K/256*144) for Q4_K; vectors are fp32.  Per-layer tensors: */
 enum ec_tensor {
-    EC_T_EMBED = 0,      /* [vocab x hidden] Q8_0 (global) */
+    EC_T_EMBED = 0,      /* [vocab x hidden] Q8_0 blocks, F16 or F32 rows (global) */
     EC_T_FINAL_NORM = 1, /* [hidden] (global) */
-    EC_T_LM_HEAD = 2,    /* [vocab x hidden] Q8_0 (global) */
+    EC_T_LM_HEAD = 2,    /* [vocab x hidden] (global) */
     EC_T_ATTN_NORM = 10, /* [hidden] */
     EC_T_FFN_NORM = 11,  /* [hidden] */
     EC_T_W_IN = 12,      /* delta: rows qkv(conv_dim) | z(ssm_inner) | alpha(ssm_heads) | beta(ssm_heads);
@@ -75,13 +76,21 @@ enum ec_tensor {
 };
 
 int ec_engine_create(const ec_engine_cfg* cfg, ec_engine** out);
+/* Storage format of a matrix, chosen per tensor as the reference's matvec_d
+ * dispatch does (src/inference.cpp:526-545): EC_Q8_0 (default) or EC_Q4_K
+ * (K % 256 == 0) for EC_T_W_IN, EC_T_W_OUT, EC_T_W_GATE / EC_T_W_UP (one format
+ * for both: they are stored as one matrix), EC_T_W_DOWN and EC_T_LM_HEAD;
+ * EC_Q8_0, EC_F16 or EC_F32 rows for EC_T_EMBED.  Reallocates the tensor (its
+ * contents are undefined until set) and drops the captured step graph. */
+int ec_engine_set_format(ec_engine* e, int layer, int tensor, int fmt);
+int ec_engine_get_format(const ec_engine* e, int layer, int tensor);
 /* The configuration the engine was created with. */
 int ec_engine_get_config(const ec_engine* e, ec_engine_cfg* out);
 void ec_engine_destroy(ec_engine* e);
 /* Copy one tensor from host memory (layer ignored for global tensors). */
 int ec_engine_set_tensor(ec_engine* e, int layer, int tensor, const void* host, size_t bytes);
 /* Copy one tensor back to host memory in the set_tensor format (matrices as
- * GGUF Q8_0 bytes; EC_T_W_GATE / EC_T_W_UP each return their half). */
+ * GGUF bytes of their format; EC_T_W_GATE / EC_T_W_UP each return their half). */
 int ec_engine_get_tensor(ec_engine* e, int layer, int tensor, void* host, size_t bytes);
 
 /* Recurrent and cached state of one sequence after the last completed step
@@ -158,18 +167,23 @@ enum {
     EC_OP_MV_OUT = 4,      /* ACT_V or ACT_Q -> PARTS [nparts][B][H] */
     EC_OP_ROPE_APPEND = 5, /* PROJ -> KV row at pos, Q_PACKED + Q_SCALES (or QBUF), CTX */
     EC_OP_ATTN = 6,        /* Q_PACKED (or QBUF), KV cache, CTX -> ATTN_OUT (and ACT_Q when packed) */
-    EC_OP_QUANT_ATTN = 7,  /* ATTN_OUT -> ACT_Q (unpacked attention only) */
+    EC_OP_QUANT_ACT = 7,   /* fp32 rows (buffer x_in) -> activation (buffer x_out): ATTN_OUT -> ACT_Q (fp32
+                              attention), and the inputs of Q4_K matrices (HN, CORE, ATTN_OUT, FF -> ACT4_*) */
     EC_OP_MV_GU = 8,       /* ACT_H -> GU [nparts][B][2F] (gate rows, then up rows) */
-    EC_OP_SWIGLU = 9,      /* GU -> ACT_F */
+    EC_OP_SWIGLU = 9,      /* GU -> ACT_F, or fp32 FF rows (x_out says which) */
     EC_OP_MV_DOWN = 10,    /* ACT_F -> PARTS [nparts][B][H] */
     EC_OP_LM_HEAD = 11,    /* ACT_H -> LOGITS */
     EC_OP_ARGMAX = 12,     /* LOGITS, POS -> GEN, TOK, POS */
+    EC_OP_NORM_ROWS = 13,  /* x_in -> HN: the fp32 RMSNorm rows a Q4_K consumer quantizes */
 };
 typedef struct {
     int op, layer;   /* layer -1: embedding, final norm, head, argmax */
     int phase;       /* 0: before the launch, 1: after it completed */
     int nparts;      /* partial sums the op writes (MV_*) or reads (NORM, DELTA_STEP, ROPE_APPEND, SWIGLU) */
-    int x_in, x_out; /* residual buffers (EC_B_X / EC_B_X2) an EMBED / NORM reads and writes, else -1 */
+    int x_in, x_out; /* EMBED / NORM / NORM_ROWS: the residual buffers (EC_B_X / EC_B_X2) read and written;
+                        MV_*: x_in = the activation buffer read; QUANT_ACT: source and destination buffers;
+                        DELTA_STEP / SWIGLU / ATTN: x_out = the output buffer (ACT_V or CORE, ACT_F or FF,
+                        ACT_Q or -1); else -1 */
 } ec_trace_event;
 typedef void (*ec_trace_fn)(void* user, const ec_trace_event* ev);
 int ec_engine_step_traced(ec_engine* e, ec_trace_fn cb, void* user);
@@ -180,6 +194,9 @@ enum {
     EC_B_X = 0, EC_B_X2 = 1, EC_B_PARTS = 2, EC_B_PROJ = 3, EC_B_GU = 4, EC_B_ACT_H = 5, EC_B_ACT_V = 6,
     EC_B_ACT_F = 7, EC_B_ACT_Q = 8, EC_B_ATTN_OUT = 9, EC_B_Q_PACKED = 10, EC_B_Q_SCALES = 11, EC_B_QBUF = 12,
     EC_B_LOGITS = 13, EC_B_TOK = 14, EC_B_POS = 15, EC_B_GEN = 16, EC_B_CTX = 17, EC_B_INV_FREQ = 18,
+    /* inputs of Q4_K matrices (present once a matrix is Q4_K): fp32 rows and their Q4_K activations */
+    EC_B_HN = 19, EC_B_CORE = 20, EC_B_FF = 21, EC_B_ACT4_H = 22, EC_B_ACT4_V = 23, EC_B_ACT4_Q = 24,
+    EC_B_ACT4_F = 25,
 };
 int ec_engine_buffer(ec_engine* e, int which, void** dev, size_t* bytes);
 

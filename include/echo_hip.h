@@ -61,7 +61,7 @@ int ec_quantize_rows(const float* x, int8_t* q, float* scales, uint32_t rows, ui
  * gguf: N rows of K/32*34 (Q8_0) or K/256*144 (Q4_K) bytes. */
 size_t ec_tiled_bytes(int fmt, uint32_t N, uint32_t K);
 int ec_repack(int fmt, const void* gguf, void* tiled, uint32_t N, uint32_t K, void* stream);
-/* Inverse of ec_repack (Q8_0): tiled -> GGUF rows. */
+/* Inverse of ec_repack (Q8_0 or Q4_K): tiled -> GGUF rows. */
 int ec_unpack_tiled(int fmt, const void* tiled, void* gguf, uint32_t N, uint32_t K, void* stream);
 
 /* --------------------------------------------------- activation quantization
@@ -191,6 +191,12 @@ int ec_deltanet(float* state, const float* q, const float* k, const float* v, co
 int ec_delta_step(const float* proj, uint32_t Nin, float* conv_state, const float* conv_w, const float* a_log,
                   const float* dt_bias, const float* norm_w, float* state, void* act, const int32_t* pos,
                   uint32_t n_seq, uint32_t n_k, uint32_t n_v, uint32_t kern, void* stream);
+/* ec_delta_step_split writing the gated-norm output as fp32 out[n_seq][n_v*128]
+ * (when out != NULL) and/or quantized into act (when act != NULL). */
+int ec_delta_step_out(const float* proj, uint32_t nparts, uint32_t Nin, float* conv_state, const float* conv_w,
+                      const float* a_log, const float* dt_bias, const float* norm_w, float* state, void* act,
+                      float* out, const int32_t* pos, uint32_t n_seq, uint32_t n_k, uint32_t n_v, uint32_t kern,
+                      void* stream);
 /* seq_pos (may be NULL): sequence s is skipped entirely (state untouched, no
  * output written) when seq_pos[s] < 0. */
 /* ec_delta_step with the input projection given as nparts (1..8) partial sums
@@ -204,6 +210,10 @@ int ec_delta_step_split(const float* proj, uint32_t nparts, uint32_t Nin, float*
  * "_quant" op writes the Q8_0 activation layout consumed by ec_matvec. */
 int ec_glue_embed(const void* emb, const int32_t* tok, float* x, uint32_t n_seq, uint32_t H, uint32_t vocab,
                   void* stream);
+/* Embedding rows of a Q8_0 (GGUF blocks), F16 or F32 table [vocab][H]
+ * (echo-core-zig/src/inference/engine.zig:30-54). */
+int ec_glue_embed_fmt(int fmt, const void* emb, const int32_t* tok, float* x, uint32_t n_seq, uint32_t H,
+                      uint32_t vocab, void* stream);
 int ec_glue_rmsnorm_quant(const float* x, const float* w, void* act, uint32_t M, uint32_t H, void* stream);
 /* x_out = x + parts[0] + ... + parts[nparts-1] (added in that order; parts is
  * [nparts][M][H], the output of ec_matvec_split), then RMSNorm + quantize of

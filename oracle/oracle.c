@@ -468,6 +468,17 @@ void oc_embed_row_q8_0(const uint8_t* embed, uint32_t H, uint32_t token, float* 
     }
 }
 
+void oc_embed_row(int fmt, const void* embed, uint32_t H, uint32_t token, float* x) {
+    if (fmt == OC_F16) {
+        const uint8_t* row = (const uint8_t*)embed + (size_t)token * H * 2;
+        for (uint32_t i = 0; i < H; ++i) x[i] = oc_fp16_to_fp32(rd16(row + 2 * i));
+    } else if (fmt == OC_F32) {
+        memcpy(x, (const float*)embed + (size_t)token * H, H * sizeof(float));
+    } else {
+        oc_embed_row_q8_0((const uint8_t*)embed, H, token, x);
+    }
+}
+
 /* echo-core-zig/src/kernels/qwen_linear.zig:215-219 (per value head h):
  * beta = 1/(1+exp(-b)), g = -exp(A_log)*softplus(alpha + dt_bias), decay = exp(g). */
 void oc_deltanet_gates(const float* alpha, const float* beta_logit, const float* a_log, const float* dt_bias,
@@ -543,10 +554,20 @@ static void mv_free(mv_scratch* m) { free(m->deq); free(m->qq); free(m->qq1); fr
 
 /* Matvec with optional activation quantization: y = W * x (y zeroed first).
  * quant_act 0: fp32 x (reference); 1: x quantized per 32-block; 2: x as two
- * int8 pieces per 32-block (oc_quantize_act2_q8_0). */
-static void mv(const uint8_t* W, const float* x, float* y, uint32_t M, uint32_t K, int quant_act, mv_scratch* s) {
+ * int8 pieces per 32-block (oc_quantize_act2_q8_0).  A Q4_K matrix quantizes
+ * its input per 32-element sub-block (oc_quantize_act_q4_K) for 1 and 2. */
+static void mv_fmt(int fmt, const uint8_t* W, const float* x, float* y, uint32_t M, uint32_t K, int quant_act,
+                   mv_scratch* s) {
     memset(y, 0, sizeof(float) * M);
-    if (quant_act == 2) {
+    if (fmt == OC_Q4_K) {
+        if (quant_act) {
+            oc_quantize_act_q4_K(x, s->qq, s->qd, NULL, K);
+            oc_dequant_act_q4_K(s->qq, s->qd, s->deq, K);
+            oc_matvec_q4_K(W, s->deq, y, M, K);
+        } else {
+            oc_matvec_q4_K(W, x, y, M, K);
+        }
+    } else if (quant_act == 2) {
         oc_quantize_act2_q8_0(x, s->qq, s->qq1, s->qd, K);
         oc_dequant_act2_q8_0(s->qq, s->qq1, s->qd, s->deq, K);
         OC_MV_IMPL(W, s->deq, y, M, K);
@@ -559,11 +580,25 @@ static void mv(const uint8_t* W, const float* x, float* y, uint32_t M, uint32_t 
     }
 }
 
+static void mv(const uint8_t* W, const float* x, float* y, uint32_t M, uint32_t K, int quant_act, mv_scratch* s) {
+    mv_fmt(OC_Q8_0, W, x, y, M, K, quant_act, s);
+}
+
 void oc_matvec_act_q8_0(const void* W, const float* x, float* y, uint32_t M, uint32_t K, int quant_act) {
     mv_scratch s = mv_alloc(K);
     mv((const uint8_t*)W, x, y, M, K, quant_act, &s);
     mv_free(&s);
 }
+
+void oc_matvec_act(int fmt, const void* W, const float* x, float* y, uint32_t M, uint32_t K, int quant_act) {
+    mv_scratch s = mv_alloc(K);
+    mv_fmt(fmt, (const uint8_t*)W, x, y, M, K, quant_act, &s);
+    mv_free(&s);
+}
+
+/* Format of matrix `which` (0 w_qkv|w_z|w_ab, 1 w_out, 2 w_gate|w_up, 3
+ * w_down) of layer l; l == n_layers: 0 lm_head, 1 the embedding. */
+static int fmt_of(const oc_model_w* w, uint32_t l, int which) { return w->fmt ? w->fmt[4 * l + which] : OC_Q8_0; }
 
 static int is_attn_layer(const oc_model_cfg* c, uint32_t l) {
     return c->attn_interval != 0 && ((l + 1) % c->attn_interval) == 0;
@@ -589,16 +624,17 @@ void oc_deltanet_block(const oc_model_cfg* c, const oc_model_w* w, uint32_t l, f
     float* ab = (float*)calloc(2 * d.n_v, sizeof(float));
     float* dec = (float*)calloc(d.n_v, sizeof(float));
     float* bet = (float*)calloc(d.n_v, sizeof(float));
-    mv(w->w_qkv[l], in, a, d.conv_dim, d.H, quant_act, &s);
-    mv(w->w_z[l], in, z, d.value_dim, d.H, quant_act, &s);
-    mv(w->w_ab[l], in, ab, 2 * d.n_v, d.H, quant_act, &s);
+    const int fin = fmt_of(w, l, 0), fo = fmt_of(w, l, 1);
+    mv_fmt(fin, w->w_qkv[l], in, a, d.conv_dim, d.H, quant_act, &s);
+    mv_fmt(fin, w->w_z[l], in, z, d.value_dim, d.H, quant_act, &s);
+    mv_fmt(fin, w->w_ab[l], in, ab, 2 * d.n_v, d.H, quant_act, &s);
     oc_conv_step(conv_state, a, w->conv_w[l], b, d.conv_dim, c->conv_kernel);
     oc_l2norm_heads(b, d.n_k, d.d_k);
     oc_l2norm_heads(b + d.key_dim, d.n_k, d.d_k);
     oc_deltanet_gates(ab, ab + d.n_v, w->a_log[l], w->dt_bias[l], dec, bet, d.n_v);
     oc_deltanet_step(ssm_state, b, b + d.key_dim, b + 2 * d.key_dim, dec, bet, core, d.n_v, d.n_k, d.d_k, d.d_v);
     oc_gated_rmsnorm(core, z, w->ssm_norm[l], d.n_v, d.d_v);
-    mv(w->w_out[l], core, out, d.H, d.value_dim, quant_act, &s);
+    mv_fmt(fo, w->w_out[l], core, out, d.H, d.value_dim, quant_act, &s);
     free(a); free(b); free(z); free(core); free(ab); free(dec); free(bet);
     mv_free(&s);
 }
@@ -617,7 +653,7 @@ void oc_attention_block(const oc_model_cfg* c, const oc_model_w* w, uint32_t l, 
     float* core = (float*)calloc(d.q_dim, sizeof(float));
     float* inv_freq = (float*)calloc(c->head_dim / 2 + 1, sizeof(float));
     oc_rope_inv_freq(inv_freq, c->head_dim, c->rope_base);
-    mv(w->w_qkv[l], in, a, d.q_dim + 2 * d.kv_dim, d.H, quant_act, &s);
+    mv_fmt(fmt_of(w, l, 0), w->w_qkv[l], in, a, d.q_dim + 2 * d.kv_dim, d.H, quant_act, &s);
     float* q = a;
     float* k = a + d.q_dim;
     float* v = a + d.q_dim + d.kv_dim;
@@ -627,7 +663,7 @@ void oc_attention_block(const oc_model_cfg* c, const oc_model_w* w, uint32_t l, 
     oc_rope(k, c->n_kv, c->head_dim, pos, inv_freq);
     oc_kv_append(k, v, keys, vals, kscales, vscales, pos, c->n_kv, c->head_dim);
     oc_attn_decode_int8(q, keys, vals, kscales, vscales, core, c->n_heads, c->n_kv, c->head_dim, pos + 1);
-    mv(w->w_out[l], core, out, d.H, d.q_dim, quant_act, &s);
+    mv_fmt(fmt_of(w, l, 1), w->w_out[l], core, out, d.H, d.q_dim, quant_act, &s);
     free(a); free(core); free(inv_freq);
     mv_free(&s);
 }
@@ -645,10 +681,11 @@ void oc_ffn_block(const oc_model_cfg* c, const oc_model_w* w, uint32_t l, const 
     mv_scratch s = mv_alloc(d.maxK);
     float* g = (float*)calloc(c->ffn, sizeof(float));
     float* u = (float*)calloc(c->ffn, sizeof(float));
-    mv(w->w_gate[l], in, g, c->ffn, d.H, quant_act, &s);
-    mv(w->w_up[l], in, u, c->ffn, d.H, quant_act, &s);
+    const int fgu = fmt_of(w, l, 2);
+    mv_fmt(fgu, w->w_gate[l], in, g, c->ffn, d.H, quant_act, &s);
+    mv_fmt(fgu, w->w_up[l], in, u, c->ffn, d.H, quant_act, &s);
     oc_swiglu(g, u, g, c->ffn);
-    mv(w->w_down[l], g, out, d.H, c->ffn, quant_act, &s);
+    mv_fmt(fmt_of(w, l, 3), w->w_down[l], g, out, d.H, c->ffn, quant_act, &s);
     free(g); free(u);
     mv_free(&s);
 }
@@ -665,7 +702,7 @@ void oc_decoder_token(const oc_model_cfg* c, const oc_model_w* w, oc_seq_state* 
     float* hbuf = (float*)calloc(H, sizeof(float));
     float* tmp = (float*)calloc(H, sizeof(float));
     mv_scratch s = mv_alloc(d.maxK);
-    oc_embed_row_q8_0(w->embed, H, token, x);
+    oc_embed_row(fmt_of(w, c->n_layers, 1), w->embed, H, token, x);
     for (uint32_t l = 0; l < c->n_layers; ++l) {
         oc_rmsnorm(x, w->attn_norm[l], hbuf, H);
         if (!is_attn_layer(c, l))
@@ -679,7 +716,7 @@ void oc_decoder_token(const oc_model_cfg* c, const oc_model_w* w, oc_seq_state* 
         for (uint32_t i = 0; i < H; ++i) x[i] = x[i] + tmp[i];
     }
     oc_rmsnorm(x, w->final_norm, hbuf, H);
-    mv(w->lm_head, hbuf, logits, c->vocab, H, quant_act, &s);
+    mv_fmt(fmt_of(w, c->n_layers, 0), w->lm_head, hbuf, logits, c->vocab, H, quant_act, &s);
     st->pos += 1;
     free(x); free(hbuf); free(tmp);
     mv_free(&s);

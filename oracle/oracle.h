@@ -170,10 +170,18 @@ typedef struct {
     const float** ssm_norm;  /* delta: [head_v_dim] */
     const float** q_norm;    /* attn: [head_dim] */
     const float** k_norm;    /* attn: [head_dim] */
-    const uint8_t* embed;    /* [vocab x hidden] Q8_0 */
+    const uint8_t* embed;    /* [vocab x hidden] Q8_0 (or per fmt) */
     const float* final_norm; /* [hidden] */
-    const uint8_t* lm_head;  /* [vocab x hidden] Q8_0 */
+    const uint8_t* lm_head;  /* [vocab x hidden] Q8_0 (or per fmt) */
+    /* Storage formats, chosen per tensor as src/inference.cpp:526-545
+     * dispatches them: NULL = every matrix and the embedding Q8_0; else
+     * [n_layers][4] (w_qkv|w_z|w_ab as one fused matrix, w_out, w_gate|w_up,
+     * w_down) in {OC_Q8_0, OC_Q4_K}, then lm_head, then the embedding in
+     * {OC_Q8_0, OC_F16, OC_F32}. */
+    const int32_t* fmt;
 } oc_model_w;
+
+enum { OC_F32 = 0, OC_F16 = 1, OC_Q8_0 = 6, OC_Q4_K = 10 };
 
 typedef struct {
     /* per layer pointers; NULL for layers of the other type */
@@ -188,6 +196,8 @@ typedef struct {
 
 /* Q8_0 embedding row (engine.zig:41-50). */
 void oc_embed_row_q8_0(const uint8_t* embed, uint32_t H, uint32_t token, float* x);
+/* Embedding row of a table in format fmt (OC_Q8_0, OC_F16 or OC_F32 rows). */
+void oc_embed_row(int fmt, const void* embed, uint32_t H, uint32_t token, float* x);
 /* Delta-net gates (qwen_linear.zig:215-219) per value head:
  * beta = sigmoid(beta_logit), decay = exp(-exp(a_log) * softplus(alpha + dt_bias)). */
 void oc_deltanet_gates(const float* alpha, const float* beta_logit, const float* a_log, const float* dt_bias,
@@ -197,6 +207,10 @@ void oc_deltanet_gates(const float* alpha, const float* beta_logit, const float*
 void oc_gated_rmsnorm(float* core, const float* z, const float* w, uint32_t n_v, uint32_t d_v);
 /* y = W x (y zeroed), x first quantized per 32-block when quant_act != 0. */
 void oc_matvec_act_q8_0(const void* W, const float* x, float* y, uint32_t M, uint32_t K, int quant_act);
+/* The same for a matrix of format fmt (OC_Q8_0 or OC_Q4_K; a Q4_K input is
+ * quantized per 32-element sub-block, oc_quantize_act_q4_K; quant_act 2
+ * applies to Q8_0 only and quantizes a Q4_K input as 1 does). */
+void oc_matvec_act(int fmt, const void* W, const float* x, float* y, uint32_t M, uint32_t K, int quant_act);
 /* qwen_linear.forward of block l (qwen_linear.zig:103-271): in = the block's
  * normed input [hidden], out = its output [hidden] (before the residual). */
 void oc_deltanet_block(const oc_model_cfg* c, const oc_model_w* w, uint32_t l, float* conv_state, float* ssm_state,

@@ -74,6 +74,8 @@ class Oracle:
         L.oc_deltanet_gates.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _u32]
         L.oc_gated_rmsnorm.argtypes = [_f32p, _f32p, _f32p, _u32, _u32]
         L.oc_matvec_act_q8_0.argtypes = [_u8p, _f32p, _f32p, _u32, _u32, C.c_int]
+        L.oc_matvec_act.argtypes = [C.c_int, _u8p, _f32p, _f32p, _u32, _u32, C.c_int]
+        L.oc_embed_row.argtypes = [C.c_int, C.c_void_p, _u32, _u32, _f32p]
         L.oc_swiglu.argtypes = [_f32p, _f32p, _f32p, _u32]
 
     def swiglu(self, gate, up):
@@ -92,6 +94,21 @@ class Oracle:
         out = np.zeros(H, np.float32)
         self.lib.oc_embed_row_q8_0(np.ascontiguousarray(embed).reshape(-1), H, int(tok), out)
         return out
+
+    def embed_row(self, fmt, embed, H, tok):
+        """Row `tok` of an embedding table of format fmt (6 Q8_0 blocks, 1 F16, 0 F32 rows)."""
+        e = np.ascontiguousarray(embed).reshape(-1)
+        out = np.zeros(H, np.float32)
+        self.lib.oc_embed_row(int(fmt), e.ctypes.data, H, int(tok), out)
+        return out
+
+    def matvec_act(self, fmt, W, x, quant_act=True):
+        """y = W x for a GGUF matrix of format fmt (6 Q8_0, 10 Q4_K), x quantized first when quant_act."""
+        M = W.shape[0]
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        y = np.zeros(M, np.float32)
+        self.lib.oc_matvec_act(int(fmt), np.ascontiguousarray(W).reshape(-1), x, y, M, x.size, int(quant_act))
+        return y
 
     def conv_step(self, state, x, w, C_, kernel):
         """Advances state ([kernel][C] newest first) in place; returns silu(conv)."""
@@ -296,7 +313,7 @@ _PP = C.POINTER(C.c_void_p)
 class _OcW(C.Structure):
     _fields_ = [(n, _PP) for n in ("w_qkv", "w_z", "w_ab", "w_out", "w_gate", "w_up", "w_down", "attn_norm",
                                    "ffn_norm", "conv_w", "a_log", "dt_bias", "ssm_norm", "q_norm", "k_norm")] + \
-               [("embed", C.c_void_p), ("final_norm", C.c_void_p), ("lm_head", C.c_void_p)]
+               [("embed", C.c_void_p), ("final_norm", C.c_void_p), ("lm_head", C.c_void_p), ("fmt", C.c_void_p)]
 
 
 class _OcSeq(C.Structure):
@@ -307,8 +324,9 @@ class _OcSeq(C.Structure):
 class Decoder:
     """n_seq independent sequences decoded token by token by oc_decoder_token
     (oracle.c).  `cfg` is an echohip.engine.EngineConfig-like object and `m`
-    the weight dict of tests/decoder_util.make_model (GGUF Q8_0 matrices,
-    fp32 vectors, the fused w_in rows of the engine)."""
+    the weight dict of tests/decoder_util.make_model (GGUF matrices, Q8_0
+    unless m["fmt"] maps (layer, name) to another format -- layer -1 for
+    "lm_head" and "embed" -- fp32 vectors, the fused w_in rows of the engine)."""
 
     def __init__(self, oc, cfg: EngineConfig, m, n_seq, quant_act=True):
         self.oc, self.cfg, self.quant_act = oc, cfg, int(quant_act)
@@ -332,10 +350,17 @@ class Decoder:
             return x.ctypes.data
 
         H = cfg.hidden
-        rowb = H // 32 * 34
+        fm = m.get("fmt", {})
         lay = m["layers"]
+        fmt = np.full(4 * L + 2, 6, np.int32)
+        for l in range(L):
+            fmt[4 * l:4 * l + 4] = [fm.get((l, n), 6) for n in ("w_in", "w_out", "w_gate", "w_down")]
+            assert fm.get((l, "w_up"), 6) == fmt[4 * l + 2], "gate and up share one format"
+        fmt[4 * L] = fm.get((-1, "lm_head"), 6)
+        fmt[4 * L + 1] = fm.get((-1, "embed"), 6)
         w = {k: [] for k, _ in _OcW._fields_[:15]}
-        for y in lay:
+        for l, y in enumerate(lay):
+            rowb = H // 32 * 34 if fmt[4 * l] == 6 else H // 256 * 144
             w["w_qkv"].append(p(y["w_in"]))
             base = y["w_in"].reshape(-1)
             if y["attn"]:
@@ -348,7 +373,7 @@ class Decoder:
                       "ssm_norm", "q_norm", "k_norm"):
                 w[k].append(p(y.get(k)))
         self.w = _OcW(**{k: arr(v) for k, v in w.items()}, embed=p(m["embed"]), final_norm=p(m["final_norm"]),
-                      lm_head=p(m["lm_head"]))
+                      lm_head=p(m["lm_head"]), fmt=p(fmt) if fm else None)
         self.seqs, self.states = [], []
         kvd = cfg.n_kv * cfg.head_dim
         for _ in range(n_seq):

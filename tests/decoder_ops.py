@@ -18,6 +18,12 @@ comparison measures that one operation:
                          fp32 values may round to neighbours), such flips at
                          most MAX_FLIP_FRACTION of the elements.
 
+A quantization launch of the GPU's own fp32 rows (QUANT_ACT) is compared bit
+for bit with the reference quantizer.  Matrices stored as Q4_K read a Q4_K
+activation (per 32-element sub-block, in the quantizer's sub-block order) and
+are checked against the oracle's Q4_K matvec; their producers write fp32 rows
+(NORM_ROWS, the delta step's fp32 output, SwiGLU rows), checked within FP_TOL.
+
 Matrices are compared on a subset of rows when `rows_per_matrix` is set (the
 4B-shape run); every row otherwise.
 """
@@ -42,6 +48,7 @@ def rel_l2(a, b):
 
 class OpChecker:
     def __init__(self, oc, eng, cfg, m, rows_per_matrix=None, seed=0):
+        self.fmts = m.get("fmt", {})
         self.oc, self.eng, self.cfg, self.m = oc, eng, cfg, m
         self.B = cfg.max_batch
         self.H, self.F = cfg.hidden, cfg.ffn
@@ -65,7 +72,28 @@ class OpChecker:
         self._note(op, err)
         assert err <= FP_TOL, f"{what}: rel_l2 {err:.3e} > {FP_TOL}"
 
-    def _quant(self, op, xq, xd, ref, what):
+    def _fmt(self, layer, name):
+        return self.fmts.get((layer, name), E.Q8_0)
+
+    def _sub_order(self, K):
+        """Index into a K vector of each element of a Q4_K activation (sub-block order)."""
+        if getattr(self, "_perm_k", None) != K:
+            pos = np.array([self.oc.lib.oc_q4k_pos(s, i) for s in range(8) for i in range(32)], np.int64)
+            self._perm = (256 * np.arange(K // 256)[:, None] + pos[None, :]).reshape(-1)
+            self._perm_k = K
+        return self._perm
+
+    def _width(self, which):
+        """Elements per row of an fp32 step buffer or an activation buffer."""
+        return {E.B_ACT_H: self.H, E.B_ACT4_H: self.H, E.B_HN: self.H, E.B_ACT_V: self.V, E.B_ACT4_V: self.V,
+                E.B_CORE: self.V, E.B_ACT_F: self.F, E.B_ACT4_F: self.F, E.B_FF: self.F, E.B_ACT_Q: self.q_dim,
+                E.B_ACT4_Q: self.q_dim, E.B_ATTN_OUT: self.q_dim}[which]
+
+    def _rows_f32(self, which):
+        K = self._width(which)
+        return self.eng.read_buffer(which, np.float32, 0, self.B * K).reshape(self.B, K)
+
+    def _quant(self, op, xq, xd, ref, what, fmt=E.Q8_0):
         """GPU int8 block activation (xq, xd) against the reference quantizer of the oracle's fp32 `ref`.
 
         The GPU quantizes its own fp32 value g (bit-exact reference quantizer,
@@ -78,7 +106,12 @@ class OpChecker:
         (there the neighbour is allowed), such flips at most
         MAX_FLIP_FRACTION of all elements compared.  The dequantized vectors'
         relative L2 is reported (one flip moves a block by one quantum)."""
-        rq, rd = self.oc.quantize_act_q8_0(np.ascontiguousarray(ref, np.float32))
+        ref = np.ascontiguousarray(ref, np.float32)
+        if fmt == E.Q4_K:
+            rq, rd, _ = self.oc.quantize_act_q4_K(ref)
+            ref = ref[self._sub_order(ref.size)]
+        else:
+            rq, rd = self.oc.quantize_act_q8_0(ref)
         xd64, rd64 = xd.astype(np.float64), rd.astype(np.float64)
         sdev = np.abs(xd64 - rd64) / max(rd64.max(initial=0.0), 1e-30)
         self.scale_dev = max(getattr(self, "scale_dev", 0.0), float(sdev.max(initial=0.0)))
@@ -118,26 +151,22 @@ class OpChecker:
         return np.sort(self.rng.choice(n, self.rows_per_matrix, replace=False))
 
     def _matrix(self, op, layer):
-        """(GGUF Q8_0 rows [N][K/32*34], K) of the op's matrix."""
+        """(GGUF rows [N][row bytes], K, format) of the op's matrix."""
         y = self.m["layers"][layer] if layer >= 0 else None
-        rows = lambda w, K: (np.asarray(w).reshape(-1, K // 32 * 34), K)  # noqa: E731
+
+        def rows(w, K, name):
+            fmt = self._fmt(layer, name)
+            return np.asarray(w).reshape(-1, E.gguf_row_bytes(fmt, K)), K, fmt
         if op == E.OP_MV_IN:
-            return rows(y["w_in"], self.H)
+            return rows(y["w_in"], self.H, "w_in")
         if op == E.OP_MV_OUT:
-            return rows(y["w_out"], self.q_dim if y["attn"] else self.V)
+            return rows(y["w_out"], self.q_dim if y["attn"] else self.V, "w_out")
         if op == E.OP_MV_GU:
             return rows(np.concatenate([np.asarray(y["w_gate"]).reshape(-1), np.asarray(y["w_up"]).reshape(-1)]),
-                        self.H)
+                        self.H, "w_gate")
         if op == E.OP_MV_DOWN:
-            return rows(y["w_down"], self.F)
-        return rows(self.m["lm_head"], self.H)
-
-    def _act_in(self, op, layer):
-        if op in (E.OP_MV_IN, E.OP_MV_GU, E.OP_LM_HEAD):
-            return E.B_ACT_H, self.H
-        if op == E.OP_MV_DOWN:
-            return E.B_ACT_F, self.F
-        return (E.B_ACT_Q, self.q_dim) if self.m["layers"][layer]["attn"] else (E.B_ACT_V, self.V)
+            return rows(y["w_down"], self.F, "w_down")
+        return rows(self.m["lm_head"], self.H, "lm_head")
 
     def _decode_q(self, qa, qsc, s):
         """q [n_heads][head_dim] from the three-piece int8 layout (csrc/layout.hpp)."""
@@ -172,8 +201,10 @@ class OpChecker:
             if ev.nparts:
                 b["parts"] = self._parts(E.B_PARTS, ev.nparts, self.H)
         elif op in (E.OP_MV_IN, E.OP_MV_OUT, E.OP_MV_GU, E.OP_MV_DOWN, E.OP_LM_HEAD):
-            which, K = self._act_in(op, L)
-            b["xq"], b["xd"] = eng.read_act(which, K)
+            b["xq"], b["xd"] = eng.read_act(ev.x_in, self._width(ev.x_in))
+        elif op in (E.OP_NORM_ROWS, E.OP_QUANT_ACT):
+            b["rows"] = self._rows_f32(ev.x_in) if op == E.OP_QUANT_ACT else \
+                eng.read_buffer(ev.x_in, np.float32, 0, self.B * self.H).reshape(self.B, self.H)
         elif op == E.OP_DELTA_STEP:
             b["proj"] = self._parts(E.B_PROJ, ev.nparts, c.nin_delta)
             b["conv"] = {s: eng.get_state(L, E.S_CONV, s) for s in self._active()}
@@ -186,8 +217,6 @@ class OpChecker:
             b["ctx"] = eng.read_buffer(E.B_CTX, np.int32)
             b["kv"] = {s: [eng.get_state(L, w, s) for w in (E.S_KEYS, E.S_VALS, E.S_KSCALES, E.S_VSCALES)]
                        for s in self._active()}
-        elif op == E.OP_QUANT_ATTN:
-            b["attn"] = eng.read_buffer(E.B_ATTN_OUT, np.float32, 0, self.B * self.q_dim).reshape(self.B, self.q_dim)
         elif op == E.OP_SWIGLU:
             b["gu"] = self._parts(E.B_GU, ev.nparts, 2 * self.F)
         elif op == E.OP_ARGMAX:
@@ -199,12 +228,14 @@ class OpChecker:
         where = f"op {op} layer {L}"
         if op == E.OP_EMBED:
             x = eng.read_buffer(E.B_X, np.float32, 0, self.B * self.H).reshape(self.B, self.H)
+            fmt = self._fmt(-1, "embed")
             for s in act:
-                assert np.array_equal(x[s], oc.embed_row_q8_0(self.m["embed"], self.H, b["tok"][s])), where
+                assert np.array_equal(x[s], oc.embed_row(fmt, self.m["embed"], self.H, b["tok"][s])), where
                 self._note(op)
         elif op == E.OP_NORM:
             w = self.m["final_norm"] if L < 0 else \
                 self.m["layers"][L]["ffn_norm" if self._norm_is_ffn(L) else "attn_norm"]
+            self.norm_w = w
             xo = eng.read_buffer(ev.x_out, np.float32, 0, self.B * self.H).reshape(self.B, self.H)
             xq, xd = eng.read_act(E.B_ACT_H, self.H)
             xin = b["x"]
@@ -213,8 +244,22 @@ class OpChecker:
             for s in act:
                 assert np.array_equal(xo[s], xin[s]), f"{where}: residual + partial sums not bit-exact"
                 self._quant(op, xq[s], xd[s], oc.rmsnorm(xin[s], w), f"{where} seq {s}")
+        elif op == E.OP_NORM_ROWS:
+            hn = self._rows_f32(ev.x_out)
+            for s in act:
+                self._fp(op, hn[s], oc.rmsnorm(b["rows"][s], self.norm_w), f"{where} seq {s}")
+        elif op == E.OP_QUANT_ACT:
+            K = self._width(ev.x_out)
+            xq, xd = eng.read_act(ev.x_out, K)
+            q4 = ev.x_out in E.ACT4_BUFFERS
+            for s in act:
+                rq, rd = (oc.quantize_act_q4_K(b["rows"][s])[:2] if q4 else oc.quantize_act_q8_0(b["rows"][s]))
+                assert np.array_equal(xq[s], rq) and np.array_equal(xd[s], rd), \
+                    f"{where} seq {s}: quantized activation of the GPU's rows not bit-exact"
+                self._note(op)
         elif op in (E.OP_MV_IN, E.OP_MV_OUT, E.OP_MV_GU, E.OP_MV_DOWN, E.OP_LM_HEAD):
-            W, K = self._matrix(op, L)
+            W, K, fmt = self._matrix(op, L)
+            assert (ev.x_in in E.ACT4_BUFFERS) == (fmt == E.Q4_K), f"{where}: activation format"
             N = W.shape[0]
             if op == E.OP_LM_HEAD:
                 y = eng.read_buffer(E.B_LOGITS, np.float32).reshape(self.B, N)
@@ -224,15 +269,18 @@ class OpChecker:
             rows = self._rows(N)
             Wr = np.ascontiguousarray(W[rows])
             for s in act:
-                x = oc.dequant_act_q8_0(b["xq"][s], b["xd"][s])
-                self._fp(op, y[s][rows], oc.matvec_q8_0(Wr, x), f"{where} seq {s}")
+                if fmt == E.Q4_K:
+                    ref = oc.matvec_q4_K(Wr, oc.dequant_act_q4_K(b["xq"][s], b["xd"][s]))
+                else:
+                    ref = oc.matvec_q8_0(Wr, oc.dequant_act_q8_0(b["xq"][s], b["xd"][s]))
+                self._fp(op, y[s][rows], ref, f"{where} seq {s}")
         elif op == E.OP_DELTA_STEP:
-            self._check_delta(L, act, b, where)
+            self._check_delta(L, act, b, where, ev.x_out)
         elif op == E.OP_ROPE_APPEND:
             self._check_rope(L, act, b, where)
         elif op == E.OP_ATTN:
             out = eng.read_buffer(E.B_ATTN_OUT, np.float32, 0, self.B * self.q_dim).reshape(self.B, self.q_dim)
-            xq, xd = eng.read_act(E.B_ACT_Q, self.q_dim)
+            xq, xd = eng.read_act(E.B_ACT_Q, self.q_dim) if ev.x_out == E.B_ACT_Q else (None, None)
             for s in act:
                 q = self._decode_q(b["qa"], b["qsc"], s).astype(np.float32)
                 keys, vals, ks, vs = b["kv"][s]
@@ -241,16 +289,18 @@ class OpChecker:
                 ref = oc.attn_decode(q, keys[:ctx * self.kv_dim], vals[:ctx * self.kv_dim], ks[:ctx * c.n_kv],
                                      vs[:ctx * c.n_kv], c.n_heads, c.n_kv, c.head_dim, ctx).reshape(-1)
                 self._fp(op, out[s], ref, f"{where} seq {s} attention")
-                self._quant(op, xq[s], xd[s], ref, f"{where} seq {s} attention activation")
-        elif op == E.OP_QUANT_ATTN:
-            xq, xd = eng.read_act(E.B_ACT_Q, self.q_dim)
-            for s in act:
-                self._quant(op, xq[s], xd[s], b["attn"][s], f"{where} seq {s}")
+                if xq is not None:
+                    self._quant(op, xq[s], xd[s], ref, f"{where} seq {s} attention activation")
         elif op == E.OP_SWIGLU:
             gu = self._sum_parts(b["gu"])
-            xq, xd = eng.read_act(E.B_ACT_F, self.F)
-            for s in act:
-                self._quant(op, xq[s], xd[s], oc.swiglu(gu[s][:self.F], gu[s][self.F:]), f"{where} seq {s}")
+            if ev.x_out == E.B_FF:
+                ff = self._rows_f32(E.B_FF)
+                for s in act:
+                    self._fp(op, ff[s], oc.swiglu(gu[s][:self.F], gu[s][self.F:]), f"{where} seq {s} rows")
+            else:
+                xq, xd = eng.read_act(E.B_ACT_F, self.F)
+                for s in act:
+                    self._quant(op, xq[s], xd[s], oc.swiglu(gu[s][:self.F], gu[s][self.F:]), f"{where} seq {s}")
         elif op == E.OP_ARGMAX:
             gen = eng.read_buffer(E.B_GEN, np.int32)
             pos = eng.read_buffer(E.B_POS, np.int32)
@@ -268,12 +318,16 @@ class OpChecker:
         self.counts[key] = n + 1
         return n % 2 == 1
 
-    def _check_delta(self, L, act, b, where):
+    def _check_delta(self, L, act, b, where, x_out):
         eng, oc, c, y = self.eng, self.oc, self.cfg, self.m["layers"][L]
         n_v, kd = c.ssm_heads, c.key_dim
         n_k, C_, kern = kd // 128, c.conv_dim, c.conv_kernel
         proj = self._sum_parts(b["proj"])
-        xq, xd = eng.read_act(E.B_ACT_V, self.V)
+        fp_out = x_out == E.B_CORE
+        if fp_out:
+            core_f = self._rows_f32(E.B_CORE)
+        else:
+            xq, xd = eng.read_act(E.B_ACT_V, self.V)
         for s in act:
             p = int(b["pos"][s])
             pr = proj[s]
@@ -292,7 +346,10 @@ class OpChecker:
             S = np.ascontiguousarray(b["ssm"][s].reshape(n_v, 128, 128).transpose(0, 2, 1))
             core = oc.deltanet_step(S, qn, kn, v, dec, bet, n_v, n_k, 128, 128)
             g = oc.gated_rmsnorm(core, z, y["ssm_norm"], n_v, 128).reshape(-1)
-            self._quant(E.OP_DELTA_STEP, xq[s], xd[s], g, f"{where} seq {s} gated-norm activation")
+            if fp_out:
+                self._fp(E.OP_DELTA_STEP, core_f[s], g, f"{where} seq {s} gated-norm rows")
+            else:
+                self._quant(E.OP_DELTA_STEP, xq[s], xd[s], g, f"{where} seq {s} gated-norm activation")
             S_gpu = eng.get_state(L, E.S_SSM, s).reshape(n_v, 128, 128).transpose(0, 2, 1)
             self._fp(E.OP_DELTA_STEP, S_gpu, S, f"{where} seq {s} recurrent state")
             ring_after = eng.get_state(L, E.S_CONV, s).reshape(kern, C_)

@@ -19,7 +19,7 @@ import pytest
 
 from conftest import rel_l2
 from decoder_ops import OpChecker
-from decoder_util import OracleDecoder, make_model, small_config, upload
+from decoder_util import MIXED_FMTS, OracleDecoder, make_model, small_config, upload
 
 pytestmark = pytest.mark.gpu
 
@@ -61,11 +61,14 @@ def _ragged_inputs(step, prompt, start, nxt):
     return tok, pos
 
 
-def test_decoder_every_op_matches_oracle(oc):
-    """12 ragged steps of the small model, every launch of every step checked against the oracle."""
-    from echohip.engine import Engine
+@pytest.mark.parametrize("fmts", [None, MIXED_FMTS], ids=["q8_0", "mixed"])
+def test_decoder_every_op_matches_oracle(oc, fmts):
+    """12 ragged steps of the small model, every launch of every step checked
+    against the oracle; "mixed": Q4_K matrices on every kind of input path
+    next to Q8_0 ones, F16 embedding."""
+    from echohip.engine import OP_NORM_ROWS, OP_QUANT_ACT, Engine
     cfg = small_config(max_batch=3, max_ctx=64)
-    m = make_model(cfg, seed=7)
+    m = make_model(cfg, seed=7, fmts=fmts)
     eng = Engine(cfg)
     upload(eng, m)
     eng.reset()
@@ -87,14 +90,17 @@ def test_decoder_every_op_matches_oracle(oc):
                 assert gpos[s] == -1
     print(chk.summary())
     assert chk.counts.get(3, 0) > 0 and chk.counts.get(6, 0) > 0  # delta steps and attention were checked
+    if fmts:
+        assert chk.counts.get(OP_QUANT_ACT, 0) > 0 and chk.counts.get(OP_NORM_ROWS, 0) > 0
     eng.close()
 
 
-def test_traced_step_equals_eager_and_graph(oc):
+@pytest.mark.parametrize("fmts", [None, MIXED_FMTS], ids=["q8_0", "mixed"])
+def test_traced_step_equals_eager_and_graph(oc, fmts):
     """The traced step launches the same kernels on the same buffers: logits, tokens and states bit-identical."""
     from echohip.engine import S_KEYS, S_SSM, Engine
     cfg = small_config(max_batch=3, max_ctx=64)
-    m = make_model(cfg, seed=8)
+    m = make_model(cfg, seed=8, fmts=fmts)
     outs = []
     for mode in ("traced", "eager", "graph"):
         eng = Engine(cfg)
@@ -220,3 +226,70 @@ def test_queued_inputs_match_synchronous_feeding():
     assert np.array_equal(ga, gb)
     for x, y in zip(la, lb):
         assert np.array_equal(x, y)
+
+
+def test_mixed_formats_end_to_end_matches_oracle_decoder(oc):
+    """The mixed-format small model, one sequence, 8 greedy steps on the GPU
+    graph and on the oracle's decoder (int8 activations, the same per-tensor
+    formats): logits within 5e-2 relative L2 (per-operation parity is the
+    gate; this bounds the accumulation of int8 rounding-boundary flips)."""
+    from echohip.engine import Engine
+    cfg = small_config(max_batch=1, max_ctx=16)
+    m = make_model(cfg, seed=31, fmts=MIXED_FMTS)
+    eng = Engine(cfg)
+    upload(eng, m)
+    eng.reset()
+    dec = OracleDecoder(oc, cfg, m, n_seq=1, quant_act=True)
+    tok = 77
+    errs = []
+    for p in range(8):
+        ref = dec.token(0, tok)
+        eng.set_inputs(np.array([tok], np.int32), np.array([p], np.int32))
+        eng.step(graph=True)
+        got = eng.logits(0)
+        errs.append(rel_l2(got, ref))
+        tok = int(np.argmax(ref))
+    print("per-step logits rel_l2", " ".join(f"{e:.1e}" for e in errs))
+    assert max(errs) < 5e-2
+    eng.close()
+
+
+def test_formats_round_trip_and_errors():
+    """set_format / get_format / get_tensor: every tensor reads back the bytes
+    it was given in its own format; the matrix bytes shrink to Q4_K's; bad
+    formats and shapes are refused."""
+    from echohip.engine import (F16, F32, Q4_K, Q8_0, T_ATTN_NORM, T_EMBED, T_LM_HEAD, T_W_DOWN, T_W_GATE, T_W_IN,
+                                T_W_OUT, T_W_UP, Engine, EngineConfig, gguf_row_bytes)
+    from echohip.lib import EchoHipError
+    cfg = small_config(max_batch=2, max_ctx=16)
+    m = make_model(cfg, seed=5, fmts=MIXED_FMTS)
+    eng = Engine(cfg)
+    q8_bytes = eng.weight_bytes()
+    upload(eng, m)
+    assert eng.weight_bytes() < q8_bytes
+    ids = {"w_in": T_W_IN, "w_out": T_W_OUT, "w_gate": T_W_GATE, "w_up": T_W_UP, "w_down": T_W_DOWN}
+    for l, y in enumerate(m["layers"]):
+        for name, t in ids.items():
+            fmt = MIXED_FMTS.get((l, name), Q8_0)
+            assert eng.get_format(l, t) == fmt
+            ref = np.asarray(y[name]).reshape(-1)
+            assert np.array_equal(eng.get_tensor(l, t, ref.nbytes), ref.view(np.uint8)), (l, name)
+    assert eng.get_format(0, T_LM_HEAD) == Q4_K and eng.get_format(0, T_EMBED) == F16
+    lm = np.asarray(m["lm_head"]).reshape(-1)
+    assert np.array_equal(eng.get_tensor(0, T_LM_HEAD, lm.nbytes), lm)
+    emb = np.asarray(m["embed"]).reshape(-1)
+    assert np.array_equal(eng.get_tensor(0, T_EMBED, emb.nbytes).view(np.float16), emb)
+    with pytest.raises(EchoHipError):
+        eng.set_tensor(0, T_W_IN, np.zeros(cfg.nin_delta * gguf_row_bytes(Q8_0, cfg.hidden), np.uint8))  # size
+    for bad in ((0, T_ATTN_NORM, Q4_K), (0, T_W_IN, F16), (0, T_EMBED, Q4_K), (0, T_W_IN, 8)):
+        with pytest.raises(EchoHipError):
+            eng.set_format(*bad)
+    eng.set_format(0, T_EMBED, F32)
+    assert eng.get_format(0, T_EMBED) == F32
+    eng.close()
+    odd = Engine(EngineConfig(vocab=300, hidden=384, ffn=512, n_layers=1, n_heads=2, n_kv=2, head_dim=256,
+                              ssm_inner=0, ssm_heads=0, conv_kernel=4, attn_interval=1, max_batch=1, max_ctx=8))
+    with pytest.raises(EchoHipError):
+        odd.set_format(0, T_W_IN, Q4_K)   # K = hidden 384 is not a multiple of 256
+    odd.set_format(0, T_W_OUT, Q4_K)      # K = 2 * 256
+    odd.close()

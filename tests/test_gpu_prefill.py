@@ -22,7 +22,7 @@ import numpy as np
 import pytest
 
 from conftest import rel_l2
-from decoder_util import make_model, small_config, upload
+from decoder_util import MIXED_FMTS, make_model, small_config, upload
 from echohip import synth
 from test_gpu_kernels import dev, empty, host
 
@@ -119,11 +119,12 @@ def _compare_states(a, b, cfg):
             assert rel_l2(x, y) < 5e-2, (key, rel_l2(x, y))
 
 
-@pytest.mark.parametrize("lens", [(40, 7, 1), (600, 3, 25)])
-def test_prefill_matches_token_loop(lens):
+@pytest.mark.parametrize("lens,fmts", [((40, 7, 1), None), ((600, 3, 25), None), ((40, 7, 1), MIXED_FMTS)],
+                         ids=["short", "long", "mixed"])
+def test_prefill_matches_token_loop(lens, fmts):
     from echohip.engine import Engine
     cfg = small_config(max_batch=3, max_ctx=640)
-    m = make_model(cfg, seed=21)
+    m = make_model(cfg, seed=21, fmts=fmts)
     rng = np.random.default_rng(3)
     prompts = [rng.integers(0, cfg.vocab, n).astype(np.int32) for n in lens]
     a, b = Engine(cfg), Engine(cfg)
@@ -229,11 +230,15 @@ def test_prefill_rejects_bad_arguments():
     e.close()
 
 
-def test_prefill_one_token_is_the_decode_step():
-    """A one-token prompt: the GEMM path and the decode graph agree to fp32 rounding."""
+@pytest.mark.parametrize("fmts", [None, MIXED_FMTS], ids=["q8_0", "mixed"])
+def test_prefill_one_token_is_the_decode_step(fmts):
+    """A one-token prompt: the GEMM path and the decode graph agree to fp32
+    rounding.  A Q4_K product is the difference of two terms (d*sc*isum and
+    dmin*m*xsum, each larger than the result) that the GEMM and the matvec
+    round in different groupings, so the mixed model's bound is 1e-4."""
     from echohip.engine import Engine
     cfg = small_config(max_batch=2, max_ctx=16)
-    m = make_model(cfg, seed=23)
+    m = make_model(cfg, seed=23, fmts=fmts)
     a, b = Engine(cfg), Engine(cfg)
     upload(a, m)
     upload(b, m)
@@ -242,7 +247,7 @@ def test_prefill_one_token_is_the_decode_step():
     a.prefill(1, [417], 0)
     b.set_inputs(np.array([0, 417], np.int32), np.array([-1, 0], np.int32))
     b.step(graph=False)
-    assert rel_l2(a.logits(1), b.logits(1)) < 1e-6
+    assert rel_l2(a.logits(1), b.logits(1)) < (1e-6 if fmts is None else 1e-4)
     assert a.tokens()[0][1] == b.tokens()[0][1]
     a.close()
     b.close()
