@@ -21,6 +21,7 @@
 #include "echo_gguf.h"
 #include "echo_hip.h"
 #include "gguf_reader.h"
+#include "types.h"
 
 extern "C" int ec_set_error(int code, const char* msg);
 
@@ -422,37 +423,99 @@ bool has(const GGUFReader& r, const std::string& n) { return r.tensors().count(n
 
 std::string blk(uint32_t l, const char* s) { return "blk." + std::to_string(l) + "." + s; }
 
+// The engine's storage format of a ggml type (-1: not one it stores).
+int engine_fmt(GGMLType t) {
+    switch (t) {
+        case GGMLType::Q8_0: return EC_Q8_0;
+        case GGMLType::Q4_K: return EC_Q4_K;
+        case GGMLType::F16: return EC_F16;
+        case GGMLType::F32: return EC_F32;
+        default: return -1;
+    }
+}
+
+const char* type_name(GGMLType t) {
+    switch (t) {
+        case GGMLType::Q8_0: return "Q8_0";
+        case GGMLType::Q4_K: return "Q4_K";
+        case GGMLType::F16: return "F16";
+        case GGMLType::F32: return "F32";
+        default: return "another type";
+    }
+}
+
+// Tensors by kind, each in the formats the reference reads it in
+// (src/inference.cpp:526-545 dispatches matrices per dtype; norms and the
+// embedding are fp16 there, :233-237): matrices Q8_0 or Q4_K, vectors F32 or
+// F16 (widened to fp32 here, exactly), the embedding Q8_0, F16 or F32.
 struct Loader {
     const GGUFReader& r;
     ec_engine* e;
-    const TensorInfo& need(const std::string& n, GGMLType t, uint64_t ne0, uint64_t ne1) {
+    const TensorInfo& need(const std::string& n, std::initializer_list<GGMLType> ok_types, uint64_t ne0,
+                           uint64_t ne1) {
         auto it = r.tensors().find(n);
         if (it == r.tensors().end()) throw std::runtime_error("GGUF: tensor '" + n + "' not found");
         const TensorInfo& ti = it->second;
         const uint64_t s1 = ti.shape.size() > 1 ? ti.shape[1] : 1;
-        bool ok = ti.dtype == t && ti.shape[0] == ne0 && s1 == ne1;
+        bool ok = ti.shape[0] == ne0 && s1 == ne1;
         for (size_t d = 2; d < ti.shape.size(); ++d) ok = ok && ti.shape[d] == 1;
         if (!ok)
-            throw std::runtime_error("GGUF: tensor '" + n + "' must be " + (t == GGMLType::Q8_0 ? "Q8_0" : "F32") +
-                                     " [" + std::to_string(ne0) + ", " + std::to_string(ne1) + "]");
+            throw std::runtime_error("GGUF: tensor '" + n + "' must be [" + std::to_string(ne0) + ", " +
+                                     std::to_string(ne1) + "]");
+        bool type_ok = false;
+        std::string names;
+        for (GGMLType t : ok_types) {
+            type_ok = type_ok || ti.dtype == t;
+            names += std::string(names.empty() ? "" : " or ") + type_name(t);
+        }
+        if (!type_ok)
+            throw std::runtime_error("GGUF: tensor '" + n + "' is " + type_name(ti.dtype) + ", must be " + names);
         return ti;
     }
     void set(uint32_t layer, int id, const void* p, size_t bytes) {
         if (ec_engine_set_tensor(e, (int)layer, id, p, bytes) != EC_OK)
             throw std::runtime_error(std::string("GGUF load: ") + ec_last_error());
     }
-    void put(uint32_t layer, int id, const std::string& n, GGMLType t, uint64_t ne0, uint64_t ne1) {
-        const TensorInfo& ti = need(n, t, ne0, ne1);
+    void format(uint32_t layer, int id, GGMLType t, const std::string& n) {
+        if (ec_engine_set_format(e, (int)layer, id, engine_fmt(t)) != EC_OK)
+            throw std::runtime_error("GGUF load: '" + n + "': " + ec_last_error());
+    }
+    // fp32 vector from an F32 or F16 tensor
+    void vec(uint32_t layer, int id, const std::string& n, uint64_t ne0, uint64_t ne1) {
+        const TensorInfo& ti = need(n, {GGMLType::F32, GGMLType::F16}, ne0, ne1);
+        if (ti.dtype == GGMLType::F32) return set(layer, id, r.tensor_data(n), ti.size);
+        const uint8_t* src = r.tensor_data(n);
+        std::vector<float> v(ne0 * ne1);
+        for (size_t i = 0; i < v.size(); ++i) {
+            fp16_t h;
+            memcpy(&h, src + 2 * i, 2);
+            v[i] = fp16_to_fp32(h);
+        }
+        set(layer, id, v.data(), v.size() * sizeof(float));
+    }
+    // one matrix, stored in its own format
+    void mat(uint32_t layer, int id, const std::string& n, uint64_t ne0, uint64_t ne1) {
+        const TensorInfo& ti = need(n, {GGMLType::Q8_0, GGMLType::Q4_K}, ne0, ne1);
+        format(layer, id, ti.dtype, n);
         set(layer, id, r.tensor_data(n), ti.size);
     }
-    // rows of several Q8_0 matrices (same K) stacked in order
+    // rows of several matrices (same K, one format) stacked in order into one
+    // engine matrix
     void stack(uint32_t layer, int id, const std::vector<std::pair<std::string, uint64_t>>& parts, uint64_t K) {
         std::vector<uint8_t> buf;
-        for (const auto& p : parts) {
-            const TensorInfo& ti = need(p.first, GGMLType::Q8_0, K, p.second);
+        GGMLType t0 = GGMLType::Q8_0;
+        for (size_t i = 0; i < parts.size(); ++i) {
+            const auto& p = parts[i];
+            const TensorInfo& ti = need(p.first, {GGMLType::Q8_0, GGMLType::Q4_K}, K, p.second);
+            if (i == 0) t0 = ti.dtype;
+            if (ti.dtype != t0)
+                throw std::runtime_error("GGUF: '" + p.first + "' is " + type_name(ti.dtype) + " but '" +
+                                         parts[0].first + "' is " + type_name(t0) +
+                                         ": the fused projection needs one format");
             const uint8_t* d = r.tensor_data(p.first);
             buf.insert(buf.end(), d, d + ti.size);
         }
+        format(layer, id, t0, parts[0].first);
         set(layer, id, buf.data(), buf.size());
     }
 };
@@ -522,28 +585,37 @@ void ec_load_gguf_tensors(ec_engine* e, const GGUFReader& r) {
         const uint64_t H = c.hidden, F = c.ffn, V = c.vocab;
         const uint64_t q_dim = (uint64_t)c.n_heads * c.head_dim, kv_dim = (uint64_t)c.n_kv * c.head_dim;
         const uint64_t value_dim = c.ssm_inner, key_dim = c.ssm_inner / 2, conv_dim = 2 * key_dim + value_dim;
-        L.put(0, EC_T_EMBED, "token_embd.weight", GGMLType::Q8_0, H, V);
-        L.put(0, EC_T_FINAL_NORM, "output_norm.weight", GGMLType::F32, H, 1);
-        L.put(0, EC_T_LM_HEAD, has(r, "output.weight") ? "output.weight" : "token_embd.weight", GGMLType::Q8_0, H, V);
+        const TensorInfo& emb = L.need("token_embd.weight", {GGMLType::Q8_0, GGMLType::F16, GGMLType::F32}, H, V);
+        L.format(0, EC_T_EMBED, emb.dtype, "token_embd.weight");
+        L.set(0, EC_T_EMBED, r.tensor_data("token_embd.weight"), emb.size);
+        L.vec(0, EC_T_FINAL_NORM, "output_norm.weight", H, 1);
+        L.mat(0, EC_T_LM_HEAD, has(r, "output.weight") ? "output.weight" : "token_embd.weight", H, V);
         for (uint32_t l = 0; l < c.n_layers; ++l) {
             const bool attn = (l + 1) % c.attn_interval == 0;
-            L.put(l, EC_T_ATTN_NORM, blk(l, "attn_norm.weight"), GGMLType::F32, H, 1);
+            L.vec(l, EC_T_ATTN_NORM, blk(l, "attn_norm.weight"), H, 1);
             const std::string fn = has(r, blk(l, "post_attention_norm.weight")) ? blk(l, "post_attention_norm.weight")
                                                                               : blk(l, "ffn_norm.weight");
-            L.put(l, EC_T_FFN_NORM, fn, GGMLType::F32, H, 1);
-            L.put(l, EC_T_W_GATE, blk(l, "ffn_gate.weight"), GGMLType::Q8_0, H, F);
-            L.put(l, EC_T_W_UP, blk(l, "ffn_up.weight"), GGMLType::Q8_0, H, F);
-            L.put(l, EC_T_W_DOWN, blk(l, "ffn_down.weight"), GGMLType::Q8_0, F, H);
+            L.vec(l, EC_T_FFN_NORM, fn, H, 1);
+            // gate and up are one engine matrix: one format for both
+            const TensorInfo& gate = L.need(blk(l, "ffn_gate.weight"), {GGMLType::Q8_0, GGMLType::Q4_K}, H, F);
+            const TensorInfo& up = L.need(blk(l, "ffn_up.weight"), {GGMLType::Q8_0, GGMLType::Q4_K}, H, F);
+            if (gate.dtype != up.dtype)
+                throw std::runtime_error("GGUF: block " + std::to_string(l) + " ffn_gate is " + type_name(gate.dtype) +
+                                         ", ffn_up " + type_name(up.dtype) + ": gate and up need one format");
+            L.format(l, EC_T_W_GATE, gate.dtype, blk(l, "ffn_gate.weight"));
+            L.set(l, EC_T_W_GATE, r.tensor_data(blk(l, "ffn_gate.weight")), gate.size);
+            L.set(l, EC_T_W_UP, r.tensor_data(blk(l, "ffn_up.weight")), up.size);
+            L.mat(l, EC_T_W_DOWN, blk(l, "ffn_down.weight"), F, H);
             if (attn) {
                 L.stack(l, EC_T_W_IN, {{blk(l, "attn_q.weight"), q_dim}, {blk(l, "attn_k.weight"), kv_dim},
                                        {blk(l, "attn_v.weight"), kv_dim}}, H);
-                L.put(l, EC_T_W_OUT, blk(l, "attn_output.weight"), GGMLType::Q8_0, q_dim, H);
+                L.mat(l, EC_T_W_OUT, blk(l, "attn_output.weight"), q_dim, H);
                 const std::vector<float> zero(c.head_dim, 0.0f);
                 const char* norms[2] = {"attn_q_norm.weight", "attn_k_norm.weight"};
                 const int ids[2] = {EC_T_Q_NORM, EC_T_K_NORM};
                 for (int i = 0; i < 2; ++i) {
                     if (has(r, blk(l, norms[i])))
-                        L.put(l, ids[i], blk(l, norms[i]), GGMLType::F32, c.head_dim, 1);
+                        L.vec(l, ids[i], blk(l, norms[i]), c.head_dim, 1);
                     else
                         L.set(l, ids[i], zero.data(), zero.size() * 4);
                 }
@@ -551,11 +623,11 @@ void ec_load_gguf_tensors(ec_engine* e, const GGUFReader& r) {
                 L.stack(l, EC_T_W_IN, {{blk(l, "attn_qkv.weight"), conv_dim}, {blk(l, "attn_gate.weight"), value_dim},
                                        {blk(l, "ssm_alpha.weight"), c.ssm_heads},
                                        {blk(l, "ssm_beta.weight"), c.ssm_heads}}, H);
-                L.put(l, EC_T_W_OUT, blk(l, "ssm_out.weight"), GGMLType::Q8_0, value_dim, H);
-                L.put(l, EC_T_CONV_W, blk(l, "ssm_conv1d.weight"), GGMLType::F32, c.conv_kernel, conv_dim);
-                L.put(l, EC_T_A_LOG, blk(l, "ssm_a"), GGMLType::F32, c.ssm_heads, 1);
-                L.put(l, EC_T_DT_BIAS, blk(l, "ssm_dt.bias"), GGMLType::F32, c.ssm_heads, 1);
-                L.put(l, EC_T_SSM_NORM, blk(l, "ssm_norm.weight"), GGMLType::F32, 128, 1);
+                L.mat(l, EC_T_W_OUT, blk(l, "ssm_out.weight"), value_dim, H);
+                L.vec(l, EC_T_CONV_W, blk(l, "ssm_conv1d.weight"), c.conv_kernel, conv_dim);
+                L.vec(l, EC_T_A_LOG, blk(l, "ssm_a"), c.ssm_heads, 1);
+                L.vec(l, EC_T_DT_BIAS, blk(l, "ssm_dt.bias"), c.ssm_heads, 1);
+                L.vec(l, EC_T_SSM_NORM, blk(l, "ssm_norm.weight"), 128, 1);
             }
         }
     }
