@@ -198,7 +198,10 @@ def attention_case(hip, ctxs, n_heads=16, n_kv=4, hd=256, iters=100, seed=0):
             "copies": n_copies}
 
 
-def deltanet_case(hip, T=1024, n_v=32, d=128, iters=5, seed=0):
+def deltanet_case(hip, T=1024, n_v=32, d=128, iters=5, seed=0, chunked=False):
+    """The 1024-token, 32-head gated delta-net workload: the token loop
+    (k_deltanet) or the chunked scan (k_dn_chunk_prep + k_dn_chunk_scan, both
+    launches timed); flops counted as the token loop's 7*d*d per token and head."""
     st = torch.cuda.current_stream().cuda_stream
     g = torch.Generator(device="cuda").manual_seed(seed)
     state0 = torch.randn((n_v, d, d), generator=g, device="cuda") * 0.02
@@ -209,6 +212,7 @@ def deltanet_case(hip, T=1024, n_v=32, d=128, iters=5, seed=0):
     bet = torch.sigmoid(torch.randn((T, n_v), generator=g, device="cuda"))
     out = torch.empty((T, n_v, d), device="cuda")
     state = state0.clone()
+    ws = torch.empty(hip.deltanet_chunked_ws_bytes(T, 1, n_v), dtype=torch.uint8, device="cuda") if chunked else None
 
     # time only the recurrence: events around the delta-net launch
     evs = []
@@ -216,14 +220,18 @@ def deltanet_case(hip, T=1024, n_v=32, d=128, iters=5, seed=0):
         state.copy_(state0)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
-        hip.deltanet(state, q, k, v, dec, bet, out, T, 1, n_v, n_v, d, d, stream=st)
+        if chunked:
+            hip.deltanet_chunked(state, q, k, v, dec, bet, out, T, 1, n_v, n_v, d, d, ws, stream=st)
+        else:
+            hip.deltanet(state, q, k, v, dec, bet, out, T, 1, n_v, n_v, d, d, stream=st)
         b.record()
         evs.append((a, b))
     torch.cuda.synchronize()
     us = float(np.mean([a.elapsed_time(b) for a, b in evs[1:]]) * 1e3)
     flops = 7 * n_v * d * d * T
     tf = flops / (us * 1e-6) / 1e12
-    return {"kernel": "k_deltanet", "T": T, "flops": flops, "us": round(us, 2), "us_per_token": round(us / T, 4),
+    name = "k_dn_chunk_prep+k_dn_chunk_scan" if chunked else "k_deltanet"
+    return {"kernel": name, "T": T, "flops": flops, "us": round(us, 2), "us_per_token": round(us / T, 4),
             "TFLOPs": round(tf, 2), "frac": round(tf / FP32_PEAK_TFLOPS, 4)}
 
 

@@ -45,6 +45,7 @@ _SIGS = {
     "ec_glue_qk_rope_append_split": [_vp, _u32, _u32, _vp, _vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                      _vp, _vp, _vp, _u32, _u64, _u32, _u32, _u32, _u32, _vp],
     "ec_deltanet": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp, _vp],
+    "ec_deltanet_chunked": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp, _vp, _vp],
     "ec_fill_random": [C.c_int, _vp, _u64, _u64, C.c_float, _u32, _vp],
     "ec_gemm_quantize_act": [C.c_int, _vp, _vp, _u32, _u32, _vp],
     "ec_gemm": [C.c_int, _vp, _vp, _vp, _u32, _u32, _u32, _u32, C.c_int, _vp],
@@ -72,6 +73,7 @@ _SIZE_FNS = {
     "ec_attn_qa_bytes": [_u32, _u32],
     "ec_gemm_act_bytes": [C.c_int, _u32, _u32],
     "ec_attn_noalloc_max_bytes": [],
+    "ec_deltanet_chunked_ws_bytes": [_u32, _u32, _u32],
 }
 
 
@@ -283,6 +285,14 @@ class Lib:
     def deltanet(self, state, q, k, v, decay, beta, out, T, n_seq, n_v, n_k, d_k, d_v, seq_pos=None, stream=None):
         self._call("ec_deltanet", _ptr(state), _ptr(q), _ptr(k), _ptr(v), _ptr(decay), _ptr(beta), _ptr(out), T,
                    n_seq, n_v, n_k, d_k, d_v, _ptr(seq_pos), self._stream(stream))
+
+    def deltanet_chunked_ws_bytes(self, T, n_seq, n_v):
+        return self.L.ec_deltanet_chunked_ws_bytes(T, n_seq, n_v)
+
+    def deltanet_chunked(self, state, q, k, v, decay, beta, out, T, n_seq, n_v, n_k, d_k, d_v, ws, seq_pos=None,
+                         stream=None):
+        self._call("ec_deltanet_chunked", _ptr(state), _ptr(q), _ptr(k), _ptr(v), _ptr(decay), _ptr(beta), _ptr(out),
+                   T, n_seq, n_v, n_k, d_k, d_v, _ptr(seq_pos), _ptr(ws), self._stream(stream))
 
     def stream_read_shape(self, src, nbytes, out, blocks, threads, unroll, stream=None):
         self._call("ec_stream_read_shape", _ptr(src), nbytes, _ptr(out), blocks, threads, unroll, self._stream(stream))

@@ -181,6 +181,18 @@ int ec_deltanet(float* state, const float* q, const float* k, const float* v, co
                 float* out, uint32_t T, uint32_t n_seq, uint32_t n_v, uint32_t n_k, uint32_t d_k, uint32_t d_v,
                 const int32_t* seq_pos, void* stream);
 
+/* The same recurrence for a prompt chunk, in chunks of 64 tokens (prefill):
+ * per chunk the decay-weighted key Gram matrix gives U = (I + A)^{-1} B (V -
+ * G K S0) by forward substitution, then O and the next state from the chunk's
+ * start state with fp32 MFMA products; chunks run in order, heads and value
+ * columns in parallel.  Equal to ec_deltanet up to fp32 rounding (a decay below
+ * 1e-30 counts as 1e-30).  d_k = d_v = 128; ws holds
+ * ec_deltanet_chunked_ws_bytes(T, n_seq, n_v) bytes. */
+size_t ec_deltanet_chunked_ws_bytes(uint32_t T, uint32_t n_seq, uint32_t n_v);
+int ec_deltanet_chunked(float* state, const float* q, const float* k, const float* v, const float* decay,
+                        const float* beta, float* out, uint32_t T, uint32_t n_seq, uint32_t n_v, uint32_t n_k,
+                        uint32_t d_k, uint32_t d_v, const int32_t* seq_pos, void* ws, void* stream);
+
 /* One decode token of a delta-net block (qwen_linear.zig:182-257), fused:
  * conv + SiLU over the ring conv state (see ec_glue_conv_gates), q/k L2 norms,
  * decay/beta gates, the delta rule on state (layout of ec_deltanet, d_k = d_v

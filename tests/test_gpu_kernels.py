@@ -427,6 +427,83 @@ def test_deltanet_1024_tokens_32_heads(hip, oc):
     assert es < 1e-3
 
 
+def _dn_inputs(T, n_seq, n_v, n_k, seed, d=128):
+    rng = np.random.default_rng(seed)
+    S0 = (rng.standard_normal((n_seq, n_v, d, d)) * 0.02).astype(np.float32)  # reference layout [k][v]
+    q = rng.standard_normal((T, n_seq, n_k, d)).astype(np.float32)
+    k = rng.standard_normal((T, n_seq, n_k, d)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    v = rng.standard_normal((T, n_seq, n_v, d)).astype(np.float32)
+    dec = synth.sigmoid(rng.normal(2, 0.5, (T, n_seq, n_v))).astype(np.float32)
+    bet = synth.sigmoid(rng.normal(0, 1, (T, n_seq, n_v))).astype(np.float32)
+    return S0, q, k, v, dec, bet
+
+
+@pytest.mark.parametrize("T,n_seq,n_v,n_k,zero_decay", [(1, 1, 4, 4, False), (64, 1, 4, 4, False),
+                                                        (200, 2, 4, 2, False), (130, 3, 2, 1, True)])
+def test_deltanet_chunked(hip, oc, T, n_seq, n_v, n_k, zero_decay):
+    """Chunked scan (64-token chunks, a partial last chunk, GQA head sharing,
+    several sequences, the last one skipped by seq_pos) against the oracle's
+    token loop; zero_decay: a few tokens with decay exactly 0 (the state is
+    reset there)."""
+    import torch
+    d = 128
+    S0, q, k, v, dec, bet = _dn_inputs(T, n_seq, n_v, n_k, 7 * T + n_v)
+    if zero_decay:
+        dec[[0, 63, 64, 100]] = 0.0
+    state = dev(np.ascontiguousarray(S0.transpose(0, 1, 3, 2)))  # device layout [v][k]
+    out = dev(np.full(T * n_seq * n_v * d, 7.0, np.float32))
+    ws = empty(hip.deltanet_chunked_ws_bytes(T, n_seq, n_v), torch.uint8)
+    seq_pos = np.zeros(n_seq, np.int32)
+    if n_seq > 2:
+        seq_pos[-1] = -1
+    hip.deltanet_chunked(state, dev(q), dev(k), dev(v), dev(dec), dev(bet), out, T, n_seq, n_v, n_k, d, d, ws,
+                         seq_pos=dev(seq_pos))
+    out = host(out).reshape(T, n_seq, n_v, d)
+    S = host(state).reshape(n_seq, n_v, d, d).transpose(0, 1, 3, 2)
+    for s in range(n_seq):
+        if seq_pos[s] < 0:
+            assert np.array_equal(S[s], S0[s]) and np.all(out[:, s] == 7.0)
+            continue
+        Sr = S0[s].copy()
+        for t in range(T):
+            ref = oc.deltanet_step(Sr, q[t, s], k[t, s], v[t, s], dec[t, s], bet[t, s], n_v, n_k, d, d)
+            assert rel_l2(out[t, s], ref) < TOL, (s, t, rel_l2(out[t, s], ref))
+        assert rel_l2(S[s], Sr) < TOL
+
+
+def test_deltanet_chunked_1024_tokens_32_heads(hip, oc):
+    """The 1024-token, 32-head workload through the chunked scan: every token's
+    output and the final state within 1e-3 of 1024 sequential oracle steps, and
+    within 1e-4 of the GPU token loop (ec_deltanet)."""
+    import torch
+    T, n_v, d = 1024, 32, 128
+    S0, q, k, v, dec, bet = _dn_inputs(T, 1, n_v, n_v, 1024)
+    S0 = S0[0]
+    st_c = dev(np.ascontiguousarray(S0.transpose(0, 2, 1)))
+    st_t = dev(np.ascontiguousarray(S0.transpose(0, 2, 1)))
+    out_c = empty(T * n_v * d, torch.float32)
+    out_t = empty(T * n_v * d, torch.float32)
+    ws = empty(hip.deltanet_chunked_ws_bytes(T, 1, n_v), torch.uint8)
+    args = (dev(q), dev(k), dev(v), dev(dec), dev(bet))
+    hip.deltanet_chunked(st_c, *args, out_c, T, 1, n_v, n_v, d, d, ws)
+    hip.deltanet(st_t, *args, out_t, T, 1, n_v, n_v, d, d)
+    oc_, ot = host(out_c).reshape(T, n_v, d), host(out_t).reshape(T, n_v, d)
+    S = host(st_c).reshape(n_v, d, d).transpose(0, 2, 1)
+    assert rel_l2(oc_, ot) < 1e-4 and rel_l2(host(st_c), host(st_t)) < 1e-4
+    Sr = S0.copy()
+    worst = 0.0
+    for t in range(T):
+        ref = oc.deltanet_step(Sr, q[t, 0], k[t, 0], v[t, 0], dec[t, 0], bet[t, 0], n_v, n_v, d, d)
+        e = rel_l2(oc_[t], ref)
+        worst = max(worst, e)
+        assert e < 1e-3, (t, e)
+    es = rel_l2(S, Sr)
+    print(f"chunked 1024 tokens: worst per-token output rel_l2 {worst:.2e}, final state rel_l2 {es:.2e}")
+    assert es < 1e-3
+
+
 @pytest.mark.parametrize("fmt,N,K", [(6, 9216, 2560), (6, 2560, 9216), (6, 1000, 4096), (6, 77, 96), (10, 9216, 2560),
                                      (10, 2560, 9216), (10, 333, 512)])
 def test_gguf_f32_matvec_full_shapes(hip, oc, fmt, N, K):
