@@ -293,10 +293,11 @@ def main() -> int:
                          ("attn_ctx512", lambda: kbench.attention_case(hip, 512)),
                          ("attn_ctx4096", lambda: kbench.attention_case(hip, 4096)),
                          ("attn_ctx32768", lambda: kbench.attention_case(hip, 32768)),
+                         ("attn_prefill_512tok_at_3584", lambda: kbench.attn_prefill_case(hip)),
                          ("deltanet_1024tok", lambda: kbench.deltanet_case(hip)),
                          ("deltanet_1024tok_chunked", lambda: kbench.deltanet_case(hip, chunked=True))):
             r = fn()
-            kernels[name] = {k: r[k] for k in ("us", "GBs", "TFLOPs", "frac") if k in r}
+            kernels[name] = {k: r[k] for k in ("us", "GBs", "TFLOPs", "TOPs", "frac") if k in r}
             log(f"kernel {name}: {kernels[name]}")
 
     cpu = None

@@ -1,0 +1,298 @@
+// attention_prefill.hip — causal INT8 attention of a prompt chunk (gfx950).
+//
+// Query token t of the chunk sits at position pos0 + t and attends over cache
+// positions 0 .. pos0 + t of its sequence (the chunk's own K/V rows are
+// appended first), per head exactly the decode attention of
+// echo-core-zig/src/inference/engine.zig:563-616: q head h reads kv head
+// h % n_kv, s_p = q.K_p * ks_p / sqrt(256), softmax, o = sum_p a_p V_p vs_p.
+//
+// One workgroup serves QB = 32/G query tokens x the G query heads of one kv
+// head (32 query rows) and walks the key blocks of 64 positions up to its last
+// token once: each block's K and V bytes are staged in LDS a single time for
+// all 32 rows (V transposed to [dim][position]).  Scores and softmax . V run
+// on v_mfma_i32_16x16x32_i8 as in the decode kernel: q and (probability x V
+// row scale) are each split into three int8 pieces (layout.hpp split_pieces),
+// so every product is an exact int32 and the pieces recombine in fp32.  The
+// A rows of a 16-row MFMA tile are 4 query rows x 4 piece slots (the fourth
+// zero), so the lanes of one DPP row hold one query row's scores, running
+// max / sum and output: the online softmax needs no LDS.  Contraction
+// indices are assigned so that each lane's share is contiguous (dims 64g ..
+// 64g+63, positions 16g .. 16g+15 for lane group g), fetched with 16-byte
+// LDS reads.
+#include "common.hpp"
+#include "layout.hpp"
+
+namespace ec {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+namespace {
+
+constexpr uint32_t kHd = 256;         // head_dim
+constexpr uint32_t kKb = 64;          // key positions per block
+constexpr uint32_t kRows = 32;        // query rows (token x head) per workgroup
+constexpr uint32_t kKs = kHd + 16;    // LDS bytes per staged K row
+constexpr uint32_t kVs = kKb / 4 + 2; // LDS dwords per V^T row (8-byte aligned, conflict-free b64 reads)
+constexpr uint32_t kPs = kKb + 8;     // LDS bytes per probability row
+
+struct PrefillLds {
+    uint8_t K[kKb][kKs];
+    uint32_t vT[kHd][kVs];
+    uint8_t P[kRows / 4][16][kPs];    // per row tile: [4 query rows x 4 piece slots][position]
+    uint8_t q[kRows][kQPieces][kHd];  // q pieces of the workgroup's query rows
+    float qs[kRows][4];               // piece steps (slot 3 unused)
+    float ks[kKb], vs[kKb];
+};
+
+__device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | (uint64_t)lo); }
+
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, lane_xor<1>(v));
+    v = fmaxf(v, lane_xor<2>(v));
+    v = fmaxf(v, lane_xor<4>(v));
+    v = fmaxf(v, lane_xor<8>(v));
+    return v;
+}
+
+}  // namespace
+
+// grid (ceil(T / (32/G)), n_kv), block 256.  Query row r (0 .. 31) is token
+// r/G of the workgroup's QB tokens and head kvh + n_kv*(r%G); row tile i (8
+// of them) holds query rows 4i .. 4i+3, wave w owns tiles 2w and 2w+1.
+template <int G>
+__global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ q, const int8_t* __restrict__ keys,
+                                                      const int8_t* __restrict__ vals,
+                                                      const float* __restrict__ kscales,
+                                                      const float* __restrict__ vscales, float* __restrict__ out,
+                                                      uint32_t T, uint32_t pos0, uint32_t n_kv) {
+    constexpr uint32_t QB = kRows / G;  // query tokens per workgroup
+    __shared__ PrefillLds L;
+    const uint32_t qb = blockIdx.x, kvh = blockIdx.y;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
+    const uint32_t n_heads = n_kv * G;
+    const uint32_t t_first = qb * QB, n_tok = min(QB, T - t_first);
+    const uint32_t last_pos = pos0 + t_first + n_tok - 1;
+    const uint32_t nkb = last_pos / kKb + 1;
+    const size_t row = (size_t)n_kv * kHd;
+    const int8_t* kb = keys + (size_t)kvh * kHd;
+    const int8_t* vb = vals + (size_t)kvh * kHd;
+
+    // ---- q pieces of the 32 rows: wave w packs rows 8w .. 8w+7, lane = 4 dims
+    for (uint32_t r = 8 * w; r < 8 * w + 8; ++r) {
+        const uint32_t tq = r / G, head = kvh + n_kv * (r % G);
+        float4 v4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (tq < n_tok) v4 = *(const float4*)(q + ((size_t)(t_first + tq) * n_heads + head) * kHd + 4 * lane);
+        const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+        float amax = fmaxf(fmaxf(fabsf(vv[0]), fabsf(vv[1])), fmaxf(fabsf(vv[2]), fabsf(vv[3])));
+        amax = wave_max(amax);
+        uint32_t pw[kQPieces] = {0u, 0u, 0u};
+        float steps[kQPieces];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            int8_t pcs[kQPieces];
+            split_pieces(vv[e], amax, pcs, steps);
+#pragma unroll
+            for (uint32_t pc = 0; pc < kQPieces; ++pc) pw[pc] |= (uint32_t)(uint8_t)pcs[pc] << (8 * e);
+        }
+#pragma unroll
+        for (uint32_t pc = 0; pc < kQPieces; ++pc) *(uint32_t*)&L.q[r][pc][4 * lane] = pw[pc];
+        if (lane == 0) *(float4*)&L.qs[r][0] = make_float4(steps[0], steps[1], steps[2], 0.f);
+    }
+
+    // ---- staging of key block b: K rows (thread = 16 bytes of one row) and V
+    // transposed (thread = 16 dims x 4 positions, 4x4 byte transposes);
+    // positions past last_pos repeat last_pos (masked in the scores)
+    u32x4 kr[4], vr[4];
+    float ksr = 0.f, vsr = 0.f;
+    auto load = [&](uint32_t b) {
+        const uint32_t p0 = b * kKb;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t i = tid + 256 * j, key = i / 16, c = i % 16;
+            const uint32_t p = min(p0 + key, last_pos);
+            kr[j] = *(const u32x4*)(kb + (size_t)p * row + 16 * c);
+        }
+        const uint32_t dg = tid % 16, kq = tid / 16;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t p = min(p0 + 4 * kq + j, last_pos);
+            vr[j] = *(const u32x4*)(vb + (size_t)p * row + 16 * dg);
+        }
+        if (tid < kKb) {
+            const uint32_t p = min(p0 + tid, last_pos);
+            ksr = kscales[(size_t)p * n_kv + kvh];
+            vsr = vscales[(size_t)p * n_kv + kvh];
+        }
+    };
+    auto store = [&]() {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t i = tid + 256 * j, key = i / 16, c = i % 16;
+            *(u32x4*)&L.K[key][16 * c] = kr[j];
+        }
+        const uint32_t dg = tid % 16, kq = tid / 16;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t w0 = vr[0][c], w1 = vr[1][c], w2 = vr[2][c], w3 = vr[3][c];
+            const uint32_t a0 = __builtin_amdgcn_perm(w1, w0, 0x05010400u), a1 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);
+            const uint32_t b0 = __builtin_amdgcn_perm(w3, w2, 0x05010400u), b1 = __builtin_amdgcn_perm(w3, w2, 0x07030602u);
+            L.vT[16 * dg + 4 * c + 0][kq] = __builtin_amdgcn_perm(b0, a0, 0x05040100u);
+            L.vT[16 * dg + 4 * c + 1][kq] = __builtin_amdgcn_perm(b0, a0, 0x07060302u);
+            L.vT[16 * dg + 4 * c + 2][kq] = __builtin_amdgcn_perm(b1, a1, 0x05040100u);
+            L.vT[16 * dg + 4 * c + 3][kq] = __builtin_amdgcn_perm(b1, a1, 0x07060302u);
+        }
+        if (tid < kKb) {
+            L.ks[tid] = ksr;
+            L.vs[tid] = vsr;
+        }
+    };
+
+    load(0);
+    __syncthreads();  // q pieces complete
+
+    // per owned tile tt (tile 2w + tt): A operand (lane (r, g): piece r%4 of
+    // query row 4i + r/4, dims 64g .. 64g+63; piece slot 3 is zero) and the
+    // lane's query row 4i + g in the D layout with its softmax state
+    u32x4 qa[2][4];
+    uint32_t my_tq[2], my_head[2], my_pos[2];
+    float qs[2][3], m[2], l[2], o[2][16];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const uint32_t i = 2 * w + tt, ar = 4 * i + r16 / 4, pc = r16 % 4;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            qa[tt][c] = pc < kQPieces ? *(const u32x4*)&L.q[ar][pc][64 * g4 + 16 * c] : u32x4{0u, 0u, 0u, 0u};
+        const uint32_t mr = 4 * i + g4;
+        my_tq[tt] = mr / G;
+        my_head[tt] = kvh + n_kv * (mr % G);
+        my_pos[tt] = pos0 + t_first + my_tq[tt];
+#pragma unroll
+        for (int pc2 = 0; pc2 < 3; ++pc2) qs[tt][pc2] = L.qs[mr][pc2];
+        m[tt] = -INFINITY;
+        l[tt] = 0.f;
+#pragma unroll
+        for (int d = 0; d < 16; ++d) o[tt][d] = 0.f;
+    }
+    constexpr float scale = 1.0f / 16.0f;  // 1/sqrt(256)
+
+    for (uint32_t b = 0; b < nkb; ++b) {
+        __syncthreads();  // the previous block's readers of K, vT are done
+        store();
+        __syncthreads();
+        if (b + 1 < nkb) load(b + 1);
+        // K operand of the 4 key tiles: lane (r, g) = position 16kt + r, dims 64g .. 64g+63
+        u32x4 kb4[4][4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) kb4[kt][c] = *(const u32x4*)&L.K[16 * kt + r16][64 * g4 + 16 * c];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const uint32_t i = 2 * w + tt;
+            // ---- scores: 4 key tiles x 8 k-steps
+            v4i C[4];
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) {
+                C[kt] = v4i{0, 0, 0, 0};
+#pragma unroll
+                for (int m8 = 0; m8 < 8; ++m8) {
+                    const u32x4 a = qa[tt][m8 / 2], bb = kb4[kt][m8 / 2];
+                    const long A = (m8 & 1) ? pack2(a.z, a.w) : pack2(a.x, a.y);
+                    const long B = (m8 & 1) ? pack2(bb.z, bb.w) : pack2(bb.x, bb.y);
+                    C[kt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, C[kt], 0, 0, 0);
+                }
+            }
+            // lane (r16 = position in key tile, g4 = query row): pieces, mask
+            float sc[4], bm = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) {
+                const uint32_t kp = b * kKb + 16 * kt + r16;
+                const float raw = (qs[tt][0] * (float)C[kt][0] + qs[tt][1] * (float)C[kt][1]) + qs[tt][2] * (float)C[kt][2];
+                sc[kt] = kp <= my_pos[tt] ? raw * L.ks[16 * kt + r16] * scale : -INFINITY;
+                bm = fmaxf(bm, sc[kt]);
+            }
+            bm = row16_max(bm);
+            const float mn = fmaxf(m[tt], bm);  // finite: position 0 is in every query's range
+            const float corr = __expf(m[tt] - mn);  // first block: exp(-inf) = 0
+            float es = 0.f, pm = 0.f, pr[4];
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) {
+                const float e = __expf(sc[kt] - mn);  // masked: 0
+                es += e;
+                pr[kt] = e * L.vs[16 * kt + r16];
+                pm = fmaxf(pm, fabsf(pr[kt]));
+            }
+            l[tt] = l[tt] * corr + row16_sum(es);
+            m[tt] = mn;
+            pm = row16_max(pm);
+#pragma unroll
+            for (int d = 0; d < 16; ++d) o[tt][d] *= corr;
+            // probability x V row scale as three int8 pieces: row 4*g4 + piece
+            // of tile i, position 16*kt + r16
+            float ps[kQPieces];
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) {
+                int8_t pcs[kQPieces];
+                split_pieces(pr[kt], pm, pcs, ps);
+#pragma unroll
+                for (uint32_t pc = 0; pc < kQPieces; ++pc) L.P[i][4 * g4 + pc][16 * kt + r16] = (uint8_t)pcs[pc];
+                L.P[i][4 * g4 + 3][16 * kt + r16] = 0;
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's P bytes are in LDS before its reads below
+            __builtin_amdgcn_wave_barrier();
+            // ---- P . V: 16 dim tiles x 2 k-steps (lane group g4: positions 16g4 .. 16g4+15)
+            const uint32_t* ap = (const uint32_t*)&L.P[i][r16][16 * g4];
+            const long A0 = pack2(ap[0], ap[1]), A1 = pack2(ap[2], ap[3]);
+#pragma unroll
+            for (int dt = 0; dt < 16; ++dt) {
+                const uint32_t* bp = &L.vT[16 * dt + r16][4 * g4];
+                v4i Cv = {0, 0, 0, 0};
+                Cv = __builtin_amdgcn_mfma_i32_16x16x32_i8(A0, pack2(bp[0], bp[1]), Cv, 0, 0, 0);
+                Cv = __builtin_amdgcn_mfma_i32_16x16x32_i8(A1, pack2(bp[2], bp[3]), Cv, 0, 0, 0);
+                o[tt][dt] += (ps[0] * (float)Cv[0] + ps[1] * (float)Cv[1]) + ps[2] * (float)Cv[2];
+            }
+        }
+    }
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        if (my_tq[tt] >= n_tok) continue;
+        const float inv = 1.0f / l[tt];
+        float* dst = out + ((size_t)(t_first + my_tq[tt]) * n_heads + my_head[tt]) * kHd;
+#pragma unroll
+        for (int dt = 0; dt < 16; ++dt) dst[16 * dt + r16] = o[tt][dt] * inv;
+    }
+}
+
+}  // namespace ec
+
+using namespace ec;
+
+extern "C" int ec_attn_prefill(const float* q, const int8_t* keys, const int8_t* vals, const float* kscales,
+                               const float* vscales, float* out, uint32_t T, int32_t pos0, uint32_t n_heads,
+                               uint32_t n_kv, uint32_t head_dim, uint32_t max_ctx, void* stream) {
+    if (T == 0) return EC_OK;
+    if (!q || !keys || !vals || !kscales || !vscales || !out || head_dim != kHd || n_kv == 0 || n_heads % n_kv ||
+        pos0 < 0 || (uint64_t)pos0 + T > max_ctx)
+        return ec_set_error(EC_ERR_ARG, "ec_attn_prefill: need head_dim 256, n_heads % n_kv == 0, pos0 + T <= max_ctx");
+    const uint32_t G = n_heads / n_kv;
+    const hipStream_t st = (hipStream_t)stream;
+    switch (G) {
+        case 1:
+            hipLaunchKernelGGL(k_attn_prefill<1>, dim3((T + 31) / 32, n_kv), dim3(256), 0, st, q, keys, vals, kscales,
+                               vscales, out, T, (uint32_t)pos0, n_kv);
+            break;
+        case 2:
+            hipLaunchKernelGGL(k_attn_prefill<2>, dim3((T + 15) / 16, n_kv), dim3(256), 0, st, q, keys, vals, kscales,
+                               vscales, out, T, (uint32_t)pos0, n_kv);
+            break;
+        case 4:
+            hipLaunchKernelGGL(k_attn_prefill<4>, dim3((T + 7) / 8, n_kv), dim3(256), 0, st, q, keys, vals, kscales,
+                               vscales, out, T, (uint32_t)pos0, n_kv);
+            break;
+        default:
+            return ec_set_error(EC_ERR_UNSUPPORTED, "ec_attn_prefill: n_heads / n_kv must be 1, 2 or 4");
+    }
+    EC_CHECK_LAUNCH();
+    return EC_OK;
+}

@@ -238,6 +238,36 @@ def deltanet_case(hip, T=1024, n_v=32, d=128, iters=5, seed=0, chunked=False):
 INT8_PEAK_TOPS = 5000.0
 
 
+def attn_prefill_case(hip, T=512, pos0=3584, n_heads=16, n_kv=4, iters=10, seed=0):
+    """Causal attention of a T-token prompt chunk at positions pos0 .. pos0+T-1
+    (ec_attn_prefill) over an int8 cache; int8 TOP/s counts the MFMA work
+    (QK^T and softmax . V, three int8 pieces of q and of p each:
+    2 * 2 * 3 * 256 ops per query row and visible position)."""
+    hd, max_ctx = 256, pos0 + T
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    keys = torch.randint(-127, 128, (max_ctx * n_kv * hd,), generator=g, device="cuda", dtype=torch.int32).to(torch.int8)
+    vals = torch.randint(-127, 128, (max_ctx * n_kv * hd,), generator=g, device="cuda", dtype=torch.int32).to(torch.int8)
+    ks = torch.rand(max_ctx * n_kv, generator=g, device="cuda") * 0.02
+    vs = torch.rand(max_ctx * n_kv, generator=g, device="cuda") * 0.02
+    q = torch.randn(T, n_heads * hd, generator=g, device="cuda")
+    out = torch.empty_like(q)
+    st = torch.cuda.current_stream().cuda_stream
+    hip.attn_prefill(q, keys, vals, ks, vs, out, T, pos0, n_heads, n_kv, hd, max_ctx, stream=st)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(iters):
+        hip.attn_prefill(q, keys, vals, ks, vs, out, T, pos0, n_heads, n_kv, hd, max_ctx, stream=st)
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / iters
+    visible = T * pos0 + T * (T + 1) / 2  # (query, position) pairs
+    ops = 2 * 2 * 3 * hd * n_heads * visible
+    tops = ops / (us * 1e-6) / 1e12
+    return {"kernel": "k_attn_prefill", "T": T, "pos0": pos0, "us": round(us, 2), "TOPs": round(tops, 1),
+            "frac": round(tops / INT8_PEAK_TOPS, 4)}
+
+
 def gemm_case(hip, fmt, N, K, M=512, iters=20, seed=0):
     """Prefill GEMM (M tokens x N rows x K) on int8 MFMA over a >= 512 MB weight
     rotation; reports int8 TOP/s (2*M*N*K ops) and the fraction of the dense

@@ -1026,10 +1026,21 @@ int prefill_chunk(ec_engine* e, Lane& L, uint32_t s, uint32_t T, uint32_t p) {
             EC_TRY(ec_glue_qk_rope_append(L.proj, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn, e->inv_freq, L.pos,
                                           L.n, nullptr, nullptr, keys, vals, ks, vs, L.ctx, T, 0, c.max_ctx,
                                           c.n_heads, c.n_kv, c.head_dim, st));
-            for (uint32_t s0 = 0; s0 < T; s0 += ec_engine::kPrefillAttnSlots) {
-                const uint32_t n = std::min(T - s0, ec_engine::kPrefillAttnSlots);
-                EC_TRY(ec_attn_decode(L.n + (size_t)s0 * e->q_dim, keys, vals, ks, vs, L.attn + (size_t)s0 * e->q_dim,
-                                      L.ctx + s0, n, 0, c.n_heads, c.n_kv, c.head_dim, c.max_ctx, L.ws, st));
+            // causal attention of the chunk's T queries (positions p .. p+T-1)
+            // over the sequence's cache, one pass per 32/G query tokens
+            const uint32_t G = c.n_heads / c.n_kv;
+            if (G == 1 || G == 2 || G == 4) {
+                EC_TRY(ec_attn_prefill(L.n, keys, vals, ks, vs, L.attn, T, (int32_t)p, c.n_heads, c.n_kv,
+                                       c.head_dim, c.max_ctx, st));
+            } else {
+                // other group sizes: the decode kernel with the chunk's tokens
+                // as slots sharing the cache (ctx = position + 1)
+                for (uint32_t s0 = 0; s0 < T; s0 += ec_engine::kPrefillAttnSlots) {
+                    const uint32_t n = std::min(T - s0, ec_engine::kPrefillAttnSlots);
+                    EC_TRY(ec_attn_decode(L.n + (size_t)s0 * e->q_dim, keys, vals, ks, vs,
+                                          L.attn + (size_t)s0 * e->q_dim, L.ctx + s0, n, 0, c.n_heads, c.n_kv,
+                                          c.head_dim, c.max_ctx, L.ws, st));
+                }
             }
             EC_TRY(gemm_rows(L, y.w_out, L.attn, L.x, T, H, 1));
         }

@@ -168,6 +168,17 @@ int ec_attn_decode_packed(const void* q_packed, const float* q_scales, const int
                           uint32_t n_seq, uint64_t seq_stride, uint32_t n_heads, uint32_t n_kv, uint32_t max_ctx,
                           void* ws, void* stream);
 
+/* Causal attention of a prompt chunk over one sequence's cache: query token t
+ * (q, out: [T][n_heads][256]) sits at position pos0 + t and attends over
+ * positions 0 .. pos0 + t of keys/vals/kscales/vscales (the layout above, the
+ * chunk's rows already appended), each head as ec_attn_decode computes it.
+ * One pass over the cache per group of 32/G query tokens and kv head, QK^T and
+ * softmax . V on int8 MFMA.  head_dim 256, n_heads / n_kv in {1, 2, 4},
+ * pos0 + T <= max_ctx. */
+int ec_attn_prefill(const float* q, const int8_t* keys, const int8_t* vals, const float* kscales,
+                    const float* vscales, float* out, uint32_t T, int32_t pos0, uint32_t n_heads, uint32_t n_kv,
+                    uint32_t head_dim, uint32_t max_ctx, void* stream);
+
 /* --------------------------------------------------------------- delta-net
  * Gated delta rule for T tokens of n_seq sequences (qwen_linear.zig:207-250):
  *   S <- decay*S; kv = S^T k; delta = (v - kv)*beta; S += k (x) delta; o = S^T q/sqrt(d_k)
