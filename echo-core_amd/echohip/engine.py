@@ -22,6 +22,11 @@ MATRICES = (T_W_IN, T_W_OUT, T_W_GATE, T_W_UP, T_W_DOWN)
  B_LOGITS, B_TOK, B_POS, B_GEN, B_CTX, B_INV_FREQ, B_HN, B_CORE, B_FF, B_ACT4_H, B_ACT4_V, B_ACT4_Q,
  B_ACT4_F) = range(26)
 ACT4_BUFFERS = (B_ACT4_H, B_ACT4_V, B_ACT4_Q, B_ACT4_F)
+# chunked prefill trace operations and lane-0 chunk buffers
+(OP_PF_EMBED, OP_PF_NORM, OP_PF_GEMM_IN, OP_PF_CONV, OP_PF_DELTA, OP_PF_GATED_NORM, OP_PF_GEMM_OUT,
+ OP_PF_ROPE_APPEND, OP_PF_ATTN, OP_PF_GEMM_GU, OP_PF_SWIGLU, OP_PF_GEMM_DOWN, OP_PF_HEAD) = range(20, 33)
+(B_PF_X, B_PF_N, B_PF_PROJ, B_PF_Q, B_PF_K, B_PF_V, B_PF_DEC, B_PF_BETA, B_PF_CORE, B_PF_GU, B_PF_ATTN, B_PF_TOK,
+ B_PF_ACT1) = range(30, 43)
 
 
 def gguf_row_bytes(fmt: int, K: int) -> int:
@@ -107,6 +112,7 @@ class Engine:
         L.ec_engine_profile_matvecs.argtypes = [vp, u32, C.POINTER(u32), C.POINTER(C.c_double),
                                                 C.POINTER(C.c_double)]
         L.ec_engine_step_traced.argtypes = [vp, _TRACE_FN, vp]
+        L.ec_engine_prefill_traced.argtypes = [vp, u32, vp, u32, i32, _TRACE_FN, vp]
         L.ec_engine_buffer.argtypes = [vp, i32, C.POINTER(vp), C.POINTER(C.c_size_t)]
         L.ec_engine_set_format.argtypes = [vp, i32, i32, i32]
         L.ec_engine_get_format.argtypes = [vp, i32, i32]
@@ -266,6 +272,26 @@ class Engine:
             raise err[0]
         self._check(rc, "step_traced")
 
+    def prefill_traced(self, seq: int, tokens, pos0: int, fn):
+        """ec_engine_prefill of one sequence with fn(event) called before and
+        after every launch (ec_engine_prefill_traced)."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        err = []
+
+        def cb(_user, ev):
+            if err:
+                return
+            try:
+                e = ev.contents
+                fn(TraceEvent(e.op, e.layer, e.phase, e.nparts, e.x_in, e.x_out))
+            except BaseException as x:  # noqa: BLE001 (re-raised after the prefill)
+                err.append(x)
+        c_cb = _TRACE_FN(cb)
+        rc = self.L.ec_engine_prefill_traced(self.h, seq, t.ctypes.data, t.size, pos0, c_cb, None)
+        if err:
+            raise err[0]
+        self._check(rc, "prefill_traced")
+
     def buffer(self, which: int):
         """(device address, bytes) of a step buffer (ec_engine_buffer)."""
         p, n = C.c_void_p(), C.c_size_t()
@@ -283,17 +309,19 @@ class Engine:
             self.hip.copy(out, p + offset * isz, out.nbytes)
         return out
 
-    def read_act(self, which: int, K: int):
+    def read_act(self, which: int, K: int, M: int | None = None, fmt: int | None = None):
         """An activation buffer (ec_quantize_act layout, M = max_batch; Q4_K for
         the B_ACT4_* buffers, Q8_0 otherwise) as (xq int8 [B][K], xd fp32
         [B][K/32]); Q4_K values in the quantizer's sub-block order."""
         import torch
         p, n = self.buffer(which)
         assert n, f"step buffer {which} is not allocated"
-        B = self.cfg.max_batch
+        B = self.cfg.max_batch if M is None else M
         xq = torch.empty(B * K, dtype=torch.int8, device="cuda")
         xd = torch.empty(B * (K // 32), dtype=torch.float32, device="cuda")
-        self.hip.act_unpack(Q4_K if which in ACT4_BUFFERS else Q8_0, p, xq, xd, B, K)
+        if fmt is None:
+            fmt = Q4_K if which in ACT4_BUFFERS else Q8_0
+        self.hip.act_unpack(fmt, p, xq, xd, B, K)
         torch.cuda.synchronize()
         return xq.cpu().numpy().reshape(B, K), xd.cpu().numpy().reshape(B, K // 32)
 

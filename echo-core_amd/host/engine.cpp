@@ -994,45 +994,53 @@ int prefill_chunk(ec_engine* e, Lane& L, uint32_t s, uint32_t T, uint32_t p) {
     const ec_engine_cfg& c = e->c;
     const uint32_t H = e->H, F = e->F;
     hipStream_t st = L.st;
-    EC_TRY(ec_glue_embed_fmt(e->embed_fmt, e->embed, L.tok, L.x, T, H, c.vocab, st));
+    // every launch goes through launch() for ec_engine_prefill_traced (lane 0
+    // runs on the engine stream); without a callback it is a plain call
+#define EC_PF(op, layer, xin, xout, call) \
+    EC_TRY(launch(e, op, layer, 0, xin, xout, [&] { return (call); }))
+    EC_PF(EC_OP_PF_EMBED, -1, EC_B_PF_TOK, EC_B_PF_X, ec_glue_embed_fmt(e->embed_fmt, e->embed, L.tok, L.x, T, H, c.vocab, st));
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         Layer& y = e->L[l];
-        EC_TRY(ec_glue_rmsnorm_rows(L.x, y.attn_norm, L.n, T, H, st));
+        const int li = (int)l;
+        EC_PF(EC_OP_PF_NORM, li, EC_B_PF_X, EC_B_PF_N, ec_glue_rmsnorm_rows(L.x, y.attn_norm, L.n, T, H, st));
         if (!y.attn) {
             const uint32_t Nin = e->nin_delta;
-            EC_TRY(gemm_rows(L, y.w_in, L.n, L.proj, T, Nin, 0));
+            EC_PF(EC_OP_PF_GEMM_IN, li, EC_B_PF_N, EC_B_PF_PROJ, gemm_rows(L, y.w_in, L.n, L.proj, T, Nin, 0));
             float* ring = y.conv_state + (size_t)s * c.conv_kernel * e->conv_dim;
             float* state = y.ssm_state + (size_t)s * e->n_v * 128 * 128;
-            EC_TRY(ec_glue_conv_gates_chunk(L.proj, Nin, ring, y.conv_w, y.a_log, y.dt_bias, L.q, L.k, L.v, L.dec,
-                                            L.beta, T, p, e->n_k, e->n_v, c.conv_kernel, st));
+            EC_PF(EC_OP_PF_CONV, li, EC_B_PF_PROJ, EC_B_PF_Q,
+                  ec_glue_conv_gates_chunk(L.proj, Nin, ring, y.conv_w, y.a_log, y.dt_bias, L.q, L.k, L.v, L.dec,
+                                           L.beta, T, p, e->n_k, e->n_v, c.conv_kernel, st));
             // chunked scan from 128 tokens on (MI355X, 32 heads: 64 tokens 21 us
             // token loop vs 29 us chunked; 512 tokens 130 vs 71 us)
-            if (T >= kChunkedDeltaMin)
-                EC_TRY(ec_deltanet_chunked(state, L.q, L.k, L.v, L.dec, L.beta, L.core, T, 1, e->n_v, e->n_k, 128, 128,
-                                           nullptr, L.dnws, st));
-            else
-                EC_TRY(ec_deltanet(state, L.q, L.k, L.v, L.dec, L.beta, L.core, T, 1, e->n_v, e->n_k, 128, 128,
-                                   nullptr, st));
-            EC_TRY(ec_glue_gated_norm_rows(L.core, L.proj, Nin, e->conv_dim, y.ssm_norm, L.n, T, e->n_v, st));
-            EC_TRY(gemm_rows(L, y.w_out, L.n, L.x, T, H, 1));
+            EC_PF(EC_OP_PF_DELTA, li, EC_B_PF_Q, EC_B_PF_CORE,
+                  T >= kChunkedDeltaMin
+                      ? ec_deltanet_chunked(state, L.q, L.k, L.v, L.dec, L.beta, L.core, T, 1, e->n_v, e->n_k, 128,
+                                            128, nullptr, L.dnws, st)
+                      : ec_deltanet(state, L.q, L.k, L.v, L.dec, L.beta, L.core, T, 1, e->n_v, e->n_k, 128, 128,
+                                    nullptr, st));
+            EC_PF(EC_OP_PF_GATED_NORM, li, EC_B_PF_CORE, EC_B_PF_N,
+                  ec_glue_gated_norm_rows(L.core, L.proj, Nin, e->conv_dim, y.ssm_norm, L.n, T, e->n_v, st));
+            EC_PF(EC_OP_PF_GEMM_OUT, li, EC_B_PF_N, EC_B_PF_X, gemm_rows(L, y.w_out, L.n, L.x, T, H, 1));
         } else {
             const uint32_t Nin = e->nin_attn;
-            EC_TRY(gemm_rows(L, y.w_in, L.n, L.proj, T, Nin, 0));
+            EC_PF(EC_OP_PF_GEMM_IN, li, EC_B_PF_N, EC_B_PF_PROJ, gemm_rows(L, y.w_in, L.n, L.proj, T, Nin, 0));
             int8_t* keys = y.keys + (size_t)s * e->seq_stride;
             int8_t* vals = y.vals + (size_t)s * e->seq_stride;
             float* ks = y.ks + (size_t)s * c.max_ctx * c.n_kv;
             float* vs = y.vs + (size_t)s * c.max_ctx * c.n_kv;
             // slots = the chunk's tokens sharing sequence s's cache (seq_stride 0)
-            EC_TRY(ec_glue_qk_rope_append(L.proj, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn, e->inv_freq, L.pos,
-                                          L.n, nullptr, nullptr, keys, vals, ks, vs, L.ctx, T, 0, c.max_ctx,
-                                          c.n_heads, c.n_kv, c.head_dim, st));
+            EC_PF(EC_OP_PF_ROPE_APPEND, li, EC_B_PF_PROJ, EC_B_PF_N,
+                  ec_glue_qk_rope_append(L.proj, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn, e->inv_freq, L.pos,
+                                         L.n, nullptr, nullptr, keys, vals, ks, vs, L.ctx, T, 0, c.max_ctx,
+                                         c.n_heads, c.n_kv, c.head_dim, st));
             // causal attention of the chunk's T queries (positions p .. p+T-1)
             // over the sequence's cache, one pass per 32/G query tokens
             const uint32_t G = c.n_heads / c.n_kv;
-            if (G == 1 || G == 2 || G == 4) {
-                EC_TRY(ec_attn_prefill(L.n, keys, vals, ks, vs, L.attn, T, (int32_t)p, c.n_heads, c.n_kv,
-                                       c.head_dim, c.max_ctx, st));
-            } else {
+            EC_PF(EC_OP_PF_ATTN, li, EC_B_PF_N, EC_B_PF_ATTN, [&]() -> int {
+                if (G == 1 || G == 2 || G == 4)
+                    return ec_attn_prefill(L.n, keys, vals, ks, vs, L.attn, T, (int32_t)p, c.n_heads, c.n_kv,
+                                           c.head_dim, c.max_ctx, st);
                 // other group sizes: the decode kernel with the chunk's tokens
                 // as slots sharing the cache (ctx = position + 1)
                 for (uint32_t s0 = 0; s0 < T; s0 += ec_engine::kPrefillAttnSlots) {
@@ -1041,14 +1049,16 @@ int prefill_chunk(ec_engine* e, Lane& L, uint32_t s, uint32_t T, uint32_t p) {
                                           L.attn + (size_t)s0 * e->q_dim, L.ctx + s0, n, 0, c.n_heads, c.n_kv,
                                           c.head_dim, c.max_ctx, L.ws, st));
                 }
-            }
-            EC_TRY(gemm_rows(L, y.w_out, L.attn, L.x, T, H, 1));
+                return EC_OK;
+            }());
+            EC_PF(EC_OP_PF_GEMM_OUT, li, EC_B_PF_ATTN, EC_B_PF_X, gemm_rows(L, y.w_out, L.attn, L.x, T, H, 1));
         }
-        EC_TRY(ec_glue_rmsnorm_rows(L.x, y.ffn_norm, L.n, T, H, st));
-        EC_TRY(gemm_rows(L, y.w_gu, L.n, L.gu, T, 2 * F, 0));
-        EC_TRY(ec_glue_swiglu_rows(L.gu, L.n, T, F, st));
-        EC_TRY(gemm_rows(L, y.w_down, L.n, L.x, T, H, 1));
+        EC_PF(EC_OP_PF_NORM, li, EC_B_PF_X, EC_B_PF_N, ec_glue_rmsnorm_rows(L.x, y.ffn_norm, L.n, T, H, st));
+        EC_PF(EC_OP_PF_GEMM_GU, li, EC_B_PF_N, EC_B_PF_GU, gemm_rows(L, y.w_gu, L.n, L.gu, T, 2 * F, 0));
+        EC_PF(EC_OP_PF_SWIGLU, li, EC_B_PF_GU, EC_B_PF_N, ec_glue_swiglu_rows(L.gu, L.n, T, F, st));
+        EC_PF(EC_OP_PF_GEMM_DOWN, li, EC_B_PF_N, EC_B_PF_X, gemm_rows(L, y.w_down, L.n, L.x, T, H, 1));
     }
+#undef EC_PF
     return EC_OK;
 }
 
@@ -1075,14 +1085,16 @@ int prefill_step(ec_engine* e, Lane& L, PrefillJob& j) {
     // the last token's logits and greedy next token; pos[seq] = pos0 + n
     const int32_t last = j.pos0 + (int32_t)j.n - 1;
     const float* xl = L.x + (size_t)(T - 1) * e->H;
-    if (e->lm_head.fmt == EC_Q4_K) {
-        EC_TRY(ec_glue_rmsnorm_rows(xl, e->final_norm, L.n, 1, e->H, L.st));
-        EC_TRY(ec_quantize_act(EC_Q4_K, L.n, L.act1, 1, e->H, L.st));
-    } else {
-        EC_TRY(ec_glue_rmsnorm_quant(xl, e->final_norm, L.act1, 1, e->H, L.st));
-    }
-    EC_TRY(ec_matvec(e->lm_head.fmt, e->lm_head.tiled, L.act1, e->logits + (size_t)j.seq * e->c.vocab, 1, e->c.vocab,
-                     e->H, e->c.vocab, 0, L.st));
+    EC_TRY(launch(e, EC_OP_PF_HEAD, -1, 0, EC_B_PF_X, EC_B_LOGITS, [&]() -> int {
+        if (e->lm_head.fmt == EC_Q4_K) {
+            EC_TRY(ec_glue_rmsnorm_rows(xl, e->final_norm, L.n, 1, e->H, L.st));
+            EC_TRY(ec_quantize_act(EC_Q4_K, L.n, L.act1, 1, e->H, L.st));
+        } else {
+            EC_TRY(ec_glue_rmsnorm_quant(xl, e->final_norm, L.act1, 1, e->H, L.st));
+        }
+        return ec_matvec(e->lm_head.fmt, e->lm_head.tiled, L.act1, e->logits + (size_t)j.seq * e->c.vocab, 1,
+                         e->c.vocab, e->H, e->c.vocab, 0, L.st);
+    }));
     EC_HIP(hipMemcpyAsync(e->pos + j.seq, &last, 4, hipMemcpyHostToDevice, L.st));
     EC_TRY(ec_glue_argmax_advance(e->logits + (size_t)j.seq * e->c.vocab, e->c.vocab, e->gen + j.seq,
                                   e->tok + j.seq, e->pos + j.seq, 1, e->c.max_ctx, L.st));
@@ -1138,6 +1150,19 @@ extern "C" int ec_engine_prefill(ec_engine* e, uint32_t seq, const int32_t* toke
     EC_TRY(check_prefill_args(e, seq, tokens, n, pos0, "ec_engine_prefill"));
     std::vector<PrefillJob> jobs{PrefillJob{seq, n, tokens, pos0}};
     return prefill_run(e, jobs, 1);
+}
+
+extern "C" int ec_engine_prefill_traced(ec_engine* e, uint32_t seq, const int32_t* tokens, uint32_t n, int32_t pos0,
+                                        ec_trace_fn cb, void* user) {
+    EC_TRY(check_prefill_args(e, seq, tokens, n, pos0, "ec_engine_prefill_traced"));
+    if (!cb) return ec_set_error(EC_ERR_ARG, "ec_engine_prefill_traced: null callback");
+    std::vector<PrefillJob> jobs{PrefillJob{seq, n, tokens, pos0}};
+    e->trace_cb = cb;
+    e->trace_user = user;
+    const int rc = prefill_run(e, jobs, 1);
+    e->trace_cb = nullptr;
+    e->trace_user = nullptr;
+    return rc;
 }
 
 extern "C" int ec_engine_prefill_batch(ec_engine* e, uint32_t n_seqs, const uint32_t* seqs,
@@ -1242,7 +1267,32 @@ extern "C" int ec_engine_buffer(ec_engine* e, int which, void** dev, size_t* byt
             break;
         case EC_B_ACT4_Q: p = e->act4_q, n = e->q4 ? ec_act_bytes(EC_Q4_K, e->B, e->q_dim) : 0; break;
         case EC_B_ACT4_F: p = e->act4_f, n = e->q4 && e->F % 256 == 0 ? ec_act_bytes(EC_Q4_K, e->B, e->F) : 0; break;
-        default: return ec_set_error(EC_ERR_ARG, "ec_engine_buffer: unknown buffer id");
+        default: {
+            // chunk buffers of prefill lane 0 (none before the first prefill)
+            const ec_engine::PrefillLane& L = e->pf[0];
+            const size_t C = ec_engine::kPrefillChunk * 4;
+            const size_t wide = std::max({(size_t)e->H, (size_t)e->F, (size_t)e->value_dim, (size_t)e->q_dim});
+            const bool r = L.ready, d = r && e->value_dim;
+            switch (which) {
+                case EC_B_PF_X: p = L.x, n = r ? C * e->H : 0; break;
+                case EC_B_PF_N: p = L.n, n = r ? C * wide : 0; break;
+                case EC_B_PF_PROJ: p = L.proj, n = r ? C * e->nin_max : 0; break;
+                case EC_B_PF_Q: p = L.q, n = d ? C * e->key_dim : 0; break;
+                case EC_B_PF_K: p = L.k, n = d ? C * e->key_dim : 0; break;
+                case EC_B_PF_V: p = L.v, n = d ? C * e->value_dim : 0; break;
+                case EC_B_PF_DEC: p = L.dec, n = d ? C * e->n_v : 0; break;
+                case EC_B_PF_BETA: p = L.beta, n = d ? C * e->n_v : 0; break;
+                case EC_B_PF_CORE: p = L.core, n = d ? C * e->value_dim : 0; break;
+                case EC_B_PF_GU: p = L.gu, n = r ? C * 2 * e->F : 0; break;
+                case EC_B_PF_ATTN: p = L.attn, n = r ? C * e->q_dim : 0; break;
+                case EC_B_PF_TOK: p = L.tok, n = r ? C : 0; break;
+                case EC_B_PF_ACT1:
+                    p = L.act1, n = r ? ec_act_bytes(e->lm_head.fmt == EC_Q4_K ? EC_Q4_K : EC_Q8_0, 1, e->H) : 0;
+                    break;
+                default: return ec_set_error(EC_ERR_ARG, "ec_engine_buffer: unknown buffer");
+            }
+            if (!r) p = nullptr;
+        }
     }
     *dev = p;
     *bytes = n;

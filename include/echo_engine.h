@@ -175,6 +175,21 @@ enum {
     EC_OP_LM_HEAD = 11,    /* ACT_H -> LOGITS */
     EC_OP_ARGMAX = 12,     /* LOGITS, POS -> GEN, TOK, POS */
     EC_OP_NORM_ROWS = 13,  /* x_in -> HN: the fp32 RMSNorm rows a Q4_K consumer quantizes */
+    /* chunked prefill (ec_engine_prefill_traced), rows = the chunk's T tokens,
+       buffers EC_B_PF_*: */
+    EC_OP_PF_EMBED = 20,      /* PF_TOK -> PF_X */
+    EC_OP_PF_NORM = 21,       /* PF_X -> PF_N: RMSNorm rows (attention / ffn norm, then the final norm) */
+    EC_OP_PF_GEMM_IN = 22,    /* PF_N -> PF_PROJ [T][Nin]: activation quantized per row, int8-MFMA GEMM */
+    EC_OP_PF_CONV = 23,       /* PF_PROJ, conv ring -> PF_Q, PF_K, PF_V, PF_DEC, PF_BETA, ring */
+    EC_OP_PF_DELTA = 24,      /* PF_Q .. PF_BETA, recurrent state -> PF_CORE, state */
+    EC_OP_PF_GATED_NORM = 25, /* PF_CORE, PF_PROJ (z) -> PF_N */
+    EC_OP_PF_GEMM_OUT = 26,   /* PF_N (delta) or PF_ATTN -> PF_X += */
+    EC_OP_PF_ROPE_APPEND = 27,/* PF_PROJ -> PF_N (q rows), KV rows of the chunk */
+    EC_OP_PF_ATTN = 28,       /* PF_N (q rows), KV cache -> PF_ATTN */
+    EC_OP_PF_GEMM_GU = 29,    /* PF_N -> PF_GU [T][2F] */
+    EC_OP_PF_SWIGLU = 30,     /* PF_GU -> PF_N [T][F] */
+    EC_OP_PF_GEMM_DOWN = 31,  /* PF_N -> PF_X += */
+    EC_OP_PF_HEAD = 32,       /* last row of PF_X -> LOGITS row of the sequence (final RMSNorm, quantize, head) */
 };
 typedef struct {
     int op, layer;   /* layer -1: embedding, final norm, head, argmax */
@@ -187,6 +202,11 @@ typedef struct {
 } ec_trace_event;
 typedef void (*ec_trace_fn)(void* user, const ec_trace_event* ev);
 int ec_engine_step_traced(ec_engine* e, ec_trace_fn cb, void* user);
+/* ec_engine_prefill of one sequence with cb called around every launch (one
+ * lane, so chunks run in order); layer -1 for the embedding and the head.
+ * The chunk buffers are EC_B_PF_* (rows = up to 512 tokens). */
+int ec_engine_prefill_traced(ec_engine* e, uint32_t seq, const int32_t* tokens, uint32_t n, int32_t pos0,
+                             ec_trace_fn cb, void* user);
 
 /* Device address and size of one of the engine's step buffers (activation
  * buffers in the ec_quantize_act layout, M = max_batch). */
@@ -197,6 +217,10 @@ enum {
     /* inputs of Q4_K matrices (present once a matrix is Q4_K): fp32 rows and their Q4_K activations */
     EC_B_HN = 19, EC_B_CORE = 20, EC_B_FF = 21, EC_B_ACT4_H = 22, EC_B_ACT4_V = 23, EC_B_ACT4_Q = 24,
     EC_B_ACT4_F = 25,
+    /* chunked prefill, lane 0 (allocated by the first prefill): fp32 rows [512][...] */
+    EC_B_PF_X = 30, EC_B_PF_N = 31, EC_B_PF_PROJ = 32, EC_B_PF_Q = 33, EC_B_PF_K = 34, EC_B_PF_V = 35,
+    EC_B_PF_DEC = 36, EC_B_PF_BETA = 37, EC_B_PF_CORE = 38, EC_B_PF_GU = 39, EC_B_PF_ATTN = 40, EC_B_PF_TOK = 41,
+    EC_B_PF_ACT1 = 42, /* the last token's head activation (Q8_0 or Q4_K layout, M = 1) */
 };
 int ec_engine_buffer(ec_engine* e, int which, void** dev, size_t* bytes);
 

@@ -231,8 +231,9 @@ def test_queued_inputs_match_synchronous_feeding():
 def test_mixed_formats_end_to_end_matches_oracle_decoder(oc):
     """The mixed-format small model, one sequence, 8 greedy steps on the GPU
     graph and on the oracle's decoder (int8 activations, the same per-tensor
-    formats): logits within 5e-2 relative L2 (per-operation parity is the
-    gate; this bounds the accumulation of int8 rounding-boundary flips)."""
+    formats): logits within 1e-3 relative L2 at every step (measured
+    <= 4e-7: no int8 activation of this trajectory sits on a rounding
+    boundary; per-operation parity is the gate for every operation)."""
     from echohip.engine import Engine
     cfg = small_config(max_batch=1, max_ctx=16)
     m = make_model(cfg, seed=31, fmts=MIXED_FMTS)
@@ -250,7 +251,7 @@ def test_mixed_formats_end_to_end_matches_oracle_decoder(oc):
         errs.append(rel_l2(got, ref))
         tok = int(np.argmax(ref))
     print("per-step logits rel_l2", " ".join(f"{e:.1e}" for e in errs))
-    assert max(errs) < 5e-2
+    assert max(errs) < 1e-3
     eng.close()
 
 

@@ -152,7 +152,8 @@ def _fp16_vectors(m):
 def test_gguf_mixed_formats_load_matches_upload_and_oracle(tmp_path, oc):
     """Q4_K and Q8_0 matrices, F16 embedding and F16 vectors: the loaded engine
     holds the same bytes and formats as the uploaded one, decodes bit-identical
-    logits, and stays within 5e-2 of the oracle decoder on the same formats."""
+    logits, and stays within 1e-3 of the oracle decoder on the same formats
+    at every step (measured <= 2.4e-4)."""
     from echohip.engine import (T_A_LOG, T_ATTN_NORM, T_CONV_W, T_DT_BIAS, T_EMBED, T_FFN_NORM, T_FINAL_NORM, T_K_NORM,
                                 T_LM_HEAD, T_Q_NORM, T_SSM_NORM, T_W_DOWN, T_W_GATE, T_W_IN, T_W_OUT, T_W_UP, Engine)
     from echohip.gguf import GGUF
@@ -185,7 +186,7 @@ def test_gguf_mixed_formats_load_matches_upload_and_oracle(tmp_path, oc):
         errs.append(rel_l2(la[step][0], ref))
         tok = int(np.argmax(la[step][0]))
     print("GGUF mixed model vs oracle, per-step logits rel_l2", " ".join(f"{e:.1e}" for e in errs))
-    assert max(errs) < 5e-2
+    assert max(errs) < 1e-3
     a.close()
     b.close()
 

@@ -6,17 +6,19 @@
 * The fp32 row ops equal their formulas (engine.zig:783-792, core/math.zig:35-37,
   qwen_linear.zig:252-257) to fp32 rounding.
 * A prefilled sequence matches the same prompt fed through the decode graph
-  one token per step (whose parity with the oracle decoder test_gpu_decoder
-  establishes): the two differ only in fp32 summation order (int8-MFMA GEMM
-  vs matvec epilogues).  A one-token prompt therefore agrees to fp32 rounding
-  (1.4e-7 measured); over longer prompts an activation that lands on an int8
-  rounding boundary flips by one quantum in one path and the difference is
-  carried by the recurrent state until it decays (measured: conv/delta states
-  within 2.4e-2, logits within 2.7e-2 over 1..1100 tokens, no step at the
-  512-token chunk boundary), so states and logits are held to the decoder
-  tests' 5e-2 bound (KV caches dequantized); prompts of 1,
-  3, 7, 25, 40 and 600 tokens (two 512-token chunks) are checked, followed by
-  decode steps on both engines.
+  one token per step.  This is a consistency check of two GPU paths; parity
+  with the oracle is established per operation for both
+  (tests/test_gpu_prefill_ops.py, tests/test_gpu_decoder.py, 1e-5 per op).
+  The two paths differ only in fp32 summation order (int8-MFMA GEMM vs
+  matvec epilogues), so a prompt agrees to fp32 rounding unless an activation
+  lands on an int8 rounding boundary in one path: it then moves by one
+  quantum and the recurrent state carries the difference until it decays.
+  Measured on MI355X: prompts of 1, 3, 7 and 25 tokens (and 7, 40 mixed)
+  agree within 2e-7; 40..1100-token prompts over four seeds differ by
+  7e-3..1.2e-2 in the logits and at most 6.9e-3 in the fp32 states.  States
+  and logits are held to PATH_TOL = 2e-2 (KV caches dequantized), the first
+  KV position within one quantum; prompts of 1, 3, 7, 25, 40 and 600 tokens
+  (two 512-token chunks), followed by decode steps on both engines.
 """
 import numpy as np
 import pytest
@@ -27,6 +29,8 @@ from echohip import synth
 from test_gpu_kernels import dev, empty, host
 
 pytestmark = pytest.mark.gpu
+
+PATH_TOL = 2e-2  # prefill vs token loop, one-quantum flips carried (measured <= 1.2e-2)
 
 
 @pytest.mark.parametrize("T,p0,zero_ring", [(7, 5, False), (2, 9, False), (6, 0, True), (3, 1, True), (1, 12, False)])
@@ -100,8 +104,8 @@ def _states(eng, cfg, seq):
 
 
 def _compare_states(a, b, cfg):
-    """fp32 states within 5e-2; KV caches compared dequantized (int8 x row
-    scale) within 5e-2, and the first position's rows (before any carried
+    """fp32 states within PATH_TOL; KV caches compared dequantized (int8 x
+    row scale) within PATH_TOL, and the first position's rows (before any carried
     difference) within one quantum."""
     from echohip.engine import S_KEYS, S_KSCALES, S_VALS, S_VSCALES
     scale_of = {S_KEYS: S_KSCALES, S_VALS: S_VSCALES}
@@ -113,10 +117,10 @@ def _compare_states(a, b, cfg):
             xb = y.reshape(cfg.max_ctx, cfg.n_kv, cfg.head_dim).astype(np.float64)
             da = xa * a[sk].reshape(cfg.max_ctx, cfg.n_kv, 1)
             db = xb * b[sk].reshape(cfg.max_ctx, cfg.n_kv, 1)
-            assert rel_l2(da, db) < 5e-2, (key, rel_l2(da, db))
+            assert rel_l2(da, db) < PATH_TOL, (key, rel_l2(da, db))
             assert np.abs(xa[0] - xb[0]).max() <= 1, key
         else:
-            assert rel_l2(x, y) < 5e-2, (key, rel_l2(x, y))
+            assert rel_l2(x, y) < PATH_TOL, (key, rel_l2(x, y))
 
 
 @pytest.mark.parametrize("lens,fmts", [((40, 7, 1), None), ((600, 3, 25), None), ((40, 7, 1), MIXED_FMTS)],
@@ -150,7 +154,8 @@ def test_prefill_matches_token_loop(lens, fmts):
     for s in range(3):
         _compare_states(_states(a, cfg, s), _states(b, cfg, s), cfg)
         la, lb = a.logits(s), last_b[s]
-        assert rel_l2(la, lb) < 5e-2, (s, rel_l2(la, lb))
+        print(f"prompt {lens[s]}: logits rel_l2 {rel_l2(la, lb):.1e}")
+        assert rel_l2(la, lb) < (1e-5 if lens[s] == 1 else PATH_TOL), (s, rel_l2(la, lb))
         top2 = np.sort(lb)[-2:]
         if top2[1] - top2[0] > 1e-2 * max(1.0, abs(top2[1])):
             assert ga[s] == gb[s]
@@ -161,7 +166,7 @@ def test_prefill_matches_token_loop(lens, fmts):
         a.step(graph=True)
         b.step(graph=True)
         for s in range(3):
-            assert rel_l2(a.logits(s), b.logits(s)) < 5e-2
+            assert rel_l2(a.logits(s), b.logits(s)) < PATH_TOL
         gb, _ = b.tokens()
     a.close()
     b.close()
