@@ -57,9 +57,14 @@ __device__ __forceinline__ float row16_max(float v) {
 
 }  // namespace
 
-// grid (ceil(T / (32/G)), n_kv), block 256.  Query row r (0 .. 31) is token
-// r/G of the workgroup's QB tokens and head kvh + n_kv*(r%G); row tile i (8
-// of them) holds query rows 4i .. 4i+3, wave w owns tiles 2w and 2w+1.
+// grid 8 * ceil(nqb * n_kv / 8) (nqb = ceil(T / (32/G)) query blocks), block
+// 256.  Workgroups are dispatched to the 8 XCDs round-robin (blockIdx % 8);
+// XCD x takes the contiguous (kv head, query block) range [x*per, (x+1)*per)
+// in kv-head-major order, so each XCD's L2 holds the K/V rows of one or two
+// kv heads instead of all of them (every query block re-reads its kv head's
+// cache).  Query row r (0 .. 31) is token r/G of the workgroup's QB tokens
+// and head kvh + n_kv*(r%G); row tile i (8 of them) holds query rows
+// 4i .. 4i+3, wave w owns tiles 2w and 2w+1.
 template <int G>
 __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ q, const int8_t* __restrict__ keys,
                                                       const int8_t* __restrict__ vals,
@@ -67,8 +72,11 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
                                                       const float* __restrict__ vscales, float* __restrict__ out,
                                                       uint32_t T, uint32_t pos0, uint32_t n_kv) {
     constexpr uint32_t QB = kRows / G;  // query tokens per workgroup
-    __shared__ PrefillLds L;
-    const uint32_t qb = blockIdx.x, kvh = blockIdx.y;
+    __shared__ __align__(16) PrefillLds L;  // 16-byte aligned: b128 / b64 LDS accesses
+    const uint32_t nqb = (T + QB - 1) / QB, total = nqb * n_kv, per = (total + 7) / 8;
+    const uint32_t wg = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    if (wg >= total) return;  // grid padding (whole workgroup, before any barrier)
+    const uint32_t qb = wg % nqb, kvh = wg / nqb;
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
     const uint32_t n_heads = n_kv * G;
     const uint32_t t_first = qb * QB, n_tok = min(QB, T - t_first);
@@ -101,8 +109,11 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
     }
 
     // ---- staging of key block b: K rows (thread = 16 bytes of one row) and V
-    // transposed (thread = 16 dims x 4 positions, 4x4 byte transposes);
-    // positions past last_pos repeat last_pos (masked in the scores)
+    // transposed (thread = 16 dims x positions kq, kq+16, kq+32, kq+48 of the
+    // block, 4x4 byte transposes): softmax . V contracts over the index
+    // 4*(position % 16) + position / 16, so that a lane's four probabilities
+    // (its position in each 16-position key tile) form one LDS dword.
+    // Positions past last_pos repeat last_pos (masked in the scores).
     u32x4 kr[4], vr[4];
     float ksr = 0.f, vsr = 0.f;
     auto load = [&](uint32_t b) {
@@ -116,7 +127,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
         const uint32_t dg = tid % 16, kq = tid / 16;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint32_t p = min(p0 + 4 * kq + j, last_pos);
+            const uint32_t p = min(p0 + kq + 16 * j, last_pos);
             vr[j] = *(const u32x4*)(vb + (size_t)p * row + 16 * dg);
         }
         if (tid < kKb) {
@@ -149,7 +160,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
     };
 
     load(0);
-    __syncthreads();  // q pieces complete
+    // piece slot 3 of every probability row stays zero
+    for (uint32_t i = tid; i < sizeof(L.P) / 4; i += 256) ((uint32_t*)&L.P[0][0][0])[i] = 0u;
+    __syncthreads();  // q pieces and the zero rows complete
 
     // per owned tile tt (tile 2w + tt): A operand (lane (r, g): piece r%4 of
     // query row 4i + r/4, dims 64g .. 64g+63; piece slot 3 is zero) and the
@@ -181,34 +194,41 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
         store();
         __syncthreads();
         if (b + 1 < nkb) load(b + 1);
-        // K operand of the 4 key tiles: lane (r, g) = position 16kt + r, dims 64g .. 64g+63
-        u32x4 kb4[4][4];
+        // ---- scores of both owned tiles: 4 key tiles x 8 k-steps each; K
+        // operand lane (r, g) = position 16kt + r, dims 64g .. 64g+63
+        v4i C[2][4];
+        {
+            u32x4 kb4[4][4];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+            for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) kb4[kt][c] = *(const u32x4*)&L.K[16 * kt + r16][64 * g4 + 16 * c];
+                for (int c = 0; c < 4; ++c) kb4[kt][c] = *(const u32x4*)&L.K[16 * kt + r16][64 * g4 + 16 * c];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int kt = 0; kt < 4; ++kt) {
+                    C[tt][kt] = v4i{0, 0, 0, 0};
+#pragma unroll
+                    for (int m8 = 0; m8 < 8; ++m8) {
+                        const u32x4 a = qa[tt][m8 / 2], bb = kb4[kt][m8 / 2];
+                        const long A = (m8 & 1) ? pack2(a.z, a.w) : pack2(a.x, a.y);
+                        const long B = (m8 & 1) ? pack2(bb.z, bb.w) : pack2(bb.x, bb.y);
+                        C[tt][kt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, C[tt][kt], 0, 0, 0);
+                    }
+                }
+        }
+        // ---- online softmax per tile; lane (r16 = position in key tile, g4 =
+        // query row): pieces, mask
+        float ps[2][kQPieces];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
             const uint32_t i = 2 * w + tt;
-            // ---- scores: 4 key tiles x 8 k-steps
-            v4i C[4];
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt) {
-                C[kt] = v4i{0, 0, 0, 0};
-#pragma unroll
-                for (int m8 = 0; m8 < 8; ++m8) {
-                    const u32x4 a = qa[tt][m8 / 2], bb = kb4[kt][m8 / 2];
-                    const long A = (m8 & 1) ? pack2(a.z, a.w) : pack2(a.x, a.y);
-                    const long B = (m8 & 1) ? pack2(bb.z, bb.w) : pack2(bb.x, bb.y);
-                    C[kt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, C[kt], 0, 0, 0);
-                }
-            }
-            // lane (r16 = position in key tile, g4 = query row): pieces, mask
             float sc[4], bm = -INFINITY;
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt) {
                 const uint32_t kp = b * kKb + 16 * kt + r16;
-                const float raw = (qs[tt][0] * (float)C[kt][0] + qs[tt][1] * (float)C[kt][1]) + qs[tt][2] * (float)C[kt][2];
+                const v4i c4 = C[tt][kt];
+                const float raw = (qs[tt][0] * (float)c4[0] + qs[tt][1] * (float)c4[1]) + qs[tt][2] * (float)c4[2];
                 sc[kt] = kp <= my_pos[tt] ? raw * L.ks[16 * kt + r16] * scale : -INFINITY;
                 bm = fmaxf(bm, sc[kt]);
             }
@@ -229,28 +249,41 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
 #pragma unroll
             for (int d = 0; d < 16; ++d) o[tt][d] *= corr;
             // probability x V row scale as three int8 pieces: row 4*g4 + piece
-            // of tile i, position 16*kt + r16
-            float ps[kQPieces];
+            // of tile i; the four key tiles' values of position r16 are bytes
+            // 0..3 of dword r16 (contraction index 4*r16 + kt)
+            uint32_t pw[kQPieces] = {0u, 0u, 0u};
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt) {
                 int8_t pcs[kQPieces];
-                split_pieces(pr[kt], pm, pcs, ps);
+                split_pieces(pr[kt], pm, pcs, ps[tt]);
 #pragma unroll
-                for (uint32_t pc = 0; pc < kQPieces; ++pc) L.P[i][4 * g4 + pc][16 * kt + r16] = (uint8_t)pcs[pc];
-                L.P[i][4 * g4 + 3][16 * kt + r16] = 0;
+                for (uint32_t pc = 0; pc < kQPieces; ++pc) pw[pc] |= (uint32_t)(uint8_t)pcs[pc] << (8 * kt);
             }
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's P bytes are in LDS before its reads below
-            __builtin_amdgcn_wave_barrier();
-            // ---- P . V: 16 dim tiles x 2 k-steps (lane group g4: positions 16g4 .. 16g4+15)
-            const uint32_t* ap = (const uint32_t*)&L.P[i][r16][16 * g4];
-            const long A0 = pack2(ap[0], ap[1]), A1 = pack2(ap[2], ap[3]);
 #pragma unroll
-            for (int dt = 0; dt < 16; ++dt) {
-                const uint32_t* bp = &L.vT[16 * dt + r16][4 * g4];
+            for (uint32_t pc = 0; pc < kQPieces; ++pc) ((uint32_t*)&L.P[i][4 * g4 + pc][0])[r16] = pw[pc];
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's P dwords are in LDS before its reads below
+        __builtin_amdgcn_wave_barrier();
+        // ---- P . V: 16 dim tiles x 2 k-steps per tile (lane group g4:
+        // contraction indices 16g4 .. 16g4+15); each V operand serves both tiles
+        long A[2][2];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const uint2* ap = (const uint2*)&L.P[2 * w + tt][r16][16 * g4];
+            const uint2 a0 = ap[0], a1 = ap[1];
+            A[tt][0] = pack2(a0.x, a0.y);
+            A[tt][1] = pack2(a1.x, a1.y);
+        }
+#pragma unroll
+        for (int dt = 0; dt < 16; ++dt) {
+            const uint2* bp = (const uint2*)&L.vT[16 * dt + r16][4 * g4];
+            const uint2 b0 = bp[0], b1 = bp[1];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
                 v4i Cv = {0, 0, 0, 0};
-                Cv = __builtin_amdgcn_mfma_i32_16x16x32_i8(A0, pack2(bp[0], bp[1]), Cv, 0, 0, 0);
-                Cv = __builtin_amdgcn_mfma_i32_16x16x32_i8(A1, pack2(bp[2], bp[3]), Cv, 0, 0, 0);
-                o[tt][dt] += (ps[0] * (float)Cv[0] + ps[1] * (float)Cv[1]) + ps[2] * (float)Cv[2];
+                Cv = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[tt][0], pack2(b0.x, b0.y), Cv, 0, 0, 0);
+                Cv = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[tt][1], pack2(b1.x, b1.y), Cv, 0, 0, 0);
+                o[tt][dt] += (ps[tt][0] * (float)Cv[0] + ps[tt][1] * (float)Cv[1]) + ps[tt][2] * (float)Cv[2];
             }
         }
     }
@@ -277,18 +310,21 @@ extern "C" int ec_attn_prefill(const float* q, const int8_t* keys, const int8_t*
         return ec_set_error(EC_ERR_ARG, "ec_attn_prefill: need head_dim 256, n_heads % n_kv == 0, pos0 + T <= max_ctx");
     const uint32_t G = n_heads / n_kv;
     const hipStream_t st = (hipStream_t)stream;
+    const uint64_t total = (uint64_t)((T + 32 / G - 1) / (32 / G)) * n_kv;
+    if (total > (1u << 28)) return ec_set_error(EC_ERR_ARG, "ec_attn_prefill: too many query blocks");
+    const dim3 grid(8 * (uint32_t)((total + 7) / 8));
     switch (G) {
         case 1:
-            hipLaunchKernelGGL(k_attn_prefill<1>, dim3((T + 31) / 32, n_kv), dim3(256), 0, st, q, keys, vals, kscales,
-                               vscales, out, T, (uint32_t)pos0, n_kv);
+            hipLaunchKernelGGL(k_attn_prefill<1>, grid, dim3(256), 0, st, q, keys, vals, kscales, vscales, out, T,
+                               (uint32_t)pos0, n_kv);
             break;
         case 2:
-            hipLaunchKernelGGL(k_attn_prefill<2>, dim3((T + 15) / 16, n_kv), dim3(256), 0, st, q, keys, vals, kscales,
-                               vscales, out, T, (uint32_t)pos0, n_kv);
+            hipLaunchKernelGGL(k_attn_prefill<2>, grid, dim3(256), 0, st, q, keys, vals, kscales, vscales, out, T,
+                               (uint32_t)pos0, n_kv);
             break;
         case 4:
-            hipLaunchKernelGGL(k_attn_prefill<4>, dim3((T + 7) / 8, n_kv), dim3(256), 0, st, q, keys, vals, kscales,
-                               vscales, out, T, (uint32_t)pos0, n_kv);
+            hipLaunchKernelGGL(k_attn_prefill<4>, grid, dim3(256), 0, st, q, keys, vals, kscales, vscales, out, T,
+                               (uint32_t)pos0, n_kv);
             break;
         default:
             return ec_set_error(EC_ERR_UNSUPPORTED, "ec_attn_prefill: n_heads / n_kv must be 1, 2 or 4");
