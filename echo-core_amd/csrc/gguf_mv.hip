@@ -39,15 +39,18 @@ __device__ __forceinline__ uint4 ld_nt16(const uint8_t* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// Rows' partial sums red[rr][0 .. ncol) -> y[r0 + rr] += sum, one wave per row.
-__device__ __forceinline__ void reduce_rows(const float* red, uint32_t ncol, uint32_t nr, float* __restrict__ y,
-                                            uint32_t r0) {
+// Rows' partial sums red[rr][0 .. ncol) -> y[r0 + rr] = y0[rr] + sum, one wave
+// per row.  y0 holds the rows' previous y values, read at kernel start (no
+// dependent global load at the end of the workgroup: 10.3 -> 9.9 us at
+// 9216 x 2560); nothing else writes these rows during the kernel.
+__device__ __forceinline__ void reduce_rows(const float* red, const float* y0, uint32_t ncol, uint32_t nr,
+                                            float* __restrict__ y, uint32_t r0) {
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
     for (uint32_t rr = w; rr < nr; rr += nw) {
         float s = 0.0f;
         for (uint32_t c = lane; c < ncol; c += 64) s += red[rr * ncol + c];
         s = wave_sum(s);
-        if (lane == 0) y[r0 + rr] += s;
+        if (lane == 0) y[r0 + rr] = y0[rr] + s;
     }
 }
 
@@ -65,6 +68,8 @@ __global__ __launch_bounds__(1024) void k_gguf_q8_0_f32(const uint8_t* __restric
     const size_t rowbytes = (size_t)nb * 34;
     const uint32_t r0 = blockIdx.x * R, nr = min(R, M - r0);
     float* red = (float*)(lds + ((R * rowbytes + 15) & ~(size_t)15));
+    float* y0 = red + (size_t)R * nb;  // previous y of the tile's rows (R <= blockDim.x)
+    const float yp = t < nr ? y[r0 + t] : 0.0f;
     const uint8_t* src = W + (size_t)r0 * rowbytes;
     const uint32_t n16 = (uint32_t)(nr * rowbytes / 16);
     uint4 v[kQ8Stage];
@@ -98,8 +103,9 @@ __global__ __launch_bounds__(1024) void k_gguf_q8_0_f32(const uint8_t* __restric
         }
         red[rr * nb + b] = d * bs;
     }
+    if (t < nr) y0[t] = yp;
     __syncthreads();
-    reduce_rows(red, nb, nr, y, r0);
+    reduce_rows(red, y0, nb, nr, y, r0);
 }
 
 // grid.x = ceil(M / R), R = RPT * P rows (RPT rows per thread, each one 16-byte
@@ -115,6 +121,8 @@ __global__ __launch_bounds__(1024) void k_gguf_q4_K_f32(const uint8_t* __restric
     const uint32_t q = t % nq, ph = t / nq, sb = q / 4, g = q % 4;
     const size_t rowbytes = (size_t)nsb * 144;
     const uint32_t r0 = blockIdx.x * R, nr = min(R, M - r0);
+    float* y0 = red + (size_t)R * nq;  // previous y of the tile's rows (R <= blockDim.x)
+    const float yp = t < nr ? y[r0 + t] : 0.0f;
     uint4 hd[RPT], q0[RPT], q1[RPT];
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
@@ -183,8 +191,9 @@ __global__ __launch_bounds__(1024) void k_gguf_q4_K_f32(const uint8_t* __restric
         red[rr * nq + q] = (d * (float)sc0) * S0 - (dmin * (float)mn0) * xs0 + (d * (float)sc1) * S1 -
                            (dmin * (float)mn1) * xs1;
     }
+    if (t < nr) y0[t] = yp;
     __syncthreads();
-    reduce_rows(red, nq, nr, y, r0);
+    reduce_rows(red, y0, nq, nr, y, r0);
 }
 
 uint32_t gcd32(uint32_t a, uint32_t b) {
@@ -218,7 +227,8 @@ int gguf_mv_fast(int fmt, const uint8_t* W, const float* x, float* y, uint32_t M
         uint32_t R = P;
         while ((R + P) * rowbytes <= (size_t)kQ8Stage * 16 * T && (R + P) * (rowbytes + 4 * nb) <= 48 * 1024) R += P;
         if (R * rowbytes > (size_t)kQ8Stage * 16 * T) return EC_ERR_UNSUPPORTED;
-        const size_t lds = ((R * rowbytes + 15) & ~(size_t)15) + (size_t)R * nb * 4;
+        const size_t lds = ((R * rowbytes + 15) & ~(size_t)15) + (size_t)R * nb * 4 + (size_t)R * 4;
+        if (R > T) return EC_ERR_UNSUPPORTED;
         hipLaunchKernelGGL(k_gguf_q8_0_f32, dim3((M + R - 1) / R), dim3(T), lds, st, W, x, y, M, nb, P, R);
         return EC_OK;
     }
@@ -232,7 +242,8 @@ int gguf_mv_fast(int fmt, const uint8_t* W, const float* x, float* y, uint32_t M
         const uint32_t rpt = (M + 2 * P - 1) / (2 * P) >= 512 ? 2 : 1;
         const uint32_t R = rpt * P;
         const dim3 grid((M + R - 1) / R), blk(P * nq);
-        const size_t lds = (size_t)R * nq * 4;
+        const size_t lds = (size_t)R * nq * 4 + (size_t)R * 4;
+        if (R > P * nq) return EC_ERR_UNSUPPORTED;
         if (rpt == 2) hipLaunchKernelGGL(k_gguf_q4_K_f32<2>, grid, blk, lds, st, W, x, y, M, nsb, P, R);
         else hipLaunchKernelGGL(k_gguf_q4_K_f32<1>, grid, blk, lds, st, W, x, y, M, nsb, P, R);
         return EC_OK;
