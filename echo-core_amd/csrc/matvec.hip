@@ -239,6 +239,17 @@ __global__ __launch_bounds__(1024) void k_mv_q8_0(const uint8_t* __restrict__ W,
 }
 
 // --------------------------------------------------------------------- Q4_K
+// The eight 6-bit (scale, min) pairs of a super-block from its 12 scale bytes
+// (q[0] = bytes 0-3, ...), four per dword: sc[0] holds sub-blocks 0-3 (byte s
+// = scale of sub-block s), sc[1] sub-blocks 4-7, mn likewise -- the unpack of
+// src/kernels/quant.cpp:222-242 done on four bytes per operation.
+__device__ __forceinline__ void q4k_scale_min4(const uint32_t (&q)[3], uint32_t (&sc)[2], uint32_t (&mn)[2]) {
+    sc[0] = q[0] & 0x3F3F3F3Fu;
+    mn[0] = q[1] & 0x3F3F3F3Fu;
+    sc[1] = (q[2] & 0x0F0F0F0Fu) | ((q[0] >> 2) & 0x30303030u);
+    mn[1] = ((q[2] >> 4) & 0x0F0F0F0Fu) | ((q[1] >> 2) & 0x30303030u);
+}
+
 __device__ __forceinline__ void q4k_scale_min(const uint32_t (&q)[3], int s, uint32_t& sc, uint32_t& m) {
     // q holds scales[0..11] little-endian: byte i = (q[i/4] >> 8*(i%4)) & 0xFF
     auto byte = [&](int i) -> uint32_t { return (q[i >> 2] >> (8 * (i & 3))) & 0xFFu; };
@@ -308,6 +319,9 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
                                      a[2].x, a[2].y, a[2].z, a[2].w, a[3].x, a[3].y, a[3].z, a[3].w};
             const float d = h2f(hdr[u].x & 0xFFFF), dmin = h2f(hdr[u].x >> 16);
             const uint32_t scb[3] = {hdr[u].y, hdr[u].z, hdr[u].w};
+            uint32_t sc4[2], mn4[2];
+            q4k_scale_min4(scb, sc4, mn4);
+            float a_sc = 0.0f, a_mn = 0.0f;  // M = 1: sum_s sc_s*dot_s*dx_s and sum_s m_s*dxs_s, scaled once
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
                 const uint32_t lo = qw[s] & 0x0F0F0F0Fu, hi = (qw[s] >> 4) & 0x0F0F0F0Fu;
@@ -319,14 +333,14 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
                         for (int r = 0; r < 4; ++r)
                             if (4 * g + r < M) dots[((size_t)(4 * g + r) * N + n) * nsb + sbi] = cc[r];
                 } else {
-                    uint32_t scv, mnv;
-                    q4k_scale_min(scb, s, scv, mnv);
-                    const float dsc = d * (float)scv, dmn = dmin * (float)mnv;
+                    const uint32_t scv = (sc4[s >> 2] >> (8 * (s & 3))) & 0xFFu;
+                    const uint32_t mnv = (mn4[s >> 2] >> (8 * (s & 3))) & 0xFFu;
                     const int e = 8 * u + s;
                     if constexpr (MT == 1) {
-                        acc[0] = fmaf((float)cc[0], dsc * xs[e], acc[0]);
-                        acc[0] = fmaf(-dmn, xms[e], acc[0]);
+                        a_sc = fmaf((float)cc[0], (float)scv * xs[e], a_sc);
+                        a_mn = fmaf((float)mnv, xms[e], a_mn);
                     } else {
+                        const float dsc = d * (float)scv, dmn = dmin * (float)mnv;
                         const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
                         const float4 dx = (4 * g < S) ? *(const float4*)(xs + e * S + 4 * g) : z4;
                         const float4 dm = (4 * g < S) ? *(const float4*)(xms + e * S + 4 * g) : z4;
@@ -339,6 +353,10 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
                         }
                     }
                 }
+            }
+            if constexpr (MT == 1 && !DOTS) {
+                acc[0] = fmaf(d, a_sc, acc[0]);
+                acc[0] = fmaf(-dmin, a_mn, acc[0]);
             }
         }
     }
@@ -480,7 +498,7 @@ __global__ void k_dequant_fp16(int fmt, const uint8_t* __restrict__ src, uint16_
 // where possible.  Q8_0: 12288 waves (EC_MV_TARGET_WAVES overrides; with the
 // decode step's split-K projections 12288 measured best of 2048 .. 32768:
 // 1.92 ms/step at 2048, 1.86 at 4096, 1.80 at 12288, 1.86 at 24576); Q4_K:
-// 4096.
+// 4096 (EC_MV_TARGET_WAVES_Q4 overrides).
 static uint32_t target_waves_q8() {
     static uint32_t v = [] {
         const char* e = getenv("EC_MV_TARGET_WAVES");
@@ -488,7 +506,13 @@ static uint32_t target_waves_q8() {
     }();
     return v;
 }
-constexpr uint32_t kTargetWavesQ4 = 4096;
+static uint32_t target_waves_q4() {
+    static uint32_t v = [] {
+        const char* e = getenv("EC_MV_TARGET_WAVES_Q4");
+        return e ? (uint32_t)atoi(e) : 4096u;
+    }();
+    return v;
+}
 
 static void plan(uint32_t n_tiles, uint32_t n_chunks, int max_gpw, int& gpw, uint32_t& nw, uint32_t target) {
     const uint32_t want = (target + n_tiles - 1) / n_tiles;  // waves per tile wanted
@@ -559,7 +583,7 @@ static void launch_q4(const void* W, const void* act, float* y, int32_t* dots, u
     const uint32_t nT = round_up(N, 16) / 16, nB = round_up(K, 256) / 256;
     int gpw;
     uint32_t nw;
-    plan(nT, nB, MT == 1 ? 3 : 1, gpw, nw, kTargetWavesQ4);
+    plan(nT, nB, MT == 1 ? 3 : 1, gpw, nw, target_waves_q4());
     switch (gpw) {
         case 1: launch_q4_g<MT, DOTS, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
         case 2: launch_q4_g<MT, DOTS, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;

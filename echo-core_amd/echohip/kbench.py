@@ -396,7 +396,8 @@ def pmc_summary(csv_path, counter):
 
 
 def pmc_cases(hip, which):
-    """Eager launches for counter collection: `attention` runs the decode
+    """Eager launches for counter collection: `matvec` runs the decode matvec
+    at M = 1 (Q8_0 9216 x 2560, Q4_K 9216 x 2560 and 2560 x 9216), `attention` runs the decode
     attention at 512 / 4096 / 32768 positions (16 query heads, 4 KV heads,
     head_dim 256, one sequence), `gemm` the M = 512 prefill GEMMs (Q8_0 and
     Q4_K, 9216 x 2560 and 2560 x 9216), PMC_LAUNCHES times each on different
@@ -423,6 +424,29 @@ def pmc_cases(hip, which):
                 hip.attn_decode(q, keys[c], vals[c], ks[c], vs[c], out, cl, 1, kv, n_heads, n_kv, hd, ctx, ws, stream=st)
                 torch.cuda.synchronize()
             del keys, vals, ks, vs
+            torch.cuda.empty_cache()
+    elif which == "matvec":
+        for fmt, N, K in ((L.Q8_0, 9216, 2560), (L.Q4_K, 9216, 2560), (L.Q4_K, 2560, 9216)):
+            if fmt == L.Q8_0:
+                Wd = torch.empty(N * K // 32 * 34, dtype=torch.uint8, device="cuda")
+                hip.fill_random(1, Wd, N * K // 32, 0, 0.02, stream=st)
+            else:
+                Wd = torch.from_numpy(synth.q4_K_blocks(0, N, K).reshape(-1)).cuda()
+            tb = hip.tiled_bytes(fmt, N, K)
+            n_copies = max(PMC_LAUNCHES, math.ceil(ROTATE_BYTES / tb) + 1)
+            tiled = torch.empty((n_copies, tb), dtype=torch.uint8, device="cuda")
+            hip.repack(fmt, Wd, tiled[0], N, K, stream=st)
+            for i in range(1, n_copies):
+                tiled[i].copy_(tiled[0])
+            x = torch.from_numpy(synth.activations(1, K)).cuda()
+            act = torch.empty(hip.act_bytes(fmt, 1, K), dtype=torch.uint8, device="cuda")
+            hip.quantize_act(fmt, x, act, 1, K, stream=st)
+            y = torch.empty(N, dtype=torch.float32, device="cuda")
+            torch.cuda.synchronize()
+            for i in range(PMC_LAUNCHES):
+                hip.matvec(fmt, tiled[(i * 7919) % n_copies], act, y, 1, N, K, stream=st)
+                torch.cuda.synchronize()
+            del Wd, tiled, x, act, y
             torch.cuda.empty_cache()
     elif which == "gemm":
         for fmt in (L.Q8_0, L.Q4_K):
