@@ -34,11 +34,16 @@ constexpr uint32_t kKb = 64;          // key positions per block
 constexpr uint32_t kRows = 32;        // query rows (token x head) per workgroup
 constexpr uint32_t kKs = kHd + 16;    // LDS bytes per staged K row
 constexpr uint32_t kVs = kKb / 4 + 2; // LDS dwords per V^T row (8-byte aligned, conflict-free b64 reads)
+// V^T row d starts at dword d*kVs + 2*(d/16): without the skew the 16 rows a
+// store instruction writes (dims 16*dg + const, dg = 0..15) would all start
+// in the same bank (16*kVs is a multiple of the 32 banks), a 16-way conflict
+// (512 tokens at 3584: 291 -> 249 us)
+__device__ __forceinline__ uint32_t vt_at(uint32_t d, uint32_t col) { return d * kVs + 2 * (d >> 4) + col; }
 constexpr uint32_t kPs = kKb + 8;     // LDS bytes per probability row
 
 struct PrefillLds {
     uint8_t K[kKb][kKs];
-    uint32_t vT[kHd][kVs];
+    uint32_t vT[kHd * kVs + 2 * (kHd / 16)];  // [dim][position quad], rows skewed (vt_at)
     uint8_t P[kRows / 4][16][kPs];    // per row tile: [4 query rows x 4 piece slots][position]
     uint8_t q[kRows][kQPieces][kHd];  // q pieces of the workgroup's query rows
     float qs[kRows][4];               // piece steps (slot 3 unused)
@@ -148,10 +153,10 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
             const uint32_t w0 = vr[0][c], w1 = vr[1][c], w2 = vr[2][c], w3 = vr[3][c];
             const uint32_t a0 = __builtin_amdgcn_perm(w1, w0, 0x05010400u), a1 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);
             const uint32_t b0 = __builtin_amdgcn_perm(w3, w2, 0x05010400u), b1 = __builtin_amdgcn_perm(w3, w2, 0x07030602u);
-            L.vT[16 * dg + 4 * c + 0][kq] = __builtin_amdgcn_perm(b0, a0, 0x05040100u);
-            L.vT[16 * dg + 4 * c + 1][kq] = __builtin_amdgcn_perm(b0, a0, 0x07060302u);
-            L.vT[16 * dg + 4 * c + 2][kq] = __builtin_amdgcn_perm(b1, a1, 0x05040100u);
-            L.vT[16 * dg + 4 * c + 3][kq] = __builtin_amdgcn_perm(b1, a1, 0x07060302u);
+            L.vT[vt_at(16 * dg + 4 * c + 0, kq)] = __builtin_amdgcn_perm(b0, a0, 0x05040100u);
+            L.vT[vt_at(16 * dg + 4 * c + 1, kq)] = __builtin_amdgcn_perm(b0, a0, 0x07060302u);
+            L.vT[vt_at(16 * dg + 4 * c + 2, kq)] = __builtin_amdgcn_perm(b1, a1, 0x05040100u);
+            L.vT[vt_at(16 * dg + 4 * c + 3, kq)] = __builtin_amdgcn_perm(b1, a1, 0x07060302u);
         }
         if (tid < kKb) {
             L.ks[tid] = ksr;
@@ -276,7 +281,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
         }
 #pragma unroll
         for (int dt = 0; dt < 16; ++dt) {
-            const uint2* bp = (const uint2*)&L.vT[16 * dt + r16][4 * g4];
+            const uint2* bp = (const uint2*)&L.vT[vt_at(16 * dt + r16, 4 * g4)];
             const uint2 b0 = bp[0], b1 = bp[1];
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {

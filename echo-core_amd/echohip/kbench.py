@@ -396,7 +396,9 @@ def pmc_summary(csv_path, counter):
 
 
 def pmc_cases(hip, which):
-    """Eager launches for counter collection: `matvec` runs the decode matvec
+    """Eager launches for counter collection: `attn_prefill` runs the causal
+    chunk attention of 512 tokens at position 3584 (16 heads, 4 KV heads),
+    `matvec` runs the decode matvec
     at M = 1 (Q8_0 9216 x 2560, Q4_K 9216 x 2560 and 2560 x 9216), `attention` runs the decode
     attention at 512 / 4096 / 32768 positions (16 query heads, 4 KV heads,
     head_dim 256, one sequence), `gemm` the M = 512 prefill GEMMs (Q8_0 and
@@ -425,6 +427,22 @@ def pmc_cases(hip, which):
                 torch.cuda.synchronize()
             del keys, vals, ks, vs
             torch.cuda.empty_cache()
+    elif which == "attn_prefill":
+        T, pos0, n_heads, n_kv, hd = 512, 3584, 16, 4, 256
+        max_ctx = pos0 + T
+        g = torch.Generator(device="cuda").manual_seed(0)
+        keys = torch.randint(-127, 128, (max_ctx * n_kv * hd,), generator=g, device="cuda", dtype=torch.int32).to(torch.int8)
+        vals = torch.randint(-127, 128, (max_ctx * n_kv * hd,), generator=g, device="cuda", dtype=torch.int32).to(torch.int8)
+        ks = torch.rand(max_ctx * n_kv, generator=g, device="cuda") * 0.02
+        vs = torch.rand(max_ctx * n_kv, generator=g, device="cuda") * 0.02
+        q = torch.randn(T, n_heads * hd, generator=g, device="cuda")
+        out = torch.empty_like(q)
+        torch.cuda.synchronize()
+        for _ in range(PMC_LAUNCHES):
+            hip.attn_prefill(q, keys, vals, ks, vs, out, T, pos0, n_heads, n_kv, hd, max_ctx, stream=st)
+            torch.cuda.synchronize()
+        del keys, vals, ks, vs, q, out
+        torch.cuda.empty_cache()
     elif which == "matvec":
         for fmt, N, K in ((L.Q8_0, 9216, 2560), (L.Q4_K, 9216, 2560), (L.Q4_K, 2560, 9216)):
             if fmt == L.Q8_0:

@@ -315,12 +315,12 @@ def test_attention_decode(hip, oc, ctxs, max_ctx, n_heads, n_kv, hd):
 
 
 @pytest.mark.parametrize("T,pos0,n_heads,n_kv", [(64, 0, 16, 4), (100, 333, 16, 4), (1, 0, 16, 4), (37, 5, 8, 4),
-                                                  (20, 64, 4, 4), (512, 3584, 16, 4)])
+                                                  (20, 64, 4, 4), (512, 3584, 16, 4), (24, 16000, 16, 4)])
 def test_attention_prefill(hip, oc, T, pos0, n_heads, n_kv):
     """Causal chunk attention (ec_attn_prefill): query t at position pos0 + t
     against the oracle's decode attention over pos0 + t + 1 positions, every
     token within 1e-5 (partial key blocks, partial query groups, GQA 4:1, 2:1
-    and 1:1, a 512-token chunk at 3584)."""
+    and 1:1, a 512-token chunk at 3584, 24 tokens after 16000 positions)."""
     import torch
     hd, max_ctx = 256, pos0 + T + 3
     ctx = pos0 + T
