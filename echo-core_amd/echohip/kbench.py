@@ -251,13 +251,14 @@ def attn_prefill_case(hip, T=512, pos0=3584, n_heads=16, n_kv=4, iters=10, seed=
     vs = torch.rand(max_ctx * n_kv, generator=g, device="cuda") * 0.02
     q = torch.randn(T, n_heads * hd, generator=g, device="cuda")
     out = torch.empty_like(q)
+    ws = torch.empty(max(hip.attn_prefill_ws_bytes(T, n_heads, max_ctx), 16), dtype=torch.uint8, device="cuda")
     st = torch.cuda.current_stream().cuda_stream
-    hip.attn_prefill(q, keys, vals, ks, vs, out, T, pos0, n_heads, n_kv, hd, max_ctx, stream=st)
+    hip.attn_prefill(q, keys, vals, ks, vs, out, T, pos0, n_heads, n_kv, hd, max_ctx, ws=ws, stream=st)
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for _ in range(iters):
-        hip.attn_prefill(q, keys, vals, ks, vs, out, T, pos0, n_heads, n_kv, hd, max_ctx, stream=st)
+        hip.attn_prefill(q, keys, vals, ks, vs, out, T, pos0, n_heads, n_kv, hd, max_ctx, ws=ws, stream=st)
     b.record()
     torch.cuda.synchronize()
     us = a.elapsed_time(b) * 1e3 / iters
@@ -437,9 +438,10 @@ def pmc_cases(hip, which):
         vs = torch.rand(max_ctx * n_kv, generator=g, device="cuda") * 0.02
         q = torch.randn(T, n_heads * hd, generator=g, device="cuda")
         out = torch.empty_like(q)
+        ws = torch.empty(max(hip.attn_prefill_ws_bytes(T, n_heads, max_ctx), 16), dtype=torch.uint8, device="cuda")
         torch.cuda.synchronize()
         for _ in range(PMC_LAUNCHES):
-            hip.attn_prefill(q, keys, vals, ks, vs, out, T, pos0, n_heads, n_kv, hd, max_ctx, stream=st)
+            hip.attn_prefill(q, keys, vals, ks, vs, out, T, pos0, n_heads, n_kv, hd, max_ctx, ws=ws, stream=st)
             torch.cuda.synchronize()
         del keys, vals, ks, vs, q, out
         torch.cuda.empty_cache()

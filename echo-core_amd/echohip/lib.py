@@ -45,7 +45,7 @@ _SIGS = {
     "ec_glue_qk_rope_append_split": [_vp, _u32, _u32, _vp, _vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                      _vp, _vp, _vp, _u32, _u64, _u32, _u32, _u32, _u32, _vp],
     "ec_deltanet": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp, _vp],
-    "ec_attn_prefill": [_vp, _vp, _vp, _vp, _vp, _vp, _u32, C.c_int32, _u32, _u32, _u32, _u32, _vp],
+    "ec_attn_prefill": [_vp, _vp, _vp, _vp, _vp, _vp, _u32, C.c_int32, _u32, _u32, _u32, _u32, _vp, _vp],
     "ec_deltanet_chunked": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp, _vp, _vp],
     "ec_fill_random": [C.c_int, _vp, _u64, _u64, C.c_float, _u32, _vp],
     "ec_gemm_quantize_act": [C.c_int, _vp, _vp, _u32, _u32, _vp],
@@ -75,6 +75,7 @@ _SIZE_FNS = {
     "ec_gemm_act_bytes": [C.c_int, _u32, _u32],
     "ec_attn_noalloc_max_bytes": [],
     "ec_deltanet_chunked_ws_bytes": [_u32, _u32, _u32],
+    "ec_attn_prefill_ws_bytes": [_u32, _u32, _u32],
 }
 
 
@@ -287,9 +288,13 @@ class Lib:
         self._call("ec_deltanet", _ptr(state), _ptr(q), _ptr(k), _ptr(v), _ptr(decay), _ptr(beta), _ptr(out), T,
                    n_seq, n_v, n_k, d_k, d_v, _ptr(seq_pos), self._stream(stream))
 
-    def attn_prefill(self, q, keys, vals, ks, vs, out, T, pos0, n_heads, n_kv, head_dim, max_ctx, stream=None):
+    def attn_prefill_ws_bytes(self, T, n_heads, max_ctx):
+        return self.L.ec_attn_prefill_ws_bytes(T, n_heads, max_ctx)
+
+    def attn_prefill(self, q, keys, vals, ks, vs, out, T, pos0, n_heads, n_kv, head_dim, max_ctx, ws=None,
+                     stream=None):
         self._call("ec_attn_prefill", _ptr(q), _ptr(keys), _ptr(vals), _ptr(ks), _ptr(vs), _ptr(out), T, pos0,
-                   n_heads, n_kv, head_dim, max_ctx, self._stream(stream))
+                   n_heads, n_kv, head_dim, max_ctx, _ptr(ws), self._stream(stream))
 
     def deltanet_chunked_ws_bytes(self, T, n_seq, n_v):
         return self.L.ec_deltanet_chunked_ws_bytes(T, n_seq, n_v)

@@ -135,6 +135,7 @@ struct ec_engine {
         float *dec = nullptr, *beta = nullptr, *core = nullptr, *gu = nullptr, *attn = nullptr;
         void *act = nullptr, *ws = nullptr, *act1 = nullptr;  // act1: one row, for the last token's logits
         void* dnws = nullptr;  // chunked delta-net workspace
+        void* aws = nullptr;   // segment partials of the chunk attention
         int32_t *tok = nullptr, *pos = nullptr, *ctx = nullptr;
         std::vector<int32_t> h_pos;
     };
@@ -970,6 +971,8 @@ int prefill_alloc(ec_engine* e, Lane& L, uint32_t i) {
          (rc = dalloc(e, &L.beta, C * e->n_v)) || (rc = dalloc(e, &L.core, C * e->value_dim)) ||
          (rc = dalloc(e, &L.dnws, ec_deltanet_chunked_ws_bytes((uint32_t)C, 1, e->n_v)))))
         return rc;
+    const size_t aws = ec_attn_prefill_ws_bytes((uint32_t)C, e->c.n_heads, e->c.max_ctx);
+    if (aws && (rc = dalloc(e, &L.aws, aws))) return rc;
     if ((rc = dalloc(e, &L.attn, C * e->q_dim)) ||
         (rc = dalloc(e, &L.ws, ec_attn_ws_bytes(ec_engine::kPrefillAttnSlots, e->c.n_heads, e->c.head_dim,
                                                 e->c.max_ctx))))
@@ -1040,7 +1043,7 @@ int prefill_chunk(ec_engine* e, Lane& L, uint32_t s, uint32_t T, uint32_t p) {
             EC_PF(EC_OP_PF_ATTN, li, EC_B_PF_N, EC_B_PF_ATTN, [&]() -> int {
                 if (G == 1 || G == 2 || G == 4)
                     return ec_attn_prefill(L.n, keys, vals, ks, vs, L.attn, T, (int32_t)p, c.n_heads, c.n_kv,
-                                           c.head_dim, c.max_ctx, st);
+                                           c.head_dim, c.max_ctx, L.aws, st);
                 // other group sizes: the decode kernel with the chunk's tokens
                 // as slots sharing the cache (ctx = position + 1)
                 for (uint32_t s0 = 0; s0 < T; s0 += ec_engine::kPrefillAttnSlots) {

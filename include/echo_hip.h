@@ -173,11 +173,16 @@ int ec_attn_decode_packed(const void* q_packed, const float* q_scales, const int
  * positions 0 .. pos0 + t of keys/vals/kscales/vscales (the layout above, the
  * chunk's rows already appended), each head as ec_attn_decode computes it.
  * One pass over the cache per group of 32/G query tokens and kv head, QK^T and
- * softmax . V on int8 MFMA.  head_dim 256, n_heads / n_kv in {1, 2, 4},
- * pos0 + T <= max_ctx. */
+ * softmax . V on int8 MFMA; with a workspace (ws, ec_attn_prefill_ws_bytes(T',
+ * n_heads, max_ctx) bytes for any T <= T') long walks are cut into up to 8
+ * segments run in parallel and merged; ws NULL: one segment.  head_dim 256,
+ * n_heads / n_kv in {1, 2, 4}, pos0 + T <= max_ctx.  No counterpart in the
+ * reference (its prefill runs the decode attention token by token,
+ * engine.zig:520-621). */
+size_t ec_attn_prefill_ws_bytes(uint32_t T, uint32_t n_heads, uint32_t max_ctx);
 int ec_attn_prefill(const float* q, const int8_t* keys, const int8_t* vals, const float* kscales,
                     const float* vscales, float* out, uint32_t T, int32_t pos0, uint32_t n_heads, uint32_t n_kv,
-                    uint32_t head_dim, uint32_t max_ctx, void* stream);
+                    uint32_t head_dim, uint32_t max_ctx, void* ws, void* stream);
 
 /* --------------------------------------------------------------- delta-net
  * Gated delta rule for T tokens of n_seq sequences (qwen_linear.zig:207-250):

@@ -315,28 +315,35 @@ def test_attention_decode(hip, oc, ctxs, max_ctx, n_heads, n_kv, hd):
 
 
 @pytest.mark.parametrize("T,pos0,n_heads,n_kv", [(64, 0, 16, 4), (100, 333, 16, 4), (1, 0, 16, 4), (37, 5, 8, 4),
-                                                  (20, 64, 4, 4), (512, 3584, 16, 4), (24, 16000, 16, 4)])
+                                                  (20, 64, 4, 4), (512, 3584, 16, 4), (24, 16000, 16, 4),
+                                                  (128, 3968, 16, 4)])
 def test_attention_prefill(hip, oc, T, pos0, n_heads, n_kv):
     """Causal chunk attention (ec_attn_prefill): query t at position pos0 + t
     against the oracle's decode attention over pos0 + t + 1 positions, every
     token within 1e-5 (partial key blocks, partial query groups, GQA 4:1, 2:1
-    and 1:1, a 512-token chunk at 3584, 24 tokens after 16000 positions)."""
+    and 1:1, a 512-token chunk at 3584, 24 tokens after 16000 positions),
+    with the walk cut into merged segments (workspace) and in one pass."""
     import torch
     hd, max_ctx = 256, pos0 + T + 3
     ctx = pos0 + T
     keys, vals, ks, vs, _, _ = _kv_case(oc, 1, [ctx], max_ctx, n_kv, hd, 90 + T)
     q = synth.activations(91 + pos0, T * n_heads * hd).reshape(T, n_heads * hd)
-    out = dev(np.full(T * n_heads * hd, 7.0, np.float32))
-    hip.attn_prefill(dev(q), dev(keys[0]), dev(vals[0]), dev(ks[0]), dev(vs[0]), out, T, pos0, n_heads, n_kv, hd,
-                     max_ctx)
-    out = host(out).reshape(T, n_heads * hd)
-    worst = 0.0
-    for t in range(T):
-        ref = oc.attn_decode(q[t], keys[0], vals[0], ks[0], vs[0], n_heads, n_kv, hd, pos0 + t + 1)
-        e = rel_l2(out[t], ref)
-        worst = max(worst, e)
-        assert e < 1e-5, (t, e)
-    print(f"T {T} pos0 {pos0}: worst per-token rel_l2 {worst:.2e}")
+    nws = hip.attn_prefill_ws_bytes(T, n_heads, max_ctx)
+    ws = empty(max(nws, 16), torch.uint8)
+    outs = {}
+    for tag, w in (("segments", ws), ("one pass", None)):
+        out = dev(np.full(T * n_heads * hd, 7.0, np.float32))
+        hip.attn_prefill(dev(q), dev(keys[0]), dev(vals[0]), dev(ks[0]), dev(vs[0]), out, T, pos0, n_heads, n_kv, hd,
+                         max_ctx, ws=w)
+        outs[tag] = host(out).reshape(T, n_heads * hd)
+    for tag, out in outs.items():
+        worst = 0.0
+        for t in range(T):
+            ref = oc.attn_decode(q[t], keys[0], vals[0], ks[0], vs[0], n_heads, n_kv, hd, pos0 + t + 1)
+            e = rel_l2(out[t], ref)
+            worst = max(worst, e)
+            assert e < 1e-5, (tag, t, e)
+        print(f"T {T} pos0 {pos0} ({tag}, workspace {nws} B): worst per-token rel_l2 {worst:.2e}")
 
 
 def _pack_q_pieces(q, n_heads, n_kv):
