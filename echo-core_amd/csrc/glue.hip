@@ -300,10 +300,14 @@ __global__ __launch_bounds__(128) void k_conv_gates(const float* __restrict__ pr
 
 // ------------------------------------- chunked prefill: conv + gates, T tokens
 // One sequence, T consecutive tokens at positions p0 .. p0+T-1 (proj rows
-// [T][Nin]).  grid (2*n_k + n_v, T), block 128: token t of one 128-channel
-// head, the same sums as k_conv_gates (conv_ring's tap order) with the taps of
-// positions >= p0 read from earlier rows of the chunk and older ones from the
-// ring.  The ring is updated afterwards by k_conv_ring_chunk.
+// [T][Nin]).  grid (2*n_k + n_v, ceil(T / kConvTokensPerBlock)), block 128:
+// kConvTokensPerBlock consecutive tokens of one 128-channel head (their shared
+// taps come from L1), the same sums as k_conv_gates (conv_ring's tap order)
+// with the taps of positions >= p0 read from earlier rows of the chunk and
+// older ones from the ring.  The ring is updated afterwards by
+// k_conv_ring_chunk.  (One token per workgroup: 32768 two-wave workgroups for
+// a 512-token chunk, 19.9 us.)
+constexpr uint32_t kConvTokensPerBlock = 8;
 __global__ __launch_bounds__(128) void k_conv_gates_chunk(const float* __restrict__ proj, uint32_t Nin,
                                                           const float* __restrict__ ring,
                                                           const float* __restrict__ conv_w,
@@ -311,42 +315,47 @@ __global__ __launch_bounds__(128) void k_conv_gates_chunk(const float* __restric
                                                           const float* __restrict__ dt_bias, float* __restrict__ q_out,
                                                           float* __restrict__ k_out, float* __restrict__ v_out,
                                                           float* __restrict__ dec, float* __restrict__ beta,
-                                                          uint32_t p0, uint32_t n_k, uint32_t n_v, uint32_t kern) {
-    __shared__ float sh[2];
-    const uint32_t hb = blockIdx.x, t = blockIdx.y, i = threadIdx.x;
+                                                          uint32_t T, uint32_t p0, uint32_t n_k, uint32_t n_v,
+                                                          uint32_t kern) {
+    __shared__ float sh[2][2];  // per-wave sums of squares, alternating between tokens
+    const uint32_t hb = blockIdx.x, i = threadIdx.x;
     const uint32_t key_dim = n_k * 128, value_dim = n_v * 128, conv_dim = 2 * key_dim + value_dim;
-    const float* pr = proj + (size_t)t * Nin;
     const uint32_t c = hb * 128 + i;
-    const uint32_t p = p0 + t;
-    float acc = pr[c] * conv_w[(size_t)(kern - 1) * conv_dim + c];
-    for (uint32_t k = 1; k < kern; ++k) {
-        float x = 0.0f;
-        if (k <= t) x = proj[(size_t)(t - k) * Nin + c];
-        else if (k <= p) x = ring[(size_t)((p - k) % kern) * conv_dim + c];
-        acc += x * conv_w[(size_t)(kern - 1 - k) * conv_dim + c];
-    }
-    const float a = silu(acc);
-    if (c >= 2 * key_dim) {  // v head
-        const uint32_t h = hb - 2 * n_k;
-        v_out[((size_t)t * n_v + h) * 128 + i] = a;
-        if (i == 0) {
-            const float al = pr[conv_dim + value_dim + h];
-            const float br = pr[conv_dim + value_dim + n_v + h];
-            const float sp_in = al + dt_bias[h];
-            const float sp = sp_in > 20.0f ? sp_in : log1pf(expf(sp_in));
-            const float g = -expf(a_log[h]) * sp;
-            dec[(size_t)t * n_v + h] = expf(g);
-            beta[(size_t)t * n_v + h] = 1.0f / (1.0f + expf(-br));
+    const uint32_t t_end = min((blockIdx.y + 1) * kConvTokensPerBlock, T);
+    for (uint32_t t = blockIdx.y * kConvTokensPerBlock; t < t_end; ++t) {
+        const float* pr = proj + (size_t)t * Nin;
+        const uint32_t p = p0 + t;
+        float acc = pr[c] * conv_w[(size_t)(kern - 1) * conv_dim + c];
+        for (uint32_t k = 1; k < kern; ++k) {
+            float x = 0.0f;
+            if (k <= t) x = proj[(size_t)(t - k) * Nin + c];
+            else if (k <= p) x = ring[(size_t)((p - k) % kern) * conv_dim + c];
+            acc += x * conv_w[(size_t)(kern - 1 - k) * conv_dim + c];
         }
-        return;
+        const float a = silu(acc);
+        if (c >= 2 * key_dim) {  // v head (the whole workgroup)
+            const uint32_t h = hb - 2 * n_k;
+            v_out[((size_t)t * n_v + h) * 128 + i] = a;
+            if (i == 0) {
+                const float al = pr[conv_dim + value_dim + h];
+                const float br = pr[conv_dim + value_dim + n_v + h];
+                const float sp_in = al + dt_bias[h];
+                const float sp = sp_in > 20.0f ? sp_in : log1pf(expf(sp_in));
+                const float g = -expf(a_log[h]) * sp;
+                dec[(size_t)t * n_v + h] = expf(g);
+                beta[(size_t)t * n_v + h] = 1.0f / (1.0f + expf(-br));
+            }
+            continue;
+        }
+        float* shb = sh[t & 1];
+        const float ss = wave_sum(a * a);
+        if ((i & 63) == 0) shb[i >> 6] = ss;
+        __syncthreads();  // also orders this token's reads of sh[t & 1] before token t+2 rewrites it
+        const float inv = 1.0f / sqrtf((shb[0] + shb[1]) + 1e-6f);
+        const bool is_q = c < key_dim;
+        const uint32_t h = is_q ? hb : hb - n_k;
+        (is_q ? q_out : k_out)[((size_t)t * n_k + h) * 128 + i] = a * inv;
     }
-    const float ss = wave_sum(a * a);
-    if ((i & 63) == 0) sh[i >> 6] = ss;
-    __syncthreads();
-    const float inv = 1.0f / sqrtf((sh[0] + sh[1]) + 1e-6f);
-    const bool is_q = c < key_dim;
-    const uint32_t h = is_q ? hb : hb - n_k;
-    (is_q ? q_out : k_out)[((size_t)t * n_k + h) * 128 + i] = a * inv;
 }
 
 // Ring update after a chunk: the inputs of the last min(T, kern) positions.
@@ -362,16 +371,50 @@ __global__ __launch_bounds__(256) void k_conv_ring_chunk(const float* __restrict
 
 // --------------------------------------------- fp32 row ops (chunked prefill)
 // RMSNorm rows: y[i] = x[i] * 1/sqrt(mean(x[i]^2) + 1e-6) * w.  grid (M), block 256.
+// Rows of H <= 4096 with H % 4 == 0 and 16-byte aligned rows: float4 loads
+// kept in registers for the second pass (kRowRegs per thread); others scalar.
+constexpr uint32_t kRowRegs = 4;
 __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* __restrict__ x, const float* __restrict__ w,
                                                       float* __restrict__ y, uint32_t H) {
     __shared__ float sh[4];
-    const uint32_t i = blockIdx.x;
+    const uint32_t i = blockIdx.x, t = threadIdx.x;
     const float* xr = x + (size_t)i * H;
+    float* yr = y + (size_t)i * H;
+    const bool vec = H % 4 == 0 && H <= 1024 * kRowRegs && (((uintptr_t)xr | (uintptr_t)yr | (uintptr_t)w) & 15) == 0;
+    if (vec) {
+        const uint32_t n4 = H / 4;
+        float4 v[kRowRegs];
+        float ss = 0.0f;
+#pragma unroll
+        for (uint32_t u = 0; u < kRowRegs; ++u) {
+            const uint32_t k = t + 256 * u;
+            v[u] = k < n4 ? ((const float4*)xr)[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kRowRegs; ++u) {
+            ss = fmaf(v[u].x, v[u].x, ss);
+            ss = fmaf(v[u].y, v[u].y, ss);
+            ss = fmaf(v[u].z, v[u].z, ss);
+            ss = fmaf(v[u].w, v[u].w, ss);
+        }
+        ss = block_sum256(ss, sh);
+        const float inv = 1.0f / sqrtf(ss / (float)H + 1e-6f);
+#pragma unroll
+        for (uint32_t u = 0; u < kRowRegs; ++u) {
+            const uint32_t k = t + 256 * u;
+            if (k < n4) {
+                const float4 wv = ((const float4*)w)[k];
+                ((float4*)yr)[k] = make_float4(v[u].x * inv * wv.x, v[u].y * inv * wv.y, v[u].z * inv * wv.z,
+                                               v[u].w * inv * wv.w);
+            }
+        }
+        return;
+    }
     float ss = 0.0f;
-    for (uint32_t k = threadIdx.x; k < H; k += 256) ss = fmaf(xr[k], xr[k], ss);
+    for (uint32_t k = t; k < H; k += 256) ss = fmaf(xr[k], xr[k], ss);
     ss = block_sum256(ss, sh);
     const float inv = 1.0f / sqrtf(ss / (float)H + 1e-6f);
-    for (uint32_t k = threadIdx.x; k < H; k += 256) y[(size_t)i * H + k] = xr[k] * inv * w[k];
+    for (uint32_t k = t; k < H; k += 256) yr[k] = xr[k] * inv * w[k];
 }
 
 // SwiGLU rows: gu [M][2F] (gate | up) -> y [M][F].  grid (ceil(F/256), M).
@@ -675,8 +718,9 @@ extern "C" int ec_glue_conv_gates_chunk(const float* proj, uint32_t Nin, float* 
         return ec_set_error(EC_ERR_ARG, "ec_glue_conv_gates_chunk: bad argument");
     const uint32_t conv_dim = 2 * n_k * 128 + n_v * 128;
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(k_conv_gates_chunk, dim3(2 * n_k + n_v, T), dim3(128), 0, st, proj, Nin, ring, conv_w, a_log,
-                       dt_bias, q, k, v, dec, beta, p0, n_k, n_v, kern);
+    hipLaunchKernelGGL(k_conv_gates_chunk, dim3(2 * n_k + n_v, (T + kConvTokensPerBlock - 1) / kConvTokensPerBlock),
+                       dim3(128), 0, st, proj, Nin, ring, conv_w, a_log, dt_bias, q, k, v, dec, beta, T, p0, n_k, n_v,
+                       kern);
     EC_CHECK_LAUNCH();
     EC_GLUE_LAUNCH(k_conv_ring_chunk, dim3((conv_dim + 255) / 256, T < kern ? T : kern), dim3(256), 0, st, proj, Nin,
                    ring, conv_dim, T, p0, kern);

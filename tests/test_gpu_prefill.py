@@ -33,7 +33,8 @@ pytestmark = pytest.mark.gpu
 PATH_TOL = 2e-2  # prefill vs token loop, one-quantum flips carried (measured <= 1.2e-2)
 
 
-@pytest.mark.parametrize("T,p0,zero_ring", [(7, 5, False), (2, 9, False), (6, 0, True), (3, 1, True), (1, 12, False)])
+@pytest.mark.parametrize("T,p0,zero_ring", [(7, 5, False), (2, 9, False), (6, 0, True), (3, 1, True), (1, 12, False),
+                                             (20, 3, False), (17, 0, True)])
 def test_conv_gates_chunk_equals_single_steps(hip, T, p0, zero_ring):
     import torch
     n_k, n_v, kern = 2, 4, 4
@@ -62,9 +63,10 @@ def test_conv_gates_chunk_equals_single_steps(hip, T, p0, zero_ring):
         assert np.array_equal(host(a).view(np.uint32), host(b).view(np.uint32))
 
 
-def test_row_ops(hip, oc):
+@pytest.mark.parametrize("H", [640, 642, 4100])  # float4 path; scalar path (H % 4, H > 4096)
+def test_row_ops(hip, oc, H):
     import torch
-    M, H, F, n_v = 5, 640, 384, 3
+    M, F, n_v = 5, 384, 3
     x = (3 * synth.normal(synth.stream_seed(6, 0), M * H)).astype(np.float32).reshape(M, H)
     w = (1 + 0.1 * synth.normal(synth.stream_seed(7, 0), H)).astype(np.float32)
     y = empty(M * H, torch.float32)
