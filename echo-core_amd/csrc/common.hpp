@@ -128,7 +128,9 @@ __device__ __forceinline__ float rope_pair(float x, float other, uint32_t d, flo
 //   sum_k x_{p-k} * w[(kern-1-k)*conv_dim + c], x_p = xin, newest tap first.
 __device__ __forceinline__ float conv_ring(const float* __restrict__ st, const float* __restrict__ w, float xin,
                                            uint32_t p, uint32_t kern, uint32_t conv_dim, uint32_t c) {
-    float acc = xin * w[(size_t)(kern - 1) * conv_dim + c];
+    // newest tap first, each further tap one fma: the order every conv kernel
+    // (decode step, prefill chunk) uses, so their sums agree bit for bit
+    float acc = __fmul_rn(xin, w[(size_t)(kern - 1) * conv_dim + c]);
     if (kern <= 4) {
         // all taps loaded before the first use (one memory round trip); a tap
         // k >= kern reads slot 0 / tap 0 and is multiplied by zero
@@ -141,11 +143,11 @@ __device__ __forceinline__ float conv_ring(const float* __restrict__ st, const f
             wv[k - 1] = ok ? wk : 0.0f;
         }
 #pragma unroll
-        for (int k = 0; k < 3; ++k) acc += sv[k] * wv[k];
+        for (int k = 0; k < 3; ++k) acc = fmaf(sv[k], wv[k], acc);
         return acc;
     }
     for (uint32_t k = 1; k < kern; ++k)
-        acc += st[(size_t)((p + kern - k) % kern) * conv_dim + c] * w[(size_t)(kern - 1 - k) * conv_dim + c];
+        acc = fmaf(st[(size_t)((p + kern - k) % kern) * conv_dim + c], w[(size_t)(kern - 1 - k) * conv_dim + c], acc);
     return acc;
 }
 

@@ -262,12 +262,12 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
     if (t < 384) {
         float acc;
         if (ring4) {  // conv_ring's sum with the slots already in registers
-            acc = xin * w4[3];
+            acc = __fmul_rn(xin, w4[3]);
 #pragma unroll
             for (uint32_t k = 1; k < 4; ++k) {
                 const uint32_t q = ((uint32_t)p + 4 - k) & 3;
                 const float rv = q == 0 ? r4[0] : (q == 1 ? r4[1] : (q == 2 ? r4[2] : r4[3]));
-                acc += rv * w4[3 - k];
+                acc = fmaf(rv, w4[3 - k], acc);
             }
         } else {
             acc = conv_ring(cst, conv_w, xin, (uint32_t)p, kern, conv_dim, c);

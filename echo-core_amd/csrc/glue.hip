@@ -308,6 +308,83 @@ __global__ __launch_bounds__(128) void k_conv_gates(const float* __restrict__ pr
 // k_conv_ring_chunk.  (One token per workgroup: 32768 two-wave workgroups for
 // a 512-token chunk, 19.9 us.)
 constexpr uint32_t kConvTokensPerBlock = 8;
+// Four-tap case (the model's conv kernel): the 8 tokens' inputs and their 3
+// earlier taps are loaded once into registers (11 loads per thread, all in
+// flight), the 8 tokens computed together, one barrier for their L2 norms.
+__global__ __launch_bounds__(128) void k_conv_gates_chunk4(const float* __restrict__ proj, uint32_t Nin,
+                                                           const float* __restrict__ ring,
+                                                           const float* __restrict__ conv_w,
+                                                           const float* __restrict__ a_log,
+                                                           const float* __restrict__ dt_bias, float* __restrict__ q_out,
+                                                           float* __restrict__ k_out, float* __restrict__ v_out,
+                                                           float* __restrict__ dec, float* __restrict__ beta,
+                                                           uint32_t T, uint32_t p0, uint32_t n_k, uint32_t n_v) {
+    constexpr uint32_t KERN = 4, TPB = kConvTokensPerBlock;
+    __shared__ float sh[TPB][2];
+    const uint32_t hb = blockIdx.x, i = threadIdx.x;
+    const uint32_t key_dim = n_k * 128, value_dim = n_v * 128, conv_dim = 2 * key_dim + value_dim;
+    const uint32_t c = hb * 128 + i;
+    const int32_t t0 = (int32_t)(blockIdx.y * TPB);
+    // xs[j] = input of chunk row t0 - 3 + j (earlier positions from the ring, 0 before position 0)
+    float xs[TPB + KERN - 1];
+#pragma unroll
+    for (int j = 0; j < (int)(TPB + KERN - 1); ++j) {
+        const int32_t t = t0 - (int32_t)(KERN - 1) + j;
+        float x = 0.0f;
+        if (t >= 0) {
+            if (t < (int32_t)T) x = proj[(size_t)t * Nin + c];
+        } else if ((int32_t)p0 + t >= 0) {
+            x = ring[(size_t)(((int32_t)p0 + t) % (int32_t)KERN) * conv_dim + c];
+        }
+        xs[j] = x;
+    }
+    float wv[KERN];
+#pragma unroll
+    for (int k = 0; k < (int)KERN; ++k) wv[k] = conv_w[(size_t)k * conv_dim + c];
+    float a[TPB];
+#pragma unroll
+    for (int tt = 0; tt < (int)TPB; ++tt) {
+        // the sum of k_conv_gates in its order: newest tap first
+        float acc = __fmul_rn(xs[tt + KERN - 1], wv[KERN - 1]);
+#pragma unroll
+        for (int k = 1; k < (int)KERN; ++k) acc = fmaf(xs[tt + KERN - 1 - k], wv[KERN - 1 - k], acc);
+        a[tt] = silu(acc);
+    }
+    const uint32_t nt = min((uint32_t)TPB, T - (uint32_t)t0);
+    if (c >= 2 * key_dim) {  // v head (the whole workgroup)
+        const uint32_t h = hb - 2 * n_k;
+#pragma unroll
+        for (int tt = 0; tt < (int)TPB; ++tt)
+            if ((uint32_t)tt < nt) v_out[((size_t)(t0 + tt) * n_v + h) * 128 + i] = a[tt];
+        if (i < nt) {
+            const float* pr = proj + (size_t)(t0 + i) * Nin;
+            const float al = pr[conv_dim + value_dim + h];
+            const float br = pr[conv_dim + value_dim + n_v + h];
+            const float sp_in = al + dt_bias[h];
+            const float sp = sp_in > 20.0f ? sp_in : log1pf(expf(sp_in));
+            const float g = -expf(a_log[h]) * sp;
+            dec[(size_t)(t0 + i) * n_v + h] = expf(g);
+            beta[(size_t)(t0 + i) * n_v + h] = 1.0f / (1.0f + expf(-br));
+        }
+        return;
+    }
+#pragma unroll
+    for (int tt = 0; tt < (int)TPB; ++tt) {
+        const float ss = wave_sum(a[tt] * a[tt]);
+        if ((i & 63) == 0) sh[tt][i >> 6] = ss;
+    }
+    __syncthreads();
+    const bool is_q = c < key_dim;
+    const uint32_t h = is_q ? hb : hb - n_k;
+#pragma unroll
+    for (int tt = 0; tt < (int)TPB; ++tt) {
+        if ((uint32_t)tt >= nt) break;
+        const float inv = 1.0f / sqrtf((sh[tt][0] + sh[tt][1]) + 1e-6f);
+        (is_q ? q_out : k_out)[((size_t)(t0 + tt) * n_k + h) * 128 + i] = a[tt] * inv;
+    }
+}
+
+// Any number of taps: one token per iteration.
 __global__ __launch_bounds__(128) void k_conv_gates_chunk(const float* __restrict__ proj, uint32_t Nin,
                                                           const float* __restrict__ ring,
                                                           const float* __restrict__ conv_w,
@@ -325,12 +402,12 @@ __global__ __launch_bounds__(128) void k_conv_gates_chunk(const float* __restric
     for (uint32_t t = blockIdx.y * kConvTokensPerBlock; t < t_end; ++t) {
         const float* pr = proj + (size_t)t * Nin;
         const uint32_t p = p0 + t;
-        float acc = pr[c] * conv_w[(size_t)(kern - 1) * conv_dim + c];
+        float acc = __fmul_rn(pr[c], conv_w[(size_t)(kern - 1) * conv_dim + c]);
         for (uint32_t k = 1; k < kern; ++k) {
             float x = 0.0f;
             if (k <= t) x = proj[(size_t)(t - k) * Nin + c];
             else if (k <= p) x = ring[(size_t)((p - k) % kern) * conv_dim + c];
-            acc += x * conv_w[(size_t)(kern - 1 - k) * conv_dim + c];
+            acc = fmaf(x, conv_w[(size_t)(kern - 1 - k) * conv_dim + c], acc);
         }
         const float a = silu(acc);
         if (c >= 2 * key_dim) {  // v head (the whole workgroup)
@@ -718,9 +795,13 @@ extern "C" int ec_glue_conv_gates_chunk(const float* proj, uint32_t Nin, float* 
         return ec_set_error(EC_ERR_ARG, "ec_glue_conv_gates_chunk: bad argument");
     const uint32_t conv_dim = 2 * n_k * 128 + n_v * 128;
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(k_conv_gates_chunk, dim3(2 * n_k + n_v, (T + kConvTokensPerBlock - 1) / kConvTokensPerBlock),
-                       dim3(128), 0, st, proj, Nin, ring, conv_w, a_log, dt_bias, q, k, v, dec, beta, T, p0, n_k, n_v,
-                       kern);
+    const dim3 grid(2 * n_k + n_v, (T + kConvTokensPerBlock - 1) / kConvTokensPerBlock);
+    if (kern == 4)
+        hipLaunchKernelGGL(k_conv_gates_chunk4, grid, dim3(128), 0, st, proj, Nin, ring, conv_w, a_log, dt_bias, q, k,
+                           v, dec, beta, T, p0, n_k, n_v);
+    else
+        hipLaunchKernelGGL(k_conv_gates_chunk, grid, dim3(128), 0, st, proj, Nin, ring, conv_w, a_log, dt_bias, q, k,
+                           v, dec, beta, T, p0, n_k, n_v, kern);
     EC_CHECK_LAUNCH();
     EC_GLUE_LAUNCH(k_conv_ring_chunk, dim3((conv_dim + 255) / 256, T < kern ? T : kern), dim3(256), 0, st, proj, Nin,
                    ring, conv_dim, T, p0, kern);

@@ -33,11 +33,14 @@ pytestmark = pytest.mark.gpu
 PATH_TOL = 2e-2  # prefill vs token loop, one-quantum flips carried (measured <= 1.2e-2)
 
 
-@pytest.mark.parametrize("T,p0,zero_ring", [(7, 5, False), (2, 9, False), (6, 0, True), (3, 1, True), (1, 12, False),
-                                             (20, 3, False), (17, 0, True)])
-def test_conv_gates_chunk_equals_single_steps(hip, T, p0, zero_ring):
+@pytest.mark.parametrize("T,p0,zero_ring,kern", [(7, 5, False, 4), (2, 9, False, 4), (6, 0, True, 4),
+                                                  (3, 1, True, 4), (1, 12, False, 4), (20, 3, False, 4),
+                                                  (17, 0, True, 4), (20, 5, False, 3), (9, 6, False, 5)])
+def test_conv_gates_chunk_equals_single_steps(hip, T, p0, zero_ring, kern):
+    """Four taps take the register-window kernel, other tap counts the
+    one-token-per-iteration kernel; both bit-identical to single steps."""
     import torch
-    n_k, n_v, kern = 2, 4, 4
+    n_k, n_v = 2, 4
     Nin = 2 * n_k * 128 + 2 * n_v * 128 + 2 * n_v
     conv_dim = 2 * n_k * 128 + n_v * 128
     proj = synth.normal(synth.stream_seed(1, T), T * Nin).astype(np.float32).reshape(T, Nin)
