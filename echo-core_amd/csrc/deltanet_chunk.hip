@@ -31,9 +31,10 @@ constexpr uint32_t kLd = kDh + 4;   // LDS row of a C x 128 matrix (floats)
 constexpr uint32_t kPd = kCk + 4;   // LDS row of a C x C matrix
 constexpr uint32_t kUd = kVs + 4;   // LDS row of the C x 16 U tile
 // workspace floats per (sequence, head, chunk): W [C][128], U~ [C][128],
-// P [C][C], G [C], G_C/G_t [C]
+// P [C][C], G [C], G_C/G_t [C], K^T [128][C] (zero past the last token)
 constexpr uint32_t kWsW = 0, kWsU = kCk * kDh, kWsP = 2 * kCk * kDh, kWsG = kWsP + kCk * kCk, kWsF = kWsG + kCk;
-constexpr uint32_t kWsFloats = kWsF + kCk;
+constexpr uint32_t kWsK = kWsF + kCk;
+constexpr uint32_t kWsFloats = kWsK + kDh * kCk;
 
 // D (16 x 16) += A (16 x 4) B (4 x 16): lane l holds A[l%16][l/16],
 // B[l/16][l%16] and D[4*(l/16) + r][l%16] in element r.
@@ -201,6 +202,14 @@ __global__ __launch_bounds__(256) void k_dn_chunk_prep(const float* __restrict__
     float* dst = wsc + (col < kDh ? kWsW + col : kWsU + (col - kDh));
 #pragma unroll 8
     for (uint32_t t = 0; t < kCk; ++t) dst[t * kDh] = L.X[t][col];
+    // K^T for the scan's state update, read so that the lanes of a wave take
+    // 64 consecutive keys of one token row (no LDS bank conflicts)
+#pragma unroll
+    for (uint32_t u = 0; u < kDh * kCk / 4 / 256; ++u) {
+        const uint32_t key = 64 * (u & 1) + lane, t = 4 * (4 * w + (u >> 1));
+        const f32x4 kv = {L.K[t][key], L.K[t + 1][key], L.K[t + 2][key], L.K[t + 3][key]};
+        *(f32x4*)(wsc + kWsK + key * kCk + t) = kv;
+    }
 }
 
 // ------------------------------------------------------------------ pass 2
@@ -226,7 +235,7 @@ struct ScanLds {
 // are dealt to the 8 XCDs round-robin, so with n_v % 8 == 0 the 8 column
 // slices of a head share one XCD's L2 and its W, Q, K, P are fetched once.
 __global__ __launch_bounds__(256) void k_dn_chunk_scan(float* __restrict__ state, const float* __restrict__ q,
-                                                       const float* __restrict__ k, const float* __restrict__ ws,
+                                                       const float* __restrict__ ws,
                                                        float* __restrict__ out, uint32_t T, uint32_t n_seq,
                                                        uint32_t n_v, uint32_t n_k, uint32_t nc,
                                                        const int32_t* __restrict__ seq_pos) {
@@ -249,7 +258,9 @@ __global__ __launch_bounds__(256) void k_dn_chunk_scan(float* __restrict__ state
     constexpr uint32_t NL = kCk * (kDh / 4) / 256, NP = kCk * (kCk / 4) / 256;
     f32x4 rw[NL], rq[NL], rk[NL], rp[NP], ru;
     float rg = 0.f, rf = 0.f;
-    auto load = [&](uint32_t c) {
+    // Two groups, issued at different points of the previous chunk, so that a
+    // wave never has all 34 loads waiting for a slot in the memory pipeline.
+    auto load_a = [&](uint32_t c) {
         const uint32_t t0 = c * kCk, n = min(kCk, T - t0);
         const float* wsc = ws + ((size_t)(s * n_v + h) * nc + c) * kWsFloats;
 #pragma unroll
@@ -257,10 +268,14 @@ __global__ __launch_bounds__(256) void k_dn_chunk_scan(float* __restrict__ state
             const uint32_t i = tid + 256 * u, t = i / (kDh / 4), e = 4 * (i % (kDh / 4));
             rw[u] = *(const f32x4*)(wsc + kWsW + t * kDh + e);
             rq[u] = *(const f32x4*)(q + (((size_t)(t0 + min(t, n - 1)) * n_seq + s) * n_k + qh) * kDh + e);
-            // K with lane = token, so that its transposed LDS store below
-            // writes 64 consecutive tokens per instruction
-            const uint32_t ek = 4 * (w + 4 * u);
-            rk[u] = *(const f32x4*)(k + (((size_t)(t0 + min(lane, n - 1)) * n_seq + s) * n_k + qh) * kDh + ek);
+        }
+    };
+    auto load_b = [&](uint32_t c) {
+        const float* wsc = ws + ((size_t)(s * n_v + h) * nc + c) * kWsFloats;
+#pragma unroll
+        for (uint32_t u = 0; u < NL; ++u) {
+            const uint32_t i = tid + 256 * u;
+            rk[u] = *(const f32x4*)(wsc + kWsK + 4 * i);  // K^T row i / 16, tokens 4 (i % 16) ..
         }
 #pragma unroll
         for (uint32_t u = 0; u < NP; ++u) {
@@ -283,10 +298,7 @@ __global__ __launch_bounds__(256) void k_dn_chunk_scan(float* __restrict__ state
             const bool ok = t < n;
             *(f32x4*)&L.W[t][e] = rw[u];
             *(f32x4*)&L.Q[t][e] = ok ? rq[u] : z4;
-            const uint32_t ek = 4 * (w + 4 * u);
-            const f32x4 kv = lane < n ? rk[u] : z4;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) L.Kt[ek + r][lane] = kv[r];
+            *(f32x4*)&L.Kt[i / (kCk / 4)][4 * (i % (kCk / 4))] = rk[u];
         }
 #pragma unroll
         for (uint32_t u = 0; u < NP; ++u) {
@@ -298,7 +310,8 @@ __global__ __launch_bounds__(256) void k_dn_chunk_scan(float* __restrict__ state
             L.F[tid] = rf;
         }
     };
-    load(0);
+    load_a(0);
+    load_b(0);
     const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
     for (uint32_t c = 0; c < nc; ++c) {
         const uint32_t t0 = c * kCk, n = min(kCk, T - t0);
@@ -306,7 +319,7 @@ __global__ __launch_bounds__(256) void k_dn_chunk_scan(float* __restrict__ state
         store(c);
         const f32x4 uin = ru;
         __syncthreads();
-        if (c + 1 < nc) load(c + 1);
+        if (c + 1 < nc) load_a(c + 1);
 
         // U = U~ - W S0 and QS = Q S0 for row tile w (B[k][j] = S[j][k]),
         // lane (r, g) contracting over k = 32g .. 32g+31
@@ -330,6 +343,7 @@ __global__ __launch_bounds__(256) void k_dn_chunk_scan(float* __restrict__ state
         // lane holds U[16w + 4g + r][r16]: four consecutive tokens of U^T
         *(f32x4*)&L.Ut[r16][16 * w + 4 * g4] = uin - du;
         __syncthreads();  // U^T complete; S no longer read this chunk
+        if (c + 1 < nc) load_b(c + 1);
 
         // O = (G QS + P U)/sqrt(d_k): P is lower triangular, so row tile w
         // contracts over tokens 0 .. 16w+15, lane (r, g) over 4(w+1) of them
@@ -401,7 +415,7 @@ extern "C" int ec_deltanet_chunked(float* state, const float* q, const float* k,
     hipLaunchKernelGGL(k_dn_chunk_prep, dim3(nc, n_v, n_seq), dim3(256), sizeof(PrepLds), st, q, k, v, decay, beta,
                        (float*)ws, T, n_seq, n_v, n_k, seq_pos);
     EC_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_dn_chunk_scan, dim3(n_v * (kDh / kVs), n_seq), dim3(256), sizeof(ScanLds), st, state, q, k,
+    hipLaunchKernelGGL(k_dn_chunk_scan, dim3(n_v * (kDh / kVs), n_seq), dim3(256), sizeof(ScanLds), st, state, q,
                        (const float*)ws, out, T, n_seq, n_v, n_k, nc, seq_pos);
     EC_CHECK_LAUNCH();
     return EC_OK;
