@@ -129,6 +129,48 @@ __global__ __launch_bounds__(256) void k_gemm_quantize_x(const float* __restrict
     }
 }
 
+// Q8_0 with 16-byte loads: each lane quantizes 4 consecutive elements, 8
+// consecutive lanes one 32-element block (the same amax, scale and rounding as
+// above: the lane maximum, then xor 1, 2, 4 over the 8 lanes); a wave covers 8
+// blocks (1 KB of its token's row) per step and kQxSteps steps, the workgroup's
+// four waves four tokens.  grid (ceil(nbp / (8 kQxSteps)), Mp / 4).
+constexpr uint32_t kQxSteps = 2;
+__global__ __launch_bounds__(256) void k_gemm_quantize_x8(const float* __restrict__ x, uint8_t* __restrict__ xt,
+                                                          uint32_t M, uint32_t K, uint32_t ldx, uint32_t nch,
+                                                          uint32_t nbp, size_t xd_off) {
+    const uint32_t lane = threadIdx.x & 63, m = blockIdx.y * 4 + (threadIdx.x >> 6);
+    const uint32_t T = m / 16, r = m % 16, b0 = blockIdx.x * 8 * kQxSteps;
+    float4 v[kQxSteps];
+#pragma unroll
+    for (uint32_t st = 0; st < kQxSteps; ++st) {
+        const uint32_t k = 32 * b0 + 256 * st + 4 * lane;  // K % 32 == 0: a block is all real or all padding
+        v[st] = (m < M && k < K) ? *(const float4*)(x + (size_t)m * ldx + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (uint32_t st = 0; st < kQxSteps; ++st) {
+        const uint32_t b = b0 + 8 * st + lane / 8;
+        if (b >= nbp) continue;  // whole 8-lane groups
+        float amax = fmaxf(fmaxf(fabsf(v[st].x), fabsf(v[st].y)), fmaxf(fabsf(v[st].z), fabsf(v[st].w)));
+        amax = fmaxf(amax, lane_xor<1>(amax));
+        amax = fmaxf(amax, lane_xor<2>(amax));
+        amax = fmaxf(amax, lane_xor<4>(amax));
+        const float scale = q_scale(amax);
+        const float inv = __fdiv_rn(1.0f, scale);
+        const uint32_t w4 = (uint32_t)(uint8_t)q_body(v[st].x, inv) | ((uint32_t)(uint8_t)q_body(v[st].y, inv) << 8) |
+                            ((uint32_t)(uint8_t)q_body(v[st].z, inv) << 16) |
+                            ((uint32_t)(uint8_t)q_body(v[st].w, inv) << 24);
+        // elements 8g..8g+7 of the block (lanes 2g, 2g+1 of the group) are the
+        // 8 bytes of lane r + 16g of the chunk's operand
+        const uint32_t hi = row_down<1>(w4);
+        const uint32_t e = lane & 7;
+        if ((e & 1) == 0) {
+            const uint32_t G = b / 4, j = b % 4, l = r + 16 * (e / 2);
+            *(uint2*)(xt + ((size_t)T * nch + G) * 2048 + (j / 2) * 1024 + 16 * l + 8 * (j % 2)) = make_uint2(w4, hi);
+        }
+        if (e == 0) ((float*)(xt + xd_off))[(size_t)m * nbp + b] = m < M ? scale : 0.0f;
+    }
+}
+
 // ------------------------------------------------------------------ Q8_0
 template <int RTW>
 __global__ __launch_bounds__(256, 2) void k_gemm_q8_0(const uint8_t* __restrict__ W, const uint8_t* __restrict__ xt,
@@ -382,8 +424,8 @@ extern "C" int ec_gemm_quantize_act(int fmt, const float* x, void* act, uint32_t
     const XtLayout L = xt_layout(fmt, M, K);
     const uint32_t nbp = L.Kp / 32;
     if (fmt == EC_Q8_0)
-        hipLaunchKernelGGL(k_gemm_quantize_x<false>, dim3((nbp + 7) / 8, L.Mp), dim3(256), 0, (hipStream_t)stream, x,
-                           (uint8_t*)act, M, K, K, L.nch, nbp, L.xd_off, L.dxs_off);
+        hipLaunchKernelGGL(k_gemm_quantize_x8, dim3((nbp + 8 * kQxSteps - 1) / (8 * kQxSteps), L.Mp / 4), dim3(256), 0,
+                           (hipStream_t)stream, x, (uint8_t*)act, M, K, K, L.nch, nbp, L.xd_off);
     else
         hipLaunchKernelGGL(k_gemm_quantize_x<true>, dim3((nbp + 7) / 8, L.Mp), dim3(256), 0, (hipStream_t)stream, x,
                            (uint8_t*)act, M, K, K, L.nch, nbp, L.xd_off, L.dxs_off);

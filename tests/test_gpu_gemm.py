@@ -88,6 +88,7 @@ def _q4k_perm(K):
 
 
 CASES = [(Q8_0, 37, 256, 512), (Q8_0, 512, 9216, 2560), (Q8_0, 512, 2560, 9216), (Q8_0, 100, 272, 384),
+         (Q8_0, 19, 48, 160), (Q8_0, 70, 40, 4128),
          (Q4_K, 37, 256, 512), (Q4_K, 512, 9216, 2560), (Q4_K, 512, 2560, 9216), (Q4_K, 64, 48, 768)]
 
 
