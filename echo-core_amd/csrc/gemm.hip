@@ -11,7 +11,7 @@
 // which is the reference's matvec arithmetic (matvec.cpp:62-142) on the
 // quantized activations, in a different summation order.
 //
-// Activation layout ("XT"), tokens in tiles of 16:
+// Activation layout ("XT", gemm_act.hpp), tokens in tiles of 16:
 //   Q8_0: chunk (token tile T, group G of 4 blocks) = 2048 B at (T*nG+G)*2048,
 //         lane l's 16 B at 16l (blocks 0,1) and 1024+16l (blocks 2,3), 8 B per
 //         block = x[16T + l%16][128G + 32j + 8(l/16) .. +8] (the MFMA A operand);
@@ -31,8 +31,7 @@
 // roughly a third of the int8 MFMA peak by construction of 32-element scales.
 #include <type_traits>
 
-#include "common.hpp"
-#include "layout.hpp"
+#include "gemm_act.hpp"
 
 namespace ec {
 
@@ -43,45 +42,19 @@ __device__ __forceinline__ long gpack2(uint32_t lo, uint32_t hi) {
     return (long)(((uint64_t)hi << 32) | (uint64_t)lo);
 }
 
-struct XtLayout {
-    uint32_t Mp, Kp, nch;  // padded tokens, padded K, chunks per token tile
-    size_t xq_bytes, xd_off, dxs_off, total;
-};
-
-__host__ __device__ inline XtLayout xt_layout(int fmt, uint32_t M, uint32_t K) {
-    XtLayout L;
-    L.Mp = round_up(M, 16);
-    const bool q4 = fmt == EC_Q4_K;
-    L.Kp = round_up(K, q4 ? 256u : 128u);
-    L.nch = L.Kp / (q4 ? 256u : 128u);
-    L.xq_bytes = (size_t)(L.Mp / 16) * L.nch * (q4 ? 4096u : 2048u);
-    L.xd_off = (L.xq_bytes + 255) & ~(size_t)255;
-    const size_t xd = (size_t)L.Mp * (L.Kp / 32) * sizeof(float);
-    L.dxs_off = L.xd_off + ((xd + 255) & ~(size_t)255);
-    L.total = L.dxs_off + (q4 ? xd : 0);
-    return L;
-}
-
 // ----------------------------------------------------------- activation prep
-// grid (ceil(Kp/32 / 8), Mp tokens), block 256: eight 32-lane groups, one
-// quantization block each, one lane per element.  Q8_0: block b holds
-// x[m][32b .. 32b+32); Q4_K: sub-block s of super-block b/8 holds the 32
-// positions pos(s, i) (reference order, oc_q4k_pos).  Each run of 8 bytes of
-// the tiled layout is gathered with shuffles and stored by one lane.
-template <bool Q4>
-__global__ __launch_bounds__(256) void k_gemm_quantize_x(const float* __restrict__ x, uint8_t* __restrict__ xt,
-                                                         uint32_t M, uint32_t K, uint32_t ldx, uint32_t nch,
-                                                         uint32_t nbp, size_t xd_off, size_t dxs_off) {
+// Q4_K: grid (ceil(Kp/32 / 8), Mp tokens), block 256: eight 32-lane groups,
+// one sub-block each, one lane per element; sub-block s of super-block b/8
+// holds the 32 positions pos(s, i) (reference order, oc_q4k_pos).  Each run of
+// 8 bytes of the tiled layout is gathered with shuffles and stored by one lane.
+__global__ __launch_bounds__(256) void k_gemm_quantize_x_q4(const float* __restrict__ x, uint8_t* __restrict__ xt,
+                                                            uint32_t M, uint32_t K, uint32_t ldx, uint32_t nch,
+                                                            uint32_t nbp, size_t xd_off, size_t dxs_off) {
     const uint32_t b = blockIdx.x * 8 + (threadIdx.x >> 5), m = blockIdx.y, i = threadIdx.x & 31;
     if (b >= nbp) return;  // whole 32-lane groups leave together
-    uint32_t k;
-    if constexpr (Q4) {
-        const uint32_t s = b % 8;  // sub-block of super-block b/8
-        const uint32_t p = (i < 16) ? 64 * (s / 2) + 16 * (s % 2) + i : 64 * (s / 2) + 32 + 16 * (s % 2) + (i - 16);
-        k = 256 * (b / 8) + p;
-    } else {
-        k = 32 * b + i;
-    }
+    const uint32_t s = b % 8;  // sub-block of super-block b/8
+    const uint32_t p = (i < 16) ? 64 * (s / 2) + 16 * (s % 2) + i : 64 * (s / 2) + 32 + 16 * (s % 2) + (i - 16);
+    const uint32_t k = 256 * (b / 8) + p;
     const bool real = m < M && k < K;
     const float v = real ? x[(size_t)m * ldx + k] : 0.0f;
     float amax = fabsf(v);
@@ -97,77 +70,45 @@ __global__ __launch_bounds__(256) void k_gemm_quantize_x(const float* __restrict
     // 4 consecutive elements' bytes, gathered at the first lane of each 4
     const uint32_t qb = (uint8_t)q;
     const uint32_t w4 = qb | (row_down<1>(qb) << 8) | (row_down<2>(qb) << 16) | (row_down<3>(qb) << 24);
-    if constexpr (Q4) {
-        // elements 4g..4g+3 are bytes 0..3 and elements 16+4g..16+4g+3 bytes
-        // 4..7 of lane r + 16g of sub-block pair s/2
-        const uint32_t hi = __shfl_down(w4, 16, 32);
-        if (i < 16 && (i & 3) == 0) {
-            const uint32_t s = b % 8, l = r + 16 * (i / 4);
-            *(uint2*)(xt + ((size_t)T * nch + b / 8) * 4096 + (s / 2) * 1024 + 16 * l + 8 * (s % 2)) =
-                make_uint2(w4, hi);
-        }
-    } else {
-        // elements 8g..8g+7 are the 8 bytes of lane r + 16g
-        const uint32_t hi = row_down<4>(w4);
-        if ((i & 7) == 0) {
-            const uint32_t G = b / 4, j = b % 4, l = r + 16 * (i / 8);
-            *(uint2*)(xt + ((size_t)T * nch + G) * 2048 + (j / 2) * 1024 + 16 * l + 8 * (j % 2)) = make_uint2(w4, hi);
-        }
+    // elements 4g..4g+3 are bytes 0..3 and elements 16+4g..16+4g+3 bytes
+    // 4..7 of lane r + 16g of sub-block pair s/2
+    const uint32_t hi = __shfl_down(w4, 16, 32);
+    if (i < 16 && (i & 3) == 0) {
+        const uint32_t l = r + 16 * (i / 4);
+        *(uint2*)(xt + ((size_t)T * nch + b / 8) * 4096 + (s / 2) * 1024 + 16 * l + 8 * (s % 2)) = make_uint2(w4, hi);
     }
     int sum = q;
-    if constexpr (Q4) {
-        sum += lane_xor_i<1>(sum);
-        sum += lane_xor_i<2>(sum);
-        sum += lane_xor_i<4>(sum);
-        sum += lane_xor_i<8>(sum);
-        sum += lane_xor_i<16>(sum);
-    }
+    sum += lane_xor_i<1>(sum);
+    sum += lane_xor_i<2>(sum);
+    sum += lane_xor_i<4>(sum);
+    sum += lane_xor_i<8>(sum);
+    sum += lane_xor_i<16>(sum);
     if (i == 0) {
-        float* xd = (float*)(xt + xd_off);
-        xd[(size_t)m * nbp + b] = m < M ? scale : 0.0f;
-        if constexpr (Q4) ((float*)(xt + dxs_off))[(size_t)m * nbp + b] = scale * (float)sum;
+        ((float*)(xt + xd_off))[(size_t)m * nbp + b] = m < M ? scale : 0.0f;
+        ((float*)(xt + dxs_off))[(size_t)m * nbp + b] = scale * (float)sum;
     }
 }
 
-// Q8_0 with 16-byte loads: each lane quantizes 4 consecutive elements, 8
-// consecutive lanes one 32-element block (the same amax, scale and rounding as
-// above: the lane maximum, then xor 1, 2, 4 over the 8 lanes); a wave covers 8
-// blocks (1 KB of its token's row) per step and kQxSteps steps, the workgroup's
-// four waves four tokens.  grid (ceil(nbp / (8 kQxSteps)), Mp / 4).
+// Q8_0: each lane quantizes 4 consecutive elements (one 16-byte load), 8
+// consecutive lanes a 32-element block; a wave covers 8 blocks (1 KB of its
+// token's row) per step and kQxSteps steps, the workgroup's four waves four
+// tokens.  grid (ceil(nbp / (8 kQxSteps)), Mp / 4).
 constexpr uint32_t kQxSteps = 2;
 __global__ __launch_bounds__(256) void k_gemm_quantize_x8(const float* __restrict__ x, uint8_t* __restrict__ xt,
                                                           uint32_t M, uint32_t K, uint32_t ldx, uint32_t nch,
                                                           uint32_t nbp, size_t xd_off) {
     const uint32_t lane = threadIdx.x & 63, m = blockIdx.y * 4 + (threadIdx.x >> 6);
-    const uint32_t T = m / 16, r = m % 16, b0 = blockIdx.x * 8 * kQxSteps;
+    const uint32_t q0 = blockIdx.x * 64 * kQxSteps;  // first float4 of the wave
     float4 v[kQxSteps];
 #pragma unroll
     for (uint32_t st = 0; st < kQxSteps; ++st) {
-        const uint32_t k = 32 * b0 + 256 * st + 4 * lane;  // K % 32 == 0: a block is all real or all padding
+        const uint32_t k = 4 * (q0 + 64 * st + lane);  // K % 32 == 0: a block is all real or all padding
         v[st] = (m < M && k < K) ? *(const float4*)(x + (size_t)m * ldx + k) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 #pragma unroll
     for (uint32_t st = 0; st < kQxSteps; ++st) {
-        const uint32_t b = b0 + 8 * st + lane / 8;
-        if (b >= nbp) continue;  // whole 8-lane groups
-        float amax = fmaxf(fmaxf(fabsf(v[st].x), fabsf(v[st].y)), fmaxf(fabsf(v[st].z), fabsf(v[st].w)));
-        amax = fmaxf(amax, lane_xor<1>(amax));
-        amax = fmaxf(amax, lane_xor<2>(amax));
-        amax = fmaxf(amax, lane_xor<4>(amax));
-        const float scale = q_scale(amax);
-        const float inv = __fdiv_rn(1.0f, scale);
-        const uint32_t w4 = (uint32_t)(uint8_t)q_body(v[st].x, inv) | ((uint32_t)(uint8_t)q_body(v[st].y, inv) << 8) |
-                            ((uint32_t)(uint8_t)q_body(v[st].z, inv) << 16) |
-                            ((uint32_t)(uint8_t)q_body(v[st].w, inv) << 24);
-        // elements 8g..8g+7 of the block (lanes 2g, 2g+1 of the group) are the
-        // 8 bytes of lane r + 16g of the chunk's operand
-        const uint32_t hi = row_down<1>(w4);
-        const uint32_t e = lane & 7;
-        if ((e & 1) == 0) {
-            const uint32_t G = b / 4, j = b % 4, l = r + 16 * (e / 2);
-            *(uint2*)(xt + ((size_t)T * nch + G) * 2048 + (j / 2) * 1024 + 16 * l + 8 * (j % 2)) = make_uint2(w4, hi);
-        }
-        if (e == 0) ((float*)(xt + xd_off))[(size_t)m * nbp + b] = m < M ? scale : 0.0f;
+        const uint32_t q = q0 + 64 * st + lane;
+        if (q / 8 < nbp) xt_q8_store4(v[st], m, q, m < M, xt, nch, nbp, xd_off);  // whole 8-lane groups
     }
 }
 
@@ -427,7 +368,7 @@ extern "C" int ec_gemm_quantize_act(int fmt, const float* x, void* act, uint32_t
         hipLaunchKernelGGL(k_gemm_quantize_x8, dim3((nbp + 8 * kQxSteps - 1) / (8 * kQxSteps), L.Mp / 4), dim3(256), 0,
                            (hipStream_t)stream, x, (uint8_t*)act, M, K, K, L.nch, nbp, L.xd_off);
     else
-        hipLaunchKernelGGL(k_gemm_quantize_x<true>, dim3((nbp + 7) / 8, L.Mp), dim3(256), 0, (hipStream_t)stream, x,
+        hipLaunchKernelGGL(k_gemm_quantize_x_q4, dim3((nbp + 7) / 8, L.Mp), dim3(256), 0, (hipStream_t)stream, x,
                            (uint8_t*)act, M, K, K, L.nch, nbp, L.xd_off, L.dxs_off);
     EC_CHECK_LAUNCH();
     return EC_OK;

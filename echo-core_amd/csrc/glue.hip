@@ -17,8 +17,7 @@
 //
 // A sequence s is active when pos[s] >= 0; inactive sequences never touch
 // their recurrent state, conv state or KV cache.
-#include "common.hpp"
-#include "layout.hpp"
+#include "gemm_act.hpp"
 
 namespace ec {
 
@@ -518,6 +517,87 @@ __global__ __launch_bounds__(128) void k_gated_norm_rows(const float* __restrict
     y[((size_t)s * n_v + h) * 128 + i] = o * inv * norm_w[i] * silu(proj[(size_t)s * Nin + z_off + h * 128 + i]);
 }
 
+// ------------------------------- prefill rows straight into the GEMM layout
+// The _rows arithmetic above, quantized into the prefill GEMM's Q8_0
+// activation layout (gemm_act.hpp) by the same quantizer as
+// ec_gemm_quantize_act, so the bytes are those of _rows + quantize.  Padding
+// tokens (M .. Mp) and blocks (K .. Kp) are written as the quantizer writes
+// them.
+
+// grid (Mp), block 256: k_rmsnorm_rows' float4 path (H % 32 == 0, Kp <= 4096).
+__global__ __launch_bounds__(256) void k_rmsnorm_rows_gemm_act(const float* __restrict__ x,
+                                                               const float* __restrict__ w, uint8_t* __restrict__ xt,
+                                                               uint32_t M, uint32_t H, uint32_t nch, uint32_t nbp,
+                                                               size_t xd_off) {
+    __shared__ float sh[4];
+    const uint32_t i = blockIdx.x, t = threadIdx.x;
+    const bool real = i < M;
+    const float4* xr = (const float4*)(x + (size_t)(real ? i : 0) * H);
+    const uint32_t n4 = H / 4, nq = 8 * nbp;  // float4s of the row, of the padded row
+    float4 v[kRowRegs];
+    float ss = 0.0f;
+#pragma unroll
+    for (uint32_t u = 0; u < kRowRegs; ++u) {
+        const uint32_t k = t + 256 * u;
+        v[u] = real && k < n4 ? xr[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kRowRegs; ++u) {
+        ss = fmaf(v[u].x, v[u].x, ss);
+        ss = fmaf(v[u].y, v[u].y, ss);
+        ss = fmaf(v[u].z, v[u].z, ss);
+        ss = fmaf(v[u].w, v[u].w, ss);
+    }
+    ss = block_sum256(ss, sh);
+    const float inv = 1.0f / sqrtf(ss / (float)H + 1e-6f);
+#pragma unroll
+    for (uint32_t u = 0; u < kRowRegs; ++u) {
+        const uint32_t k = t + 256 * u;
+        if (k >= nq) continue;  // whole 8-lane groups (nq % 8 == 0)
+        float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (real && k < n4) {
+            const float4 wv = ((const float4*)w)[k];
+            y = make_float4(v[u].x * inv * wv.x, v[u].y * inv * wv.y, v[u].z * inv * wv.z, v[u].w * inv * wv.w);
+        }
+        xt_q8_store4(y, i, k, real, xt, nch, nbp, xd_off);
+    }
+}
+
+// grid (ceil(8 nbp / 256), Mp), block 256: thread q -> elements 4q .. 4q+3.
+__global__ __launch_bounds__(256) void k_swiglu_rows_gemm_act(const float* __restrict__ gu, uint8_t* __restrict__ xt,
+                                                              uint32_t M, uint32_t F, uint32_t nch, uint32_t nbp,
+                                                              size_t xd_off) {
+    const uint32_t m = blockIdx.y, q = blockIdx.x * 256 + threadIdx.x;
+    if (q >= 8 * nbp) return;  // whole 8-lane groups
+    const bool real = m < M;
+    float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (real && 4 * q < F) {
+        const float* g = gu + (size_t)m * 2 * F + 4 * q;
+        const float4 a = *(const float4*)g, b = *(const float4*)(g + F);
+        y = make_float4(silu(a.x) * b.x, silu(a.y) * b.y, silu(a.z) * b.z, silu(a.w) * b.w);
+    }
+    xt_q8_store4(y, m, q, real, xt, nch, nbp, xd_off);
+}
+
+// grid (n_v, Mp), block 128: k_gated_norm_rows; a head's 128 outputs are 4 blocks.
+__global__ __launch_bounds__(128) void k_gated_norm_rows_gemm_act(const float* __restrict__ core,
+                                                                  const float* __restrict__ proj, uint32_t Nin,
+                                                                  uint32_t z_off, const float* __restrict__ norm_w,
+                                                                  uint8_t* __restrict__ xt, uint32_t M, uint32_t n_v,
+                                                                  uint32_t nch, uint32_t nbp, size_t xd_off) {
+    __shared__ float sh[2];
+    const uint32_t h = blockIdx.x, s = blockIdx.y, i = threadIdx.x;
+    const bool real = s < M;
+    const float o = real ? core[((size_t)s * n_v + h) * 128 + i] : 0.0f;
+    const float ss = wave_sum(o * o);
+    if ((i & 63) == 0) sh[i >> 6] = ss;
+    __syncthreads();
+    const float rms = sqrtf((sh[0] + sh[1]) / 128.0f + 1e-6f);
+    const float inv = 1.0f / rms;
+    const float val = real ? o * inv * norm_w[i] * silu(proj[(size_t)s * Nin + z_off + h * 128 + i]) : 0.0f;
+    xt_q8_store1(val, s, h * 128 + i, real, xt, nch, nbp, xd_off);
+}
+
 // ------------------------------------------------ gated RMSNorm + quantize
 // grid (n_v, M), block 128: core [M][n_v][128], z at proj[s][z_off + h*128 + i]
 // -> act (K = n_v*128).  The head's 128 outputs are 4 whole 32-blocks.
@@ -825,6 +905,37 @@ extern "C" int ec_glue_gated_norm_rows(const float* core, const float* proj, uin
     if (!core || !proj || !norm_w || !y || n_v == 0) return ec_set_error(EC_ERR_ARG, "ec_glue_gated_norm_rows");
     EC_GLUE_LAUNCH(k_gated_norm_rows, dim3(n_v, M), dim3(128), 0, (hipStream_t)stream, core, proj, Nin, z_off, norm_w,
                    y, n_v);
+}
+
+extern "C" int ec_glue_rmsnorm_rows_gemm_act(const float* x, const float* w, void* act, uint32_t M, uint32_t H,
+                                              void* stream) {
+    if (M == 0) return EC_OK;
+    const XtLayout L = xt_layout(EC_Q8_0, M, H);
+    if (!x || !w || !act || H == 0 || H % 32 || L.Kp > 1024 * kRowRegs || ((uintptr_t)x | (uintptr_t)w) & 15)
+        return ec_set_error(EC_ERR_ARG, "ec_glue_rmsnorm_rows_gemm_act: need H % 32 == 0, H <= 4096, 16-byte rows");
+    EC_GLUE_LAUNCH(k_rmsnorm_rows_gemm_act, dim3(L.Mp), dim3(256), 0, (hipStream_t)stream, x, w, (uint8_t*)act, M, H,
+                   L.nch, L.Kp / 32, L.xd_off);
+}
+
+extern "C" int ec_glue_swiglu_rows_gemm_act(const float* gu, void* act, uint32_t M, uint32_t F, void* stream) {
+    if (M == 0) return EC_OK;
+    if (!gu || !act || F == 0 || F % 32 || (uintptr_t)gu & 15)
+        return ec_set_error(EC_ERR_ARG, "ec_glue_swiglu_rows_gemm_act: need F % 32 == 0, 16-byte rows");
+    const XtLayout L = xt_layout(EC_Q8_0, M, F);
+    const uint32_t nbp = L.Kp / 32;
+    EC_GLUE_LAUNCH(k_swiglu_rows_gemm_act, dim3((8 * nbp + 255) / 256, L.Mp), dim3(256), 0, (hipStream_t)stream, gu,
+                   (uint8_t*)act, M, F, L.nch, nbp, L.xd_off);
+}
+
+extern "C" int ec_glue_gated_norm_rows_gemm_act(const float* core, const float* proj, uint32_t Nin, uint32_t z_off,
+                                                const float* norm_w, void* act, uint32_t M, uint32_t n_v,
+                                                void* stream) {
+    if (M == 0) return EC_OK;
+    if (!core || !proj || !norm_w || !act || n_v == 0)
+        return ec_set_error(EC_ERR_ARG, "ec_glue_gated_norm_rows_gemm_act: bad argument");
+    const XtLayout L = xt_layout(EC_Q8_0, M, n_v * 128);
+    EC_GLUE_LAUNCH(k_gated_norm_rows_gemm_act, dim3(n_v, L.Mp), dim3(128), 0, (hipStream_t)stream, core, proj, Nin,
+                   z_off, norm_w, (uint8_t*)act, M, n_v, L.nch, L.Kp / 32, L.xd_off);
 }
 
 extern "C" int ec_glue_gated_norm_quant(const float* core, const float* proj, uint32_t Nin, uint32_t z_off,

@@ -26,7 +26,7 @@ ACT4_BUFFERS = (B_ACT4_H, B_ACT4_V, B_ACT4_Q, B_ACT4_F)
 (OP_PF_EMBED, OP_PF_NORM, OP_PF_GEMM_IN, OP_PF_CONV, OP_PF_DELTA, OP_PF_GATED_NORM, OP_PF_GEMM_OUT,
  OP_PF_ROPE_APPEND, OP_PF_ATTN, OP_PF_GEMM_GU, OP_PF_SWIGLU, OP_PF_GEMM_DOWN, OP_PF_HEAD) = range(20, 33)
 (B_PF_X, B_PF_N, B_PF_PROJ, B_PF_Q, B_PF_K, B_PF_V, B_PF_DEC, B_PF_BETA, B_PF_CORE, B_PF_GU, B_PF_ATTN, B_PF_TOK,
- B_PF_ACT1) = range(30, 43)
+ B_PF_ACT1, B_PF_ACT) = range(30, 44)
 
 
 def gguf_row_bytes(fmt: int, K: int) -> int:
@@ -308,6 +308,23 @@ class Engine:
         if count:
             self.hip.copy(out, p + offset * isz, out.nbytes)
         return out
+
+    def read_gemm_act(self, which: int, M: int, K: int):
+        """A prefill GEMM activation (ec_gemm_quantize_act's Q8_0 layout for M
+        tokens of K elements) as (xq int8 [M][K], xd fp32 [M][K/32])."""
+        p, n = self.buffer(which)
+        Mp, Kp = -(-M // 16) * 16, -(-K // 128) * 128
+        nch, nbp = Kp // 128, Kp // 32
+        xq_bytes = Mp // 16 * nch * 2048
+        xd_off = -(-xq_bytes // 256) * 256
+        assert xd_off + Mp * nbp * 4 <= n, (which, M, K, n)
+        raw = np.empty(xd_off + Mp * nbp * 4, np.uint8)
+        self.hip.copy(raw, p, raw.nbytes)
+        # chunk (token tile T, 4-block group G) = [block pair][operand lane = r + 16*(8-group)][block of the pair][8 B]
+        q = raw[:xq_bytes].view(np.int8).reshape(Mp // 16, nch, 2, 4, 16, 2, 8)
+        xq = q.transpose(0, 4, 1, 2, 5, 3, 6).reshape(Mp, Kp)[:M, :K]
+        xd = raw[xd_off:].view(np.float32).reshape(Mp, nbp)[:M, :K // 32]
+        return np.ascontiguousarray(xq), np.ascontiguousarray(xd)
 
     def read_act(self, which: int, K: int, M: int | None = None, fmt: int | None = None):
         """An activation buffer (ec_quantize_act layout, M = max_batch; Q4_K for

@@ -64,6 +64,9 @@ _SIGS = {
     "ec_glue_rmsnorm_rows": [_vp, _vp, _vp, _u32, _u32, _vp],
     "ec_glue_swiglu_rows": [_vp, _vp, _u32, _u32, _vp],
     "ec_glue_gated_norm_rows": [_vp, _vp, _u32, _u32, _vp, _vp, _u32, _u32, _vp],
+    "ec_glue_rmsnorm_rows_gemm_act": [_vp, _vp, _vp, _u32, _u32, _vp],
+    "ec_glue_swiglu_rows_gemm_act": [_vp, _vp, _u32, _u32, _vp],
+    "ec_glue_gated_norm_rows_gemm_act": [_vp, _vp, _u32, _u32, _vp, _vp, _u32, _u32, _vp],
     "ec_stream_read": [_vp, _sz, _vp, _u32, _vp],
     "ec_stream_read_shape": [_vp, _sz, _vp, _u32, _u32, _u32, _vp],
 }
@@ -256,6 +259,16 @@ class Lib:
     def gated_norm_rows(self, core, proj, Nin, z_off, norm_w, y, M, n_v, stream=None):
         self._call("ec_glue_gated_norm_rows", _ptr(core), _ptr(proj), Nin, z_off, _ptr(norm_w), _ptr(y), M, n_v,
                    self._stream(stream))
+
+    def rmsnorm_rows_gemm_act(self, x, w, act, M, H, stream=None):
+        self._call("ec_glue_rmsnorm_rows_gemm_act", _ptr(x), _ptr(w), _ptr(act), M, H, self._stream(stream))
+
+    def swiglu_rows_gemm_act(self, gu, act, M, F, stream=None):
+        self._call("ec_glue_swiglu_rows_gemm_act", _ptr(gu), _ptr(act), M, F, self._stream(stream))
+
+    def gated_norm_rows_gemm_act(self, core, proj, Nin, z_off, norm_w, act, M, n_v, stream=None):
+        self._call("ec_glue_gated_norm_rows_gemm_act", _ptr(core), _ptr(proj), Nin, z_off, _ptr(norm_w), _ptr(act), M,
+                   n_v, self._stream(stream))
 
     def rmsnorm_quant(self, x, w, act, M, H, stream=None):
         self._call("ec_glue_rmsnorm_quant", _ptr(x), _ptr(w), _ptr(act), M, H, self._stream(stream))

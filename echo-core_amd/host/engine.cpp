@@ -134,6 +134,7 @@ struct ec_engine {
         float *x = nullptr, *n = nullptr, *proj = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
         float *dec = nullptr, *beta = nullptr, *core = nullptr, *gu = nullptr, *attn = nullptr;
         void *act = nullptr, *ws = nullptr, *act1 = nullptr;  // act1: one row, for the last token's logits
+        size_t act_bytes = 0;
         void* dnws = nullptr;  // chunked delta-net workspace
         void* aws = nullptr;   // segment partials of the chunk attention
         int32_t *tok = nullptr, *pos = nullptr, *ctx = nullptr;
@@ -962,7 +963,8 @@ int prefill_alloc(ec_engine* e, Lane& L, uint32_t i) {
     }
     if ((rc = dalloc(e, &L.x, C * e->H)) || (rc = dalloc(e, &L.n, C * wide)) ||
         (rc = dalloc(e, &L.proj, C * e->nin_max)) || (rc = dalloc(e, &L.gu, C * 2 * (size_t)e->F)) ||
-        (rc = dalloc(e, &L.act, act_rows_bytes)) || (rc = dalloc(e, &L.act1, act1_bytes)) || (rc = dalloc(e, &L.tok, C)) ||
+        (rc = dalloc(e, &L.act, L.act_bytes = act_rows_bytes)) || (rc = dalloc(e, &L.act1, act1_bytes)) ||
+        (rc = dalloc(e, &L.tok, C)) ||
         (rc = dalloc(e, &L.pos, C)) || (rc = dalloc(e, &L.ctx, C)))
         return rc;
     if (e->value_dim &&
@@ -990,6 +992,18 @@ int gemm_rows(Lane& L, const Mat& m, const float* x, float* y, uint32_t T, uint3
     EC_TRY(ec_gemm_quantize_act(m.fmt, x, L.act, T, m.K, L.st));
     return ec_gemm(m.fmt, m.tiled, L.act, y, T, m.N, m.K, ldy, acc, L.st);
 }
+// The GEMM on the lane's activation buffer, written by the producing row op.
+int gemm_act(Lane& L, const Mat& m, float* y, uint32_t T, uint32_t ldy, int acc) {
+    return ec_gemm(m.fmt, m.tiled, L.act, y, T, m.N, m.K, ldy, acc, L.st);
+}
+// A Q8_0 GEMM's activation is quantized by the row op that produces it (RMSNorm
+// rows, SwiGLU rows, gated-norm rows: one launch instead of op + quantize;
+// byte-identical); Q4_K matrices and RMSNorm rows wider than 4096 take the fp32
+// rows and ec_gemm_quantize_act.
+bool fused_act(const Mat& m, uint32_t max_k = 0xFFFFFFFFu) {
+    return m.fmt == EC_Q8_0 && m.K % 32 == 0 && (m.K + 127) / 128 * 128 <= max_k;
+}
+constexpr uint32_t kNormActMaxK = 4096;
 
 // One chunk of T tokens of sequence s at positions p .. p+T-1 through every
 // block, on the lane's stream (L.tok / L.pos already hold the chunk).
@@ -1005,10 +1019,17 @@ int prefill_chunk(ec_engine* e, Lane& L, uint32_t s, uint32_t T, uint32_t p) {
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         Layer& y = e->L[l];
         const int li = (int)l;
-        EC_PF(EC_OP_PF_NORM, li, EC_B_PF_X, EC_B_PF_N, ec_glue_rmsnorm_rows(L.x, y.attn_norm, L.n, T, H, st));
+        const bool fin = fused_act(y.w_in, kNormActMaxK);
+        if (fin)
+            EC_PF(EC_OP_PF_NORM, li, EC_B_PF_X, EC_B_PF_ACT,
+                  ec_glue_rmsnorm_rows_gemm_act(L.x, y.attn_norm, L.act, T, H, st));
+        else
+            EC_PF(EC_OP_PF_NORM, li, EC_B_PF_X, EC_B_PF_N, ec_glue_rmsnorm_rows(L.x, y.attn_norm, L.n, T, H, st));
+        const int in_buf = fin ? EC_B_PF_ACT : EC_B_PF_N;
         if (!y.attn) {
             const uint32_t Nin = e->nin_delta;
-            EC_PF(EC_OP_PF_GEMM_IN, li, EC_B_PF_N, EC_B_PF_PROJ, gemm_rows(L, y.w_in, L.n, L.proj, T, Nin, 0));
+            EC_PF(EC_OP_PF_GEMM_IN, li, in_buf, EC_B_PF_PROJ,
+                  fin ? gemm_act(L, y.w_in, L.proj, T, Nin, 0) : gemm_rows(L, y.w_in, L.n, L.proj, T, Nin, 0));
             float* ring = y.conv_state + (size_t)s * c.conv_kernel * e->conv_dim;
             float* state = y.ssm_state + (size_t)s * e->n_v * 128 * 128;
             EC_PF(EC_OP_PF_CONV, li, EC_B_PF_PROJ, EC_B_PF_Q,
@@ -1022,12 +1043,20 @@ int prefill_chunk(ec_engine* e, Lane& L, uint32_t s, uint32_t T, uint32_t p) {
                                             128, nullptr, L.dnws, st)
                       : ec_deltanet(state, L.q, L.k, L.v, L.dec, L.beta, L.core, T, 1, e->n_v, e->n_k, 128, 128,
                                     nullptr, st));
-            EC_PF(EC_OP_PF_GATED_NORM, li, EC_B_PF_CORE, EC_B_PF_N,
-                  ec_glue_gated_norm_rows(L.core, L.proj, Nin, e->conv_dim, y.ssm_norm, L.n, T, e->n_v, st));
-            EC_PF(EC_OP_PF_GEMM_OUT, li, EC_B_PF_N, EC_B_PF_X, gemm_rows(L, y.w_out, L.n, L.x, T, H, 1));
+            if (fused_act(y.w_out)) {
+                EC_PF(EC_OP_PF_GATED_NORM, li, EC_B_PF_CORE, EC_B_PF_ACT,
+                      ec_glue_gated_norm_rows_gemm_act(L.core, L.proj, Nin, e->conv_dim, y.ssm_norm, L.act, T, e->n_v,
+                                                       st));
+                EC_PF(EC_OP_PF_GEMM_OUT, li, EC_B_PF_ACT, EC_B_PF_X, gemm_act(L, y.w_out, L.x, T, H, 1));
+            } else {
+                EC_PF(EC_OP_PF_GATED_NORM, li, EC_B_PF_CORE, EC_B_PF_N,
+                      ec_glue_gated_norm_rows(L.core, L.proj, Nin, e->conv_dim, y.ssm_norm, L.n, T, e->n_v, st));
+                EC_PF(EC_OP_PF_GEMM_OUT, li, EC_B_PF_N, EC_B_PF_X, gemm_rows(L, y.w_out, L.n, L.x, T, H, 1));
+            }
         } else {
             const uint32_t Nin = e->nin_attn;
-            EC_PF(EC_OP_PF_GEMM_IN, li, EC_B_PF_N, EC_B_PF_PROJ, gemm_rows(L, y.w_in, L.n, L.proj, T, Nin, 0));
+            EC_PF(EC_OP_PF_GEMM_IN, li, in_buf, EC_B_PF_PROJ,
+                  fin ? gemm_act(L, y.w_in, L.proj, T, Nin, 0) : gemm_rows(L, y.w_in, L.n, L.proj, T, Nin, 0));
             int8_t* keys = y.keys + (size_t)s * e->seq_stride;
             int8_t* vals = y.vals + (size_t)s * e->seq_stride;
             float* ks = y.ks + (size_t)s * c.max_ctx * c.n_kv;
@@ -1056,10 +1085,21 @@ int prefill_chunk(ec_engine* e, Lane& L, uint32_t s, uint32_t T, uint32_t p) {
             }());
             EC_PF(EC_OP_PF_GEMM_OUT, li, EC_B_PF_ATTN, EC_B_PF_X, gemm_rows(L, y.w_out, L.attn, L.x, T, H, 1));
         }
-        EC_PF(EC_OP_PF_NORM, li, EC_B_PF_X, EC_B_PF_N, ec_glue_rmsnorm_rows(L.x, y.ffn_norm, L.n, T, H, st));
-        EC_PF(EC_OP_PF_GEMM_GU, li, EC_B_PF_N, EC_B_PF_GU, gemm_rows(L, y.w_gu, L.n, L.gu, T, 2 * F, 0));
-        EC_PF(EC_OP_PF_SWIGLU, li, EC_B_PF_GU, EC_B_PF_N, ec_glue_swiglu_rows(L.gu, L.n, T, F, st));
-        EC_PF(EC_OP_PF_GEMM_DOWN, li, EC_B_PF_N, EC_B_PF_X, gemm_rows(L, y.w_down, L.n, L.x, T, H, 1));
+        if (fused_act(y.w_gu, kNormActMaxK)) {
+            EC_PF(EC_OP_PF_NORM, li, EC_B_PF_X, EC_B_PF_ACT,
+                  ec_glue_rmsnorm_rows_gemm_act(L.x, y.ffn_norm, L.act, T, H, st));
+            EC_PF(EC_OP_PF_GEMM_GU, li, EC_B_PF_ACT, EC_B_PF_GU, gemm_act(L, y.w_gu, L.gu, T, 2 * F, 0));
+        } else {
+            EC_PF(EC_OP_PF_NORM, li, EC_B_PF_X, EC_B_PF_N, ec_glue_rmsnorm_rows(L.x, y.ffn_norm, L.n, T, H, st));
+            EC_PF(EC_OP_PF_GEMM_GU, li, EC_B_PF_N, EC_B_PF_GU, gemm_rows(L, y.w_gu, L.n, L.gu, T, 2 * F, 0));
+        }
+        if (fused_act(y.w_down)) {
+            EC_PF(EC_OP_PF_SWIGLU, li, EC_B_PF_GU, EC_B_PF_ACT, ec_glue_swiglu_rows_gemm_act(L.gu, L.act, T, F, st));
+            EC_PF(EC_OP_PF_GEMM_DOWN, li, EC_B_PF_ACT, EC_B_PF_X, gemm_act(L, y.w_down, L.x, T, H, 1));
+        } else {
+            EC_PF(EC_OP_PF_SWIGLU, li, EC_B_PF_GU, EC_B_PF_N, ec_glue_swiglu_rows(L.gu, L.n, T, F, st));
+            EC_PF(EC_OP_PF_GEMM_DOWN, li, EC_B_PF_N, EC_B_PF_X, gemm_rows(L, y.w_down, L.n, L.x, T, H, 1));
+        }
     }
 #undef EC_PF
     return EC_OK;
@@ -1292,6 +1332,7 @@ extern "C" int ec_engine_buffer(ec_engine* e, int which, void** dev, size_t* byt
                 case EC_B_PF_ACT1:
                     p = L.act1, n = r ? ec_act_bytes(e->lm_head.fmt == EC_Q4_K ? EC_Q4_K : EC_Q8_0, 1, e->H) : 0;
                     break;
+                case EC_B_PF_ACT: p = L.act, n = r ? L.act_bytes : 0; break;
                 default: return ec_set_error(EC_ERR_ARG, "ec_engine_buffer: unknown buffer");
             }
             if (!r) p = nullptr;

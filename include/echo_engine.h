@@ -221,6 +221,7 @@ enum {
     EC_B_PF_X = 30, EC_B_PF_N = 31, EC_B_PF_PROJ = 32, EC_B_PF_Q = 33, EC_B_PF_K = 34, EC_B_PF_V = 35,
     EC_B_PF_DEC = 36, EC_B_PF_BETA = 37, EC_B_PF_CORE = 38, EC_B_PF_GU = 39, EC_B_PF_ATTN = 40, EC_B_PF_TOK = 41,
     EC_B_PF_ACT1 = 42, /* the last token's head activation (Q8_0 or Q4_K layout, M = 1) */
+    EC_B_PF_ACT = 43,  /* the chunk's GEMM activation (ec_gemm_quantize_act layout of the GEMM's format and K) */
 };
 int ec_engine_buffer(ec_engine* e, int which, void** dev, size_t* bytes);
 

@@ -298,6 +298,15 @@ int ec_glue_rmsnorm_rows(const float* x, const float* w, float* y, uint32_t M, u
 int ec_glue_swiglu_rows(const float* gu, float* y, uint32_t M, uint32_t F, void* stream);
 int ec_glue_gated_norm_rows(const float* core, const float* proj, uint32_t Nin, uint32_t z_off, const float* norm_w,
                             float* y, uint32_t M, uint32_t n_v, void* stream);
+/* The same three ops with their output quantized straight into the prefill
+ * GEMM's Q8_0 activation layout (ec_gemm_act_bytes(EC_Q8_0, M, K) bytes, K =
+ * H, F or n_v*128): byte for byte what the _rows op followed by
+ * ec_gemm_quantize_act(EC_Q8_0, ...) writes, one launch instead of two.
+ * rmsnorm: H % 32 == 0 and H <= 4096; swiglu: F % 32 == 0. */
+int ec_glue_rmsnorm_rows_gemm_act(const float* x, const float* w, void* act, uint32_t M, uint32_t H, void* stream);
+int ec_glue_swiglu_rows_gemm_act(const float* gu, void* act, uint32_t M, uint32_t F, void* stream);
+int ec_glue_gated_norm_rows_gemm_act(const float* core, const float* proj, uint32_t Nin, uint32_t z_off,
+                                     const float* norm_w, void* act, uint32_t M, uint32_t n_v, void* stream);
 
 /* Plain streaming read of `bytes` (multiple of 16) with `blocks` workgroups of
  * 256 threads: the HBM-bandwidth calibration used by the benchmarks. */

@@ -6,12 +6,18 @@ recomputed by the oracle (oracle.c) from the GPU's own inputs, row by row (one
 row per token of the chunk), with the tolerances of tests/decoder_ops.py:
 
   embedding rows             bit-exact
-  RMSNorm / gated-norm rows  fp32, relative L2 <= FP_TOL per token
+  RMSNorm / gated-norm rows  fp32, relative L2 <= FP_TOL per token; when the
+  and SwiGLU rows            op writes the next Q8_0 GEMM's activation itself,
+                             that activation against the reference quantizer
+                             of the oracle's row (as decoder_ops checks
+                             quantized outputs: boundary flips only)
   GEMMs                      the reference quantizer applied to the GPU's fp32
                              input row (Q8_0 per 32 elements, Q4_K per
-                             sub-block), then the oracle's matvec on that
-                             activation (+ the residual row for the output
-                             projections): relative L2 <= FP_TOL per token
+                             sub-block), or the GPU's own activation where the
+                             producing op wrote it, then the oracle's matvec on
+                             that activation (+ the residual row for the
+                             output projections): relative L2 <= FP_TOL per
+                             token
   conv + gates               q, k (L2-normalized), v, decay, beta per token
                              within FP_TOL, the conv ring's new slots bit-exact
   delta rule                 the oracle's token loop from the GPU's state:
@@ -64,6 +70,15 @@ class PrefillChecker(OpChecker):
         for t in range(got.shape[0]):
             self._fp(op, got[t], ref[t], f"{what} token {t}")
 
+    def _rows_out(self, op, ev, width, ref, where):
+        """A row op's output: fp32 rows, or the Q8_0 GEMM activation it wrote."""
+        if ev.x_out == E.B_PF_ACT:
+            xq, xd = self.eng.read_gemm_act(E.B_PF_ACT, self.T, width)
+            for t in range(self.T):
+                self._quant(op, xq[t], xd[t], ref[t], f"{where} token {t} activation")
+        else:
+            self._fp_rows(op, self._rows(E.B_PF_N, width), ref, where)
+
     def _sub(self, n):
         """Row subset of an n-row matrix (all rows unless rows_per_matrix)."""
         return OpChecker._rows(self, n)
@@ -83,7 +98,10 @@ class PrefillChecker(OpChecker):
             b["x"] = self._rows(E.B_PF_X, self.H)
         elif op in _MV_OF:
             W, K, fmt = self._matrix(_MV_OF[op], L)
-            b["x"] = self._rows(ev.x_in, K)
+            if ev.x_in == E.B_PF_ACT:
+                b["xq"], b["xd"] = eng.read_gemm_act(E.B_PF_ACT, self.T, K)
+            else:
+                b["x"] = self._rows(ev.x_in, K)
             if op in (E.OP_PF_GEMM_OUT, E.OP_PF_GEMM_DOWN):
                 b["res"] = self._rows(E.B_PF_X, self.H)
         elif op == E.OP_PF_CONV:
@@ -122,8 +140,7 @@ class PrefillChecker(OpChecker):
             n = self.norms.get(L, 0)
             self.norms[L] = n + 1
             w = self.m["layers"][L]["ffn_norm" if n % 2 else "attn_norm"]
-            got = self._rows(E.B_PF_N, self.H)
-            self._fp_rows(op, got, np.stack([oc.rmsnorm(b["x"][t], w) for t in range(T)]), where)
+            self._rows_out(op, ev, self.H, np.stack([oc.rmsnorm(b["x"][t], w) for t in range(T)]), where)
         elif op in _MV_OF:
             W, K, fmt = self._matrix(_MV_OF[op], L)
             N = W.shape[0]
@@ -131,7 +148,9 @@ class PrefillChecker(OpChecker):
             rows = self._sub(N)
             Wr = np.ascontiguousarray(W[rows])
             for t in range(T):
-                if fmt == E.Q4_K:
+                if "xq" in b:
+                    ref = oc.matvec_q8_0(Wr, oc.dequant_act_q8_0(b["xq"][t], b["xd"][t]))
+                elif fmt == E.Q4_K:
                     xq, xd, _ = oc.quantize_act_q4_K(b["x"][t])
                     ref = oc.matvec_q4_K(Wr, oc.dequant_act_q4_K(xq, xd))
                 else:
@@ -146,11 +165,10 @@ class PrefillChecker(OpChecker):
             self._check_delta_chunk(L, b, where)
         elif op == E.OP_PF_GATED_NORM:
             y = self.m["layers"][L]
-            got = self._rows(E.B_PF_N, self.V)
             z0 = c.conv_dim
             ref = np.stack([oc.gated_rmsnorm(b["core"][t], b["proj"][t][z0:z0 + self.V], y["ssm_norm"],
                                              c.ssm_heads, 128).reshape(-1) for t in range(T)])
-            self._fp_rows(op, got, ref, where)
+            self._rows_out(op, ev, self.V, ref, where)
         elif op == E.OP_PF_ROPE_APPEND:
             self._check_rope_chunk(L, b, where)
         elif op == E.OP_PF_ATTN:
@@ -163,9 +181,8 @@ class PrefillChecker(OpChecker):
                                      ctx).reshape(-1)
                 self._fp(op, got[t], ref, f"{where} token {t}")
         elif op == E.OP_PF_SWIGLU:
-            got = self._rows(E.B_PF_N, self.F)
             F = self.F
-            self._fp_rows(op, got, np.stack([oc.swiglu(g[:F], g[F:]) for g in b["gu"]]), where)
+            self._rows_out(op, ev, F, np.stack([oc.swiglu(g[:F], g[F:]) for g in b["gu"]]), where)
         elif op == E.OP_PF_HEAD:
             W, K, fmt = self._matrix(E.OP_LM_HEAD, -1)
             xq, xd = eng.read_act(E.B_PF_ACT1, self.H, M=1, fmt=fmt)

@@ -98,6 +98,40 @@ def test_row_ops(hip, oc, H):
     assert rel_l2(host(y).reshape(M, n_v, 128), ref) < 1e-6
 
 
+@pytest.mark.parametrize("M,H,F,n_v", [(5, 640, 384, 3), (37, 2560, 9216, 32), (16, 4000, 160, 1)])
+def test_row_ops_gemm_act(hip, M, H, F, n_v):
+    """The _gemm_act row ops write byte for byte what the fp32 row op followed
+    by ec_gemm_quantize_act writes: block bytes, scales, padding tokens (M not
+    a multiple of 16) and padding blocks (H = 4000, F = 160: K not a multiple
+    of 128)."""
+    import torch
+    from echohip.lib import Q8_0
+
+    def both(K, fp32_op, fused_op):
+        nbytes = hip.gemm_act_bytes(Q8_0, M, K)
+        y = empty(M * K, torch.float32)
+        ref = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+        got = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+        fp32_op(y)
+        hip.gemm_quantize_act(Q8_0, y, ref, M, K)
+        fused_op(got)
+        r, g = host(ref), host(got)
+        assert np.array_equal(r, g), f"K {K}: {np.count_nonzero(r != g)} bytes differ"
+
+    x = (3 * synth.normal(synth.stream_seed(16, 0), M * H)).astype(np.float32).reshape(M, H)
+    w = (1 + 0.1 * synth.normal(synth.stream_seed(17, 0), H)).astype(np.float32)
+    xd, wd = dev(x), dev(w)
+    both(H, lambda y: hip.rmsnorm_rows(xd, wd, y, M, H), lambda a: hip.rmsnorm_rows_gemm_act(xd, wd, a, M, H))
+    gu = dev((2 * synth.normal(synth.stream_seed(18, 0), M * 2 * F)).astype(np.float32))
+    both(F, lambda y: hip.swiglu_rows(gu, y, M, F), lambda a: hip.swiglu_rows_gemm_act(gu, a, M, F))
+    Nin, z_off = n_v * 128 + 300, 200
+    core = dev(synth.normal(synth.stream_seed(19, 0), M * n_v * 128).astype(np.float32))
+    proj = dev(synth.normal(synth.stream_seed(20, 0), M * Nin).astype(np.float32))
+    nw = dev((1 + 0.1 * synth.normal(synth.stream_seed(21, 0), 128)).astype(np.float32))
+    both(n_v * 128, lambda y: hip.gated_norm_rows(core, proj, Nin, z_off, nw, y, M, n_v),
+         lambda a: hip.gated_norm_rows_gemm_act(core, proj, Nin, z_off, nw, a, M, n_v))
+
+
 def _states(eng, cfg, seq):
     from echohip.engine import S_CONV, S_KEYS, S_KSCALES, S_SSM, S_VALS, S_VSCALES
     out = {}
