@@ -304,14 +304,18 @@ __global__ __launch_bounds__(128) void k_conv_gates(const float* __restrict__ pr
 // taps come from L1), the same sums as k_conv_gates (conv_ring's tap order)
 // with the taps of positions >= p0 read from earlier rows of the chunk and
 // older ones from the ring.  The ring is updated afterwards by
-// k_conv_ring_chunk.  (One token per workgroup: 32768 two-wave workgroups for
-// a 512-token chunk, 19.9 us.)
+// k_conv_ring_chunk (in the four-tap kernel by the token-group-0 workgroups
+// themselves).  (One token per workgroup: 32768 two-wave workgroups for a
+// 512-token chunk, 19.9 us.)
 constexpr uint32_t kConvTokensPerBlock = 8;
 // Four-tap case (the model's conv kernel): the 8 tokens' inputs and their 3
 // earlier taps are loaded once into registers (11 loads per thread, all in
 // flight), the 8 tokens computed together, one barrier for their L2 norms.
+// The workgroups of token group 0 are the only readers of the ring: each then
+// writes its channels' new ring slots (the chunk's last min(T, 4) inputs),
+// after its taps have been used.
 __global__ __launch_bounds__(128) void k_conv_gates_chunk4(const float* __restrict__ proj, uint32_t Nin,
-                                                           const float* __restrict__ ring,
+                                                           float* ring,
                                                            const float* __restrict__ conv_w,
                                                            const float* __restrict__ a_log,
                                                            const float* __restrict__ dt_bias, float* __restrict__ q_out,
@@ -348,6 +352,12 @@ __global__ __launch_bounds__(128) void k_conv_gates_chunk4(const float* __restri
 #pragma unroll
         for (int k = 1; k < (int)KERN; ++k) acc = fmaf(xs[tt + KERN - 1 - k], wv[KERN - 1 - k], acc);
         a[tt] = silu(acc);
+    }
+    if (blockIdx.y == 0) {
+        for (uint32_t j = 0; j < min(T, KERN); ++j) {
+            const uint32_t t = T - 1 - j;
+            ring[(size_t)((p0 + t) % KERN) * conv_dim + c] = proj[(size_t)t * Nin + c];
+        }
     }
     const uint32_t nt = min((uint32_t)TPB, T - (uint32_t)t0);
     if (c >= 2 * key_dim) {  // v head (the whole workgroup)
@@ -876,12 +886,11 @@ extern "C" int ec_glue_conv_gates_chunk(const float* proj, uint32_t Nin, float* 
     const uint32_t conv_dim = 2 * n_k * 128 + n_v * 128;
     hipStream_t st = (hipStream_t)stream;
     const dim3 grid(2 * n_k + n_v, (T + kConvTokensPerBlock - 1) / kConvTokensPerBlock);
-    if (kern == 4)
-        hipLaunchKernelGGL(k_conv_gates_chunk4, grid, dim3(128), 0, st, proj, Nin, ring, conv_w, a_log, dt_bias, q, k,
-                           v, dec, beta, T, p0, n_k, n_v);
-    else
-        hipLaunchKernelGGL(k_conv_gates_chunk, grid, dim3(128), 0, st, proj, Nin, ring, conv_w, a_log, dt_bias, q, k,
-                           v, dec, beta, T, p0, n_k, n_v, kern);
+    if (kern == 4)  // updates the ring itself
+        EC_GLUE_LAUNCH(k_conv_gates_chunk4, grid, dim3(128), 0, st, proj, Nin, ring, conv_w, a_log, dt_bias, q, k, v,
+                       dec, beta, T, p0, n_k, n_v);
+    hipLaunchKernelGGL(k_conv_gates_chunk, grid, dim3(128), 0, st, proj, Nin, ring, conv_w, a_log, dt_bias, q, k, v,
+                       dec, beta, T, p0, n_k, n_v, kern);
     EC_CHECK_LAUNCH();
     EC_GLUE_LAUNCH(k_conv_ring_chunk, dim3((conv_dim + 255) / 256, T < kern ? T : kern), dim3(256), 0, st, proj, Nin,
                    ring, conv_dim, T, p0, kern);
