@@ -403,7 +403,9 @@ def pmc_cases(hip, which):
     at M = 1 (Q8_0 9216 x 2560, Q4_K 9216 x 2560 and 2560 x 9216), `attention` runs the decode
     attention at 512 / 4096 / 32768 positions (16 query heads, 4 KV heads,
     head_dim 256, one sequence), `gemm` the M = 512 prefill GEMMs (Q8_0 and
-    Q4_K, 9216 x 2560 and 2560 x 9216), PMC_LAUNCHES times each on different
+    Q4_K, 9216 x 2560 and 2560 x 9216), `deltanet` the 1024-token 32-head
+    recurrence (token loop, chunked scan) and the batch-8 fused decode update,
+    PMC_LAUNCHES times each on different
     buffer copies of a >= 512 MB rotation; then the calibration kernels of
     pmc_workload (a 256 MiB read, a 256 MiB fill)."""
     st = torch.cuda.current_stream().cuda_stream
@@ -489,6 +491,47 @@ def pmc_cases(hip, which):
                     torch.cuda.synchronize()
                 del Wd, tiled, x, act, y
                 torch.cuda.empty_cache()
+    elif which == "deltanet":
+        # the 1024-token, 32-head recurrence (token loop, then chunked scan) and
+        # the decode step's fused delta-net update at batch 8 (4B shapes: 32
+        # value heads, 16 key heads, conv kernel 4)
+        T, n_v, d = 1024, 32, 128
+        g = torch.Generator(device="cuda").manual_seed(0)
+        state = torch.randn((n_v, d, d), generator=g, device="cuda") * 0.02
+        q = torch.nn.functional.normalize(torch.randn((T, n_v, d), generator=g, device="cuda"), dim=-1)
+        k = torch.nn.functional.normalize(torch.randn((T, n_v, d), generator=g, device="cuda"), dim=-1)
+        v = torch.randn((T, n_v, d), generator=g, device="cuda")
+        dec = torch.sigmoid(torch.randn((T, n_v), generator=g, device="cuda") * 0.5 + 2)
+        bet = torch.sigmoid(torch.randn((T, n_v), generator=g, device="cuda"))
+        out = torch.empty((T, n_v, d), device="cuda")
+        ws = torch.empty(hip.deltanet_chunked_ws_bytes(T, 1, n_v), dtype=torch.uint8, device="cuda")
+        torch.cuda.synchronize()
+        for _ in range(PMC_LAUNCHES):
+            hip.deltanet(state, q, k, v, dec, bet, out, T, 1, n_v, n_v, d, d, stream=st)
+            torch.cuda.synchronize()
+        for _ in range(PMC_LAUNCHES):
+            hip.deltanet_chunked(state, q, k, v, dec, bet, out, T, 1, n_v, n_v, d, d, ws, stream=st)
+            torch.cuda.synchronize()
+        del q, k, v, dec, bet, out, ws
+        B, n_k, kern = 8, 16, 4
+        conv_dim = 2 * n_k * d + n_v * d
+        Nin = conv_dim + n_v * d + 2 * n_v
+        proj = torch.randn((B, Nin), generator=g, device="cuda")
+        conv_state = torch.randn((B, kern, conv_dim), generator=g, device="cuda") * 0.1
+        conv_w = torch.randn((kern, conv_dim), generator=g, device="cuda") * 0.3
+        a_log = torch.randn(n_v, generator=g, device="cuda") * 0.1
+        dt_bias = torch.randn(n_v, generator=g, device="cuda") * 0.1
+        norm_w = 1 + 0.1 * torch.randn(d, generator=g, device="cuda")
+        states = torch.randn((3, B, n_v, d, d), generator=g, device="cuda") * 0.02
+        act = torch.empty(hip.act_bytes(L.Q8_0, B, n_v * d), dtype=torch.uint8, device="cuda")
+        pos = torch.arange(100, 100 + B, dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+        for i in range(PMC_LAUNCHES):
+            hip.delta_step(proj, Nin, conv_state, conv_w, a_log, dt_bias, norm_w, states[i % 3], act, pos, B, n_k,
+                           n_v, kern, stream=st)
+            torch.cuda.synchronize()
+        del states
+        torch.cuda.empty_cache()
     else:
         raise ValueError(which)
     bufs = [torch.full((CALIB_BYTES,), 1, dtype=torch.uint8, device="cuda") for _ in range(3)]
