@@ -43,49 +43,54 @@ __device__ __forceinline__ long gpack2(uint32_t lo, uint32_t hi) {
 }
 
 // ----------------------------------------------------------- activation prep
-// Q4_K: grid (ceil(Kp/32 / 8), Mp tokens), block 256: eight 32-lane groups,
-// one sub-block each, one lane per element; sub-block s of super-block b/8
-// holds the 32 positions pos(s, i) (reference order, oc_q4k_pos).  Each run of
-// 8 bytes of the tiled layout is gathered with shuffles and stored by one lane.
-__global__ __launch_bounds__(256) void k_gemm_quantize_x_q4(const float* __restrict__ x, uint8_t* __restrict__ xt,
-                                                            uint32_t M, uint32_t K, uint32_t ldx, uint32_t nch,
-                                                            uint32_t nbp, size_t xd_off, size_t dxs_off) {
-    const uint32_t b = blockIdx.x * 8 + (threadIdx.x >> 5), m = blockIdx.y, i = threadIdx.x & 31;
-    if (b >= nbp) return;  // whole 32-lane groups leave together
-    const uint32_t s = b % 8;  // sub-block of super-block b/8
-    const uint32_t p = (i < 16) ? 64 * (s / 2) + 16 * (s % 2) + i : 64 * (s / 2) + 32 + 16 * (s % 2) + (i - 16);
-    const uint32_t k = 256 * (b / 8) + p;
-    const bool real = m < M && k < K;
-    const float v = real ? x[(size_t)m * ldx + k] : 0.0f;
-    float amax = fabsf(v);
-    amax = fmaxf(amax, lane_xor<1>(amax));
-    amax = fmaxf(amax, lane_xor<2>(amax));
-    amax = fmaxf(amax, lane_xor<4>(amax));
-    amax = fmaxf(amax, lane_xor<8>(amax));
-    amax = fmaxf(amax, lane_xor<16>(amax));
-    const float scale = q_scale(amax);
-    const float inv = __fdiv_rn(1.0f, scale);
-    const int8_t q = q_body(v, inv);  // a 32-element row: all elements are in whole 8-chunks
-    const uint32_t T = m / 16, r = m % 16;
-    // 4 consecutive elements' bytes, gathered at the first lane of each 4
-    const uint32_t qb = (uint8_t)q;
-    const uint32_t w4 = qb | (row_down<1>(qb) << 8) | (row_down<2>(qb) << 16) | (row_down<3>(qb) << 24);
-    // elements 4g..4g+3 are bytes 0..3 and elements 16+4g..16+4g+3 bytes
-    // 4..7 of lane r + 16g of sub-block pair s/2
-    const uint32_t hi = __shfl_down(w4, 16, 32);
-    if (i < 16 && (i & 3) == 0) {
-        const uint32_t l = r + 16 * (i / 4);
-        *(uint2*)(xt + ((size_t)T * nch + b / 8) * 4096 + (s / 2) * 1024 + 16 * l + 8 * (s % 2)) = make_uint2(w4, hi);
+// Q4_K with 16-byte loads: a wave takes one super-block (256 elements) of its
+// token per step, lane l elements 4l .. 4l+3.  Sub-block s = 2h + j holds the
+// runs 64h + 16j + (0..15) and 64h + 32 + 16j + (0..15) (the reference's
+// position order), i.e. lanes 16h + 4j + (0..3) and those 8 above: the
+// sub-block's amax and int8 sum take xor 1, 2, 8 over its 8 lanes, and the
+// run-0 lane stores its 4 bytes with the run-1 lane's 4 (bytes 4g .. 4g+3 and
+// 16+4g .. 16+4g+3 of operand lane token%16 + 16g).  The reference
+// quantizer per sub-block (scale = amax/127, bytes rne(x * (1/scale)), dxs =
+// scale * the sub-block's int8 sum).  grid (ceil(nch / 2), Mp / 4).
+__global__ __launch_bounds__(256) void k_gemm_quantize_x4v(const float* __restrict__ x, uint8_t* __restrict__ xt,
+                                                           uint32_t M, uint32_t K, uint32_t ldx, uint32_t nch,
+                                                           uint32_t nbp, size_t xd_off, size_t dxs_off) {
+    const uint32_t lane = threadIdx.x & 63, m = blockIdx.y * 4 + (threadIdx.x >> 6);
+    const uint32_t b0 = blockIdx.x * 2, h = lane / 16, j = (lane & 7) / 4, g = lane & 3;
+    const uint32_t s = 2 * h + j;
+    float4 v[2];
+#pragma unroll
+    for (uint32_t st = 0; st < 2; ++st) {
+        const uint32_t k = 256 * (b0 + st) + 4 * lane;  // K % 256 == 0
+        v[st] = (m < M && k < K) ? *(const float4*)(x + (size_t)m * ldx + k) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    int sum = q;
-    sum += lane_xor_i<1>(sum);
-    sum += lane_xor_i<2>(sum);
-    sum += lane_xor_i<4>(sum);
-    sum += lane_xor_i<8>(sum);
-    sum += lane_xor_i<16>(sum);
-    if (i == 0) {
-        ((float*)(xt + xd_off))[(size_t)m * nbp + b] = m < M ? scale : 0.0f;
-        ((float*)(xt + dxs_off))[(size_t)m * nbp + b] = scale * (float)sum;
+#pragma unroll
+    for (uint32_t st = 0; st < 2; ++st) {
+        const uint32_t b = b0 + st;
+        if (b >= nch) break;  // uniform over the wave
+        float amax = fmaxf(fmaxf(fabsf(v[st].x), fabsf(v[st].y)), fmaxf(fabsf(v[st].z), fabsf(v[st].w)));
+        amax = fmaxf(amax, lane_xor<1>(amax));
+        amax = fmaxf(amax, lane_xor<2>(amax));
+        amax = fmaxf(amax, lane_xor<8>(amax));
+        const float scale = q_scale(amax);
+        const float inv = __fdiv_rn(1.0f, scale);
+        const int8_t q0 = q_body(v[st].x, inv), q1 = q_body(v[st].y, inv), q2 = q_body(v[st].z, inv),
+                     q3 = q_body(v[st].w, inv);
+        const uint32_t w4 = (uint32_t)(uint8_t)q0 | ((uint32_t)(uint8_t)q1 << 8) | ((uint32_t)(uint8_t)q2 << 16) |
+                            ((uint32_t)(uint8_t)q3 << 24);
+        const uint32_t hi = row_down<8>(w4);
+        int sum = (int)q0 + (int)q1 + (int)q2 + (int)q3;
+        sum += lane_xor_i<1>(sum);
+        sum += lane_xor_i<2>(sum);
+        sum += lane_xor_i<8>(sum);
+        if ((lane & 8) == 0) {  // run-0 lanes
+            const uint32_t l = m % 16 + 16 * g;
+            *(uint2*)(xt + ((size_t)(m / 16) * nch + b) * 4096 + h * 1024 + 16 * l + 8 * j) = make_uint2(w4, hi);
+            if (g == 0) {
+                ((float*)(xt + xd_off))[(size_t)m * nbp + 8 * b + s] = m < M ? scale : 0.0f;
+                ((float*)(xt + dxs_off))[(size_t)m * nbp + 8 * b + s] = scale * (float)sum;
+            }
+        }
     }
 }
 
@@ -368,8 +373,8 @@ extern "C" int ec_gemm_quantize_act(int fmt, const float* x, void* act, uint32_t
         hipLaunchKernelGGL(k_gemm_quantize_x8, dim3((nbp + 8 * kQxSteps - 1) / (8 * kQxSteps), L.Mp / 4), dim3(256), 0,
                            (hipStream_t)stream, x, (uint8_t*)act, M, K, K, L.nch, nbp, L.xd_off);
     else
-        hipLaunchKernelGGL(k_gemm_quantize_x_q4, dim3((nbp + 7) / 8, L.Mp), dim3(256), 0, (hipStream_t)stream, x,
-                           (uint8_t*)act, M, K, K, L.nch, nbp, L.xd_off, L.dxs_off);
+        hipLaunchKernelGGL(k_gemm_quantize_x4v, dim3((L.nch + 1) / 2, L.Mp / 4), dim3(256), 0, (hipStream_t)stream,
+                           x, (uint8_t*)act, M, K, K, L.nch, nbp, L.xd_off, L.dxs_off);
     EC_CHECK_LAUNCH();
     return EC_OK;
 }
