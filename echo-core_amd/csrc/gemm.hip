@@ -367,6 +367,8 @@ extern "C" int ec_gemm_quantize_act(int fmt, const float* x, void* act, uint32_t
     if (M == 0) return EC_OK;
     if (!x || !act || (fmt != EC_Q8_0 && fmt != EC_Q4_K) || K == 0 || K % 32 || (fmt == EC_Q4_K && K % 256))
         return ec_set_error(EC_ERR_ARG, "ec_gemm_quantize_act: bad argument (Q8_0: K % 32 == 0, Q4_K: K % 256 == 0)");
+    if ((uintptr_t)x % 16)  // the quantizers read x with 16-byte loads
+        return ec_set_error(EC_ERR_ARG, "ec_gemm_quantize_act: x must be 16-byte aligned");
     const XtLayout L = xt_layout(fmt, M, K);
     const uint32_t nbp = L.Kp / 32;
     if (fmt == EC_Q8_0)

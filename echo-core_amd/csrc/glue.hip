@@ -984,9 +984,14 @@ extern "C" int ec_glue_qk_rope_append(const float* proj, uint32_t Nin, const flo
                                         n_heads, n_kv, head_dim, stream);
 }
 
-extern "C" int ec_glue_argmax_advance(const float* logits, uint32_t vocab, int32_t* gen, int32_t* next, int32_t* pos,
-                                      uint32_t n_seq, uint32_t max_pos, void* stream) {
+extern "C" int ec_glue_argmax_advance_bounded(const float* logits, uint32_t vocab, int32_t* gen, int32_t* next,
+                                              int32_t* pos, uint32_t n_seq, uint32_t max_pos, void* stream) {
     if (!logits || !gen || !next || !pos) return ec_set_error(EC_ERR_ARG, "ec_glue_argmax_advance: bad argument");
     EC_GLUE_LAUNCH(k_argmax_advance, dim3(n_seq), dim3(1024), 0, (hipStream_t)stream, logits, vocab, gen, next, pos,
                    max_pos);
+}
+
+extern "C" int ec_glue_argmax_advance(const float* logits, uint32_t vocab, int32_t* gen, int32_t* next, int32_t* pos,
+                                      uint32_t n_seq, void* stream) {
+    return ec_glue_argmax_advance_bounded(logits, vocab, gen, next, pos, n_seq, 0, stream);
 }

@@ -434,7 +434,7 @@ int record_step(ec_engine* e) {
     EC_MV(EC_OP_LM_HEAD, -1, 0, aid(e->lm_head, EC_B_ACT_H, EC_B_ACT4_H),
           mv(e, e->lm_head, ain(e->lm_head, e->act_h, e->act4_h), e->logits, c.vocab, 0));
     EC_GLUE(EC_OP_ARGMAX, -1, 0, -1, -1,
-            ec_glue_argmax_advance(e->logits, c.vocab, e->gen, e->tok, e->pos, B, c.max_ctx, st));
+            ec_glue_argmax_advance_bounded(e->logits, c.vocab, e->gen, e->tok, e->pos, B, c.max_ctx, st));
     return EC_OK;
 #undef EC_GLUE
 #undef EC_MV
@@ -1139,8 +1139,8 @@ int prefill_step(ec_engine* e, Lane& L, PrefillJob& j) {
                          e->c.vocab, e->H, e->c.vocab, 0, L.st);
     }));
     EC_HIP(hipMemcpyAsync(e->pos + j.seq, &last, 4, hipMemcpyHostToDevice, L.st));
-    EC_TRY(ec_glue_argmax_advance(e->logits + (size_t)j.seq * e->c.vocab, e->c.vocab, e->gen + j.seq,
-                                  e->tok + j.seq, e->pos + j.seq, 1, e->c.max_ctx, L.st));
+    EC_TRY(ec_glue_argmax_advance_bounded(e->logits + (size_t)j.seq * e->c.vocab, e->c.vocab, e->gen + j.seq,
+                                          e->tok + j.seq, e->pos + j.seq, 1, e->c.max_ctx, L.st));
     EC_HIP(hipStreamSynchronize(L.st));  // `last` lives on this frame
     return EC_OK;
 }

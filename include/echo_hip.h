@@ -124,7 +124,7 @@ int ec_kv_append(const float* k, const float* v, int8_t* keys, int8_t* vals, flo
  * scaling: Q8_0 Y += dx*dw*isum; Q4_K Y += dx*(d*sc*isum - dmin*m*xsum).
  * ldy >= N; accumulate != 0 adds to Y. */
 size_t ec_gemm_act_bytes(int fmt, uint32_t M, uint32_t K);
-int ec_gemm_quantize_act(int fmt, const float* x, void* act, uint32_t M, uint32_t K, void* stream);
+int ec_gemm_quantize_act(int fmt, const float* x, void* act, uint32_t M, uint32_t K, void* stream);  /* x 16-byte aligned */
 int ec_gemm(int fmt, const void* tiled, const void* act, float* y, uint32_t M, uint32_t N, uint32_t K, uint32_t ldy,
             int accumulate, void* stream);
 
@@ -272,11 +272,16 @@ int ec_glue_qk_rope_append_split(const float* proj, uint32_t nparts, uint32_t Ni
                                  uint64_t seq_stride, uint32_t max_ctx, uint32_t n_heads, uint32_t n_kv,
                                  uint32_t head_dim, void* stream);
 /* Greedy pick (first maximum) of every active sequence (pos[s] >= 0):
- * gen[s] = next[s] = argmax, pos[s] += 1; when the new position would be
- * >= max_pos (the KV cache length; 0 = no limit) the sequence is instead
- * made inactive, pos[s] = -1, after its last token is written to gen. */
+ * gen[s] = next[s] = argmax, pos[s] += 1.  The _bounded form stops a
+ * sequence at the cache end: when the new position would be >= max_pos (the
+ * KV cache length; 0 = no limit) the sequence is instead made inactive,
+ * pos[s] = -1, after its last token is written to gen.
+ * ec_glue_argmax_advance keeps its original signature and has no limit
+ * (max_pos = 0). */
 int ec_glue_argmax_advance(const float* logits, uint32_t vocab, int32_t* gen, int32_t* next, int32_t* pos,
-                           uint32_t n_seq, uint32_t max_pos, void* stream);
+                           uint32_t n_seq, void* stream);
+int ec_glue_argmax_advance_bounded(const float* logits, uint32_t vocab, int32_t* gen, int32_t* next, int32_t* pos,
+                                   uint32_t n_seq, uint32_t max_pos, void* stream);
 
 /* ------------------------------------------------- chunked prefill glue
  * T consecutive tokens of ONE sequence at positions p0 .. p0+T-1.

@@ -101,3 +101,19 @@ int main() {
     enc = np.array([int(s, 16) for s in out[65536:]], np.uint32).astype(np.uint16)
     want = probes.astype(np.float16).view(np.uint16)
     assert np.array_equal(enc, want), np.flatnonzero(enc != want)[:10]
+
+
+def test_argument_checks_before_any_gpu_call():
+    """Entry points refuse bad arguments on the host, before any HIP call (no GPU needed): a GEMM activation
+    source that is not 16-byte aligned (the quantizer reads 16-byte pieces), and null pointers for the greedy
+    pick in both its original and its bounded form."""
+    lib = C.CDLL(str(LIB))
+    lib.ec_last_error.restype = C.c_char_p
+    vp = C.c_void_p
+    lib.ec_gemm_quantize_act.argtypes = [C.c_int, vp, vp, C.c_uint32, C.c_uint32, vp]
+    assert lib.ec_gemm_quantize_act(6, 0x10004, 0x20000, 4, 256, None) == 1
+    assert b"16-byte aligned" in lib.ec_last_error()
+    lib.ec_glue_argmax_advance.argtypes = [vp, C.c_uint32, vp, vp, vp, C.c_uint32, vp]
+    assert lib.ec_glue_argmax_advance(None, 100, None, None, None, 1, None) == 1
+    lib.ec_glue_argmax_advance_bounded.argtypes = [vp, C.c_uint32, vp, vp, vp, C.c_uint32, C.c_uint32, vp]
+    assert lib.ec_glue_argmax_advance_bounded(None, 100, None, None, None, 1, 64, None) == 1

@@ -8,13 +8,22 @@ echo-core-zig/src/kernels/qwen_linear.zig:103-271) and no Zig toolchain is
 available to produce vectors, so these cases are chosen from the mathematics
 of qwen_linear.zig:215-219 (gates) and :252-257 (gated norm) so that a dropped
 softplus, a dropped SiLU(z), a swapped gate/up, a wrong slice of the fused
-projection or a transposed state fails:
+projection (the alpha/beta rows, and the q / k order, which only a non-zero
+initial state with q != k can show: from S0 = 0 the first token is symmetric
+in q and k) or a transposed state fails:
 
   softplus(0) = ln 2          ->  alpha + dt_bias = 0 gives decay 2^-exp(A_log)
   softplus(x > 20) = x        ->  decay = exp(-exp(A_log) * x)
   sigmoid(0) = 1/2            ->  beta = 0.5
+  sigmoid(-63.5) ~ 3e-28      ->  beta ~ 0: o = decay * S0^T q / sqrt(128)
   z = 0                       ->  SiLU(z) = 0, so the gated norm is 0
   constant core c             ->  w * c / sqrt(c^2 + 1e-6) * SiLU(z)
+
+The attention block (engine.zig:520-621) is pinned at position 1, where the
+softmax runs over two keys: equal scores give the mean of the two cached V
+rows (the block attends over pos + 1 positions, itself included), and an
+fp64 brute force over the oracle's own cache pins the q / k head RMSNorm
+(applied only when its weight is not all zero, :548-553) and RoPE.
 
 The block tests use Q8_0 matrices whose rows are unit vectors (d = 1.0 and a
 single qs = 1), so every projection is an exact copy of its input slice and
@@ -280,3 +289,168 @@ def test_decoder_token_composes_the_blocks(oc):
                 x = (x + parts.ffn_block(l, rms(x, y["ffn_norm"]))).astype(np.float32)
             ref = oc.matvec_act_q8_0(m["lm_head"], rms(x, m["final_norm"]), quant_act)
             assert np.array_equal(lg, ref)
+
+
+# ------------------------------------------------------- head RMSNorm (q, k)
+def test_head_rmsnorm_closed_forms(oc):
+    """oc_head_rmsnorm (engine.zig:507-518): each head of head_dim values is RMS-normalised on its own and scaled
+    by the same per-dimension weight."""
+    n_h, hd = 3, 256
+    w = (1.0 + 0.1 * synth.normal(80, hd)).astype(np.float32)
+    # a constant head c: mean(c^2) = c^2 -> w * c / sqrt(c^2 + 1e-6)
+    c = np.array([0.5, -3.0, 1e-3], np.float32)
+    got = oc.head_rmsnorm(np.repeat(c, hd), w, n_h, hd).reshape(n_h, hd)
+    c64 = c.astype(np.float64)[:, None]
+    assert rel_l2(got, w[None, :] * c64 / np.sqrt(c64 ** 2 + 1e-6)) < 2e-6
+    # per head: scaling head 1 by 8 changes no head's output (eps aside); head h uses w, not w shifted by h
+    x = (3.0 * synth.normal(81, n_h * hd)).astype(np.float32)
+    a = oc.head_rmsnorm(x, w, n_h, hd).reshape(n_h, hd)
+    x2 = x.reshape(n_h, hd).copy()
+    x2[1] *= 8.0
+    b = oc.head_rmsnorm(x2, w, n_h, hd).reshape(n_h, hd)
+    assert rel_l2(a, b) < 1e-6
+    xh = x.reshape(n_h, hd).astype(np.float64)
+    ref = w[None, :] * xh / np.sqrt(np.mean(xh * xh, axis=1, keepdims=True) + 1e-6)
+    assert rel_l2(a, ref) < 2e-6
+
+
+def _attn_cfg():
+    # q_dim 1024 (4 heads), kv_dim 512 (2 kv heads), hidden 2048 so q, k and v read disjoint input slices
+    return EngineConfig(vocab=64, hidden=2048, ffn=256, n_layers=1, n_heads=4, n_kv=2, head_dim=256, ssm_inner=0,
+                        ssm_heads=0, conv_kernel=4, attn_interval=1, max_batch=1, max_ctx=8)
+
+
+def _attn_model(cfg, q_norm, k_norm, zero_k=False):
+    """q rows copy x[0:1024], k rows x[1024:1536] (zero rows if zero_k), v rows x[1536:2048]; the output projection
+    copies the attention output into out[0:1024]."""
+    H, hd = cfg.hidden, cfg.head_dim
+    q_dim, kv_dim = cfg.n_heads * hd, cfg.n_kv * hd
+    k_rows = np.zeros((kv_dim, H), np.int64) if zero_k else select(kv_dim, H, np.arange(1024, 1536))
+    w_in = np.concatenate([select(q_dim, H, np.arange(q_dim)), k_rows, select(kv_dim, H, np.arange(1536, 2048))])
+    w_out = np.zeros((H, q_dim), np.int64)
+    w_out[np.arange(q_dim), np.arange(q_dim)] = 1
+    y = {"attn": True, "w_in": q8_0_from_int(w_in), "w_out": q8_0_from_int(w_out),
+         "w_gate": q8_0_from_int(np.zeros((cfg.ffn, H))), "w_up": q8_0_from_int(np.zeros((cfg.ffn, H))),
+         "w_down": q8_0_from_int(np.zeros((H, cfg.ffn))), "attn_norm": np.ones(H, np.float32),
+         "ffn_norm": np.ones(H, np.float32), "q_norm": np.asarray(q_norm, np.float32),
+         "k_norm": np.asarray(k_norm, np.float32)}
+    return {"embed": q8_0_from_int(np.zeros((cfg.vocab, H))), "final_norm": np.ones(H, np.float32),
+            "lm_head": q8_0_from_int(np.zeros((cfg.vocab, H))), "layers": [y]}
+
+
+def test_attention_block_attends_over_itself_at_position_1(oc):
+    """k = 0 makes every score 0, so at position 1 the softmax weights the two cached V rows 1/2 each: the output
+    is their mean -- the block appends the token before attending and covers pos + 1 positions
+    (engine.zig:556-567)."""
+    cfg = _attn_cfg()
+    hd = cfg.head_dim
+    m = _attn_model(cfg, np.zeros(hd), np.zeros(hd), zero_k=True)
+    dec = OracleDecoder(oc, cfg, m, n_seq=1, quant_act=False)
+    xs = [synth.normal(90 + p, cfg.hidden).astype(np.float32) for p in range(2)]
+    for pos, x in enumerate(xs):
+        out = dec.attention_block(0, 0, x, pos)
+    vdeq = []
+    for x in xs:  # V row of each position, per (token, kv head) scale
+        vq, vs = oc.quantize(x[1536:2048], hd)
+        vdeq.append(vq.astype(np.float64) * vs[:, None])
+    mean = 0.5 * (vdeq[0] + vdeq[1])
+    ref = np.stack([mean[h % cfg.n_kv] for h in range(cfg.n_heads)]).reshape(-1)
+    assert rel_l2(out[:1024], ref) < 1e-6
+    assert np.array_equal(out[1024:], np.zeros(1024, np.float32))
+
+
+def _rope64(heads, pos, base=10000.0):
+    """GPT-J RoPE of adjacent pairs (d, d+1) at angle pos * base^(-d/head_dim), in fp64."""
+    hd = heads.shape[-1]
+    ang = pos * base ** (-np.arange(0, hd, 2, dtype=np.float64) / hd)
+    c, s = np.cos(ang), np.sin(ang)
+    a, b = heads[..., 0::2], heads[..., 1::2]
+    out = np.empty_like(heads)
+    out[..., 0::2] = a * c - b * s
+    out[..., 1::2] = a * s + b * c
+    return out
+
+
+@pytest.mark.parametrize("normed", [True, False], ids=["head_norm", "zero_norm_weight"])
+def test_attention_block_head_norm_rope_at_position_1(oc, normed):
+    """fp64 brute force of the block at position 1 over the oracle's own cache.  q and k are 3 x N(0,1), so the
+    head RMSNorm (x / rms(x) * w, rms ~ 3) visibly rescales them; an all-zero norm weight means no norm
+    (engine.zig:548-553), not a zero vector.  The cached keys are checked as int8 of RoPE(norm(k)) per
+    (token, kv head), and the output as softmax over both positions of q . k / 16 times the cached V."""
+    cfg = _attn_cfg()
+    hd, n_h, n_kv = cfg.head_dim, cfg.n_heads, cfg.n_kv
+    qn = (1.0 + 0.2 * synth.normal(95, hd)).astype(np.float32) if normed else np.zeros(hd, np.float32)
+    kn = (1.0 + 0.2 * synth.normal(96, hd)).astype(np.float32) if normed else np.zeros(hd, np.float32)
+    dec = OracleDecoder(oc, cfg, _attn_model(cfg, qn, kn), n_seq=1, quant_act=False)
+    xs = []
+    for pos in range(2):
+        x = synth.normal(97 + pos, cfg.hidden).astype(np.float32)
+        x[:1536] *= 3.0
+        xs.append(x)
+        out = dec.attention_block(0, 0, x, pos)
+
+    def prep(v, w, n, pos):
+        h = v.reshape(n, hd).astype(np.float64)
+        if normed:
+            h = w[None, :] * h / np.sqrt(np.mean(h * h, axis=1, keepdims=True) + 1e-6)
+        return _rope64(h, pos)
+
+    st = dec.states[0]
+    keys = st["k"][0].reshape(cfg.max_ctx, n_kv, hd)[:2].astype(np.float64)
+    vals = st["v"][0].reshape(cfg.max_ctx, n_kv, hd)[:2].astype(np.float64)
+    ks = st["ks"][0].reshape(cfg.max_ctx, n_kv)[:2]
+    vs = st["vs"][0].reshape(cfg.max_ctx, n_kv)[:2]
+    for p, x in enumerate(xs):
+        kref = prep(x[1024:1536], kn, n_kv, p)
+        kq, kscale = oc.quantize(kref.astype(np.float32).reshape(-1), hd)
+        assert np.allclose(ks[p], kscale, rtol=1e-6)
+        assert np.mean(kq.reshape(n_kv, hd) != keys[p]) <= 0.01  # int8 of the same values up to rounding ties
+        assert np.abs(kq.reshape(n_kv, hd) - keys[p]).max() <= 1
+    kdeq = keys * ks[:, :, None]
+    vdeq = vals * vs[:, :, None]
+    q = prep(xs[1][:1024], qn, n_h, 1)
+    ref = np.zeros((n_h, hd))
+    for h in range(n_h):
+        s = kdeq[:, h % n_kv, :] @ q[h] / np.sqrt(hd)
+        a = np.exp(s - s.max())
+        a /= a.sum()
+        ref[h] = a @ vdeq[:, h % n_kv, :]
+    assert rel_l2(out[:1024], ref.reshape(-1)) < 1e-5
+    # the two scores differ enough that a change of q's scale would move the output
+    s_spread = [np.ptp(kdeq[:, h % n_kv, :] @ q[h]) / np.sqrt(hd) for h in range(n_h)]
+    assert max(s_spread) > 0.5
+
+
+def test_deltanet_block_q_k_slices_with_nonzero_state(oc):
+    """q rows copy x[0:128] and k rows x[128:256], S0 != 0 and beta ~ 0 (a beta row reading 127 * x[255] with
+    x[255] = -0.5): the state only decays, S1 = decay S0, and o = decay S0^T q_hat / sqrt(128) before the gated
+    norm (qwen_linear.zig:209-211, 221-249).  Swapping the q and k slices gives S0^T k_hat instead."""
+    cfg = _delta_cfg()
+    H = cfg.hidden
+    qkv = np.concatenate([select(128, H, np.arange(128)), select(128, H, np.arange(128, 256)),
+                          select(256, H, np.arange(256))])
+    ab = np.zeros((4, H), np.int64)
+    ab[2, 255] = 127  # beta logits of both heads = 127 * x[255]
+    ab[3, 255] = 127
+    a_log = (0.3, -0.5)
+    m = _delta_model(cfg, qkv, select(256, H, np.arange(256)), w_ab=ab, a_log=a_log)
+    dec = OracleDecoder(oc, cfg, m, n_seq=1, quant_act=False)
+    S0 = (0.02 * synth.normal(100, 2 * 128 * 128)).astype(np.float32)
+    np.copyto(dec.states[0]["ssm"][0], S0)
+    x = synth.normal(101, H).astype(np.float32)
+    x[255] = -0.5
+    out = dec.deltanet_block(0, 0, x)
+    xin = x.astype(np.float64)
+    conv = silu(xin)  # zero conv history, newest tap weight 1: conv output = SiLU(projection)
+    q = conv[:128] / np.sqrt(np.sum(conv[:128] ** 2) + 1e-6)
+    k = conv[128:256] / np.sqrt(np.sum(conv[128:256] ** 2) + 1e-6)
+    decay = 2.0 ** -np.exp(np.array(a_log))  # alpha = 0: softplus(0) = ln 2
+    S = S0.reshape(2, 128, 128).astype(np.float64)  # [head][k][v]
+    o = decay[:, None] * np.einsum("hkv,k->hv", S, q) / np.sqrt(128.0)
+    g = o / np.sqrt(np.mean(o * o, axis=1, keepdims=True) + 1e-6) * m["layers"][0]["ssm_norm"] * silu(xin).reshape(2, 128)
+    assert rel_l2(out, g.reshape(-1)) < 1e-5
+    S1 = dec.states[0]["ssm"][0].reshape(2, 128, 128)
+    assert rel_l2(S1, decay[:, None, None] * S) < 1e-6
+    # the q / k order matters here: S0^T k_hat is far from S0^T q_hat
+    o_k = decay[:, None] * np.einsum("hkv,k->hv", S, k) / np.sqrt(128.0)
+    assert rel_l2(o_k, o) > 0.5
