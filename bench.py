@@ -184,6 +184,9 @@ def main() -> int:
                          "(rocprofv3 counter collection does not follow graph launches)")
     ap.add_argument("--prefill", choices=("chunked", "loop"), default="chunked",
                     help="chunked: ec_engine_prefill per sequence; loop: token by token through the decode graph")
+    ap.add_argument("--act-pieces", type=int, choices=(1, 2), default=2,
+                    help="int8 pieces per decode-matvec activation element (2: within ~2e-5 of the reference's "
+                         "fp32-activation matvec; 1: the reference quantizer alone, ~5e-3)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="after the run, one device-to-device copy of this many MiB (a kernel of known "
                          "traffic, for calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -207,6 +210,7 @@ def main() -> int:
     log(f"engine: {cfg}")
     t0 = time.perf_counter()
     eng = Engine(cfg)
+    eng.set_act_pieces(args.act_pieces)
     eng.init_random(seed=args.seed)
     eng.reset()
     log(f"weights generated and repacked in {time.perf_counter() - t0:.1f} s ({eng.weight_bytes() / 1e9:.3f} GB)")
@@ -323,6 +327,7 @@ def main() -> int:
         "config": {"workload": "hybrid 4B-class Q8_0 decoder: 24 delta-net + 8 attention blocks, hidden 2560, "
                                "ffn 9216, vocab 151936; ragged batch of 8, greedy decode",
                    "global_batch": B, "prompt_lens": lens.tolist(), "decode_steps": W + K,
+                   "act_pieces": args.act_pieces,
                    "prefill": ("chunked (512-token int8-MFMA GEMM chunks per sequence, two sequences in flight)" if args.prefill == "chunked"
                                else "token loop through the decode graph"),
                    "prefill_tok_s": round(prefill_tps, 1),

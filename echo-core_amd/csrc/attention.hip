@@ -458,13 +458,14 @@ constexpr uint32_t kMergeThreads = 64 * kMergeWaves;
 constexpr uint32_t kMergeRegs = 8;  // chunk records per wave loaded per batch (the first with the maxima)
 
 // With act != nullptr the merged rows are also quantized into the Q8_0
-// activation layout (M = n_seq rows, K = n_heads*256; quantize_act's format).
+// activation layout (M = n_seq rows, K = n_heads*256, P pieces;
+// quantize_act's format).
 template <int DS>
 __global__ __launch_bounds__(kMergeThreads) void k_attn_merge(const float* __restrict__ ws, const int32_t* __restrict__ ctx,
                                                     float* __restrict__ out, uint8_t* __restrict__ act,
                                                     uint32_t act_xd_off, uint32_t n_seq, uint32_t n_heads,
                                                     uint32_t n_chunks_max,
-                                                    uint32_t max_ctx, uint32_t chunk) {
+                                                    uint32_t max_ctx, uint32_t chunk, uint32_t P) {
     static_assert(DS == 1 || DS == 2 || DS == 4, "dim slices of 256, 128 or 64");
     constexpr uint32_t HD = 256, SD = HD / DS, LPR = 64 / DS;  // slice dims, lanes per record
     extern __shared__ float w_s[];
@@ -479,7 +480,7 @@ __global__ __launch_bounds__(kMergeThreads) void k_attn_merge(const float* __res
             dst[tid] = 0.0f;
             if (act)
                 store_act_q8_lane(0.0f, act, (float*)(act + act_xd_off), n_seq, n_heads * HD / 32, s,
-                                  h * HD + SD * z + tid);
+                                  h * HD + SD * z + tid, P);
         }
         return;
     }
@@ -553,7 +554,8 @@ __global__ __launch_bounds__(kMergeThreads) void k_attn_merge(const float* __res
         o = o / dn;
         dst[tid] = o;
         if (act)
-            store_act_q8_lane(o, act, (float*)(act + act_xd_off), n_seq, n_heads * HD / 32, s, h * HD + SD * z + tid);
+            store_act_q8_lane(o, act, (float*)(act + act_xd_off), n_seq, n_heads * HD / 32, s, h * HD + SD * z + tid,
+                              P);
     }
 }
 
@@ -583,7 +585,7 @@ template <int G>
 static void launch_mfma(const uint8_t* qa, const float* qsc, const float* qf, const int8_t* keys, const int8_t* vals,
                         const float* ks,
                         const float* vs, float* out, uint8_t* act, const int32_t* ctx, uint32_t n_seq,
-                        uint64_t seq_stride, uint32_t n_kv, uint32_t max_ctx, float* ws, hipStream_t st) {
+                        uint64_t seq_stride, uint32_t n_kv, uint32_t max_ctx, float* ws, hipStream_t st, uint32_t P) {
     const uint32_t CH = attn_chunk(max_ctx, n_kv, n_seq);
     const uint32_t ncm = (max_ctx + CH - 1) / CH;
     const dim3 grid(ncm, n_kv, n_seq);
@@ -599,22 +601,22 @@ static void launch_mfma(const uint8_t* qa, const float* qsc, const float* qf, co
     else
         hipLaunchKernelGGL((k_attn_mfma<G, 64, false>), grid, dim3(256), 0, st, qa, qsc, qf, keys, vals, ks, vs, ctx,
                            seq_stride, n_kv, ncm, max_ctx, ws);
-    const uint32_t xd_off = (uint32_t)act_layout(EC_Q8_0, n_seq, n_kv * G * 256).xd_off;
+    const uint32_t xd_off = (uint32_t)act_layout(EC_Q8_0, P * n_seq, n_kv * G * 256).xd_off;
     // few (head, sequence) pairs: four workgroups per pair, 64 dims each
     if (n_kv * G * n_seq <= 32)
         hipLaunchKernelGGL(k_attn_merge<4>, dim3(n_kv * G, n_seq, 4), dim3(kMergeThreads), ncm * sizeof(float), st, ws,
-                           ctx, out, act, xd_off, n_seq, n_kv * G, ncm, max_ctx, CH);
+                           ctx, out, act, xd_off, n_seq, n_kv * G, ncm, max_ctx, CH, P);
     else
         hipLaunchKernelGGL(k_attn_merge<1>, dim3(n_kv * G, n_seq), dim3(kMergeThreads), ncm * sizeof(float), st, ws,
-                           ctx, out, act, xd_off, n_seq, n_kv * G, ncm, max_ctx, CH);
+                           ctx, out, act, xd_off, n_seq, n_kv * G, ncm, max_ctx, CH, P);
 }
 
 static int mfma_dispatch(uint32_t G, const uint8_t* qa, const float* qsc, const float* qf, const int8_t* keys,
                          const int8_t* vals,
                          const float* ks, const float* vs, float* out, uint8_t* act, const int32_t* ctx,
                          uint32_t n_seq, uint64_t seq_stride, uint32_t n_kv, uint32_t max_ctx, float* ws,
-                         hipStream_t st) {
-#define EC_MF(G_) launch_mfma<G_>(qa, qsc, qf, keys, vals, ks, vs, out, act, ctx, n_seq, seq_stride, n_kv, max_ctx, ws, st)
+                         hipStream_t st, uint32_t P = 1) {
+#define EC_MF(G_) launch_mfma<G_>(qa, qsc, qf, keys, vals, ks, vs, out, act, ctx, n_seq, seq_stride, n_kv, max_ctx, ws, st, P)
     switch (G) {
         case 1: EC_MF(1); break;
         case 2: EC_MF(2); break;
@@ -697,20 +699,30 @@ extern "C" int ec_attn_decode(const float* q, const int8_t* keys, const int8_t* 
     return EC_OK;
 }
 
+extern "C" int ec_attn_decode_packed_pieces(const void* qa, const float* qsc, const int8_t* keys,
+                                            const int8_t* vals, const float* kscales, const float* vscales, float* out,
+                                            void* act_q8, const int32_t* ctx, uint32_t n_seq, uint64_t seq_stride,
+                                            uint32_t n_heads, uint32_t n_kv, uint32_t max_ctx, uint32_t pieces,
+                                            void* ws, void* stream) {
+    if (n_seq == 0) return EC_OK;
+    if (!qa || !qsc || !keys || !vals || !kscales || !vscales || !out || !ctx || !ws || n_kv == 0 ||
+        n_heads % n_kv || max_ctx == 0 || (seq_stride != 0 && seq_stride < (uint64_t)max_ctx * n_kv * 256) ||
+        (act_q8 && n_seq > 16) || (pieces != 1 && pieces != 2))
+        return ec_set_error(EC_ERR_ARG, "ec_attn_decode_packed: bad argument");
+    int rc = mfma_dispatch(n_heads / n_kv, (const uint8_t*)qa, qsc, nullptr, keys, vals, kscales, vscales, out,
+                           (uint8_t*)act_q8, ctx, n_seq, seq_stride, n_kv, max_ctx, (float*)ws, (hipStream_t)stream,
+                           pieces);
+    if (rc) return rc;
+    EC_CHECK_LAUNCH();
+    return EC_OK;
+}
+
 extern "C" int ec_attn_decode_packed(const void* qa, const float* qsc, const int8_t* keys, const int8_t* vals,
                                      const float* kscales, const float* vscales, float* out, void* act_q8,
                                      const int32_t* ctx, uint32_t n_seq, uint64_t seq_stride, uint32_t n_heads,
                                      uint32_t n_kv, uint32_t max_ctx, void* ws, void* stream) {
-    if (n_seq == 0) return EC_OK;
-    if (!qa || !qsc || !keys || !vals || !kscales || !vscales || !out || !ctx || !ws || n_kv == 0 ||
-        n_heads % n_kv || max_ctx == 0 || (seq_stride != 0 && seq_stride < (uint64_t)max_ctx * n_kv * 256) ||
-        (act_q8 && n_seq > 16))
-        return ec_set_error(EC_ERR_ARG, "ec_attn_decode_packed: bad argument");
-    int rc = mfma_dispatch(n_heads / n_kv, (const uint8_t*)qa, qsc, nullptr, keys, vals, kscales, vscales, out,
-                           (uint8_t*)act_q8, ctx, n_seq, seq_stride, n_kv, max_ctx, (float*)ws, (hipStream_t)stream);
-    if (rc) return rc;
-    EC_CHECK_LAUNCH();
-    return EC_OK;
+    return ec_attn_decode_packed_pieces(qa, qsc, keys, vals, kscales, vscales, out, act_q8, ctx, n_seq, seq_stride,
+                                        n_heads, n_kv, max_ctx, 1, ws, stream);
 }
 
 extern "C" size_t ec_attn_qa_bytes(uint32_t n_seq, uint32_t n_heads) { return qa_bytes(n_seq, n_heads); }

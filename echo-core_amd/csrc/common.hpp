@@ -107,6 +107,17 @@ __device__ __forceinline__ int8_t q_tail(float x, float scale) {
     return (int8_t)v;
 }
 
+// Second int8 piece of a two-piece activation: with q0 = q_body(x, inv) at
+// scale s (inv = 1/s), the residual r = fma(-q0, s, x) in steps of s/256,
+// q1 = sat8(rne(r * (inv*256))).  x ~ s*q0 + (s/256)*q1 with |error| <= s/512
+// unless q0 saturated.
+__device__ __forceinline__ int8_t q_piece1(float x, int8_t q0, float scale, float inv) {
+    const float r = fmaf(-(float)q0, scale, x);
+    int v = (int)rintf(__fmul_rn(r, inv * 256.0f));
+    v = v > 127 ? 127 : (v < -128 ? -128 : v);
+    return (int8_t)v;
+}
+
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
 
 // RoPE of element d paired with its neighbour d^1 (value `other`) at angle
@@ -151,14 +162,21 @@ __device__ __forceinline__ float conv_ring(const float* __restrict__ st, const f
     return acc;
 }
 
+// Four lanes' bytes (this lane's and the next three of its row) in one dword.
+__device__ __forceinline__ uint32_t pack4_lanes(uint32_t b) {
+    return b | (row_down<1>(b) << 8) | (row_down<2>(b) << 16) | (row_down<3>(b) << 24);
+}
+
 // Lanes 32m .. 32m+31 of a wave hold the 32 values of one Q8_0 block of
 // activation row i (block sb = k/32, lane % 32 == k % 32): quantize it with the
 // reference quantizer's body rule and store it in the Q8_0 activation layout
-// (quant.hip: element e of block sb = 4G + j at byte ((G*4 + e/8)*M + i)*32 +
-// 8j + e%8, scale at xd[i][sb], nbp = blocks per row).  Four lanes pack their
-// bytes into one dword store.
+// (quant.hip: element e of block sb = 4G + j of layout row r at byte
+// ((G*4 + e/8)*R + r)*32 + 8j + e%8, scale at xd[i][sb], nbp = blocks per
+// row).  P = 2 pieces: M tokens occupy R = 2M layout rows, token i's piece p
+// in row 2i + p (q_piece1 for p = 1); P = 1: R = M, row i.  Four lanes pack
+// their bytes into one dword store.
 __device__ __forceinline__ void store_act_q8_lane(float v, uint8_t* __restrict__ act, float* __restrict__ xd,
-                                                  uint32_t M, uint32_t nbp, uint32_t i, uint32_t k) {
+                                                  uint32_t M, uint32_t nbp, uint32_t i, uint32_t k, uint32_t P = 1) {
     float amax = fabsf(v);
     amax = fmaxf(amax, lane_xor<1>(amax));
     amax = fmaxf(amax, lane_xor<2>(amax));
@@ -167,10 +185,15 @@ __device__ __forceinline__ void store_act_q8_lane(float v, uint8_t* __restrict__
     amax = fmaxf(amax, lane_xor<16>(amax));
     const float scale = q_scale(amax);
     const float inv = __fdiv_rn(1.0f, scale);
-    const uint32_t b = (uint8_t)q_body(v, inv);
-    const uint32_t w = b | (row_down<1>(b) << 8) | (row_down<2>(b) << 16) | (row_down<3>(b) << 24);
+    const int8_t q0 = q_body(v, inv);
+    const uint32_t w = pack4_lanes((uint8_t)q0);
     const uint32_t sb = k / 32, e = k % 32, G = sb / 4, j = sb % 4;
-    if ((e & 3) == 0) *(uint32_t*)(act + (((size_t)G * 4 + e / 8) * M + i) * 32 + 8 * j + (e % 8)) = w;
+    uint8_t* dst = act + (((size_t)G * 4 + e / 8) * (P * M) + P * i) * 32 + 8 * j + (e % 8);
+    if ((e & 3) == 0) *(uint32_t*)dst = w;
+    if (P == 2) {
+        const uint32_t w1 = pack4_lanes((uint8_t)q_piece1(v, q0, scale, inv));
+        if ((e & 3) == 0) *(uint32_t*)(dst + 32) = w1;
+    }
     if (e == 0) xd[(size_t)i * nbp + sb] = scale;
 }
 

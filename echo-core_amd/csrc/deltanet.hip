@@ -206,7 +206,7 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
                                                      const float* __restrict__ norm_w, float* __restrict__ state,
                                                      uint8_t* __restrict__ act, uint32_t xd_off, uint32_t M,
                                                      const int32_t* __restrict__ pos, uint32_t n_k, uint32_t n_v,
-                                                     uint32_t kern, float* __restrict__ yout) {
+                                                     uint32_t kern, float* __restrict__ yout, uint32_t P) {
     __shared__ float q_s[128], k_s[128], v_s[128], o_s[128];
     __shared__ float red[4], red2[2], gate_s[2];
     const uint32_t h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
@@ -340,7 +340,7 @@ __global__ __launch_bounds__(1024) void k_delta_step(const float* __restrict__ p
         const float rms = sqrtf((red2[0] + red2[1]) / 128.0f + 1e-6f);
         const float inv = 1.0f / rms;
         const float val = o * inv * nwt * silu(zg);
-        if (act) store_act_q8_lane(val, act, (float*)(act + xd_off), M, value_dim / 32, s, h * 128 + t);
+        if (act) store_act_q8_lane(val, act, (float*)(act + xd_off), M, value_dim / 32, s, h * 128 + t, P);
         if (yout) yout[(size_t)s * value_dim + h * 128 + t] = val;
     }
 }
@@ -362,21 +362,22 @@ extern "C" int ec_deltanet(float* state, const float* q, const float* k, const f
     return EC_OK;
 }
 
-extern "C" int ec_delta_step_out(const float* proj, uint32_t nparts, uint32_t Nin, float* conv_state,
-                                 const float* conv_w, const float* a_log, const float* dt_bias, const float* norm_w,
-                                 float* state, void* act, float* out, const int32_t* pos, uint32_t n_seq, uint32_t n_k,
-                                 uint32_t n_v, uint32_t kern, void* stream) {
+extern "C" int ec_delta_step_out_pieces(const float* proj, uint32_t nparts, uint32_t Nin, float* conv_state,
+                                        const float* conv_w, const float* a_log, const float* dt_bias,
+                                        const float* norm_w, float* state, void* act, float* out, const int32_t* pos,
+                                        uint32_t n_seq, uint32_t n_k, uint32_t n_v, uint32_t kern, uint32_t pieces,
+                                        void* stream) {
     if (n_seq == 0) return EC_OK;
     if (!proj || !conv_state || !conv_w || !a_log || !dt_bias || !norm_w || !state || (!act && !out) || !pos || n_k == 0 ||
         n_v == 0 || n_v % n_k || kern == 0 || n_seq > 16 || nparts == 0 || nparts > 8 ||
-        Nin < 2 * n_k * 128 + 2 * n_v * 128 + 2 * n_v)
+        Nin < 2 * n_k * 128 + 2 * n_v * 128 + 2 * n_v || (pieces != 1 && pieces != 2))
         return ec_set_error(EC_ERR_ARG, "ec_delta_step: bad argument");
-    const ActLayout L = act_layout(EC_Q8_0, n_seq, n_v * 128);
+    const ActLayout L = act_layout(EC_Q8_0, pieces * n_seq, n_v * 128);
     const dim3 grid(n_v, n_seq);
     const hipStream_t st = (hipStream_t)stream;
 #define EC_DSTEP(NP)                                                                                               \
     hipLaunchKernelGGL(k_delta_step<NP>, grid, dim3(1024), 0, st, proj, Nin, conv_state, conv_w, a_log, dt_bias, \
-                       norm_w, state, (uint8_t*)act, (uint32_t)L.xd_off, n_seq, pos, n_k, n_v, kern, out)
+                       norm_w, state, (uint8_t*)act, (uint32_t)L.xd_off, n_seq, pos, n_k, n_v, kern, out, pieces)
     switch (nparts) {
         case 1: EC_DSTEP(1); break;
         case 2: EC_DSTEP(2); break;
@@ -390,6 +391,14 @@ extern "C" int ec_delta_step_out(const float* proj, uint32_t nparts, uint32_t Ni
 #undef EC_DSTEP
     EC_CHECK_LAUNCH();
     return EC_OK;
+}
+
+extern "C" int ec_delta_step_out(const float* proj, uint32_t nparts, uint32_t Nin, float* conv_state,
+                                 const float* conv_w, const float* a_log, const float* dt_bias, const float* norm_w,
+                                 float* state, void* act, float* out, const int32_t* pos, uint32_t n_seq, uint32_t n_k,
+                                 uint32_t n_v, uint32_t kern, void* stream) {
+    return ec_delta_step_out_pieces(proj, nparts, Nin, conv_state, conv_w, a_log, dt_bias, norm_w, state, act, out,
+                                    pos, n_seq, n_k, n_v, kern, 1, stream);
 }
 
 extern "C" int ec_delta_step_split(const float* proj, uint32_t nparts, uint32_t Nin, float* conv_state,

@@ -94,7 +94,7 @@ __global__ __launch_bounds__(256) void k_embed_rows(const T* __restrict__ emb, c
 // K = H); thread = element, so each 32-lane half-wave quantizes one block.
 __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__ x, const float* __restrict__ w,
                                                        uint8_t* __restrict__ act, uint32_t M, uint32_t H,
-                                                       uint32_t xd_off) {
+                                                       uint32_t xd_off, uint32_t P) {
     __shared__ float sh[4];
     const uint32_t i = blockIdx.y, t = threadIdx.x, k = blockIdx.x * 256 + t;
     const float* xr = x + (size_t)i * H;
@@ -118,7 +118,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__
     ss = block_sum256(ss, sh);
     const float inv = 1.0f / sqrtf(ss / (float)H + 1e-6f);
     if (k >= Kp) return;  // whole 32-lane blocks leave together
-    store_act_q8_lane(xk * inv * wk, act, (float*)(act + xd_off), M, Kp / 32, i, k);
+    store_act_q8_lane(xk * inv * wk, act, (float*)(act + xd_off), M, Kp / 32, i, k, P);
 }
 
 // Residual add of split-K partial sums fused with RMSNorm + quantize:
@@ -131,7 +131,7 @@ template <int NP>
 __global__ __launch_bounds__(256) void k_add_rmsnorm_quant(const float* __restrict__ x, const float* __restrict__ parts,
                                                            float* __restrict__ x_out, const float* __restrict__ w,
                                                            uint8_t* __restrict__ act, uint32_t M, uint32_t H,
-                                                           uint32_t xd_off) {
+                                                           uint32_t xd_off, uint32_t P) {
     __shared__ float sh[4];
     const uint32_t i = blockIdx.y, t = threadIdx.x, k = blockIdx.x * 256 + t;
     const size_t ps = (size_t)M * H;
@@ -174,19 +174,19 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm_quant(const float* __restri
     const float inv = 1.0f / sqrtf(ss / (float)H + 1e-6f);
     if (k >= Kp) return;  // whole 32-lane blocks leave together
     if (k < H) x_out[(size_t)i * H + k] = xk;
-    store_act_q8_lane(xk * inv * wk, act, (float*)(act + xd_off), M, Kp / 32, i, k);
+    store_act_q8_lane(xk * inv * wk, act, (float*)(act + xd_off), M, Kp / 32, i, k, P);
 }
 
 // Row variant: grid (M), block Kp/4 threads (Kp <= 4096), thread = 4
 // consecutive elements (one float4 of x and of each partial); the row is read
 // once.  Eight lanes form one Q8_0 block (max over 8 lanes), each stores its
-// 4 quantized bytes as one word.
+// 4 quantized bytes (per piece) as one word.
 template <int NP>
 __global__ __launch_bounds__(1024) void k_add_rmsnorm_quant_row(const float* __restrict__ x,
                                                                const float* __restrict__ parts,
                                                                float* __restrict__ x_out, const float* __restrict__ w,
                                                                uint8_t* __restrict__ act, uint32_t M, uint32_t H,
-                                                               uint32_t xd_off) {
+                                                               uint32_t xd_off, uint32_t P) {
     __shared__ float sh[16];
     const uint32_t i = blockIdx.x, t = threadIdx.x, k = 4 * t, lane = t & 63, wv = t >> 6;
     const size_t ps = (size_t)M * H;
@@ -216,10 +216,19 @@ __global__ __launch_bounds__(1024) void k_add_rmsnorm_quant_row(const float* __r
     amax = fmaxf(amax, lane_xor<4>(amax));
     const float scale = q_scale(amax);
     const float iq = __fdiv_rn(1.0f, scale);
-    const uint32_t word = (uint32_t)(uint8_t)q_body(v0, iq) | ((uint32_t)(uint8_t)q_body(v1, iq) << 8) |
-                          ((uint32_t)(uint8_t)q_body(v2, iq) << 16) | ((uint32_t)(uint8_t)q_body(v3, iq) << 24);
+    const int8_t q0[4] = {q_body(v0, iq), q_body(v1, iq), q_body(v2, iq), q_body(v3, iq)};
+    const uint32_t word = (uint32_t)(uint8_t)q0[0] | ((uint32_t)(uint8_t)q0[1] << 8) |
+                          ((uint32_t)(uint8_t)q0[2] << 16) | ((uint32_t)(uint8_t)q0[3] << 24);
     const uint32_t sb = k / 32, e = k % 32, G = sb / 4, j = sb % 4;
-    *(uint32_t*)(act + (((size_t)G * 4 + e / 8) * M + i) * 32 + 8 * j + (e % 8)) = word;
+    uint8_t* dst = act + (((size_t)G * 4 + e / 8) * (P * M) + P * i) * 32 + 8 * j + (e % 8);
+    *(uint32_t*)dst = word;
+    if (P == 2) {
+        const uint32_t w1 = (uint32_t)(uint8_t)q_piece1(v0, q0[0], scale, iq) |
+                            ((uint32_t)(uint8_t)q_piece1(v1, q0[1], scale, iq) << 8) |
+                            ((uint32_t)(uint8_t)q_piece1(v2, q0[2], scale, iq) << 16) |
+                            ((uint32_t)(uint8_t)q_piece1(v3, q0[3], scale, iq) << 24);
+        *(uint32_t*)(dst + 32) = w1;
+    }
     if (e == 0) ((float*)(act + xd_off))[(size_t)i * nbp + sb] = scale;
 }
 
@@ -230,7 +239,7 @@ __global__ __launch_bounds__(1024) void k_add_rmsnorm_quant_row(const float* __r
 // added in part order.
 template <int NP>
 __global__ __launch_bounds__(256) void k_swiglu_quant(const float* __restrict__ gu, uint8_t* __restrict__ act,
-                                                      uint32_t M, uint32_t F, uint32_t xd_off) {
+                                                      uint32_t M, uint32_t F, uint32_t xd_off, uint32_t P) {
     const uint32_t Kp = round_up(F, 128);
     const uint32_t i = blockIdx.y, k = blockIdx.x * 256 + threadIdx.x;
     if (k >= Kp) return;  // whole 32-lane blocks leave together (Kp % 32 == 0)
@@ -246,7 +255,7 @@ __global__ __launch_bounds__(256) void k_swiglu_quant(const float* __restrict__ 
         for (int q = 1; q < NP; ++q) a += gp[q], b += up[q];
         v = silu(a) * b;
     }
-    store_act_q8_lane(v, act, (float*)(act + xd_off), M, Kp / 32, i, k);
+    store_act_q8_lane(v, act, (float*)(act + xd_off), M, Kp / 32, i, k, P);
 }
 
 // ------------------------------------------------ delta-net conv + norms + gates
@@ -615,7 +624,7 @@ __global__ __launch_bounds__(128) void k_gated_norm_quant(const float* __restric
                                                           const float* __restrict__ proj, uint32_t Nin,
                                                           uint32_t z_off, const float* __restrict__ norm_w,
                                                           uint8_t* __restrict__ act, uint32_t M, uint32_t n_v,
-                                                          uint32_t xd_off) {
+                                                          uint32_t xd_off, uint32_t P) {
     __shared__ float sh[2];
     const uint32_t h = blockIdx.x, s = blockIdx.y, i = threadIdx.x;
     const float o = core[((size_t)s * n_v + h) * 128 + i];
@@ -625,7 +634,7 @@ __global__ __launch_bounds__(128) void k_gated_norm_quant(const float* __restric
     const float rms = sqrtf((sh[0] + sh[1]) / 128.0f + 1e-6f);
     const float inv = 1.0f / rms;
     const float val = o * inv * norm_w[i] * silu(proj[(size_t)s * Nin + z_off + h * 128 + i]);
-    store_act_q8_lane(val, act, (float*)(act + xd_off), M, n_v * 4, s, h * 128 + i);
+    store_act_q8_lane(val, act, (float*)(act + xd_off), M, n_v * 4, s, h * 128 + i, P);
 }
 
 // -------------------------------------------- head norm + RoPE + KV append
@@ -797,21 +806,28 @@ extern "C" int ec_glue_embed_fmt(int fmt, const void* emb, const int32_t* tok, f
                    vocab);
 }
 
-extern "C" int ec_glue_rmsnorm_quant(const float* x, const float* w, void* act, uint32_t M, uint32_t H,
-                                     void* stream) {
-    if (!x || !w || !act || M == 0 || M > 16 || H % 32 || ((uintptr_t)x & 15))
+extern "C" int ec_glue_rmsnorm_quant_pieces(const float* x, const float* w, void* act, uint32_t M, uint32_t H,
+                                            uint32_t pieces, void* stream) {
+    if (!x || !w || !act || M == 0 || M > 16 || H % 32 || ((uintptr_t)x & 15) || (pieces != 1 && pieces != 2))
         return ec_set_error(EC_ERR_ARG, "ec_glue_rmsnorm_quant: bad argument");
-    const ActLayout L = act_layout(EC_Q8_0, M, H);
+    const ActLayout L = act_layout(EC_Q8_0, pieces * M, H);
     EC_GLUE_LAUNCH(k_rmsnorm_quant, dim3((L.Kp + 255) / 256, M), dim3(256), 0, (hipStream_t)stream, x, w,
-                   (uint8_t*)act, M, H, (uint32_t)L.xd_off);
+                   (uint8_t*)act, M, H, (uint32_t)L.xd_off, pieces);
 }
 
-extern "C" int ec_glue_add_rmsnorm_quant(const float* x, const float* parts, uint32_t nparts, float* x_out,
-                                         const float* w, void* act, uint32_t M, uint32_t H, void* stream) {
+extern "C" int ec_glue_rmsnorm_quant(const float* x, const float* w, void* act, uint32_t M, uint32_t H,
+                                     void* stream) {
+    return ec_glue_rmsnorm_quant_pieces(x, w, act, M, H, 1, stream);
+}
+
+extern "C" int ec_glue_add_rmsnorm_quant_pieces(const float* x, const float* parts, uint32_t nparts, float* x_out,
+                                                const float* w, void* act, uint32_t M, uint32_t H, uint32_t pieces,
+                                                void* stream) {
     if (!x || !parts || !x_out || !w || !act || x == x_out || M == 0 || M > 16 || H % 32 || nparts == 0 ||
-        nparts > 8 || ((uintptr_t)x & 15) || ((uintptr_t)parts & 15))
+        nparts > 8 || ((uintptr_t)x & 15) || ((uintptr_t)parts & 15) || (pieces != 1 && pieces != 2))
         return ec_set_error(EC_ERR_ARG, "ec_glue_add_rmsnorm_quant: bad argument");
-    const ActLayout L = act_layout(EC_Q8_0, M, H);
+    const uint32_t P = pieces;
+    const ActLayout L = act_layout(EC_Q8_0, P * M, H);
     const dim3 grid((L.Kp + 255) / 256, M);
     const hipStream_t st = (hipStream_t)stream;
     uint8_t* a = (uint8_t*)act;
@@ -821,43 +837,54 @@ extern "C" int ec_glue_add_rmsnorm_quant(const float* x, const float* parts, uin
     if (nparts <= 4 && L.Kp <= 4096 && H % 4 == 0 && ((uintptr_t)x_out & 15) == 0 && ((uintptr_t)w & 15) == 0) {
         const dim3 g1(M), b1(L.Kp / 4);
         switch (nparts) {
-            case 1: EC_GLUE_LAUNCH(k_add_rmsnorm_quant_row<1>, g1, b1, 0, st, x, parts, x_out, w, a, M, H, xo);
-            case 2: EC_GLUE_LAUNCH(k_add_rmsnorm_quant_row<2>, g1, b1, 0, st, x, parts, x_out, w, a, M, H, xo);
-            case 3: EC_GLUE_LAUNCH(k_add_rmsnorm_quant_row<3>, g1, b1, 0, st, x, parts, x_out, w, a, M, H, xo);
-            default: EC_GLUE_LAUNCH(k_add_rmsnorm_quant_row<4>, g1, b1, 0, st, x, parts, x_out, w, a, M, H, xo);
+            case 1: EC_GLUE_LAUNCH(k_add_rmsnorm_quant_row<1>, g1, b1, 0, st, x, parts, x_out, w, a, M, H, xo, P);
+            case 2: EC_GLUE_LAUNCH(k_add_rmsnorm_quant_row<2>, g1, b1, 0, st, x, parts, x_out, w, a, M, H, xo, P);
+            case 3: EC_GLUE_LAUNCH(k_add_rmsnorm_quant_row<3>, g1, b1, 0, st, x, parts, x_out, w, a, M, H, xo, P);
+            default: EC_GLUE_LAUNCH(k_add_rmsnorm_quant_row<4>, g1, b1, 0, st, x, parts, x_out, w, a, M, H, xo, P);
         }
     }
     switch (nparts) {
-        case 1: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<1>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo);
-        case 2: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<2>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo);
-        case 3: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<3>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo);
-        case 4: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<4>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo);
-        case 5: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<5>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo);
-        case 6: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<6>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo);
-        case 7: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<7>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo);
-        default: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<8>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo);
+        case 1: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<1>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo, P);
+        case 2: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<2>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo, P);
+        case 3: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<3>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo, P);
+        case 4: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<4>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo, P);
+        case 5: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<5>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo, P);
+        case 6: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<6>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo, P);
+        case 7: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<7>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo, P);
+        default: EC_GLUE_LAUNCH(k_add_rmsnorm_quant<8>, grid, dim3(256), 0, st, x, parts, x_out, w, a, M, H, xo, P);
     }
 }
 
-extern "C" int ec_glue_swiglu_quant_split(const float* gu, uint32_t nparts, void* act, uint32_t M, uint32_t F,
-                                          void* stream) {
-    if (!gu || !act || M == 0 || M > 16 || F % 32 || nparts == 0 || nparts > 8)
+extern "C" int ec_glue_add_rmsnorm_quant(const float* x, const float* parts, uint32_t nparts, float* x_out,
+                                         const float* w, void* act, uint32_t M, uint32_t H, void* stream) {
+    return ec_glue_add_rmsnorm_quant_pieces(x, parts, nparts, x_out, w, act, M, H, 1, stream);
+}
+
+extern "C" int ec_glue_swiglu_quant_split_pieces(const float* gu, uint32_t nparts, void* act, uint32_t M,
+                                                 uint32_t F, uint32_t pieces, void* stream) {
+    if (!gu || !act || M == 0 || M > 16 || F % 32 || nparts == 0 || nparts > 8 || (pieces != 1 && pieces != 2))
         return ec_set_error(EC_ERR_ARG, "ec_glue_swiglu_quant");
-    const ActLayout L = act_layout(EC_Q8_0, M, F);
+    const uint32_t P = pieces;
+    const ActLayout L = act_layout(EC_Q8_0, P * M, F);
     const dim3 grid((L.Kp + 255) / 256, M);
     const hipStream_t st = (hipStream_t)stream;
     uint8_t* a = (uint8_t*)act;
     const uint32_t xo = (uint32_t)L.xd_off;
     switch (nparts) {
-        case 1: EC_GLUE_LAUNCH(k_swiglu_quant<1>, grid, dim3(256), 0, st, gu, a, M, F, xo);
-        case 2: EC_GLUE_LAUNCH(k_swiglu_quant<2>, grid, dim3(256), 0, st, gu, a, M, F, xo);
-        case 3: EC_GLUE_LAUNCH(k_swiglu_quant<3>, grid, dim3(256), 0, st, gu, a, M, F, xo);
-        case 4: EC_GLUE_LAUNCH(k_swiglu_quant<4>, grid, dim3(256), 0, st, gu, a, M, F, xo);
-        case 5: EC_GLUE_LAUNCH(k_swiglu_quant<5>, grid, dim3(256), 0, st, gu, a, M, F, xo);
-        case 6: EC_GLUE_LAUNCH(k_swiglu_quant<6>, grid, dim3(256), 0, st, gu, a, M, F, xo);
-        case 7: EC_GLUE_LAUNCH(k_swiglu_quant<7>, grid, dim3(256), 0, st, gu, a, M, F, xo);
-        default: EC_GLUE_LAUNCH(k_swiglu_quant<8>, grid, dim3(256), 0, st, gu, a, M, F, xo);
+        case 1: EC_GLUE_LAUNCH(k_swiglu_quant<1>, grid, dim3(256), 0, st, gu, a, M, F, xo, P);
+        case 2: EC_GLUE_LAUNCH(k_swiglu_quant<2>, grid, dim3(256), 0, st, gu, a, M, F, xo, P);
+        case 3: EC_GLUE_LAUNCH(k_swiglu_quant<3>, grid, dim3(256), 0, st, gu, a, M, F, xo, P);
+        case 4: EC_GLUE_LAUNCH(k_swiglu_quant<4>, grid, dim3(256), 0, st, gu, a, M, F, xo, P);
+        case 5: EC_GLUE_LAUNCH(k_swiglu_quant<5>, grid, dim3(256), 0, st, gu, a, M, F, xo, P);
+        case 6: EC_GLUE_LAUNCH(k_swiglu_quant<6>, grid, dim3(256), 0, st, gu, a, M, F, xo, P);
+        case 7: EC_GLUE_LAUNCH(k_swiglu_quant<7>, grid, dim3(256), 0, st, gu, a, M, F, xo, P);
+        default: EC_GLUE_LAUNCH(k_swiglu_quant<8>, grid, dim3(256), 0, st, gu, a, M, F, xo, P);
     }
+}
+
+extern "C" int ec_glue_swiglu_quant_split(const float* gu, uint32_t nparts, void* act, uint32_t M, uint32_t F,
+                                          void* stream) {
+    return ec_glue_swiglu_quant_split_pieces(gu, nparts, act, M, F, 1, stream);
 }
 
 extern "C" int ec_glue_swiglu_quant(const float* gu, void* act, uint32_t M, uint32_t F, void* stream) {
@@ -947,12 +974,19 @@ extern "C" int ec_glue_gated_norm_rows_gemm_act(const float* core, const float* 
                    z_off, norm_w, (uint8_t*)act, M, n_v, L.nch, L.Kp / 32, L.xd_off);
 }
 
+extern "C" int ec_glue_gated_norm_quant_pieces(const float* core, const float* proj, uint32_t Nin, uint32_t z_off,
+                                               const float* norm_w, void* act, uint32_t M, uint32_t n_v,
+                                               uint32_t pieces, void* stream) {
+    if (!core || !proj || !norm_w || !act || M == 0 || M > 16 || (pieces != 1 && pieces != 2))
+        return ec_set_error(EC_ERR_ARG, "ec_glue_gated_norm");
+    const ActLayout L = act_layout(EC_Q8_0, pieces * M, n_v * 128);
+    EC_GLUE_LAUNCH(k_gated_norm_quant, dim3(n_v, M), dim3(128), 0, (hipStream_t)stream, core, proj, Nin, z_off,
+                   norm_w, (uint8_t*)act, M, n_v, (uint32_t)L.xd_off, pieces);
+}
+
 extern "C" int ec_glue_gated_norm_quant(const float* core, const float* proj, uint32_t Nin, uint32_t z_off,
                                         const float* norm_w, void* act, uint32_t M, uint32_t n_v, void* stream) {
-    if (!core || !proj || !norm_w || !act || M == 0 || M > 16) return ec_set_error(EC_ERR_ARG, "ec_glue_gated_norm");
-    const ActLayout L = act_layout(EC_Q8_0, M, n_v * 128);
-    EC_GLUE_LAUNCH(k_gated_norm_quant, dim3(n_v, M), dim3(128), 0, (hipStream_t)stream, core, proj, Nin, z_off,
-                   norm_w, (uint8_t*)act, M, n_v, (uint32_t)L.xd_off);
+    return ec_glue_gated_norm_quant_pieces(core, proj, Nin, z_off, norm_w, act, M, n_v, 1, stream);
 }
 
 extern "C" int ec_glue_qk_rope_append_split(const float* proj, uint32_t nparts, uint32_t Nin, const float* q_norm,

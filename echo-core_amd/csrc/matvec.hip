@@ -15,6 +15,11 @@
 //
 // MFMA lane layout (16x16x32 i8): A[i][k] and B[k][j] live in lane
 // (i or j) + 16*(k/8), byte k%8; D[i][j] lives in lane j + 16*(i/4), element i%4.
+//
+// Two-piece activations (P = 2): token i's pieces are A rows 2i and 2i+1
+// (rows 16a.. of MFMA group a for tokens 8a..), so D rows 2i and 2i+1 sit in
+// one lane and the epilogue combines them exactly as 256*dot0 + dot1 (|dot| <=
+// 2^19: no int32 overflow), one conversion and one FMA with d_w * d_x / 256.
 #include "common.hpp"
 #include "layout.hpp"
 
@@ -43,11 +48,18 @@ __device__ __forceinline__ v4i mfma_i8(long a, long b) {
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
 }
 
+// Output token of accumulator r of a lane in D row group g: P = 1, token
+// 4g + r (D row = token); P = 2, token 8(r/2) + 2g + r%2 (MFMA group r/2).
+template <int P>
+__device__ __forceinline__ uint32_t out_token(uint32_t g, uint32_t r) {
+    return P == 1 ? 4 * g + r : 8 * (r >> 1) + 2 * g + (r & 1);
+}
+
 // Cross-wave reduction of acc[4] and the store of y / accumulate.  Each
 // wave parks its partials in LDS; then thread s (s < 256) sums slot s over the
-// waves in wave order (deterministic) and stores it: slot s = lane*4 + r of
-// the MFMA D layout, i.e. weight row 16t + lane%16, token 4*(lane/16) + r.
-template <int R>
+// waves in wave order (deterministic) and stores it: slot s = lane*4 + r, i.e.
+// weight row 16t + lane%16, token out_token(lane/16, r).
+template <int R, int P>
 __device__ __forceinline__ void reduce_store(float (&acc)[4], float* red, float* __restrict__ y, uint32_t t,
                                              uint32_t M, uint32_t N, uint32_t ldy, int accumulate) {
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -55,7 +67,7 @@ __device__ __forceinline__ void reduce_store(float (&acc)[4], float* red, float*
         const uint32_t row = lane & 15, g = lane >> 4, n = 16 * t + row;
         if (n >= N) return;
         for (int r = 0; r < R; ++r) {
-            const uint32_t m = 4 * g + r;
+            const uint32_t m = out_token<P>(g, r);
             if (m < M) {
                 float* dst = y + (size_t)m * ldy + n;
                 *dst = accumulate ? *dst + acc[r] : acc[r];
@@ -67,7 +79,7 @@ __device__ __forceinline__ void reduce_store(float (&acc)[4], float* red, float*
     __syncthreads();
     for (uint32_t sl = threadIdx.x; sl < 256; sl += blockDim.x) {  // slot = lane' * 4 + r'
         const uint32_t ln = sl >> 2, r = sl & 3;
-        const uint32_t m = 4 * (ln >> 4) + r, n = 16 * t + (ln & 15);
+        const uint32_t m = out_token<P>(ln >> 4, r), n = 16 * t + (ln & 15);
         if ((int)r >= R || m >= M || n >= N) continue;
         float s = red[sl];
         for (uint32_t v = 1; v < nw; ++v) s += red[v * 256 + sl];
@@ -89,10 +101,19 @@ __device__ __forceinline__ void reduce_store(float (&acc)[4], float* red, float*
 // exactly and GPW*2 KB per wave stay in flight.
 template <int MT>
 constexpr int slots() { return MT == 1 ? 1 : (MT <= 4 ? 4 : (MT <= 8 ? 8 : 16)); }
+// Activation layout rows staged per token slot group: P pieces per token.
+template <int MT, int P>
+constexpr int lrows() { return P * slots<MT>(); }
+// MFMA row groups (16 layout rows each) and accumulators per lane.
+template <int MT, int P>
+constexpr int ngroups() { return (lrows<MT, P>() + 15) / 16; }
+template <int MT, int P>
+constexpr int naccs() { return P == 1 ? (MT < 4 ? MT : 4) : (MT == 1 ? 1 : 2 * ngroups<MT, P>()); }
 
 // Scales of blocks [b0, b0+NB) for token slots [0, S): LDS slice xs[NB][S],
-// source layout token-major [16][nblk].  Values for tokens >= M are zero.
-template <int NB, int S>
+// source layout token-major [16][nblk].  Values for tokens >= M are zero;
+// PRE multiplies every value by 1/256 (the two-piece epilogue's step).
+template <int NB, int S, bool PRE = false>
 struct ScaleStage {
     static constexpr int N = NB * S;
     static constexpr int PER_LANE = (N + 63) / 64;
@@ -105,7 +126,7 @@ struct ScaleStage {
             const uint32_t b = b0 + e / S, t = e % S;
             const bool ok = e < (uint32_t)N && b < nblk && t < M;
             const float x = src[(size_t)(ok ? t : 0) * nblk + (ok ? b : 0)];
-            v[i] = ok ? x : 0.0f;
+            v[i] = ok ? (PRE ? x * (1.0f / 256.0f) : x) : 0.0f;
         }
     }
     __device__ __forceinline__ void store(float* xs, uint32_t lane) const {
@@ -143,25 +164,27 @@ struct ByteStage {
 
 // --------------------------------------------------------------------- Q8_0
 // One wave's share of 16-row tile t: chunks gbeg, gbeg+1, ... (GPW per pass,
-// passes gstep apart), accumulated into acc (D layout).  xs / as: the wave's
-// LDS slice for staged scales and activation bytes.
-template <int MT, bool DOTS, int GPW>
+// passes gstep apart), accumulated into acc (one value per naccs slot).
+// xs / as: the wave's LDS slice for staged scales and activation bytes.
+// P = 2: the activation holds 2M layout rows (two pieces per token).
+template <int MT, int P, bool DOTS, int GPW>
 __device__ __forceinline__ void q8_0_wave(const uint8_t* __restrict__ wt, const uint8_t* __restrict__ act,
                                           int32_t* __restrict__ dots, uint32_t t, uint32_t M, uint32_t N, uint32_t K,
                                           uint32_t nG, uint32_t xd_off, uint32_t gbeg, uint32_t gstep, uint32_t gend,
                                           float* xs, uint8_t* as, float (&acc)[4]) {
-    constexpr int R = MT < 4 ? MT : 4;
+    constexpr int R = naccs<MT, P>();
     constexpr int S = slots<MT>();
+    constexpr int NA = ngroups<MT, P>();
     constexpr int NB = 4 * GPW;
-    constexpr int ACT_MAX = GPW * 128 * S;  // act bytes per wave pass (M <= S tokens)
+    constexpr int ACT_MAX = GPW * 128 * lrows<MT, P>();  // act bytes per wave pass
     const uint32_t lane = threadIdx.x & 63, row = lane & 15, g = lane >> 4;
-    const bool aval = row < M;
-    const size_t act_bytes = (size_t)nG * 128 * M;
+    const uint32_t VR = P * M;  // layout rows
+    const size_t act_bytes = (size_t)nG * 128 * VR;
     for (uint32_t G0 = gbeg; G0 < gend; G0 += gstep) {
-        ScaleStage<NB, S> sc;
+        ScaleStage<NB, S, P == 2> sc;
         ByteStage<ACT_MAX> ast;
         if constexpr (!DOTS) sc.load((const float*)(act + xd_off), nG * 4, 4 * G0, M, lane);
-        ast.load(act, (size_t)G0 * 128 * M, (size_t)GPW * 128 * M, act_bytes, lane);
+        ast.load(act, (size_t)G0 * 128 * VR, (size_t)GPW * 128 * VR, act_bytes, lane);
         uint4 b01[GPW], b23[GPW];
         uint2 dw[GPW];
 #pragma unroll
@@ -173,37 +196,61 @@ __device__ __forceinline__ void q8_0_wave(const uint8_t* __restrict__ wt, const 
             dw[u] = ld_stream8(ch + 2048 + row * 8);
         }
         if constexpr (!DOTS) sc.store(xs, lane);
-        ast.store(as, (size_t)GPW * 128 * M, lane);
+        ast.store(as, (size_t)GPW * 128 * VR, lane);
 #pragma unroll
         for (int u = 0; u < GPW; ++u) {
             const uint32_t G = G0 + u;
             if (G >= gend) break;
-            const uint8_t* ap = as + (((size_t)u * 4 + g) * M + (aval ? row : 0)) * 32;
-            const uint4 a01 = *(const uint4*)ap;
-            const uint4 a23 = *(const uint4*)(ap + 16);
-            const long A[4] = {aval ? pack2(a01.x, a01.y) : 0l, aval ? pack2(a01.z, a01.w) : 0l,
-                               aval ? pack2(a23.x, a23.y) : 0l, aval ? pack2(a23.z, a23.w) : 0l};
+            long A[NA][4];
+#pragma unroll
+            for (int a = 0; a < NA; ++a) {
+                const uint32_t va = 16 * a + row;
+                const bool aval = va < VR;
+                const uint8_t* ap = as + (((size_t)u * 4 + g) * VR + (aval ? va : 0)) * 32;
+                const uint4 a01 = *(const uint4*)ap;
+                const uint4 a23 = *(const uint4*)(ap + 16);
+                A[a][0] = aval ? pack2(a01.x, a01.y) : 0l;
+                A[a][1] = aval ? pack2(a01.z, a01.w) : 0l;
+                A[a][2] = aval ? pack2(a23.x, a23.y) : 0l;
+                A[a][3] = aval ? pack2(a23.z, a23.w) : 0l;
+            }
             const long B[4] = {pack2(b01[u].x, b01[u].y), pack2(b01[u].z, b01[u].w), pack2(b23[u].x, b23[u].y),
                                pack2(b23[u].z, b23[u].w)};
             const float dwf[4] = {h2f(dw[u].x & 0xFFFF), h2f(dw[u].x >> 16), h2f(dw[u].y & 0xFFFF),
                                   h2f(dw[u].y >> 16)};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const v4i cc = mfma_i8(A[j], B[j]);
+                v4i cc[NA];
+#pragma unroll
+                for (int a = 0; a < NA; ++a) cc[a] = mfma_i8(A[a][j], B[j]);
                 const uint32_t b = 4 * G + j;
                 if constexpr (DOTS) {
                     const uint32_t n = 16 * t + row, nb = K / 32;
                     if (n < N && b < nb)
-                        for (int r = 0; r < 4; ++r)
-                            if (4 * g + r < M) dots[((size_t)(4 * g + r) * N + n) * nb + b] = cc[r];
-                } else if constexpr (MT == 1) {
-                    acc[0] = fmaf((float)cc[0], dwf[j] * xs[4 * u + j], acc[0]);
-                } else {
+                        for (int a = 0; a < NA; ++a)
+                            for (int r = 0; r < 4; ++r) {
+                                const uint32_t vr = 16 * a + 4 * g + r;
+                                if (vr < VR) dots[((size_t)vr * N + n) * nb + b] = cc[a][r];
+                            }
+                } else if constexpr (MT == 1 && P == 1) {
+                    acc[0] = fmaf((float)cc[0][0], dwf[j] * xs[4 * u + j], acc[0]);
+                } else if constexpr (MT == 1) {  // P = 2: D rows 0, 1 of lanes 0-15
+                    acc[0] = fmaf((float)(cc[0][0] * 256 + cc[0][1]), dwf[j] * xs[4 * u + j], acc[0]);
+                } else if constexpr (P == 1) {
                     const float4 dx =
                         (4 * g < S) ? *(const float4*)(xs + (4 * u + j) * S + 4 * g) : make_float4(0.f, 0.f, 0.f, 0.f);
                     const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
 #pragma unroll
-                    for (int r = 0; r < R; ++r) acc[r] = fmaf((float)cc[r], dwf[j] * dxv[r], acc[r]);
+                    for (int r = 0; r < R; ++r) acc[r] = fmaf((float)cc[0][r], dwf[j] * dxv[r], acc[r]);
+                } else {
+#pragma unroll
+                    for (int a = 0; a < NA; ++a) {
+                        const uint32_t t0 = 8 * a + 2 * g;  // tokens t0, t0 + 1 (scales pre-divided by 256)
+                        const float2 dx =
+                            (t0 < (uint32_t)S) ? *(const float2*)(xs + (4 * u + j) * S + t0) : make_float2(0.f, 0.f);
+                        acc[2 * a] = fmaf((float)(cc[a][0] * 256 + cc[a][1]), dwf[j] * dx.x, acc[2 * a]);
+                        acc[2 * a + 1] = fmaf((float)(cc[a][2] * 256 + cc[a][3]), dwf[j] * dx.y, acc[2 * a + 1]);
+                    }
                 }
             }
         }
@@ -211,31 +258,31 @@ __device__ __forceinline__ void q8_0_wave(const uint8_t* __restrict__ wt, const 
 }
 
 // LDS floats of one wave's slice (scales + activation bytes).
-template <int MT, int GPW>
-constexpr uint32_t q8_wave_lds() { return 4 * GPW * slots<MT>() + GPW * 128 * slots<MT>() / 4; }
+template <int MT, int P, int GPW>
+constexpr uint32_t q8_wave_lds() { return 4 * GPW * slots<MT>() + GPW * 128 * lrows<MT, P>() / 4; }
 
 // grid = (16-row tiles, K splits): workgroup (t, sp) covers chunks
 // [sp*nG/ns, (sp+1)*nG/ns) of tile t (ns = gridDim.y), split over its nw
 // waves, and writes its sums to y + sp*split_stride (one partial result per
 // split; ns = 1: the whole K range).
-template <int MT, bool DOTS, int GPW>
+template <int MT, int P, bool DOTS, int GPW>
 __global__ __launch_bounds__(1024) void k_mv_q8_0(const uint8_t* __restrict__ W, const uint8_t* __restrict__ act,
                                                   float* __restrict__ y, int32_t* __restrict__ dots, uint32_t M,
                                                   uint32_t N, uint32_t K, uint32_t nG, uint32_t xd_off, uint32_t ldy,
                                                   int accumulate, size_t split_stride) {
     extern __shared__ float lds[];
-    constexpr int R = MT < 4 ? MT : 4;
+    constexpr int R = naccs<MT, P>();
     const uint32_t t = blockIdx.x, sp = blockIdx.y;
     const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t nw = blockDim.x >> 6;
     const uint32_t g0 = sp * nG / gridDim.y, g1 = (sp + 1) * nG / gridDim.y;
     float* red = lds;
-    float* xs = lds + nw * 256 + w * q8_wave_lds<MT, GPW>();
+    float* xs = lds + nw * 256 + w * q8_wave_lds<MT, P, GPW>();
     uint8_t* as = (uint8_t*)(xs + 4 * GPW * slots<MT>());
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    q8_0_wave<MT, DOTS, GPW>(W + (size_t)t * nG * kQ8TChunk, act, dots, t, M, N, K, nG, xd_off, g0 + w * GPW, nw * GPW,
-                             g1, xs, as, acc);
-    if constexpr (!DOTS) reduce_store<R>(acc, red, y + sp * split_stride, t, M, N, ldy, accumulate);
+    q8_0_wave<MT, P, DOTS, GPW>(W + (size_t)t * nG * kQ8TChunk, act, dots, t, M, N, K, nG, xd_off, g0 + w * GPW,
+                                nw * GPW, g1, xs, as, acc);
+    if constexpr (!DOTS) reduce_store<R, P>(acc, red, y + sp * split_stride, t, M, N, ldy, accumulate);
 }
 
 // --------------------------------------------------------------------- Q4_K
@@ -262,36 +309,38 @@ __device__ __forceinline__ void q4k_scale_min(const uint32_t (&q)[3], int s, uin
     }
 }
 
-template <int MT, bool DOTS, int GPW>
+template <int MT, int P, bool DOTS, int GPW>
 __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W, const uint8_t* __restrict__ act,
                                                   float* __restrict__ y, int32_t* __restrict__ dots, uint32_t M,
                                                   uint32_t N, uint32_t K, uint32_t nB, uint32_t xd_off,
                                                   uint32_t dxs_off, uint32_t ldy, int accumulate) {
     extern __shared__ float lds[];
-    constexpr int R = MT < 4 ? MT : 4;
+    constexpr int R = naccs<MT, P>();
     constexpr int S = slots<MT>();
+    constexpr int NA = ngroups<MT, P>();
     constexpr int NB = 8 * GPW;
     const uint32_t t = blockIdx.x, lane = threadIdx.x & 63, row = lane & 15, g = lane >> 4;
     const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t nw = blockDim.x >> 6;
-    constexpr int ACT_MAX = GPW * 256 * S;
+    constexpr int ACT_MAX = GPW * 256 * lrows<MT, P>();
     float* red = lds;
     float* xs = lds + nw * 256 + w * (2 * NB * S + ACT_MAX / 4);
     float* xms = xs + NB * S;
     uint8_t* as = (uint8_t*)(xms + NB * S);
     const uint8_t* wt = W + (size_t)t * nB * kQ4TChunk;
-    const bool aval = row < M;
-    const size_t act_bytes = (size_t)nB * 256 * M;
+    const uint32_t VR = P * M;  // layout rows
+    const size_t act_bytes = (size_t)nB * 256 * VR;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
 
     for (uint32_t B0 = w * GPW; B0 < nB; B0 += nw * GPW) {
-        ScaleStage<NB, S> sd, sm;
+        ScaleStage<NB, S, P == 2> sd;
+        ScaleStage<NB, S> sm;
         ByteStage<ACT_MAX> ast;
         if constexpr (!DOTS) {
             sd.load((const float*)(act + xd_off), nB * 8, 8 * B0, M, lane);
             sm.load((const float*)(act + dxs_off), nB * 8, 8 * B0, M, lane);
         }
-        ast.load(act, (size_t)B0 * 256 * M, (size_t)GPW * 256 * M, act_bytes, lane);
+        ast.load(act, (size_t)B0 * 256 * VR, (size_t)GPW * 256 * VR, act_bytes, lane);
         uint4 q0[GPW], q1[GPW], hdr[GPW];
 #pragma unroll
         for (int u = 0; u < GPW; ++u) {
@@ -305,18 +354,25 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
             sd.store(xs, lane);
             sm.store(xms, lane);
         }
-        ast.store(as, (size_t)GPW * 256 * M, lane);
+        ast.store(as, (size_t)GPW * 256 * VR, lane);
 #pragma unroll
         for (int u = 0; u < GPW; ++u) {
             const uint32_t b = B0 + u;
             if (b >= nB) break;
-            uint4 a[4];
-            const uint8_t* ap = as + (((size_t)u * 4 + g) * M + (aval ? row : 0)) * 64;
+            uint32_t aw[NA][16];
+            bool aval[NA];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = *(const uint4*)(ap + 16 * i);
+            for (int ga = 0; ga < NA; ++ga) {
+                const uint32_t va = 16 * ga + row;
+                aval[ga] = va < VR;
+                const uint8_t* ap = as + (((size_t)u * 4 + g) * VR + (aval[ga] ? va : 0)) * 64;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint4 a4 = *(const uint4*)(ap + 16 * i);
+                    aw[ga][4 * i] = a4.x, aw[ga][4 * i + 1] = a4.y, aw[ga][4 * i + 2] = a4.z, aw[ga][4 * i + 3] = a4.w;
+                }
+            }
             const uint32_t qw[8] = {q0[u].x, q0[u].y, q0[u].z, q0[u].w, q1[u].x, q1[u].y, q1[u].z, q1[u].w};
-            const uint32_t aw[16] = {a[0].x, a[0].y, a[0].z, a[0].w, a[1].x, a[1].y, a[1].z, a[1].w,
-                                     a[2].x, a[2].y, a[2].z, a[2].w, a[3].x, a[3].y, a[3].z, a[3].w};
             const float d = h2f(hdr[u].x & 0xFFFF), dmin = h2f(hdr[u].x >> 16);
             const uint32_t scb[3] = {hdr[u].y, hdr[u].z, hdr[u].w};
             uint32_t sc4[2], mn4[2];
@@ -325,20 +381,40 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
                 const uint32_t lo = qw[s] & 0x0F0F0F0Fu, hi = (qw[s] >> 4) & 0x0F0F0F0Fu;
-                const v4i cc = mfma_i8(aval ? pack2(aw[2 * s], aw[2 * s + 1]) : 0l, pack2(lo, hi));
+                v4i cc[NA];
+#pragma unroll
+                for (int ga = 0; ga < NA; ++ga)
+                    cc[ga] = mfma_i8(aval[ga] ? pack2(aw[ga][2 * s], aw[ga][2 * s + 1]) : 0l, pack2(lo, hi));
                 const uint32_t sbi = 8 * b + s;
                 if constexpr (DOTS) {
                     const uint32_t n = 16 * t + row, nsb = K / 32;
                     if (n < N && sbi < nsb)
-                        for (int r = 0; r < 4; ++r)
-                            if (4 * g + r < M) dots[((size_t)(4 * g + r) * N + n) * nsb + sbi] = cc[r];
+                        for (int ga = 0; ga < NA; ++ga)
+                            for (int r = 0; r < 4; ++r) {
+                                const uint32_t vr = 16 * ga + 4 * g + r;
+                                if (vr < VR) dots[((size_t)vr * N + n) * nsb + sbi] = cc[ga][r];
+                            }
                 } else {
                     const uint32_t scv = (sc4[s >> 2] >> (8 * (s & 3))) & 0xFFu;
                     const uint32_t mnv = (mn4[s >> 2] >> (8 * (s & 3))) & 0xFFu;
                     const int e = 8 * u + s;
                     if constexpr (MT == 1) {
-                        a_sc = fmaf((float)cc[0], (float)scv * xs[e], a_sc);
+                        const int32_t dot = P == 2 ? cc[0][0] * 256 + cc[0][1] : cc[0][0];
+                        a_sc = fmaf((float)dot, (float)scv * xs[e], a_sc);
                         a_mn = fmaf((float)mnv, xms[e], a_mn);
+                    } else if constexpr (P == 2) {
+                        const float dsc = d * (float)scv, dmn = dmin * (float)mnv;
+#pragma unroll
+                        for (int ga = 0; ga < NA; ++ga) {
+                            const uint32_t t0 = 8 * ga + 2 * g;  // tokens t0, t0 + 1
+                            const bool ok = t0 < (uint32_t)S;
+                            const float2 dx = ok ? *(const float2*)(xs + e * S + t0) : make_float2(0.f, 0.f);
+                            const float2 dm = ok ? *(const float2*)(xms + e * S + t0) : make_float2(0.f, 0.f);
+                            acc[2 * ga] = fmaf((float)(cc[ga][0] * 256 + cc[ga][1]), dsc * dx.x, acc[2 * ga]);
+                            acc[2 * ga] = fmaf(-dmn, dm.x, acc[2 * ga]);
+                            acc[2 * ga + 1] = fmaf((float)(cc[ga][2] * 256 + cc[ga][3]), dsc * dx.y, acc[2 * ga + 1]);
+                            acc[2 * ga + 1] = fmaf(-dmn, dm.y, acc[2 * ga + 1]);
+                        }
                     } else {
                         const float dsc = d * (float)scv, dmn = dmin * (float)mnv;
                         const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -348,7 +424,7 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
                         const float dmv[4] = {dm.x, dm.y, dm.z, dm.w};
 #pragma unroll
                         for (int r = 0; r < R; ++r) {
-                            acc[r] = fmaf((float)cc[r], dsc * dxv[r], acc[r]);
+                            acc[r] = fmaf((float)cc[0][r], dsc * dxv[r], acc[r]);
                             acc[r] = fmaf(-dmn, dmv[r], acc[r]);
                         }
                     }
@@ -360,7 +436,7 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
             }
         }
     }
-    if constexpr (!DOTS) reduce_store<R>(acc, red, y, t, M, N, ldy, accumulate);
+    if constexpr (!DOTS) reduce_store<R, P>(acc, red, y, t, M, N, ldy, accumulate);
 }
 
 // ------------------------------------------------ reference-semantics fp32 path
@@ -532,14 +608,14 @@ static void plan(uint32_t n_tiles, uint32_t n_chunks, int max_gpw, int& gpw, uin
 constexpr size_t kLdsBytes = 160 * 1024;
 static uint32_t lds_cap_waves(uint32_t wave_floats) { return (uint32_t)(kLdsBytes / ((256 + wave_floats) * 4)); }
 
-template <int MT, bool DOTS, int GPW>
+template <int MT, int P, bool DOTS, int GPW>
 static void launch_q8_g(const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N, uint32_t K,
                         uint32_t ldy, int accumulate, uint32_t nw, uint32_t nsplit, hipStream_t st) {
-    const ActLayout L = act_layout(EC_Q8_0, M, K);
+    const ActLayout L = act_layout(EC_Q8_0, P * M, K);
     const uint32_t nT = round_up(N, 16) / 16, nG = L.Kp / 128;
-    nw = min(nw, lds_cap_waves(q8_wave_lds<MT, GPW>()));
-    const size_t lds = ((size_t)nw * 256 + (size_t)nw * q8_wave_lds<MT, GPW>()) * sizeof(float);
-    hipLaunchKernelGGL((k_mv_q8_0<MT, DOTS, GPW>), dim3(nT, nsplit), dim3(64 * nw), lds, st, (const uint8_t*)W,
+    nw = min(nw, lds_cap_waves(q8_wave_lds<MT, P, GPW>()));
+    const size_t lds = ((size_t)nw * 256 + (size_t)nw * q8_wave_lds<MT, P, GPW>()) * sizeof(float);
+    hipLaunchKernelGGL((k_mv_q8_0<MT, P, DOTS, GPW>), dim3(nT, nsplit), dim3(64 * nw), lds, st, (const uint8_t*)W,
                        (const uint8_t*)act, y, dots, M, N, K, nG, (uint32_t)L.xd_off, ldy, accumulate,
                        (size_t)M * ldy);
 }
@@ -547,37 +623,38 @@ static void launch_q8_g(const void* W, const void* act, float* y, int32_t* dots,
 // nsplit > 1 (<= the 128-element chunks of K): the K range is cut into
 // nsplit balanced chunk ranges, one workgroup per (tile, range), partial sums
 // to y + sp*M*ldy.
-template <int MT, bool DOTS>
+template <int MT, int P, bool DOTS>
 static void launch_q8(const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N, uint32_t K,
                       uint32_t ldy, int accumulate, hipStream_t st, uint32_t nsplit = 1) {
     const uint32_t nT = round_up(N, 16) / 16, nG = round_up(K, 128) / 128;
     const uint32_t cps = (nG + nsplit - 1) / nsplit;  // longest range
     int gpw;
     uint32_t nw;
-    plan(nT * nsplit, cps, 5, gpw, nw, target_waves_q8());  // GPW <= 5: every variant under 128 VGPRs
+    // GPW <= 5 (3 for 32 layout rows: 16 tokens in two pieces): every variant under 128 VGPRs, no spills
+    plan(nT * nsplit, cps, (MT == 16 && P == 2) ? 3 : 5, gpw, nw, target_waves_q8());
     switch (gpw) {
-        case 1: launch_q8_g<MT, DOTS, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
-        case 2: launch_q8_g<MT, DOTS, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
-        case 3: launch_q8_g<MT, DOTS, 3>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
-        case 4: launch_q8_g<MT, DOTS, 4>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
-        default: launch_q8_g<MT, DOTS, 5>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
+        case 1: launch_q8_g<MT, P, DOTS, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
+        case 2: launch_q8_g<MT, P, DOTS, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
+        case 3: launch_q8_g<MT, P, DOTS, 3>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
+        case 4: launch_q8_g<MT, P, DOTS, 4>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
+        default: launch_q8_g<MT, P, DOTS, 5>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
     }
 }
 
-template <int MT, bool DOTS, int GPW>
+template <int MT, int P, bool DOTS, int GPW>
 static void launch_q4_g(const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N, uint32_t K,
                         uint32_t ldy, int accumulate, uint32_t nw, hipStream_t st) {
-    const ActLayout L = act_layout(EC_Q4_K, M, K);
+    const ActLayout L = act_layout(EC_Q4_K, P * M, K);
     const uint32_t nT = round_up(N, 16) / 16, nB = L.Kp / 256;
-    const uint32_t wave_floats = 2 * 8 * GPW * slots<MT>() + GPW * 256 * slots<MT>() / 4;
+    const uint32_t wave_floats = 2 * 8 * GPW * slots<MT>() + GPW * 256 * lrows<MT, P>() / 4;
     nw = min(nw, lds_cap_waves(wave_floats));
     const size_t lds = ((size_t)nw * 256 + (size_t)nw * wave_floats) * sizeof(float);
-    hipLaunchKernelGGL((k_mv_q4_K<MT, DOTS, GPW>), dim3(nT), dim3(64 * nw), lds, st, (const uint8_t*)W,
+    hipLaunchKernelGGL((k_mv_q4_K<MT, P, DOTS, GPW>), dim3(nT), dim3(64 * nw), lds, st, (const uint8_t*)W,
                        (const uint8_t*)act, y, dots, M, N, K, nB, (uint32_t)L.xd_off, (uint32_t)L.dxs_off, ldy,
                        accumulate);
 }
 
-template <int MT, bool DOTS>
+template <int MT, int P, bool DOTS>
 static void launch_q4(const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N, uint32_t K,
                       uint32_t ldy, int accumulate, hipStream_t st) {
     const uint32_t nT = round_up(N, 16) / 16, nB = round_up(K, 256) / 256;
@@ -585,26 +662,33 @@ static void launch_q4(const void* W, const void* act, float* y, int32_t* dots, u
     uint32_t nw;
     plan(nT, nB, MT == 1 ? 3 : 1, gpw, nw, target_waves_q4());
     switch (gpw) {
-        case 1: launch_q4_g<MT, DOTS, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
-        case 2: launch_q4_g<MT, DOTS, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
-        default: launch_q4_g<MT, DOTS, 3>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
+        case 1: launch_q4_g<MT, P, DOTS, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
+        case 2: launch_q4_g<MT, P, DOTS, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
+        default: launch_q4_g<MT, P, DOTS, 3>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
+    }
+}
+
+template <int P, bool DOTS>
+static void dispatch_p(int fmt, const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N,
+                       uint32_t K, uint32_t ldy, int accumulate, hipStream_t st, uint32_t nsplit) {
+    if (fmt == EC_Q8_0) {
+        if (M == 1) launch_q8<1, P, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st, nsplit);
+        else if (M <= 4) launch_q8<4, P, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st, nsplit);
+        else if (M <= 8) launch_q8<8, P, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st, nsplit);
+        else launch_q8<16, P, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st, nsplit);
+    } else {
+        if (M == 1) launch_q4<1, P, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
+        else if (M <= 4) launch_q4<4, P, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
+        else if (M <= 8) launch_q4<8, P, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
+        else launch_q4<16, P, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
     }
 }
 
 template <bool DOTS>
-static int dispatch(int fmt, const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N,
-                    uint32_t K, uint32_t ldy, int accumulate, hipStream_t st) {
-    if (fmt == EC_Q8_0) {
-        if (M == 1) launch_q8<1, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
-        else if (M <= 4) launch_q8<4, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
-        else if (M <= 8) launch_q8<8, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
-        else launch_q8<16, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
-    } else {
-        if (M == 1) launch_q4<1, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
-        else if (M <= 4) launch_q4<4, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
-        else if (M <= 8) launch_q4<8, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
-        else launch_q4<16, DOTS>(W, act, y, dots, M, N, K, ldy, accumulate, st);
-    }
+static int dispatch(int fmt, uint32_t pieces, const void* W, const void* act, float* y, int32_t* dots, uint32_t M,
+                    uint32_t N, uint32_t K, uint32_t ldy, int accumulate, hipStream_t st, uint32_t nsplit = 1) {
+    if (pieces == 2) dispatch_p<2, DOTS>(fmt, W, act, y, dots, M, N, K, ldy, accumulate, st, nsplit);
+    else dispatch_p<1, DOTS>(fmt, W, act, y, dots, M, N, K, ldy, accumulate, st, nsplit);
     return EC_OK;
 }
 
@@ -667,51 +751,63 @@ extern "C" int ec_stream_read_shape(const void* src, size_t bytes, uint32_t* out
     return EC_OK;
 }
 
-static int check_mv(int fmt, const void* W, const void* act, const void* out, uint32_t M, uint32_t N, uint32_t K,
-                    const char* who) {
+static int check_mv(int fmt, uint32_t pieces, const void* W, const void* act, const void* out, uint32_t M,
+                    uint32_t N, uint32_t K, const char* who) {
     if (fmt != EC_Q8_0 && fmt != EC_Q4_K) return ec_set_error(EC_ERR_UNSUPPORTED, "matvec: format must be Q8_0 or Q4_K");
-    if (!W || !act || !out || M == 0 || M > 16 || N == 0 || K == 0 || K % (fmt == EC_Q8_0 ? 32u : 256u)) {
-        char buf[160];
-        snprintf(buf, sizeof buf, "%s: bad arguments (M=%u N=%u K=%u; need 1<=M<=16, K%%%u==0)", who, M, N, K,
-                 fmt == EC_Q8_0 ? 32u : 256u);
+    if (!W || !act || !out || M == 0 || M > 16 || N == 0 || K == 0 || K % (fmt == EC_Q8_0 ? 32u : 256u) ||
+        (pieces != 1 && pieces != 2)) {
+        char buf[192];
+        snprintf(buf, sizeof buf, "%s: bad arguments (M=%u N=%u K=%u pieces=%u; need 1<=M<=16, K%%%u==0, 1 or 2 pieces)",
+                 who, M, N, K, pieces, fmt == EC_Q8_0 ? 32u : 256u);
         return ec_set_error(EC_ERR_ARG, buf);
     }
     return EC_OK;
 }
 
-extern "C" int ec_matvec(int fmt, const void* tiled, const void* act, float* y, uint32_t M, uint32_t N, uint32_t K,
-                         uint32_t ldy, int accumulate, void* stream) {
-    int rc = check_mv(fmt, tiled, act, y, M, N, K, "ec_matvec");
+extern "C" int ec_matvec_pieces(int fmt, uint32_t pieces, const void* tiled, const void* act, float* y, uint32_t M,
+                                uint32_t N, uint32_t K, uint32_t ldy, int accumulate, void* stream) {
+    int rc = check_mv(fmt, pieces, tiled, act, y, M, N, K, "ec_matvec");
     if (rc) return rc;
     if (ldy < N) return ec_set_error(EC_ERR_ARG, "ec_matvec: ldy < N");
-    dispatch<false>(fmt, tiled, act, y, nullptr, M, N, K, ldy, accumulate, (hipStream_t)stream);
+    dispatch<false>(fmt, pieces, tiled, act, y, nullptr, M, N, K, ldy, accumulate, (hipStream_t)stream);
+    EC_CHECK_LAUNCH();
+    return EC_OK;
+}
+
+extern "C" int ec_matvec(int fmt, const void* tiled, const void* act, float* y, uint32_t M, uint32_t N, uint32_t K,
+                         uint32_t ldy, int accumulate, void* stream) {
+    return ec_matvec_pieces(fmt, 1, tiled, act, y, M, N, K, ldy, accumulate, stream);
+}
+
+extern "C" int ec_matvec_split_pieces(int fmt, uint32_t pieces, const void* tiled, const void* act, float* parts,
+                                      uint32_t M, uint32_t N, uint32_t K, uint32_t nsplit, void* stream) {
+    int rc = check_mv(fmt, pieces, tiled, act, parts, M, N, K, "ec_matvec_split");
+    if (rc) return rc;
+    if (fmt != EC_Q8_0) return ec_set_error(EC_ERR_UNSUPPORTED, "ec_matvec_split: Q8_0 weights only");
+    if (nsplit == 0 || nsplit > round_up(K, 128) / 128)
+        return ec_set_error(EC_ERR_ARG, "ec_matvec_split: nsplit must be in [1, ceil(K/128)]");
+    dispatch<false>(fmt, pieces, tiled, act, parts, nullptr, M, N, K, N, 0, (hipStream_t)stream, nsplit);
     EC_CHECK_LAUNCH();
     return EC_OK;
 }
 
 extern "C" int ec_matvec_split(int fmt, const void* tiled, const void* act, float* parts, uint32_t M, uint32_t N,
                                uint32_t K, uint32_t nsplit, void* stream) {
-    int rc = check_mv(fmt, tiled, act, parts, M, N, K, "ec_matvec_split");
+    return ec_matvec_split_pieces(fmt, 1, tiled, act, parts, M, N, K, nsplit, stream);
+}
+
+extern "C" int ec_block_dots_pieces(int fmt, uint32_t pieces, const void* tiled, const void* act, int32_t* out,
+                                    uint32_t M, uint32_t N, uint32_t K, void* stream) {
+    int rc = check_mv(fmt, pieces, tiled, act, out, M, N, K, "ec_block_dots");
     if (rc) return rc;
-    if (fmt != EC_Q8_0) return ec_set_error(EC_ERR_UNSUPPORTED, "ec_matvec_split: Q8_0 weights only");
-    if (nsplit == 0 || nsplit > round_up(K, 128) / 128)
-        return ec_set_error(EC_ERR_ARG, "ec_matvec_split: nsplit must be in [1, ceil(K/128)]");
-    const hipStream_t st = (hipStream_t)stream;
-    if (M == 1) launch_q8<1, false>(tiled, act, parts, nullptr, M, N, K, N, 0, st, nsplit);
-    else if (M <= 4) launch_q8<4, false>(tiled, act, parts, nullptr, M, N, K, N, 0, st, nsplit);
-    else if (M <= 8) launch_q8<8, false>(tiled, act, parts, nullptr, M, N, K, N, 0, st, nsplit);
-    else launch_q8<16, false>(tiled, act, parts, nullptr, M, N, K, N, 0, st, nsplit);
+    dispatch<true>(fmt, pieces, tiled, act, nullptr, out, M, N, K, N, 0, (hipStream_t)stream);
     EC_CHECK_LAUNCH();
     return EC_OK;
 }
 
 extern "C" int ec_block_dots(int fmt, const void* tiled, const void* act, int32_t* out, uint32_t M, uint32_t N,
                              uint32_t K, void* stream) {
-    int rc = check_mv(fmt, tiled, act, out, M, N, K, "ec_block_dots");
-    if (rc) return rc;
-    dispatch<true>(fmt, tiled, act, nullptr, out, M, N, K, N, 0, (hipStream_t)stream);
-    EC_CHECK_LAUNCH();
-    return EC_OK;
+    return ec_block_dots_pieces(fmt, 1, tiled, act, out, M, N, K, stream);
 }
 
 extern "C" int ec_matvec_gguf_f32(int fmt, const void* gguf, const float* x, float* y, uint32_t M, uint32_t K,

@@ -27,6 +27,9 @@
 //        Q4_K: [nB][4][M][64 B]: s=0..7 x (xsub[4g..+4], xsub[16+4g..+4])
 //   xd   fp32 [16][Kp/32]   scale of each 32-block per token slot (0 for padding)
 //   dxs  fp32 [16][Kp/32]   Q4_K only: xd * sum(block int8), the min term
+// Two-piece activations (P = 2) store M tokens as 2M rows of xq, token i's
+// piece p (q_piece1 for p = 1, scale xd/256) in row 2i + p, with xd and dxs
+// per token as above (dxs = xd * (sum q0 + sum q1 / 256)).
 #include "common.hpp"
 #include "layout.hpp"
 
@@ -128,7 +131,7 @@ __global__ void k_unpack_q4_K(const uint8_t* __restrict__ src, uint8_t* __restri
 // ------------------------------------------------------- activation packing
 // One thread per (token slot i < 16, 32-block).  Slots >= M only zero scales.
 __global__ void k_quantize_act_q8_0(const float* __restrict__ x, uint8_t* __restrict__ act, uint32_t M, uint32_t K,
-                                    uint32_t Kp, size_t xd_off) {
+                                    uint32_t Kp, size_t xd_off, uint32_t P) {
     uint32_t nbp = Kp / 32;
     uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= 16 * nbp) return;
@@ -151,14 +154,17 @@ __global__ void k_quantize_act_q8_0(const float* __restrict__ x, uint8_t* __rest
     for (int e = 0; e < 32; ++e) qv[e] = real ? q_body(v[e], inv) : 0;
     uint32_t G = sb / 4, j = sb % 4;
     for (int g = 0; g < 4; ++g) {
-        uint8_t* p = act + (((size_t)G * 4 + g) * M + i) * 32 + 8 * j;
+        uint8_t* p = act + (((size_t)G * 4 + g) * (P * M) + P * i) * 32 + 8 * j;
         for (int e = 0; e < 8; ++e) p[e] = (uint8_t)qv[8 * g + e];
+        if (P == 2)
+            for (int e = 0; e < 8; ++e)
+                p[32 + e] = real ? (uint8_t)q_piece1(v[8 * g + e], qv[8 * g + e], scale, inv) : (uint8_t)0;
     }
     xd[(size_t)i * nbp + sb] = scale;
 }
 
 __global__ void k_quantize_act_q4_K(const float* __restrict__ x, uint8_t* __restrict__ act, uint32_t M, uint32_t K,
-                                    uint32_t Kp, size_t xd_off, size_t dxs_off) {
+                                    uint32_t Kp, size_t xd_off, size_t dxs_off, uint32_t P) {
     uint32_t nsb = Kp / 32;
     uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= 16 * nsb) return;
@@ -182,29 +188,43 @@ __global__ void k_quantize_act_q4_K(const float* __restrict__ x, uint8_t* __rest
     for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(v[e]));
     float scale = real ? q_scale(amax) : 0.0f;
     float inv = real ? __fdiv_rn(1.0f, scale) : 0.0f;
-    int8_t qv[32];
-    int sum = 0;
+    int8_t qv[32], qv1[32];
+    int sum = 0, sum1 = 0;
     for (int e = 0; e < 32; ++e) {
         qv[e] = real ? q_body(v[e], inv) : 0;
+        qv1[e] = (real && P == 2) ? q_piece1(v[e], qv[e], scale, inv) : 0;
         sum += qv[e];
+        sum1 += qv1[e];
     }
     for (int g = 0; g < 4; ++g) {
-        uint8_t* dp = act + (((size_t)b * 4 + g) * M + i) * 64 + 8 * s;
+        uint8_t* dp = act + (((size_t)b * 4 + g) * (P * M) + P * i) * 64 + 8 * s;
         for (int e = 0; e < 4; ++e) {
             dp[e] = (uint8_t)qv[4 * g + e];
             dp[4 + e] = (uint8_t)qv[16 + 4 * g + e];
         }
+        if (P == 2)
+            for (int e = 0; e < 4; ++e) {
+                dp[64 + e] = (uint8_t)qv1[4 * g + e];
+                dp[64 + 4 + e] = (uint8_t)qv1[16 + 4 * g + e];
+            }
     }
     xd[(size_t)i * nsb + sbi] = scale;
-    dxs[(size_t)i * nsb + sbi] = __fmul_rn(scale, (float)sum);
+    // the min term's activation sum: scale * sum(q0), or with two pieces
+    // (scale/256) * (256 sum(q0) + sum(q1)), the integer sum exact
+    dxs[(size_t)i * nsb + sbi] =
+        P == 2 ? __fmul_rn(scale * (1.0f / 256.0f), (float)(256 * sum + sum1)) : __fmul_rn(scale, (float)sum);
 }
 
+// One thread per (layout row i < R = P*M, block); row i's bytes to xq[i], and
+// for piece-0 rows the token's scale to xdo[i / P].
 __global__ void k_act_unpack(int fmt, const uint8_t* __restrict__ act, int8_t* __restrict__ xq,
-                             float* __restrict__ xdo, uint32_t M, uint32_t K, uint32_t Kp, size_t xd_off) {
+                             float* __restrict__ xdo, uint32_t R, uint32_t K, uint32_t Kp, size_t xd_off,
+                             uint32_t P) {
     uint32_t nb = K / 32;
     uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= M * nb) return;
+    if (idx >= R * nb) return;
     uint32_t i = idx / nb, sb = idx % nb;
+    const uint32_t M = R;  // layout rows
     const float* xd = (const float*)(act + xd_off);
     int8_t* out = xq + (size_t)i * K + 32 * sb;
     if (fmt == EC_Q8_0) {
@@ -219,7 +239,7 @@ __global__ void k_act_unpack(int fmt, const uint8_t* __restrict__ act, int8_t* _
                 out[16 + 4 * g + e] = (int8_t)act[(((size_t)b * 4 + g) * M + i) * 64 + 8 * s + 4 + e];
             }
     }
-    xdo[(size_t)i * nb + sb] = xd[(size_t)i * (Kp / 32) + sb];
+    if (i % P == 0) xdo[(size_t)(i / P) * nb + sb] = xd[(size_t)(i / P) * (Kp / 32) + sb];
 }
 
 // ------------------------------------------------------------------ random
@@ -362,18 +382,24 @@ extern "C" size_t ec_act_bytes(int fmt, uint32_t M, uint32_t K) {
     return act_layout(fmt, M, K).total;
 }
 
-extern "C" int ec_quantize_act(int fmt, const float* x, void* act, uint32_t M, uint32_t K, void* stream) {
-    if (!x || !act || M == 0 || M > 16 || K == 0 || K % 32)
-        return ec_set_error(EC_ERR_ARG, "ec_quantize_act: need 1 <= M <= 16, K % 32 == 0");
-    ActLayout L = act_layout(fmt, M, K);
+extern "C" size_t ec_act_bytes_pieces(int fmt, uint32_t M, uint32_t K, uint32_t pieces) {
+    if ((fmt != EC_Q8_0 && fmt != EC_Q4_K) || (pieces != 1 && pieces != 2)) return 0;
+    return act_layout(fmt, pieces * M, K).total;
+}
+
+extern "C" int ec_quantize_act_pieces(int fmt, const float* x, void* act, uint32_t M, uint32_t K, uint32_t pieces,
+                                      void* stream) {
+    if (!x || !act || M == 0 || M > 16 || K == 0 || K % 32 || (pieces != 1 && pieces != 2))
+        return ec_set_error(EC_ERR_ARG, "ec_quantize_act: need 1 <= M <= 16, K % 32 == 0, 1 or 2 pieces");
+    ActLayout L = act_layout(fmt, pieces * M, K);
     uint32_t n = 16 * (L.Kp / 32);
     if (fmt == EC_Q8_0) {
         hipLaunchKernelGGL(k_quantize_act_q8_0, dim3((n + 127) / 128), dim3(128), 0, (hipStream_t)stream, x,
-                           (uint8_t*)act, M, K, L.Kp, L.xd_off);
+                           (uint8_t*)act, M, K, L.Kp, L.xd_off, pieces);
     } else if (fmt == EC_Q4_K) {
         if (K % 256) return ec_set_error(EC_ERR_ARG, "ec_quantize_act: Q4_K needs K % 256 == 0");
         hipLaunchKernelGGL(k_quantize_act_q4_K, dim3((n + 127) / 128), dim3(128), 0, (hipStream_t)stream, x,
-                           (uint8_t*)act, M, K, L.Kp, L.xd_off, L.dxs_off);
+                           (uint8_t*)act, M, K, L.Kp, L.xd_off, L.dxs_off, pieces);
     } else {
         return ec_set_error(EC_ERR_UNSUPPORTED, "ec_quantize_act: format must be Q8_0 or Q4_K");
     }
@@ -381,15 +407,25 @@ extern "C" int ec_quantize_act(int fmt, const float* x, void* act, uint32_t M, u
     return EC_OK;
 }
 
-extern "C" int ec_act_unpack(int fmt, const void* act, int8_t* xq, float* xd, uint32_t M, uint32_t K, void* stream) {
-    if (!act || !xq || !xd || M == 0 || M > 16 || K % 32 || (fmt != EC_Q8_0 && fmt != EC_Q4_K))
+extern "C" int ec_quantize_act(int fmt, const float* x, void* act, uint32_t M, uint32_t K, void* stream) {
+    return ec_quantize_act_pieces(fmt, x, act, M, K, 1, stream);
+}
+
+extern "C" int ec_act_unpack_pieces(int fmt, uint32_t pieces, const void* act, int8_t* xq, float* xd, uint32_t M,
+                                    uint32_t K, void* stream) {
+    if (!act || !xq || !xd || M == 0 || M > 16 || K % 32 || (fmt != EC_Q8_0 && fmt != EC_Q4_K) ||
+        (pieces != 1 && pieces != 2))
         return ec_set_error(EC_ERR_ARG, "ec_act_unpack: bad argument");
-    ActLayout L = act_layout(fmt, M, K);
-    uint32_t n = M * (K / 32);
+    ActLayout L = act_layout(fmt, pieces * M, K);
+    uint32_t n = pieces * M * (K / 32);
     hipLaunchKernelGGL(k_act_unpack, dim3((n + 127) / 128), dim3(128), 0, (hipStream_t)stream, fmt,
-                       (const uint8_t*)act, xq, xd, M, K, L.Kp, L.xd_off);
+                       (const uint8_t*)act, xq, xd, pieces * M, K, L.Kp, L.xd_off, pieces);
     EC_CHECK_LAUNCH();
     return EC_OK;
+}
+
+extern "C" int ec_act_unpack(int fmt, const void* act, int8_t* xq, float* xd, uint32_t M, uint32_t K, void* stream) {
+    return ec_act_unpack_pieces(fmt, 1, act, xq, xd, M, K, stream);
 }
 
 extern "C" int ec_fill_random(int kind, void* dst, uint64_t n, uint64_t seed, float scale, uint32_t K,

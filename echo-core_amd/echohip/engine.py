@@ -115,6 +115,8 @@ class Engine:
         L.ec_engine_prefill_traced.argtypes = [vp, u32, vp, u32, i32, _TRACE_FN, vp]
         L.ec_engine_buffer.argtypes = [vp, i32, C.POINTER(vp), C.POINTER(C.c_size_t)]
         L.ec_engine_set_format.argtypes = [vp, i32, i32, i32]
+        L.ec_engine_set_act_pieces.argtypes = [vp, C.c_uint32]
+        L.ec_engine_get_act_pieces.argtypes = [vp]
         L.ec_engine_get_format.argtypes = [vp, i32, i32]
         c = _Cfg(**{f.name: getattr(cfg, f.name) for f in fields(cfg)})
         h = vp()
@@ -134,6 +136,14 @@ class Engine:
         self.close()
 
     # ---- weights
+    def set_act_pieces(self, pieces: int):
+        """int8 pieces per decode-matvec activation element (ec_engine_set_act_pieces): 2 (default) or 1."""
+        self._check(self.L.ec_engine_set_act_pieces(self.h, pieces), "set_act_pieces")
+
+    @property
+    def act_pieces(self) -> int:
+        return self.L.ec_engine_get_act_pieces(self.h)
+
     def set_format(self, layer: int, tensor: int, fmt: int):
         """Storage format of a matrix (Q8_0 / Q4_K) or of the embedding (Q8_0 / F16 / F32)."""
         self._check(self.L.ec_engine_set_format(self.h, layer, tensor, fmt), "set_format")
@@ -326,21 +336,23 @@ class Engine:
         xd = raw[xd_off:].view(np.float32).reshape(Mp, nbp)[:M, :K // 32]
         return np.ascontiguousarray(xq), np.ascontiguousarray(xd)
 
-    def read_act(self, which: int, K: int, M: int | None = None, fmt: int | None = None):
-        """An activation buffer (ec_quantize_act layout, M = max_batch; Q4_K for
-        the B_ACT4_* buffers, Q8_0 otherwise) as (xq int8 [B][K], xd fp32
-        [B][K/32]); Q4_K values in the quantizer's sub-block order."""
+    def read_act(self, which: int, K: int, M: int | None = None, fmt: int | None = None, pieces: int | None = None):
+        """An activation buffer (ec_quantize_act_pieces layout, M = max_batch;
+        Q4_K for the B_ACT4_* buffers, Q8_0 otherwise; pieces = the engine's)
+        as (xq int8 [B][pieces][K], xd fp32 [B][K/32]); Q4_K values in the
+        quantizer's sub-block order."""
         import torch
         p, n = self.buffer(which)
         assert n, f"step buffer {which} is not allocated"
         B = self.cfg.max_batch if M is None else M
-        xq = torch.empty(B * K, dtype=torch.int8, device="cuda")
+        P = self.act_pieces if pieces is None else pieces
+        xq = torch.empty(P * B * K, dtype=torch.int8, device="cuda")
         xd = torch.empty(B * (K // 32), dtype=torch.float32, device="cuda")
         if fmt is None:
             fmt = Q4_K if which in ACT4_BUFFERS else Q8_0
-        self.hip.act_unpack(fmt, p, xq, xd, B, K)
+        self.hip.act_unpack(fmt, p, xq, xd, B, K, pieces=P)
         torch.cuda.synchronize()
-        return xq.cpu().numpy().reshape(B, K), xd.cpu().numpy().reshape(B, K // 32)
+        return xq.cpu().numpy().reshape(B, P, K), xd.cpu().numpy().reshape(B, K // 32)
 
     @property
     def stream(self) -> int:

@@ -68,11 +68,26 @@ _SIGS = {
     "ec_glue_swiglu_rows_gemm_act": [_vp, _vp, _u32, _u32, _vp],
     "ec_glue_gated_norm_rows_gemm_act": [_vp, _vp, _u32, _u32, _vp, _vp, _u32, _u32, _vp],
     "ec_stream_read": [_vp, _sz, _vp, _u32, _vp],
+    # two-piece activation variants (the trailing _u32 before the stream is the piece count)
+    "ec_quantize_act_pieces": [C.c_int, _vp, _vp, _u32, _u32, _u32, _vp],
+    "ec_act_unpack_pieces": [C.c_int, _u32, _vp, _vp, _vp, _u32, _u32, _vp],
+    "ec_matvec_pieces": [C.c_int, _u32, _vp, _vp, _vp, _u32, _u32, _u32, _u32, C.c_int, _vp],
+    "ec_matvec_split_pieces": [C.c_int, _u32, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp],
+    "ec_block_dots_pieces": [C.c_int, _u32, _vp, _vp, _vp, _u32, _u32, _u32, _vp],
+    "ec_glue_rmsnorm_quant_pieces": [_vp, _vp, _vp, _u32, _u32, _u32, _vp],
+    "ec_glue_add_rmsnorm_quant_pieces": [_vp, _vp, _u32, _vp, _vp, _vp, _u32, _u32, _u32, _vp],
+    "ec_glue_swiglu_quant_split_pieces": [_vp, _u32, _vp, _u32, _u32, _u32, _vp],
+    "ec_glue_gated_norm_quant_pieces": [_vp, _vp, _u32, _u32, _vp, _vp, _u32, _u32, _u32, _vp],
+    "ec_delta_step_out_pieces": [_vp, _u32, _u32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32,
+                                 _u32, _u32, _vp],
+    "ec_attn_decode_packed_pieces": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u64, _u32, _u32, _u32, _u32,
+                                     _vp, _vp],
     "ec_stream_read_shape": [_vp, _sz, _vp, _u32, _u32, _u32, _vp],
 }
 _SIZE_FNS = {
     "ec_tiled_bytes": [C.c_int, _u32, _u32],
     "ec_act_bytes": [C.c_int, _u32, _u32],
+    "ec_act_bytes_pieces": [C.c_int, _u32, _u32, _u32],
     "ec_attn_ws_bytes": [_u32, _u32, _u32, _u32],
     "ec_attn_qa_bytes": [_u32, _u32],
     "ec_gemm_act_bytes": [C.c_int, _u32, _u32],
@@ -139,8 +154,8 @@ class Lib:
     def tiled_bytes(self, fmt, N, K):
         return self.L.ec_tiled_bytes(fmt, N, K)
 
-    def act_bytes(self, fmt, M, K):
-        return self.L.ec_act_bytes(fmt, M, K)
+    def act_bytes(self, fmt, M, K, pieces=1):
+        return self.L.ec_act_bytes_pieces(fmt, M, K, pieces)
 
     def attn_ws_bytes(self, n_seq, n_heads, head_dim, max_ctx):
         return self.L.ec_attn_ws_bytes(n_seq, n_heads, head_dim, max_ctx)
@@ -155,22 +170,40 @@ class Lib:
     def repack(self, fmt, gguf, tiled, N, K, stream=None):
         self._call("ec_repack", fmt, _ptr(gguf), _ptr(tiled), N, K, self._stream(stream))
 
-    def quantize_act(self, fmt, x, act, M, K, stream=None):
-        self._call("ec_quantize_act", fmt, _ptr(x), _ptr(act), M, K, self._stream(stream))
+    def quantize_act(self, fmt, x, act, M, K, stream=None, pieces=1):
+        """ec_quantize_act (pieces 1) or its two-piece form ec_quantize_act_pieces."""
+        if pieces == 1:
+            self._call("ec_quantize_act", fmt, _ptr(x), _ptr(act), M, K, self._stream(stream))
+        else:
+            self._call("ec_quantize_act_pieces", fmt, _ptr(x), _ptr(act), M, K, pieces, self._stream(stream))
 
-    def act_unpack(self, fmt, act, xq, xd, M, K, stream=None):
-        self._call("ec_act_unpack", fmt, _ptr(act), _ptr(xq), _ptr(xd), M, K, self._stream(stream))
+    def act_unpack(self, fmt, act, xq, xd, M, K, stream=None, pieces=1):
+        """xq [pieces*M][K] (row 2i + p: token i, piece p), xd [M][K/32]."""
+        self._call("ec_act_unpack_pieces", fmt, pieces, _ptr(act), _ptr(xq), _ptr(xd), M, K, self._stream(stream))
 
-    def matvec(self, fmt, tiled, act, y, M, N, K, ldy=None, accumulate=False, stream=None):
-        self._call("ec_matvec", fmt, _ptr(tiled), _ptr(act), _ptr(y), M, N, K, N if ldy is None else ldy,
-                   int(bool(accumulate)), self._stream(stream))
+    def matvec(self, fmt, tiled, act, y, M, N, K, ldy=None, accumulate=False, stream=None, pieces=1):
+        if pieces == 1:
+            self._call("ec_matvec", fmt, _ptr(tiled), _ptr(act), _ptr(y), M, N, K, N if ldy is None else ldy,
+                       int(bool(accumulate)), self._stream(stream))
+        else:
+            self._call("ec_matvec_pieces", fmt, pieces, _ptr(tiled), _ptr(act), _ptr(y), M, N, K,
+                       N if ldy is None else ldy, int(bool(accumulate)), self._stream(stream))
 
-    def matvec_split(self, fmt, tiled, act, parts, M, N, K, nsplit, stream=None):
-        self._call("ec_matvec_split", fmt, _ptr(tiled), _ptr(act), _ptr(parts), M, N, K, nsplit,
-                   self._stream(stream))
+    def matvec_split(self, fmt, tiled, act, parts, M, N, K, nsplit, stream=None, pieces=1):
+        if pieces == 1:
+            self._call("ec_matvec_split", fmt, _ptr(tiled), _ptr(act), _ptr(parts), M, N, K, nsplit,
+                       self._stream(stream))
+        else:
+            self._call("ec_matvec_split_pieces", fmt, pieces, _ptr(tiled), _ptr(act), _ptr(parts), M, N, K, nsplit,
+                       self._stream(stream))
 
-    def block_dots(self, fmt, tiled, act, out, M, N, K, stream=None):
-        self._call("ec_block_dots", fmt, _ptr(tiled), _ptr(act), _ptr(out), M, N, K, self._stream(stream))
+    def block_dots(self, fmt, tiled, act, out, M, N, K, stream=None, pieces=1):
+        """int32 block dots; with two pieces out is [2M][N][K/32] (row 2i + p = token i, piece p)."""
+        if pieces == 1:
+            self._call("ec_block_dots", fmt, _ptr(tiled), _ptr(act), _ptr(out), M, N, K, self._stream(stream))
+        else:
+            self._call("ec_block_dots_pieces", fmt, pieces, _ptr(tiled), _ptr(act), _ptr(out), M, N, K,
+                       self._stream(stream))
 
     def matvec_gguf_f32(self, fmt, gguf, x, y, M, K, stream=None):
         self._call("ec_matvec_gguf_f32", fmt, _ptr(gguf), _ptr(x), _ptr(y), M, K, self._stream(stream))
@@ -201,10 +234,10 @@ class Lib:
         return self.L.ec_attn_noalloc_max_bytes()
 
     def attn_decode_packed(self, q_packed, q_scales, keys, vals, ks, vs, out, act_q8, ctx, n_seq, seq_stride, n_heads,
-                           n_kv, max_ctx, ws, stream=None):
-        self._call("ec_attn_decode_packed", _ptr(q_packed), _ptr(q_scales), _ptr(keys), _ptr(vals), _ptr(ks),
-                   _ptr(vs), _ptr(out), _ptr(act_q8), _ptr(ctx), n_seq, seq_stride, n_heads, n_kv, max_ctx, _ptr(ws),
-                   self._stream(stream))
+                           n_kv, max_ctx, ws, stream=None, pieces=1):
+        self._call("ec_attn_decode_packed_pieces", _ptr(q_packed), _ptr(q_scales), _ptr(keys), _ptr(vals), _ptr(ks),
+                   _ptr(vs), _ptr(out), _ptr(act_q8), _ptr(ctx), n_seq, seq_stride, n_heads, n_kv, max_ctx, pieces,
+                   _ptr(ws), self._stream(stream))
 
     def qk_rope_append(self, proj, Nin, q_norm, k_norm, use_qn, use_kn, inv_freq, pos, q_out, q_packed, q_scales, keys,
                        vals, ks, vs, ctx, n_seq, seq_stride, max_ctx, n_heads, n_kv, head_dim, stream=None):
@@ -241,9 +274,15 @@ class Lib:
                    _ptr(dt_bias), _ptr(q), _ptr(k), _ptr(v), _ptr(dec), _ptr(beta), _ptr(pos), n_seq, n_k, n_v, kern,
                    self._stream(stream))
 
-    def gated_norm_quant(self, core, proj, Nin, z_off, norm_w, act, M, n_v, stream=None):
-        self._call("ec_glue_gated_norm_quant", _ptr(core), _ptr(proj), Nin, z_off, _ptr(norm_w), _ptr(act), M, n_v,
-                   self._stream(stream))
+    def gated_norm_quant(self, core, proj, Nin, z_off, norm_w, act, M, n_v, stream=None, pieces=1):
+        self._call("ec_glue_gated_norm_quant_pieces", _ptr(core), _ptr(proj), Nin, z_off, _ptr(norm_w), _ptr(act), M,
+                   n_v, pieces, self._stream(stream))
+
+    def delta_step_out(self, proj, nparts, Nin, conv_state, conv_w, a_log, dt_bias, norm_w, state, act, out, pos,
+                       n_seq, n_k, n_v, kern, stream=None, pieces=1):
+        self._call("ec_delta_step_out_pieces", _ptr(proj), nparts, Nin, _ptr(conv_state), _ptr(conv_w), _ptr(a_log),
+                   _ptr(dt_bias), _ptr(norm_w), _ptr(state), _ptr(act), _ptr(out), _ptr(pos), n_seq, n_k, n_v, kern,
+                   pieces, self._stream(stream))
 
     def conv_gates_chunk(self, proj, Nin, ring, conv_w, a_log, dt_bias, q, k, v, dec, beta, T, p0, n_k, n_v, kern,
                          stream=None):
@@ -270,18 +309,29 @@ class Lib:
         self._call("ec_glue_gated_norm_rows_gemm_act", _ptr(core), _ptr(proj), Nin, z_off, _ptr(norm_w), _ptr(act), M,
                    n_v, self._stream(stream))
 
-    def rmsnorm_quant(self, x, w, act, M, H, stream=None):
-        self._call("ec_glue_rmsnorm_quant", _ptr(x), _ptr(w), _ptr(act), M, H, self._stream(stream))
+    def rmsnorm_quant(self, x, w, act, M, H, stream=None, pieces=1):
+        if pieces == 1:
+            self._call("ec_glue_rmsnorm_quant", _ptr(x), _ptr(w), _ptr(act), M, H, self._stream(stream))
+        else:
+            self._call("ec_glue_rmsnorm_quant_pieces", _ptr(x), _ptr(w), _ptr(act), M, H, pieces, self._stream(stream))
 
-    def add_rmsnorm_quant(self, x, parts, nparts, x_out, w, act, M, H, stream=None):
-        self._call("ec_glue_add_rmsnorm_quant", _ptr(x), _ptr(parts), nparts, _ptr(x_out), _ptr(w), _ptr(act), M, H,
-                   self._stream(stream))
+    def add_rmsnorm_quant(self, x, parts, nparts, x_out, w, act, M, H, stream=None, pieces=1):
+        if pieces == 1:
+            self._call("ec_glue_add_rmsnorm_quant", _ptr(x), _ptr(parts), nparts, _ptr(x_out), _ptr(w), _ptr(act), M,
+                       H, self._stream(stream))
+        else:
+            self._call("ec_glue_add_rmsnorm_quant_pieces", _ptr(x), _ptr(parts), nparts, _ptr(x_out), _ptr(w),
+                       _ptr(act), M, H, pieces, self._stream(stream))
 
     def swiglu_quant(self, gu, act, M, F, stream=None):
         self._call("ec_glue_swiglu_quant", _ptr(gu), _ptr(act), M, F, self._stream(stream))
 
-    def swiglu_quant_split(self, gu, nparts, act, M, F, stream=None):
-        self._call("ec_glue_swiglu_quant_split", _ptr(gu), nparts, _ptr(act), M, F, self._stream(stream))
+    def swiglu_quant_split(self, gu, nparts, act, M, F, stream=None, pieces=1):
+        if pieces == 1:
+            self._call("ec_glue_swiglu_quant_split", _ptr(gu), nparts, _ptr(act), M, F, self._stream(stream))
+        else:
+            self._call("ec_glue_swiglu_quant_split_pieces", _ptr(gu), nparts, _ptr(act), M, F, pieces,
+                       self._stream(stream))
 
     def gemm_act_bytes(self, fmt, M, K):
         return self.L.ec_gemm_act_bytes(fmt, M, K)

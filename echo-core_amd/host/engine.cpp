@@ -103,6 +103,10 @@ struct ec_engine {
     float *hn = nullptr, *core_f = nullptr, *ff = nullptr;
     void *act4_h = nullptr, *act4_v = nullptr, *act4_q = nullptr, *act4_f = nullptr;
     bool packed_attn = false;  // int8-MFMA attention with q packed by the rope kernel
+    // int8 pieces per activation element of the decode step's matvecs (1: the
+    // reference quantizer alone; 2: plus the residual at scale/256, within
+    // ~2e-5 of the fp32-activation matvec); buffers are sized for 2
+    uint32_t P = 2;
     int32_t *tok = nullptr, *pos = nullptr, *gen = nullptr, *ctx = nullptr;
     // pinned staging for ec_engine_set_inputs: a ring of slots (tok[16],
     // pos[16]), each reused only after the event recorded behind its copies
@@ -221,7 +225,7 @@ std::vector<float> gen_vec(uint64_t seed, size_t n, double mean, double std) {
 // Activation bytes of one matvec input (int8 + fp32 block scales; Q4_K also
 // fp32 per-block sums).
 double act_alg_bytes(const ec_engine* e, const Mat& m) {
-    return (double)e->B * (m.K + m.K / 32 * 4 * (m.fmt == EC_Q4_K ? 2 : 1));
+    return (double)e->B * (e->P * m.K + m.K / 32 * 4 * (m.fmt == EC_Q4_K ? 2 : 1));
 }
 
 // One matvec launch; in profiling mode also its algorithmic bytes (weights,
@@ -230,7 +234,7 @@ int mv(ec_engine* e, const Mat& m, const void* act, float* y, uint32_t ldy, int 
     if (e->mv_bytes)
         e->mv_bytes->push_back((double)gguf_bytes(m, m.N) + act_alg_bytes(e, m) +
                                (double)e->B * m.N * 4 * (acc ? 2 : 1));
-    return ec_matvec(m.fmt, m.tiled, act, y, e->B, m.N, m.K, ldy, acc, e->st);
+    return ec_matvec_pieces(m.fmt, e->P, m.tiled, act, y, e->B, m.N, m.K, ldy, acc, e->st);
 }
 
 // K splits of a residual-adding projection (N = hidden): with N/16 tiles
@@ -289,8 +293,8 @@ uint32_t split_count(const Mat& m, uint32_t ns) { return m.fmt == EC_Q8_0 ? std:
 int mv_split(ec_engine* e, const Mat& m, const void* act, float* y, uint32_t ns) {
     if (e->mv_bytes)  // the output counted once (the extra partial sums are not algorithmic bytes)
         e->mv_bytes->push_back((double)gguf_bytes(m, m.N) + act_alg_bytes(e, m) + (double)e->B * m.N * 4);
-    if (m.fmt != EC_Q8_0) return ec_matvec(m.fmt, m.tiled, act, y, e->B, m.N, m.K, m.N, 0, e->st);
-    return ec_matvec_split(EC_Q8_0, m.tiled, act, y, e->B, m.N, m.K, ns, e->st);
+    if (m.fmt != EC_Q8_0) return ec_matvec_pieces(m.fmt, e->P, m.tiled, act, y, e->B, m.N, m.K, m.N, 0, e->st);
+    return ec_matvec_split_pieces(EC_Q8_0, e->P, m.tiled, act, y, e->B, m.N, m.K, ns, e->st);
 }
 
 // Residual projection: ns = resid_split(m) partial sums into e->parts.
@@ -337,17 +341,19 @@ int record_step(ec_engine* e) {
     // with a Q4_K consumer also the fp32 rows and their Q4_K activation
     auto norm = [&](const float* w, int layer, bool need4) -> int {
         if (ns == 0) {
-            EC_GLUE(EC_OP_NORM, layer, 0, xid(xc), xid(xc), ec_glue_rmsnorm_quant(xc, w, e->act_h, B, H, st));
+            EC_GLUE(EC_OP_NORM, layer, 0, xid(xc), xid(xc),
+                    ec_glue_rmsnorm_quant_pieces(xc, w, e->act_h, B, H, e->P, st));
         } else {
             float* xn = xc == e->x ? e->x2 : e->x;
             EC_GLUE(EC_OP_NORM, layer, ns, xid(xc), xid(xn),
-                    ec_glue_add_rmsnorm_quant(xc, e->parts, ns, xn, w, e->act_h, B, H, st));
+                    ec_glue_add_rmsnorm_quant_pieces(xc, e->parts, ns, xn, w, e->act_h, B, H, e->P, st));
             xc = xn;
             ns = 0;
         }
         if (need4) {
             EC_GLUE(EC_OP_NORM_ROWS, layer, 0, xid(xc), EC_B_HN, ec_glue_rmsnorm_rows(xc, w, e->hn, B, H, st));
-            EC_GLUE(EC_OP_QUANT_ACT, layer, 0, EC_B_HN, EC_B_ACT4_H, ec_quantize_act(EC_Q4_K, e->hn, e->act4_h, B, H, st));
+            EC_GLUE(EC_OP_QUANT_ACT, layer, 0, EC_B_HN, EC_B_ACT4_H,
+                    ec_quantize_act_pieces(EC_Q4_K, e->hn, e->act4_h, B, H, e->P, st));
         }
         return EC_OK;
     };
@@ -367,12 +373,13 @@ int record_step(ec_engine* e) {
             // (fp32 output instead when the output projection is Q4_K)
             const bool o4 = q4(y.w_out);
             EC_GLUE(EC_OP_DELTA_STEP, li, nsi, -1, o4 ? EC_B_CORE : EC_B_ACT_V,
-                    ec_delta_step_out(e->proj, nsi, Nin, y.conv_state, y.conv_w, y.a_log, y.dt_bias, y.ssm_norm,
-                                      y.ssm_state, o4 ? nullptr : e->act_v, o4 ? e->core_f : nullptr, e->pos, B,
-                                      e->n_k, e->n_v, c.conv_kernel, st));
+                    ec_delta_step_out_pieces(e->proj, nsi, Nin, y.conv_state, y.conv_w, y.a_log, y.dt_bias,
+                                             y.ssm_norm, y.ssm_state, o4 ? nullptr : e->act_v,
+                                             o4 ? e->core_f : nullptr, e->pos, B, e->n_k, e->n_v, c.conv_kernel, e->P,
+                                             st));
             if (o4)
                 EC_GLUE(EC_OP_QUANT_ACT, li, 0, EC_B_CORE, EC_B_ACT4_V,
-                        ec_quantize_act(EC_Q4_K, e->core_f, e->act4_v, B, e->value_dim, st));
+                        ec_quantize_act_pieces(EC_Q4_K, e->core_f, e->act4_v, B, e->value_dim, e->P, st));
             ns = resid_split(y.w_out.N, y.w_out.K, y.w_out.fmt);
             EC_MV(EC_OP_MV_OUT, li, ns, aid(y.w_out, EC_B_ACT_V, EC_B_ACT4_V),
                   mv_resid(e, y.w_out, ain(y.w_out, e->act_v, e->act4_v), ns));
@@ -391,9 +398,9 @@ int record_step(ec_engine* e) {
                                                      y.vals, y.ks, y.vs, e->ctx, B, e->seq_stride, c.max_ctx,
                                                      c.n_heads, c.n_kv, c.head_dim, st));
                 EC_GLUE(EC_OP_ATTN, li, 0, -1, o4 ? -1 : EC_B_ACT_Q,
-                        ec_attn_decode_packed(e->q_packed, e->q_scales, y.keys, y.vals, y.ks, y.vs, e->attn_out,
-                                              o4 ? nullptr : e->act_q, e->ctx, B, e->seq_stride, c.n_heads, c.n_kv,
-                                              c.max_ctx, e->attn_ws, st));
+                        ec_attn_decode_packed_pieces(e->q_packed, e->q_scales, y.keys, y.vals, y.ks, y.vs,
+                                                     e->attn_out, o4 ? nullptr : e->act_q, e->ctx, B, e->seq_stride,
+                                                     c.n_heads, c.n_kv, c.max_ctx, e->P, e->attn_ws, st));
             } else {
                 EC_GLUE(EC_OP_ROPE_APPEND, li, nsa, -1, -1,
                         ec_glue_qk_rope_append_split(e->proj, nsa, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn,
@@ -405,11 +412,11 @@ int record_step(ec_engine* e) {
                                        c.n_heads, c.n_kv, c.head_dim, c.max_ctx, e->attn_ws, st));
                 if (!o4)
                     EC_GLUE(EC_OP_QUANT_ACT, li, 0, EC_B_ATTN_OUT, EC_B_ACT_Q,
-                            ec_quantize_act(EC_Q8_0, e->attn_out, e->act_q, B, e->q_dim, st));
+                            ec_quantize_act_pieces(EC_Q8_0, e->attn_out, e->act_q, B, e->q_dim, e->P, st));
             }
             if (o4)
                 EC_GLUE(EC_OP_QUANT_ACT, li, 0, EC_B_ATTN_OUT, EC_B_ACT4_Q,
-                        ec_quantize_act(EC_Q4_K, e->attn_out, e->act4_q, B, e->q_dim, st));
+                        ec_quantize_act_pieces(EC_Q4_K, e->attn_out, e->act4_q, B, e->q_dim, e->P, st));
             ns = resid_split(y.w_out.N, y.w_out.K, y.w_out.fmt);
             EC_MV(EC_OP_MV_OUT, li, ns, aid(y.w_out, EC_B_ACT_Q, EC_B_ACT4_Q),
                   mv_resid(e, y.w_out, ain(y.w_out, e->act_q, e->act4_q), ns));
@@ -422,9 +429,11 @@ int record_step(ec_engine* e) {
               mv_split(e, y.w_gu, ain(y.w_gu, e->act_h, e->act4_h), e->gu, nsg));
         if (d4) {
             EC_GLUE(EC_OP_SWIGLU, li, nsg, -1, EC_B_FF, ec_glue_swiglu_rows(e->gu, e->ff, B, F, st));
-            EC_GLUE(EC_OP_QUANT_ACT, li, 0, EC_B_FF, EC_B_ACT4_F, ec_quantize_act(EC_Q4_K, e->ff, e->act4_f, B, F, st));
+            EC_GLUE(EC_OP_QUANT_ACT, li, 0, EC_B_FF, EC_B_ACT4_F,
+                    ec_quantize_act_pieces(EC_Q4_K, e->ff, e->act4_f, B, F, e->P, st));
         } else {
-            EC_GLUE(EC_OP_SWIGLU, li, nsg, -1, EC_B_ACT_F, ec_glue_swiglu_quant_split(e->gu, nsg, e->act_f, B, F, st));
+            EC_GLUE(EC_OP_SWIGLU, li, nsg, -1, EC_B_ACT_F,
+                    ec_glue_swiglu_quant_split_pieces(e->gu, nsg, e->act_f, B, F, e->P, st));
         }
         ns = resid_split(y.w_down.N, y.w_down.K, y.w_down.fmt);
         EC_MV(EC_OP_MV_DOWN, li, ns, aid(y.w_down, EC_B_ACT_F, EC_B_ACT4_F),
@@ -529,10 +538,10 @@ extern "C" int ec_engine_create(const ec_engine_cfg* cfg, ec_engine** out) {
         (rc = dalloc(e, &e->dec, (size_t)B * e->n_v)) || (rc = dalloc(e, &e->beta, (size_t)B * e->n_v)) ||
         (rc = dalloc(e, &e->qbuf, (size_t)B * e->q_dim)) || (rc = dalloc(e, &e->attn_out, (size_t)B * e->q_dim)) ||
         (rc = dalloc(e, &e->logits, (size_t)B * c.vocab)) || (rc = dalloc(e, &e->inv_freq, c.head_dim / 2)) ||
-        (rc = dalloc(e, &e->act_h, ec_act_bytes(EC_Q8_0, B, H))) ||
-        (rc = dalloc(e, &e->act_v, ec_act_bytes(EC_Q8_0, B, e->value_dim))) ||
-        (rc = dalloc(e, &e->act_f, ec_act_bytes(EC_Q8_0, B, e->F))) ||
-        (rc = dalloc(e, &e->act_q, ec_act_bytes(EC_Q8_0, B, e->q_dim))) ||
+        (rc = dalloc(e, &e->act_h, ec_act_bytes_pieces(EC_Q8_0, B, H, 2))) ||
+        (rc = dalloc(e, &e->act_v, ec_act_bytes_pieces(EC_Q8_0, B, e->value_dim, 2))) ||
+        (rc = dalloc(e, &e->act_f, ec_act_bytes_pieces(EC_Q8_0, B, e->F, 2))) ||
+        (rc = dalloc(e, &e->act_q, ec_act_bytes_pieces(EC_Q8_0, B, e->q_dim, 2))) ||
         (rc = dalloc(e, &e->attn_ws, ec_attn_ws_bytes(B, c.n_heads, c.head_dim, c.max_ctx))) ||
         (rc = dalloc(e, &e->tok, B)) || (rc = dalloc(e, &e->pos, B)) || (rc = dalloc(e, &e->gen, B)) ||
         (rc = dalloc(e, &e->ctx, B)))
@@ -588,10 +597,10 @@ int alloc_q4(ec_engine* e) {
     EC_TRY(dalloc(e, &e->hn, (size_t)B * e->H));
     EC_TRY(dalloc(e, &e->core_f, (size_t)B * std::max(e->value_dim, 1u)));
     EC_TRY(dalloc(e, &e->ff, (size_t)B * e->F));
-    EC_TRY(dalloc(e, &e->act4_h, ec_act_bytes(EC_Q4_K, B, e->H)));
-    EC_TRY(dalloc(e, &e->act4_v, e->value_dim % 256 ? 16 : ec_act_bytes(EC_Q4_K, B, e->value_dim)));
-    EC_TRY(dalloc(e, &e->act4_q, ec_act_bytes(EC_Q4_K, B, e->q_dim)));
-    EC_TRY(dalloc(e, &e->act4_f, e->F % 256 ? 16 : ec_act_bytes(EC_Q4_K, B, e->F)));
+    EC_TRY(dalloc(e, &e->act4_h, ec_act_bytes_pieces(EC_Q4_K, B, e->H, 2)));
+    EC_TRY(dalloc(e, &e->act4_v, e->value_dim % 256 ? 16 : ec_act_bytes_pieces(EC_Q4_K, B, e->value_dim, 2)));
+    EC_TRY(dalloc(e, &e->act4_q, ec_act_bytes_pieces(EC_Q4_K, B, e->q_dim, 2)));
+    EC_TRY(dalloc(e, &e->act4_f, e->F % 256 ? 16 : ec_act_bytes_pieces(EC_Q4_K, B, e->F, 2)));
     e->q4 = true;
     return EC_OK;
 }
@@ -631,6 +640,19 @@ extern "C" int ec_engine_set_format(ec_engine* e, int layer, int tensor, int fmt
     m->fmt = fmt;
     destroy_graph(e);
     return dalloc(e, &m->tiled, ec_tiled_bytes(fmt, m->N, m->K));
+}
+
+extern "C" int ec_engine_set_act_pieces(ec_engine* e, uint32_t pieces) {
+    if (!e || (pieces != 1 && pieces != 2)) return ec_set_error(EC_ERR_ARG, "ec_engine_set_act_pieces: 1 or 2 pieces");
+    if (pieces == e->P) return EC_OK;
+    EC_HIP(hipStreamSynchronize(e->st));
+    e->P = pieces;
+    return destroy_graph(e);
+}
+
+extern "C" int ec_engine_get_act_pieces(const ec_engine* e) {
+    if (!e) return ec_set_error(EC_ERR_ARG, "ec_engine_get_act_pieces: null engine");
+    return (int)e->P;
 }
 
 extern "C" int ec_engine_get_format(const ec_engine* e, int layer, int tensor) {
@@ -954,7 +976,8 @@ int prefill_alloc(ec_engine* e, Lane& L, uint32_t i) {
     const size_t act_rows_bytes = std::max(ec_gemm_act_bytes(EC_Q8_0, (uint32_t)C, (uint32_t)wide),
                                            ec_gemm_act_bytes(EC_Q4_K, (uint32_t)C, (uint32_t)(wide / 256 * 256)));
     const size_t act1_bytes =
-        std::max(ec_act_bytes(EC_Q8_0, 1, e->H), e->H % 256 ? (size_t)0 : ec_act_bytes(EC_Q4_K, 1, e->H));
+        std::max(ec_act_bytes_pieces(EC_Q8_0, 1, e->H, 2),
+                 e->H % 256 ? (size_t)0 : ec_act_bytes_pieces(EC_Q4_K, 1, e->H, 2));
     int rc;
     if (i == 0) {
         L.st = e->st;
@@ -1131,12 +1154,12 @@ int prefill_step(ec_engine* e, Lane& L, PrefillJob& j) {
     EC_TRY(launch(e, EC_OP_PF_HEAD, -1, 0, EC_B_PF_X, EC_B_LOGITS, [&]() -> int {
         if (e->lm_head.fmt == EC_Q4_K) {
             EC_TRY(ec_glue_rmsnorm_rows(xl, e->final_norm, L.n, 1, e->H, L.st));
-            EC_TRY(ec_quantize_act(EC_Q4_K, L.n, L.act1, 1, e->H, L.st));
+            EC_TRY(ec_quantize_act_pieces(EC_Q4_K, L.n, L.act1, 1, e->H, e->P, L.st));
         } else {
-            EC_TRY(ec_glue_rmsnorm_quant(xl, e->final_norm, L.act1, 1, e->H, L.st));
+            EC_TRY(ec_glue_rmsnorm_quant_pieces(xl, e->final_norm, L.act1, 1, e->H, e->P, L.st));
         }
-        return ec_matvec(e->lm_head.fmt, e->lm_head.tiled, L.act1, e->logits + (size_t)j.seq * e->c.vocab, 1,
-                         e->c.vocab, e->H, e->c.vocab, 0, L.st);
+        return ec_matvec_pieces(e->lm_head.fmt, e->P, e->lm_head.tiled, L.act1,
+                                e->logits + (size_t)j.seq * e->c.vocab, 1, e->c.vocab, e->H, e->c.vocab, 0, L.st);
     }));
     EC_HIP(hipMemcpyAsync(e->pos + j.seq, &last, 4, hipMemcpyHostToDevice, L.st));
     EC_TRY(ec_glue_argmax_advance_bounded(e->logits + (size_t)j.seq * e->c.vocab, e->c.vocab, e->gen + j.seq,
@@ -1287,10 +1310,10 @@ extern "C" int ec_engine_buffer(ec_engine* e, int which, void** dev, size_t* byt
         case EC_B_PARTS: p = e->parts, n = (size_t)kMaxResidSplit * B * e->H * 4; break;
         case EC_B_PROJ: p = e->proj, n = (size_t)kMaxResidSplit * B * e->nin_max * 4; break;
         case EC_B_GU: p = e->gu, n = (size_t)kMaxResidSplit * B * 2 * e->F * 4; break;
-        case EC_B_ACT_H: p = e->act_h, n = ec_act_bytes(EC_Q8_0, e->B, e->H); break;
-        case EC_B_ACT_V: p = e->act_v, n = ec_act_bytes(EC_Q8_0, e->B, e->value_dim); break;
-        case EC_B_ACT_F: p = e->act_f, n = ec_act_bytes(EC_Q8_0, e->B, e->F); break;
-        case EC_B_ACT_Q: p = e->act_q, n = ec_act_bytes(EC_Q8_0, e->B, e->q_dim); break;
+        case EC_B_ACT_H: p = e->act_h, n = ec_act_bytes_pieces(EC_Q8_0, e->B, e->H, e->P); break;
+        case EC_B_ACT_V: p = e->act_v, n = ec_act_bytes_pieces(EC_Q8_0, e->B, e->value_dim, e->P); break;
+        case EC_B_ACT_F: p = e->act_f, n = ec_act_bytes_pieces(EC_Q8_0, e->B, e->F, e->P); break;
+        case EC_B_ACT_Q: p = e->act_q, n = ec_act_bytes_pieces(EC_Q8_0, e->B, e->q_dim, e->P); break;
         case EC_B_ATTN_OUT: p = e->attn_out, n = B * e->q_dim * 4; break;
         case EC_B_Q_PACKED: p = e->q_packed, n = e->q_packed ? ec_attn_qa_bytes(e->B, c.n_heads) : 0; break;
         case EC_B_Q_SCALES: p = e->q_scales, n = e->q_scales ? B * c.n_heads * 3 * 4 : 0; break;
@@ -1304,12 +1327,12 @@ extern "C" int ec_engine_buffer(ec_engine* e, int which, void** dev, size_t* byt
         case EC_B_HN: p = e->hn, n = e->hn ? B * e->H * 4 : 0; break;
         case EC_B_CORE: p = e->core_f, n = e->core_f ? B * e->value_dim * 4 : 0; break;
         case EC_B_FF: p = e->ff, n = e->ff ? B * e->F * 4 : 0; break;
-        case EC_B_ACT4_H: p = e->act4_h, n = e->q4 ? ec_act_bytes(EC_Q4_K, e->B, e->H) : 0; break;
+        case EC_B_ACT4_H: p = e->act4_h, n = e->q4 ? ec_act_bytes_pieces(EC_Q4_K, e->B, e->H, e->P) : 0; break;
         case EC_B_ACT4_V:
-            p = e->act4_v, n = e->q4 && e->value_dim % 256 == 0 ? ec_act_bytes(EC_Q4_K, e->B, e->value_dim) : 0;
+            p = e->act4_v, n = e->q4 && e->value_dim % 256 == 0 ? ec_act_bytes_pieces(EC_Q4_K, e->B, e->value_dim, e->P) : 0;
             break;
-        case EC_B_ACT4_Q: p = e->act4_q, n = e->q4 ? ec_act_bytes(EC_Q4_K, e->B, e->q_dim) : 0; break;
-        case EC_B_ACT4_F: p = e->act4_f, n = e->q4 && e->F % 256 == 0 ? ec_act_bytes(EC_Q4_K, e->B, e->F) : 0; break;
+        case EC_B_ACT4_Q: p = e->act4_q, n = e->q4 ? ec_act_bytes_pieces(EC_Q4_K, e->B, e->q_dim, e->P) : 0; break;
+        case EC_B_ACT4_F: p = e->act4_f, n = e->q4 && e->F % 256 == 0 ? ec_act_bytes_pieces(EC_Q4_K, e->B, e->F, e->P) : 0; break;
         default: {
             // chunk buffers of prefill lane 0 (none before the first prefill)
             const ec_engine::PrefillLane& L = e->pf[0];
@@ -1330,7 +1353,7 @@ extern "C" int ec_engine_buffer(ec_engine* e, int which, void** dev, size_t* byt
                 case EC_B_PF_ATTN: p = L.attn, n = r ? C * e->q_dim : 0; break;
                 case EC_B_PF_TOK: p = L.tok, n = r ? C : 0; break;
                 case EC_B_PF_ACT1:
-                    p = L.act1, n = r ? ec_act_bytes(e->lm_head.fmt == EC_Q4_K ? EC_Q4_K : EC_Q8_0, 1, e->H) : 0;
+                    p = L.act1, n = r ? ec_act_bytes_pieces(e->lm_head.fmt == EC_Q4_K ? EC_Q4_K : EC_Q8_0, 1, e->H, e->P) : 0;
                     break;
                 case EC_B_PF_ACT: p = L.act, n = r ? L.act_bytes : 0; break;
                 default: return ec_set_error(EC_ERR_ARG, "ec_engine_buffer: unknown buffer");

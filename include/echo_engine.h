@@ -22,8 +22,10 @@
  *
  * Differences from the reference, all deliberate:
  *  - activations entering a matvec are quantized per 32-element block with the
- *    reference quantizer (src/kernels/quant.cpp:18-98) and multiplied with
- *    int8 MFMA (exact int32 block dots, fp32 scale epilogue);
+ *    reference quantizer (src/kernels/quant.cpp:18-98), plus (by default) a
+ *    second int8 piece for the residual at 1/256 of the block scale, and
+ *    multiplied with int8 MFMA (exact int32 block dots, fp32 scale epilogue);
+ *    the prefill GEMMs use the one-piece activation;
  *  - the INT8 KV cache has one scale per (token, kv head) row, the layout its
  *    readers index (src/inference.cpp:347,387) (the reference writers store
  *    one scale per token);
@@ -84,6 +86,15 @@ int ec_engine_create(const ec_engine_cfg* cfg, ec_engine** out);
  * contents are undefined until set) and drops the captured step graph. */
 int ec_engine_set_format(ec_engine* e, int layer, int tensor, int fmt);
 int ec_engine_get_format(const ec_engine* e, int layer, int tensor);
+/* int8 pieces per activation element entering the decode step's matvecs (and
+ * the last prompt token's vocab projection): 2 (default) = the reference
+ * quantizer's int8 plus its residual at 1/256 of the block scale
+ * (ec_quantize_act_pieces; each matvec within ~2e-5 relative of the
+ * reference's fp32-activation arithmetic, src/kernels/matvec.cpp:62-142), 1 =
+ * the reference quantizer alone (~5e-3).  No counterpart in the reference.
+ * Drops the captured step graph. */
+int ec_engine_set_act_pieces(ec_engine* e, uint32_t pieces);
+int ec_engine_get_act_pieces(const ec_engine* e);
 /* The configuration the engine was created with. */
 int ec_engine_get_config(const ec_engine* e, ec_engine_cfg* out);
 void ec_engine_destroy(ec_engine* e);

@@ -72,9 +72,25 @@ int ec_unpack_tiled(int fmt, const void* tiled, void* gguf, uint32_t N, uint32_t
  * K must be a multiple of 32; the buffer is padded like the weights. */
 size_t ec_act_bytes(int fmt, uint32_t M, uint32_t K);
 int ec_quantize_act(int fmt, const float* x, void* act, uint32_t M, uint32_t K, void* stream);
+/* Two-piece activations (no counterpart in the reference, whose matvecs take
+ * fp32 x, src/kernels/matvec.cpp:62-142): pieces = 2 stores, per block, piece
+ * 0 = the reference quantizer's int8 q0 at scale s and piece 1 = the residual
+ * x - s*q0 quantized with the scale s/256, q1 = sat8(rne((x - s*q0) * (256/s)))
+ * (x ~ s*q0 + (s/256)*q1, |error| <= s/512: within ~2e-5 relative of the
+ * fp32 matvec instead of ~5e-3 with one piece).  The M tokens occupy 2M rows
+ * of the one-piece layout (token i's pieces in rows 2i, 2i+1;
+ * ec_act_unpack_pieces reads them back), scales per token; Q4_K's sum
+ * becomes s * (sum q0 + sum q1 / 256).  pieces = 1 is ec_quantize_act. */
+size_t ec_act_bytes_pieces(int fmt, uint32_t M, uint32_t K, uint32_t pieces);
+int ec_quantize_act_pieces(int fmt, const float* x, void* act, uint32_t M, uint32_t K, uint32_t pieces,
+                           void* stream);
 /* Read back the quantized activation in natural order: xq[M][K] int8 (block
  * grouping as above, i.e. Q4_K values in sub-block order) and xd[M][K/32]. */
 int ec_act_unpack(int fmt, const void* act, int8_t* xq, float* xd, uint32_t M, uint32_t K, void* stream);
+/* The same for `pieces` (1 or 2) pieces: xq[pieces*M][K] (row 2i + p = token
+ * i, piece p), xd[M][K/32]. */
+int ec_act_unpack_pieces(int fmt, uint32_t pieces, const void* act, int8_t* xq, float* xd, uint32_t M, uint32_t K,
+                         void* stream);
 
 /* ------------------------------------------------------- decode matvec / GEMV
  * y[m][n] (+)= sum_b d_w[n,b] * d_x[m,b] * isum[m,n,b] for M (1..16) token rows,
@@ -93,6 +109,16 @@ int ec_matvec_split(int fmt, const void* tiled, const void* act, float* parts, u
 /* The int32 block dots themselves: out[m][n][K/32] (parity contract). */
 int ec_block_dots(int fmt, const void* tiled, const void* act, int32_t* out, uint32_t M, uint32_t N, uint32_t K,
                   void* stream);
+/* The same three over an activation of 1 or 2 pieces (ec_quantize_act_pieces):
+ * with two pieces each block dot is 256*isum0 + isum1 (exact int32) scaled by
+ * d_w * d_x / 256; ec_block_dots_pieces writes the dots of every layout row,
+ * out[pieces*M][N][K/32] (row 2i + p: token i, piece p). */
+int ec_matvec_pieces(int fmt, uint32_t pieces, const void* tiled, const void* act, float* y, uint32_t M, uint32_t N,
+                     uint32_t K, uint32_t ldy, int accumulate, void* stream);
+int ec_matvec_split_pieces(int fmt, uint32_t pieces, const void* tiled, const void* act, float* parts, uint32_t M,
+                           uint32_t N, uint32_t K, uint32_t nsplit, void* stream);
+int ec_block_dots_pieces(int fmt, uint32_t pieces, const void* tiled, const void* act, int32_t* out, uint32_t M,
+                         uint32_t N, uint32_t K, void* stream);
 
 /* ------------------------------------------- reference-semantics fp32 matvec
  * y[m] += W[m,:] . x over GGUF bytes with fp32 activations (no activation
@@ -167,6 +193,12 @@ int ec_attn_decode_packed(const void* q_packed, const float* q_scales, const int
                           const float* kscales, const float* vscales, float* out, void* act_q8, const int32_t* ctx,
                           uint32_t n_seq, uint64_t seq_stride, uint32_t n_heads, uint32_t n_kv, uint32_t max_ctx,
                           void* ws, void* stream);
+/* ec_attn_decode_packed whose act_q8 holds `pieces` (1 or 2) pieces per
+ * element (ec_quantize_act_pieces' layout). */
+int ec_attn_decode_packed_pieces(const void* q_packed, const float* q_scales, const int8_t* keys, const int8_t* vals,
+                                 const float* kscales, const float* vscales, float* out, void* act_q8,
+                                 const int32_t* ctx, uint32_t n_seq, uint64_t seq_stride, uint32_t n_heads,
+                                 uint32_t n_kv, uint32_t max_ctx, uint32_t pieces, void* ws, void* stream);
 
 /* Causal attention of a prompt chunk over one sequence's cache: query token t
  * (q, out: [T][n_heads][256]) sits at position pos0 + t and attends over
@@ -225,6 +257,11 @@ int ec_delta_step_out(const float* proj, uint32_t nparts, uint32_t Nin, float* c
                       const float* a_log, const float* dt_bias, const float* norm_w, float* state, void* act,
                       float* out, const int32_t* pos, uint32_t n_seq, uint32_t n_k, uint32_t n_v, uint32_t kern,
                       void* stream);
+/* ec_delta_step_out with act in `pieces` (1 or 2) pieces (ec_quantize_act_pieces' layout). */
+int ec_delta_step_out_pieces(const float* proj, uint32_t nparts, uint32_t Nin, float* conv_state, const float* conv_w,
+                             const float* a_log, const float* dt_bias, const float* norm_w, float* state, void* act,
+                             float* out, const int32_t* pos, uint32_t n_seq, uint32_t n_k, uint32_t n_v,
+                             uint32_t kern, uint32_t pieces, void* stream);
 /* seq_pos (may be NULL): sequence s is skipped entirely (state untouched, no
  * output written) when seq_pos[s] < 0. */
 /* ec_delta_step with the input projection given as nparts (1..8) partial sums
@@ -258,6 +295,17 @@ int ec_glue_conv_gates(const float* proj, uint32_t Nin, float* conv_state, const
                        const int32_t* pos, uint32_t n_seq, uint32_t n_k, uint32_t n_v, uint32_t kern, void* stream);
 int ec_glue_gated_norm_quant(const float* core, const float* proj, uint32_t Nin, uint32_t z_off, const float* norm_w,
                              void* act, uint32_t M, uint32_t n_v, void* stream);
+/* The _quant ops writing `pieces` (1 or 2) pieces per element (ec_quantize_act_pieces' layout). */
+int ec_glue_rmsnorm_quant_pieces(const float* x, const float* w, void* act, uint32_t M, uint32_t H, uint32_t pieces,
+                                 void* stream);
+int ec_glue_add_rmsnorm_quant_pieces(const float* x, const float* parts, uint32_t nparts, float* x_out,
+                                     const float* w, void* act, uint32_t M, uint32_t H, uint32_t pieces,
+                                     void* stream);
+int ec_glue_swiglu_quant_split_pieces(const float* gu, uint32_t nparts, void* act, uint32_t M, uint32_t F,
+                                      uint32_t pieces, void* stream);
+int ec_glue_gated_norm_quant_pieces(const float* core, const float* proj, uint32_t Nin, uint32_t z_off,
+                                    const float* norm_w, void* act, uint32_t M, uint32_t n_v, uint32_t pieces,
+                                    void* stream);
 int ec_glue_qk_rope_append(const float* proj, uint32_t Nin, const float* q_norm, const float* k_norm, int use_qn,
                            int use_kn, const float* inv_freq, const int32_t* pos, float* q_out, void* q_packed,
                            float* q_scales, int8_t* keys, int8_t* vals, float* kscales, float* vscales, int32_t* ctx,

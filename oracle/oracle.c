@@ -272,6 +272,27 @@ void oc_dequant_act2_q8_0(const int8_t* xq0, const int8_t* xq1, const float* xd,
     }
 }
 
+/* Two pieces per 32-element Q4_K sub-block (positions in oc_q4k_pos order, as
+ * oc_quantize_act_q4_K): piece 0 the reference quantizer of the sub-block,
+ * piece 1 its residual at scale/256 as in oc_quantize_act2_q8_0. */
+void oc_quantize_act2_q4_K(const float* x, int8_t* xq0, int8_t* xq1, float* xd, uint32_t K) {
+    float tmp[32];
+    for (uint32_t sb = 0; sb < K / 32; ++sb) {
+        uint32_t b = sb / 8, s = sb % 8;
+        for (uint32_t i = 0; i < 32; ++i) tmp[i] = x[256 * b + oc_q4k_pos(s, i)];
+        oc_quantize_act2_q8_0(tmp, xq0 + 32 * sb, xq1 + 32 * sb, xd + sb, 32);
+    }
+}
+
+void oc_dequant_act2_q4_K(const int8_t* xq0, const int8_t* xq1, const float* xd, float* x_deq, uint32_t K) {
+    for (uint32_t sb = 0; sb < K / 32; ++sb) {
+        uint32_t b = sb / 8, s = sb % 8;
+        float tmp[32];
+        oc_dequant_act2_q8_0(xq0 + 32 * sb, xq1 + 32 * sb, xd + sb, tmp, 32);
+        for (uint32_t i = 0; i < 32; ++i) x_deq[256 * b + oc_q4k_pos(s, i)] = tmp[i];
+    }
+}
+
 void oc_dequant_act_q8_0(const int8_t* xq, const float* xd, float* x_deq, uint32_t K) {
     for (uint32_t k = 0; k < K; ++k) x_deq[k] = (float)xq[k] * xd[k / 32];
 }
@@ -555,12 +576,17 @@ static void mv_free(mv_scratch* m) { free(m->deq); free(m->qq); free(m->qq1); fr
 /* Matvec with optional activation quantization: y = W * x (y zeroed first).
  * quant_act 0: fp32 x (reference); 1: x quantized per 32-block; 2: x as two
  * int8 pieces per 32-block (oc_quantize_act2_q8_0).  A Q4_K matrix quantizes
- * its input per 32-element sub-block (oc_quantize_act_q4_K) for 1 and 2. */
+ * its input per 32-element sub-block (oc_quantize_act_q4_K, or
+ * oc_quantize_act2_q4_K for 2). */
 static void mv_fmt(int fmt, const uint8_t* W, const float* x, float* y, uint32_t M, uint32_t K, int quant_act,
                    mv_scratch* s) {
     memset(y, 0, sizeof(float) * M);
     if (fmt == OC_Q4_K) {
-        if (quant_act) {
+        if (quant_act == 2) {
+            oc_quantize_act2_q4_K(x, s->qq, s->qq1, s->qd, K);
+            oc_dequant_act2_q4_K(s->qq, s->qq1, s->qd, s->deq, K);
+            oc_matvec_q4_K(W, s->deq, y, M, K);
+        } else if (quant_act) {
             oc_quantize_act_q4_K(x, s->qq, s->qd, NULL, K);
             oc_dequant_act_q4_K(s->qq, s->qd, s->deq, K);
             oc_matvec_q4_K(W, s->deq, y, M, K);

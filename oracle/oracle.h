@@ -88,6 +88,8 @@ void oc_quantize_act_q4_K(const float* x, int8_t* xq, float* xd, int32_t* xsum, 
  * scale s/256.  x ~ q0*s + q1*s/256; x_deq = q0*s + q1*(s/256). */
 void oc_quantize_act2_q8_0(const float* x, int8_t* xq0, int8_t* xq1, float* xd, uint32_t K);
 void oc_dequant_act2_q8_0(const int8_t* xq0, const int8_t* xq1, const float* xd, float* x_deq, uint32_t K);
+void oc_quantize_act2_q4_K(const float* x, int8_t* xq0, int8_t* xq1, float* xd, uint32_t K);
+void oc_dequant_act2_q4_K(const int8_t* xq0, const int8_t* xq1, const float* xd, float* x_deq, uint32_t K);
 /* Dequantize back to natural order (x_deq[k] = xq*xd) for the reference matvec. */
 void oc_dequant_act_q8_0(const int8_t* xq, const float* xd, float* x_deq, uint32_t K);
 void oc_dequant_act_q4_K(const int8_t* xq, const float* xd, float* x_deq, uint32_t K);
@@ -142,7 +144,8 @@ void oc_conv_step(float* conv_state, const float* x, const float* w, float* out,
  * Small, self-contained restatement used as the decoder checker and as the
  * CPU baseline.  Weights are GGUF Q8_0 byte blocks; norms and small vectors
  * are fp32.  quant_act 1 inserts the one-piece int8 activation quantization
- * before every matvec, 2 the two-piece one (design; oc_quantize_act2_q8_0),
+ * before every matvec, 2 the two-piece one (oc_quantize_act2_q8_0 /
+ * oc_quantize_act2_q4_K, what the GPU decode step computes by default),
  * 0 keeps fp32 activations (reference semantics). */
 typedef struct {
     uint32_t hidden, ffn, n_layers, vocab;
@@ -208,8 +211,8 @@ void oc_gated_rmsnorm(float* core, const float* z, const float* w, uint32_t n_v,
 /* y = W x (y zeroed), x first quantized per 32-block when quant_act != 0. */
 void oc_matvec_act_q8_0(const void* W, const float* x, float* y, uint32_t M, uint32_t K, int quant_act);
 /* The same for a matrix of format fmt (OC_Q8_0 or OC_Q4_K; a Q4_K input is
- * quantized per 32-element sub-block, oc_quantize_act_q4_K; quant_act 2
- * applies to Q8_0 only and quantizes a Q4_K input as 1 does). */
+ * quantized per 32-element sub-block, oc_quantize_act_q4_K; quant_act 2 in
+ * two pieces, oc_quantize_act2_q4_K). */
 void oc_matvec_act(int fmt, const void* W, const float* x, float* y, uint32_t M, uint32_t K, int quant_act);
 /* qwen_linear.forward of block l (qwen_linear.zig:103-271): in = the block's
  * normed input [hidden], out = its output [hidden] (before the residual). */

@@ -52,6 +52,10 @@ class Oracle:
         L.oc_quantize_act_q8_0.argtypes = [_f32p, _i8p, _f32p, _u32]
         L.oc_quantize_act_q4_K.argtypes = [_f32p, _i8p, _f32p, _i32p, _u32]
         L.oc_dequant_act_q8_0.argtypes = [_i8p, _f32p, _f32p, _u32]
+        L.oc_quantize_act2_q8_0.argtypes = [_f32p, _i8p, _i8p, _f32p, _u32]
+        L.oc_dequant_act2_q8_0.argtypes = [_i8p, _i8p, _f32p, _f32p, _u32]
+        L.oc_quantize_act2_q4_K.argtypes = [_f32p, _i8p, _i8p, _f32p, _u32]
+        L.oc_dequant_act2_q4_K.argtypes = [_i8p, _i8p, _f32p, _f32p, _u32]
         L.oc_dequant_act_q4_K.argtypes = [_i8p, _f32p, _f32p, _u32]
         L.oc_block_dots_q8_0.argtypes = [_u8p, _i8p, _i32p, _u32, _u32]
         L.oc_block_dots_q4_K.argtypes = [_u8p, _i8p, _i32p, _u32, _u32]
@@ -194,6 +198,34 @@ class Oracle:
         xs = np.zeros(K // 32, np.int32)
         self.lib.oc_quantize_act_q4_K(np.ascontiguousarray(x, np.float32), xq, xd, xs, K)
         return xq, xd, xs
+
+    def quantize_act2_q8_0(self, x: np.ndarray):
+        """Two int8 pieces per 32-block (oc_quantize_act2_q8_0): (q0, q1, scales)."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        q0, q1 = np.zeros(x.size, np.int8), np.zeros(x.size, np.int8)
+        d = np.zeros(x.size // 32, np.float32)
+        self.lib.oc_quantize_act2_q8_0(x, q0, q1, d, x.size)
+        return q0, q1, d
+
+    def dequant_act2_q8_0(self, q0, q1, xd):
+        q0, q1 = np.ascontiguousarray(q0, np.int8).reshape(-1), np.ascontiguousarray(q1, np.int8).reshape(-1)
+        out = np.zeros(q0.size, np.float32)
+        self.lib.oc_dequant_act2_q8_0(q0, q1, np.ascontiguousarray(xd, np.float32).reshape(-1), out, q0.size)
+        return out
+
+    def quantize_act2_q4_K(self, x: np.ndarray):
+        """Two pieces per Q4_K sub-block (oc_quantize_act2_q4_K), values in sub-block order: (q0, q1, scales)."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        q0, q1 = np.zeros(x.size, np.int8), np.zeros(x.size, np.int8)
+        d = np.zeros(x.size // 32, np.float32)
+        self.lib.oc_quantize_act2_q4_K(x, q0, q1, d, x.size)
+        return q0, q1, d
+
+    def dequant_act2_q4_K(self, q0, q1, xd):
+        q0, q1 = np.ascontiguousarray(q0, np.int8).reshape(-1), np.ascontiguousarray(q1, np.int8).reshape(-1)
+        out = np.zeros(q0.size, np.float32)
+        self.lib.oc_dequant_act2_q4_K(q0, q1, np.ascontiguousarray(xd, np.float32).reshape(-1), out, q0.size)
+        return out
 
     def dequant_act_q8_0(self, xq, xd):
         out = np.zeros(xq.size, np.float32)

@@ -16,7 +16,14 @@ comparison measures that one operation:
                          element whose x/scale lies within the scale difference
                          or QUANT_SLACK of a rounding boundary (there the two
                          fp32 values may round to neighbours), such flips at
-                         most MAX_FLIP_FRACTION of the elements.
+                         most MAX_FLIP_FRACTION of the elements.  With two
+                         pieces (the engine's default) piece 0 is held to that,
+                         and the two-piece value s*(q0 + q1/256) to the
+                         oracle's two-piece quantizer of its fp32 value within
+                         two piece-1 steps (each side errs by at most s/512)
+                         plus the fp32 slack: piece 1 resolves the input 256x
+                         finer, so fp32 differences between the two producers
+                         flip it far more often than piece 0 (reported).
 
 A quantization launch of the GPU's own fp32 rows (QUANT_ACT) is compared bit
 for bit with the reference quantizer.  Matrices stored as Q4_K read a Q4_K
@@ -60,6 +67,7 @@ class OpChecker:
         self.counts = {}     # op -> number of (op, sequence) comparisons made
         self.worst = {}      # op -> worst fp32 relative error seen
         self.flips = [0, 0]  # int8 elements that differ by one at a boundary, elements compared
+        self.flips2 = [0, 0]  # two-piece values (256 q0 + q1) that differ, elements compared
 
     # ------------------------------------------------------------- helpers
     def _note(self, op, err=None):
@@ -93,6 +101,15 @@ class OpChecker:
         K = self._width(which)
         return self.eng.read_buffer(which, np.float32, 0, self.B * K).reshape(self.B, K)
 
+    def _dequant(self, xq, xd, fmt):
+        """fp32 value of a GPU activation row: xq [K] or [1][K] (one piece) or [2][K] (two pieces)."""
+        xq = np.asarray(xq)
+        oc = self.oc
+        if xq.ndim == 2 and xq.shape[0] == 2:
+            return oc.dequant_act2_q4_K(xq[0], xq[1], xd) if fmt == E.Q4_K else oc.dequant_act2_q8_0(xq[0], xq[1], xd)
+        q = xq.reshape(-1)
+        return oc.dequant_act_q4_K(q, xd) if fmt == E.Q4_K else oc.dequant_act_q8_0(q, xd)
+
     def _quant(self, op, xq, xd, ref, what, fmt=E.Q8_0):
         """GPU int8 block activation (xq, xd) against the reference quantizer of the oracle's fp32 `ref`.
 
@@ -105,8 +122,14 @@ class OpChecker:
         within the scale difference or QUANT_SLACK of a rounding boundary
         (there the neighbour is allowed), such flips at most
         MAX_FLIP_FRACTION of all elements compared.  The dequantized vectors'
-        relative L2 is reported (one flip moves a block by one quantum)."""
+        relative L2 is reported (one flip moves a block by one quantum).
+        xq [P][K] with P = 2: piece 0 as above, then the two-piece values."""
         ref = np.ascontiguousarray(ref, np.float32)
+        xq = np.asarray(xq)
+        xq1 = xq[1] if xq.ndim == 2 and xq.shape[0] == 2 else None
+        xq = xq.reshape(-1) if xq.ndim == 1 else xq[0]
+        if xq1 is not None:
+            r2 = self.oc.quantize_act2_q4_K(ref) if fmt == E.Q4_K else self.oc.quantize_act2_q8_0(ref)
         if fmt == E.Q4_K:
             rq, rd, _ = self.oc.quantize_act_q4_K(ref)
             ref = ref[self._sub_order(ref.size)]
@@ -129,6 +152,16 @@ class OpChecker:
         self.flips[0] += int((diff != 0).sum())
         self.flips[1] += diff.size
         assert self.flips[0] <= MAX_FLIP_FRACTION * self.flips[1], f"{what}: too many boundary flips {self.flips}"
+        if xq1 is not None:
+            s_g, s_r = np.repeat(xd64, 32), np.repeat(rd64, 32)
+            t_g = 256.0 * xq.astype(np.float64) + xq1
+            t_r = 256.0 * r2[0].astype(np.float64) + r2[1]
+            dev = np.abs(t_g * s_g - t_r * s_r) / 256.0
+            tol = s_r * (2.04 / 256.0 + QUANT_SLACK) + 128.0 * np.abs(s_g - s_r)
+            assert np.all(dev <= tol), f"{what}: two-piece value off by {np.max(dev / np.maximum(s_r, 1e-30)):.2e} scales"
+            self.flips2[0] += int((t_g != t_r).sum())
+            self.flips2[1] += t_g.size
+            self.act2_dev = max(getattr(self, "act2_dev", 0.0), rel_l2(t_g * s_g, t_r * s_r))
         self._note(op)
 
     def _active(self):
@@ -253,8 +286,13 @@ class OpChecker:
             xq, xd = eng.read_act(ev.x_out, K)
             q4 = ev.x_out in E.ACT4_BUFFERS
             for s in act:
-                rq, rd = (oc.quantize_act_q4_K(b["rows"][s])[:2] if q4 else oc.quantize_act_q8_0(b["rows"][s]))
-                assert np.array_equal(xq[s], rq) and np.array_equal(xd[s], rd), \
+                if xq.shape[1] == 2:
+                    rq0, rq1, rd = (oc.quantize_act2_q4_K if q4 else oc.quantize_act2_q8_0)(b["rows"][s])
+                    ok = np.array_equal(xq[s][0], rq0) and np.array_equal(xq[s][1], rq1)
+                else:
+                    rq, rd = (oc.quantize_act_q4_K(b["rows"][s])[:2] if q4 else oc.quantize_act_q8_0(b["rows"][s]))
+                    ok = np.array_equal(xq[s][0], rq)
+                assert ok and np.array_equal(xd[s], rd), \
                     f"{where} seq {s}: quantized activation of the GPU's rows not bit-exact"
                 self._note(op)
         elif op in (E.OP_MV_IN, E.OP_MV_OUT, E.OP_MV_GU, E.OP_MV_DOWN, E.OP_LM_HEAD):
@@ -269,10 +307,8 @@ class OpChecker:
             rows = self._rows(N)
             Wr = np.ascontiguousarray(W[rows])
             for s in act:
-                if fmt == E.Q4_K:
-                    ref = oc.matvec_q4_K(Wr, oc.dequant_act_q4_K(b["xq"][s], b["xd"][s]))
-                else:
-                    ref = oc.matvec_q8_0(Wr, oc.dequant_act_q8_0(b["xq"][s], b["xd"][s]))
+                x = self._dequant(b["xq"][s], b["xd"][s], fmt)
+                ref = oc.matvec_q4_K(Wr, x) if fmt == E.Q4_K else oc.matvec_q8_0(Wr, x)
                 self._fp(op, y[s][rows], ref, f"{where} seq {s}")
         elif op == E.OP_DELTA_STEP:
             self._check_delta(L, act, b, where, ev.x_out)
@@ -391,5 +427,7 @@ class OpChecker:
         parts = [f"{ops.get(k, k)}:{n}" for k, n in self.counts.items() if not isinstance(k, tuple)]
         worst = " ".join(f"{ops.get(k, k)}={v:.1e}" for k, v in self.worst.items())
         return (f"checks {' '.join(parts)}; worst fp32 rel_l2 {worst}; int8 flips {self.flips[0]}/{self.flips[1]}; "
+                f"two-piece value flips {self.flips2[0]}/{self.flips2[1]}; "
                 f"worst block-scale deviation {getattr(self, 'scale_dev', 0.0):.1e}, "
-                f"dequantized activation rel_l2 {getattr(self, 'act_dev', 0.0):.1e}")
+                f"dequantized activation rel_l2 {getattr(self, 'act_dev', 0.0):.1e} "
+                f"(two-piece {getattr(self, 'act2_dev', 0.0):.1e})")

@@ -32,10 +32,10 @@ row per token of the chunk), with the tolerances of tests/decoder_ops.py:
                              decoder_ops (boundary flips only)
   causal attention           the oracle's decode attention of each token over
                              its positions 0 .. p+t, within FP_TOL
-  head                       the last token's activation against the
-                             reference quantizer of the oracle's final norm
-                             (boundary flips only), logits from that
-                             activation within FP_TOL
+  head                       the last token's activation (the engine's pieces)
+                             against the reference quantizer of the oracle's
+                             final norm (boundary flips only), logits from
+                             that activation within FP_TOL
 """
 from __future__ import annotations
 
@@ -189,10 +189,8 @@ class PrefillChecker(OpChecker):
             self._quant(op, xq[0], xd[0], oc.rmsnorm(b["x"], self.m["final_norm"]), f"{where} head activation", fmt)
             rows = self._sub(W.shape[0])
             Wr = np.ascontiguousarray(W[rows])
-            if fmt == E.Q4_K:
-                ref = oc.matvec_q4_K(Wr, oc.dequant_act_q4_K(xq[0], xd[0]))
-            else:
-                ref = oc.matvec_q8_0(Wr, oc.dequant_act_q8_0(xq[0], xd[0]))
+            x = self._dequant(xq[0], xd[0], fmt)
+            ref = oc.matvec_q4_K(Wr, x) if fmt == E.Q4_K else oc.matvec_q8_0(Wr, x)
             logits = eng.read_buffer(E.B_LOGITS, np.float32, self.seq * c.vocab, c.vocab)
             self._fp(op, logits[rows], ref, f"{where} logits")
 

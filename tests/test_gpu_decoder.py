@@ -147,36 +147,57 @@ def test_decoder_4b_shapes_every_op_matches_oracle(oc):
 
 
 def test_decoder_4b_end_to_end_vs_fp32_reference(oc):
-    """The quantized-activation decoder against the reference arithmetic (fp32 activations, oc_decoder_token
-    quant_act=0) on the 4B-class weights, one sequence, four tokens: the deviation and greedy-token agreement
-    are reported.  (Parity is the per-operation test above; this is the accumulated effect of int8 activations
-    over 32 blocks, also shown by the oracle itself run with quantized activations.)"""
+    """The 4B-class decoder (graph steps, two-piece activations) against the reference arithmetic: fp32
+    activations (oc_decoder_token quant_act=0, AVX2 build: the fused-dot order of src/kernels/quant.cpp:150-194),
+    one sequence, six teacher-forced tokens.  For scale, the reference's own two fp32 orders (the scalar
+    matvec_q8_0 of src/kernels/matvec.cpp:62-87 against the AVX2 fused dot) and the one-piece engine are run on
+    the same tokens: with random weights the 32 blocks amplify any per-matvec difference ~10^4-fold (a 4e-7
+    summation-order difference becomes ~4e-3 in the logits), so the bound is held relative to that spread.
+    Greedy tokens must agree wherever the reference's top-2 margin exceeds twice the largest logit difference
+    the one-piece path shows (a clear margin)."""
     from echohip.engine import Engine, EngineConfig
     from oracle import Baseline
     cfg = EngineConfig(max_batch=1, max_ctx=16)
     eng = Engine(cfg)
     eng.init_random(seed=0)
-    eng.reset()
     m = eng.export_model()
     bl = Baseline()
     bl.threads(16)
-    ref = OracleDecoder(bl, cfg, m, n_seq=1, quant_act=False)
-    refq = OracleDecoder(bl, cfg, m, n_seq=1, quant_act=True)
-    errs, errq, same = [], [], []
-    for step, t in enumerate((1000, 77, 151935, 9)):
-        eng.set_inputs(np.array([t], np.int32), np.array([step], np.int32))
-        eng.step(graph=True)
-        g = eng.logits(0)
-        lr, lq = ref.token(0, t), refq.token(0, t)
-        errs.append(rel_l2(g, lr))
-        errq.append(rel_l2(g, lq))
-        same.append((int(np.argmax(g)) == int(np.argmax(lr)), int(np.argmax(lq)) == int(np.argmax(lr))))
+    toks = (1000, 77, 151935, 9, 40000, 123)
+    ref = OracleDecoder(bl, cfg, m, n_seq=1, quant_act=0)
+    ref2 = OracleDecoder(bl, cfg, m, n_seq=1, quant_act=2)
+    scalar = OracleDecoder(oc, cfg, m, n_seq=1, quant_act=0)
+
+    def run(pieces):
+        eng.set_act_pieces(pieces)
+        eng.reset()
+        out = []
+        for step, t in enumerate(toks):
+            eng.set_inputs(np.array([t], np.int32), np.array([step], np.int32))
+            eng.step(graph=True)
+            out.append(eng.logits(0))
+        return out
+    g2, g1 = run(2), run(1)
     eng.close()
-    print("4B logits rel_l2 vs fp32-activation reference:", " ".join(f"{e:.2e}" for e in errs))
-    print("4B logits rel_l2 vs oracle with quantized activations:", " ".join(f"{e:.2e}" for e in errq))
-    print("greedy token equal to the fp32 reference's (GPU, quantized oracle):", same)
-    # a report, not a parity bar (the per-operation test is): the logits must still be the same function
-    assert max(errs) < 0.5 and max(errq) < max(errs)
+    errs, errq, spread, err1, agree = [], [], [], [], []
+    for step, t in enumerate(toks):
+        lr, lq, ls = ref.token(0, t), ref2.token(0, t), scalar.token(0, t)
+        errs.append(rel_l2(g2[step], lr))
+        errq.append(rel_l2(g2[step], lq))
+        spread.append(rel_l2(ls, lr))
+        err1.append(rel_l2(g1[step], lr))
+        top2 = np.sort(lr)[-2:]
+        clear = top2[1] - top2[0] > 2.0 * np.abs(g1[step] - lr).max()
+        agree.append((bool(clear), int(np.argmax(g2[step])) == int(np.argmax(lr))))
+    print("4B logits rel_l2 vs fp32 reference, two pieces:", " ".join(f"{e:.2e}" for e in errs))
+    print("4B logits rel_l2 vs fp32 reference, one piece: ", " ".join(f"{e:.2e}" for e in err1))
+    print("reference scalar order vs AVX2 order:          ", " ".join(f"{e:.2e}" for e in spread))
+    print("4B logits rel_l2 vs the oracle's two-piece decoder:", " ".join(f"{e:.2e}" for e in errq))
+    print("(clear top-2 margin, greedy token equal):", agree)
+    assert max(errs) < 4.0 * max(spread) and max(errs) < 3e-2
+    assert max(errq) < 4.0 * max(spread)
+    assert max(errs) * 5 < min(err1)  # the second piece removes most of the one-piece deviation
+    assert all(eq for clear, eq in agree if clear)
 
 
 def test_decoder_graph_replay_matches_eager():
@@ -230,17 +251,16 @@ def test_queued_inputs_match_synchronous_feeding():
 
 def test_mixed_formats_end_to_end_matches_oracle_decoder(oc):
     """The mixed-format small model, one sequence, 8 greedy steps on the GPU
-    graph and on the oracle's decoder (int8 activations, the same per-tensor
-    formats): logits within 1e-3 relative L2 at every step (measured
-    <= 4e-7: no int8 activation of this trajectory sits on a rounding
-    boundary; per-operation parity is the gate for every operation)."""
+    graph and on the oracle's decoder (two-piece int8 activations, the same
+    per-tensor formats): logits within 1e-3 relative L2 at every step
+    (per-operation parity is the gate for every operation)."""
     from echohip.engine import Engine
     cfg = small_config(max_batch=1, max_ctx=16)
     m = make_model(cfg, seed=31, fmts=MIXED_FMTS)
     eng = Engine(cfg)
     upload(eng, m)
     eng.reset()
-    dec = OracleDecoder(oc, cfg, m, n_seq=1, quant_act=True)
+    dec = OracleDecoder(oc, cfg, m, n_seq=1, quant_act=2)
     tok = 77
     errs = []
     for p in range(8):

@@ -179,7 +179,7 @@ def test_gguf_mixed_formats_load_matches_upload_and_oracle(tmp_path, oc):
         for x, y in zip(sa, sb):
             assert np.array_equal(x, y)
     # sequence 0 of _decode against the oracle decoder (5, then greedy)
-    dec = OracleDecoder(oc, cfg, m, n_seq=1, quant_act=True)
+    dec = OracleDecoder(oc, cfg, m, n_seq=1, quant_act=2)  # the engine's two-piece activations
     tok, errs = 5, []
     for step in range(len(la)):
         ref = dec.token(0, tok)

@@ -6,7 +6,9 @@
 * The fp32 row ops equal their formulas (engine.zig:783-792, core/math.zig:35-37,
   qwen_linear.zig:252-257) to fp32 rounding.
 * A prefilled sequence matches the same prompt fed through the decode graph
-  one token per step.  This is a consistency check of two GPU paths; parity
+  one token per step, both engines with one-piece activations (the prefill
+  GEMMs' arithmetic; the decode step's default second piece would add its own
+  difference).  This is a consistency check of two GPU paths; parity
   with the oracle is established per operation for both
   (tests/test_gpu_prefill_ops.py, tests/test_gpu_decoder.py, 1e-5 per op).
   The two paths differ only in fp32 summation order (int8-MFMA GEMM vs
@@ -173,6 +175,8 @@ def test_prefill_matches_token_loop(lens, fmts):
     a, b = Engine(cfg), Engine(cfg)
     upload(a, m)
     upload(b, m)
+    a.set_act_pieces(1)
+    b.set_act_pieces(1)
     a.reset()
     b.reset()
     for s, p in enumerate(prompts):
@@ -277,15 +281,18 @@ def test_prefill_rejects_bad_arguments():
 @pytest.mark.parametrize("fmts", [None, MIXED_FMTS], ids=["q8_0", "mixed"])
 def test_prefill_one_token_is_the_decode_step(fmts):
     """A one-token prompt: the GEMM path and the decode graph agree to fp32
-    rounding.  A Q4_K product is the difference of two terms (d*sc*isum and
-    dmin*m*xsum, each larger than the result) that the GEMM and the matvec
-    round in different groupings, so the mixed model's bound is 1e-4."""
+    rounding (both with one-piece activations, the GEMMs' arithmetic).  A Q4_K
+    product is the difference of two terms (d*sc*isum and dmin*m*xsum, each
+    larger than the result) that the GEMM and the matvec round in different
+    groupings, so the mixed model's bound is 1e-4."""
     from echohip.engine import Engine
     cfg = small_config(max_batch=2, max_ctx=16)
     m = make_model(cfg, seed=23, fmts=fmts)
     a, b = Engine(cfg), Engine(cfg)
     upload(a, m)
     upload(b, m)
+    a.set_act_pieces(1)
+    b.set_act_pieces(1)
     a.reset()
     b.reset()
     a.prefill(1, [417], 0)
