@@ -177,10 +177,11 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm_quant(const float* __restri
     store_act_q8_lane(xk * inv * wk, act, (float*)(act + xd_off), M, Kp / 32, i, k, P);
 }
 
-// Row variant: grid (M), block Kp/4 threads (Kp <= 4096), thread = 4
-// consecutive elements (one float4 of x and of each partial); the row is read
-// once.  Eight lanes form one Q8_0 block (max over 8 lanes), each stores its
-// 4 quantized bytes (per piece) as one word.
+// Row variant: grid (M), block Kp/4 threads rounded up to whole waves (Kp <=
+// 4096), thread = 4 consecutive elements (one float4 of x and of each
+// partial); the row is read once.  Eight lanes form one Q8_0 block (max over
+// 8 lanes), each stores its 4 quantized bytes (per piece) as one word; the
+// threads past Kp/4 only add zeros to the sum.
 template <int NP>
 __global__ __launch_bounds__(1024) void k_add_rmsnorm_quant_row(const float* __restrict__ x,
                                                                const float* __restrict__ parts,
@@ -209,6 +210,7 @@ __global__ __launch_bounds__(1024) void k_add_rmsnorm_quant_row(const float* __r
     float tot = 0.0f;
     for (uint32_t v = 0; v < blockDim.x / 64; ++v) tot += sh[v];
     const float inv = 1.0f / sqrtf(tot / (float)H + 1e-6f);
+    if (k >= Kp) return;  // whole 8-lane blocks (Kp % 32 == 0)
     const float v0 = a.x * inv * wk.x, v1 = a.y * inv * wk.y, v2 = a.z * inv * wk.z, v3 = a.w * inv * wk.w;
     float amax = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
     amax = fmaxf(amax, lane_xor<1>(amax));
@@ -835,7 +837,7 @@ extern "C" int ec_glue_add_rmsnorm_quant_pieces(const float* x, const float* par
     // one workgroup per row where it fits (rows up to 4096, 16-byte aligned rows): 2560-wide rows
     // 3.9 -> ~3.5 us per call in the decode step; otherwise row-parallel blocks
     if (nparts <= 4 && L.Kp <= 4096 && H % 4 == 0 && ((uintptr_t)x_out & 15) == 0 && ((uintptr_t)w & 15) == 0) {
-        const dim3 g1(M), b1(L.Kp / 4);
+        const dim3 g1(M), b1(round_up(L.Kp / 4, 64));  // whole waves: the sum adds every wave's part
         switch (nparts) {
             case 1: EC_GLUE_LAUNCH(k_add_rmsnorm_quant_row<1>, g1, b1, 0, st, x, parts, x_out, w, a, M, H, xo, P);
             case 2: EC_GLUE_LAUNCH(k_add_rmsnorm_quant_row<2>, g1, b1, 0, st, x, parts, x_out, w, a, M, H, xo, P);

@@ -55,34 +55,42 @@ __device__ __forceinline__ uint32_t out_token(uint32_t g, uint32_t r) {
     return P == 1 ? 4 * g + r : 8 * (r >> 1) + 2 * g + (r & 1);
 }
 
-// Cross-wave reduction of acc[4] and the store of y / accumulate.  Each
-// wave parks its partials in LDS; then thread s (s < 256) sums slot s over the
-// waves in wave order (deterministic) and stores it: slot s = lane*4 + r, i.e.
-// weight row 16t + lane%16, token out_token(lane/16, r).
-template <int R, int P>
-__device__ __forceinline__ void reduce_store(float (&acc)[4], float* red, float* __restrict__ y, uint32_t t,
+// Cross-wave reduction of the TPW tiles' acc[4] and the store of y /
+// accumulate.  Each wave parks its partials in LDS (red: [TPW][waves][256]);
+// then thread s (s < TPW*256) sums slot s%256 of tile s/256 over the waves in
+// wave order (deterministic) and stores it: slot = lane*4 + r, i.e. weight row
+// 16(t0 + tile) + lane%16, token out_token(lane/16, r).
+template <int R, int P, int TPW>
+__device__ __forceinline__ void reduce_store(float (&acc)[TPW][4], float* red, float* __restrict__ y, uint32_t t0,
                                              uint32_t M, uint32_t N, uint32_t ldy, int accumulate) {
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     if (nw == 1) {
-        const uint32_t row = lane & 15, g = lane >> 4, n = 16 * t + row;
-        if (n >= N) return;
-        for (int r = 0; r < R; ++r) {
-            const uint32_t m = out_token<P>(g, r);
-            if (m < M) {
-                float* dst = y + (size_t)m * ldy + n;
-                *dst = accumulate ? *dst + acc[r] : acc[r];
+        const uint32_t row = lane & 15, g = lane >> 4;
+#pragma unroll
+        for (int tt = 0; tt < TPW; ++tt) {
+            const uint32_t n = 16 * (t0 + tt) + row;
+            if (n >= N) continue;
+            for (int r = 0; r < R; ++r) {
+                const uint32_t m = out_token<P>(g, r);
+                if (m < M) {
+                    float* dst = y + (size_t)m * ldy + n;
+                    *dst = accumulate ? *dst + acc[tt][r] : acc[tt][r];
+                }
             }
         }
         return;
     }
-    for (int r = 0; r < R; ++r) red[(w * 64 + lane) * 4 + r] = acc[r];
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt)
+        for (int r = 0; r < R; ++r) red[((tt * nw + w) * 64 + lane) * 4 + r] = acc[tt][r];
     __syncthreads();
-    for (uint32_t sl = threadIdx.x; sl < 256; sl += blockDim.x) {  // slot = lane' * 4 + r'
-        const uint32_t ln = sl >> 2, r = sl & 3;
-        const uint32_t m = out_token<P>(ln >> 4, r), n = 16 * t + (ln & 15);
+    for (uint32_t q = threadIdx.x; q < 256 * TPW; q += blockDim.x) {  // tile q/256, slot lane' * 4 + r'
+        const uint32_t tt = q >> 8, sl = q & 255, ln = sl >> 2, r = sl & 3;
+        const uint32_t m = out_token<P>(ln >> 4, r), n = 16 * (t0 + tt) + (ln & 15);
         if ((int)r >= R || m >= M || n >= N) continue;
-        float s = red[sl];
-        for (uint32_t v = 1; v < nw; ++v) s += red[v * 256 + sl];
+        const float* rt = red + (size_t)tt * nw * 256;
+        float s = rt[sl];
+        for (uint32_t v = 1; v < nw; ++v) s += rt[v * 256 + sl];
         float* dst = y + (size_t)m * ldy + n;
         *dst = accumulate ? *dst + s : s;
     }
@@ -163,15 +171,20 @@ struct ByteStage {
 };
 
 // --------------------------------------------------------------------- Q8_0
-// One wave's share of 16-row tile t: chunks gbeg, gbeg+1, ... (GPW per pass,
-// passes gstep apart), accumulated into acc (one value per naccs slot).
-// xs / as: the wave's LDS slice for staged scales and activation bytes.
-// P = 2: the activation holds 2M layout rows (two pieces per token).
-template <int MT, int P, bool DOTS, int GPW>
-__device__ __forceinline__ void q8_0_wave(const uint8_t* __restrict__ wt, const uint8_t* __restrict__ act,
-                                          int32_t* __restrict__ dots, uint32_t t, uint32_t M, uint32_t N, uint32_t K,
-                                          uint32_t nG, uint32_t xd_off, uint32_t gbeg, uint32_t gstep, uint32_t gend,
-                                          float* xs, uint8_t* as, float (&acc)[4]) {
+// One wave's share of the TPW 16-row tiles t0 .. t0+TPW-1 (tile t0 + tt at
+// wt + tt*tstride; an index past the last tile reads tile t0 and is not
+// stored): chunks gbeg, gbeg+1, ... (GPW per pass, passes gstep apart),
+// accumulated into acc[tt] (one value per naccs slot).  Every staged
+// activation chunk serves the TPW tiles' weights (TPW = 2 halves the
+// activation bytes per weight byte).  xs / as: the wave's LDS slice for
+// staged scales and activation bytes.  P = 2: the activation holds 2M layout
+// rows (two pieces per token).
+template <int MT, int P, bool DOTS, int GPW, int TPW>
+__device__ __forceinline__ void q8_0_wave(const uint8_t* __restrict__ wt, size_t tstride,
+                                          const uint8_t* __restrict__ act, int32_t* __restrict__ dots, uint32_t t0,
+                                          uint32_t M, uint32_t N, uint32_t K, uint32_t nG, uint32_t xd_off,
+                                          uint32_t gbeg, uint32_t gstep, uint32_t gend, float* xs, uint8_t* as,
+                                          float (&acc)[TPW][4]) {
     constexpr int R = naccs<MT, P>();
     constexpr int S = slots<MT>();
     constexpr int NA = ngroups<MT, P>();
@@ -185,15 +198,18 @@ __device__ __forceinline__ void q8_0_wave(const uint8_t* __restrict__ wt, const 
         ByteStage<ACT_MAX> ast;
         if constexpr (!DOTS) sc.load((const float*)(act + xd_off), nG * 4, 4 * G0, M, lane);
         ast.load(act, (size_t)G0 * 128 * VR, (size_t)GPW * 128 * VR, act_bytes, lane);
-        uint4 b01[GPW], b23[GPW];
-        uint2 dw[GPW];
+        uint4 b01[GPW][TPW], b23[GPW][TPW];
+        uint2 dw[GPW][TPW];
 #pragma unroll
         for (int u = 0; u < GPW; ++u) {
             const uint32_t G = min(G0 + u, gend - 1);
-            const uint8_t* ch = wt + (size_t)G * kQ8TChunk;
-            b01[u] = ld_stream16(ch + lane * 16);
-            b23[u] = ld_stream16(ch + 1024 + lane * 16);
-            dw[u] = ld_stream8(ch + 2048 + row * 8);
+#pragma unroll
+            for (int tt = 0; tt < TPW; ++tt) {
+                const uint8_t* ch = wt + tt * tstride + (size_t)G * kQ8TChunk;
+                b01[u][tt] = ld_stream16(ch + lane * 16);
+                b23[u][tt] = ld_stream16(ch + 1024 + lane * 16);
+                dw[u][tt] = ld_stream8(ch + 2048 + row * 8);
+            }
         }
         if constexpr (!DOTS) sc.store(xs, lane);
         ast.store(as, (size_t)GPW * 128 * VR, lane);
@@ -214,10 +230,13 @@ __device__ __forceinline__ void q8_0_wave(const uint8_t* __restrict__ wt, const 
                 A[a][2] = aval ? pack2(a23.x, a23.y) : 0l;
                 A[a][3] = aval ? pack2(a23.z, a23.w) : 0l;
             }
-            const long B[4] = {pack2(b01[u].x, b01[u].y), pack2(b01[u].z, b01[u].w), pack2(b23[u].x, b23[u].y),
-                               pack2(b23[u].z, b23[u].w)};
-            const float dwf[4] = {h2f(dw[u].x & 0xFFFF), h2f(dw[u].x >> 16), h2f(dw[u].y & 0xFFFF),
-                                  h2f(dw[u].y >> 16)};
+#pragma unroll
+            for (int tt = 0; tt < TPW; ++tt) {
+            const long B[4] = {pack2(b01[u][tt].x, b01[u][tt].y), pack2(b01[u][tt].z, b01[u][tt].w),
+                               pack2(b23[u][tt].x, b23[u][tt].y), pack2(b23[u][tt].z, b23[u][tt].w)};
+            const float dwf[4] = {h2f(dw[u][tt].x & 0xFFFF), h2f(dw[u][tt].x >> 16), h2f(dw[u][tt].y & 0xFFFF),
+                                  h2f(dw[u][tt].y >> 16)};
+            float(&ac)[4] = acc[tt];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 v4i cc[NA];
@@ -225,7 +244,7 @@ __device__ __forceinline__ void q8_0_wave(const uint8_t* __restrict__ wt, const 
                 for (int a = 0; a < NA; ++a) cc[a] = mfma_i8(A[a][j], B[j]);
                 const uint32_t b = 4 * G + j;
                 if constexpr (DOTS) {
-                    const uint32_t n = 16 * t + row, nb = K / 32;
+                    const uint32_t n = 16 * (t0 + tt) + row, nb = K / 32;
                     if (n < N && b < nb)
                         for (int a = 0; a < NA; ++a)
                             for (int r = 0; r < 4; ++r) {
@@ -233,25 +252,26 @@ __device__ __forceinline__ void q8_0_wave(const uint8_t* __restrict__ wt, const 
                                 if (vr < VR) dots[((size_t)vr * N + n) * nb + b] = cc[a][r];
                             }
                 } else if constexpr (MT == 1 && P == 1) {
-                    acc[0] = fmaf((float)cc[0][0], dwf[j] * xs[4 * u + j], acc[0]);
+                    ac[0] = fmaf((float)cc[0][0], dwf[j] * xs[4 * u + j], ac[0]);
                 } else if constexpr (MT == 1) {  // P = 2: D rows 0, 1 of lanes 0-15
-                    acc[0] = fmaf((float)(cc[0][0] * 256 + cc[0][1]), dwf[j] * xs[4 * u + j], acc[0]);
+                    ac[0] = fmaf((float)(cc[0][0] * 256 + cc[0][1]), dwf[j] * xs[4 * u + j], ac[0]);
                 } else if constexpr (P == 1) {
                     const float4 dx =
                         (4 * g < S) ? *(const float4*)(xs + (4 * u + j) * S + 4 * g) : make_float4(0.f, 0.f, 0.f, 0.f);
                     const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
 #pragma unroll
-                    for (int r = 0; r < R; ++r) acc[r] = fmaf((float)cc[0][r], dwf[j] * dxv[r], acc[r]);
+                    for (int r = 0; r < R; ++r) ac[r] = fmaf((float)cc[0][r], dwf[j] * dxv[r], ac[r]);
                 } else {
 #pragma unroll
                     for (int a = 0; a < NA; ++a) {
-                        const uint32_t t0 = 8 * a + 2 * g;  // tokens t0, t0 + 1 (scales pre-divided by 256)
+                        const uint32_t tk = 8 * a + 2 * g;  // tokens tk, tk + 1 (scales pre-divided by 256)
                         const float2 dx =
-                            (t0 < (uint32_t)S) ? *(const float2*)(xs + (4 * u + j) * S + t0) : make_float2(0.f, 0.f);
-                        acc[2 * a] = fmaf((float)(cc[a][0] * 256 + cc[a][1]), dwf[j] * dx.x, acc[2 * a]);
-                        acc[2 * a + 1] = fmaf((float)(cc[a][2] * 256 + cc[a][3]), dwf[j] * dx.y, acc[2 * a + 1]);
+                            (tk < (uint32_t)S) ? *(const float2*)(xs + (4 * u + j) * S + tk) : make_float2(0.f, 0.f);
+                        ac[2 * a] = fmaf((float)(cc[a][0] * 256 + cc[a][1]), dwf[j] * dx.x, ac[2 * a]);
+                        ac[2 * a + 1] = fmaf((float)(cc[a][2] * 256 + cc[a][3]), dwf[j] * dx.y, ac[2 * a + 1]);
                     }
                 }
+            }
             }
         }
     }
@@ -261,28 +281,31 @@ __device__ __forceinline__ void q8_0_wave(const uint8_t* __restrict__ wt, const 
 template <int MT, int P, int GPW>
 constexpr uint32_t q8_wave_lds() { return 4 * GPW * slots<MT>() + GPW * 128 * lrows<MT, P>() / 4; }
 
-// grid = (16-row tiles, K splits): workgroup (t, sp) covers chunks
-// [sp*nG/ns, (sp+1)*nG/ns) of tile t (ns = gridDim.y), split over its nw
-// waves, and writes its sums to y + sp*split_stride (one partial result per
-// split; ns = 1: the whole K range).
-template <int MT, int P, bool DOTS, int GPW>
+// grid = (groups of TPW 16-row tiles, K splits): workgroup (b, sp) covers
+// chunks [sp*nG/ns, (sp+1)*nG/ns) of tiles TPW*b .. TPW*b+TPW-1 (ns =
+// gridDim.y), split over its nw waves, and writes its sums to y +
+// sp*split_stride (one partial result per split; ns = 1: the whole K range).
+template <int MT, int P, bool DOTS, int GPW, int TPW>
 __global__ __launch_bounds__(1024) void k_mv_q8_0(const uint8_t* __restrict__ W, const uint8_t* __restrict__ act,
                                                   float* __restrict__ y, int32_t* __restrict__ dots, uint32_t M,
                                                   uint32_t N, uint32_t K, uint32_t nG, uint32_t xd_off, uint32_t ldy,
                                                   int accumulate, size_t split_stride) {
     extern __shared__ float lds[];
     constexpr int R = naccs<MT, P>();
-    const uint32_t t = blockIdx.x, sp = blockIdx.y;
+    const uint32_t t0 = TPW * blockIdx.x, sp = blockIdx.y;
     const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t nw = blockDim.x >> 6;
     const uint32_t g0 = sp * nG / gridDim.y, g1 = (sp + 1) * nG / gridDim.y;
+    const uint32_t nT = (N + 15) / 16;
     float* red = lds;
-    float* xs = lds + nw * 256 + w * q8_wave_lds<MT, P, GPW>();
+    float* xs = lds + TPW * nw * 256 + w * q8_wave_lds<MT, P, GPW>();
     uint8_t* as = (uint8_t*)(xs + 4 * GPW * slots<MT>());
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    q8_0_wave<MT, P, DOTS, GPW>(W + (size_t)t * nG * kQ8TChunk, act, dots, t, M, N, K, nG, xd_off, g0 + w * GPW,
-                                nw * GPW, g1, xs, as, acc);
-    if constexpr (!DOTS) reduce_store<R, P>(acc, red, y + sp * split_stride, t, M, N, ldy, accumulate);
+    float acc[TPW][4] = {};
+    // a second tile past the last one reads the first (its rows are not stored)
+    const size_t tstride = TPW > 1 && t0 + 1 < nT ? (size_t)nG * kQ8TChunk : 0;
+    q8_0_wave<MT, P, DOTS, GPW, TPW>(W + (size_t)t0 * nG * kQ8TChunk, tstride, act, dots, t0, M, N, K, nG, xd_off,
+                                     g0 + w * GPW, nw * GPW, g1, xs, as, acc);
+    if constexpr (!DOTS) reduce_store<R, P, TPW>(acc, red, y + sp * split_stride, t0, M, N, ldy, accumulate);
 }
 
 // --------------------------------------------------------------------- Q4_K
@@ -330,7 +353,8 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
     const uint8_t* wt = W + (size_t)t * nB * kQ4TChunk;
     const uint32_t VR = P * M;  // layout rows
     const size_t act_bytes = (size_t)nB * 256 * VR;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float acc4[1][4] = {};
+    float(&acc)[4] = acc4[0];
 
     for (uint32_t B0 = w * GPW; B0 < nB; B0 += nw * GPW) {
         ScaleStage<NB, S, P == 2> sd;
@@ -436,7 +460,7 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
             }
         }
     }
-    if constexpr (!DOTS) reduce_store<R, P>(acc, red, y, t, M, N, ldy, accumulate);
+    if constexpr (!DOTS) reduce_store<R, P, 1>(acc4, red, y, t, M, N, ldy, accumulate);
 }
 
 // ------------------------------------------------ reference-semantics fp32 path
@@ -582,6 +606,21 @@ static uint32_t target_waves_q8() {
     }();
     return v;
 }
+// 16-row tiles per wave of the Q8_0 matvec (1, 2 or 4): with one activation
+// piece 1 (EC_MV_TPW_P1 overrides), with two 2 (EC_MV_TPW overrides).
+static uint32_t tpw_q8(int pieces) {
+    static uint32_t v[2] = {[] {
+                                const char* e = getenv("EC_MV_TPW_P1");
+                                const int t = e ? atoi(e) : 1;
+                                return t == 2 || t == 4 ? (uint32_t)t : 1u;
+                            }(),
+                            [] {
+                                const char* e = getenv("EC_MV_TPW");
+                                const int t = e ? atoi(e) : 2;
+                                return t == 1 || t == 4 ? (uint32_t)t : 2u;
+                            }()};
+    return v[pieces == 2];
+}
 static uint32_t target_waves_q4() {
     static uint32_t v = [] {
         const char* e = getenv("EC_MV_TARGET_WAVES_Q4");
@@ -606,18 +645,20 @@ static void plan(uint32_t n_tiles, uint32_t n_chunks, int max_gpw, int& gpw, uin
 // LDS per workgroup is 160 KB on gfx950: cap the waves of a workgroup so that
 // nw * (reduction slice + wave slice) fits (more passes per wave instead).
 constexpr size_t kLdsBytes = 160 * 1024;
-static uint32_t lds_cap_waves(uint32_t wave_floats) { return (uint32_t)(kLdsBytes / ((256 + wave_floats) * 4)); }
+static uint32_t lds_cap_waves(uint32_t wave_floats, uint32_t tpw = 1) {
+    return (uint32_t)(kLdsBytes / ((256 * tpw + wave_floats) * 4));
+}
 
-template <int MT, int P, bool DOTS, int GPW>
+template <int MT, int P, bool DOTS, int GPW, int TPW>
 static void launch_q8_g(const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N, uint32_t K,
                         uint32_t ldy, int accumulate, uint32_t nw, uint32_t nsplit, hipStream_t st) {
     const ActLayout L = act_layout(EC_Q8_0, P * M, K);
     const uint32_t nT = round_up(N, 16) / 16, nG = L.Kp / 128;
-    nw = min(nw, lds_cap_waves(q8_wave_lds<MT, P, GPW>()));
-    const size_t lds = ((size_t)nw * 256 + (size_t)nw * q8_wave_lds<MT, P, GPW>()) * sizeof(float);
-    hipLaunchKernelGGL((k_mv_q8_0<MT, P, DOTS, GPW>), dim3(nT, nsplit), dim3(64 * nw), lds, st, (const uint8_t*)W,
-                       (const uint8_t*)act, y, dots, M, N, K, nG, (uint32_t)L.xd_off, ldy, accumulate,
-                       (size_t)M * ldy);
+    nw = min(nw, lds_cap_waves(q8_wave_lds<MT, P, GPW>(), TPW));
+    const size_t lds = ((size_t)TPW * nw * 256 + (size_t)nw * q8_wave_lds<MT, P, GPW>()) * sizeof(float);
+    hipLaunchKernelGGL((k_mv_q8_0<MT, P, DOTS, GPW, TPW>), dim3((nT + TPW - 1) / TPW, nsplit), dim3(64 * nw), lds, st,
+                       (const uint8_t*)W, (const uint8_t*)act, y, dots, M, N, K, nG, (uint32_t)L.xd_off, ldy,
+                       accumulate, (size_t)M * ldy);
 }
 
 // nsplit > 1 (<= the 128-element chunks of K): the K range is cut into
@@ -630,14 +671,33 @@ static void launch_q8(const void* W, const void* act, float* y, int32_t* dots, u
     const uint32_t cps = (nG + nsplit - 1) / nsplit;  // longest range
     int gpw;
     uint32_t nw;
-    // GPW <= 5 (3 for 32 layout rows: 16 tokens in two pieces): every variant under 128 VGPRs, no spills
-    plan(nT * nsplit, cps, (MT == 16 && P == 2) ? 3 : 5, gpw, nw, target_waves_q8());
+    // GPW <= 5 (two pieces: 4, and 3 for 16 tokens): every variant under 128 VGPRs, no spills
+    constexpr int max_gpw = P == 1 || MT == 1 ? 5 : (MT == 16 ? 3 : 4);
+    plan(nT * nsplit, cps, max_gpw, gpw, nw, target_waves_q8());
+    // several tiles per wave: each staged activation chunk serves 16*tpw weight rows (with two pieces
+    // the activation bytes of one tile equal its weight bytes), with 1/tpw of the chunks per pass, so a
+    // wave streams about the same weight bytes per pass
+    const uint32_t tpw = tpw_q8(P);
+    if (tpw == 2) {
+        const int g2 = (gpw + 1) / 2;
+        const uint32_t nw2 = min((cps + g2 - 1) / g2, 16u);
+        switch (g2) {
+            case 1: launch_q8_g<MT, P, DOTS, 1, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw2, nsplit, st); break;
+            default: launch_q8_g<MT, P, DOTS, 2, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw2, nsplit, st); break;
+        }
+        return;
+    }
+    if (tpw == 4) {
+        const uint32_t nw4 = min(cps, 16u);
+        launch_q8_g<MT, P, DOTS, 1, 4>(W, act, y, dots, M, N, K, ldy, accumulate, nw4, nsplit, st);
+        return;
+    }
     switch (gpw) {
-        case 1: launch_q8_g<MT, P, DOTS, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
-        case 2: launch_q8_g<MT, P, DOTS, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
-        case 3: launch_q8_g<MT, P, DOTS, 3>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
-        case 4: launch_q8_g<MT, P, DOTS, 4>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
-        default: launch_q8_g<MT, P, DOTS, 5>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
+        case 1: launch_q8_g<MT, P, DOTS, 1, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
+        case 2: launch_q8_g<MT, P, DOTS, 2, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
+        case 3: launch_q8_g<MT, P, DOTS, 3, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
+        case 4: launch_q8_g<MT, P, DOTS, 4, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
+        default: launch_q8_g<MT, P, DOTS, 5, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, nsplit, st); break;
     }
 }
 

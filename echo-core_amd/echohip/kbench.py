@@ -52,8 +52,9 @@ def _events_mean_us(launch, n_copies, iters, replays=5):
     return float(np.mean(t)), float(np.min(t))
 
 
-def matvec_case(hip, fmt, N, K, M=1, iters=200, seed=0):
-    """Decode matvec y = W x over a rotation of weight copies."""
+def matvec_case(hip, fmt, N, K, M=1, iters=200, seed=0, pieces=1, nsplit=1):
+    """Decode matvec y = W x over a rotation of weight copies; `pieces` int8
+    pieces per activation element, nsplit > 1: the split-K form (partial sums)."""
     st = torch.cuda.current_stream().cuda_stream
     if fmt == L.Q8_0:
         wbytes = N * K // 32 * 34
@@ -70,20 +71,23 @@ def matvec_case(hip, fmt, N, K, M=1, iters=200, seed=0):
         tiled[i].copy_(tiled[0])
     del Wd
     x = torch.from_numpy(synth.activations(seed + 1, M * K)).cuda()
-    act = torch.empty(hip.act_bytes(fmt, M, K), dtype=torch.uint8, device="cuda")
-    hip.quantize_act(fmt, x, act, M, K, stream=st)
-    y = torch.empty(M * N, dtype=torch.float32, device="cuda")
+    act = torch.empty(hip.act_bytes(fmt, M, K, pieces=pieces), dtype=torch.uint8, device="cuda")
+    hip.quantize_act(fmt, x, act, M, K, stream=st, pieces=pieces)
+    y = torch.empty(nsplit * M * N, dtype=torch.float32, device="cuda")
 
     def launch(i, stream):
-        hip.matvec(fmt, tiled[i], act, y, M, N, K, stream=stream)
+        if nsplit > 1:
+            hip.matvec_split(fmt, tiled[i], act, y, M, N, K, nsplit, stream=stream, pieces=pieces)
+        else:
+            hip.matvec(fmt, tiled[i], act, y, M, N, K, stream=stream, pieces=pieces)
 
     mean_us, med_us = _events_mean_us(launch, n_copies, iters)
-    x_bytes = M * (K + K // 32 * 4 * (2 if fmt == L.Q4_K else 1))
+    x_bytes = M * (pieces * K + K // 32 * 4 * (2 if fmt == L.Q4_K else 1))
     alg = wbytes + x_bytes + M * N * 4
     gbs = alg / (mean_us * 1e-6) / 1e9
     del tiled
     torch.cuda.empty_cache()
-    return {"kernel": "k_mv_q8_0" if fmt == L.Q8_0 else "k_mv_q4_K", "M": M, "N": N, "K": K,
+    return {"kernel": "k_mv_q8_0" if fmt == L.Q8_0 else "k_mv_q4_K", "M": M, "N": N, "K": K, "pieces": pieces,
             "bytes": alg, "us": round(mean_us, 3), "us_best": round(med_us, 3), "GBs": round(gbs, 1),
             "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": n_copies}
 
@@ -446,6 +450,29 @@ def pmc_cases(hip, which):
             hip.attn_prefill(q, keys, vals, ks, vs, out, T, pos0, n_heads, n_kv, hd, max_ctx, ws=ws, stream=st)
             torch.cuda.synchronize()
         del keys, vals, ks, vs, q, out
+        torch.cuda.empty_cache()
+    elif which == "pieces":
+        # the decode step's gate/up projection (18432 x 2560, 3 K-splits) at M = 8 with one, then two
+        # activation pieces
+        N, K, M, ns = 18432, 2560, 8, 3
+        Wd = torch.empty(N * K // 32 * 34, dtype=torch.uint8, device="cuda")
+        hip.fill_random(1, Wd, N * K // 32, 0, 0.02, stream=st)
+        tb = hip.tiled_bytes(L.Q8_0, N, K)
+        n_copies = max(PMC_LAUNCHES, math.ceil(ROTATE_BYTES / tb) + 1)
+        tiled = torch.empty((n_copies, tb), dtype=torch.uint8, device="cuda")
+        hip.repack(L.Q8_0, Wd, tiled[0], N, K, stream=st)
+        for i in range(1, n_copies):
+            tiled[i].copy_(tiled[0])
+        x = torch.from_numpy(synth.activations(1, M * K)).cuda()
+        y = torch.empty(ns * M * N, dtype=torch.float32, device="cuda")
+        for pieces in (1, 2):
+            act = torch.empty(hip.act_bytes(L.Q8_0, M, K, pieces=pieces), dtype=torch.uint8, device="cuda")
+            hip.quantize_act(L.Q8_0, x, act, M, K, stream=st, pieces=pieces)
+            torch.cuda.synchronize()
+            for i in range(PMC_LAUNCHES):
+                hip.matvec_split(L.Q8_0, tiled[(i * 7919) % n_copies], act, y, M, N, K, ns, stream=st, pieces=pieces)
+                torch.cuda.synchronize()
+        del tiled
         torch.cuda.empty_cache()
     elif which == "matvec":
         for fmt, N, K in ((L.Q8_0, 9216, 2560), (L.Q4_K, 9216, 2560), (L.Q4_K, 2560, 9216)):
