@@ -22,6 +22,7 @@
 // 2^19: no int32 overflow), one conversion and one FMA with d_w * d_x / 256.
 #include "common.hpp"
 #include "layout.hpp"
+#include <cstring>
 
 namespace ec {
 
@@ -621,6 +622,15 @@ static uint32_t tpw_q8(int pieces) {
                             }()};
     return v[pieces == 2];
 }
+// Two tiles per wave with the one-tile plan's chunks per pass (EC_MV_TPW_GPW=full;
+// default: half of them, so a wave streams the one-tile plan's weight bytes).
+static bool tpw_full_gpw() {
+    static bool v = [] {
+        const char* e = getenv("EC_MV_TPW_GPW");
+        return e && strcmp(e, "full") == 0;
+    }();
+    return v;
+}
 static uint32_t target_waves_q4() {
     static uint32_t v = [] {
         const char* e = getenv("EC_MV_TARGET_WAVES_Q4");
@@ -679,7 +689,7 @@ static void launch_q8(const void* W, const void* act, float* y, int32_t* dots, u
     // wave streams about the same weight bytes per pass
     const uint32_t tpw = tpw_q8(P);
     if (tpw == 2) {
-        const int g2 = (gpw + 1) / 2;
+        const int g2 = tpw_full_gpw() ? gpw : (gpw + 1) / 2;
         const uint32_t nw2 = min((cps + g2 - 1) / g2, 16u);
         switch (g2) {
             case 1: launch_q8_g<MT, P, DOTS, 1, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw2, nsplit, st); break;

@@ -260,22 +260,25 @@ uint32_t resid_split(uint32_t N, uint32_t K, int fmt = EC_Q8_0) {
 
 // K splits of the input projection of a delta-net block and of gate/up
 // (their consumers, the fused delta step and SwiGLU, add the partial sums).
-// Decode step on MI355X (4B-class, batch 8, ~12k matvec waves per launch):
-// best at 2 and 2 (EC_IN_SPLIT / EC_GU_SPLIT override).
+// Decode step on MI355X (4B-class, batch 8, ~12k matvec waves per launch),
+// one activation piece: best at 2 and 3; two pieces (two tiles per matvec
+// wave): 1 and 4 (EC_IN_SPLIT / EC_GU_SPLIT override both).
 uint32_t env_split(const char* name, uint32_t dflt) {
     const char* v = getenv(name);
     return std::clamp(v ? (uint32_t)atoi(v) : dflt, 1u, kMaxResidSplit);
 }
-uint32_t in_split() {
-    static const uint32_t v = env_split("EC_IN_SPLIT", 2);
-    return v;
+// two pieces, batch 8: 1 / 2 / 3 splits 4497 / 4482 / 4476 tok/s
+uint32_t in_split(uint32_t pieces) {
+    static const uint32_t v[2] = {env_split("EC_IN_SPLIT", 2), env_split("EC_IN_SPLIT", 1)};
+    return v[pieces == 2];
 }
 // gate/up (18432 x 2560), partials added by SwiGLU.  Decode batch 8 on MI355X
-// with the other splits at their defaults: 2 / 3 / 4 / 5 / 6 splits
-// 4632 / 4645 / 4604 / 4612 / 4553 tok/s.
-uint32_t gu_split() {
-    static const uint32_t v = env_split("EC_GU_SPLIT", 3);
-    return v;
+// with the other splits at their defaults, one piece: 2 / 3 / 4 / 5 / 6 splits
+// 4632 / 4645 / 4604 / 4612 / 4553 tok/s; two pieces: 2 / 3 / 4 splits
+// 4458 / 4482 / 4491 (4519 with the input projection unsplit).
+uint32_t gu_split(uint32_t pieces) {
+    static const uint32_t v[2] = {env_split("EC_GU_SPLIT", 3), env_split("EC_GU_SPLIT", 4)};
+    return v[pieces == 2];
 }
 // attention input projection (q|k|v, 6144 x 2560), partials added by the rope
 // kernel.  Decode batch 8 on MI355X: 1 / 2 / 3 / 4 / 5 / 6 / 8 splits
@@ -366,7 +369,7 @@ int record_step(ec_engine* e) {
         EC_TRY(norm(y.attn_norm, li, q4(y.w_in)));
         if (!y.attn) {
             const uint32_t Nin = e->nin_delta;
-            const uint32_t nsi = split_count(y.w_in, in_split());
+            const uint32_t nsi = split_count(y.w_in, in_split(e->P));
             EC_MV(EC_OP_MV_IN, li, nsi, aid(y.w_in, EC_B_ACT_H, EC_B_ACT4_H),
                   mv_split(e, y.w_in, ain(y.w_in, e->act_h, e->act4_h), e->proj, nsi));
             // conv + gates + delta rule + gated norm + quantize in one launch
@@ -424,7 +427,7 @@ int record_step(ec_engine* e) {
         EC_TRY(norm(y.ffn_norm, li, q4(y.w_gu)));
         const bool d4 = q4(y.w_down);
         // a Q4_K down projection reads SwiGLU rows, which take one gate/up part
-        const uint32_t nsg = d4 ? 1u : split_count(y.w_gu, gu_split());
+        const uint32_t nsg = d4 ? 1u : split_count(y.w_gu, gu_split(e->P));
         EC_MV(EC_OP_MV_GU, li, nsg, aid(y.w_gu, EC_B_ACT_H, EC_B_ACT4_H),
               mv_split(e, y.w_gu, ain(y.w_gu, e->act_h, e->act4_h), e->gu, nsg));
         if (d4) {

@@ -154,7 +154,9 @@ def test_decoder_4b_end_to_end_vs_fp32_reference(oc):
     the same tokens: with random weights the 32 blocks amplify any per-matvec difference ~10^4-fold (a 4e-7
     summation-order difference becomes ~4e-3 in the logits), so the bound is held relative to that spread.
     Greedy tokens must agree wherever the reference's top-2 margin exceeds twice the largest logit difference
-    the one-piece path shows (a clear margin)."""
+    between the reference's own two orders (a margin the reference itself does not blur).  Measured on
+    MI355X: two pieces 6.1e-3 .. 9.2e-3, the reference's spread 3.7e-3 .. 5.4e-3, one piece 0.19 .. 0.20;
+    greedy tokens equal at all six steps."""
     from echohip.engine import Engine, EngineConfig
     from oracle import Baseline
     cfg = EngineConfig(max_batch=1, max_ctx=16)
@@ -187,7 +189,7 @@ def test_decoder_4b_end_to_end_vs_fp32_reference(oc):
         spread.append(rel_l2(ls, lr))
         err1.append(rel_l2(g1[step], lr))
         top2 = np.sort(lr)[-2:]
-        clear = top2[1] - top2[0] > 2.0 * np.abs(g1[step] - lr).max()
+        clear = top2[1] - top2[0] > 2.0 * np.abs(ls - lr).max()
         agree.append((bool(clear), int(np.argmax(g2[step])) == int(np.argmax(lr))))
     print("4B logits rel_l2 vs fp32 reference, two pieces:", " ".join(f"{e:.2e}" for e in errs))
     print("4B logits rel_l2 vs fp32 reference, one piece: ", " ".join(f"{e:.2e}" for e in err1))
