@@ -681,15 +681,16 @@ static void launch_q8(const void* W, const void* act, float* y, int32_t* dots, u
     const uint32_t cps = (nG + nsplit - 1) / nsplit;  // longest range
     int gpw;
     uint32_t nw;
-    // GPW <= 5 (two pieces: 4, and 3 for 16 tokens): every variant under 128 VGPRs, no spills
-    constexpr int max_gpw = P == 1 || MT == 1 ? 5 : (MT == 16 ? 3 : 4);
-    plan(nT * nsplit, cps, max_gpw, gpw, nw, target_waves_q8());
     // several tiles per wave: each staged activation chunk serves 16*tpw weight rows (with two pieces
     // the activation bytes of one tile equal its weight bytes), with 1/tpw of the chunks per pass, so a
-    // wave streams about the same weight bytes per pass
+    // wave streams about the same weight bytes per pass.  GPW <= 5 (two pieces: 4, and 3 for 16 tokens;
+    // two tiles: 2): every variant under 128 VGPRs, no spills (two tiles with 3 chunks per pass: lm_head
+    // 151936 x 2560, M = 8, 70.2 -> 73.8 us)
     const uint32_t tpw = tpw_q8(P);
+    constexpr int max_gpw = P == 1 || MT == 1 ? 5 : (MT == 16 ? 3 : 4);
+    plan(nT * nsplit, cps, max_gpw, gpw, nw, target_waves_q8());
     if (tpw == 2) {
-        const int g2 = tpw_full_gpw() ? gpw : (gpw + 1) / 2;
+        const int g2 = min(tpw_full_gpw() ? gpw : (gpw + 1) / 2, 2);
         const uint32_t nw2 = min((cps + g2 - 1) / g2, 16u);
         switch (g2) {
             case 1: launch_q8_g<MT, P, DOTS, 1, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw2, nsplit, st); break;
