@@ -18,12 +18,18 @@ replayed alone in a HIP graph between HIP events), vs 8 TB/s; traffic = HBM
 bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE
 (profiles/matvec_q8_0_traffic.txt).
 cpu_baseline: the oracle's AVX2 restatement of the reference decoder
-(fp32 activations, OpenMP over matvec rows) on this host's cores, on a short
-sample of single-sequence decode tokens with the same weights.
+(fp32 activations, OpenMP over matvec rows) on this host's cores with the same
+weights, the reference's token-at-a-time loop (engine.zig:843-854): decode
+steps of the same batch of 8 at the same contexts (each step = 8 sequence
+tokens in turn) and one 512-token prompt chunk as a token loop; all-core
+sample: 16 decode steps and the 512-token chunk; 1-thread sample: one decode
+step and 16 prompt tokens (the rates are per token, so the extrapolation to
+the full workload is linear; stated in the line).
 """
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import sys
@@ -65,25 +71,45 @@ def cpu_model():
     return "unknown"
 
 
-def cpu_baseline(eng, cfg, n_tokens, threads):
-    """Time the oracle's AVX2 decoder on the engine's own weights (host copy)."""
-    from echohip.engine import EngineConfig
+def cpu_baseline(eng, cfg, lens, threads, decode_steps=16, prefill_tokens=512):
+    """The reference decoder's CPU rate on the engine's own weights (host copy):
+    the oracle's AVX2 decoder, fp32 activations, one token at a time
+    (engine.zig:843-854).  Decode: the benchmark's batch of sequences at its
+    contexts (lens; cache and state contents do not change the work), each
+    step one token of every sequence in turn; prefill: a fresh sequence's
+    prompt tokens one by one from position 0.  `threads` threads, then 1
+    thread on a 1-step / 16-token sample.  Returns {threads: (decode tok/s,
+    prefill tok/s, seconds)}."""
     from oracle import Baseline, Decoder
 
     m = eng.export_model()
-    ccfg = EngineConfig(max_batch=1, max_ctx=n_tokens + 4)
     bl = Baseline()
+    B = len(lens)
+    dcfg = dataclasses.replace(cfg, max_batch=B, max_ctx=max(lens) + decode_steps + 2)
+    pcfg = dataclasses.replace(cfg, max_batch=1, max_ctx=prefill_tokens + 2)
     res = {}
-    for nthr, ntok in ((1, max(1, n_tokens // 10)), (threads, n_tokens)):
+    for nthr, nsteps, ntok in ((threads, decode_steps, prefill_tokens), (1, 1, 16)):
         bl.threads(nthr)
-        dec = Decoder(bl, ccfg, m, n_seq=1, quant_act=False)
-        dec.token(0, 1)  # warm-up (page-in)
+        dec = Decoder(bl, dcfg, m, n_seq=B, quant_act=False)
+        for s in range(B):
+            dec.seqs[s].pos = int(lens[s])
+        dec.token(0, 1)  # warm-up (page-in), then back to the sequence's context
+        dec.seqs[0].pos = int(lens[0])
+        t0 = time.perf_counter()
+        for step in range(nsteps):
+            for s in range(B):
+                dec.token(s, 1000 + 17 * step + 3 * s)
+        td = time.perf_counter() - t0
+        del dec
+        pre = Decoder(bl, pcfg, m, n_seq=1, quant_act=False)
         t0 = time.perf_counter()
         for i in range(ntok):
-            dec.token(0, 1000 + 17 * i)
-        dt = time.perf_counter() - t0
-        res[nthr] = ntok / dt
-        log(f"cpu baseline: {nthr} thread(s): {ntok} tokens in {dt:.2f} s -> {ntok / dt:.3f} tok/s")
+            pre.token(0, 2000 + 13 * i)
+        tp = time.perf_counter() - t0
+        del pre
+        res[nthr] = (nsteps * B / td, ntok / tp, td + tp)
+        log(f"cpu baseline: {nthr} thread(s): {nsteps} batch-{B} decode steps in {td:.2f} s "
+            f"({res[nthr][0]:.3f} tok/s), {ntok} prompt tokens in {tp:.2f} s ({res[nthr][1]:.3f} tok/s)")
     return res
 
 
@@ -175,8 +201,10 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=8)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--max-prompt", type=int, default=4096, help="upper bound of the prompt-length draw")
-    ap.add_argument("--cpu-tokens", type=int, default=256,
-                    help="all-core CPU baseline sample (tokens; ~10 s on 16 cores); the 1-thread leg runs 1/10 of it")
+    ap.add_argument("--cpu-steps", type=int, default=16,
+                    help="all-core CPU baseline: batch-8 decode steps (the 1-thread leg runs one)")
+    ap.add_argument("--cpu-prefill", type=int, default=512,
+                    help="all-core CPU baseline: prompt tokens of the token-loop prefill (1 thread: 16)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
@@ -306,18 +334,30 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu:
-        threads = min(os.cpu_count() or 1, 16)
-        res = cpu_baseline(eng, cfg, args.cpu_tokens, threads)
+        # the host share of one GPU: OMP_NUM_THREADS (16 on this pool's one-GPU boxes), else every core
+        threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+        res = cpu_baseline(eng, cfg, lens.tolist(), threads, args.cpu_steps, args.cpu_prefill)
         log("cpu baseline: kernel workloads")
         cpu_kernels = cpu_kernel_baselines(threads)
         log(f"cpu kernels: {cpu_kernels}")
-        cpu = {"value": round(res[threads], 4), "unit": "tok/s", "cores": threads, "kind": "port",
-               "sample": f"{args.cpu_tokens} single-sequence decode tokens ({max(1, args.cpu_tokens // 10)} on 1 thread) "
-                         f"of the same 4B-class model and weights "
-                         f"(oracle AVX2 decoder, fp32 activations, OpenMP over matvec rows, {threads} threads, "
-                         f"context < {args.cpu_tokens + 2}); 1 thread: {res[1]:.4f} tok/s; host CPU: {cpu_model()}, "
-                         f"{os.cpu_count()} hardware threads visible",
-               "kernels": cpu_kernels}
+        d_all, p_all, s_all = res[threads]
+        d_one, p_one, s_one = res[1]
+        full_tokens = B * (W + K)
+        cpu = {"value": round(d_all, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+               "sample": f"the reference's token-at-a-time loop (oracle AVX2 decoder, fp32 activations, OpenMP over "
+                         f"matvec rows, {threads} threads = the host share of one GPU, OMP_NUM_THREADS) on the same "
+                         f"4B-class weights: {args.cpu_steps} decode steps of the same batch of {B} at the same "
+                         f"contexts ({min(lens.tolist())}..{max(lens.tolist())}), i.e. {args.cpu_steps * B} tokens, "
+                         f"{d_all:.3f} tok/s, and one {args.cpu_prefill}-token prompt chunk fed token by token, "
+                         f"{p_all:.3f} tok/s ({s_all:.1f} s); 1 thread on 1 decode step ({B} tokens) and "
+                         f"{16} prompt tokens: {d_one:.4f} / {p_one:.4f} tok/s ({s_one:.1f} s).  Extrapolated "
+                         f"linearly (per-token rates): this run's {W + K} decode steps ({full_tokens} tokens) take "
+                         f"{full_tokens / d_all:.0f} s on {threads} threads and {full_tokens / d_one:.0f} s on "
+                         f"1 thread; its {int(lens.sum())} prompt tokens {int(lens.sum()) / p_all:.0f} s and "
+                         f"{int(lens.sum()) / p_one:.0f} s.  Host CPU: {cpu_model()}, {os.cpu_count()} hardware "
+                         f"threads visible",
+               "decode_tok_s_1t": round(d_one, 4), "prefill_tok_s": round(p_all, 4),
+               "prefill_tok_s_1t": round(p_one, 4), "kernels": cpu_kernels}
 
     line = {
         "metric": "decode tok/s (4B-class Q8_0, 1 GPU); matvec HBM GB/s as % of peak",

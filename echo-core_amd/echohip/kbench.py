@@ -333,20 +333,21 @@ def run_all(hip, quick=False):
 # decoder at batch 8, with the split-K counts the engine uses (host/engine.cpp:
 # 2 for the delta-net input projection and gate/up, 3 for the projections that
 # add into the residual; a split writes one partial output per split).
-DECODE_STEP_MATVECS = [("delta_in", 12352, 2560, 24, 2), ("delta_out", 2560, 4096, 24, 3),
+# (name, N, K, launches per decode step, K splits) with the engine's defaults for two activation pieces
+DECODE_STEP_MATVECS = [("delta_in", 12352, 2560, 24, 1), ("delta_out", 2560, 4096, 24, 3),
                        ("attn_in", 6144, 2560, 8, 4), ("attn_out", 2560, 4096, 8, 3),
-                       ("ffn_gate_up", 18432, 2560, 32, 3), ("ffn_down", 2560, 9216, 32, 3),
+                       ("ffn_gate_up", 18432, 2560, 32, 4), ("ffn_down", 2560, 9216, 32, 3),
                        ("lm_head", 151936, 2560, 1, 1)]
 PMC_LAUNCHES = 3
 CALIB_BYTES = 256 << 20
 
 
-def pmc_workload(hip, M=8):
+def pmc_workload(hip, M=8, pieces=2):
     """Launch sequence for rocprofv3 counter collection: every decode-step
     matvec shape PMC_LAUNCHES times (eager, each launch on a different weight
-    copy of a >= 512 MB rotation), then the calibration kernels of known
-    traffic: k_stream_read of CALIB_BYTES twice (reads) and a CALIB_BYTES
-    fill twice (writes)."""
+    copy of a >= 512 MB rotation; the decode step's two-piece activations),
+    then the calibration kernels of known traffic: k_stream_read of
+    CALIB_BYTES twice (reads) and a CALIB_BYTES fill twice (writes)."""
     st = torch.cuda.current_stream().cuda_stream
     for name, N, K, _, ns in DECODE_STEP_MATVECS:
         tb = hip.tiled_bytes(L.Q8_0, N, K)
@@ -359,12 +360,12 @@ def pmc_workload(hip, M=8):
             tiled[i].copy_(tiled[0])
         del Wd
         x = torch.from_numpy(synth.activations(1, M * K)).cuda()
-        act = torch.empty(hip.act_bytes(L.Q8_0, M, K), dtype=torch.uint8, device="cuda")
-        hip.quantize_act(L.Q8_0, x, act, M, K, stream=st)
+        act = torch.empty(hip.act_bytes(L.Q8_0, M, K, pieces=pieces), dtype=torch.uint8, device="cuda")
+        hip.quantize_act(L.Q8_0, x, act, M, K, stream=st, pieces=pieces)
         y = torch.empty(ns * M * N, dtype=torch.float32, device="cuda")
         torch.cuda.synchronize()
         for i in range(PMC_LAUNCHES):
-            hip.matvec_split(L.Q8_0, tiled[(i * 7919) % n_copies], act, y, M, N, K, ns, stream=st)
+            hip.matvec_split(L.Q8_0, tiled[(i * 7919) % n_copies], act, y, M, N, K, ns, stream=st, pieces=pieces)
             torch.cuda.synchronize()
         del tiled
         torch.cuda.empty_cache()
