@@ -10,8 +10,9 @@
 // 64-element quarter of a super-block) and holds that column's activations in
 // registers for the workgroup's whole life; P threads share a column and take
 // every P-th row of the tile.  Per row a thread produces one partial sum,
-// parked in LDS; a wave then adds a row's partials (wave-level DPP sum) and
-// accumulates into y.
+// parked in LDS; then a row's partials are added with lane exchanges (Q8_0: a
+// wave per row; Q4_K: a group of up to 64 threads per row) and one lane
+// accumulates the row into y.
 //
 // Q8_0 (34-byte blocks, 2-byte aligned): the tile's bytes are one contiguous
 // range (rows are contiguous in GGUF), loaded with 16-byte coalesced loads
@@ -19,10 +20,14 @@
 // thread reads its block at its 2-byte-aligned offset.  Needs K % 256 == 0 so
 // that rows start 16-byte aligned.
 // Q4_K (144-byte super-blocks, 16-byte aligned): each thread loads its own
-// 16-byte header and 32 bytes of nibbles straight from HBM (lanes of a wave
-// cover consecutive 32-byte runs); the per-sub-block form
-// y = sum (d*sc) * sum(q x) - (dmin*m) * sum(x) uses activation sums computed
-// once per thread.
+// 16-byte header and 32 bytes of nibbles straight from HBM for each of its
+// RPT rows (lanes of a wave cover consecutive 32-byte runs), all issued
+// first; the workgroup stages x once in LDS (quarters 272 bytes apart, so 16
+// consecutive lanes' 16-byte reads fall in distinct banks) and each thread
+// copies its quarter to registers for its rows -- x is read from L2 once per
+// workgroup of R = RPT * P rows instead of once per thread; the
+// per-sub-block form y = sum (d*sc) * sum(q x) - (dmin*m) * sum(x) uses
+// activation sums computed once per thread.
 #include <algorithm>
 #include <cstdlib>
 
@@ -39,10 +44,29 @@ __device__ __forceinline__ uint4 ld_nt16(const uint8_t* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Hides v's known-zero bits from the optimizer (an empty asm, no
+// instruction): with four nibbles masked into the low halves of four bytes,
+// (float)((v >> 8n) & 0xFF) then selects the single v_cvt_f32_ubyte<n>
+// instead of a 4-bit field extract plus a convert.
+__device__ __forceinline__ void hide_bits(uint32_t& v) { asm("" : "+v"(v)); }
+
+// Sum of v over this lane's aligned group of G consecutive lanes (G a power
+// of two <= 64, uniform); every lane of the group receives the total.
+__device__ __forceinline__ float sum_group(float v, uint32_t G) {
+    if (G >= 2) v += lane_xor<1>(v);
+    if (G >= 4) v += lane_xor<2>(v);
+    if (G >= 8) v += lane_xor<4>(v);
+    if (G >= 16) v += lane_xor<8>(v);
+    if (G >= 32) v += lane_xor<16>(v);
+    if (G >= 64) v += lane_xor<32>(v);
+    return v;
+}
+
 // Rows' partial sums red[rr][0 .. ncol) -> y[r0 + rr] = y0[rr] + sum, one wave
 // per row.  y0 holds the rows' previous y values, read at kernel start (no
 // dependent global load at the end of the workgroup: 10.3 -> 9.9 us at
-// 9216 x 2560); nothing else writes these rows during the kernel.
+// 9216 x 2560); nothing else writes these rows during the kernel.  (The
+// grouped row sums below measured 10.4 us here.)
 __device__ __forceinline__ void reduce_rows(const float* red, const float* y0, uint32_t ncol, uint32_t nr,
                                             float* __restrict__ y, uint32_t r0) {
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
@@ -52,6 +76,24 @@ __device__ __forceinline__ void reduce_rows(const float* red, const float* y0, u
         s = wave_sum(s);
         if (lane == 0) y[r0 + rr] = y0[rr] + s;
     }
+}
+
+// Rows' values red[rr][0 .. ncol) -> y[r0 + rr] = yp + sum for rr < nr: the G
+// consecutive threads rr*G .. rr*G + G-1 (G a power of two <= 64, G * R <=
+// blockDim) add every G-th value, then exchange; thread rr*G stores.  yp is
+// the row's previous y, loaded by every thread of the group at kernel start
+// (y[r0 + min(t / G, nr - 1)]: no dependent global load at the end of the
+// workgroup); nothing else writes these rows during the kernel.  One store
+// per row (a wave per row with scattered single-float stores cost 1.8 us of
+// 8.2 at Q4_K 9216 x 2560).
+__device__ __forceinline__ void row_sums_store(const float* red, uint32_t ncol, uint32_t nr, uint32_t G, float yp,
+                                               float* __restrict__ y, uint32_t r0) {
+    const uint32_t t = threadIdx.x, rr = t / G, G0 = rr * G;
+    float acc = 0.0f;
+    if (rr < nr)
+        for (uint32_t c = t - G0; c < ncol; c += G) acc += red[rr * ncol + c];
+    acc = sum_group(acc, G);
+    if (t == G0 && rr < nr) y[r0 + rr] = yp + acc;
 }
 
 constexpr int kQ8Stage = 8;  // 16-byte tile chunks per thread (R rows x K/32*34 bytes <= 8 * 16 * threads)
@@ -108,71 +150,126 @@ __global__ __launch_bounds__(1024) void k_gguf_q8_0_f32(const uint8_t* __restric
     reduce_rows(red, y0, nb, nr, y, r0);
 }
 
-// grid.x = ceil(M / R), R = RPT * P rows (RPT rows per thread, each one 16-byte
-// header + 32 bytes of nibbles loaded straight from HBM); blockDim = P * nq
-// (nq = 4 * K/256 quarters per row).
+// grid.x = ceil(M / R), R = RPT * P rows; blockDim T = P * nq rounded up to
+// whole waves (nq = 4 * K/256 quarters per row, P a power of two).  Thread t
+// takes quarter q = t % nq of rows ph + i*P (ph = t / nq, i < RPT): per row a
+// 16-byte header and 32 bytes of nibbles loaded straight from HBM, so the
+// lanes of one load instruction cover consecutive quarters of one row.
+// Threads t >= P * nq only pad the last wave.  The workgroup's 16 * nq float4s
+// of x are XPT per thread (T * XPT >= 16 * nq).  LDS (floats): x as nq
+// quarters of 68 (64 + 4 padding, where padding threads' stores land), x's
+// pair sums [nq][2], then the rows' quarter values [R][nq] and a spare slot.
+//
+// Issue order matters: vector-memory loads complete in order, so x's loads go
+// first and the weights' after them, all unconditional (a row past the
+// tile's end re-reads row r0 and is never used) -- the wait before x's LDS
+// store then covers x alone, and the staging, barrier and LDS reads overlap
+// the weights' HBM latency.
+//
+// x's pair sums come from the staging registers: 16 consecutive lanes hold
+// one quarter's 16 float4s, so two lane-exchange sums give both pairs.  The
+// row sums: G = T / R (a power of two, at most 64) consecutive threads share
+// a row, each adding every G-th quarter value, then lane exchanges; thread
+// rr * G stores y for row rr -- one store per row, after all loads.
+constexpr uint32_t kQ4XStride = 68;  // floats per staged quarter (272 bytes)
+
+// Four rows' loads (48 registers) beside the 64 activations need more than
+// the 128 registers a 1024-thread workgroup allows: RPT = 4 is bounded at 768
+// threads (up to 168 registers, spill-free).
 template <int RPT>
-__global__ __launch_bounds__(1024) void k_gguf_q4_K_f32(const uint8_t* __restrict__ W, const float* __restrict__ x,
-                                                        float* __restrict__ y, uint32_t M, uint32_t nsb, uint32_t P,
-                                                        uint32_t R) {
+constexpr int q4_f32_max_threads() { return RPT == 4 ? 768 : 1024; }
+
+size_t q4_f32_lds_bytes(uint32_t nq, uint32_t R) {
+    return ((size_t)nq * (kQ4XStride + 2) + (size_t)R * nq + 1) * 4;
+}
+
+// 6-bit scale and min of sub-blocks 2g and 2g + 1 from the 12 scale bytes
+// (w0 = bytes 0-3, w1 = 4-7, w2 = 8-11), the packing of src/kernels/quant.cpp:222-242:
+// sub-block j < 4: scale = byte j & 63, min = byte j+4 & 63; j >= 4: scale =
+// (byte j+4 & 15) | (byte j-4 >> 6) << 4, min = (byte j+4 >> 4) | (byte j >> 6) << 4.
+// Both cases read bytes 2(g & 1) + s of w0, w1 (and w2), branch-free.
+__device__ __forceinline__ void q4_scale_min(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t g, uint32_t& sc0,
+                                             uint32_t& mn0, uint32_t& sc1, uint32_t& mn1) {
+    const uint32_t sh = 16 * (g & 1);
+    const uint32_t a = w0 >> sh, b = w1 >> sh, c = w2 >> sh;
+    const bool hi = g >= 2;
+    sc0 = hi ? (c & 15u) | ((a >> 2) & 48u) : a & 63u;
+    mn0 = hi ? ((c >> 4) & 15u) | ((b >> 2) & 48u) : b & 63u;
+    sc1 = hi ? ((c >> 8) & 15u) | ((a >> 10) & 48u) : (a >> 8) & 63u;
+    mn1 = hi ? ((c >> 12) & 15u) | ((b >> 10) & 48u) : (b >> 8) & 63u;
+}
+
+// nq_magic = ceil(2^32 / nq): t / nq == umulhi(t, nq_magic) exactly for
+// t, nq < 2^10 (the rounding error t * (nq_magic - 2^32/nq) / 2^32 < 2^-22
+// is below the 1/nq gap to the next integer).
+template <int RPT, int XPT>
+__global__ __launch_bounds__(q4_f32_max_threads<RPT>()) void k_gguf_q4_K_f32(
+    const uint8_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ y, uint32_t M, uint32_t nsb,
+    uint32_t P, uint32_t R, uint32_t G, uint32_t nq_magic) {
     extern __shared__ uint8_t lds[];
-    float* red = (float*)lds;
-    const uint32_t t = threadIdx.x, nq = 4 * nsb;
-    const uint32_t q = t % nq, ph = t / nq, sb = q / 4, g = q % 4;
+    const uint32_t t = threadIdx.x, T = blockDim.x, nq = 4 * nsb;
+    float* xs = (float*)lds;
+    float2* xsum = (float2*)(xs + (size_t)nq * kQ4XStride);
+    float* red = (float*)(xsum + nq);  // [R][nq] + 1
+    const uint32_t ph0 = __umulhi(t, nq_magic), q = t - ph0 * nq;
+    const uint32_t ph = min(ph0, P - 1), sb = q / 4, g = q % 4;  // padding threads: q < nq, ph0 >= P
     const size_t rowbytes = (size_t)nsb * 144;
-    const uint32_t r0 = blockIdx.x * R, nr = min(R, M - r0);
-    float* y0 = red + (size_t)R * nq;  // previous y of the tile's rows (R <= blockDim.x)
-    const float yp = t < nr ? y[r0 + t] : 0.0f;
+    const uint32_t r0 = blockIdx.x * R, nr = min(R, M - r0), n4 = 16 * nq;
+    float4 xf[XPT];  // float4s t, t + T, ... of x
+#pragma unroll
+    for (int j = 0; j < XPT; ++j) xf[j] = ((const float4*)x)[min(t + j * T, n4 - 1)];
+    const float yp = y[r0 + min(t / G, nr - 1)];
+    __builtin_amdgcn_sched_barrier(0);  // keep x's loads ahead of the weights'
     uint4 hd[RPT], q0[RPT], q1[RPT];
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
         const uint32_t rr = ph + i * P;
-        const bool ok = rr < nr;
-        const uint8_t* bp = W + (size_t)(r0 + (ok ? rr : 0)) * rowbytes + 144 * (size_t)sb;
-        hd[i] = ok ? *(const uint4*)bp : make_uint4(0u, 0u, 0u, 0u);
-        q0[i] = ok ? ld_nt16(bp + 16 + 32 * g) : make_uint4(0u, 0u, 0u, 0u);
-        q1[i] = ok ? ld_nt16(bp + 32 + 32 * g) : make_uint4(0u, 0u, 0u, 0u);
+        const uint8_t* bp = W + (size_t)(r0 + (rr < nr ? rr : 0)) * rowbytes + 144 * (size_t)sb;
+        hd[i] = *(const uint4*)bp;
+        q0[i] = ld_nt16(bp + 16 + 32 * g);
+        q1[i] = ld_nt16(bp + 32 + 32 * g);
     }
-    // activations of the quarter, in the reference's position order: pair 0 of
-    // the 64-group at positions 0-15 (low nibbles of bytes 0-15) and 32-47
-    // (their high nibbles), pair 1 at 16-31 and 48-63 (bytes 16-31)
+    // x -> LDS, quarter c (64 floats) at c * 68 floats, float4s past x's end
+    // into the last quarter's padding; float4 k of a quarter (lane % 16 == k)
+    // is in pair 0 for k & 4 == 0 (positions 0-15, 32-47), pair 1 otherwise
+#pragma unroll
+    for (int j = 0; j < XPT; ++j) {
+        const uint32_t c4 = t + j * T;
+        const uint32_t o = c4 < n4 ? (c4 / 16) * kQ4XStride + 4 * (c4 % 16) : (nq - 1) * kQ4XStride + 64;
+        *(float4*)(xs + o) = xf[j];
+        float ps = (xf[j].x + xf[j].y) + (xf[j].z + xf[j].w);
+        ps += lane_xor<1>(ps);
+        ps += lane_xor<2>(ps);
+        ps += lane_xor<8>(ps);
+        if (c4 < n4 && (c4 & 11) == 0) ((float*)xsum)[2 * (c4 / 16) + ((c4 >> 2) & 1)] = ps;
+    }
+    __syncthreads();
+    // the thread's quarter, in the reference's position order: pair 0 of the
+    // 64-group at positions 0-15 (low nibbles of bytes 0-15) and 32-47 (their
+    // high nibbles), pair 1 at 16-31 and 48-63 (bytes 16-31)
     float xv[64];
-    const float4* xb = (const float4*)(x + 256 * sb + 64 * g);
+    const float4* xq = (const float4*)(xs + q * kQ4XStride);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        const float4 f = xb[i];
+        const float4 f = xq[i];
         xv[4 * i] = f.x, xv[4 * i + 1] = f.y, xv[4 * i + 2] = f.z, xv[4 * i + 3] = f.w;
     }
-    float xs0 = 0.0f, xs1 = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        xs0 += xv[j] + xv[32 + j];
-        xs1 += xv[16 + j] + xv[48 + j];
-    }
+    const float2 xm = xsum[q];
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
+        // branch-free: a row past the tile's end (rr >= nr) sums row r0's
+        // bytes, and its value is never read -- a branch here would let the
+        // compiler sink the weights' loads below the barrier
         const uint32_t rr = ph + i * P;
-        if (rr >= nr) break;
-        const uint32_t scw[3] = {hd[i].y, hd[i].z, hd[i].w};  // scales[0..11]
-        auto byte = [&](int k) -> uint32_t { return (scw[k >> 2] >> (8 * (k & 3))) & 0xFFu; };
         uint32_t sc0, mn0, sc1, mn1;
-        const int s0 = 2 * (int)g, s1 = s0 + 1;
-        // 6-bit scale / min unpack (src/kernels/quant.cpp:222-242)
-        if (s0 < 4) {
-            sc0 = byte(s0) & 63u, mn0 = byte(s0 + 4) & 63u;
-            sc1 = byte(s1) & 63u, mn1 = byte(s1 + 4) & 63u;
-        } else {
-            sc0 = (byte(s0 + 4) & 0x0Fu) | ((byte(s0 - 4) >> 6) << 4);
-            mn0 = (byte(s0 + 4) >> 4) | ((byte(s0) >> 6) << 4);
-            sc1 = (byte(s1 + 4) & 0x0Fu) | ((byte(s1 - 4) >> 6) << 4);
-            mn1 = (byte(s1 + 4) >> 4) | ((byte(s1) >> 6) << 4);
-        }
+        q4_scale_min(hd[i].y, hd[i].z, hd[i].w, g, sc0, mn0, sc1, mn1);
         const float d = h2f(hd[i].x & 0xFFFF), dmin = h2f(hd[i].x >> 16);
         const uint32_t qw[8] = {q0[i].x, q0[i].y, q0[i].z, q0[i].w, q1[i].x, q1[i].y, q1[i].z, q1[i].w};
         float S0 = 0.0f, S1 = 0.0f;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {  // bytes 0-15: pair 0
-            const uint32_t lo = qw[k] & 0x0F0F0F0Fu, hi = (qw[k] >> 4) & 0x0F0F0F0Fu;
+            uint32_t lo = qw[k] & 0x0F0F0F0Fu, hi = (qw[k] >> 4) & 0x0F0F0F0Fu;
+            hide_bits(lo), hide_bits(hi);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 S0 = fmaf((float)((lo >> (8 * e)) & 0xFF), xv[4 * k + e], S0);
@@ -181,19 +278,44 @@ __global__ __launch_bounds__(1024) void k_gguf_q4_K_f32(const uint8_t* __restric
         }
 #pragma unroll
         for (int k = 4; k < 8; ++k) {  // bytes 16-31: pair 1
-            const uint32_t lo = qw[k] & 0x0F0F0F0Fu, hi = (qw[k] >> 4) & 0x0F0F0F0Fu;
+            uint32_t lo = qw[k] & 0x0F0F0F0Fu, hi = (qw[k] >> 4) & 0x0F0F0F0Fu;
+            hide_bits(lo), hide_bits(hi);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 S1 = fmaf((float)((lo >> (8 * e)) & 0xFF), xv[4 * k + e], S1);
                 S1 = fmaf((float)((hi >> (8 * e)) & 0xFF), xv[32 + 4 * k + e], S1);
             }
         }
-        red[rr * nq + q] = (d * (float)sc0) * S0 - (dmin * (float)mn0) * xs0 + (d * (float)sc1) * S1 -
-                           (dmin * (float)mn1) * xs1;
+        const float val = ((d * (float)sc0) * S0 + (d * (float)sc1) * S1) -
+                          dmin * ((float)mn0 * xm.x + (float)mn1 * xm.y);
+        red[ph0 < P ? rr * nq + q : R * nq] = val;  // padding threads: the spare slot
     }
-    if (t < nr) y0[t] = yp;
     __syncthreads();
-    reduce_rows(red, y0, nq, nr, y, r0);
+    row_sums_store(red, nq, nr, G, yp, y, r0);
+}
+
+template <int RPT>
+int launch_q4_f32_x(uint32_t xpt, dim3 grid, dim3 blk, size_t lds, hipStream_t st, const uint8_t* W, const float* x,
+                    float* y, uint32_t M, uint32_t nsb, uint32_t P, uint32_t R, uint32_t G, uint32_t mg) {
+    switch (xpt) {
+        case 1: hipLaunchKernelGGL((k_gguf_q4_K_f32<RPT, 1>), grid, blk, lds, st, W, x, y, M, nsb, P, R, G, mg); break;
+        case 2: hipLaunchKernelGGL((k_gguf_q4_K_f32<RPT, 2>), grid, blk, lds, st, W, x, y, M, nsb, P, R, G, mg); break;
+        case 4: hipLaunchKernelGGL((k_gguf_q4_K_f32<RPT, 4>), grid, blk, lds, st, W, x, y, M, nsb, P, R, G, mg); break;
+        case 8: hipLaunchKernelGGL((k_gguf_q4_K_f32<RPT, 8>), grid, blk, lds, st, W, x, y, M, nsb, P, R, G, mg); break;
+        case 16: hipLaunchKernelGGL((k_gguf_q4_K_f32<RPT, 16>), grid, blk, lds, st, W, x, y, M, nsb, P, R, G, mg); break;
+        default: return EC_ERR_UNSUPPORTED;
+    }
+    return EC_OK;
+}
+
+int launch_q4_f32(uint32_t rpt, uint32_t xpt, dim3 grid, dim3 blk, size_t lds, hipStream_t st, const uint8_t* W,
+                  const float* x, float* y, uint32_t M, uint32_t nsb, uint32_t P, uint32_t R) {
+    const uint32_t nq = 4 * nsb, mg = (uint32_t)((((uint64_t)1 << 32) + nq - 1) / nq);
+    uint32_t G = 64;  // threads per row in the row sums: a power of two with G * R <= T
+    while (G * R > blk.x) G /= 2;
+    if (rpt == 4) return launch_q4_f32_x<4>(xpt, grid, blk, lds, st, W, x, y, M, nsb, P, R, G, mg);
+    if (rpt == 2) return launch_q4_f32_x<2>(xpt, grid, blk, lds, st, W, x, y, M, nsb, P, R, G, mg);
+    return launch_q4_f32_x<1>(xpt, grid, blk, lds, st, W, x, y, M, nsb, P, R, G, mg);
 }
 
 uint32_t gcd32(uint32_t a, uint32_t b) {
@@ -237,16 +359,33 @@ int gguf_mv_fast(int fmt, const uint8_t* W, const float* x, float* y, uint32_t M
         if (nq > 1024) return EC_ERR_UNSUPPORTED;
         uint32_t P = 64 / gcd32(nq, 64);
         while (P > 1 && P * nq > 1024) P /= 2;
-        // two rows per thread (both rows' loads in flight) unless that leaves
-        // fewer than 512 workgroups
-        const uint32_t rpt = (M + 2 * P - 1) / (2 * P) >= 512 ? 2 : 1;
+        static const uint32_t p_env = [] {
+            const char* v = getenv("EC_GGUF_P");  // threads per quarter (a power of two <= the default), for comparison
+            return v ? (uint32_t)atoi(v) : 0u;
+        }();
+        if (p_env && p_env < P && (p_env & (p_env - 1)) == 0) P = p_env;
+        // RPT rows per thread (all rows' loads in flight): x is read from L2
+        // once per workgroup of R = RPT * P rows, so larger R means fewer
+        // activation bytes per weight byte, but fewer waves to hide the
+        // latency and spread the arithmetic; RPT = 1 while that leaves at
+        // least 512 workgroups, else 2, else 4
+        static const uint32_t rpt_env = [] {
+            const char* v = getenv("EC_GGUF_RPT");  // 1, 2 or 4: fixed rows per thread, for comparison
+            return v ? (uint32_t)atoi(v) : 0u;
+        }();
+        uint32_t rpt = 1;
+        while (rpt < 4 && (M + rpt * P - 1) / (rpt * P) < 512) rpt *= 2;
+        const uint32_t T = (P * nq + 63) / 64 * 64;
+        if (rpt == 4 && T > (uint32_t)q4_f32_max_threads<4>()) rpt = 2;
+        if ((rpt_env == 1 || rpt_env == 2 || rpt_env == 4) && T <= (rpt_env == 4 ? 768u : 1024u)) rpt = rpt_env;
         const uint32_t R = rpt * P;
-        const dim3 grid((M + R - 1) / R), blk(P * nq);
-        const size_t lds = (size_t)R * nq * 4 + (size_t)R * 4;
-        if (R > P * nq) return EC_ERR_UNSUPPORTED;
-        if (rpt == 2) hipLaunchKernelGGL(k_gguf_q4_K_f32<2>, grid, blk, lds, st, W, x, y, M, nsb, P, R);
-        else hipLaunchKernelGGL(k_gguf_q4_K_f32<1>, grid, blk, lds, st, W, x, y, M, nsb, P, R);
-        return EC_OK;
+        const dim3 grid((M + R - 1) / R), blk(T);
+        const size_t lds = q4_f32_lds_bytes(nq, R);
+        // x's 16 * nq float4s over T threads, rounded up to a compiled count
+        uint32_t xpt = 1;
+        while (xpt * T < 16 * nq) xpt *= 2;
+        if (T > 1024 || R > T || lds > 160 * 1024 || xpt > 16) return EC_ERR_UNSUPPORTED;
+        return launch_q4_f32(rpt, xpt, grid, blk, lds, st, W, x, y, M, nsb, P, R);
     }
     return EC_ERR_UNSUPPORTED;
 }

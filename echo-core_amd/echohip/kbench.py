@@ -412,7 +412,8 @@ def pmc_cases(hip, which):
     recurrence (token loop, chunked scan) and the batch-8 fused decode update,
     PMC_LAUNCHES times each on different
     buffer copies of a >= 512 MB rotation; then the calibration kernels of
-    pmc_workload (a 256 MiB read, a 256 MiB fill)."""
+    pmc_workload (a 256 MiB read, a 256 MiB fill).  `gguf` runs the fp32 Q4_K
+    matvec over GGUF bytes (ec_matvec_gguf_f32) at 9216 x 2560 and 2560 x 9216."""
     st = torch.cuda.current_stream().cuda_stream
     if which == "attention":
         for ctx in (512, 4096, 32768):
@@ -498,6 +499,23 @@ def pmc_cases(hip, which):
                 torch.cuda.synchronize()
             del Wd, tiled, x, act, y
             torch.cuda.empty_cache()
+    elif which == "gguf":
+        # the reference-signature fp32 Q4_K matvec (GGUF bytes in place) at 9216 x 2560, then 2560 x 9216
+        for N, K in ((9216, 2560), (2560, 9216)):
+            wbytes = N * K // 256 * 144
+            n_copies = max(PMC_LAUNCHES, math.ceil(ROTATE_BYTES / wbytes) + 1)
+            Ws = torch.empty((n_copies, wbytes), dtype=torch.uint8, device="cuda")
+            Ws[0].copy_(torch.from_numpy(synth.q4_K_blocks(0, N, K).reshape(-1)))
+            for i in range(1, n_copies):
+                Ws[i].copy_(Ws[0])
+            x = torch.from_numpy(synth.activations(1, K)).cuda()
+            y = torch.zeros(N, dtype=torch.float32, device="cuda")
+            torch.cuda.synchronize()
+            for i in range(PMC_LAUNCHES):
+                hip.matvec_gguf_f32(L.Q4_K, Ws[(i * 7919) % n_copies], x, y, N, K, stream=st)
+                torch.cuda.synchronize()
+            del Ws, x, y
+            torch.cuda.empty_cache()
     elif which == "gemm":
         for fmt in (L.Q8_0, L.Q4_K):
             for N, K in ((9216, 2560), (2560, 9216)):
@@ -581,7 +599,7 @@ def pmc_kernel_means(csv_path, counters):
     for r in csv.DictReader(open(csv_path)):
         if r.get("Counter_Name") not in counters:
             continue
-        k = r["Kernel_Name"].split("(")[0]
+        k = r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0]
         d = acc.setdefault(k, {}).setdefault(r["Counter_Name"], [])
         d.append(float(r["Counter_Value"]))
     return {k: {c: round(sum(v) / len(v), 1) for c, v in cs.items()} | {"dispatches": len(next(iter(cs.values())))}

@@ -537,11 +537,16 @@ def test_deltanet_chunked_1024_tokens_32_heads(hip, oc):
 
 
 @pytest.mark.parametrize("fmt,N,K", [(6, 9216, 2560), (6, 2560, 9216), (6, 1000, 4096), (6, 77, 96), (10, 9216, 2560),
-                                     (10, 2560, 9216), (10, 333, 512)])
+                                     (10, 2560, 9216), (10, 333, 512), (10, 1001, 4096), (10, 2563, 9216),
+                                     (10, 1030, 13312), (10, 700, 11008), (10, 130, 16640)])
 def test_gguf_f32_matvec_full_shapes(hip, oc, fmt, N, K):
     """The reference-signature path (GGUF bytes in place, fp32 activations, y += W x) at the matvec workloads'
     full shapes, ragged row counts and a K whose rows are not 16-byte aligned (K = 96: per-row kernel), against
-    the oracle's reference-order matvec: within 1e-5 relative L2 (fp32 summation order only)."""
+    the oracle's reference-order matvec: within 1e-5 relative L2 (fp32 summation order only).  The Q4_K shapes
+    take every rows-per-thread variant (1 row: 9216 x 2560, 2560 x 9216, 2563 x 9216 with a last tile of 3 of
+    4 rows; 2 rows: 1030 x 13312, whose 832 threads exceed the 4-row variant's bound; 4 rows: 333 x 512,
+    1001 x 4096 with a last tile of 1 row) and workgroups padded to whole waves (11008: 688 threads of 704,
+    16640: 520 of 576), both with ragged last tiles."""
     W = synth.q8_0_blocks(fmt + N, N, K) if fmt == 6 else synth.q4_K_blocks(fmt + N, N, K)
     x = synth.activations(N + 1, K)
     y0 = synth.activations(N + 2, N)
