@@ -333,6 +333,22 @@ __device__ __forceinline__ void q4k_scale_min(const uint32_t (&q)[3], int s, uin
     }
 }
 
+// Sum of v over lanes l, l^16, l^32, l^48, in every lane: v_permlane32_swap
+// pairs lanes 0-31 with 32-63 and v_permlane16_swap odd with even 16-lane
+// rows, each returning both halves; every lane adds the same two operands.
+__device__ __forceinline__ float sum_lane_groups(float v) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// M = 1 (the epilogue split, !DOTS): one token leaves 15 of the MFMA's 16 A
+// rows free, so every A row carries the token (row r: layout row r % P, i.e.
+// piece r % 2 for P = 2) and every lane holds its weight row's sub-block dots;
+// lane group g (lanes 16g .. 16g+15) applies the epilogue of sub-blocks g and
+// 4+g only -- a quarter of the per-sub-block instructions -- and the four
+// groups' fp32 partials are added once at the end.
 template <int MT, int P, bool DOTS, int GPW>
 __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W, const uint8_t* __restrict__ act,
                                                   float* __restrict__ y, int32_t* __restrict__ dots, uint32_t M,
@@ -386,10 +402,11 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
             if (b >= nB) break;
             uint32_t aw[NA][16];
             bool aval[NA];
+            constexpr bool SPLIT = MT == 1 && !DOTS;
 #pragma unroll
             for (int ga = 0; ga < NA; ++ga) {
-                const uint32_t va = 16 * ga + row;
-                aval[ga] = va < VR;
+                const uint32_t va = SPLIT ? row % P : 16 * ga + row;
+                aval[ga] = SPLIT || va < VR;
                 const uint8_t* ap = as + (((size_t)u * 4 + g) * VR + (aval[ga] ? va : 0)) * 64;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -403,6 +420,7 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
             uint32_t sc4[2], mn4[2];
             q4k_scale_min4(scb, sc4, mn4);
             float a_sc = 0.0f, a_mn = 0.0f;  // M = 1: sum_s sc_s*dot_s*dx_s and sum_s m_s*dxs_s, scaled once
+            int dsplit[8];
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
                 const uint32_t lo = qw[s] & 0x0F0F0F0Fu, hi = (qw[s] >> 4) & 0x0F0F0F0Fu;
@@ -424,9 +442,7 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
                     const uint32_t mnv = (mn4[s >> 2] >> (8 * (s & 3))) & 0xFFu;
                     const int e = 8 * u + s;
                     if constexpr (MT == 1) {
-                        const int32_t dot = P == 2 ? cc[0][0] * 256 + cc[0][1] : cc[0][0];
-                        a_sc = fmaf((float)dot, (float)scv * xs[e], a_sc);
-                        a_mn = fmaf((float)mnv, xms[e], a_mn);
+                        dsplit[s] = P == 2 ? cc[0][0] * 256 + cc[0][1] : cc[0][0];  // |dot| <= 2^19 per piece
                     } else if constexpr (P == 2) {
                         const float dsc = d * (float)scv, dmn = dmin * (float)mnv;
 #pragma unroll
@@ -456,11 +472,21 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
                 }
             }
             if constexpr (MT == 1 && !DOTS) {
+                // lane group g: sub-blocks g and 4 + g
+                const int da = g == 0 ? dsplit[0] : g == 1 ? dsplit[1] : g == 2 ? dsplit[2] : dsplit[3];
+                const int db = g == 0 ? dsplit[4] : g == 1 ? dsplit[5] : g == 2 ? dsplit[6] : dsplit[7];
+                const uint32_t sh = 8 * g;
+                const int ea = 8 * u + g, eb = ea + 4;
+                a_sc = (float)da * ((float)((sc4[0] >> sh) & 0xFFu) * xs[ea]);
+                a_sc = fmaf((float)db, (float)((sc4[1] >> sh) & 0xFFu) * xs[eb], a_sc);
+                a_mn = (float)((mn4[0] >> sh) & 0xFFu) * xms[ea];
+                a_mn = fmaf((float)((mn4[1] >> sh) & 0xFFu), xms[eb], a_mn);
                 acc[0] = fmaf(d, a_sc, acc[0]);
                 acc[0] = fmaf(-dmin, a_mn, acc[0]);
             }
         }
     }
+    if constexpr (MT == 1 && !DOTS) acc[0] = sum_lane_groups(acc[0]);
     if constexpr (!DOTS) reduce_store<R, P, 1>(acc4, red, y, t, M, N, ldy, accumulate);
 }
 
