@@ -222,86 +222,112 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q8_0(const uint8_t* __restrict_
 }
 
 // ------------------------------------------------------------------ Q4_K
-__device__ __forceinline__ void q4k_sm(const uint32_t (&q)[3], int s, uint32_t& sc, uint32_t& mn) {
-    auto byte = [&](int i) -> uint32_t { return (q[i >> 2] >> (8 * (i & 3))) & 0xFFu; };
-    if (s < 4) {
-        sc = byte(s) & 63u;
-        mn = byte(s + 4) & 63u;
-    } else {
-        sc = (byte(s + 4) & 0x0Fu) | ((byte(s - 4) >> 6) << 4);
-        mn = (byte(s + 4) >> 4) | ((byte(s) >> 6) << 4);
-    }
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// The eight 6-bit (scale, min) pairs of a super-block from its 12 scale
+// bytes (q[0] = bytes 0-3, ...), four per dword: sc[0] holds sub-blocks 0-3
+// (byte s = scale of sub-block s), sc[1] sub-blocks 4-7, mn likewise -- the
+// unpack of src/kernels/quant.cpp:222-242 on four bytes per operation.
+__device__ __forceinline__ void q4k_sm4(const uint32_t (&q)[3], uint32_t (&sc)[2], uint32_t (&mn)[2]) {
+    sc[0] = q[0] & 0x3F3F3F3Fu;
+    mn[0] = q[1] & 0x3F3F3F3Fu;
+    sc[1] = (q[2] & 0x0F0F0F0Fu) | ((q[0] >> 2) & 0x30303030u);
+    mn[1] = ((q[2] >> 4) & 0x0F0F0F0Fu) | ((q[1] >> 2) & 0x30303030u);
 }
 
+// Byte n of v as a float (v_cvt_f32_ubyte<n>).
+__device__ __forceinline__ float ubyte_f(uint32_t v, int n) { return (float)((v >> (8 * n)) & 0xFFu); }
+
+// The K loop steps over half super-blocks (128 elements, 4 sub-blocks: the
+// Q8_0 kernel's chunk, so the double-buffered operands fit two waves per
+// SIMD).  Per step a wave unpacks its rows' headers once: d*sc of the four
+// sub-blocks (the integer dots' scale) and dmin*m of the sub-block its lane
+// group feeds to the min-term product.  The min term
+//   Y[t][n] -= sum_s (dmin*m)[n][s] * dxs[t][s]
+// is a dense fp32 product with contraction over the sub-blocks: one
+// v_mfma_f32_16x16x4_f32 per (token tile, row tile) and step (A = -dxs[token]
+// [4h + k], B = (dmin*m)[4h + k][row]; lane l holds A[l%16][l/16] and
+// B[l/16][l%16], its D layout the int8 MFMA's) into accumulators of its own
+// (added to the others at the end), so the per-(token, row, sub-block)
+// epilogue is the Q8_0 kernel's: one conversion and one FMA per output
+// element.
 template <int RTW>
-__global__ __launch_bounds__(256) void k_gemm_q4_K(const uint8_t* __restrict__ W, const uint8_t* __restrict__ xt,
-                                                   float* __restrict__ y, uint32_t M, uint32_t N, uint32_t n_tt,
-                                                   uint32_t n_rt, uint32_t nB, uint32_t nbp, size_t xd_off,
-                                                   size_t dxs_off, uint32_t ldy, int accumulate) {
+__global__ __launch_bounds__(256, 2) void k_gemm_q4_K(const uint8_t* __restrict__ W, const uint8_t* __restrict__ xt,
+                                                      float* __restrict__ y, uint32_t M, uint32_t N, uint32_t n_tt,
+                                                      uint32_t n_rt, uint32_t nB, uint32_t nbp, size_t xd_off,
+                                                      size_t dxs_off, uint32_t ldy, int accumulate) {
     constexpr int TTW = 2;
-    __shared__ float dx_s[2][8][64], dm_s[2][8][64];  // [buffer][sub-block][token]
-    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4;
+    __shared__ float dx_s[2][4][64], dm_s[2][4][64];  // [buffer][sub-block of the step][token]
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, row = lane & 15;
     const uint32_t wt = w & 1, wr = w >> 1;
     const uint32_t tt0 = blockIdx.y * 4 + wt * TTW;
     const uint32_t rt0 = blockIdx.x * (2 * RTW) + wr * RTW;
     const float* xd = (const float*)(xt + xd_off);
     const float* dxs = (const float*)(xt + dxs_off);
-    const uint32_t tok = blockIdx.y * 64 + (threadIdx.x & 63), sq = threadIdx.x >> 6;  // stages s = sq, sq+4
+    const uint32_t tok = blockIdx.y * 64 + (threadIdx.x & 63), sq = threadIdx.x >> 6;  // stages sub-block sq
+    const uint32_t nC = 2 * nB;  // half super-blocks
 
-    float acc[TTW][RTW][4];
+    v4f acc[TTW][RTW], accm[TTW][RTW];
 #pragma unroll
     for (int t = 0; t < TTW; ++t)
 #pragma unroll
-        for (int r = 0; r < RTW; ++r)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[t][r][e] = 0.0f;
+        for (int r = 0; r < RTW; ++r) acc[t][r] = accm[t][r] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-    u32x4 a[2][TTW][4], b[2][RTW][2], hd[2][RTW];
-    float sv[2][4];
-    auto load = [&](int buf, uint32_t B) {
+    u32x4 a[2][TTW][2], b[2][RTW], hd[2][RTW];
+    float sv[2][2];
+    auto load = [&](int buf, uint32_t C) {
+        const uint32_t B = C >> 1, h = C & 1;
 #pragma unroll
         for (int t = 0; t < TTW; ++t) {
             const uint32_t T = min(tt0 + t, n_tt - 1);
-            const uint8_t* p = xt + ((size_t)T * nB + B) * 4096 + 16 * lane;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) a[buf][t][i] = *(const u32x4*)(p + 1024 * i);
+            const uint8_t* p = xt + ((size_t)T * nB + B) * 4096 + 2048 * h + 16 * lane;
+            a[buf][t][0] = *(const u32x4*)p;
+            a[buf][t][1] = *(const u32x4*)(p + 1024);
         }
 #pragma unroll
         for (int r = 0; r < RTW; ++r) {
             const uint32_t R = min(rt0 + r, n_rt - 1);
             const uint8_t* p = W + ((size_t)R * nB + B) * kQ4TChunk;
-            b[buf][r][0] = *(const u32x4*)(p + 16 * lane);
-            b[buf][r][1] = *(const u32x4*)(p + 1024 + 16 * lane);
-            hd[buf][r] = *(const u32x4*)(p + 2048 + 16 * (lane & 15));
+            b[buf][r] = *(const u32x4*)(p + 1024 * h + 16 * lane);
+            hd[buf][r] = *(const u32x4*)(p + 2048 + 16 * row);
         }
         const bool ok = tok < n_tt * 16;
-        const size_t base = (size_t)(ok ? tok : 0) * nbp + 8 * B;
-        sv[buf][0] = ok ? xd[base + sq] : 0.0f;
-        sv[buf][1] = ok ? xd[base + sq + 4] : 0.0f;
-        sv[buf][2] = ok ? dxs[base + sq] : 0.0f;
-        sv[buf][3] = ok ? dxs[base + sq + 4] : 0.0f;
+        const size_t at = (size_t)(ok ? tok : 0) * nbp + 8 * B + 4 * h + sq;
+        sv[buf][0] = ok ? xd[at] : 0.0f;
+        sv[buf][1] = ok ? dxs[at] : 0.0f;
     };
 
-    auto step = [&](auto bufc, uint32_t B) {
+    auto step = [&](auto bufc, uint32_t C) {
         constexpr int cur = decltype(bufc)::value;
+        const uint32_t h = C & 1;
         dx_s[cur][sq][threadIdx.x & 63] = sv[cur][0];
-        dx_s[cur][sq + 4][threadIdx.x & 63] = sv[cur][1];
-        dm_s[cur][sq][threadIdx.x & 63] = sv[cur][2];
-        dm_s[cur][sq + 4][threadIdx.x & 63] = sv[cur][3];
+        dm_s[cur][sq][threadIdx.x & 63] = sv[cur][1];
         __syncthreads();
-        if (B + 1 < nB) load(cur ^ 1, B + 1);
+        if (C + 1 < nC) load(cur ^ 1, C + 1);
+        // the rows' headers: this half's four (scale, min) pairs
+        float dr[RTW], bmin[RTW];
+        uint32_t scr[RTW];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
+        for (int r = 0; r < RTW; ++r) {
+            const uint32_t scb[3] = {hd[cur][r].y, hd[cur][r].z, hd[cur][r].w};
+            uint32_t sc4[2], mn4[2];
+            q4k_sm4(scb, sc4, mn4);
+            scr[r] = h ? sc4[1] : sc4[0];
+            dr[r] = h2f(hd[cur][r].x & 0xFFFF);
+            bmin[r] = h2f(hd[cur][r].x >> 16) * (float)(((h ? mn4[1] : mn4[0]) >> (8 * g)) & 0xFFu);
+        }
+        // min term on the fp32 matrix core
+#pragma unroll
+        for (int t = 0; t < TTW; ++t) {
+            const float am = -dm_s[cur][g][(wt * TTW + t) * 16 + row];
+#pragma unroll
+            for (int r = 0; r < RTW; ++r)
+                accm[t][r] = __builtin_amdgcn_mfma_f32_16x16x4f32(am, bmin[r], accm[t][r], 0, 0, 0);
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
             long A[TTW], Bq[RTW];
-            float dsc[RTW], dmn[RTW];
-#pragma unroll
-            for (int r = 0; r < RTW; ++r) {
-                const uint32_t scb[3] = {hd[cur][r].y, hd[cur][r].z, hd[cur][r].w};
-                uint32_t sc, mn;
-                q4k_sm(scb, s, sc, mn);
-                dsc[r] = h2f(hd[cur][r].x & 0xFFFF) * (float)sc;
-                dmn[r] = h2f(hd[cur][r].x >> 16) * (float)mn;
-            }
+            float dsc[RTW];
 #pragma unroll
             for (int t = 0; t < TTW; ++t) {
                 const u32x4 v = a[cur][t][s >> 1];
@@ -309,46 +335,43 @@ __global__ __launch_bounds__(256) void k_gemm_q4_K(const uint8_t* __restrict__ W
             }
 #pragma unroll
             for (int r = 0; r < RTW; ++r) {
-                const u32x4 v = b[cur][r][s >> 2];
-                const uint32_t q = (s & 3) == 0 ? v.x : (s & 3) == 1 ? v.y : (s & 3) == 2 ? v.z : v.w;
+                dsc[r] = dr[r] * ubyte_f(scr[r], s);
+                const u32x4 v = b[cur][r];
+                const uint32_t q = s == 0 ? v.x : s == 1 ? v.y : s == 2 ? v.z : v.w;
                 Bq[r] = gpack2(q & 0x0F0F0F0Fu, (q >> 4) & 0x0F0F0F0Fu);
             }
 #pragma unroll
             for (int t = 0; t < TTW; ++t) {
                 const int tb = (wt * TTW + t) * 16 + 4 * g;
                 const float4 d4 = *(const float4*)&dx_s[cur][s][tb];
-                const float4 m4 = *(const float4*)&dm_s[cur][s][tb];
                 const float dxe[4] = {d4.x, d4.y, d4.z, d4.w};
-                const float dme[4] = {m4.x, m4.y, m4.z, m4.w};
 #pragma unroll
                 for (int r = 0; r < RTW; ++r) {
                     const v4i z = {0, 0, 0, 0};
                     const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[t], Bq[r], z, 0, 0, 0);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        acc[t][r][e] = fmaf((float)c[e], dxe[e] * dsc[r], acc[t][r][e]);
-                        acc[t][r][e] = fmaf(-dmn[r], dme[e], acc[t][r][e]);
-                    }
+                    for (int e = 0; e < 4; ++e) acc[t][r][e] = fmaf((float)c[e], dxe[e] * dsc[r], acc[t][r][e]);
                 }
             }
         }
     };
     load(0, 0);
-    for (uint32_t B = 0; B < nB; B += 2) {
-        step(std::integral_constant<int, 0>{}, B);
-        if (B + 1 < nB) step(std::integral_constant<int, 1>{}, B + 1);
+    for (uint32_t C = 0; C < nC; C += 2) {
+        step(std::integral_constant<int, 0>{}, C);
+        step(std::integral_constant<int, 1>{}, C + 1);  // nC is even
     }
 #pragma unroll
     for (int t = 0; t < TTW; ++t)
 #pragma unroll
         for (int r = 0; r < RTW; ++r) {
-            const uint32_t n = 16 * (rt0 + r) + (lane & 15);
+            const uint32_t n = 16 * (rt0 + r) + row;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const uint32_t m = 16 * (tt0 + t) + 4 * g + e;
                 if (m < M && n < N && tt0 + t < n_tt && rt0 + r < n_rt) {
                     float* dst = y + (size_t)m * ldy + n;
-                    *dst = accumulate ? *dst + acc[t][r][e] : acc[t][r][e];
+                    const float v = acc[t][r][e] + accm[t][r][e];
+                    *dst = accumulate ? *dst + v : v;
                 }
             }
         }
@@ -391,15 +414,36 @@ extern "C" int ec_gemm(int fmt, const void* tiled, const void* act, float* y, ui
     const uint32_t n_tt = L.Mp / 16, n_rt = round_up(N, 16) / 16, nbp = L.Kp / 32;
     const uint32_t gy = (n_tt + 3) / 4;
     hipStream_t st = (hipStream_t)stream;
-    // 64 tokens x 64 rows per workgroup: with the epilogue as the bottleneck,
-    // two waves per SIMD (<= 256 registers) beat larger register tiles
+    // 64 tokens x 64 rows per workgroup (RTW = 2): with the epilogue as the
+    // bottleneck, two waves per SIMD (<= 256 registers) beat larger register
+    // tiles.  Q4_K takes RTW = 1 (64 x 32, three waves per SIMD) where RTW = 2
+    // leaves fewer than 1024 workgroups (M = 512, 2560 x 9216: 116.7 -> 104.2
+    // us; Q8_0 there 81.9 -> 84.5, so Q8_0 keeps RTW = 2).  EC_GEMM_RTW = 1 or
+    // 2 forces one, for comparison.
+    static const int rtw_env = [] {
+        const char* v = getenv("EC_GEMM_RTW");
+        return v ? atoi(v) : 0;
+    }();
+    const int rtw = rtw_env == 1 || rtw_env == 2       ? rtw_env
+                    : fmt == EC_Q4_K && (n_rt + 3) / 4 * gy < 1024 ? 1
+                                                                    : 2;
+    const dim3 blk(256);
     if (fmt == EC_Q8_0) {
-        hipLaunchKernelGGL(k_gemm_q8_0<2>, dim3((n_rt + 3) / 4, gy), dim3(256), 0, st, (const uint8_t*)tiled,
-                           (const uint8_t*)act, y, M, N, n_tt, n_rt, L.nch, nbp, L.xd_off, ldy, accumulate);
+        if (rtw == 1)
+            hipLaunchKernelGGL(k_gemm_q8_0<1>, dim3((n_rt + 1) / 2, gy), blk, 0, st, (const uint8_t*)tiled,
+                               (const uint8_t*)act, y, M, N, n_tt, n_rt, L.nch, nbp, L.xd_off, ldy, accumulate);
+        else
+            hipLaunchKernelGGL(k_gemm_q8_0<2>, dim3((n_rt + 3) / 4, gy), blk, 0, st, (const uint8_t*)tiled,
+                               (const uint8_t*)act, y, M, N, n_tt, n_rt, L.nch, nbp, L.xd_off, ldy, accumulate);
     } else {
-        hipLaunchKernelGGL(k_gemm_q4_K<2>, dim3((n_rt + 3) / 4, gy), dim3(256), 0, st, (const uint8_t*)tiled,
-                           (const uint8_t*)act, y, M, N, n_tt, n_rt, L.nch, nbp, L.xd_off, L.dxs_off, ldy,
-                           accumulate);
+        if (rtw == 1)
+            hipLaunchKernelGGL(k_gemm_q4_K<1>, dim3((n_rt + 1) / 2, gy), blk, 0, st, (const uint8_t*)tiled,
+                               (const uint8_t*)act, y, M, N, n_tt, n_rt, L.nch, nbp, L.xd_off, L.dxs_off, ldy,
+                               accumulate);
+        else
+            hipLaunchKernelGGL(k_gemm_q4_K<2>, dim3((n_rt + 3) / 4, gy), blk, 0, st, (const uint8_t*)tiled,
+                               (const uint8_t*)act, y, M, N, n_tt, n_rt, L.nch, nbp, L.xd_off, L.dxs_off, ldy,
+                               accumulate);
     }
     EC_CHECK_LAUNCH();
     return EC_OK;
