@@ -247,10 +247,12 @@ __device__ __forceinline__ float ubyte_f(uint32_t v, int n) { return (float)((v 
 // is a dense fp32 product with contraction over the sub-blocks: one
 // v_mfma_f32_16x16x4_f32 per (token tile, row tile) and step (A = -dxs[token]
 // [4h + k], B = (dmin*m)[4h + k][row]; lane l holds A[l%16][l/16] and
-// B[l/16][l%16], its D layout the int8 MFMA's) into accumulators of its own
-// (added to the others at the end), so the per-(token, row, sub-block)
-// epilogue is the Q8_0 kernel's: one conversion and one FMA per output
-// element.
+// B[l/16][l%16], its D layout the int8 MFMA's) into the same accumulators,
+// once per step, so the running sums stay at the result's magnitude (the min
+// and scale terms, each larger than the result, cancel every 4 sub-blocks as
+// in the reference's per-sub-block form), and the per-(token, row,
+// sub-block) epilogue is the Q8_0 kernel's: one conversion and one FMA per
+// output element.
 template <int RTW>
 __global__ __launch_bounds__(256, 2) void k_gemm_q4_K(const uint8_t* __restrict__ W, const uint8_t* __restrict__ xt,
                                                       float* __restrict__ y, uint32_t M, uint32_t N, uint32_t n_tt,
@@ -267,11 +269,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q4_K(const uint8_t* __restrict_
     const uint32_t tok = blockIdx.y * 64 + (threadIdx.x & 63), sq = threadIdx.x >> 6;  // stages sub-block sq
     const uint32_t nC = 2 * nB;  // half super-blocks
 
-    v4f acc[TTW][RTW], accm[TTW][RTW];
+    v4f acc[TTW][RTW];
 #pragma unroll
     for (int t = 0; t < TTW; ++t)
 #pragma unroll
-        for (int r = 0; r < RTW; ++r) acc[t][r] = accm[t][r] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int r = 0; r < RTW; ++r) acc[t][r] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
     u32x4 a[2][TTW][2], b[2][RTW], hd[2][RTW];
     float sv[2][2];
@@ -322,7 +324,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q4_K(const uint8_t* __restrict_
             const float am = -dm_s[cur][g][(wt * TTW + t) * 16 + row];
 #pragma unroll
             for (int r = 0; r < RTW; ++r)
-                accm[t][r] = __builtin_amdgcn_mfma_f32_16x16x4f32(am, bmin[r], accm[t][r], 0, 0, 0);
+                acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x4f32(am, bmin[r], acc[t][r], 0, 0, 0);
         }
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
@@ -370,8 +372,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q4_K(const uint8_t* __restrict_
                 const uint32_t m = 16 * (tt0 + t) + 4 * g + e;
                 if (m < M && n < N && tt0 + t < n_tt && rt0 + r < n_rt) {
                     float* dst = y + (size_t)m * ldy + n;
-                    const float v = acc[t][r][e] + accm[t][r][e];
-                    *dst = accumulate ? *dst + v : v;
+                    *dst = accumulate ? *dst + acc[t][r][e] : acc[t][r][e];
                 }
             }
         }
