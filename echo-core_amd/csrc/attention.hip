@@ -199,9 +199,9 @@ __global__ __launch_bounds__(64) void k_attn_combine(const float* __restrict__ w
 // One workgroup of four waves owns a 64-position (or 128-position) chunk of
 // one kv head for all G query heads of its GQA group and writes one partial
 // (max / sum / output) per head.  Wave w scores positions 16w .. 16w+15 (+64q)
-// and stages their V rows in LDS, transposed to [dim][position]; wave 0 takes
-// the softmax over the chunk and splits probability x V row scale into three
-// int8 pieces per head the same way; softmax(.)V then runs on the same MFMA,
+// and stages their V rows in LDS, transposed to [dim][position]; wave g takes
+// the softmax of head g over the chunk and splits probability x V row scale
+// into three int8 pieces the same way; softmax(.)V then runs on the same MFMA,
 // wave w producing dims 64w .. 64w+63 as exact int32 sums per piece.
 //
 // Packed q layout: layout.hpp (store_q_pieces).
@@ -361,60 +361,52 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ q
     }
     __syncthreads();
 
-    // ---- softmax over the chunk (wave 0, lane = positions lane + 64q)
+    // ---- softmax over the chunk: wave g takes head g (lane = positions lane
+    // + 64q); it reads score rows g, G+g, 2G+g and writes its probability
+    // pieces over row g only, so the waves touch disjoint rows
     constexpr float scale = 1.0f / 16.0f;  // 1/sqrt(256)
-    if (wv == 0) {
-        float m[G], l[G];
-        float pr[NPW][G];
+    if (wv < (uint32_t)G) {
+        const uint32_t g = wv;
+        float sc[NPW], pr[NPW], mx = -INFINITY;
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float sc[NPW], mx = -INFINITY;
-#pragma unroll
-            for (int q = 0; q < NPW; ++q) {
-                const uint32_t tl = 64 * q + lane;
-                const float raw = (part_s[g][tl] + part_s[G + g][tl]) + part_s[2 * G + g][tl];
-                sc[q] = tl < ntok ? raw * scale : -INFINITY;
-                mx = fmaxf(mx, sc[q]);
-            }
-            m[g] = wave_max(mx);
-            float es = 0.0f;
-#pragma unroll
-            for (int q = 0; q < NPW; ++q) {
-                const float e = 64 * q + lane < ntok ? __expf(sc[q] - m[g]) : 0.0f;
-                es += e;
-                pr[q][g] = e * vsv[q];
-            }
-            l[g] = wave_sum(es);
+        for (int q = 0; q < NPW; ++q) {
+            const uint32_t tl = 64 * q + lane;
+            const float raw = (part_s[g][tl] + part_s[G + g][tl]) + part_s[2 * G + g][tl];
+            sc[q] = tl < ntok ? raw * scale : -INFINITY;
+            mx = fmaxf(mx, sc[q]);
         }
-        // probabilities x V row scale as three int8 pieces per head (as q):
-        // A rows 4g + piece, bytes in the slot order of vT (part_s is free now)
+        const float m = wave_max(mx);
+        float es = 0.0f;
+#pragma unroll
+        for (int q = 0; q < NPW; ++q) {
+            const float e = 64 * q + lane < ntok ? __expf(sc[q] - m) : 0.0f;
+            es += e;
+            pr[q] = e * vsv[q];
+        }
+        const float l = wave_sum(es);
+        // probabilities x V row scale as three int8 pieces (as q): A rows
+        // 4g + piece, bytes in the slot order of vT (over score row g)
         uint8_t* pA = (uint8_t*)&part_s[0][0];
         const uint32_t rr = lane & 15;
+        float pm = 0.0f;
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float mx = 0.0f;
+        for (int q = 0; q < NPW; ++q) pm = fmaxf(pm, pr[q]);
+        pm = wave_max(pm);
 #pragma unroll
-            for (int q = 0; q < NPW; ++q) mx = fmaxf(mx, pr[q][g]);
-            mx = wave_max(mx);
+        for (int q = 0; q < NPW; ++q) {
+            const uint32_t byte = 4 * (16 * q + 4 * (lane >> 4) + (rr & 3)) + (rr >> 2);
+            int8_t pcs[kQPieces];
+            float steps[kQPieces];
+            split_pieces(pr[q], pm, pcs, steps);
 #pragma unroll
-            for (int q = 0; q < NPW; ++q) {
-                const uint32_t byte = 4 * (16 * q + 4 * (lane >> 4) + (rr & 3)) + (rr >> 2);
-                int8_t pcs[kQPieces];
-                float steps[kQPieces];
-                split_pieces(pr[q][g], mx, pcs, steps);
-#pragma unroll
-                for (uint32_t pc = 0; pc < kQPieces; ++pc) {
-                    pA[(4 * g + pc) * CH + byte] = (uint8_t)pcs[pc];
-                    if (lane == 0 && q == 0) psc_s[g][pc] = steps[pc];
-                }
+            for (uint32_t pc = 0; pc < kQPieces; ++pc) {
+                pA[(4 * g + pc) * CH + byte] = (uint8_t)pcs[pc];
+                if (lane == 0 && q == 0) psc_s[g][pc] = steps[pc];
             }
         }
         if (lane == 0) {
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float* rec = ws + (((size_t)s * n_chunks_max + chunk) * n_heads + kvh + n_kv * g) * kRec64;
-                *(float4*)rec = make_float4(m[g], l[g], 0.0f, 0.0f);
-            }
+            float* rec = ws + (((size_t)s * n_chunks_max + chunk) * n_heads + kvh + n_kv * g) * kRec64;
+            *(float4*)rec = make_float4(m, l, 0.0f, 0.0f);
         }
     }
     __syncthreads();
