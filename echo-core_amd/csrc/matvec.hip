@@ -490,6 +490,105 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
     if constexpr (!DOTS) reduce_store<R, P, 1>(acc4, red, y, t, M, N, ldy, accumulate);
 }
 
+// Lane 16*(lane/16) + K's value in every lane of its 16-lane row (DPP
+// row_newbcast:K).
+template <int K>
+__device__ __forceinline__ uint32_t row_bcast(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x150 + K, 0xF, 0xF, false);
+}
+
+// M = 1, one activation piece, without LDS staging: the k_mv_q4_K<1, 1>
+// arithmetic (every MFMA A row carries the token, lane group g applies the
+// epilogue of sub-blocks g and 4+g, the groups' partials added at the end)
+// with the activation operand fetched once per wave: lane l loads dword l of
+// the super-block's 256 activation bytes (one coalesced 256-byte load), and
+// lane group g, whose A operand is dwords 16g .. 16g+15 -- exactly the
+// dwords its own 16-lane row loaded -- takes them with 16 row broadcasts.
+// The group's two sub-block scales and d_x*sum values are loaded per lane.
+// Loads are issued activation first, weights after, all before any compute
+// (no branch: a clamped index past the range reads the last super-block and
+// enters with d = dmin = 0).
+template <int GPW>
+__global__ __launch_bounds__(1024) void k_mv_q4_K_m1(const uint8_t* __restrict__ W, const uint8_t* __restrict__ act,
+                                                     float* __restrict__ y, uint32_t N, uint32_t nB, uint32_t xd_off,
+                                                     uint32_t dxs_off, int accumulate) {
+    extern __shared__ float lds[];  // [nw][16] wave partials
+    const uint32_t t = blockIdx.x, lane = threadIdx.x & 63, row = lane & 15, g = lane >> 4;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
+    const uint8_t* wt = W + (size_t)t * nB * kQ4TChunk;
+    const float* xd = (const float*)(act + xd_off);   // token 0's sub-block scales
+    const float* xm = (const float*)(act + dxs_off);  // token 0's d_x * sum(q) per sub-block
+    float acc = 0.0f;
+    for (uint32_t B0 = w * GPW; B0 < nB; B0 += nw * GPW) {
+        uint32_t bb[GPW];
+#pragma unroll
+        for (int u = 0; u < GPW; ++u) bb[u] = min(B0 + u, nB - 1);
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t av[GPW];
+        float dxa[GPW], dxb[GPW], dma[GPW], dmb[GPW];
+#pragma unroll
+        for (int u = 0; u < GPW; ++u) {
+            av[u] = ((const uint32_t*)(act + (size_t)bb[u] * 256))[lane];
+            dxa[u] = xd[8 * bb[u] + g], dxb[u] = xd[8 * bb[u] + 4 + g];
+            dma[u] = xm[8 * bb[u] + g], dmb[u] = xm[8 * bb[u] + 4 + g];
+        }
+        __builtin_amdgcn_sched_barrier(0);  // activation loads complete first (in-order returns)
+        uint4 q0[GPW], q1[GPW], hdr[GPW];
+#pragma unroll
+        for (int u = 0; u < GPW; ++u) {
+            const uint8_t* ch = wt + (size_t)bb[u] * kQ4TChunk;
+            q0[u] = ld_stream16(ch + lane * 16);
+            q1[u] = ld_stream16(ch + 1024 + lane * 16);
+            hdr[u] = ld_stream16(ch + 2048 + row * 16);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // every load of the pass before any compute
+#pragma unroll
+        for (int u = 0; u < GPW; ++u) {
+            const bool live = B0 + u < nB;
+            const uint32_t aw[16] = {row_bcast<0>(av[u]),  row_bcast<1>(av[u]),  row_bcast<2>(av[u]),
+                                     row_bcast<3>(av[u]),  row_bcast<4>(av[u]),  row_bcast<5>(av[u]),
+                                     row_bcast<6>(av[u]),  row_bcast<7>(av[u]),  row_bcast<8>(av[u]),
+                                     row_bcast<9>(av[u]),  row_bcast<10>(av[u]), row_bcast<11>(av[u]),
+                                     row_bcast<12>(av[u]), row_bcast<13>(av[u]), row_bcast<14>(av[u]),
+                                     row_bcast<15>(av[u])};
+            const uint32_t qw[8] = {q0[u].x, q0[u].y, q0[u].z, q0[u].w, q1[u].x, q1[u].y, q1[u].z, q1[u].w};
+            int dot[8];
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const uint32_t lo = qw[s] & 0x0F0F0F0Fu, hi = (qw[s] >> 4) & 0x0F0F0F0Fu;
+                dot[s] = mfma_i8(pack2(aw[2 * s], aw[2 * s + 1]), pack2(lo, hi))[0];
+            }
+            const int da = g == 0 ? dot[0] : g == 1 ? dot[1] : g == 2 ? dot[2] : dot[3];
+            const int db = g == 0 ? dot[4] : g == 1 ? dot[5] : g == 2 ? dot[6] : dot[7];
+            const uint32_t scb[3] = {hdr[u].y, hdr[u].z, hdr[u].w};
+            uint32_t sc4[2], mn4[2];
+            q4k_scale_min4(scb, sc4, mn4);
+            const uint32_t sh = 8 * g;
+            float a_sc = (float)da * ((float)((sc4[0] >> sh) & 0xFFu) * dxa[u]);
+            a_sc = fmaf((float)db, (float)((sc4[1] >> sh) & 0xFFu) * dxb[u], a_sc);
+            float a_mn = (float)((mn4[0] >> sh) & 0xFFu) * dma[u];
+            a_mn = fmaf((float)((mn4[1] >> sh) & 0xFFu), dmb[u], a_mn);
+            const float d = live ? h2f(hdr[u].x & 0xFFFF) : 0.0f, dmin = live ? h2f(hdr[u].x >> 16) : 0.0f;
+            acc = fmaf(d, a_sc, acc);
+            acc = fmaf(-dmin, a_mn, acc);
+        }
+    }
+    acc = sum_lane_groups(acc);
+    const uint32_t n = 16 * t + row;
+    if (nw == 1) {
+        if (lane < 16 && n < N) y[n] = accumulate ? y[n] + acc : acc;
+        return;
+    }
+    if (lane < 16) lds[w * 16 + lane] = acc;
+    __syncthreads();
+    if (threadIdx.x < 16 && 16 * t + threadIdx.x < N) {
+        const uint32_t nn = 16 * t + threadIdx.x;
+        float s = lds[threadIdx.x];
+        for (uint32_t v = 1; v < nw; ++v) s += lds[v * 16 + threadIdx.x];
+        y[nn] = accumulate ? y[nn] + s : s;
+    }
+}
+
 // ------------------------------------------------ reference-semantics fp32 path
 int gguf_mv_fast(int fmt, const uint8_t* W, const float* x, float* y, uint32_t M, uint32_t K, hipStream_t st);
 
@@ -751,6 +850,17 @@ static void launch_q4_g(const void* W, const void* act, float* y, int32_t* dots,
                        accumulate);
 }
 
+// M = 1 with one piece: the activation operand by row broadcasts instead of
+// LDS staging (k_mv_q4_K_m1; EC_MV_Q4_M1=staged selects k_mv_q4_K, for
+// comparison).
+static bool q4_m1_direct() {
+    static bool v = [] {
+        const char* e = getenv("EC_MV_Q4_M1");
+        return !(e && strcmp(e, "staged") == 0);
+    }();
+    return v;
+}
+
 template <int MT, int P, bool DOTS>
 static void launch_q4(const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N, uint32_t K,
                       uint32_t ldy, int accumulate, hipStream_t st) {
@@ -758,6 +868,23 @@ static void launch_q4(const void* W, const void* act, float* y, int32_t* dots, u
     int gpw;
     uint32_t nw;
     plan(nT, nB, MT == 1 ? 3 : 1, gpw, nw, target_waves_q4());
+    if constexpr (MT == 1 && P == 1 && !DOTS) {
+        if (q4_m1_direct()) {
+            const ActLayout L = act_layout(EC_Q4_K, 1, K);
+            const size_t lds = (size_t)nw * 16 * sizeof(float);
+            switch (gpw) {
+#define EC_Q4M1(G)                                                                                          \
+    hipLaunchKernelGGL((k_mv_q4_K_m1<G>), dim3(nT), dim3(64 * nw), lds, st, (const uint8_t*)W, (const uint8_t*)act, \
+                       y, N, nB, (uint32_t)L.xd_off, (uint32_t)L.dxs_off, accumulate);                   \
+    break;
+                case 1: EC_Q4M1(1)
+                case 2: EC_Q4M1(2)
+                default: EC_Q4M1(3)
+#undef EC_Q4M1
+            }
+            return;
+        }
+    }
     switch (gpw) {
         case 1: launch_q4_g<MT, P, DOTS, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
         case 2: launch_q4_g<MT, P, DOTS, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
