@@ -309,6 +309,104 @@ __global__ __launch_bounds__(1024) void k_mv_q8_0(const uint8_t* __restrict__ W,
     if constexpr (!DOTS) reduce_store<R, P, TPW>(acc, red, y + sp * split_stride, t0, M, N, ldy, accumulate);
 }
 
+// Sum of v over lanes l, l^16, l^32, l^48, in every lane: v_permlane32_swap
+// pairs lanes 0-31 with 32-63 and v_permlane16_swap odd with even 16-lane
+// rows, each returning both halves; every lane adds the same two operands.
+__device__ __forceinline__ float sum_lane_groups(float v) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Lane 16*(lane/16) + K's value in every lane of its 16-lane row (DPP
+// row_newbcast:K).
+template <int K>
+__device__ __forceinline__ uint32_t row_bcast(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x150 + K, 0xF, 0xF, false);
+}
+
+// M = 1, one piece, one K range (the decode matvec of a single sequence):
+// every MFMA A row carries the token, so every lane holds its weight row's
+// four block dots of a chunk, and lane group g applies the epilogue of block
+// g only (one conversion, scale and FMA per chunk instead of four), the four
+// groups' partials added once at the end.  The activation operand skips LDS:
+// lane 16g + k loads dword k % 8 of group g's 32 bytes in chunk G0 + k/8 (a
+// wave's loads cover two chunks with no repeated byte), and lane group g's
+// operand for a chunk -- those 8 dwords -- is what its own 16-lane row loaded,
+// taken with row broadcasts.  Loads: activation and scales first, weights
+// after, all before any compute (a clamped index past the range reads the
+// last chunk again and enters with a zero scale).
+template <int GPW>
+__global__ __launch_bounds__(1024) void k_mv_q8_0_m1(const uint8_t* __restrict__ W, const uint8_t* __restrict__ act,
+                                                     float* __restrict__ y, uint32_t N, uint32_t nG, uint32_t xd_off,
+                                                     int accumulate) {
+    extern __shared__ float lds[];  // [nw][16] wave partials
+    constexpr int NPAIR = (GPW + 1) / 2;
+    const uint32_t t = blockIdx.x, lane = threadIdx.x & 63, row = lane & 15, g = lane >> 4;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
+    const uint8_t* wt = W + (size_t)t * nG * kQ8TChunk;
+    const float* xd = (const float*)(act + xd_off);  // token 0's block scales
+    const uint32_t* a32 = (const uint32_t*)act;
+    float acc = 0.0f;
+    for (uint32_t G0 = w * GPW; G0 < nG; G0 += nw * GPW) {
+        uint32_t av[NPAIR];
+        float dxg[GPW];
+#pragma unroll
+        for (int pr = 0; pr < NPAIR; ++pr) {
+            const uint32_t G = min(G0 + 2 * pr + (row >> 3), nG - 1);
+            av[pr] = a32[(4 * G + g) * 8 + (row & 7)];
+        }
+#pragma unroll
+        for (int u = 0; u < GPW; ++u) dxg[u] = xd[4 * min(G0 + u, nG - 1) + g];
+        __builtin_amdgcn_sched_barrier(0);  // activation loads complete first (in-order returns)
+        uint4 b01[GPW], b23[GPW];
+        uint2 dw[GPW];
+#pragma unroll
+        for (int u = 0; u < GPW; ++u) {
+            const uint8_t* ch = wt + (size_t)min(G0 + u, nG - 1) * kQ8TChunk;
+            b01[u] = ld_stream16(ch + lane * 16);
+            b23[u] = ld_stream16(ch + 1024 + lane * 16);
+            dw[u] = ld_stream8(ch + 2048 + row * 8);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // every load of the pass before any compute
+#pragma unroll
+        for (int u = 0; u < GPW; ++u) {
+            const uint32_t v = av[u / 2];
+            uint32_t aw[8];  // the chunk's 8 dwords: lanes 8 (u % 2) .. +7 of the row
+#define EC_BC(i) aw[i] = (u & 1) ? row_bcast<8 + i>(v) : row_bcast<i>(v);
+            EC_BC(0) EC_BC(1) EC_BC(2) EC_BC(3) EC_BC(4) EC_BC(5) EC_BC(6) EC_BC(7)
+#undef EC_BC
+            const long B[4] = {pack2(b01[u].x, b01[u].y), pack2(b01[u].z, b01[u].w), pack2(b23[u].x, b23[u].y),
+                               pack2(b23[u].z, b23[u].w)};
+            int dot[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dot[j] = mfma_i8(pack2(aw[2 * j], aw[2 * j + 1]), B[j])[0];
+            const int dg = g == 0 ? dot[0] : g == 1 ? dot[1] : g == 2 ? dot[2] : dot[3];
+            // block g's fp16 scale, by masks (a select on g becomes a stack-indexed load)
+            const uint32_t hm = (g & 2) ? 0xFFFFFFFFu : 0u;
+            const uint32_t h = dw[u].x ^ ((dw[u].x ^ dw[u].y) & hm);
+            const float dwf = h2f((uint16_t)(h >> (16 * (g & 1))));
+            const float dx = G0 + u < nG ? dxg[u] : 0.0f;
+            acc = fmaf((float)dg, dwf * dx, acc);
+        }
+    }
+    acc = sum_lane_groups(acc);
+    const uint32_t n = 16 * t + row;
+    if (nw == 1) {
+        if (lane < 16 && n < N) y[n] = accumulate ? y[n] + acc : acc;
+        return;
+    }
+    if (lane < 16) lds[w * 16 + lane] = acc;
+    __syncthreads();
+    if (threadIdx.x < 16 && 16 * t + threadIdx.x < N) {
+        const uint32_t nn = 16 * t + threadIdx.x;
+        float sm = lds[threadIdx.x];
+        for (uint32_t v = 1; v < nw; ++v) sm += lds[v * 16 + threadIdx.x];
+        y[nn] = accumulate ? y[nn] + sm : sm;
+    }
+}
+
 // --------------------------------------------------------------------- Q4_K
 // The eight 6-bit (scale, min) pairs of a super-block from its 12 scale bytes
 // (q[0] = bytes 0-3, ...), four per dword: sc[0] holds sub-blocks 0-3 (byte s
@@ -333,15 +431,6 @@ __device__ __forceinline__ void q4k_scale_min(const uint32_t (&q)[3], int s, uin
     }
 }
 
-// Sum of v over lanes l, l^16, l^32, l^48, in every lane: v_permlane32_swap
-// pairs lanes 0-31 with 32-63 and v_permlane16_swap odd with even 16-lane
-// rows, each returning both halves; every lane adds the same two operands.
-__device__ __forceinline__ float sum_lane_groups(float v) {
-    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
 
 // M = 1 (the epilogue split, !DOTS): one token leaves 15 of the MFMA's 16 A
 // rows free, so every A row carries the token (row r: layout row r % P, i.e.
@@ -490,12 +579,6 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
     if constexpr (!DOTS) reduce_store<R, P, 1>(acc4, red, y, t, M, N, ldy, accumulate);
 }
 
-// Lane 16*(lane/16) + K's value in every lane of its 16-lane row (DPP
-// row_newbcast:K).
-template <int K>
-__device__ __forceinline__ uint32_t row_bcast(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x150 + K, 0xF, 0xF, false);
-}
 
 // M = 1, one activation piece, without LDS staging: the k_mv_q4_K<1, 1>
 // arithmetic (every MFMA A row carries the token, lane group g applies the
@@ -799,6 +882,16 @@ static void launch_q8_g(const void* W, const void* act, float* y, int32_t* dots,
 // nsplit > 1 (<= the 128-element chunks of K): the K range is cut into
 // nsplit balanced chunk ranges, one workgroup per (tile, range), partial sums
 // to y + sp*M*ldy.
+// M = 1 with one piece and one K range: k_mv_q8_0_m1 (EC_MV_Q8_M1=staged
+// selects k_mv_q8_0, for comparison).
+static bool q8_m1_direct() {
+    static bool v = [] {
+        const char* e = getenv("EC_MV_Q8_M1");
+        return !(e && strcmp(e, "staged") == 0);
+    }();
+    return v;
+}
+
 template <int MT, int P, bool DOTS>
 static void launch_q8(const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N, uint32_t K,
                       uint32_t ldy, int accumulate, hipStream_t st, uint32_t nsplit = 1) {
@@ -814,6 +907,25 @@ static void launch_q8(const void* W, const void* act, float* y, int32_t* dots, u
     const uint32_t tpw = tpw_q8(P);
     constexpr int max_gpw = P == 1 || MT == 1 ? 5 : (MT == 16 ? 3 : 4);
     plan(nT * nsplit, cps, max_gpw, gpw, nw, target_waves_q8());
+    if constexpr (MT == 1 && P == 1 && !DOTS) {
+        if (nsplit == 1 && q8_m1_direct()) {
+            const ActLayout L = act_layout(EC_Q8_0, 1, K);
+            const size_t lds = (size_t)nw * 16 * sizeof(float);
+            switch (gpw) {
+#define EC_Q8M1(G)                                                                                            \
+    hipLaunchKernelGGL((k_mv_q8_0_m1<G>), dim3(nT), dim3(64 * nw), lds, st, (const uint8_t*)W, (const uint8_t*)act, \
+                       y, N, nG, (uint32_t)L.xd_off, accumulate);                                          \
+    break;
+                case 1: EC_Q8M1(1)
+                case 2: EC_Q8M1(2)
+                case 3: EC_Q8M1(3)
+                case 4: EC_Q8M1(4)
+                default: EC_Q8M1(5)
+#undef EC_Q8M1
+            }
+            return;
+        }
+    }
     if (tpw == 2) {
         const int g2 = min(tpw_full_gpw() ? gpw : (gpw + 1) / 2, 2);
         const uint32_t nw2 = min((cps + g2 - 1) / g2, 16u);

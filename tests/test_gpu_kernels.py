@@ -82,7 +82,8 @@ def _unpack(hip, fmt, act, M, K):
 
 # (16, 64, 9216): 72 chunks per tile at 16 tokens, where a workgroup's LDS
 # (waves x staged activation) must be capped below 160 KB.
-CASES = [(1, 48, 512), (3, 40, 384), (8, 64, 2560), (16, 16, 256), (5, 33, 1024), (16, 64, 9216)]
+CASES = [(1, 48, 512), (3, 40, 384), (8, 64, 2560), (16, 16, 256), (5, 33, 1024), (16, 64, 9216), (1, 40, 384),
+         (1, 16, 9216), (1, 24, 160)]
 
 
 @pytest.mark.parametrize("M,N,K", CASES)
