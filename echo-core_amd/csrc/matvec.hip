@@ -57,10 +57,12 @@ __device__ __forceinline__ uint32_t out_token(uint32_t g, uint32_t r) {
 }
 
 // Cross-wave reduction of the TPW tiles' acc[4] and the store of y /
-// accumulate.  Each wave parks its partials in LDS (red: [TPW][waves][256]);
-// then thread s (s < TPW*256) sums slot s%256 of tile s/256 over the waves in
-// wave order (deterministic) and stores it: slot = lane*4 + r, i.e. weight row
-// 16(t0 + tile) + lane%16, token out_token(lane/16, r).
+// accumulate.  Each wave parks its partials in LDS (red: [TPW][waves][R][64]);
+// then thread q (q < TPW*R*64) sums accumulator r of lane l of tile tt over
+// the waves in wave order (deterministic) and stores it: weight row
+// 16(t0 + tt) + l%16, token out_token(l/16, r).  Measured on the batch-8
+// decode step's 128 projections: 999 -> 990 us per step against a [..][lane][4]
+// layout (8-way LDS bank conflicts) summed one wave per LDS round trip.
 template <int R, int P, int TPW>
 __device__ __forceinline__ void reduce_store(float (&acc)[TPW][4], float* red, float* __restrict__ y, uint32_t t0,
                                              uint32_t M, uint32_t N, uint32_t ldy, int accumulate) {
@@ -81,17 +83,30 @@ __device__ __forceinline__ void reduce_store(float (&acc)[TPW][4], float* red, f
         }
         return;
     }
+    // red[tt][w][r][lane]: consecutive lanes touch consecutive dwords (no
+    // LDS bank conflicts on the writes or on the reads below)
 #pragma unroll
     for (int tt = 0; tt < TPW; ++tt)
-        for (int r = 0; r < R; ++r) red[((tt * nw + w) * 64 + lane) * 4 + r] = acc[tt][r];
+        for (int r = 0; r < R; ++r) red[((tt * nw + w) * R + r) * 64 + lane] = acc[tt][r];
     __syncthreads();
-    for (uint32_t q = threadIdx.x; q < 256 * TPW; q += blockDim.x) {  // tile q/256, slot lane' * 4 + r'
-        const uint32_t tt = q >> 8, sl = q & 255, ln = sl >> 2, r = sl & 3;
+    // thread q: tile q / (64R), accumulator (q / 64) % R of lane q % 64.  The
+    // waves' values are summed in wave order; their LDS reads are issued
+    // eight at a time (clamped to the last wave), not one round trip per wave:
+    // this sum is the tail of the workgroup, and of the launch.
+    for (uint32_t q = threadIdx.x; q < 64 * R * TPW; q += blockDim.x) {
+        const uint32_t ln = q & 63, r = (q >> 6) % R, tt = (q >> 6) / R;
         const uint32_t m = out_token<P>(ln >> 4, r), n = 16 * (t0 + tt) + (ln & 15);
-        if ((int)r >= R || m >= M || n >= N) continue;
-        const float* rt = red + (size_t)tt * nw * 256;
-        float s = rt[sl];
-        for (uint32_t v = 1; v < nw; ++v) s += rt[v * 256 + sl];
+        if (m >= M || n >= N) continue;
+        const float* rs = red + ((size_t)tt * nw * R + r) * 64 + ln;
+        float s = rs[0];
+        for (uint32_t v0 = 1; v0 < nw; v0 += 8) {
+            float x[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[i] = rs[min(v0 + i, nw - 1) * (64 * R)];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (v0 + i < nw) s += x[i];
+        }
         float* dst = y + (size_t)m * ldy + n;
         *dst = accumulate ? *dst + s : s;
     }
