@@ -6,19 +6,18 @@
 // instruction, and every weight needs its own fp32 multiply-add anyway.
 //
 // Thread layout: a workgroup owns R consecutive rows.  Each thread owns one
-// weight-block column of the row (Q8_0: one 32-element block; Q4_K: one
-// 64-element quarter of a super-block) and holds that column's activations in
-// registers for the workgroup's whole life; P threads share a column and take
-// every P-th row of the tile.  Per row a thread produces one partial sum,
-// parked in LDS; then a row's partials are added with lane exchanges (Q8_0: a
-// wave per row; Q4_K: a group of up to 64 threads per row) and one lane
-// accumulates the row into y.
+// 64-element column of the row (Q8_0: a pair of 32-element blocks; Q4_K: a
+// quarter of a super-block) and holds that column's activations in registers
+// for the workgroup's whole life; P threads share a column and take every
+// P-th row of the tile.  Per row a thread produces one partial sum, parked in
+// LDS; then a group of up to 64 threads adds a row's partials with lane
+// exchanges and one thread accumulates the row into y.
 //
-// Q8_0 (34-byte blocks, 2-byte aligned): the tile's bytes are one contiguous
-// range (rows are contiguous in GGUF), loaded with 16-byte coalesced loads
-// (non-temporal: every byte is used once) and staged in LDS, where each
-// thread reads its block at its 2-byte-aligned offset.  Needs K % 256 == 0 so
-// that rows start 16-byte aligned.
+// Q8_0 (34-byte blocks, 2-byte aligned; K % 64 == 0): a block pair is 68
+// bytes at a dword-aligned offset, loaded by its thread straight from HBM
+// (four 16-byte loads and a dword per row, lanes of a wave covering
+// consecutive pairs) with x staged in LDS as for Q4_K; each weight byte is
+// converted by its own byte select, so block 0's 2-byte offset costs nothing.
 // Q4_K (144-byte super-blocks, 16-byte aligned): each thread loads its own
 // 16-byte header and 32 bytes of nibbles straight from HBM for each of its
 // RPT rows (lanes of a wave cover consecutive 32-byte runs), all issued
@@ -62,22 +61,6 @@ __device__ __forceinline__ float sum_group(float v, uint32_t G) {
     return v;
 }
 
-// Rows' partial sums red[rr][0 .. ncol) -> y[r0 + rr] = y0[rr] + sum, one wave
-// per row.  y0 holds the rows' previous y values, read at kernel start (no
-// dependent global load at the end of the workgroup: 10.3 -> 9.9 us at
-// 9216 x 2560); nothing else writes these rows during the kernel.  (The
-// grouped row sums below measured 10.4 us here.)
-__device__ __forceinline__ void reduce_rows(const float* red, const float* y0, uint32_t ncol, uint32_t nr,
-                                            float* __restrict__ y, uint32_t r0) {
-    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
-    for (uint32_t rr = w; rr < nr; rr += nw) {
-        float s = 0.0f;
-        for (uint32_t c = lane; c < ncol; c += 64) s += red[rr * ncol + c];
-        s = wave_sum(s);
-        if (lane == 0) y[r0 + rr] = y0[rr] + s;
-    }
-}
-
 // Rows' values red[rr][0 .. ncol) -> y[r0 + rr] = yp + sum for rr < nr: the G
 // consecutive threads rr*G .. rr*G + G-1 (G a power of two <= 64, G * R <=
 // blockDim) add every G-th value, then exchange; thread rr*G stores.  yp is
@@ -96,58 +79,105 @@ __device__ __forceinline__ void row_sums_store(const float* red, uint32_t ncol, 
     if (t == G0 && rr < nr) y[r0 + rr] = yp + acc;
 }
 
-constexpr int kQ8Stage = 8;  // 16-byte tile chunks per thread (R rows x K/32*34 bytes <= 8 * 16 * threads)
+// Block-pair form (K % 64 == 0): thread column c owns blocks 2c and 2c + 1
+// of its rows, 68 bytes at a dword-aligned offset (the row stride nb * 34 is
+// a multiple of 4), loaded straight from memory as four 16-byte loads and a
+// dword per row, all RPT rows issued before any use.  Element j of block 0
+// is byte 2 + j of those 17 dwords and of block 1 byte 36 + j; each is
+// converted with its own byte select, so the 2-byte offset of block 0 costs
+// nothing.  x is staged in LDS once per workgroup (pairs of 64 floats 68
+// apart), read into registers by each thread for its column, and the rows'
+// pair values are summed by row_sums_store.  Issue order as in the Q4_K
+// kernel below: x's loads, the previous y, then the weights, all
+// unconditional, so the x staging and barrier overlap the weights' latency.
+constexpr uint32_t kQ8XStride = 68;  // floats per staged block pair (272 bytes)
 
-// grid.x = ceil(M / R); blockDim = P * nb (nb = K/32 blocks per row).  The
-// tile's bytes and the thread's 32 activations are all in flight before the
-// first use.
-__global__ __launch_bounds__(1024) void k_gguf_q8_0_f32(const uint8_t* __restrict__ W, const float* __restrict__ x,
-                                                        float* __restrict__ y, uint32_t M, uint32_t nb, uint32_t P,
-                                                        uint32_t R) {
+// Four rows' loads (68 registers) beside the 64 activations: RPT = 4 is
+// bounded at 768 threads like the Q4_K kernel.
+template <int RPT>
+constexpr int q8_f32_max_threads() { return RPT == 4 ? 768 : 1024; }
+
+size_t q8_f32_lds_bytes(uint32_t nc, uint32_t R) { return ((size_t)nc * kQ8XStride + (size_t)R * nc + 1) * 4; }
+
+typedef uint32_t gu32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+// nc_magic = ceil(2^32 / nc): t / nc == umulhi(t, nc_magic) for t, nc < 2^10.
+template <int RPT, int XPT>
+__global__ __launch_bounds__(q8_f32_max_threads<RPT>()) void k_gguf_q8_0_f32_pairs(
+    const uint8_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ y, uint32_t M, uint32_t nc,
+    uint32_t P, uint32_t R, uint32_t G, uint32_t nc_magic) {
     extern __shared__ uint8_t lds[];
     const uint32_t t = threadIdx.x, T = blockDim.x;
-    const uint32_t b = t % nb, ph = t / nb;
-    const size_t rowbytes = (size_t)nb * 34;
-    const uint32_t r0 = blockIdx.x * R, nr = min(R, M - r0);
-    float* red = (float*)(lds + ((R * rowbytes + 15) & ~(size_t)15));
-    float* y0 = red + (size_t)R * nb;  // previous y of the tile's rows (R <= blockDim.x)
-    const float yp = t < nr ? y[r0 + t] : 0.0f;
-    const uint8_t* src = W + (size_t)r0 * rowbytes;
-    const uint32_t n16 = (uint32_t)(nr * rowbytes / 16);
-    uint4 v[kQ8Stage];
+    float* xs = (float*)lds;
+    float* red = xs + (size_t)nc * kQ8XStride;  // [R][nc] + 1
+    const uint32_t ph0 = __umulhi(t, nc_magic), c = t - ph0 * nc;
+    const uint32_t ph = min(ph0, P - 1);  // padding threads: c < nc, ph0 >= P
+    const size_t rowbytes = (size_t)nc * 68;
+    const uint32_t r0 = blockIdx.x * R, nr = min(R, M - r0), n4 = 16 * nc;
+    float4 xf[XPT];  // float4s t, t + T, ... of x
 #pragma unroll
-    for (int i = 0; i < kQ8Stage; ++i) {
-        const uint32_t c = t + i * T;
-        v[i] = c < n16 ? ld_nt16(src + 16 * (size_t)c) : make_uint4(0u, 0u, 0u, 0u);
+    for (int j = 0; j < XPT; ++j) xf[j] = ((const float4*)x)[min(t + j * T, n4 - 1)];
+    const float yp = y[r0 + min(t / G, nr - 1)];
+    __builtin_amdgcn_sched_barrier(0);  // keep x's loads ahead of the weights'
+    uint32_t w[RPT][17];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+        const uint32_t rr = ph + i * P;
+        const uint8_t* bp = W + (size_t)(r0 + (rr < nr ? rr : 0)) * rowbytes + 68 * (size_t)c;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const gu32x4a4 v = *(const gu32x4a4*)(bp + 16 * k);
+            w[i][4 * k] = v.x, w[i][4 * k + 1] = v.y, w[i][4 * k + 2] = v.z, w[i][4 * k + 3] = v.w;
+        }
+        w[i][16] = *(const uint32_t*)(bp + 64);
     }
-    float xv[32];
-    const float4* xb = (const float4*)(x + 32 * b);
+    // x -> LDS: pair c (64 floats) at c * 68 floats; float4s past x's end go
+    // to the last pair's padding
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float4 f = xb[i];
+    for (int j = 0; j < XPT; ++j) {
+        const uint32_t c4 = t + j * T;
+        const uint32_t o = c4 < n4 ? (c4 / 16) * kQ8XStride + 4 * (c4 % 16) : (nc - 1) * kQ8XStride + 64;
+        *(float4*)(xs + o) = xf[j];
+    }
+    __syncthreads();
+    float xv[64];
+    const float4* xq = (const float4*)(xs + c * kQ8XStride);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float4 f = xq[i];
         xv[4 * i] = f.x, xv[4 * i + 1] = f.y, xv[4 * i + 2] = f.z, xv[4 * i + 3] = f.w;
     }
 #pragma unroll
-    for (int i = 0; i < kQ8Stage; ++i) {
-        const uint32_t c = t + i * T;
-        if (c < n16) *(uint4*)(lds + 16 * (size_t)c) = v[i];
-    }
-    __syncthreads();
-    for (uint32_t rr = ph; rr < nr; rr += P) {
-        const uint16_t* bp = (const uint16_t*)(lds + rr * rowbytes + 34 * (size_t)b);
-        const float d = h2f(bp[0]);
-        float bs = 0.0f;  // the block's sum in element order, as the reference's inner loop
+    for (int i = 0; i < RPT; ++i) {
+        // branch-free: a row past the tile's end (rr >= nr) sums row r0's
+        // bytes into the spare slot or a slot that is never read
+        const uint32_t rr = ph + i * P;
+        const float d0 = h2f(w[i][0] & 0xFFFF), d1 = h2f(w[i][8] >> 16);
+        // each block's sum in element order, as the reference's inner loop
+        float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const uint32_t w2 = bp[1 + k];
-            bs = fmaf((float)(int8_t)(w2 & 0xFF), xv[2 * k], bs);
-            bs = fmaf((float)(int8_t)(w2 >> 8), xv[2 * k + 1], bs);
+        for (int j = 0; j < 32; ++j) {
+            s0 = fmaf((float)(int8_t)(w[i][(2 + j) >> 2] >> (8 * ((2 + j) & 3))), xv[j], s0);
+            s1 = fmaf((float)(int8_t)(w[i][9 + (j >> 2)] >> (8 * (j & 3))), xv[32 + j], s1);
         }
-        red[rr * nb + b] = d * bs;
+        red[ph0 < P ? rr * nc + c : R * nc] = d0 * s0 + d1 * s1;
     }
-    if (t < nr) y0[t] = yp;
     __syncthreads();
-    reduce_rows(red, y0, nb, nr, y, r0);
+    row_sums_store(red, nc, nr, G, yp, y, r0);
+}
+
+template <int RPT>
+int launch_q8_f32_x(uint32_t xpt, dim3 grid, dim3 blk, size_t lds, hipStream_t st, const uint8_t* W, const float* x,
+                    float* y, uint32_t M, uint32_t nc, uint32_t P, uint32_t R, uint32_t G, uint32_t mg) {
+    switch (xpt) {
+        case 1: hipLaunchKernelGGL((k_gguf_q8_0_f32_pairs<RPT, 1>), grid, blk, lds, st, W, x, y, M, nc, P, R, G, mg); break;
+        case 2: hipLaunchKernelGGL((k_gguf_q8_0_f32_pairs<RPT, 2>), grid, blk, lds, st, W, x, y, M, nc, P, R, G, mg); break;
+        case 4: hipLaunchKernelGGL((k_gguf_q8_0_f32_pairs<RPT, 4>), grid, blk, lds, st, W, x, y, M, nc, P, R, G, mg); break;
+        case 8: hipLaunchKernelGGL((k_gguf_q8_0_f32_pairs<RPT, 8>), grid, blk, lds, st, W, x, y, M, nc, P, R, G, mg); break;
+        case 16: hipLaunchKernelGGL((k_gguf_q8_0_f32_pairs<RPT, 16>), grid, blk, lds, st, W, x, y, M, nc, P, R, G, mg); break;
+        default: return EC_ERR_UNSUPPORTED;
+    }
+    return EC_OK;
 }
 
 // grid.x = ceil(M / R), R = RPT * P rows; blockDim T = P * nq rounded up to
@@ -338,21 +368,49 @@ int gguf_mv_fast(int fmt, const uint8_t* W, const float* x, float* y, uint32_t M
         return v && v[0] == 'r';
     }();
     if (rows || ((uintptr_t)x & 15) || ((uintptr_t)W & 15)) return EC_ERR_UNSUPPORTED;
+    static const uint32_t rpt_env = [] {
+        const char* v = getenv("EC_GGUF_RPT");  // 1, 2 or 4: fixed rows per thread, for comparison
+        return v ? (uint32_t)atoi(v) : 0u;
+    }();
     if (fmt == EC_Q8_0) {
-        const uint32_t nb = K / 32;
-        if (K % 256 || nb > 1024) return EC_ERR_UNSUPPORTED;
-        uint32_t P = 64 / gcd32(nb, 64);  // P * nb a whole number of waves
-        while (P > 1 && P * nb > 1024) P /= 2;
-        const uint32_t T = P * nb;
-        const size_t rowbytes = (size_t)nb * 34;
-        // rows per workgroup: a multiple of P whose bytes fit the staging registers and ~48 KB of LDS
-        uint32_t R = P;
-        while ((R + P) * rowbytes <= (size_t)kQ8Stage * 16 * T && (R + P) * (rowbytes + 4 * nb) <= 48 * 1024) R += P;
-        if (R * rowbytes > (size_t)kQ8Stage * 16 * T) return EC_ERR_UNSUPPORTED;
-        const size_t lds = ((R * rowbytes + 15) & ~(size_t)15) + (size_t)R * nb * 4 + (size_t)R * 4;
-        if (R > T) return EC_ERR_UNSUPPORTED;
-        hipLaunchKernelGGL(k_gguf_q8_0_f32, dim3((M + R - 1) / R), dim3(T), lds, st, W, x, y, M, nb, P, R);
-        return EC_OK;
+        if (K % 64 || K / 64 > 1024) return EC_ERR_UNSUPPORTED;
+        const uint32_t nc = K / 64;  // block pairs per row
+        // threads per pair column: the smallest power of two that makes
+        // P * nc a whole number of waves and at least 512 threads (x staged
+        // once per workgroup for more rows); measured on MI355X (us, 9216 x
+        // 2560 / 2560 x 9216 / 12352 x 2560 / 2560 x 4096 / 6144 x 2560):
+        // 9.37 / 11.83 / 10.81 / 6.58 / 7.20 against 9.65 / 11.83 / 10.92 /
+        // 7.36 / 7.84 with the whole-waves minimum alone, and 9.86 / 13.66 /
+        // 12.77 / 6.63 / 8.34 for a kernel staging the tile's bytes in LDS
+        uint32_t P = 64 / gcd32(nc, 64);
+        while (P * nc < 512 && 2 * P * nc <= 1024) P *= 2;
+        while (P > 1 && P * nc > 1024) P /= 2;
+        static const uint32_t q8p_env = [] {
+            const char* v = getenv("EC_GGUF_Q8_P");  // threads per pair column (a power of two), for comparison
+            return v ? (uint32_t)atoi(v) : 0u;
+        }();
+        if (q8p_env && (q8p_env & (q8p_env - 1)) == 0 && q8p_env * nc <= 1024) P = q8p_env;
+        const uint32_t T = (P * nc + 63) / 64 * 64;
+        // rows per thread: 1 while that leaves at least 512 workgroups, 2
+        // while that leaves 128 (with 512-1024 threads per workgroup, 4 rows
+        // leave few workgroups: 2560 x 4096 9.0 us at 80 workgroups, 6.6 at
+        // 160 with 2 rows), else 4
+        const uint32_t wg1 = (M + P - 1) / P, wg2 = (M + 2 * P - 1) / (2 * P);
+        uint32_t rpt = wg1 >= 512 ? 1 : (wg2 >= 128 ? 2 : 4);
+        if (rpt == 4 && T > (uint32_t)q8_f32_max_threads<4>()) rpt = 2;
+        if ((rpt_env == 1 || rpt_env == 2 || rpt_env == 4) && T <= (rpt_env == 4 ? 768u : 1024u)) rpt = rpt_env;
+        const uint32_t R = rpt * P;
+        uint32_t xpt = 1;
+        while (xpt * T < 16 * nc) xpt *= 2;
+        uint32_t G = 64;  // threads per row in the row sums: a power of two with G * R <= T
+        while (G * R > T) G /= 2;
+        const size_t lds = q8_f32_lds_bytes(nc, R);
+        const uint32_t mg = (uint32_t)((((uint64_t)1 << 32) + nc - 1) / nc);
+        if (xpt > 16 || G < 1 || lds > 64 * 1024) return EC_ERR_UNSUPPORTED;
+        const dim3 grid((M + R - 1) / R), blk(T);
+        if (rpt == 4) return launch_q8_f32_x<4>(xpt, grid, blk, lds, st, W, x, y, M, nc, P, R, G, mg);
+        if (rpt == 2) return launch_q8_f32_x<2>(xpt, grid, blk, lds, st, W, x, y, M, nc, P, R, G, mg);
+        return launch_q8_f32_x<1>(xpt, grid, blk, lds, st, W, x, y, M, nc, P, R, G, mg);
     }
     if (fmt == EC_Q4_K) {
         const uint32_t nsb = K / 256, nq = 4 * nsb;
@@ -369,10 +427,6 @@ int gguf_mv_fast(int fmt, const uint8_t* W, const float* x, float* y, uint32_t M
         // activation bytes per weight byte, but fewer waves to hide the
         // latency and spread the arithmetic; RPT = 1 while that leaves at
         // least 512 workgroups, else 2, else 4
-        static const uint32_t rpt_env = [] {
-            const char* v = getenv("EC_GGUF_RPT");  // 1, 2 or 4: fixed rows per thread, for comparison
-            return v ? (uint32_t)atoi(v) : 0u;
-        }();
         uint32_t rpt = 1;
         while (rpt < 4 && (M + rpt * P - 1) / (rpt * P) < 512) rpt *= 2;
         const uint32_t T = (P * nq + 63) / 64 * 64;
