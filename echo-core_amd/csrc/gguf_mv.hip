@@ -406,7 +406,7 @@ int gguf_mv_fast(int fmt, const uint8_t* W, const float* x, float* y, uint32_t M
         while (G * R > T) G /= 2;
         const size_t lds = q8_f32_lds_bytes(nc, R);
         const uint32_t mg = (uint32_t)((((uint64_t)1 << 32) + nc - 1) / nc);
-        if (xpt > 16 || G < 1 || lds > 64 * 1024) return EC_ERR_UNSUPPORTED;
+        if (xpt > 16 || G < 1 || lds > 160 * 1024) return EC_ERR_UNSUPPORTED;  // gfx950: 160 KB per workgroup
         const dim3 grid((M + R - 1) / R), blk(T);
         if (rpt == 4) return launch_q8_f32_x<4>(xpt, grid, blk, lds, st, W, x, y, M, nc, P, R, G, mg);
         if (rpt == 2) return launch_q8_f32_x<2>(xpt, grid, blk, lds, st, W, x, y, M, nc, P, R, G, mg);

@@ -541,7 +541,7 @@ def test_deltanet_chunked_1024_tokens_32_heads(hip, oc):
 
 
 @pytest.mark.parametrize("fmt,N,K", [(6, 9216, 2560), (6, 2560, 9216), (6, 1000, 4096), (6, 77, 96), (6, 2563, 9216),
-                                     (6, 1030, 13312), (6, 333, 512), (6, 500, 1088), (6, 130, 320), (6, 700, 11008),
+                                     (6, 1030, 13312), (6, 333, 512), (6, 500, 1088), (6, 130, 320), (6, 700, 11008), (6, 300, 16384),
                                      (10, 9216, 2560), (10, 2560, 9216), (10, 333, 512), (10, 1001, 4096),
                                      (10, 2563, 9216), (10, 1030, 13312), (10, 700, 11008), (10, 130, 16640)])
 def test_gguf_f32_matvec_full_shapes(hip, oc, fmt, N, K):
@@ -554,7 +554,7 @@ def test_gguf_f32_matvec_full_shapes(hip, oc, fmt, N, K):
     with a last tile of 1 row) and workgroups padded to whole waves (11008: 688 threads of 704; Q4_K 16640:
     520 of 576; Q8_0 1088: 544 of 576), with ragged last tiles.  Q8_0 at K = 1088 and 320 (multiples of 64,
     not of 256) runs the block-pair kernel with 17 and 5 pairs per row; 320 takes 128 threads per pair column
-    and one thread per row in the row sums."""
+    and one thread per row in the row sums; 16384 stages 68 KB of x (above 64 KB of LDS)."""
     W = synth.q8_0_blocks(fmt + N, N, K) if fmt == 6 else synth.q4_K_blocks(fmt + N, N, K)
     x = synth.activations(N + 1, K)
     y0 = synth.activations(N + 2, N)
