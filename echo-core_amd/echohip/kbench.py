@@ -327,13 +327,11 @@ def run_all(hip, quick=False):
 
 
 # ---------------------------------------------------------------- PMC traffic
-# Matvec shapes of one decode step of the 4B-class hybrid decoder (M = 8 token
-# rows): (name, N output rows, K, launches per step).
-# (name, N, K, launches per step, K splits): the decode step of the 4B-class
-# decoder at batch 8, with the split-K counts the engine uses (host/engine.cpp:
-# 2 for the delta-net input projection and gate/up, 3 for the projections that
-# add into the residual; a split writes one partial output per split).
-# (name, N, K, launches per decode step, K splits) with the engine's defaults for two activation pieces
+# Matvec shapes of one decode step of the 4B-class hybrid decoder at batch 8
+# (M = 8 token rows, two activation pieces): (name, N output rows, K, launches
+# per step, K splits), the splits being the engine's defaults for two pieces
+# (host/engine.cpp: delta-net input 1, gate/up 4, attention input 4, the
+# projections that add into the residual 3; a split writes one partial output).
 DECODE_STEP_MATVECS = [("delta_in", 12352, 2560, 24, 1), ("delta_out", 2560, 4096, 24, 3),
                        ("attn_in", 6144, 2560, 8, 4), ("attn_out", 2560, 4096, 8, 3),
                        ("ffn_gate_up", 18432, 2560, 32, 4), ("ffn_down", 2560, 9216, 32, 3),
