@@ -415,13 +415,18 @@ int gguf_mv_fast(int fmt, const uint8_t* W, const float* x, float* y, uint32_t M
     if (fmt == EC_Q4_K) {
         const uint32_t nsb = K / 256, nq = 4 * nsb;
         if (nq > 1024) return EC_ERR_UNSUPPORTED;
+        // threads per quarter: the smallest power of two that makes P * nq a
+        // whole number of waves and at least 256 threads (2560 x 4096, nq =
+        // 64: one thread per quarter 7.7 us, four 4.55 us; more threads than
+        // that were no faster at K = 2560, 4096 or 9216)
         uint32_t P = 64 / gcd32(nq, 64);
+        while (P * nq < 256 && 2 * P * nq <= 1024) P *= 2;
         while (P > 1 && P * nq > 1024) P /= 2;
         static const uint32_t p_env = [] {
-            const char* v = getenv("EC_GGUF_P");  // threads per quarter (a power of two <= the default), for comparison
+            const char* v = getenv("EC_GGUF_P");  // threads per quarter (a power of two), for comparison
             return v ? (uint32_t)atoi(v) : 0u;
         }();
-        if (p_env && p_env < P && (p_env & (p_env - 1)) == 0) P = p_env;
+        if (p_env && (p_env & (p_env - 1)) == 0 && p_env * nq <= 1024) P = p_env;
         // RPT rows per thread (all rows' loads in flight): x is read from L2
         // once per workgroup of R = RPT * P rows, so larger R means fewer
         // activation bytes per weight byte, but fewer waves to hide the

@@ -551,7 +551,7 @@ def test_gguf_f32_matvec_full_shapes(hip, oc, fmt, N, K):
     take every rows-per-thread variant (1 row: 9216 x 2560, 2560 x 9216, 2563 x 9216 with a last tile of 3 of
     4 rows; 2 rows: 1030 x 13312 (Q4_K: its 832 threads exceed the 4-row variant's bound; Q8_0: 129
     workgroups of 2 rows); 4 rows: 333 x 512, 700 x 11008, Q8_0 500 x 1088 and 130 x 320, Q4_K 1001 x 4096
-    with a last tile of 1 row) and workgroups padded to whole waves (11008: 688 threads of 704; Q4_K 16640:
+    with a last tile of 9 of 16 rows) and workgroups padded to whole waves (11008: 688 threads of 704; Q4_K 16640:
     520 of 576; Q8_0 1088: 544 of 576), with ragged last tiles.  Q8_0 at K = 1088 and 320 (multiples of 64,
     not of 256) runs the block-pair kernel with 17 and 5 pairs per row; 320 takes 128 threads per pair column
     and one thread per row in the row sums; 16384 stages 68 KB of x (above 64 KB of LDS)."""
