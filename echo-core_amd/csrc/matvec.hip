@@ -919,7 +919,12 @@ static void launch_q8(const void* W, const void* act, float* y, int32_t* dots, u
     // wave streams about the same weight bytes per pass.  GPW <= 5 (two pieces: 4, and 3 for 16 tokens;
     // two tiles: 2): every variant under 128 VGPRs, no spills (two tiles with 3 chunks per pass: lm_head
     // 151936 x 2560, M = 8, 70.2 -> 73.8 us)
-    const uint32_t tpw = tpw_q8(P);
+    // two tiles per wave only while that leaves >= 128 workgroups: an
+    // unsplit 2560 x 9216 at M = 8 (80 two-tile workgroups) runs 12.3 us,
+    // with one tile per wave 9.7 us; the decode step's split projections
+    // (>= 240 workgroups) keep two
+    uint32_t tpw = tpw_q8(P);
+    if (tpw > 1 && (nT + tpw - 1) / tpw * nsplit < 128) tpw = 1;
     constexpr int max_gpw = P == 1 || MT == 1 ? 5 : (MT == 16 ? 3 : 4);
     plan(nT * nsplit, cps, max_gpw, gpw, nw, target_waves_q8());
     if constexpr (MT == 1 && P == 1 && !DOTS) {
