@@ -453,7 +453,11 @@ __device__ __forceinline__ void q4k_scale_min(const uint32_t (&q)[3], int s, uin
 // lane group g (lanes 16g .. 16g+15) applies the epilogue of sub-blocks g and
 // 4+g only -- a quarter of the per-sub-block instructions -- and the four
 // groups' fp32 partials are added once at the end.
-template <int MT, int P, bool DOTS, int GPW>
+// TPW 16-row tiles per wave (MT > 1, !DOTS): each staged activation
+// super-block serves the TPW tiles' weights (tile t0 + tt at wt + tt *
+// tstride; a second tile past the last one reads the first and is not
+// stored).
+template <int MT, int P, bool DOTS, int GPW, int TPW>
 __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W, const uint8_t* __restrict__ act,
                                                   float* __restrict__ y, int32_t* __restrict__ dots, uint32_t M,
                                                   uint32_t N, uint32_t K, uint32_t nB, uint32_t xd_off,
@@ -463,18 +467,21 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
     constexpr int S = slots<MT>();
     constexpr int NA = ngroups<MT, P>();
     constexpr int NB = 8 * GPW;
-    const uint32_t t = blockIdx.x, lane = threadIdx.x & 63, row = lane & 15, g = lane >> 4;
+    static_assert(TPW == 1 || (MT > 1 && !DOTS), "two tiles per wave: M > 1, no dots output");
+    const uint32_t t = TPW * blockIdx.x, lane = threadIdx.x & 63, row = lane & 15, g = lane >> 4;
     const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t nw = blockDim.x >> 6;
     constexpr int ACT_MAX = GPW * 256 * lrows<MT, P>();
     float* red = lds;
-    float* xs = lds + nw * 256 + w * (2 * NB * S + ACT_MAX / 4);
+    float* xs = lds + TPW * nw * 256 + w * (2 * NB * S + ACT_MAX / 4);
     float* xms = xs + NB * S;
     uint8_t* as = (uint8_t*)(xms + NB * S);
     const uint8_t* wt = W + (size_t)t * nB * kQ4TChunk;
+    const uint32_t nT = (N + 15) / 16;
+    const size_t tstride = TPW > 1 && t + 1 < nT ? (size_t)nB * kQ4TChunk : 0;
     const uint32_t VR = P * M;  // layout rows
     const size_t act_bytes = (size_t)nB * 256 * VR;
-    float acc4[1][4] = {};
+    float acc4[TPW][4] = {};
     float(&acc)[4] = acc4[0];
 
     for (uint32_t B0 = w * GPW; B0 < nB; B0 += nw * GPW) {
@@ -486,14 +493,17 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
             sm.load((const float*)(act + dxs_off), nB * 8, 8 * B0, M, lane);
         }
         ast.load(act, (size_t)B0 * 256 * VR, (size_t)GPW * 256 * VR, act_bytes, lane);
-        uint4 q0[GPW], q1[GPW], hdr[GPW];
+        uint4 q0[GPW][TPW], q1[GPW][TPW], hdr[GPW][TPW];
 #pragma unroll
         for (int u = 0; u < GPW; ++u) {
             const uint32_t b = min(B0 + u, nB - 1);
-            const uint8_t* ch = wt + (size_t)b * kQ4TChunk;
-            q0[u] = ld_stream16(ch + lane * 16);
-            q1[u] = ld_stream16(ch + 1024 + lane * 16);
-            hdr[u] = ld_stream16(ch + 2048 + row * 16);
+#pragma unroll
+            for (int tt = 0; tt < TPW; ++tt) {
+                const uint8_t* ch = wt + tt * tstride + (size_t)b * kQ4TChunk;
+                q0[u][tt] = ld_stream16(ch + lane * 16);
+                q1[u][tt] = ld_stream16(ch + 1024 + lane * 16);
+                hdr[u][tt] = ld_stream16(ch + 2048 + row * 16);
+            }
         }
         if constexpr (!DOTS) {
             sd.store(xs, lane);
@@ -518,9 +528,13 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
                     aw[ga][4 * i] = a4.x, aw[ga][4 * i + 1] = a4.y, aw[ga][4 * i + 2] = a4.z, aw[ga][4 * i + 3] = a4.w;
                 }
             }
-            const uint32_t qw[8] = {q0[u].x, q0[u].y, q0[u].z, q0[u].w, q1[u].x, q1[u].y, q1[u].z, q1[u].w};
-            const float d = h2f(hdr[u].x & 0xFFFF), dmin = h2f(hdr[u].x >> 16);
-            const uint32_t scb[3] = {hdr[u].y, hdr[u].z, hdr[u].w};
+#pragma unroll
+            for (int tt = 0; tt < TPW; ++tt) {
+            float(&acc)[4] = acc4[tt];
+            const uint32_t qw[8] = {q0[u][tt].x, q0[u][tt].y, q0[u][tt].z, q0[u][tt].w,
+                                    q1[u][tt].x, q1[u][tt].y, q1[u][tt].z, q1[u][tt].w};
+            const float d = h2f(hdr[u][tt].x & 0xFFFF), dmin = h2f(hdr[u][tt].x >> 16);
+            const uint32_t scb[3] = {hdr[u][tt].y, hdr[u][tt].z, hdr[u][tt].w};
             uint32_t sc4[2], mn4[2];
             q4k_scale_min4(scb, sc4, mn4);
             float a_sc = 0.0f, a_mn = 0.0f;  // M = 1: sum_s sc_s*dot_s*dx_s and sum_s m_s*dxs_s, scaled once
@@ -588,10 +602,11 @@ __global__ __launch_bounds__(1024) void k_mv_q4_K(const uint8_t* __restrict__ W,
                 acc[0] = fmaf(d, a_sc, acc[0]);
                 acc[0] = fmaf(-dmin, a_mn, acc[0]);
             }
+            }
         }
     }
     if constexpr (MT == 1 && !DOTS) acc[0] = sum_lane_groups(acc[0]);
-    if constexpr (!DOTS) reduce_store<R, P, 1>(acc4, red, y, t, M, N, ldy, accumulate);
+    if constexpr (!DOTS) reduce_store<R, P, TPW>(acc4, red, y, t, M, N, ldy, accumulate);
 }
 
 
@@ -854,6 +869,13 @@ static bool tpw_full_gpw() {
     }();
     return v;
 }
+static uint32_t tpw_q4() {
+    static uint32_t v = [] {
+        const char* e = getenv("EC_MV_TPW_Q4");
+        return e && atoi(e) == 1 ? 1u : 2u;
+    }();
+    return v;
+}
 static uint32_t target_waves_q4() {
     static uint32_t v = [] {
         const char* e = getenv("EC_MV_TARGET_WAVES_Q4");
@@ -969,17 +991,17 @@ static void launch_q8(const void* W, const void* act, float* y, int32_t* dots, u
     }
 }
 
-template <int MT, int P, bool DOTS, int GPW>
+template <int MT, int P, bool DOTS, int GPW, int TPW = 1>
 static void launch_q4_g(const void* W, const void* act, float* y, int32_t* dots, uint32_t M, uint32_t N, uint32_t K,
                         uint32_t ldy, int accumulate, uint32_t nw, hipStream_t st) {
     const ActLayout L = act_layout(EC_Q4_K, P * M, K);
     const uint32_t nT = round_up(N, 16) / 16, nB = L.Kp / 256;
     const uint32_t wave_floats = 2 * 8 * GPW * slots<MT>() + GPW * 256 * lrows<MT, P>() / 4;
-    nw = min(nw, lds_cap_waves(wave_floats));
-    const size_t lds = ((size_t)nw * 256 + (size_t)nw * wave_floats) * sizeof(float);
-    hipLaunchKernelGGL((k_mv_q4_K<MT, P, DOTS, GPW>), dim3(nT), dim3(64 * nw), lds, st, (const uint8_t*)W,
-                       (const uint8_t*)act, y, dots, M, N, K, nB, (uint32_t)L.xd_off, (uint32_t)L.dxs_off, ldy,
-                       accumulate);
+    nw = min(nw, lds_cap_waves(wave_floats, TPW));
+    const size_t lds = ((size_t)TPW * nw * 256 + (size_t)nw * wave_floats) * sizeof(float);
+    hipLaunchKernelGGL((k_mv_q4_K<MT, P, DOTS, GPW, TPW>), dim3((nT + TPW - 1) / TPW), dim3(64 * nw), lds, st,
+                       (const uint8_t*)W, (const uint8_t*)act, y, dots, M, N, K, nB, (uint32_t)L.xd_off,
+                       (uint32_t)L.dxs_off, ldy, accumulate);
 }
 
 // M = 1 with one piece: the activation operand by row broadcasts instead of
@@ -1017,10 +1039,24 @@ static void launch_q4(const void* W, const void* act, float* y, int32_t* dots, u
             return;
         }
     }
-    switch (gpw) {
-        case 1: launch_q4_g<MT, P, DOTS, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
-        case 2: launch_q4_g<MT, P, DOTS, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
-        default: launch_q4_g<MT, P, DOTS, 3>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
+    // M = 8 with two pieces and M = 16: two 16-row tiles per wave (each staged
+    // activation super-block serves both) while that leaves >= 128
+    // workgroups (EC_MV_TPW_Q4=1 keeps one; the other M and piece counts
+    // spill registers with two tiles)
+    if constexpr (((MT == 8 && P == 2) || MT == 16) && !DOTS) {
+        if (tpw_q4() == 2 && (nT + 1) / 2 >= 128 && gpw == 1) {
+            launch_q4_g<MT, P, DOTS, 1, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st);
+            return;
+        }
+    }
+    if constexpr (MT > 1) {  // the plan gives M > 1 one super-block per pass
+        launch_q4_g<MT, P, DOTS, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st);
+    } else {
+        switch (gpw) {
+            case 1: launch_q4_g<MT, P, DOTS, 1>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
+            case 2: launch_q4_g<MT, P, DOTS, 2>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
+            default: launch_q4_g<MT, P, DOTS, 3>(W, act, y, dots, M, N, K, ldy, accumulate, nw, st); break;
+        }
     }
 }
 
