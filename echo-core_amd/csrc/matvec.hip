@@ -837,7 +837,9 @@ __global__ void k_dequant_fp16(int fmt, const uint8_t* __restrict__ src, uint16_
 // where possible.  Q8_0: 12288 waves (EC_MV_TARGET_WAVES overrides; with the
 // decode step's split-K projections 12288 measured best of 2048 .. 32768:
 // 1.92 ms/step at 2048, 1.86 at 4096, 1.80 at 12288, 1.86 at 24576); Q4_K:
-// 4096 (EC_MV_TARGET_WAVES_Q4 overrides).
+// 3072 (EC_MV_TARGET_WAVES_Q4 overrides; M = 1, us at 1536 / 2048 / 3072 /
+// 4096 / 6144: 9216 x 2560 4.83 / 4.83 / 4.76 / 4.75 / 5.14, 12352 x 2560
+// 5.52 / 5.51 / 5.51 / 5.93 / 5.94, 2560 x 9216 and 2560 x 4096 flat).
 static uint32_t target_waves_q8() {
     static uint32_t v = [] {
         const char* e = getenv("EC_MV_TARGET_WAVES");
@@ -879,7 +881,7 @@ static uint32_t tpw_q4() {
 static uint32_t target_waves_q4() {
     static uint32_t v = [] {
         const char* e = getenv("EC_MV_TARGET_WAVES_Q4");
-        return e ? (uint32_t)atoi(e) : 4096u;
+        return e ? (uint32_t)atoi(e) : 3072u;
     }();
     return v;
 }
