@@ -90,26 +90,27 @@ __device__ __forceinline__ void row_sums_store(const float* red, uint32_t ncol, 
 // pair values are summed by row_sums_store.  Issue order as in the Q4_K
 // kernel below: x's loads, the previous y, then the weights, all
 // unconditional, so the x staging and barrier overlap the weights' latency.
-constexpr uint32_t kQ8XStride = 68;  // floats per staged block pair (272 bytes)
+// x in LDS as pairs of 64 floats 65 apart: the compiler re-reads x from LDS
+// inside the row loop (it keeps the kernel at ~60 registers), and with an odd
+// stride consecutive lanes (pairs) read distinct banks, at compile-time
+// offsets.  (Pairs 68 floats apart, for 16-byte reads: lanes 16 apart shared
+// banks, 1.4 M conflict cycles per 9216 x 2560 launch.)
+constexpr uint32_t kQ8XStride = 65;
 
-// Four rows' loads (68 registers) beside the 64 activations: RPT = 4 is
-// bounded at 768 threads like the Q4_K kernel.
-template <int RPT>
-constexpr int q8_f32_max_threads() { return RPT == 4 ? 768 : 1024; }
-
-size_t q8_f32_lds_bytes(uint32_t nc, uint32_t R) { return ((size_t)nc * kQ8XStride + (size_t)R * nc + 1) * 4; }
+size_t q8_f32_lds_bytes(uint32_t nc, uint32_t R) { return ((size_t)nc * kQ8XStride + 4 + (size_t)R * nc + 1) * 4; }
 
 typedef uint32_t gu32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 // nc_magic = ceil(2^32 / nc): t / nc == umulhi(t, nc_magic) for t, nc < 2^10.
 template <int RPT, int XPT>
-__global__ __launch_bounds__(q8_f32_max_threads<RPT>()) void k_gguf_q8_0_f32_pairs(
+__global__ __launch_bounds__(1024) void k_gguf_q8_0_f32_pairs(
     const uint8_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ y, uint32_t M, uint32_t nc,
     uint32_t P, uint32_t R, uint32_t G, uint32_t nc_magic) {
     extern __shared__ uint8_t lds[];
     const uint32_t t = threadIdx.x, T = blockDim.x;
-    float* xs = (float*)lds;
-    float* red = xs + (size_t)nc * kQ8XStride;  // [R][nc] + 1
+    constexpr uint32_t XS = kQ8XStride;
+    float* xs = (float*)lds;  // [nc][XS], then a 4-float spare slot
+    float* red = xs + (size_t)nc * XS + 4;  // [R][nc] + 1
     const uint32_t ph0 = __umulhi(t, nc_magic), c = t - ph0 * nc;
     const uint32_t ph = min(ph0, P - 1);  // padding threads: c < nc, ph0 >= P
     const size_t rowbytes = (size_t)nc * 68;
@@ -131,22 +132,20 @@ __global__ __launch_bounds__(q8_f32_max_threads<RPT>()) void k_gguf_q8_0_f32_pai
         }
         w[i][16] = *(const uint32_t*)(bp + 64);
     }
-    // x -> LDS: pair c (64 floats) at c * 68 floats; float4s past x's end go
-    // to the last pair's padding
+    // x -> LDS: float4 c4 (elements 4(c4 % 16) .. +3 of pair c4 / 16)
+    // (unconditional: float4s past x's end go to the spare slot -- a branch
+    // here lets the compiler sink the weights' loads below the barrier)
 #pragma unroll
     for (int j = 0; j < XPT; ++j) {
         const uint32_t c4 = t + j * T;
-        const uint32_t o = c4 < n4 ? (c4 / 16) * kQ8XStride + 4 * (c4 % 16) : (nc - 1) * kQ8XStride + 64;
-        *(float4*)(xs + o) = xf[j];
+        float* o = xs + (c4 < n4 ? (c4 / 16) * XS + 4 * (c4 % 16) : nc * XS);
+        o[0] = xf[j].x, o[1] = xf[j].y, o[2] = xf[j].z, o[3] = xf[j].w;
     }
     __syncthreads();
     float xv[64];
-    const float4* xq = (const float4*)(xs + c * kQ8XStride);
+    const float* xq = xs + c * XS;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const float4 f = xq[i];
-        xv[4 * i] = f.x, xv[4 * i + 1] = f.y, xv[4 * i + 2] = f.z, xv[4 * i + 3] = f.w;
-    }
+    for (int i = 0; i < 64; ++i) xv[i] = xq[i];
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
         // branch-free: a row past the tile's end (rr >= nr) sums row r0's
@@ -170,11 +169,12 @@ template <int RPT>
 int launch_q8_f32_x(uint32_t xpt, dim3 grid, dim3 blk, size_t lds, hipStream_t st, const uint8_t* W, const float* x,
                     float* y, uint32_t M, uint32_t nc, uint32_t P, uint32_t R, uint32_t G, uint32_t mg) {
     switch (xpt) {
-        case 1: hipLaunchKernelGGL((k_gguf_q8_0_f32_pairs<RPT, 1>), grid, blk, lds, st, W, x, y, M, nc, P, R, G, mg); break;
-        case 2: hipLaunchKernelGGL((k_gguf_q8_0_f32_pairs<RPT, 2>), grid, blk, lds, st, W, x, y, M, nc, P, R, G, mg); break;
-        case 4: hipLaunchKernelGGL((k_gguf_q8_0_f32_pairs<RPT, 4>), grid, blk, lds, st, W, x, y, M, nc, P, R, G, mg); break;
-        case 8: hipLaunchKernelGGL((k_gguf_q8_0_f32_pairs<RPT, 8>), grid, blk, lds, st, W, x, y, M, nc, P, R, G, mg); break;
-        case 16: hipLaunchKernelGGL((k_gguf_q8_0_f32_pairs<RPT, 16>), grid, blk, lds, st, W, x, y, M, nc, P, R, G, mg); break;
+#define EC_Q8F(X)                                                                                             \
+    case X:                                                                                                   \
+        hipLaunchKernelGGL((k_gguf_q8_0_f32_pairs<RPT, X>), grid, blk, lds, st, W, x, y, M, nc, P, R, G, mg); \
+        break;
+        EC_Q8F(1) EC_Q8F(2) EC_Q8F(4) EC_Q8F(8) EC_Q8F(16)
+#undef EC_Q8F
         default: return EC_ERR_UNSUPPORTED;
     }
     return EC_OK;
@@ -375,15 +375,17 @@ int gguf_mv_fast(int fmt, const uint8_t* W, const float* x, float* y, uint32_t M
     if (fmt == EC_Q8_0) {
         if (K % 64 || K / 64 > 1024) return EC_ERR_UNSUPPORTED;
         const uint32_t nc = K / 64;  // block pairs per row
-        // threads per pair column: the smallest power of two that makes
-        // P * nc a whole number of waves and at least 512 threads (x staged
-        // once per workgroup for more rows); measured on MI355X (us, 9216 x
-        // 2560 / 2560 x 9216 / 12352 x 2560 / 2560 x 4096 / 6144 x 2560):
-        // 9.37 / 11.83 / 10.81 / 6.58 / 7.20 against 9.65 / 11.83 / 10.92 /
-        // 7.36 / 7.84 with the whole-waves minimum alone, and 9.86 / 13.66 /
-        // 12.77 / 6.63 / 8.34 for a kernel staging the tile's bytes in LDS
-        uint32_t P = 64 / gcd32(nc, 64);
-        while (P * nc < 512 && 2 * P * nc <= 1024) P *= 2;
+        // Four threads per pair column (at least one wave per workgroup, at
+        // most 1024 threads), one row per thread, two where one would mean
+        // more than 4096 workgroups.  Swept over 12 shapes (P = 1 .. 16,
+        // 1 / 2 / 4 rows per thread; graph-timed us): this choice is within
+        // 5% of each shape's best -- 9216 x 2560 7.89 (best 7.67), 2560 x 9216
+        // 9.07, 12352 x 2560 9.24, 2560 x 4096 5.42, 6144 x 2560 6.35, 18432 x
+        // 2560 12.43 (two rows; one row 13.39), 4096 x 11008 13.53, 1024 x 2560
+        // 3.49 -- and four rows per thread, which leave few workgroups, were
+        // never the best (1024 x 2560: 9.8).
+        uint32_t P = 4;
+        while (P * nc < 64) P *= 2;
         while (P > 1 && P * nc > 1024) P /= 2;
         static const uint32_t q8p_env = [] {
             const char* v = getenv("EC_GGUF_Q8_P");  // threads per pair column (a power of two), for comparison
@@ -391,14 +393,8 @@ int gguf_mv_fast(int fmt, const uint8_t* W, const float* x, float* y, uint32_t M
         }();
         if (q8p_env && (q8p_env & (q8p_env - 1)) == 0 && q8p_env * nc <= 1024) P = q8p_env;
         const uint32_t T = (P * nc + 63) / 64 * 64;
-        // rows per thread: 1 while that leaves at least 512 workgroups, 2
-        // while that leaves 128 (with 512-1024 threads per workgroup, 4 rows
-        // leave few workgroups: 2560 x 4096 9.0 us at 80 workgroups, 6.6 at
-        // 160 with 2 rows), else 4
-        const uint32_t wg1 = (M + P - 1) / P, wg2 = (M + 2 * P - 1) / (2 * P);
-        uint32_t rpt = wg1 >= 512 ? 1 : (wg2 >= 128 ? 2 : 4);
-        if (rpt == 4 && T > (uint32_t)q8_f32_max_threads<4>()) rpt = 2;
-        if ((rpt_env == 1 || rpt_env == 2 || rpt_env == 4) && T <= (rpt_env == 4 ? 768u : 1024u)) rpt = rpt_env;
+        uint32_t rpt = (M + P - 1) / P > 4096 ? 2 : 1;
+        if (rpt_env == 1 || rpt_env == 2) rpt = rpt_env;
         const uint32_t R = rpt * P;
         uint32_t xpt = 1;
         while (xpt * T < 16 * nc) xpt *= 2;
@@ -408,7 +404,6 @@ int gguf_mv_fast(int fmt, const uint8_t* W, const float* x, float* y, uint32_t M
         const uint32_t mg = (uint32_t)((((uint64_t)1 << 32) + nc - 1) / nc);
         if (xpt > 16 || G < 1 || lds > 160 * 1024) return EC_ERR_UNSUPPORTED;  // gfx950: 160 KB per workgroup
         const dim3 grid((M + R - 1) / R), blk(T);
-        if (rpt == 4) return launch_q8_f32_x<4>(xpt, grid, blk, lds, st, W, x, y, M, nc, P, R, G, mg);
         if (rpt == 2) return launch_q8_f32_x<2>(xpt, grid, blk, lds, st, W, x, y, M, nc, P, R, G, mg);
         return launch_q8_f32_x<1>(xpt, grid, blk, lds, st, W, x, y, M, nc, P, R, G, mg);
     }

@@ -411,7 +411,7 @@ def pmc_cases(hip, which):
     PMC_LAUNCHES times each on different
     buffer copies of a >= 512 MB rotation; then the calibration kernels of
     pmc_workload (a 256 MiB read, a 256 MiB fill).  `gguf` runs the fp32 Q4_K
-    matvec over GGUF bytes (ec_matvec_gguf_f32) at 9216 x 2560 and 2560 x 9216."""
+    matvec over GGUF bytes (ec_matvec_gguf_f32) at 9216 x 2560 and 2560 x 9216, then the Q8_0 one."""
     st = torch.cuda.current_stream().cuda_stream
     if which == "attention":
         for ctx in (512, 4096, 32768):
@@ -498,22 +498,30 @@ def pmc_cases(hip, which):
             del Wd, tiled, x, act, y
             torch.cuda.empty_cache()
     elif which == "gguf":
-        # the reference-signature fp32 Q4_K matvec (GGUF bytes in place) at 9216 x 2560, then 2560 x 9216
-        for N, K in ((9216, 2560), (2560, 9216)):
-            wbytes = N * K // 256 * 144
-            n_copies = max(PMC_LAUNCHES, math.ceil(ROTATE_BYTES / wbytes) + 1)
-            Ws = torch.empty((n_copies, wbytes), dtype=torch.uint8, device="cuda")
-            Ws[0].copy_(torch.from_numpy(synth.q4_K_blocks(0, N, K).reshape(-1)))
-            for i in range(1, n_copies):
-                Ws[i].copy_(Ws[0])
-            x = torch.from_numpy(synth.activations(1, K)).cuda()
-            y = torch.zeros(N, dtype=torch.float32, device="cuda")
-            torch.cuda.synchronize()
-            for i in range(PMC_LAUNCHES):
-                hip.matvec_gguf_f32(L.Q4_K, Ws[(i * 7919) % n_copies], x, y, N, K, stream=st)
+        # the reference-signature fp32 matvec (GGUF bytes in place), Q4_K then Q8_0, each at 9216 x 2560
+        # then 2560 x 9216
+        for fmt in (L.Q4_K, L.Q8_0):
+            for N, K in ((9216, 2560), (2560, 9216)):
+                if fmt == L.Q4_K:
+                    wbytes = N * K // 256 * 144
+                    W0 = torch.from_numpy(synth.q4_K_blocks(0, N, K).reshape(-1)).cuda()
+                else:
+                    wbytes = N * K // 32 * 34
+                    W0 = torch.empty(wbytes, dtype=torch.uint8, device="cuda")
+                    hip.fill_random(1, W0, N * K // 32, 0, 0.02, stream=st)
+                n_copies = max(PMC_LAUNCHES, math.ceil(ROTATE_BYTES / wbytes) + 1)
+                Ws = torch.empty((n_copies, wbytes), dtype=torch.uint8, device="cuda")
+                for i in range(n_copies):
+                    Ws[i].copy_(W0)
+                del W0
+                x = torch.from_numpy(synth.activations(1, K)).cuda()
+                y = torch.zeros(N, dtype=torch.float32, device="cuda")
                 torch.cuda.synchronize()
-            del Ws, x, y
-            torch.cuda.empty_cache()
+                for i in range(PMC_LAUNCHES):
+                    hip.matvec_gguf_f32(fmt, Ws[(i * 7919) % n_copies], x, y, N, K, stream=st)
+                    torch.cuda.synchronize()
+                del Ws, x, y
+                torch.cuda.empty_cache()
     elif which == "gemm":
         for fmt in (L.Q8_0, L.Q4_K):
             for N, K in ((9216, 2560), (2560, 9216)):

@@ -541,20 +541,24 @@ def test_deltanet_chunked_1024_tokens_32_heads(hip, oc):
 
 
 @pytest.mark.parametrize("fmt,N,K", [(6, 9216, 2560), (6, 2560, 9216), (6, 1000, 4096), (6, 77, 96), (6, 2563, 9216),
-                                     (6, 1030, 13312), (6, 333, 512), (6, 500, 1088), (6, 130, 320), (6, 700, 11008), (6, 300, 16384),
+                                     (6, 1030, 13312), (6, 333, 512), (6, 500, 1088), (6, 130, 320), (6, 700, 11008),
+                                     (6, 300, 16384), (6, 16401, 1024),
                                      (10, 9216, 2560), (10, 2560, 9216), (10, 333, 512), (10, 1001, 4096),
                                      (10, 2563, 9216), (10, 1030, 13312), (10, 700, 11008), (10, 130, 16640)])
 def test_gguf_f32_matvec_full_shapes(hip, oc, fmt, N, K):
     """The reference-signature path (GGUF bytes in place, fp32 activations, y += W x) at the matvec workloads'
     full shapes, ragged row counts and a K whose rows are not 16-byte aligned (K = 96: per-row kernel), against
-    the oracle's reference-order matvec: within 1e-5 relative L2 (fp32 summation order only).  Both formats
-    take every rows-per-thread variant (1 row: 9216 x 2560, 2560 x 9216, 2563 x 9216 with a last tile of 3 of
-    4 rows; 2 rows: 1030 x 13312 (Q4_K: its 832 threads exceed the 4-row variant's bound; Q8_0: 129
-    workgroups of 2 rows); 4 rows: 333 x 512, 700 x 11008, Q8_0 500 x 1088 and 130 x 320, Q4_K 1001 x 4096
-    with a last tile of 9 of 16 rows) and workgroups padded to whole waves (11008: 688 threads of 704; Q4_K 16640:
-    520 of 576; Q8_0 1088: 544 of 576), with ragged last tiles.  Q8_0 at K = 1088 and 320 (multiples of 64,
-    not of 256) runs the block-pair kernel with 17 and 5 pairs per row; 320 takes 128 threads per pair column
-    and one thread per row in the row sums; 16384 stages 68 KB of x (above 64 KB of LDS)."""
+    the oracle's reference-order matvec: within 1e-5 relative L2 (fp32 summation order only).
+    Q4_K: every rows-per-thread variant (1 row: 9216 x 2560, 2560 x 9216, 2563 x 9216 with a last tile of 3 of
+    4 rows; 2 rows: 1030 x 13312, whose 832 threads exceed the 4-row variant's bound; 4 rows: 333 x 512,
+    700 x 11008, 1001 x 4096 with a last tile of 9 of 16 rows) and workgroups padded to whole waves (11008:
+    688 threads of 704; 16640: 520 of 576).
+    Q8_0 (block pairs, K % 64 == 0): four threads per pair column, raised to fill a wave for narrow rows
+    (333 x 512: 8, 130 x 320: 16 with 8 threads per row in the row sums); one row per thread, two at
+    16401 x 1024 (one row would mean 4101 workgroups; last tile 1 of 8 rows); workgroups padded to whole waves
+    (9216 x 2560: 160 threads of 192, 500 x 1088 -- 17 pairs -- 68 of 128, 700 x 11008: 688 of 704); ragged
+    last tiles (2563 x 9216: 3 of 4 rows, 1030 x 13312: 2 of 4, 333 x 512: 5 of 8, 130 x 320: 2 of 16);
+    300 x 16384 stages 66 KB of x (above 64 KB of LDS)."""
     W = synth.q8_0_blocks(fmt + N, N, K) if fmt == 6 else synth.q4_K_blocks(fmt + N, N, K)
     x = synth.activations(N + 1, K)
     y0 = synth.activations(N + 2, N)
