@@ -236,7 +236,15 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ q
     constexpr uint32_t HD = 256;
     constexpr uint32_t NR = kQPieces * G;  // A rows in use
     constexpr int NPW = CH / 64;           // 16-position groups per wave
-    __shared__ float part_s[NR][CH];       // per-piece scores (times the K row scale); PQ: packed q first
+    // per-piece scores (times the K row scale); PQ: packed q first.  Rows
+    // padded by 4 floats: the score stores (lane = row 4*gq + c, position
+    // 16*wv + r16) then fall in 64 distinct banks instead of 16.
+    __shared__ float part_s[NR][CH + 4];
+    // probability pieces, A rows 4g + piece, rows padded by 8 bytes so the
+    // PV operand reads (lane = row r16, 8 bytes at 8*gq) hit distinct banks
+    // (unpadded: 4-way at 64 positions, 8-way at 128)
+    constexpr uint32_t PAS = CH + 8;
+    __shared__ uint32_t pA_w[4 * G * PAS / 4];
     __shared__ float qsc_s[PQ ? NR : 1];
     __shared__ float qmx_s[PQ ? G : 1][4];
     // the chunk's V transposed, [dim][position slots]: a dword holds 4 positions
@@ -385,8 +393,8 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ q
         }
         const float l = wave_sum(es);
         // probabilities x V row scale as three int8 pieces (as q): A rows
-        // 4g + piece, bytes in the slot order of vT (over score row g)
-        uint8_t* pA = (uint8_t*)&part_s[0][0];
+        // 4g + piece of pA, bytes in the slot order of vT
+        uint8_t* pA = (uint8_t*)pA_w;
         const uint32_t rr = lane & 15;
         float pm = 0.0f;
 #pragma unroll
@@ -400,7 +408,7 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ q
             split_pieces(pr[q], pm, pcs, steps);
 #pragma unroll
             for (uint32_t pc = 0; pc < kQPieces; ++pc) {
-                pA[(4 * g + pc) * CH + byte] = (uint8_t)pcs[pc];
+                pA[(4 * g + pc) * PAS + byte] = (uint8_t)pcs[pc];
                 if (lane == 0 && q == 0) psc_s[g][pc] = steps[pc];
             }
         }
@@ -415,12 +423,12 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint8_t* __restrict__ q
     // 4g + piece), B = vT (wave wv: dims 64wv .. +63, four 16-dim tiles), K =
     // positions in slot order; C element e of lane group g is piece e of head
     // g, exact int32.  Positions past the chunk end carry p = 0.
-    const uint8_t* pA = (const uint8_t*)&part_s[0][0];
+    const uint8_t* pA = (const uint8_t*)pA_w;
     v4i Cv[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
     for (uint32_t ks = 0; ks < CH / 32; ++ks) {
         // rows 4G .. 15 feed only C rows that are not stored: read row 0 there
-        const uint32_t* ap = (const uint32_t*)(pA + (r16 < 4 * G ? r16 : 0) * CH + 32 * ks + 8 * gq);
+        const uint32_t* ap = (const uint32_t*)(pA + (r16 < 4 * G ? r16 : 0) * PAS + 32 * ks + 8 * gq);
         const long A = pack2(ap[0], ap[1]);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
