@@ -181,10 +181,11 @@ def test_q4_K_act_and_block_dots_bit_exact(hip, oc, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 48, 512), (3, 40, 768), (8, 64, 2560), (16, 16, 256), (1, 40, 768),
-                                   (1, 16, 9216), (1, 48, 256)])
+                                   (1, 16, 9216), (1, 48, 256), (16, 4112, 512)])
 def test_q4_K_matvec(hip, oc, M, N, K):
-    """M = 1 takes the VALU kernel (one wave per tile at K = 256: the direct store; 12 waves at 9216;
-    a ragged last tile at N = 40); M > 1 the MFMA kernel."""
+    """M = 1 takes the direct-load MFMA kernel (one wave per tile at K = 256: the direct store; 12 waves at
+    9216; a ragged last tile at N = 40); M > 1 the LDS-staged MFMA kernel, at 16 x 4112 x 512 with two tiles
+    per wave (129 workgroups, the last one's second tile past the end: read, not stored)."""
     W = synth.q4_K_blocks(7000 + K, N, K)
     X = synth.activations(8000 + M, M * K).reshape(M, K)
     tiled, act = _prep(hip, 10, W, X)
