@@ -85,16 +85,16 @@ __device__ __forceinline__ void row_sums_store(const float* red, uint32_t ncol, 
 // dword per row, all RPT rows issued before any use.  Element j of block 0
 // is byte 2 + j of those 17 dwords and of block 1 byte 36 + j; each is
 // converted with its own byte select, so the 2-byte offset of block 0 costs
-// nothing.  x is staged in LDS once per workgroup (pairs of 64 floats 68
-// apart), read into registers by each thread for its column, and the rows'
-// pair values are summed by row_sums_store.  Issue order as in the Q4_K
-// kernel below: x's loads, the previous y, then the weights, all
-// unconditional, so the x staging and barrier overlap the weights' latency.
-// x in LDS as pairs of 64 floats 65 apart: the compiler re-reads x from LDS
-// inside the row loop (it keeps the kernel at ~60 registers), and with an odd
-// stride consecutive lanes (pairs) read distinct banks, at compile-time
-// offsets.  (Pairs 68 floats apart, for 16-byte reads: lanes 16 apart shared
-// banks, 1.4 M conflict cycles per 9216 x 2560 launch.)
+// nothing.  x is staged in LDS once per workgroup, read into registers by
+// each thread for its column, and the rows' pair values are summed by
+// row_sums_store.  Issue order as in the Q4_K kernel below: x's loads, the
+// previous y, then the weights, all unconditional, so the x staging and
+// barrier overlap the weights' latency.  x in LDS as pairs of 64 floats 65
+// apart: the compiler re-reads x from LDS inside the row loop (it keeps the
+// kernel at ~60 registers), and with an odd stride consecutive lanes (pairs)
+// read distinct banks, at compile-time offsets.  (Pairs 68 floats apart, for
+// 16-byte reads: lanes 16 apart shared banks, 1.4 M conflict cycles per
+// 9216 x 2560 launch.)
 constexpr uint32_t kQ8XStride = 65;
 
 size_t q8_f32_lds_bytes(uint32_t nc, uint32_t R) { return ((size_t)nc * kQ8XStride + 4 + (size_t)R * nc + 1) * 4; }
