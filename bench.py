@@ -245,14 +245,14 @@ def main() -> int:
     prompts = [synth.randint(synth.stream_seed(args.seed, 2000 + s), int(lens[s]), 0, cfg.vocab - 1).astype(np.int32)
                for s in range(B)]
 
-    # ---- prefill (not part of `value`); a two-sequence prefill first allocates
-    # the engine's prefill lanes, then the state is reset
+    # ---- prefill (not part of `value`); a one-token prefill of four sequences
+    # first allocates the engine's prefill lanes, then the state is reset
     if args.prefill == "chunked":
-        eng.prefill_batch([(0, prompts[0][:1], 0), (1, prompts[1][:1], 0)])
+        eng.prefill_batch([(s, prompts[s][:1], 0) for s in range(min(4, B))])
         eng.reset()
     t0 = time.perf_counter()
     T = int(lens.max())
-    if args.prefill == "chunked":  # all prompts, two sequences' chunks in flight at a time
+    if args.prefill == "chunked":  # all prompts, four sequences' chunks in flight at a time
         eng.prefill_batch([(s, prompts[s], 0) for s in range(B)])
         eng.sync()
     else:  # token loop through the decode graph, ragged
@@ -368,7 +368,7 @@ def main() -> int:
                                "ffn 9216, vocab 151936; ragged batch of 8, greedy decode",
                    "global_batch": B, "prompt_lens": lens.tolist(), "decode_steps": W + K,
                    "act_pieces": args.act_pieces,
-                   "prefill": ("chunked (512-token int8-MFMA GEMM chunks per sequence, two sequences in flight)" if args.prefill == "chunked"
+                   "prefill": ("chunked (512-token int8-MFMA GEMM chunks per sequence, four sequences in flight)" if args.prefill == "chunked"
                                else "token loop through the decode graph"),
                    "prefill_tok_s": round(prefill_tps, 1),
                    "step_hbm_bytes": int(step_bytes),

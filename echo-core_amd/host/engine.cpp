@@ -129,9 +129,11 @@ struct ec_engine {
     ec_trace_fn trace_cb = nullptr;
     void* trace_user = nullptr;
     // chunked prefill: lanes of scratch rows (up to kPrefillChunk tokens of
-    // one sequence each) with their own stream, allocated on first use; lane
-    // 0 runs on st.  Several sequences' chunks run concurrently on the lanes.
-    static constexpr uint32_t kPrefillChunk = 512, kPrefillAttnSlots = 128, kPrefillLanes = 2;
+    // one sequence each, ~170 MB at 4B shapes) with their own stream,
+    // allocated on first use; lane 0 runs on st.  Several sequences' chunks
+    // run concurrently on the lanes (the 4B benchmark's eight prompts, MI355X:
+    // one lane 37.8k tok/s, two 46.0k, three 47.2k, four 47.5k).
+    static constexpr uint32_t kPrefillChunk = 512, kPrefillAttnSlots = 128, kPrefillLanes = 4;
     struct PrefillLane {
         bool ready = false;
         hipStream_t st = nullptr;
@@ -1245,7 +1247,12 @@ extern "C" int ec_engine_prefill_batch(ec_engine* e, uint32_t n_seqs, const uint
         jobs.push_back(PrefillJob{seqs[i], lens[i], tokens[i], pos0[i]});
     }
     if (jobs.empty()) return EC_OK;
-    return prefill_run(e, jobs, ec_engine::kPrefillLanes);
+    // EC_PREFILL_LANES = 1 .. 4 runs fewer lanes, for comparison
+    static const uint32_t lanes_env = [] {
+        const char* v = getenv("EC_PREFILL_LANES");
+        return v ? (uint32_t)atoi(v) : 0u;
+    }();
+    return prefill_run(e, jobs, lanes_env >= 1 ? lanes_env : ec_engine::kPrefillLanes);
 }
 
 extern "C" int ec_engine_profile_matvecs(ec_engine* e, uint32_t reps, uint32_t* launches, double* bytes_per_step,
