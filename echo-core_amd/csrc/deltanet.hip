@@ -34,6 +34,7 @@ struct DnLds {
     f32x4 q[2][kDnBlock][32], k[2][kDnBlock][32];
     float v[2][kDnBlock][16];
     float dec[2][kDnBlock], bt[2][kDnBlock], kq[2][kDnBlock];
+    float kk[2][kDnBlock / 2], kqx[2][kDnBlock / 2];  // token pair (2m, 2m+1): k_2m.k_2m+1, k_2m.q_2m+1
 };
 
 // grid (n_v * d_v/16, n_seq), block 256: threadIdx/16 = column in the group, %16 = k slice.
@@ -93,6 +94,24 @@ __global__ __launch_bounds__(256) void k_deltanet(float* __restrict__ state, con
             kq += lane_xor<8>(kq);
             kq += lane_xor<16>(kq);
             if (id % 32 == 0) L.kq[buf][id / 32] = kq;
+            // the pair's cross dots: token 2m's lanes take token 2m+1's k and q
+            // from 32 lanes up (tokens 2m, 2m+1 share a wave)
+            f32x4 nk, nq;
+            nk.x = lane_xor<32>(rk[u].x), nk.y = lane_xor<32>(rk[u].y), nk.z = lane_xor<32>(rk[u].z),
+            nk.w = lane_xor<32>(rk[u].w);
+            nq.x = lane_xor<32>(rq[u].x), nq.y = lane_xor<32>(rq[u].y), nq.z = lane_xor<32>(rq[u].z),
+            nq.w = lane_xor<32>(rq[u].w);
+            float kk = rk[u].x * nk.x + rk[u].y * nk.y + rk[u].z * nk.z + rk[u].w * nk.w;
+            float kx = rk[u].x * nq.x + rk[u].y * nq.y + rk[u].z * nq.z + rk[u].w * nq.w;
+            kk += lane_xor<1>(kk), kx += lane_xor<1>(kx);
+            kk += lane_xor<2>(kk), kx += lane_xor<2>(kx);
+            kk += lane_xor<4>(kk), kx += lane_xor<4>(kx);
+            kk += lane_xor<8>(kk), kx += lane_xor<8>(kx);
+            kk += lane_xor<16>(kk), kx += lane_xor<16>(kx);
+            if (id % 64 == 0) {
+                L.kk[buf][id / 64] = kk;
+                L.kqx[buf][id / 64] = kx;
+            }
         }
 #pragma unroll
         for (uint32_t u = 0; u < NV; ++u) {
@@ -155,14 +174,73 @@ __global__ __launch_bounds__(256) void k_deltanet(float* __restrict__ state, con
             for (int i = 0; i < 8; ++i) S[i] = fmaf(kk[i], delta, S[i] * x.dec);
             if (ks == 0) out[(((size_t)(t0 + j) * n_seq + s) * n_v + h) * d_v + col] = o;
         };
-        Ops A = read_ops(0);
-        for (uint32_t j = 0; j < nt; j += 2) {
-            const Ops B = read_ops(j + 1 < nt ? j + 1 : j);
-            token(A, j);
-            if (j + 1 >= nt) break;
-            A = read_ops(j + 2 < nt ? j + 2 : j + 1);
-            token(B, j + 1);
+        // Two tokens per step (1 = j, 2 = j+1), all four column dots from the
+        // state before both updates (one set of row reductions per pair):
+        //   a1 = S.k1, b1 = S.q1, c = S.k2, e = S.q2
+        //   delta1 = (v1 - d1 a1) b1', o1 = (d1 b1 + delta1 k1.q1)/sqrt(128)
+        //   S1.k2 = d1 c + delta1 k1.k2,  S1.q2 = d1 e + delta1 k1.q2
+        //   delta2 = (v2 - d2 S1.k2) b2', o2 = (d2 S1.q2 + delta2 k2.q2)/sqrt(128)
+        //   S <- d1 d2 S + (d2 delta1) k1 + delta2 k2
+        // (the sequential rule's values up to fp32 rounding); an odd last token
+        // takes the one-token step.
+        struct Ops2 {
+            Ops t1, t2;
+            float kk, kqx;
+        };
+        auto read_pair = [&](uint32_t j) {
+            Ops2 o;
+            o.t1 = read_ops(j), o.t2 = read_ops(j + 1);
+            o.kk = L.kk[buf][j / 2], o.kqx = L.kqx[buf][j / 2];
+            return o;
+        };
+        auto pair = [&](const Ops2& x, uint32_t j) {
+            const float k1[8] = {x.t1.k0.x, x.t1.k0.y, x.t1.k0.z, x.t1.k0.w, x.t1.k1.x, x.t1.k1.y, x.t1.k1.z, x.t1.k1.w};
+            const float q1[8] = {x.t1.q0.x, x.t1.q0.y, x.t1.q0.z, x.t1.q0.w, x.t1.q1.x, x.t1.q1.y, x.t1.q1.z, x.t1.q1.w};
+            const float k2[8] = {x.t2.k0.x, x.t2.k0.y, x.t2.k0.z, x.t2.k0.w, x.t2.k1.x, x.t2.k1.y, x.t2.k1.z, x.t2.k1.w};
+            const float q2[8] = {x.t2.q0.x, x.t2.q0.y, x.t2.q0.z, x.t2.q0.w, x.t2.q1.x, x.t2.q1.y, x.t2.q1.z, x.t2.q1.w};
+            float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f, c0 = 0.f, c1 = 0.f, e0 = 0.f, e1 = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                a0 = fmaf(S[i], k1[i], a0);
+                b0 = fmaf(S[i], q1[i], b0);
+                c0 = fmaf(S[i], k2[i], c0);
+                e0 = fmaf(S[i], q2[i], e0);
+                a1 = fmaf(S[4 + i], k1[4 + i], a1);
+                b1 = fmaf(S[4 + i], q1[4 + i], b1);
+                c1 = fmaf(S[4 + i], k2[4 + i], c1);
+                e1 = fmaf(S[4 + i], q2[4 + i], e1);
+            }
+            float a = a0 + a1, bq = b0 + b1, c = c0 + c1, e = e0 + e1;
+            a += lane_xor<1>(a), bq += lane_xor<1>(bq), c += lane_xor<1>(c), e += lane_xor<1>(e);
+            a += lane_xor<2>(a), bq += lane_xor<2>(bq), c += lane_xor<2>(c), e += lane_xor<2>(e);
+            a += lane_xor<4>(a), bq += lane_xor<4>(bq), c += lane_xor<4>(c), e += lane_xor<4>(e);
+            a += lane_xor<8>(a), bq += lane_xor<8>(bq), c += lane_xor<8>(c), e += lane_xor<8>(e);
+            const float d1 = x.t1.dec, d2 = x.t2.dec;
+            const float delta1 = (x.t1.vv - d1 * a) * x.t1.bt;
+            const float o1 = (d1 * bq + delta1 * x.t1.kq) * scale;
+            const float sk2 = d1 * c + delta1 * x.kk, sq2 = d1 * e + delta1 * x.kqx;
+            const float delta2 = (x.t2.vv - d2 * sk2) * x.t2.bt;
+            const float o2 = (d2 * sq2 + delta2 * x.t2.kq) * scale;
+            const float dd = d1 * d2, w1 = d2 * delta1;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) S[i] = fmaf(k2[i], delta2, fmaf(k1[i], w1, S[i] * dd));
+            if (ks == 0) {
+                out[(((size_t)(t0 + j) * n_seq + s) * n_v + h) * d_v + col] = o1;
+                out[(((size_t)(t0 + j + 1) * n_seq + s) * n_v + h) * d_v + col] = o2;
+            }
+        };
+        const uint32_t np = nt / 2;
+        if (np > 0) {  // pair m+1's operands are read while pair m is computed
+            Ops2 A = read_pair(0);
+            for (uint32_t m = 0; m < np; m += 2) {
+                const Ops2 B = read_pair(m + 1 < np ? 2 * (m + 1) : 2 * m);
+                pair(A, 2 * m);
+                if (m + 1 >= np) break;
+                A = read_pair(m + 2 < np ? 2 * (m + 2) : 2 * (m + 1));
+                pair(B, 2 * (m + 1));
+            }
         }
+        if (nt & 1) token(read_ops(nt - 1), nt - 1);
         stage_store(buf ^ 1);
         __syncthreads();
     }
