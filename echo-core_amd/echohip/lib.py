@@ -75,6 +75,7 @@ _SIGS = {
     "ec_matvec_split_pieces": [C.c_int, _u32, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp],
     "ec_block_dots_pieces": [C.c_int, _u32, _vp, _vp, _vp, _u32, _u32, _u32, _vp],
     "ec_glue_rmsnorm_quant_pieces": [_vp, _vp, _vp, _u32, _u32, _u32, _vp],
+    "ec_glue_argmax_advance_bounded": [_vp, _u32, _vp, _vp, _vp, _u32, _u32, _vp],
     "ec_glue_add_rmsnorm_quant_pieces": [_vp, _vp, _u32, _vp, _vp, _vp, _u32, _u32, _u32, _vp],
     "ec_glue_swiglu_quant_split_pieces": [_vp, _u32, _vp, _u32, _u32, _u32, _vp],
     "ec_glue_gated_norm_quant_pieces": [_vp, _vp, _u32, _u32, _vp, _vp, _u32, _u32, _u32, _vp],
@@ -308,6 +309,10 @@ class Lib:
     def gated_norm_rows_gemm_act(self, core, proj, Nin, z_off, norm_w, act, M, n_v, stream=None):
         self._call("ec_glue_gated_norm_rows_gemm_act", _ptr(core), _ptr(proj), Nin, z_off, _ptr(norm_w), _ptr(act), M,
                    n_v, self._stream(stream))
+
+    def argmax_advance(self, logits, vocab, gen, nxt, pos, n_seq, max_pos=0, stream=None):
+        self._call("ec_glue_argmax_advance_bounded", _ptr(logits), vocab, _ptr(gen), _ptr(nxt), _ptr(pos), n_seq,
+                   max_pos, self._stream(stream))
 
     def rmsnorm_quant(self, x, w, act, M, H, stream=None, pieces=1):
         if pieces == 1:

@@ -279,3 +279,66 @@ def test_delta_step_matches_unfused_ops(hip, oc):
         for s in range(n_seq):
             if p[s] >= 0:
                 _check_q8(xqB[s], xdB[s], xqA[s], xdA[s])
+
+
+def _argmax_ref(row):
+    """First index of the maximum over the non-NaN entries above -inf (the
+    reference's strictly-greater scan, engine.zig:860-867); 0 when there is none."""
+    best, bi = -np.inf, 0
+    ok = ~np.isnan(row) & (row > -np.inf)
+    if ok.any():
+        best = row[ok].max()
+        bi = int(np.flatnonzero(ok & (row == best))[0])
+    return bi
+
+
+@pytest.mark.parametrize("vocab", [151936, 151935, 1000, 7, 70001])
+def test_argmax_advance_edge_cases(hip, vocab):
+    """ec_glue_argmax_advance_bounded on rows with ties at the maximum (first
+    index wins, also across float4 groups and threads), NaNs, -inf, an all-NaN
+    and an all -inf row (token 0), -0.0 against +0.0, unaligned rows (vocab % 4
+    != 0), an inactive sequence (pos < 0: nothing written) and the max_pos
+    bound (a sequence whose next position would reach it becomes inactive)."""
+    import torch
+    rng = np.random.default_rng(vocab)
+    rows = []
+    r = rng.standard_normal(vocab).astype(np.float32)
+    rows.append(r)                                         # plain
+    r = rng.standard_normal(vocab).astype(np.float32)
+    idx = sorted(rng.choice(vocab, size=min(5, vocab), replace=False))
+    r[idx] = 9.0
+    rows.append(r)                                         # ties: first of 5
+    r = rng.standard_normal(vocab).astype(np.float32)
+    r[rng.choice(vocab, size=max(1, vocab // 7), replace=False)] = np.nan
+    rows.append(r)                                         # NaNs
+    rows.append(np.full(vocab, np.nan, np.float32))        # all NaN
+    rows.append(np.full(vocab, -np.inf, np.float32))       # all -inf
+    r = np.full(vocab, -1.0, np.float32)
+    r[vocab - 1] = 0.0
+    r[vocab // 2] = -0.0
+    rows.append(r)                                         # -0.0 first, then +0.0: equal, first wins
+    r = rng.standard_normal(vocab).astype(np.float32)
+    r[0] = np.inf
+    r[vocab - 1] = np.inf
+    rows.append(r)                                         # +inf twice
+    r = rng.standard_normal(vocab).astype(np.float32)
+    rows.append(r)                                         # inactive sequence
+    n = len(rows)
+    logits = torch.from_numpy(np.stack(rows)).cuda()
+    max_pos = 100
+    pos0 = np.array([5, 6, 7, 8, 9, 10, max_pos - 1, -1], np.int32)
+    gen = torch.full((n,), -7, dtype=torch.int32, device="cuda")
+    nxt = torch.full((n,), -7, dtype=torch.int32, device="cuda")
+    pos = torch.from_numpy(pos0.copy()).cuda()
+    for rep in range(2):  # a second call on the advanced positions
+        before = pos.cpu().numpy().copy()
+        hip.argmax_advance(logits, vocab, gen, nxt, pos, n, max_pos)
+        torch.cuda.synchronize()
+        g, q, p = gen.cpu().numpy(), nxt.cpu().numpy(), pos.cpu().numpy()
+        for s in range(n):
+            if before[s] < 0:
+                assert g[s] == (-7 if rep == 0 else g[s]) and p[s] == before[s], s
+                continue
+            want = _argmax_ref(rows[s])
+            assert g[s] == want and q[s] == want, (vocab, s, g[s], want)
+            assert p[s] == (before[s] + 1 if before[s] + 1 < max_pos else -1), (s, p[s])
