@@ -29,7 +29,6 @@ constexpr uint32_t kDh = 128;       // d_k = d_v
 constexpr uint32_t kVs = 16;        // value columns per scan workgroup
 constexpr uint32_t kLd = kDh + 4;   // LDS row of a C x 128 matrix (floats)
 constexpr uint32_t kPd = kCk + 4;   // LDS row of a C x C matrix
-constexpr uint32_t kUd = kVs + 4;   // LDS row of the C x 16 U tile
 // workspace floats per (sequence, head, chunk): W [C][128], U~ [C][128],
 // P [C][C], G [C], G_C/G_t [C], K^T [128][C] (zero past the last token)
 constexpr uint32_t kWsW = 0, kWsU = kCk * kDh, kWsP = 2 * kCk * kDh, kWsG = kWsP + kCk * kCk, kWsF = kWsG + kCk;
