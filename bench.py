@@ -252,7 +252,7 @@ def main() -> int:
         eng.reset()
     t0 = time.perf_counter()
     T = int(lens.max())
-    if args.prefill == "chunked":  # all prompts, four sequences' chunks in flight at a time
+    if args.prefill == "chunked":  # all prompts, two passes of two sequences' chunks in flight
         eng.prefill_batch([(s, prompts[s], 0) for s in range(B)])
         eng.sync()
     else:  # token loop through the decode graph, ragged
@@ -368,7 +368,7 @@ def main() -> int:
                                "ffn 9216, vocab 151936; ragged batch of 8, greedy decode",
                    "global_batch": B, "prompt_lens": lens.tolist(), "decode_steps": W + K,
                    "act_pieces": args.act_pieces,
-                   "prefill": ("chunked (512-token int8-MFMA GEMM chunks per sequence, four sequences in flight)" if args.prefill == "chunked"
+                   "prefill": ("chunked (512-token chunks per sequence; two sequences' chunks per int8-MFMA GEMM, two such passes in flight)" if args.prefill == "chunked"
                                else "token loop through the decode graph"),
                    "prefill_tok_s": round(prefill_tps, 1),
                    "step_hbm_bytes": int(step_bytes),

@@ -128,14 +128,15 @@ struct ec_engine {
     // step tracing (ec_engine_step_traced): called around every launch
     ec_trace_fn trace_cb = nullptr;
     void* trace_user = nullptr;
-    // chunked prefill: lanes of scratch rows (up to kPrefillChunk tokens of
-    // one sequence each, ~170 MB at 4B shapes) with their own stream,
-    // allocated on first use; lane 0 runs on st.  Several sequences' chunks
-    // run concurrently on the lanes (the 4B benchmark's eight prompts, MI355X:
-    // one lane 37.8k tok/s, two 46.0k, three 47.2k, four 47.5k).
-    static constexpr uint32_t kPrefillChunk = 512, kPrefillAttnSlots = 128, kPrefillLanes = 4;
+    // chunked prefill: lanes of scratch rows (a pass of up to kPrefillGroup
+    // sequences' chunks of kPrefillChunk tokens each, ~170 MB per sequence at
+    // 4B shapes) with their own stream, allocated on first use; lane 0 runs
+    // on st.  A lane's pass runs its sequences' chunks through the row ops and
+    // GEMMs together; several lanes' passes run concurrently.
+    static constexpr uint32_t kPrefillChunk = 512, kPrefillAttnSlots = 128, kPrefillLanes = 4, kPrefillGroup = 4;
     struct PrefillLane {
         bool ready = false;
+        uint32_t rows = 0;  // row capacity: group x kPrefillChunk
         hipStream_t st = nullptr;
         float *x = nullptr, *n = nullptr, *proj = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
         float *dec = nullptr, *beta = nullptr, *core = nullptr, *gu = nullptr, *attn = nullptr;
@@ -973,9 +974,10 @@ extern "C" size_t ec_engine_weight_bytes(const ec_engine* e) {
 namespace {
 using Lane = ec_engine::PrefillLane;
 
-int prefill_alloc(ec_engine* e, Lane& L, uint32_t i) {
+int prefill_alloc(ec_engine* e, Lane& L, uint32_t i, uint32_t group) {
     if (L.ready) return EC_OK;
-    const size_t C = ec_engine::kPrefillChunk;
+    const size_t C = (size_t)group * ec_engine::kPrefillChunk;  // rows of `group` sequences' chunks
+    const size_t C1 = ec_engine::kPrefillChunk;                  // per-sequence workspaces
     const size_t wide = std::max({(size_t)e->H, (size_t)e->F, (size_t)e->value_dim, (size_t)e->q_dim});
     // token activations of either matrix format (Q4_K for K % 256 == 0)
     const size_t act_rows_bytes = std::max(ec_gemm_act_bytes(EC_Q8_0, (uint32_t)C, (uint32_t)wide),
@@ -999,15 +1001,16 @@ int prefill_alloc(ec_engine* e, Lane& L, uint32_t i) {
         ((rc = dalloc(e, &L.q, C * e->key_dim)) || (rc = dalloc(e, &L.k, C * e->key_dim)) ||
          (rc = dalloc(e, &L.v, C * e->value_dim)) || (rc = dalloc(e, &L.dec, C * e->n_v)) ||
          (rc = dalloc(e, &L.beta, C * e->n_v)) || (rc = dalloc(e, &L.core, C * e->value_dim)) ||
-         (rc = dalloc(e, &L.dnws, ec_deltanet_chunked_ws_bytes((uint32_t)C, 1, e->n_v)))))
+         (rc = dalloc(e, &L.dnws, ec_deltanet_chunked_ws_bytes((uint32_t)C1, 1, e->n_v)))))
         return rc;
-    const size_t aws = ec_attn_prefill_ws_bytes((uint32_t)C, e->c.n_heads, e->c.max_ctx);
+    const size_t aws = ec_attn_prefill_ws_bytes((uint32_t)C1, e->c.n_heads, e->c.max_ctx);
     if (aws && (rc = dalloc(e, &L.aws, aws))) return rc;
     if ((rc = dalloc(e, &L.attn, C * e->q_dim)) ||
         (rc = dalloc(e, &L.ws, ec_attn_ws_bytes(ec_engine::kPrefillAttnSlots, e->c.n_heads, e->c.head_dim,
                                                 e->c.max_ctx))))
         return rc;
     L.h_pos.resize(C);
+    L.rows = (uint32_t)C;
     L.ready = true;
     return EC_OK;
 }
@@ -1033,12 +1036,24 @@ bool fused_act(const Mat& m, uint32_t max_k = 0xFFFFFFFFu) {
 }
 constexpr uint32_t kNormActMaxK = 4096;
 
-// One chunk of T tokens of sequence s at positions p .. p+T-1 through every
-// block, on the lane's stream (L.tok / L.pos already hold the chunk).
-int prefill_chunk(ec_engine* e, Lane& L, uint32_t s, uint32_t T, uint32_t p) {
+// A sequence's chunk inside a prefill pass: T tokens of sequence seq at
+// positions p .. p+T-1, in rows r0 .. r0+T-1 of the lane's buffers.
+struct PrefillSeg {
+    uint32_t seq, T, p, r0;
+};
+
+// One pass of the segments' chunks (rows 0 .. M-1, M = the sum of their T,
+// L.tok / L.pos already filled) through every block on the lane's stream: the
+// row ops and GEMMs take all M rows at once (a ragged multi-sequence GEMM:
+// each row's result is the one it gets alone), the ops that read or write a
+// sequence's own state (conv ring, recurrent state, KV cache, causal
+// attention) run per segment on its rows.
+int prefill_chunk(ec_engine* e, Lane& L, const PrefillSeg* sg, uint32_t nsg) {
     const ec_engine_cfg& c = e->c;
     const uint32_t H = e->H, F = e->F;
     hipStream_t st = L.st;
+    uint32_t T = 0;  // rows of the pass
+    for (uint32_t i = 0; i < nsg; ++i) T += sg[i].T;
     // every launch goes through launch() for ec_engine_prefill_traced (lane 0
     // runs on the engine stream); without a callback it is a plain call
 #define EC_PF(op, layer, xin, xout, call) \
@@ -1058,19 +1073,26 @@ int prefill_chunk(ec_engine* e, Lane& L, uint32_t s, uint32_t T, uint32_t p) {
             const uint32_t Nin = e->nin_delta;
             EC_PF(EC_OP_PF_GEMM_IN, li, in_buf, EC_B_PF_PROJ,
                   fin ? gemm_act(L, y.w_in, L.proj, T, Nin, 0) : gemm_rows(L, y.w_in, L.n, L.proj, T, Nin, 0));
-            float* ring = y.conv_state + (size_t)s * c.conv_kernel * e->conv_dim;
-            float* state = y.ssm_state + (size_t)s * e->n_v * 128 * 128;
-            EC_PF(EC_OP_PF_CONV, li, EC_B_PF_PROJ, EC_B_PF_Q,
-                  ec_glue_conv_gates_chunk(L.proj, Nin, ring, y.conv_w, y.a_log, y.dt_bias, L.q, L.k, L.v, L.dec,
-                                           L.beta, T, p, e->n_k, e->n_v, c.conv_kernel, st));
-            // chunked scan from 128 tokens on (MI355X, 32 heads: 64 tokens 21 us
-            // token loop vs 29 us chunked; 512 tokens 130 vs 71 us)
-            EC_PF(EC_OP_PF_DELTA, li, EC_B_PF_Q, EC_B_PF_CORE,
-                  T >= kChunkedDeltaMin
-                      ? ec_deltanet_chunked(state, L.q, L.k, L.v, L.dec, L.beta, L.core, T, 1, e->n_v, e->n_k, 128,
-                                            128, nullptr, L.dnws, st)
-                      : ec_deltanet(state, L.q, L.k, L.v, L.dec, L.beta, L.core, T, 1, e->n_v, e->n_k, 128, 128,
-                                    nullptr, st));
+            for (uint32_t i = 0; i < nsg; ++i) {
+                const uint32_t s = sg[i].seq, Ts = sg[i].T, p = sg[i].p;
+                const size_t r0 = sg[i].r0;
+                float* ring = y.conv_state + (size_t)s * c.conv_kernel * e->conv_dim;
+                float* state = y.ssm_state + (size_t)s * e->n_v * 128 * 128;
+                float *q = L.q + r0 * e->key_dim, *k = L.k + r0 * e->key_dim, *v = L.v + r0 * e->value_dim;
+                float *dec = L.dec + r0 * e->n_v, *beta = L.beta + r0 * e->n_v;
+                EC_PF(EC_OP_PF_CONV, li, EC_B_PF_PROJ, EC_B_PF_Q,
+                      ec_glue_conv_gates_chunk(L.proj + r0 * Nin, Nin, ring, y.conv_w, y.a_log, y.dt_bias, q, k, v,
+                                               dec, beta, Ts, p, e->n_k, e->n_v, c.conv_kernel, st));
+                // chunked scan from 128 tokens on (MI355X, 32 heads: 64 tokens 21 us
+                // token loop vs 29 us chunked; 512 tokens 130 vs 71 us)
+                float* core = L.core + r0 * e->value_dim;
+                EC_PF(EC_OP_PF_DELTA, li, EC_B_PF_Q, EC_B_PF_CORE,
+                      Ts >= kChunkedDeltaMin
+                          ? ec_deltanet_chunked(state, q, k, v, dec, beta, core, Ts, 1, e->n_v, e->n_k, 128, 128,
+                                                nullptr, L.dnws, st)
+                          : ec_deltanet(state, q, k, v, dec, beta, core, Ts, 1, e->n_v, e->n_k, 128, 128, nullptr,
+                                        st));
+            }
             if (fused_act(y.w_out)) {
                 EC_PF(EC_OP_PF_GATED_NORM, li, EC_B_PF_CORE, EC_B_PF_ACT,
                       ec_glue_gated_norm_rows_gemm_act(L.core, L.proj, Nin, e->conv_dim, y.ssm_norm, L.act, T, e->n_v,
@@ -1085,32 +1107,39 @@ int prefill_chunk(ec_engine* e, Lane& L, uint32_t s, uint32_t T, uint32_t p) {
             const uint32_t Nin = e->nin_attn;
             EC_PF(EC_OP_PF_GEMM_IN, li, in_buf, EC_B_PF_PROJ,
                   fin ? gemm_act(L, y.w_in, L.proj, T, Nin, 0) : gemm_rows(L, y.w_in, L.n, L.proj, T, Nin, 0));
-            int8_t* keys = y.keys + (size_t)s * e->seq_stride;
-            int8_t* vals = y.vals + (size_t)s * e->seq_stride;
-            float* ks = y.ks + (size_t)s * c.max_ctx * c.n_kv;
-            float* vs = y.vs + (size_t)s * c.max_ctx * c.n_kv;
-            // slots = the chunk's tokens sharing sequence s's cache (seq_stride 0)
-            EC_PF(EC_OP_PF_ROPE_APPEND, li, EC_B_PF_PROJ, EC_B_PF_N,
-                  ec_glue_qk_rope_append(L.proj, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn, e->inv_freq, L.pos,
-                                         L.n, nullptr, nullptr, keys, vals, ks, vs, L.ctx, T, 0, c.max_ctx,
-                                         c.n_heads, c.n_kv, c.head_dim, st));
-            // causal attention of the chunk's T queries (positions p .. p+T-1)
-            // over the sequence's cache, one pass per 32/G query tokens
-            const uint32_t G = c.n_heads / c.n_kv;
-            EC_PF(EC_OP_PF_ATTN, li, EC_B_PF_N, EC_B_PF_ATTN, [&]() -> int {
-                if (G == 1 || G == 2 || G == 4)
-                    return ec_attn_prefill(L.n, keys, vals, ks, vs, L.attn, T, (int32_t)p, c.n_heads, c.n_kv,
-                                           c.head_dim, c.max_ctx, L.aws, st);
-                // other group sizes: the decode kernel with the chunk's tokens
-                // as slots sharing the cache (ctx = position + 1)
-                for (uint32_t s0 = 0; s0 < T; s0 += ec_engine::kPrefillAttnSlots) {
-                    const uint32_t n = std::min(T - s0, ec_engine::kPrefillAttnSlots);
-                    EC_TRY(ec_attn_decode(L.n + (size_t)s0 * e->q_dim, keys, vals, ks, vs,
-                                          L.attn + (size_t)s0 * e->q_dim, L.ctx + s0, n, 0, c.n_heads, c.n_kv,
-                                          c.head_dim, c.max_ctx, L.ws, st));
-                }
-                return EC_OK;
-            }());
+            for (uint32_t i = 0; i < nsg; ++i) {
+                const uint32_t s = sg[i].seq, Ts = sg[i].T, p = sg[i].p;
+                const size_t r0 = sg[i].r0;
+                int8_t* keys = y.keys + (size_t)s * e->seq_stride;
+                int8_t* vals = y.vals + (size_t)s * e->seq_stride;
+                float* ks = y.ks + (size_t)s * c.max_ctx * c.n_kv;
+                float* vs = y.vs + (size_t)s * c.max_ctx * c.n_kv;
+                float* qn = L.n + r0 * e->q_dim;
+                float* ao = L.attn + r0 * e->q_dim;
+                int32_t* cx = L.ctx + r0;
+                // slots = the chunk's tokens sharing sequence s's cache (seq_stride 0)
+                EC_PF(EC_OP_PF_ROPE_APPEND, li, EC_B_PF_PROJ, EC_B_PF_N,
+                      ec_glue_qk_rope_append(L.proj + r0 * Nin, Nin, y.q_norm, y.k_norm, y.use_qn, y.use_kn,
+                                             e->inv_freq, L.pos + r0, qn, nullptr, nullptr, keys, vals, ks, vs, cx,
+                                             Ts, 0, c.max_ctx, c.n_heads, c.n_kv, c.head_dim, st));
+                // causal attention of the chunk's T queries (positions p .. p+T-1)
+                // over the sequence's cache, one pass per 32/G query tokens
+                const uint32_t G = c.n_heads / c.n_kv;
+                EC_PF(EC_OP_PF_ATTN, li, EC_B_PF_N, EC_B_PF_ATTN, [&]() -> int {
+                    if (G == 1 || G == 2 || G == 4)
+                        return ec_attn_prefill(qn, keys, vals, ks, vs, ao, Ts, (int32_t)p, c.n_heads, c.n_kv,
+                                               c.head_dim, c.max_ctx, L.aws, st);
+                    // other group sizes: the decode kernel with the chunk's tokens
+                    // as slots sharing the cache (ctx = position + 1)
+                    for (uint32_t s0 = 0; s0 < Ts; s0 += ec_engine::kPrefillAttnSlots) {
+                        const uint32_t n = std::min(Ts - s0, ec_engine::kPrefillAttnSlots);
+                        EC_TRY(ec_attn_decode(qn + (size_t)s0 * e->q_dim, keys, vals, ks, vs,
+                                              ao + (size_t)s0 * e->q_dim, cx + s0, n, 0, c.n_heads, c.n_kv,
+                                              c.head_dim, c.max_ctx, L.ws, st));
+                    }
+                    return EC_OK;
+                }());
+            }
             EC_PF(EC_OP_PF_GEMM_OUT, li, EC_B_PF_ATTN, EC_B_PF_X, gemm_rows(L, y.w_out, L.attn, L.x, T, H, 1));
         }
         if (fused_act(y.w_gu, kNormActMaxK)) {
@@ -1141,21 +1170,11 @@ struct PrefillJob {
     uint32_t done = 0;  // tokens already enqueued
 };
 
-// Enqueue the job's next chunk on lane L (the lane's previous chunk must have
-// completed: its token / position rows are overwritten).
-int prefill_step(ec_engine* e, Lane& L, PrefillJob& j) {
-    const uint32_t C = ec_engine::kPrefillChunk;
-    const uint32_t T = std::min(j.n - j.done, C), p = (uint32_t)j.pos0 + j.done;
-    for (uint32_t t = 0; t < T; ++t) L.h_pos[t] = (int32_t)(p + t);
-    EC_HIP(hipMemcpyAsync(L.tok, j.tokens + j.done, T * 4, hipMemcpyHostToDevice, L.st));
-    EC_HIP(hipMemcpyAsync(L.pos, L.h_pos.data(), T * 4, hipMemcpyHostToDevice, L.st));
-    EC_HIP(hipStreamSynchronize(L.st));  // pageable sources: the copies are complete before h_pos is reused
-    EC_TRY(prefill_chunk(e, L, j.seq, T, p));
-    j.done += T;
-    if (j.done < j.n) return EC_OK;
-    // the last token's logits and greedy next token; pos[seq] = pos0 + n
+// The last token's logits and greedy next token of a finished job, whose last
+// chunk sits in the lane's rows r0 .. r0+T-1; pos[seq] = pos0 + n.
+int prefill_head(ec_engine* e, Lane& L, const PrefillJob& j, uint32_t r_last) {
     const int32_t last = j.pos0 + (int32_t)j.n - 1;
-    const float* xl = L.x + (size_t)(T - 1) * e->H;
+    const float* xl = L.x + (size_t)r_last * e->H;
     EC_TRY(launch(e, EC_OP_PF_HEAD, -1, 0, EC_B_PF_X, EC_B_LOGITS, [&]() -> int {
         if (e->lm_head.fmt == EC_Q4_K) {
             EC_TRY(ec_glue_rmsnorm_rows(xl, e->final_norm, L.n, 1, e->H, L.st));
@@ -1173,23 +1192,61 @@ int prefill_step(ec_engine* e, Lane& L, PrefillJob& j) {
     return EC_OK;
 }
 
-// Run the jobs over `lanes` lanes: each lane takes the next unstarted job when
-// its current one is done; lanes alternate so that one lane's chunk is queued
-// while the other's runs.
-int prefill_run(ec_engine* e, std::vector<PrefillJob>& jobs, uint32_t lanes) {
-    lanes = std::max(1u, std::min({lanes, ec_engine::kPrefillLanes, (uint32_t)jobs.size()}));
-    for (uint32_t i = 0; i < lanes; ++i) EC_TRY(prefill_alloc(e, e->pf[i], i));
+// Enqueue the next chunk of each of the lane's jobs (at most its row
+// capacity / kPrefillChunk) as one pass, job i's chunk after job i-1's rows
+// (the lane's previous pass must have completed: its token / position rows
+// are overwritten).
+int prefill_step(ec_engine* e, Lane& L, PrefillJob* const* js, uint32_t nj) {
+    const uint32_t C = ec_engine::kPrefillChunk;
+    PrefillSeg sg[ec_engine::kPrefillGroup];
+    uint32_t r0 = 0;
+    for (uint32_t i = 0; i < nj; ++i) {
+        const PrefillJob& j = *js[i];
+        const uint32_t T = std::min(j.n - j.done, C), p = (uint32_t)j.pos0 + j.done;
+        for (uint32_t t = 0; t < T; ++t) L.h_pos[r0 + t] = (int32_t)(p + t);
+        EC_HIP(hipMemcpyAsync(L.tok + r0, j.tokens + j.done, T * 4, hipMemcpyHostToDevice, L.st));
+        sg[i] = {j.seq, T, p, r0};
+        r0 += T;
+    }
+    EC_HIP(hipMemcpyAsync(L.pos, L.h_pos.data(), r0 * 4, hipMemcpyHostToDevice, L.st));
+    EC_HIP(hipStreamSynchronize(L.st));  // pageable sources: the copies are complete before h_pos is reused
+    EC_TRY(prefill_chunk(e, L, sg, nj));
+    for (uint32_t i = 0; i < nj; ++i) {
+        PrefillJob& j = *js[i];
+        j.done += sg[i].T;
+        if (j.done == j.n) EC_TRY(prefill_head(e, L, j, sg[i].r0 + sg[i].T - 1));
+    }
+    return EC_OK;
+}
+
+// Run the jobs over `lanes` lanes of `group` sequences each: a lane's slots
+// take the next unstarted job when theirs is done, and each pass runs one
+// chunk of every job the lane holds; lanes alternate so that one lane's pass
+// is queued while another's runs.
+int prefill_run(ec_engine* e, std::vector<PrefillJob>& jobs, uint32_t lanes, uint32_t group) {
+    group = std::max(1u, std::min(group, ec_engine::kPrefillGroup));
+    lanes = std::max(1u, std::min({lanes, ec_engine::kPrefillLanes,
+                                   (uint32_t)((jobs.size() + group - 1) / group)}));
+    for (uint32_t i = 0; i < lanes; ++i) EC_TRY(prefill_alloc(e, e->pf[i], i, group));
+    for (uint32_t i = 0; i < lanes; ++i)  // lanes allocated earlier may hold fewer rows
+        group = std::min(group, e->pf[i].rows / ec_engine::kPrefillChunk);
     EC_HIP(hipStreamSynchronize(e->st));  // whatever the decode stream queued before
-    std::vector<int> cur(lanes, -1);
+    std::vector<int> cur((size_t)lanes * group, -1);
     uint32_t next = 0;
     int rc = EC_OK;
     for (bool any = true; any && rc == EC_OK;) {
         any = false;
         for (uint32_t i = 0; i < lanes && rc == EC_OK; ++i) {
-            if (cur[i] < 0 || jobs[cur[i]].done == jobs[cur[i]].n) cur[i] = next < jobs.size() ? (int)next++ : -1;
-            if (cur[i] < 0) continue;
+            PrefillJob* act[ec_engine::kPrefillGroup];
+            uint32_t na = 0;
+            for (uint32_t g = 0; g < group; ++g) {
+                int& c = cur[(size_t)i * group + g];
+                if (c < 0 || jobs[c].done == jobs[c].n) c = next < jobs.size() ? (int)next++ : -1;
+                if (c >= 0) act[na++] = &jobs[c];
+            }
+            if (na == 0) continue;
             any = true;
-            rc = prefill_step(e, e->pf[i], jobs[cur[i]]);
+            rc = prefill_step(e, e->pf[i], act, na);
         }
     }
     // every lane drained, also after an error (no work left in flight)
@@ -1198,6 +1255,16 @@ int prefill_run(ec_engine* e, std::vector<PrefillJob>& jobs, uint32_t lanes) {
         if (rc == EC_OK && se != hipSuccess) rc = ec_set_hip_error_host(se, "ec_engine_prefill: stream");
     }
     return rc;
+}
+
+// Sequences per prefill pass (EC_PREFILL_GROUP = 1 .. 4, for comparison).
+uint32_t prefill_group() {
+    static const uint32_t g = [] {
+        const char* v = getenv("EC_PREFILL_GROUP");
+        const uint32_t n = v ? (uint32_t)atoi(v) : 0u;
+        return n >= 1 && n <= ec_engine::kPrefillGroup ? n : 2u;
+    }();
+    return g;
 }
 
 int check_prefill_args(ec_engine* e, uint32_t seq, const int32_t* tokens, uint32_t n, int32_t pos0, const char* who) {
@@ -1220,7 +1287,7 @@ int check_prefill_args(ec_engine* e, uint32_t seq, const int32_t* tokens, uint32
 extern "C" int ec_engine_prefill(ec_engine* e, uint32_t seq, const int32_t* tokens, uint32_t n, int32_t pos0) {
     EC_TRY(check_prefill_args(e, seq, tokens, n, pos0, "ec_engine_prefill"));
     std::vector<PrefillJob> jobs{PrefillJob{seq, n, tokens, pos0}};
-    return prefill_run(e, jobs, 1);
+    return prefill_run(e, jobs, 1, prefill_group());
 }
 
 extern "C" int ec_engine_prefill_traced(ec_engine* e, uint32_t seq, const int32_t* tokens, uint32_t n, int32_t pos0,
@@ -1230,7 +1297,7 @@ extern "C" int ec_engine_prefill_traced(ec_engine* e, uint32_t seq, const int32_
     std::vector<PrefillJob> jobs{PrefillJob{seq, n, tokens, pos0}};
     e->trace_cb = cb;
     e->trace_user = user;
-    const int rc = prefill_run(e, jobs, 1);
+    const int rc = prefill_run(e, jobs, 1, prefill_group());
     e->trace_cb = nullptr;
     e->trace_user = nullptr;
     return rc;
@@ -1247,12 +1314,15 @@ extern "C" int ec_engine_prefill_batch(ec_engine* e, uint32_t n_seqs, const uint
         jobs.push_back(PrefillJob{seqs[i], lens[i], tokens[i], pos0[i]});
     }
     if (jobs.empty()) return EC_OK;
-    // EC_PREFILL_LANES = 1 .. 4 runs fewer lanes, for comparison
+    // Two lanes of two sequences each (the 4B benchmark's eight prompts on one
+    // box, tok/s, lanes x sequences per pass: 4 x 1 48.3k, 2 x 2 49.0k, 3 x 2
+    // 48.7k, 4 x 2 48.6k, 2 x 4 48.2k, 1 x 4 46.3k; one lane of one sequence
+    // 37.8k).  EC_PREFILL_LANES = 1 .. 4 sets the lanes, for comparison.
     static const uint32_t lanes_env = [] {
         const char* v = getenv("EC_PREFILL_LANES");
         return v ? (uint32_t)atoi(v) : 0u;
     }();
-    return prefill_run(e, jobs, lanes_env >= 1 ? lanes_env : ec_engine::kPrefillLanes);
+    return prefill_run(e, jobs, lanes_env >= 1 ? lanes_env : 2u, prefill_group());
 }
 
 extern "C" int ec_engine_profile_matvecs(ec_engine* e, uint32_t reps, uint32_t* launches, double* bytes_per_step,

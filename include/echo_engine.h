@@ -138,8 +138,9 @@ int ec_engine_set_inputs(ec_engine* e, const int32_t* tok, const int32_t* pos, u
  * `gen`, the last token's logits); other sequences are untouched.  Synchronous. */
 int ec_engine_prefill(ec_engine* e, uint32_t seq, const int32_t* tokens, uint32_t n, int32_t pos0);
 /* ec_engine_prefill of n_seqs distinct sequences (seqs[i], tokens[i][0 ..
- * lens[i]), positions from pos0[i]); the sequences' chunks run concurrently
- * on up to four streams, each sequence's result bit for bit that of
+ * lens[i]), positions from pos0[i]); two sequences' chunks at a time share
+ * each row op and GEMM (one launch over both chunks' rows), two such passes
+ * run concurrently on two streams, each sequence's result bit for bit that of
  * ec_engine_prefill.  Synchronous. */
 int ec_engine_prefill_batch(ec_engine* e, uint32_t n_seqs, const uint32_t* seqs, const int32_t* const* tokens,
                             const uint32_t* lens, const int32_t* pos0);

@@ -216,7 +216,7 @@ def test_prefill_matches_token_loop(lens, fmts):
 
 
 def test_prefill_batch_equals_one_by_one():
-    """ec_engine_prefill_batch (sequences on up to four streams) == ec_engine_prefill per
+    """ec_engine_prefill_batch (two sequences' chunks per pass, two passes on two streams) == ec_engine_prefill per
     sequence, bit for bit: logits, greedy tokens, positions, every state;
     ragged lengths across chunk boundaries, a nonzero start position."""
     from echohip.engine import Engine
