@@ -302,3 +302,62 @@ def test_prefill_one_token_is_the_decode_step(fmts):
     assert a.tokens()[0][1] == b.tokens()[0][1]
     a.close()
     b.close()
+
+
+_ARRANGEMENT_SCRIPT = r"""
+import sys
+sys.path[:0] = [{tests!r}, {pkg!r}]
+from test_gpu_prefill import _batch_digest
+print("digest", _batch_digest(), flush=True)
+"""
+
+
+def _batch_digest():
+    """One ragged prefill_batch (5 sequences, 1 .. 1100 tokens, one starting at
+    position 10) on a small hybrid model; a digest of every sequence's greedy
+    token, position, logits and states."""
+    import hashlib
+    from echohip.engine import Engine
+    cfg = small_config(max_batch=5, max_ctx=1200)
+    m = make_model(cfg, seed=31)
+    rng = np.random.default_rng(8)
+    lens = [1100, 1, 530, 64, 200]
+    prompts = [rng.integers(0, cfg.vocab, n).astype(np.int32) for n in lens]
+    e = Engine(cfg)
+    upload(e, m)
+    e.reset()
+    e.prefill(4, prompts[4][:10], 0)
+    e.prefill_batch([(s, prompts[s], 0) for s in range(4)] + [(4, prompts[4][10:], 10)])
+    h = hashlib.sha256()
+    g, p = e.tokens()
+    h.update(g.tobytes())
+    h.update(p.tobytes())
+    for s in range(5):
+        h.update(e.logits(s).tobytes())
+        for key, v in sorted(_states(e, cfg, s).items()):
+            h.update(v.tobytes())
+    e.close()
+    return h.hexdigest()
+
+
+def test_prefill_batch_arrangements_bit_identical():
+    """The ragged multi-sequence prefill gives the same bits however the
+    sequences are arranged: lanes x sequences per pass of 1 x 1, 1 x 3, 3 x 2
+    and 2 x 4 (EC_PREFILL_LANES / EC_PREFILL_GROUP are read once per process,
+    so each arrangement runs in a child process, one after another) equal the
+    default arrangement run here -- row ops and GEMMs give each row the result
+    it gets alone, whatever rows share the launch."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    here = Path(__file__).resolve().parent
+    ref = _batch_digest()
+    script = _ARRANGEMENT_SCRIPT.format(tests=str(here), pkg=str(here.parent / "echo-core_amd"))
+    for lanes, group in ((1, 1), (1, 3), (3, 2), (2, 4)):
+        env = dict(os.environ, EC_PREFILL_LANES=str(lanes), EC_PREFILL_GROUP=str(group))
+        print(f"arrangement lanes={lanes} group={group}", flush=True)
+        r = subprocess.run([sys.executable, "-c", script], env=env, capture_output=True, text=True, timeout=150)
+        assert r.returncode == 0, r.stderr[-2000:]
+        got = [ln.split()[1] for ln in r.stdout.splitlines() if ln.startswith("digest ")]
+        assert got == [ref], (lanes, group, got, ref)
