@@ -708,17 +708,15 @@ __global__ __launch_bounds__(256) void k_qk_rope_append(const float* __restrict_
 }
 
 // ----------------------------------------------------------------- argmax
-// grid (n_seq), block 1024: first index of the maximum (engine.zig:860-867).
-// Active sequences write the token to gen and next and advance pos.
-__global__ __launch_bounds__(1024) void k_argmax_advance(const float* __restrict__ logits, uint32_t vocab,
-                                                         int32_t* __restrict__ gen, int32_t* __restrict__ next,
-                                                         int32_t* __restrict__ pos, uint32_t max_pos) {
-    __shared__ float sv[16];
-    __shared__ int32_t si[16];
-    const uint32_t s = blockIdx.x, t = threadIdx.x;
-    const float* l = logits + (size_t)s * vocab;
-    float best = -INFINITY;
-    int32_t bi = 0x7FFFFFFF;
+// First index of the maximum over l[lo, hi) (engine.zig:860-867): a value is
+// taken when strictly greater than the best so far, so NaN never is and ties
+// keep the lower index; thread 0 of the 1024-thread workgroup gets (best, bi),
+// bi = 0x7FFFFFFF when nothing was taken.  lo is a multiple of 4.
+__device__ __forceinline__ void argmax_range(const float* __restrict__ l, uint32_t lo, uint32_t hi, float& best,
+                                             int32_t& bi, float* sv, int32_t* si) {
+    const uint32_t t = threadIdx.x;
+    best = -INFINITY;
+    bi = 0x7FFFFFFF;
     // strictly greater keeps the first index among equal values within a thread
     // (its indices only grow); the reductions below break ties by index
     auto take = [&](float v, uint32_t k) {
@@ -727,9 +725,9 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float* __restrict
             bi = (int32_t)k;
         }
     };
-    if ((((uintptr_t)l) & 15) == 0) {
-        const uint32_t n4 = vocab / 4;
-        const float4* l4 = (const float4*)l;
+    if ((((uintptr_t)(l + lo)) & 15) == 0) {
+        const uint32_t n4 = (hi - lo) / 4;
+        const float4* l4 = (const float4*)(l + lo);
         uint32_t k = t;
         for (; k + 3 * 1024 < n4; k += 4 * 1024) {
             float4 v[4];
@@ -737,17 +735,18 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float* __restrict
             for (int u = 0; u < 4; ++u) v[u] = l4[k + u * 1024];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const uint32_t b = 4 * (k + u * 1024);
+                const uint32_t b = lo + 4 * (k + u * 1024);
                 take(v[u].x, b), take(v[u].y, b + 1), take(v[u].z, b + 2), take(v[u].w, b + 3);
             }
         }
         for (; k < n4; k += 1024) {
             const float4 v = l4[k];
-            take(v.x, 4 * k), take(v.y, 4 * k + 1), take(v.z, 4 * k + 2), take(v.w, 4 * k + 3);
+            const uint32_t b = lo + 4 * k;
+            take(v.x, b), take(v.y, b + 1), take(v.z, b + 2), take(v.w, b + 3);
         }
-        for (uint32_t r = 4 * n4 + t; r < vocab; r += 1024) take(l[r], r);
+        for (uint32_t r = lo + 4 * n4 + t; r < hi; r += 1024) take(l[r], r);
     } else {
-        for (uint32_t k = t; k < vocab; k += 1024) take(l[k], k);
+        for (uint32_t k = lo + t; k < hi; k += 1024) take(l[k], k);
     }
     auto merge = [&](float ov, int32_t oi) {
         if (ov > best || (ov == best && oi < bi)) {
@@ -772,16 +771,78 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float* __restrict
                 best = sv[w];
                 bi = si[w];
             }
-        if (bi == 0x7FFFFFFF) bi = 0;  // all NaN: token 0, as the reference's scan
-        if (pos[s] >= 0) {
-            gen[s] = bi;
-            next[s] = bi;
-            // a sequence whose next position would be past the cache ends here:
-            // it becomes inactive (pos -1) instead of decoding without attention
-            const int32_t np = pos[s] + 1;
-            pos[s] = (max_pos != 0 && (uint32_t)np >= max_pos) ? -1 : np;
-        }
     }
+}
+
+// Write the pick of sequence s (nothing taken: token 0, as the reference's
+// scan) and advance its position.
+__device__ __forceinline__ void argmax_commit(int32_t bi, uint32_t s, int32_t* __restrict__ gen,
+                                              int32_t* __restrict__ next, int32_t* __restrict__ pos,
+                                              uint32_t max_pos) {
+    if (bi == 0x7FFFFFFF) bi = 0;
+    if (pos[s] >= 0) {
+        gen[s] = bi;
+        next[s] = bi;
+        // a sequence whose next position would be past the cache ends here:
+        // it becomes inactive (pos -1) instead of decoding without attention
+        const int32_t np = pos[s] + 1;
+        pos[s] = (max_pos != 0 && (uint32_t)np >= max_pos) ? -1 : np;
+    }
+}
+
+// grid (n_seq), block 1024: the whole row per workgroup.  Active sequences
+// write the token to gen and next and advance pos.
+__global__ __launch_bounds__(1024) void k_argmax_advance(const float* __restrict__ logits, uint32_t vocab,
+                                                         int32_t* __restrict__ gen, int32_t* __restrict__ next,
+                                                         int32_t* __restrict__ pos, uint32_t max_pos) {
+    __shared__ float sv[16];
+    __shared__ int32_t si[16];
+    const uint32_t s = blockIdx.x;
+    float best;
+    int32_t bi;
+    argmax_range(logits + (size_t)s * vocab, 0, vocab, best, bi, sv, si);
+    if (threadIdx.x == 0) argmax_commit(bi, s, gen, next, pos, max_pos);
+}
+
+// Two launches over more CUs: grid (nsl, n_seq), block 1024, slice z of row s
+// (a multiple of 4 entries, the last one shorter) -> part[s * nsl + z] =
+// (best, index); then k_argmax_finish, grid (n_seq), one wave: the slices'
+// picks merged with the same rule (greater, or equal and a lower index).
+__global__ __launch_bounds__(1024) void k_argmax_slices(const float* __restrict__ logits, uint32_t vocab,
+                                                        uint32_t slice, float2* __restrict__ part) {
+    __shared__ float sv[16];
+    __shared__ int32_t si[16];
+    const uint32_t z = blockIdx.x, s = blockIdx.y, nsl = gridDim.x;
+    const uint32_t lo = min(z * slice, vocab), hi = min(lo + slice, vocab);
+    float best;
+    int32_t bi;
+    argmax_range(logits + (size_t)s * vocab, lo, hi, best, bi, sv, si);
+    if (threadIdx.x == 0) part[(size_t)s * nsl + z] = make_float2(best, __int_as_float(bi));
+}
+
+__global__ __launch_bounds__(64) void k_argmax_finish(const float2* __restrict__ part, uint32_t nsl,
+                                                      int32_t* __restrict__ gen, int32_t* __restrict__ next,
+                                                      int32_t* __restrict__ pos, uint32_t max_pos) {
+    const uint32_t s = blockIdx.x, lane = threadIdx.x;
+    float best = -INFINITY;
+    int32_t bi = 0x7FFFFFFF;
+    auto merge = [&](float ov, int32_t oi) {
+        if (ov > best || (ov == best && oi < bi)) {
+            best = ov;
+            bi = oi;
+        }
+    };
+    for (uint32_t z = lane; z < nsl; z += 64) {
+        const float2 p = part[(size_t)s * nsl + z];
+        merge(p.x, __float_as_int(p.y));
+    }
+    merge(lane_xor<32>(best), lane_xor_i<32>(bi));
+    merge(lane_xor<16>(best), lane_xor_i<16>(bi));
+    merge(lane_xor<8>(best), lane_xor_i<8>(bi));
+    merge(lane_xor<4>(best), lane_xor_i<4>(bi));
+    merge(lane_xor<2>(best), lane_xor_i<2>(bi));
+    merge(lane_xor<1>(best), lane_xor_i<1>(bi));
+    if (lane == 0) argmax_commit(bi, s, gen, next, pos, max_pos);
 }
 
 }  // namespace ec
@@ -1038,4 +1099,21 @@ extern "C" int ec_glue_argmax_advance_bounded(const float* logits, uint32_t voca
 extern "C" int ec_glue_argmax_advance(const float* logits, uint32_t vocab, int32_t* gen, int32_t* next, int32_t* pos,
                                       uint32_t n_seq, void* stream) {
     return ec_glue_argmax_advance_bounded(logits, vocab, gen, next, pos, n_seq, 0, stream);
+}
+
+extern "C" size_t ec_glue_argmax_ws_bytes(uint32_t n_seq, uint32_t slices) {
+    return (size_t)n_seq * slices * sizeof(float2);
+}
+
+extern "C" int ec_glue_argmax_advance_sliced(const float* logits, uint32_t vocab, int32_t* gen, int32_t* next,
+                                             int32_t* pos, uint32_t n_seq, uint32_t max_pos, uint32_t slices,
+                                             void* ws, void* stream) {
+    if (!logits || !gen || !next || !pos || !ws || slices == 0 || slices > 1024 || n_seq > 65535)
+        return ec_set_error(EC_ERR_ARG, "ec_glue_argmax_advance_sliced: bad argument");
+    if (n_seq == 0) return EC_OK;
+    const uint32_t slice = ((vocab + slices - 1) / slices + 3) / 4 * 4;
+    const hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(k_argmax_slices, dim3(slices, n_seq), dim3(1024), 0, st, logits, vocab, slice, (float2*)ws);
+    EC_CHECK_LAUNCH();
+    EC_GLUE_LAUNCH(k_argmax_finish, dim3(n_seq), dim3(64), 0, st, (const float2*)ws, slices, gen, next, pos, max_pos);
 }

@@ -76,6 +76,7 @@ _SIGS = {
     "ec_block_dots_pieces": [C.c_int, _u32, _vp, _vp, _vp, _u32, _u32, _u32, _vp],
     "ec_glue_rmsnorm_quant_pieces": [_vp, _vp, _vp, _u32, _u32, _u32, _vp],
     "ec_glue_argmax_advance_bounded": [_vp, _u32, _vp, _vp, _vp, _u32, _u32, _vp],
+    "ec_glue_argmax_advance_sliced": [_vp, _u32, _vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp],
     "ec_glue_add_rmsnorm_quant_pieces": [_vp, _vp, _u32, _vp, _vp, _vp, _u32, _u32, _u32, _vp],
     "ec_glue_swiglu_quant_split_pieces": [_vp, _u32, _vp, _u32, _u32, _u32, _vp],
     "ec_glue_gated_norm_quant_pieces": [_vp, _vp, _u32, _u32, _vp, _vp, _u32, _u32, _u32, _vp],
@@ -95,6 +96,7 @@ _SIZE_FNS = {
     "ec_attn_noalloc_max_bytes": [],
     "ec_deltanet_chunked_ws_bytes": [_u32, _u32, _u32],
     "ec_attn_prefill_ws_bytes": [_u32, _u32, _u32],
+    "ec_glue_argmax_ws_bytes": [_u32, _u32],
 }
 
 
@@ -310,9 +312,16 @@ class Lib:
         self._call("ec_glue_gated_norm_rows_gemm_act", _ptr(core), _ptr(proj), Nin, z_off, _ptr(norm_w), _ptr(act), M,
                    n_v, self._stream(stream))
 
-    def argmax_advance(self, logits, vocab, gen, nxt, pos, n_seq, max_pos=0, stream=None):
-        self._call("ec_glue_argmax_advance_bounded", _ptr(logits), vocab, _ptr(gen), _ptr(nxt), _ptr(pos), n_seq,
-                   max_pos, self._stream(stream))
+    def argmax_advance(self, logits, vocab, gen, nxt, pos, n_seq, max_pos=0, stream=None, slices=0, ws=None):
+        if slices:
+            self._call("ec_glue_argmax_advance_sliced", _ptr(logits), vocab, _ptr(gen), _ptr(nxt), _ptr(pos), n_seq,
+                       max_pos, slices, _ptr(ws), self._stream(stream))
+        else:
+            self._call("ec_glue_argmax_advance_bounded", _ptr(logits), vocab, _ptr(gen), _ptr(nxt), _ptr(pos), n_seq,
+                       max_pos, self._stream(stream))
+
+    def argmax_ws_bytes(self, n_seq, slices):
+        return self.L.ec_glue_argmax_ws_bytes(n_seq, slices)
 
     def rmsnorm_quant(self, x, w, act, M, H, stream=None, pieces=1):
         if pieces == 1:

@@ -95,6 +95,7 @@ struct ec_engine {
     float *dec = nullptr, *beta = nullptr, *qbuf = nullptr, *attn_out = nullptr, *logits = nullptr;
     float* inv_freq = nullptr;
     void *act_h = nullptr, *act_v = nullptr, *act_f = nullptr, *act_q = nullptr, *attn_ws = nullptr;
+    void* am_ws = nullptr;  // per-slice picks of the greedy argmax
     void* q_packed = nullptr;
     float* q_scales = nullptr;
     // inputs of Q4_K matrices (allocated with the first one): fp32 rows of the
@@ -306,6 +307,20 @@ int mv_split(ec_engine* e, const Mat& m, const void* act, float* y, uint32_t ns)
 // Residual projection: ns = resid_split(m) partial sums into e->parts.
 int mv_resid(ec_engine* e, const Mat& m, const void* act, uint32_t ns) { return mv_split(e, m, act, e->parts, ns); }
 
+// Slices of the decode step's greedy pick: a row per 1024-thread workgroup
+// reads ~600 KB of logits through one CU at 151936 entries; 16 slices spread
+// it over 16x the CUs, merged by a second small launch.  0 = one launch (short
+// vocabularies); EC_ARGMAX_SLICES overrides (0 .. 64), for comparison.
+constexpr uint32_t kArgmaxSlicesMax = 64;
+uint32_t argmax_slices(uint32_t vocab) {
+    static const int env = [] {
+        const char* v = getenv("EC_ARGMAX_SLICES");
+        return v ? atoi(v) : -1;
+    }();
+    if (env >= 0) return std::min((uint32_t)env, kArgmaxSlicesMax);
+    return vocab >= 32768 ? 16u : 0u;
+}
+
 // One launch of the decode step; with a trace callback installed, the stream
 // is drained and the callback called before and after it.
 template <class F>
@@ -448,8 +463,11 @@ int record_step(ec_engine* e) {
     EC_TRY(norm(e->final_norm, -1, q4(e->lm_head)));
     EC_MV(EC_OP_LM_HEAD, -1, 0, aid(e->lm_head, EC_B_ACT_H, EC_B_ACT4_H),
           mv(e, e->lm_head, ain(e->lm_head, e->act_h, e->act4_h), e->logits, c.vocab, 0));
+    const uint32_t nsl = argmax_slices(c.vocab);
     EC_GLUE(EC_OP_ARGMAX, -1, 0, -1, -1,
-            ec_glue_argmax_advance_bounded(e->logits, c.vocab, e->gen, e->tok, e->pos, B, c.max_ctx, st));
+            nsl ? ec_glue_argmax_advance_sliced(e->logits, c.vocab, e->gen, e->tok, e->pos, B, c.max_ctx, nsl,
+                                                e->am_ws, st)
+                : ec_glue_argmax_advance_bounded(e->logits, c.vocab, e->gen, e->tok, e->pos, B, c.max_ctx, st));
     return EC_OK;
 #undef EC_GLUE
 #undef EC_MV
@@ -544,6 +562,7 @@ extern "C" int ec_engine_create(const ec_engine_cfg* cfg, ec_engine** out) {
         (rc = dalloc(e, &e->dec, (size_t)B * e->n_v)) || (rc = dalloc(e, &e->beta, (size_t)B * e->n_v)) ||
         (rc = dalloc(e, &e->qbuf, (size_t)B * e->q_dim)) || (rc = dalloc(e, &e->attn_out, (size_t)B * e->q_dim)) ||
         (rc = dalloc(e, &e->logits, (size_t)B * c.vocab)) || (rc = dalloc(e, &e->inv_freq, c.head_dim / 2)) ||
+        (rc = dalloc(e, &e->am_ws, ec_glue_argmax_ws_bytes(B, kArgmaxSlicesMax))) ||
         (rc = dalloc(e, &e->act_h, ec_act_bytes_pieces(EC_Q8_0, B, H, 2))) ||
         (rc = dalloc(e, &e->act_v, ec_act_bytes_pieces(EC_Q8_0, B, e->value_dim, 2))) ||
         (rc = dalloc(e, &e->act_f, ec_act_bytes_pieces(EC_Q8_0, B, e->F, 2))) ||

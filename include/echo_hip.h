@@ -330,6 +330,13 @@ int ec_glue_argmax_advance(const float* logits, uint32_t vocab, int32_t* gen, in
                            uint32_t n_seq, void* stream);
 int ec_glue_argmax_advance_bounded(const float* logits, uint32_t vocab, int32_t* gen, int32_t* next, int32_t* pos,
                                    uint32_t n_seq, uint32_t max_pos, void* stream);
+/* The same pick in two launches over more CUs: each row cut into `slices`
+ * (1 .. 1024) ranges whose picks go to ws (ec_glue_argmax_ws_bytes(n_seq,
+ * slices) bytes), then merged per sequence; identical results.  Calls sharing
+ * ws must not overlap. */
+size_t ec_glue_argmax_ws_bytes(uint32_t n_seq, uint32_t slices);
+int ec_glue_argmax_advance_sliced(const float* logits, uint32_t vocab, int32_t* gen, int32_t* next, int32_t* pos,
+                                  uint32_t n_seq, uint32_t max_pos, uint32_t slices, void* ws, void* stream);
 
 /* ------------------------------------------------- chunked prefill glue
  * T consecutive tokens of ONE sequence at positions p0 .. p0+T-1.

@@ -292,13 +292,16 @@ def _argmax_ref(row):
     return bi
 
 
+@pytest.mark.parametrize("slices", [0, 16, 7, 64])
 @pytest.mark.parametrize("vocab", [151936, 151935, 1000, 7, 70001])
-def test_argmax_advance_edge_cases(hip, vocab):
-    """ec_glue_argmax_advance_bounded on rows with ties at the maximum (first
-    index wins, also across float4 groups and threads), NaNs, -inf, an all-NaN
-    and an all -inf row (token 0), -0.0 against +0.0, unaligned rows (vocab % 4
-    != 0), an inactive sequence (pos < 0: nothing written) and the max_pos
-    bound (a sequence whose next position would reach it becomes inactive)."""
+def test_argmax_advance_edge_cases(hip, vocab, slices):
+    """ec_glue_argmax_advance_bounded (slices = 0) and the two-launch
+    ec_glue_argmax_advance_sliced on rows with ties at the maximum (first index
+    wins, also across float4 groups, threads and slices), NaNs, -inf, an
+    all-NaN and an all -inf row (token 0), -0.0 against +0.0, unaligned rows
+    (vocab % 4 != 0), more slices than 4-entry groups (vocab 7: empty slices),
+    an inactive sequence (pos < 0: nothing written) and the max_pos bound (a
+    sequence whose next position would reach it becomes inactive)."""
     import torch
     rng = np.random.default_rng(vocab)
     rows = []
@@ -330,9 +333,10 @@ def test_argmax_advance_edge_cases(hip, vocab):
     gen = torch.full((n,), -7, dtype=torch.int32, device="cuda")
     nxt = torch.full((n,), -7, dtype=torch.int32, device="cuda")
     pos = torch.from_numpy(pos0.copy()).cuda()
+    ws = torch.empty(max(1, hip.argmax_ws_bytes(n, slices)), dtype=torch.uint8, device="cuda")
     for rep in range(2):  # a second call on the advanced positions
         before = pos.cpu().numpy().copy()
-        hip.argmax_advance(logits, vocab, gen, nxt, pos, n, max_pos)
+        hip.argmax_advance(logits, vocab, gen, nxt, pos, n, max_pos, slices=slices, ws=ws)
         torch.cuda.synchronize()
         g, q, p = gen.cpu().numpy(), nxt.cpu().numpy(), pos.cpu().numpy()
         for s in range(n):
