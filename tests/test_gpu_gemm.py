@@ -89,7 +89,9 @@ def _q4k_perm(K):
 
 CASES = [(Q8_0, 37, 256, 512), (Q8_0, 512, 9216, 2560), (Q8_0, 512, 2560, 9216), (Q8_0, 100, 272, 384),
          (Q8_0, 19, 48, 160), (Q8_0, 70, 40, 4128),
-         (Q4_K, 37, 256, 512), (Q4_K, 512, 9216, 2560), (Q4_K, 512, 2560, 9216), (Q4_K, 64, 48, 768)]
+         (Q4_K, 37, 256, 512), (Q4_K, 512, 9216, 2560), (Q4_K, 512, 2560, 9216), (Q4_K, 64, 48, 768),
+         # the rows of a ragged multi-sequence prefill pass (two or more chunks)
+         (Q8_0, 1024, 2560, 2560), (Q8_0, 1100, 272, 512), (Q4_K, 1030, 256, 768), (Q4_K, 2048, 96, 512)]
 
 
 @pytest.mark.parametrize("fmt,M,N,K", CASES)

@@ -215,13 +215,15 @@ def test_prefill_matches_token_loop(lens, fmts):
     b.close()
 
 
-def test_prefill_batch_equals_one_by_one():
+@pytest.mark.parametrize("fmts", [None, MIXED_FMTS], ids=["q8_0", "mixed"])
+def test_prefill_batch_equals_one_by_one(fmts):
     """ec_engine_prefill_batch (two sequences' chunks per pass, two passes on two streams) == ec_engine_prefill per
     sequence, bit for bit: logits, greedy tokens, positions, every state;
-    ragged lengths across chunk boundaries, a nonzero start position."""
+    ragged lengths across chunk boundaries, a nonzero start position; Q8_0
+    weights and a mix of Q8_0 / Q4_K matrices (Q4_K GEMMs over the pass's rows)."""
     from echohip.engine import Engine
     cfg = small_config(max_batch=4, max_ctx=700)
-    m = make_model(cfg, seed=25)
+    m = make_model(cfg, seed=25, fmts=fmts)
     rng = np.random.default_rng(4)
     lens = [600, 7, 513, 40]
     prompts = [rng.integers(0, cfg.vocab, n).astype(np.int32) for n in lens]
