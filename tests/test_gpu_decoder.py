@@ -316,3 +316,45 @@ def test_formats_round_trip_and_errors():
         odd.set_format(0, T_W_IN, Q4_K)   # K = hidden 384 is not a multiple of 256
     odd.set_format(0, T_W_OUT, Q4_K)      # K = 2 * 256
     odd.close()
+
+
+def test_cache_stride_does_not_change_results():
+    """The engine pads each sequence's KV-cache stride when max_ctx is a
+    multiple of 64 (128 here: a stride of 132 positions) and not otherwise
+    (129): prefilled prompts of three sequences and 10 greedy decode steps give
+    the same tokens, positions and logits bit for bit, and the state API returns
+    the same first 128 cache positions."""
+    import dataclasses
+    from echohip.engine import Engine, S_KEYS, S_KSCALES, S_VALS, S_VSCALES
+    cfg = small_config(max_batch=3, max_ctx=128)
+    m = make_model(cfg, seed=41)
+    rng = np.random.default_rng(41)
+    prompts = [rng.integers(0, cfg.vocab, n).astype(np.int32) for n in (60, 7, 100)]
+    runs = []
+    for mc in (128, 129):
+        e = Engine(dataclasses.replace(cfg, max_ctx=mc))
+        upload(e, m)
+        e.reset()
+        e.prefill_batch([(s, prompts[s], 0) for s in range(3)])
+        for _ in range(10):
+            e.step()
+        e.sync()
+        g, p = e.tokens()
+        lg = [e.logits(s) for s in range(3)]
+        kv = {}
+        for l in range(cfg.n_layers):
+            if cfg.is_attn(l):
+                for s in range(3):
+                    for w, per in ((S_KEYS, cfg.n_kv * cfg.head_dim), (S_VALS, cfg.n_kv * cfg.head_dim),
+                                   (S_KSCALES, cfg.n_kv), (S_VSCALES, cfg.n_kv)):
+                        x = e.get_state(l, w, s)
+                        kv[(l, w, s)] = x.reshape(mc, -1)[:128].copy()
+        runs.append((g, p, lg, kv))
+        e.close()
+    (g0, p0, l0, k0), (g1, p1, l1, k1) = runs
+    assert np.array_equal(g0, g1) and np.array_equal(p0, p1)
+    assert p0.tolist() == [70, 17, 110]
+    for a, b in zip(l0, l1):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    for key in k0:
+        assert np.array_equal(k0[key].view(np.uint8), k1[key].view(np.uint8)), key
