@@ -358,3 +358,49 @@ def test_cache_stride_does_not_change_results():
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     for key in k0:
         assert np.array_equal(k0[key].view(np.uint8), k1[key].view(np.uint8)), key
+
+
+@pytest.mark.gpu
+def test_sequence_at_cache_end_goes_inactive():
+    """Free-running graph decode up to the end of the cache: the step that
+    decodes position max_ctx - 1 still writes its token, then the sequence
+    becomes inactive (pos -1, its last token kept) and later steps leave it
+    alone, while the other sequence decodes bit for bit as it does alone."""
+    from echohip.engine import Engine
+    cfg = small_config(max_batch=2, max_ctx=16)
+    m = make_model(cfg, seed=5)
+    rng = np.random.default_rng(5)
+    p0 = rng.integers(0, cfg.vocab, 12).astype(np.int32)
+    p1 = rng.integers(0, cfg.vocab, 3).astype(np.int32)
+    e = Engine(cfg)
+    try:
+        upload(e, m)
+        e.reset()
+        e.prefill(0, p0, 0)
+        e.prefill(1, p1, 0)
+        e.sync()
+        _, pos = e.tokens()
+        assert pos.tolist() == [12, 3]
+        toks, poss, logs = [], [], []
+        for _ in range(8):
+            e.step(graph=True)
+            e.sync()
+            g, p = e.tokens()
+            toks.append(g.copy())
+            poss.append(p.copy())
+            logs.append(e.logits(1))
+        assert [int(p[0]) for p in poss] == [13, 14, 15, -1, -1, -1, -1, -1]
+        assert [int(p[1]) for p in poss] == list(range(4, 12))
+        assert all(int(t[0]) == int(toks[3][0]) for t in toks[3:])
+        # sequence 1 alone (sequence 0 inactive from the start)
+        e.reset()
+        e.prefill(1, p1, 0)
+        for k in range(8):
+            e.step(graph=True)
+            e.sync()
+            g, p = e.tokens()
+            assert int(p[0]) == -1 and int(p[1]) == 4 + k
+            assert int(g[1]) == int(toks[k][1]), k
+            assert np.array_equal(e.logits(1).view(np.uint32), logs[k].view(np.uint32)), k
+    finally:
+        e.close()
